@@ -1,0 +1,249 @@
+/*
+ * scope_amd.h — C ABI of the MI355X (gfx950) SCOPE attention hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as void*, NULL = the default stream).  No call allocates device
+ * memory: callers pass outputs and, where one is needed, a workspace whose
+ * size the matching *_workspace_bytes() function reports.  All launches are
+ * asynchronous on the given stream; no entry point synchronises the host.
+ *
+ * Return value: 0 on success, a negative SCOPE_E* code otherwise; the
+ * message of the last failure on the calling thread is scope_last_error().
+ *
+ * Layout conventions (B = 1 throughout, as the reference asserts,
+ * scoped_medium.py:336):
+ *   q, k, v, out, dout, dq, dk, dv : bf16 bits (uint16_t), logical [H, T, D],
+ *                                    element strides (stride_h, stride_t), d stride 1
+ *   docs                           : int32 [T] document ids
+ *   NB = QB = T / bs               : number of key blocks = number of query blocks
+ *   kv_num [H, QB], kv_idx [H, QB, MAXKV] : compact BlockMask rows (int32)
+ *   q_off [H, NB + 1], q_list [H, QB * MAXKV] : transposed lists (CSR, int32)
+ */
+#ifndef SCOPE_AMD_H
+#define SCOPE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SCOPE_ABI_VERSION 1
+
+enum {
+  SCOPE_OK = 0,
+  SCOPE_EINVAL = -1,  /* bad shape, size or parameter                  */
+  SCOPE_ELAUNCH = -2, /* a kernel launch failed (hipGetLastError)       */
+  SCOPE_ERANGE = -3   /* a size exceeds a compiled limit                */
+};
+
+int scope_abi_version(void);
+const char* scope_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Document starts.  Replaces model/attn_bias.py:688-709 (doc_change_tok,
+ * cummax, floor_divide, reset segments) of build_pointer_blockmask and the
+ * same steps of the forward debug statistics (:543-569).
+ *   ds_ptr[qb]     doc start block of token (qb+1)*bs-1, clamped by resets
+ *   ds_local[qb]   doc start block of token qb*bs, clamped by resets
+ *   ds_tok_end[qb] doc start token of token (qb+1)*bs-1 (no clamp, no reset)
+ * doc_clamp = 0 zeroes ds_ptr/ds_local (:698-700); reset_len > 0 applies the
+ * reset segments (:703-709).
+ * ---------------------------------------------------------------------- */
+int scope_doc_starts(const int32_t* docs, int64_t T, int bs, int doc_clamp, int reset_len,
+                     int32_t* ds_ptr, int32_t* ds_local, int32_t* ds_tok_end, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Reference-mode pointer mask.  Replaces the body of
+ * SpectralBias.build_pointer_blockmask, model/attn_bias.py:711-837
+ * (representatives, radius allocation, Gumbel top-k over peaks, centres,
+ * local/pointer/global pieces, sort + dedupe + pack).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int H, M, bs;
+  int64_t T;
+  int64_t stride_h, stride_t;  /* element strides of delta_star / budget_logits [H,T,M] */
+  int rep_mean;                /* 0: token (qb+1)*bs-1 ("last"), 1: block mean        */
+  int local_blocks;            /* after call-site override and max(1, .)              */
+  int ptr_half_blocks;         /* p, after override and max(0, .)                    */
+  int global_blocks_cfg;       /* pointer_global_blocks (constructor)                 */
+  int global_active;           /* active global count (argument or schedule buffer)   */
+  int radius_mode_pi;          /* 1: "pi", 0: "fixed"                                 */
+  int budget_rem;              /* integer half budget, model/attn_bias.py:724-734     */
+  float budget_temp;           /* max(pointer_budget_temp, 1e-6)                      */
+  int mask_active;             /* _pointer_mask_active                                */
+  int half_active;             /* _pointer_half_blocks_active                         */
+  int gumbel_k;                /* 0: Gumbel off; else k (< M), training only          */
+  float gumbel_tau;            /* max(gumbel_topk_tau, 1e-6)                          */
+  float eps;                   /* SpectralBias.eps                                    */
+} scope_ptr_ref_params;
+
+/* MAXKV of the reference-mode list: local + (p>0 ? M(2p+1) : M) + min(G, NB). */
+int scope_ptr_ref_maxkv(const scope_ptr_ref_params* p);
+
+int scope_pointer_mask_ref(const scope_ptr_ref_params* p, const float* delta_star,
+                           const float* budget_logits, const float* gumbel_u /* [H,QB,M] or NULL */,
+                           const int32_t* ds_ptr, const int32_t* ds_local, int32_t* kv_num,
+                           int32_t* kv_idx /* [H,QB,MAXKV] */, int32_t* radius /* [H,QB,M] */,
+                           int32_t* centre /* [H,QB,M] */, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block-scoring pointer selection (block-mean q·k + radius prior + Gumbel
+ * top-k under a budget; the BASELINE specification of kernel 1).  Produces
+ * the same (kv_num, kv_idx) layout as build_pointer_blockmask
+ * (model/attn_bias.py:825-837) for the union window ∪ pointers ∪ global.
+ * ---------------------------------------------------------------------- */
+/* Block means q̄, k̄ [H, NB, D] fp32 of bf16 q, k. */
+int scope_block_means(const uint16_t* q, const uint16_t* k, int H, int64_t T, int D, int bs,
+                      int64_t q_sh, int64_t q_st, int64_t k_sh, int64_t k_st, float* qbar,
+                      float* kbar, void* stream);
+
+typedef struct {
+  int H, NB, D, bs;
+  int window, n_global, budget; /* W, G, pointer slots (budget <= 16)                   */
+  float temp;                   /* τ of z = logit/τ + g                                  */
+  float logit_scale;            /* logit = logit_scale * q̄·k̄ + prior[qb-kb]             */
+  int noise_mode;               /* 0: none, 1: explicit uniforms, 2: counter-based draw  */
+  uint64_t seed;                /* noise_mode 2                                          */
+  float eps;                    /* Gumbel eps (1e-9)                                     */
+  int64_t prior_head_stride;    /* 0: prior is [NB] shared; NB: prior is [H, NB]         */
+} scope_ptr_score_params;
+
+int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, const float* kbar,
+                         const float* logits_in /* [H,QB,NB] or NULL */,
+                         const float* prior /* or NULL */, const float* gumbel_u /* [H,QB,NB] or NULL */,
+                         const int32_t* ds_ptr, const int32_t* ds_local, int32_t* kv_num,
+                         int32_t* kv_idx /* [H,QB,W+budget+G] */, int32_t* picks /* [H,QB,budget] */,
+                         float* logits_out /* [H,QB,NB] or NULL */, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Transposed (q-major) lists.  Replaces BlockMask.from_kv_blocks ->
+ * _transpose_ordered (torch:nn/attention/flex_attention.py:399-441, called at
+ * model/attn_bias.py:867-873) with a compact CSR: for each kv block the
+ * q-blocks that list it, ascending.
+ * ---------------------------------------------------------------------- */
+int64_t scope_transpose_workspace_bytes(int H, int NB);
+int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB,
+                           int maxkv, int32_t* q_off, int32_t* q_list, void* workspace,
+                           void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused mask statistics.  Replaces model/attn_bias.py:510-600 (forward debug
+ * statistics) and :839-849 (mask debug statistics) and defines the same
+ * histograms for the block-scoring mode.  Integer counts go to `counts`
+ * (layout SCOPE_ST_*, then the three variable-length histograms), derived
+ * fp32 values to `values` (SCOPE_SV_*).
+ * ---------------------------------------------------------------------- */
+enum {
+  SCOPE_ST_DELTA_TOKENS = 0,  /* 16 bins */
+  SCOPE_ST_DELTA_BLOCKS = 16, /* 15 bins */
+  SCOPE_ST_CENTER = 31,       /* 15 bins */
+  SCOPE_ST_DOCSTART = 46,
+  SCOPE_ST_OUTSIDE = 47,
+  SCOPE_ST_BLOCK0 = 48,
+  SCOPE_ST_BLOCK0_EXCL = 49,
+  SCOPE_ST_N_CENTRES = 50,
+  SCOPE_ST_N_CENTRES_EXCL = 51,
+  SCOPE_ST_PTR_DIST = 52,     /* 15 bins, block-scoring picks */
+  SCOPE_ST_BS_OUTSIDE = 67,
+  SCOPE_ST_BS_BLOCK0 = 68,
+  SCOPE_ST_BS_BLOCK0_EXCL = 69,
+  SCOPE_ST_BS_DOCSTART = 70,
+  SCOPE_ST_BS_N = 71,
+  SCOPE_ST_BS_N_EXCL = 72,
+  SCOPE_ST_RADIUS0 = 73,
+  SCOPE_ST_N_RADIUS = 74,
+  SCOPE_ST_FIXED = 75         /* kv_unique[maxkv_bins], radius[radius_bins], extra_sum[extra_bins] follow */
+};
+enum {
+  SCOPE_SV_PI_ENTROPY_MEAN = 0,
+  SCOPE_SV_DOCSTART_FRAC = 1,
+  SCOPE_SV_OUTSIDE_LOCAL_FRAC = 2,
+  SCOPE_SV_BLOCK0_FRAC = 3,
+  SCOPE_SV_BLOCK0_FRAC_EXCL = 4,
+  SCOPE_SV_RADIUS0_FRAC = 5,
+  SCOPE_SV_BS_OUTSIDE_LOCAL_FRAC = 6,
+  SCOPE_SV_BS_BLOCK0_FRAC = 7,
+  SCOPE_SV_BS_BLOCK0_FRAC_EXCL = 8,
+  SCOPE_SV_BS_DOCSTART_FRAC = 9,
+  SCOPE_SV_COUNT = 10
+};
+
+typedef struct {
+  int H, QB, bs, M;
+  int64_t T;
+  /* forward statistics (model/attn_bias.py:510-600); delta_star / pi non-NULL enables them */
+  int64_t stride_h, stride_t;
+  int rep_mean;
+  int has_docs;           /* docs given to SpectralBias.forward                      */
+  int docstart_enabled;   /* docs and (pointer_doc_clamp or reset_active)            */
+  int local_blocks_cfg;   /* pointer_local_blocks (constructor)                      */
+  float eps;
+  /* mask statistics (model/attn_bias.py:839-849); radius non-NULL enables them      */
+  int maxkv_bins;         /* _dbg_kv_unique_hist.numel()                             */
+  int radius_bins;        /* _dbg_ptr_radius_hist.numel()                            */
+  int extra_bins;         /* _dbg_ptr_extra_sum_hist.numel()                         */
+  /* block-scoring statistics; picks non-NULL enables them                           */
+  int budget;
+  int bs_local_blocks;
+} scope_stats_params;
+
+int64_t scope_stats_counts_len(const scope_stats_params* p);
+int64_t scope_stats_workspace_bytes(const scope_stats_params* p);
+int scope_mask_stats(const scope_stats_params* p, const float* delta_star, const float* pi,
+                     const int32_t* ds_ptr_fwd, const int32_t* ds_local_fwd, const int32_t* kv_num,
+                     const int32_t* radius, const int32_t* picks, const int32_t* ds_ptr,
+                     const int32_t* ds_local, int32_t* counts, float* values, void* workspace,
+                     void* stream);
+
+/* ------------------------------------------------------------------------
+ * Block-sparse flash attention with the SCOPE spectral bias.  Replaces the
+ * FlexAttention calls of scoped_medium.py:422, 459-466, 470-476 (Triton
+ * templates torch:_inductor/kernel/flex/templates/flex_attention.py.jinja and
+ * flex_backwards.py.jinja) for the pointer BlockMask with the
+ * document_causal mask_mod (model/attn_bias.py:674-679) and the spectral
+ * score_mod (scoped_medium.py:425-457).
+ * ---------------------------------------------------------------------- */
+enum { SCOPE_BIAS_NONE = 0, SCOPE_BIAS_BLOCK = 1, SCOPE_BIAS_TOKEN = 2 };
+enum { SCOPE_GATE_NONE = 0, SCOPE_GATE_SOFTPLUS = 1, SCOPE_GATE_RELU = 2 };
+
+typedef struct {
+  int H, D, bs, maxkv;
+  int64_t T;
+  float scale, beta;
+  int bias_mode;           /* SCOPE_BIAS_*                                           */
+  int K;                   /* spectral bands, <= 8                                   */
+  int use_slope, subtract_b0, gate_kind;
+  float ramp_lambda, tau;
+  int64_t q_sh, q_st, k_sh, k_st, v_sh, v_st, o_sh, o_st;  /* element strides */
+} scope_attn_params;
+
+/* Spectral tables: block mode [NB][16] fp32 (cos ω_k r, sin ω_k r);
+ * token mode [T][16] bf16 (cos ω_k j, sin ω_k j).  Replaces
+ * SpectralBias._get_trig_tables, model/attn_bias.py:326-340. */
+int64_t scope_spectral_table_bytes(int bias_mode, int64_t T, int bs);
+int scope_spectral_table(int bias_mode, const float* omegas, int K, int64_t T, int bs, void* table,
+                         void* stream);
+
+int scope_attn_fwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
+                   const uint16_t* v, const int32_t* kv_num, const int32_t* kv_idx,
+                   const int32_t* docs, const int32_t* ds_tok_end, const void* table,
+                   const float* coeff_cos, const float* coeff_sin, const float* b0,
+                   const float* slope, const float* delta_main, const float* width, uint16_t* out,
+                   float* lse, void* stream);
+
+int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
+int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
+                   const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,
+                   const int32_t* kv_num, const int32_t* kv_idx, const int32_t* q_off,
+                   const int32_t* q_list, const int32_t* docs, const int32_t* ds_tok_end,
+                   const void* table, const float* coeff_cos, const float* coeff_sin,
+                   const float* b0, const float* slope, const float* delta_main,
+                   const float* width, uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                   float* dcoeff_cos, float* dcoeff_sin, float* db0, float* dslope,
+                   float* ddelta_main, float* dwidth, void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SCOPE_AMD_H */

@@ -1,0 +1,121 @@
+"""``scope_attention``: the drop-in for the FlexAttention calls of
+``CausalSelfAttention.forward`` (scoped_medium.py:422, 459-466, 470-476).
+
+The reference passes a Python ``score_mod`` closure over the spectral
+coefficients (scoped_medium.py:425-457); here the same terms are passed as
+tensors in a ``SpectralTerms`` record and evaluated inside the HIP kernels.
+Gradients flow to q, k, v and to every coefficient tensor that requires grad,
+like FlexAttention's captured-buffer gradients.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+from .blockmask import ScopeBlockMask
+
+
+@dataclass
+class SpectralTerms:
+    """Inputs of the spectral bias (per query row).
+
+    ``offset="token"`` is the reference's score_mod (Δ = max(i-j, 0)):
+        Σ_k A_k cos(ω_k Δ) + B_k sin(ω_k Δ) - b0·[subtract_b0] + slope·Δ·[use_slope]
+        - ramp_lambda·gate((|Δ - delta_main| - width)/tau)
+    ``offset="block"`` uses the block offset r = qb - kb instead and only the
+    band term.  The score becomes ``scale·q·k + beta·bias``.
+    """
+    coeff_cos: torch.Tensor          # [1,H,T,K]
+    coeff_sin: torch.Tensor          # [1,H,T,K]
+    omegas: torch.Tensor             # [K]
+    offset: str = "token"
+    beta: float = 0.5
+    b0: torch.Tensor | None = None   # [1,H,T]
+    slope: torch.Tensor | None = None
+    delta_main: torch.Tensor | None = None
+    width: torch.Tensor | None = None
+    use_slope: bool = False
+    subtract_b0: bool = False
+    gate_kind: str = "none"
+    ramp_lambda: float = 0.0
+    tau: float = 64.0
+
+
+_TABLES: dict = {}
+
+
+def spectral_table(omegas: torch.Tensor, T: int, bs: int, mode: str) -> torch.Tensor:
+    """Cached cos/sin table (the analogue of SpectralBias._get_trig_tables)."""
+    key = (omegas.data_ptr(), omegas._version, omegas.device, T, bs, mode)
+    tab = _TABLES.get(key)
+    if tab is None:
+        if len(_TABLES) > 16:
+            _TABLES.clear()
+        tab = ops.spectral_table(omegas, T, bs, mode)
+        _TABLES[key] = tab
+    return tab
+
+
+def _kwargs(sp: SpectralTerms | None, bm: ScopeBlockMask):
+    if sp is None:
+        return dict(bias_mode="none")
+    T = bm.seq_len
+    return dict(bias_mode=sp.offset, beta=sp.beta, table=spectral_table(sp.omegas, T, bm.BLOCK_SIZE, sp.offset),
+                use_slope=sp.use_slope and sp.offset == "token",
+                subtract_b0=sp.subtract_b0 and sp.offset == "token",
+                gate_kind=sp.gate_kind if sp.offset == "token" else "none", ramp_lambda=sp.ramp_lambda, tau=sp.tau)
+
+
+class _ScopeAttnFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cc, cs, b0, slope, dm, wd, bm: ScopeBlockMask, sp: SpectralTerms | None, scale: float):
+        kw = _kwargs(sp, bm)
+        out, lse = ops.attn_fwd(q, k, v, bm.kv_num_blocks[0], bm.kv_indices[0], bm.docs, bm.ds_tok_end,
+                                bs=bm.BLOCK_SIZE, scale=scale, coeff_cos=cc, coeff_sin=cs, b0=b0, slope=slope,
+                                delta_main=dm, width=wd, **kw)
+        ctx.save_for_backward(q, k, v, out, lse, cc, cs, b0, slope, dm, wd)
+        ctx.bm, ctx.sp, ctx.scale = bm, sp, scale
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, out, lse, cc, cs, b0, slope, dm, wd = ctx.saved_tensors
+        bm, sp = ctx.bm, ctx.sp
+        kw = _kwargs(sp, bm)
+        q_off, q_list = bm.q_lists()
+        dout = dout if dout.stride() == q.stride() else _match(dout, q)
+        out_m = out if out.stride() == q.stride() else _match(out, q)
+        need_c = sp is not None and any(ctx.needs_input_grad[3:9])
+        g = ops.attn_bwd(q, k, v, out_m, dout, lse, bm.kv_num_blocks[0], bm.kv_indices[0], q_off, q_list, bm.docs,
+                         bm.ds_tok_end, bs=bm.BLOCK_SIZE, scale=ctx.scale, coeff_cos=cc, coeff_sin=cs, b0=b0,
+                         slope=slope, delta_main=dm, width=wd, need_coeff_grads=need_c, **kw)
+        return (g["dq"], g["dk"], g["dv"], g["dcoeff_cos"], g["dcoeff_sin"], g["db0"], g["dslope"],
+                g["ddelta_main"], g["dwidth"], None, None, None)
+
+
+def _match(x: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    y = torch.empty_like(like)
+    y.copy_(x)
+    return y
+
+
+def scope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block_mask: ScopeBlockMask,
+                    scale: float, spectral: SpectralTerms | None = None, return_lse: bool = False):
+    """Block-sparse attention over ``block_mask`` with the document-causal
+    mask and the optional spectral bias.  q, k, v: [1,H,T,D] bf16 (any
+    head/token strides, unit last stride).  Returns out [1,H,T,D] (and
+    lse [1,H,T], natural log, if ``return_lse``)."""
+    sp = spectral
+    cc = cs = b0 = sl = dm = wd = None
+    if sp is not None:
+        cc, cs = sp.coeff_cos, sp.coeff_sin
+        if sp.offset == "token":
+            b0 = sp.b0 if sp.subtract_b0 else None
+            sl = sp.slope if sp.use_slope else None
+            if sp.gate_kind != "none":
+                dm, wd = sp.delta_main, sp.width
+    out, lse = _ScopeAttnFn.apply(q, k, v, cc, cs, b0, sl, dm, wd, block_mask, sp, float(scale))
+    return (out, lse) if return_lse else out

@@ -1,0 +1,661 @@
+// Kernel 1: pointer-driven block selection for gfx950.
+//
+//  * doc starts         model/attn_bias.py:688-709
+//  * reference mode     model/attn_bias.py:711-837  (build_pointer_blockmask body)
+//  * block means        q̄, k̄ per block (block-scoring mode)
+//  * block-scoring mode block-mean q·k logits + distance prior + Gumbel top-k
+//                       under a budget, union with window and global blocks
+//
+// One wavefront per (head, q-block).  Lists are sorted with a bitonic network
+// in LDS and packed like the reference (unique ascending, then duplicates
+// ascending).  Compiled with -ffp-contract=off: the radius allocation and the
+// Gumbel scores must round exactly like the reference's fp32 tensor ops.
+#include <limits.h>
+#include <math.h>
+
+#include "common.h"
+
+namespace scope {
+
+constexpr int kMaxPeaks = 32;   // M limit of the reference mode (one lane per peak)
+constexpr int kMaxBudget = 16;  // pointer slots of the block-scoring mode
+constexpr int kMaxList = 1024;  // MAXKV limit (LDS sort network)
+
+// ---------------------------------------------------------------------------
+// shared wave-level utilities
+// ---------------------------------------------------------------------------
+// Bitonic sort of s[0..N) ascending (N a power of two) by one wavefront.
+// Every wave of the workgroup must call it with the same N (it uses
+// workgroup barriers between the network stages).
+__device__ void wave_bitonic_sort(int* s, int N) {
+  const int lane = lane_id();
+  for (int k = 2; k <= N; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = lane; i < (N >> 1); i += kWave) {
+        int lo = 2 * j * (i / j) + (i % j);
+        int hi = lo + j;
+        bool up = (lo & k) == 0;
+        int a = s[lo], b = s[hi];
+        if ((a > b) == up) {
+          s[lo] = b;
+          s[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Pack the sorted s[0..n): unique values ascending first, then duplicates
+// ascending (model/attn_bias.py:829-837).  Returns the unique count.
+__device__ int wave_pack_sorted(const int* s, int n, int* __restrict__ out, bool write) {
+  const int lane = lane_id();
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  int nkeep = 0;
+  for (int base = 0; base < n; base += kWave) {
+    int e = base + lane;
+    bool keep = e < n && (e == 0 || s[e] != s[e - 1]);
+    nkeep += __popcll(__ballot(keep));
+  }
+  int kc = 0, dc = 0;
+  for (int base = 0; base < n; base += kWave) {
+    int e = base + lane;
+    bool valid = e < n;
+    bool keep = valid && (e == 0 || s[e] != s[e - 1]);
+    bool dup = valid && !keep;
+    uint64_t mk = __ballot(keep), md = __ballot(dup);
+    if (write && keep) out[kc + __popcll(mk & below)] = s[e];
+    if (write && dup) out[nkeep + dc + __popcll(md & below)] = s[e];
+    kc += __popcll(mk);
+    dc += __popcll(md);
+  }
+  return nkeep;
+}
+
+__device__ __forceinline__ float sigmoid_ref(float x) {
+  // torch.sigmoid on fp32: 1 / (1 + exp(-x))
+  float e = expf(-x);
+  return 1.0f / (1.0f + e);
+}
+
+__device__ __forceinline__ float gumbel_of(float u, float eps) {
+  // g = -log(-log(u + eps) + eps)   (model/attn_bias.py:771)
+  float a = u + eps;
+  float b = -logf(a);
+  float c = b + eps;
+  return -logf(c);
+}
+
+// ---------------------------------------------------------------------------
+// doc starts
+// ---------------------------------------------------------------------------
+// Phase 1: per block, the last change point inside it (or -1) and whether the
+// block's first token is a change point.
+__global__ __launch_bounds__(256) void doc_blocks_kernel(const int32_t* __restrict__ docs, int64_t T,
+                                                          int bs, int32_t* __restrict__ last_change,
+                                                          int32_t* __restrict__ first_change) {
+  const int b = blockIdx.x;
+  const int64_t t0 = static_cast<int64_t>(b) * bs;
+  int best = -1;
+  for (int i = threadIdx.x; i < bs; i += blockDim.x) {
+    int64_t t = t0 + i;
+    bool ch = (t == 0) || (docs[t] != docs[t - 1]);
+    if (ch) best = max(best, static_cast<int>(t));
+  }
+  __shared__ int red[256];
+  red[threadIdx.x] = best;
+  __syncthreads();
+  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    last_change[b] = red[0];
+    first_change[b] = (t0 == 0 || docs[t0] != docs[t0 - 1]) ? 1 : 0;
+  }
+}
+
+// Phase 2 (one workgroup): prefix max over blocks, then the three outputs.
+// last_change aliases ds_tok_end and first_change aliases ds_local.
+__global__ __launch_bounds__(1024) void doc_scan_kernel(int NB, int bs, int doc_clamp, int reset_len,
+                                                         int32_t* __restrict__ ds_ptr,
+                                                         int32_t* __restrict__ ds_local,
+                                                         int32_t* __restrict__ ds_tok_end) {
+  __shared__ int carry_s;
+  __shared__ int tmax[1024];
+  if (threadIdx.x == 0) carry_s = -1;
+  __syncthreads();
+  for (int base = 0; base < NB; base += 1024) {
+    int b = base + threadIdx.x;
+    int lc = b < NB ? ds_tok_end[b] : -1;
+    int fc = b < NB ? ds_local[b] : 0;
+    // inclusive prefix max of lc within the chunk (Hillis-Steele)
+    tmax[threadIdx.x] = lc;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+      int v = threadIdx.x >= o ? tmax[threadIdx.x - o] : -1;
+      __syncthreads();
+      tmax[threadIdx.x] = max(tmax[threadIdx.x], v);
+      __syncthreads();
+    }
+    int carry = carry_s;
+    int incl = max(tmax[threadIdx.x], carry);
+    int excl = max(threadIdx.x > 0 ? tmax[threadIdx.x - 1] : -1, carry);
+    __syncthreads();
+    if (threadIdx.x == 1023) carry_s = incl;
+    if (b < NB) {
+      int64_t first_tok = static_cast<int64_t>(b) * bs;
+      int64_t last_tok = first_tok + bs - 1;
+      int dst_end = incl;                                     // doc start of the last token
+      int dst_first = fc ? static_cast<int>(first_tok) : excl;  // doc start of the first token
+      int p = doc_clamp ? dst_end / bs : 0;
+      int l = doc_clamp ? dst_first / bs : 0;
+      if (reset_len > 0) {
+        int sp = static_cast<int>(((last_tok / reset_len) * reset_len) / bs);
+        int sl = static_cast<int>(((first_tok / reset_len) * reset_len) / bs);
+        p = max(p, sp);
+        l = max(l, sl);
+      }
+      ds_ptr[b] = p;
+      ds_local[b] = l;
+      ds_tok_end[b] = dst_end;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// reference mode
+// ---------------------------------------------------------------------------
+struct RefLaunch {
+  scope_ptr_ref_params p;
+  int NB, L, N, NP, gmax;
+};
+
+__global__ __launch_bounds__(256) void ptr_ref_kernel(RefLaunch A, const float* __restrict__ delta_star,
+                                                       const float* __restrict__ budget_logits,
+                                                       const float* __restrict__ gumbel_u,
+                                                       const int32_t* __restrict__ ds_ptr_a,
+                                                       const int32_t* __restrict__ ds_local_a,
+                                                       int32_t* __restrict__ kv_num, int32_t* __restrict__ kv_idx,
+                                                       int32_t* __restrict__ radius, int32_t* __restrict__ centre) {
+  extern __shared__ int smem[];
+  const scope_ptr_ref_params& P = A.p;
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int NB = A.NB;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const bool active = row < static_cast<int64_t>(P.H) * NB;
+  const int h = active ? static_cast<int>(row / NB) : 0;
+  const int qb = active ? static_cast<int>(row % NB) : 0;
+  const int M = P.M;
+  int* list = smem + wave * A.N;
+  float* fs = reinterpret_cast<float*>(smem + 4 * A.N) + wave * 5 * kMaxPeaks;
+  float* s_d = fs;                   // Δ* representatives
+  float* s_b = fs + kMaxPeaks;       // budget representatives
+  float* s_f = fs + 2 * kMaxPeaks;   // fractional parts / Gumbel scores
+  int* s_r = reinterpret_cast<int*>(fs + 3 * kMaxPeaks);  // radius
+  int* s_c = reinterpret_cast<int*>(fs + 4 * kMaxPeaks);  // centres
+  const int ds_p = ds_ptr_a[qb];
+  const int ds_l = ds_local_a[qb];
+  const int64_t t_rep = static_cast<int64_t>(qb + 1) * P.bs - 1;
+
+  // 1. representatives (model/attn_bias.py:713-719)
+  if (active && lane < M) {
+    const int64_t base = h * P.stride_h + lane;
+    float d, b;
+    if (!P.rep_mean) {
+      d = delta_star[base + t_rep * P.stride_t];
+      b = budget_logits[base + t_rep * P.stride_t];
+    } else {
+      float sd = 0.f, sb = 0.f;
+      const int64_t t0 = static_cast<int64_t>(qb) * P.bs;
+      for (int i = 0; i < P.bs; ++i) {
+        sd += delta_star[base + (t0 + i) * P.stride_t];
+        sb += budget_logits[base + (t0 + i) * P.stride_t];
+      }
+      d = sd / static_cast<float>(P.bs);
+      b = sb / static_cast<float>(P.bs);
+    }
+    s_d[lane] = d;
+    s_b[lane] = b;
+  }
+  __syncthreads();
+
+  // 2. radius allocation (model/attn_bias.py:721-758)
+  int r = 0;
+  float fr = 0.f;
+  int fl = 0, rem_int = 0;
+  if (active && lane < M && P.radius_mode_pi && P.budget_rem > 0) {
+    float rem = static_cast<float>(P.budget_rem);
+    float a = 0.f;
+    int floor_sum = 0;
+    for (int mm = 0; mm < M - 1; ++mm) {
+      float u = s_b[mm] / P.budget_temp;
+      float v = sigmoid_ref(u);
+      float bb = v * rem;
+      if (mm == lane) a = bb;
+      floor_sum += static_cast<int>(floorf(bb));
+      rem = rem - bb;
+    }
+    if (lane == M - 1) a = rem;
+    floor_sum += static_cast<int>(floorf(rem));
+    float fa = floorf(a);
+    fl = static_cast<int>(fa);
+    fr = a - fa;
+    rem_int = min(max(P.budget_rem - floor_sum, 0), M);
+  }
+  if (active && lane < M) s_f[lane] = fr;
+  __syncthreads();
+  if (active && lane < M) {
+    if (P.radius_mode_pi) {
+      if (P.budget_rem > 0) {
+        int rank = 0;
+        for (int mm = 0; mm < M; ++mm) {
+          float o = s_f[mm];
+          rank += (o > fr || (o == fr && mm < lane)) ? 1 : 0;
+        }
+        r = min(max(fl + (rank < rem_int ? 1 : 0), 0), P.ptr_half_blocks);
+      } else {
+        r = 0;
+      }
+    } else {
+      r = P.half_active;
+    }
+    r = min(r, P.half_active);
+    if (!P.mask_active) r = 0;
+  }
+  __syncthreads();
+  // Gumbel top-k over peaks (model/attn_bias.py:763-777)
+  if (P.gumbel_k > 0) {
+    float sc = 0.f;
+    if (active && lane < M) {
+      float u = gumbel_u[(static_cast<int64_t>(h) * NB + qb) * M + lane];
+      float b = s_b[lane] / P.gumbel_tau;
+      sc = b + gumbel_of(u, P.eps);
+      s_f[lane] = sc;
+    }
+    __syncthreads();
+    if (active && lane < M) {
+      int rank = 0;
+      for (int mm = 0; mm < M; ++mm) {
+        float o = s_f[mm];
+        rank += (o > sc || (o == sc && mm < lane)) ? 1 : 0;
+      }
+      if (rank >= P.gumbel_k) r = 0;
+    }
+  }
+  // centres (model/attn_bias.py:779-784)
+  if (active && lane < M) {
+    float key = static_cast<float>(t_rep) - s_d[lane];
+    key = fmaxf(key, 0.0f);
+    int64_t c = static_cast<int64_t>(key) / P.bs;
+    c = min(c, static_cast<int64_t>(qb));
+    if (!P.mask_active) c = qb;
+    c = max(c, static_cast<int64_t>(ds_p));
+    s_r[lane] = r;
+    s_c[lane] = static_cast<int>(c);
+    radius[(static_cast<int64_t>(h) * NB + qb) * M + lane] = r;
+    centre[(static_cast<int64_t>(h) * NB + qb) * M + lane] = static_cast<int>(c);
+  }
+  __syncthreads();
+
+  // 3. pieces: local | pointer | global (model/attn_bias.py:786-823)
+  const int local = P.local_blocks;
+  const int p = P.ptr_half_blocks;
+  for (int e = lane; e < A.N; e += kWave) {
+    int v = INT_MAX;
+    if (active && e < A.L) {
+      if (e < local) {
+        v = max(max(qb - e, 0), ds_l);
+      } else if (e < local + A.NP) {
+        int idx = e - local;
+        if (p > 0) {
+          int m = idx / (2 * p + 1);
+          int o = idx % (2 * p + 1) - p;
+          int c = s_c[m];
+          if (abs(o) <= s_r[m]) {
+            v = min(max(c + o, 0), NB - 1);
+            v = min(v, qb);
+            v = max(v, ds_p);
+          } else {
+            v = c;
+          }
+        } else {
+          v = s_c[idx];
+        }
+      } else {
+        int g = e - local - A.NP;
+        int ga = min(max(P.global_active, 0), A.gmax);
+        v = g < ga ? min(ds_p + g, qb) : qb;
+      }
+    }
+    list[e] = v;
+  }
+  __syncthreads();
+
+  // 4. sort, dedupe, pack (model/attn_bias.py:825-837)
+  wave_bitonic_sort(list, A.N);
+  int n = wave_pack_sorted(list, A.L, kv_idx + row * A.L, active);
+  if (active && lane == 0) kv_num[row] = n;
+}
+
+// ---------------------------------------------------------------------------
+// block means
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void block_means_kernel(const uint16_t* __restrict__ q,
+                                                           const uint16_t* __restrict__ k, int bs,
+                                                           int64_t q_sh, int64_t q_st, int64_t k_sh,
+                                                           int64_t k_st, int NB, float* __restrict__ qbar,
+                                                           float* __restrict__ kbar) {
+  constexpr int kChunks = D / 8;        // 16-byte chunks per row
+  constexpr int kGroups = 256 / kChunks;  // row groups
+  __shared__ float red[2][kGroups][D + 4];
+  const int b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int c = threadIdx.x % kChunks;
+  const int g = threadIdx.x / kChunks;
+  float sq[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float sk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int64_t t0 = static_cast<int64_t>(b) * bs;
+  for (int r = g; r < bs; r += kGroups) {
+    const uint4 vq = *reinterpret_cast<const uint4*>(q + h * q_sh + (t0 + r) * q_st + c * 8);
+    const uint4 vk = *reinterpret_cast<const uint4*>(k + h * k_sh + (t0 + r) * k_st + c * 8);
+    const uint32_t wq[4] = {vq.x, vq.y, vq.z, vq.w};
+    const uint32_t wk[4] = {vk.x, vk.y, vk.z, vk.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sq[2 * i] += __uint_as_float(wq[i] << 16);
+      sq[2 * i + 1] += __uint_as_float(wq[i] & 0xffff0000u);
+      sk[2 * i] += __uint_as_float(wk[i] << 16);
+      sk[2 * i + 1] += __uint_as_float(wk[i] & 0xffff0000u);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    red[0][g][c * 8 + i] = sq[i];
+    red[1][g][c * 8 + i] = sk[i];
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * D) {
+    const int which = threadIdx.x / D;
+    const int d = threadIdx.x % D;
+    float s = 0.f;
+    for (int gg = 0; gg < kGroups; ++gg) s += red[which][gg][d];
+    float* out = which ? kbar : qbar;
+    out[(static_cast<int64_t>(h) * NB + b) * D + d] = s / static_cast<float>(bs);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// block-scoring selection
+// ---------------------------------------------------------------------------
+struct ScoreLaunch {
+  scope_ptr_score_params p;
+  int L, N;
+};
+
+// better(a, b): higher score first, lower block index on ties
+__device__ __forceinline__ bool better(float za, int ka, float zb, int kb) {
+  return za > zb || (za == zb && ka < kb);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void ptr_score_kernel(ScoreLaunch A, const float* __restrict__ qbar,
+                                                         const float* __restrict__ kbar,
+                                                         const float* __restrict__ logits_in,
+                                                         const float* __restrict__ prior,
+                                                         const float* __restrict__ gumbel_u,
+                                                         const int32_t* __restrict__ ds_ptr_a,
+                                                         const int32_t* __restrict__ ds_local_a,
+                                                         int32_t* __restrict__ kv_num, int32_t* __restrict__ kv_idx,
+                                                         int32_t* __restrict__ picks, float* __restrict__ logits_out) {
+  constexpr int kStride = D + 4;  // padded k̄ row in LDS (16-byte aligned, conflict-free float4 reads)
+  __shared__ float ks[kWave * kStride];
+  __shared__ int lists[4 * 64];
+  const scope_ptr_score_params& P = A.p;
+  const int NB = P.NB;
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int h = blockIdx.y;
+  const int qb0 = blockIdx.x * 4;
+  const int qb = __builtin_amdgcn_readfirstlane(qb0 + wave);
+  const bool active = qb < NB;
+  const int qbc = active ? qb : NB - 1;
+  const int ds_p = ds_ptr_a[qbc];
+  const int ds_l = ds_local_a[qbc];
+  const int W = min(P.window, NB);
+  const int G = min(P.n_global, NB);
+  const int B = P.budget;
+  const int wlo = max(qbc - W + 1, ds_l);        // window = [wlo, qb]
+  const int ghi = min(ds_p + G - 1, qbc);         // global = [ds_p, ghi] (G > 0)
+  const int64_t rowq = static_cast<int64_t>(h) * NB + qbc;
+
+  float qv[D];
+  if (!logits_in) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) qv[d] = qbar[rowq * D + d];
+  }
+
+  // per-lane top-B list, sorted best first
+  float tz[kMaxBudget];
+  int tk[kMaxBudget];
+#pragma unroll
+  for (int i = 0; i < kMaxBudget; ++i) {
+    tz[i] = -INFINITY;
+    tk[i] = INT_MAX;
+  }
+
+  // kb range of the workgroup: [ds_ptr of its first q-block, its last q-block]
+  const int lo_wg = ds_ptr_a[qb0];
+  const int hi_wg = min(qb0 + 3, NB - 1);
+  for (int kb0 = lo_wg; kb0 <= hi_wg; kb0 += kWave) {
+    if (!logits_in) {
+      __syncthreads();
+      const int nrow = min(kWave, hi_wg - kb0 + 1);
+      for (int i = threadIdx.x; i < nrow * (D / 4); i += blockDim.x) {
+        const int rr = i / (D / 4), cc = i % (D / 4);
+        const float4 v = *reinterpret_cast<const float4*>(kbar + (static_cast<int64_t>(h) * NB + kb0 + rr) * D + cc * 4);
+        *reinterpret_cast<float4*>(&ks[rr * kStride + cc * 4]) = v;
+      }
+      __syncthreads();
+    }
+    const int kb = kb0 + lane;
+    const bool cand = active && kb >= ds_p && kb <= qbc && !(kb >= wlo) && !(G > 0 && kb <= ghi);
+    float logit = 0.f;
+    bool causal = active && kb >= ds_p && kb <= qbc;
+    if (causal) {
+      if (logits_in) {
+        logit = logits_in[rowq * NB + kb];
+      } else {
+        float acc = 0.f;
+        const float* kr = &ks[lane * kStride];
+#pragma unroll
+        for (int d = 0; d < D; d += 4) {
+          const float4 kv4 = *reinterpret_cast<const float4*>(kr + d);
+          acc = fmaf(qv[d], kv4.x, acc);
+          acc = fmaf(qv[d + 1], kv4.y, acc);
+          acc = fmaf(qv[d + 2], kv4.z, acc);
+          acc = fmaf(qv[d + 3], kv4.w, acc);
+        }
+        logit = P.logit_scale * acc;
+        if (prior) logit = logit + prior[h * P.prior_head_stride + (qbc - kb)];
+      }
+      if (logits_out) logits_out[rowq * NB + kb] = logit;
+    }
+    if (cand) {
+      float z = logit / P.temp;
+      if (P.noise_mode != 0) {
+        float u = P.noise_mode == 1 ? gumbel_u[rowq * NB + kb]
+                                    : counter_uniform(P.seed, static_cast<uint32_t>(h), static_cast<uint32_t>(qbc),
+                                                      static_cast<uint32_t>(kb));
+        z = z + gumbel_of(u, P.eps);
+      }
+      // insertion into the sorted list (compile-time indexed, predicated)
+      float cz = z;
+      int ck = kb;
+#pragma unroll
+      for (int i = 0; i < kMaxBudget; ++i) {
+        if (i < B && better(cz, ck, tz[i], tk[i])) {
+          float z2 = tz[i];
+          int k2 = tk[i];
+          tz[i] = cz;
+          tk[i] = ck;
+          cz = z2;
+          ck = k2;
+        }
+      }
+    }
+  }
+  if (logits_out && active) {
+    // entries outside [ds_ptr, qb] are not candidates: -inf
+    for (int kb = lane; kb < NB; kb += kWave)
+      if (kb < ds_p || kb > qbc) logits_out[rowq * NB + kb] = -INFINITY;
+  }
+
+  // wave merge: B rounds of arg-best over the lanes' list heads
+  int* list = lists + wave * 64;
+  for (int i = 0; i < B; ++i) {
+    float bz = tz[0];
+    int bk = tk[0];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      float oz = __shfl_xor(bz, o, kWave);
+      int ok = __shfl_xor(bk, o, kWave);
+      if (better(oz, ok, bz, bk)) {
+        bz = oz;
+        bk = ok;
+      }
+    }
+    const bool valid = bk != INT_MAX;
+    if (valid && tk[0] == bk) {
+#pragma unroll
+      for (int j = 0; j < kMaxBudget - 1; ++j) {
+        tz[j] = tz[j + 1];
+        tk[j] = tk[j + 1];
+      }
+      tz[kMaxBudget - 1] = -INFINITY;
+      tk[kMaxBudget - 1] = INT_MAX;
+    }
+    if (active && lane == 0) picks[rowq * B + i] = valid ? bk : -1;
+    if (lane == 0) list[W + i] = valid ? bk : qbc;
+  }
+  // window and global entries
+  if (lane < W) list[lane] = max(max(qbc - lane, 0), ds_l);
+  if (lane < G) list[W + B + lane] = min(ds_p + lane, qbc);
+  if (lane >= A.L && lane < A.N) list[lane] = INT_MAX;
+  __syncthreads();
+  wave_bitonic_sort(list, A.N);
+  int n = wave_pack_sorted(list, A.L, kv_idx + rowq * A.L, active);
+  if (active && lane == 0) kv_num[rowq] = n;
+}
+
+}  // namespace scope
+
+using namespace scope;
+
+extern "C" {
+
+int scope_doc_starts(const int32_t* docs, int64_t T, int bs, int doc_clamp, int reset_len, int32_t* ds_ptr,
+                     int32_t* ds_local, int32_t* ds_tok_end, void* stream) {
+  SCOPE_REQUIRE(docs && ds_ptr && ds_local && ds_tok_end, "scope_doc_starts: null pointer");
+  SCOPE_REQUIRE(bs > 0 && T > 0 && T % bs == 0, "scope_doc_starts: T=%lld must be a positive multiple of bs=%d",
+                (long long)T, bs);
+  SCOPE_REQUIRE(T < (1ll << 31), "scope_doc_starts: T=%lld exceeds int32 token indices", (long long)T);
+  const int NB = static_cast<int>(T / bs);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(doc_blocks_kernel, dim3(NB), dim3(256), 0, s, docs, T, bs, ds_tok_end, ds_local);
+  int rc = check_launch("doc_blocks_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(doc_scan_kernel, dim3(1), dim3(1024), 0, s, NB, bs, doc_clamp, reset_len, ds_ptr, ds_local,
+                     ds_tok_end);
+  return check_launch("doc_scan_kernel");
+}
+
+int scope_ptr_ref_maxkv(const scope_ptr_ref_params* p) {
+  if (!p || p->bs <= 0) return 0;
+  const int NB = static_cast<int>(p->T / p->bs);
+  const int local = min(max(1, p->local_blocks), NB);
+  const int np = p->ptr_half_blocks > 0 ? p->M * (2 * p->ptr_half_blocks + 1) : p->M;
+  const int gmax = min(max(p->global_blocks_cfg, 0), NB);
+  return local + np + gmax;
+}
+
+int scope_pointer_mask_ref(const scope_ptr_ref_params* p, const float* delta_star, const float* budget_logits,
+                           const float* gumbel_u, const int32_t* ds_ptr, const int32_t* ds_local, int32_t* kv_num,
+                           int32_t* kv_idx, int32_t* radius, int32_t* centre, void* stream) {
+  SCOPE_REQUIRE(p && delta_star && budget_logits && ds_ptr && ds_local && kv_num && kv_idx && radius && centre,
+                "scope_pointer_mask_ref: null pointer");
+  SCOPE_REQUIRE(p->bs > 0 && p->T > 0 && p->T % p->bs == 0, "scope_pointer_mask_ref: T=%lld not a multiple of bs=%d",
+                (long long)p->T, p->bs);
+  SCOPE_REQUIRE(p->M >= 1 && p->M <= kMaxPeaks, "scope_pointer_mask_ref: M=%d outside [1, %d]", p->M, kMaxPeaks);
+  SCOPE_REQUIRE(p->H >= 1, "scope_pointer_mask_ref: H=%d", p->H);
+  SCOPE_REQUIRE(p->ptr_half_blocks >= 0 && p->local_blocks >= 1, "scope_pointer_mask_ref: bad local/half blocks");
+  SCOPE_REQUIRE(p->gumbel_k == 0 || gumbel_u, "scope_pointer_mask_ref: Gumbel active but no uniforms given");
+  SCOPE_REQUIRE(p->T < (1ll << 24), "scope_pointer_mask_ref: T=%lld: token indices must stay exact in fp32",
+                (long long)p->T);
+  RefLaunch A;
+  A.p = *p;
+  A.NB = static_cast<int>(p->T / p->bs);
+  A.p.local_blocks = min(max(1, p->local_blocks), A.NB);
+  A.NP = p->ptr_half_blocks > 0 ? p->M * (2 * p->ptr_half_blocks + 1) : p->M;
+  A.gmax = min(max(p->global_blocks_cfg, 0), A.NB);
+  A.L = A.p.local_blocks + A.NP + A.gmax;
+  A.N = next_pow2(A.L);
+  SCOPE_REQUIRE(A.N <= kMaxList, "scope_pointer_mask_ref: list length %d exceeds %d", A.L, kMaxList);
+  const int64_t rows = static_cast<int64_t>(p->H) * A.NB;
+  const size_t shm = 4 * A.N * sizeof(int) + 4 * 5 * kMaxPeaks * sizeof(float);
+  hipLaunchKernelGGL(ptr_ref_kernel, dim3(ceil_div(rows, 4)), dim3(256), shm, as_stream(stream), A, delta_star,
+                     budget_logits, gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, radius, centre);
+  return check_launch("ptr_ref_kernel");
+}
+
+int scope_block_means(const uint16_t* q, const uint16_t* k, int H, int64_t T, int D, int bs, int64_t q_sh,
+                      int64_t q_st, int64_t k_sh, int64_t k_st, float* qbar, float* kbar, void* stream) {
+  SCOPE_REQUIRE(q && k && qbar && kbar, "scope_block_means: null pointer");
+  SCOPE_REQUIRE(D == 64 || D == 128, "scope_block_means: D=%d (supported: 64, 128)", D);
+  SCOPE_REQUIRE(bs > 0 && T % bs == 0, "scope_block_means: T=%lld not a multiple of bs=%d", (long long)T, bs);
+  SCOPE_REQUIRE(q_st % 8 == 0 && k_st % 8 == 0 && q_sh % 8 == 0 && k_sh % 8 == 0,
+                "scope_block_means: strides must keep 16-byte row alignment");
+  const int NB = static_cast<int>(T / bs);
+  dim3 grid(NB, H);
+  if (D == 128)
+    hipLaunchKernelGGL(block_means_kernel<128>, grid, dim3(256), 0, as_stream(stream), q, k, bs, q_sh, q_st, k_sh,
+                       k_st, NB, qbar, kbar);
+  else
+    hipLaunchKernelGGL(block_means_kernel<64>, grid, dim3(256), 0, as_stream(stream), q, k, bs, q_sh, q_st, k_sh,
+                       k_st, NB, qbar, kbar);
+  return check_launch("block_means_kernel");
+}
+
+int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, const float* kbar,
+                         const float* logits_in, const float* prior, const float* gumbel_u, const int32_t* ds_ptr,
+                         const int32_t* ds_local, int32_t* kv_num, int32_t* kv_idx, int32_t* picks,
+                         float* logits_out, void* stream) {
+  SCOPE_REQUIRE(p && ds_ptr && ds_local && kv_num && kv_idx && picks, "scope_pointer_select: null pointer");
+  SCOPE_REQUIRE(logits_in || (qbar && kbar), "scope_pointer_select: need logits_in or qbar/kbar");
+  SCOPE_REQUIRE(p->D == 64 || p->D == 128, "scope_pointer_select: D=%d (supported: 64, 128)", p->D);
+  SCOPE_REQUIRE(p->budget >= 0 && p->budget <= kMaxBudget, "scope_pointer_select: budget=%d outside [0, %d]",
+                p->budget, kMaxBudget);
+  SCOPE_REQUIRE(p->window >= 1 && p->n_global >= 0, "scope_pointer_select: window >= 1 and n_global >= 0 required");
+  SCOPE_REQUIRE(p->NB >= 1 && p->H >= 1, "scope_pointer_select: bad NB/H");
+  SCOPE_REQUIRE(p->noise_mode >= 0 && p->noise_mode <= 2, "scope_pointer_select: noise_mode %d", p->noise_mode);
+  SCOPE_REQUIRE(p->noise_mode != 1 || gumbel_u, "scope_pointer_select: noise_mode 1 needs gumbel_u");
+  SCOPE_REQUIRE(p->temp > 0.f, "scope_pointer_select: temp must be > 0");
+  ScoreLaunch A;
+  A.p = *p;
+  A.L = min(p->window, p->NB) + p->budget + min(p->n_global, p->NB);
+  A.N = next_pow2(A.L);
+  SCOPE_REQUIRE(A.N <= 64, "scope_pointer_select: list length %d exceeds 64", A.L);
+  dim3 grid(ceil_div(p->NB, 4), p->H);
+  if (p->D == 128)
+    hipLaunchKernelGGL(ptr_score_kernel<128>, grid, dim3(256), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
+                       gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, picks, logits_out);
+  else
+    hipLaunchKernelGGL(ptr_score_kernel<64>, grid, dim3(256), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
+                       gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, picks, logits_out);
+  return check_launch("ptr_score_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,335 @@
+"""torch-facing wrappers of the C ABI: allocate outputs with torch's caching
+allocator on the inputs' device, pass raw device pointers and the current
+stream, raise ``ScopeLibraryError`` on failure.  Every function here requires
+GPU tensors; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import torch
+
+from . import _lib
+from ._lib import AttnParams, PtrRefParams, PtrScoreParams, StatsParams, call, query
+
+BIAS_MODES = {"none": 0, "block": 1, "token": 2}
+GATE_KINDS = {"none": 0, "softplus": 1, "relu": 2}
+
+# counts layout (include/scope_amd.h SCOPE_ST_*)
+ST_DELTA_TOKENS, ST_DELTA_BLOCKS, ST_CENTER = 0, 16, 31
+ST_DOCSTART, ST_OUTSIDE, ST_BLOCK0, ST_BLOCK0_EXCL, ST_N_CENTRES, ST_N_CENTRES_EXCL = 46, 47, 48, 49, 50, 51
+ST_PTR_DIST, ST_BS_OUTSIDE, ST_BS_BLOCK0, ST_BS_BLOCK0_EXCL, ST_BS_DOCSTART, ST_BS_N, ST_BS_N_EXCL = (
+    52, 67, 68, 69, 70, 71, 72)
+ST_RADIUS0, ST_N_RADIUS, ST_FIXED = 73, 74, 75
+SV_NAMES = ["pi_entropy_mean", "ptr_docstart_frac", "ptr_outside_local_frac", "ptr_block0_frac",
+            "ptr_block0_frac_excl", "ptr_radius0_frac", "bs_ptr_outside_local_frac", "bs_ptr_block0_frac",
+            "bs_ptr_block0_frac_excl", "bs_ptr_docstart_frac"]
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _gpu(name: str, *ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"{name}: tensors must live on the GPU (got {t.device}); there is no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{name}: tensors on different devices ({dev} vs {t.device})")
+    if dev is None:
+        raise RuntimeError(f"{name}: no GPU tensor given")
+    return dev
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
+
+
+def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
+    return None if t is None else (t if (t.dtype == torch.float32 and t.is_contiguous()) else t.float().contiguous())
+
+
+def _bhtd(name: str, x: torch.Tensor):
+    """[1,H,T,D] or [H,T,D] with unit last stride -> (H, T, D, stride_h, stride_t)."""
+    if x.dim() == 4:
+        if x.shape[0] != 1:
+            raise RuntimeError(f"{name}: batch size must be 1 (got {x.shape[0]})")
+        _, H, T, D = x.shape
+        sh, st, sd = x.stride(1), x.stride(2), x.stride(3)
+    elif x.dim() == 3:
+        H, T, D = x.shape
+        sh, st, sd = x.stride()
+    else:
+        raise RuntimeError(f"{name}: expected [1,H,T,D] or [H,T,D], got {tuple(x.shape)}")
+    if sd != 1:
+        raise RuntimeError(f"{name}: last dimension must be contiguous")
+    return H, T, D, sh, st
+
+
+# ---------------------------------------------------------------------------
+def doc_starts(docs: torch.Tensor, bs: int, *, doc_clamp: bool = True, reset_len: int = 0):
+    """(ds_ptr, ds_local, ds_tok_end) int32 [QB] (model/attn_bias.py:688-709)."""
+    dev = _gpu("doc_starts", docs)
+    docs = _i32(docs.reshape(-1))
+    T = docs.numel()
+    if T % bs:
+        raise RuntimeError(f"doc_starts: T={T} not a multiple of bs={bs}")
+    NB = T // bs
+    out = torch.empty((3, NB), dtype=torch.int32, device=dev)
+    call("scope_doc_starts", _p(docs), T, int(bs), int(bool(doc_clamp)), int(max(0, reset_len)), _p(out[0]),
+         _p(out[1]), _p(out[2]), _stream(dev))
+    return out[0], out[1], out[2]
+
+
+def pointer_mask_ref(delta_star: torch.Tensor, budget_logits: torch.Tensor, ds_ptr: torch.Tensor,
+                     ds_local: torch.Tensor, *, bs: int, local_blocks: int, ptr_half_blocks: int,
+                     global_blocks_cfg: int, global_active: int, radius_mode: str, budget_rem: int,
+                     budget_temp: float, mask_active: bool, half_active: int, rep_mode: str = "last",
+                     gumbel_k: int = 0, gumbel_tau: float = 1.0, gumbel_u: torch.Tensor | None = None,
+                     eps: float = 1e-9):
+    """Reference-mode pointer mask -> (kv_num [H,QB], kv_idx [H,QB,MAXKV], radius, centre)."""
+    dev = _gpu("pointer_mask_ref", delta_star, budget_logits, ds_ptr, ds_local, gumbel_u)
+    ds4 = delta_star.float() if delta_star.dtype != torch.float32 else delta_star
+    bl4 = budget_logits.float() if budget_logits.dtype != torch.float32 else budget_logits
+    if ds4.dim() == 4:
+        ds4, bl4 = ds4[0], bl4[0]
+    if ds4.stride() != bl4.stride() or ds4.stride(-1) != 1:
+        ds4, bl4 = ds4.contiguous(), bl4.contiguous()
+    H, T, M = ds4.shape
+    prm = PtrRefParams(H=H, M=M, bs=bs, T=T, stride_h=ds4.stride(0), stride_t=ds4.stride(1),
+                       rep_mean=int(rep_mode == "mean"), local_blocks=int(local_blocks),
+                       ptr_half_blocks=int(ptr_half_blocks), global_blocks_cfg=int(global_blocks_cfg),
+                       global_active=int(global_active), radius_mode_pi=int(radius_mode == "pi"),
+                       budget_rem=int(budget_rem), budget_temp=float(max(budget_temp, 1e-6)),
+                       mask_active=int(bool(mask_active)), half_active=int(half_active), gumbel_k=int(gumbel_k),
+                       gumbel_tau=float(max(gumbel_tau, 1e-6)), eps=float(eps))
+    L = query("scope_ptr_ref_maxkv", C.byref(prm))
+    QB = T // bs
+    kv_num = torch.empty((H, QB), dtype=torch.int32, device=dev)
+    kv_idx = torch.empty((H, QB, L), dtype=torch.int32, device=dev)
+    radius = torch.empty((H, QB, M), dtype=torch.int32, device=dev)
+    centre = torch.empty((H, QB, M), dtype=torch.int32, device=dev)
+    gu = _f32(gumbel_u) if gumbel_k > 0 else None
+    call("scope_pointer_mask_ref", C.byref(prm), _p(ds4), _p(bl4), _p(gu), _p(_i32(ds_ptr)), _p(_i32(ds_local)),
+         _p(kv_num), _p(kv_idx), _p(radius), _p(centre), _stream(dev))
+    return kv_num, kv_idx, radius, centre
+
+
+def block_means(q: torch.Tensor, k: torch.Tensor, bs: int):
+    """Block means q̄, k̄ [H, NB, D] fp32 of bf16 q, k."""
+    dev = _gpu("block_means", q, k)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise RuntimeError("block_means: q and k must be bfloat16")
+    H, T, D, qsh, qst = _bhtd("block_means q", q)
+    _, _, _, ksh, kst = _bhtd("block_means k", k)
+    NB = T // bs
+    qbar = torch.empty((H, NB, D), dtype=torch.float32, device=dev)
+    kbar = torch.empty((H, NB, D), dtype=torch.float32, device=dev)
+    call("scope_block_means", _p(q), _p(k), H, T, D, bs, qsh, qst, ksh, kst, _p(qbar), _p(kbar), _stream(dev))
+    return qbar, kbar
+
+
+def pointer_select(ds_ptr: torch.Tensor, ds_local: torch.Tensor, *, bs: int, NB: int, H: int, window: int,
+                   n_global: int, budget: int, qbar: torch.Tensor | None = None, kbar: torch.Tensor | None = None,
+                   logits_in: torch.Tensor | None = None, prior: torch.Tensor | None = None, temp: float = 1.0,
+                   logit_scale: float = 1.0, noise: str = "none", gumbel_u: torch.Tensor | None = None,
+                   seed: int = 0, eps: float = 1e-9, return_logits: bool = False):
+    """Block-scoring selection -> (kv_num [H,QB], kv_idx [H,QB,W+budget+G], picks [H,QB,budget][, logits])."""
+    dev = _gpu("pointer_select", ds_ptr, ds_local, qbar, kbar, logits_in, prior, gumbel_u)
+    noise_mode = {"none": 0, "uniform": 1, "counter": 2}[noise]
+    D = qbar.shape[-1] if qbar is not None else 128
+    pstride = 0
+    if prior is not None:
+        prior = _f32(prior)
+        pstride = NB if prior.dim() == 2 else 0
+    prm = PtrScoreParams(H=H, NB=NB, D=D, bs=bs, window=window, n_global=n_global, budget=budget,
+                         temp=float(temp), logit_scale=float(logit_scale), noise_mode=noise_mode,
+                         seed=int(seed) & 0xFFFFFFFFFFFFFFFF, eps=float(eps), prior_head_stride=pstride)
+    L = min(window, NB) + budget + min(n_global, NB)
+    kv_num = torch.empty((H, NB), dtype=torch.int32, device=dev)
+    kv_idx = torch.empty((H, NB, L), dtype=torch.int32, device=dev)
+    picks = torch.empty((H, NB, max(budget, 1)), dtype=torch.int32, device=dev)
+    logits = torch.empty((H, NB, NB), dtype=torch.float32, device=dev) if return_logits else None
+    call("scope_pointer_select", C.byref(prm), _p(_f32(qbar)), _p(_f32(kbar)), _p(_f32(logits_in)), _p(prior),
+         _p(_f32(gumbel_u) if noise_mode == 1 else None), _p(_i32(ds_ptr)), _p(_i32(ds_local)), _p(kv_num),
+         _p(kv_idx), _p(picks), _p(logits), _stream(dev))
+    picks = picks[..., :budget]
+    return (kv_num, kv_idx, picks, logits) if return_logits else (kv_num, kv_idx, picks)
+
+
+def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int):
+    """q lists (CSR): q_off [H, NB+1], q_list [H, QB*MAXKV]."""
+    dev = _gpu("transpose_blocks", kv_num, kv_idx)
+    kv_num = _i32(kv_num.reshape(kv_num.shape[-2], kv_num.shape[-1]))
+    H, QB = kv_num.shape
+    kv_idx = _i32(kv_idx.reshape(H, QB, kv_idx.shape[-1]))
+    maxkv = kv_idx.shape[-1]
+    q_off = torch.empty((H, NB + 1), dtype=torch.int32, device=dev)
+    q_list = torch.empty((H, QB * maxkv), dtype=torch.int32, device=dev)
+    ws = torch.empty(max(1, query("scope_transpose_workspace_bytes", H, NB)), dtype=torch.uint8, device=dev)
+    call("scope_transpose_blocks", _p(kv_num), _p(kv_idx), H, QB, NB, maxkv, _p(q_off), _p(q_list), _p(ws),
+         _stream(dev))
+    return q_off, q_list
+
+
+def mask_stats(*, H: int, QB: int, bs: int, M: int = 0, delta_star: torch.Tensor | None = None,
+               pi: torch.Tensor | None = None, rep_mode: str = "last", has_docs: bool = False,
+               docstart_enabled: bool = False, local_blocks_cfg: int = 1, eps: float = 1e-9,
+               ds_ptr_fwd: torch.Tensor | None = None, ds_local_fwd: torch.Tensor | None = None,
+               kv_num: torch.Tensor | None = None, radius: torch.Tensor | None = None, maxkv_bins: int = 1,
+               radius_bins: int = 1, extra_bins: int = 1, picks: torch.Tensor | None = None,
+               ds_ptr: torch.Tensor | None = None, ds_local: torch.Tensor | None = None,
+               bs_local_blocks: int = 1):
+    """Fused statistics -> (counts int32, values fp32 [SCOPE_SV_COUNT])."""
+    dev = _gpu("mask_stats", delta_star, pi, kv_num, radius, picks)
+    sh = st = 0
+    T = QB * bs
+    if delta_star is not None:
+        d3, p3 = (delta_star[0], pi[0]) if delta_star.dim() == 4 else (delta_star, pi)
+        d3, p3 = _f32(d3), _f32(p3)
+        sh, st = d3.stride(0), d3.stride(1)
+        M = d3.shape[-1]
+    else:
+        d3 = p3 = None
+    budget = picks.shape[-1] if picks is not None else 0
+    prm = StatsParams(H=H, QB=QB, bs=bs, M=M, T=T, stride_h=sh, stride_t=st, rep_mean=int(rep_mode == "mean"),
+                      has_docs=int(has_docs), docstart_enabled=int(docstart_enabled),
+                      local_blocks_cfg=int(local_blocks_cfg), eps=float(eps), maxkv_bins=int(maxkv_bins),
+                      radius_bins=int(radius_bins), extra_bins=int(extra_bins), budget=int(budget),
+                      bs_local_blocks=int(bs_local_blocks))
+    n = query("scope_stats_counts_len", C.byref(prm))
+    counts = torch.empty(n, dtype=torch.int32, device=dev)
+    values = torch.zeros(len(SV_NAMES), dtype=torch.float32, device=dev)
+    ws = torch.empty(max(4, query("scope_stats_workspace_bytes", C.byref(prm))), dtype=torch.uint8, device=dev)
+    call("scope_mask_stats", C.byref(prm), _p(d3), _p(p3), _p(_i32(ds_ptr_fwd) if ds_ptr_fwd is not None else None),
+         _p(_i32(ds_local_fwd) if ds_local_fwd is not None else None),
+         _p(_i32(kv_num) if kv_num is not None else None), _p(_i32(radius) if radius is not None else None),
+         _p(_i32(picks.contiguous()) if picks is not None else None),
+         _p(_i32(ds_ptr) if ds_ptr is not None else None), _p(_i32(ds_local) if ds_local is not None else None),
+         _p(counts), _p(values), _p(ws), _stream(dev))
+    return counts, values
+
+
+def unpack_counts(counts: torch.Tensor, maxkv_bins: int, radius_bins: int) -> dict:
+    c = counts
+    out = dict(delta_tokens_hist=c[ST_DELTA_TOKENS:ST_DELTA_TOKENS + 16],
+               delta_blocks_hist=c[ST_DELTA_BLOCKS:ST_DELTA_BLOCKS + 15],
+               ptr_center_hist=c[ST_CENTER:ST_CENTER + 15],
+               ptr_dist_hist=c[ST_PTR_DIST:ST_PTR_DIST + 15],
+               kv_unique_hist=c[ST_FIXED:ST_FIXED + maxkv_bins],
+               ptr_radius_hist=c[ST_FIXED + maxkv_bins:ST_FIXED + maxkv_bins + radius_bins],
+               ptr_extra_sum_hist=c[ST_FIXED + maxkv_bins + radius_bins:])
+    for name, i in (("docstart", ST_DOCSTART), ("outside", ST_OUTSIDE), ("block0", ST_BLOCK0),
+                    ("block0_excl", ST_BLOCK0_EXCL), ("n_centres", ST_N_CENTRES), ("bs_outside", ST_BS_OUTSIDE),
+                    ("bs_block0", ST_BS_BLOCK0), ("bs_block0_excl", ST_BS_BLOCK0_EXCL),
+                    ("bs_docstart", ST_BS_DOCSTART), ("bs_n", ST_BS_N), ("bs_n_excl", ST_BS_N_EXCL),
+                    ("radius0", ST_RADIUS0), ("n_radius", ST_N_RADIUS)):
+        out[name] = c[i]
+    return out
+
+
+def spectral_table(omegas: torch.Tensor, T: int, bs: int, mode: str) -> torch.Tensor:
+    """cos/sin(ω_k r) tables (model/attn_bias.py:326-340 restated per block or token)."""
+    dev = _gpu("spectral_table", omegas)
+    m = BIAS_MODES[mode]
+    om = _f32(omegas.reshape(-1))
+    K = om.numel()
+    nbytes = query("scope_spectral_table_bytes", m, T, bs)
+    tab = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    call("scope_spectral_table", m, _p(om), K, T, bs, _p(tab), _stream(dev))
+    return tab
+
+
+def _attn_params(q, k, v, out, *, bs, maxkv, scale, beta, bias_mode, K, use_slope, subtract_b0, gate_kind,
+                 ramp_lambda, tau) -> AttnParams:
+    H, T, D, qsh, qst = _bhtd("attention q", q)
+    _, _, _, ksh, kst = _bhtd("attention k", k)
+    _, _, _, vsh, vst = _bhtd("attention v", v)
+    _, _, _, osh, ost = _bhtd("attention out", out)
+    if not (q.shape == k.shape == v.shape):
+        raise RuntimeError(f"attention: q, k, v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    for n_, x in (("q", q), ("k", k), ("v", v)):
+        if x.dtype != torch.bfloat16:
+            raise RuntimeError(f"attention: {n_} must be bfloat16 (got {x.dtype})")
+    return AttnParams(H=H, D=D, bs=bs, maxkv=maxkv, T=T, scale=float(scale), beta=float(beta),
+                      bias_mode=int(bias_mode), K=int(K), use_slope=int(bool(use_slope)),
+                      subtract_b0=int(bool(subtract_b0)), gate_kind=int(gate_kind), ramp_lambda=float(ramp_lambda),
+                      tau=float(tau), q_sh=qsh, q_st=qst, k_sh=ksh, k_st=kst, v_sh=vsh, v_st=vst, o_sh=osh, o_st=ost)
+
+
+def empty_like_layout(x: torch.Tensor) -> torch.Tensor:
+    """New tensor with x's shape and memory order (like FlexAttention's output)."""
+    return torch.empty_like(x)
+
+
+def attn_fwd(q, k, v, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float, beta: float = 0.5,
+             bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None, slope=None,
+             delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
+             ramp_lambda=0.0, tau=64.0, out=None):
+    """Block-sparse attention forward -> (out like q, lse [1,H,T] fp32, natural log)."""
+    dev = _gpu("attn_fwd", q, k, v, kv_num, kv_idx, docs, ds_tok_end)
+    out = empty_like_layout(q) if out is None else out
+    kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
+    m = BIAS_MODES[bias_mode]
+    K = coeff_cos.shape[-1] if (m and coeff_cos is not None) else 0
+    prm = _attn_params(q, k, v, out, bs=bs, maxkv=kv_idx3.shape[-1], scale=scale, beta=beta, bias_mode=m, K=K,
+                       use_slope=use_slope, subtract_b0=subtract_b0, gate_kind=GATE_KINDS[gate_kind],
+                       ramp_lambda=ramp_lambda, tau=tau)
+    H, T = prm.H, prm.T
+    lse = torch.empty((1, H, T), dtype=torch.float32, device=dev)
+    call("scope_attn_fwd", C.byref(prm), _p(q), _p(k), _p(v), _p(_i32(kv_num)), _p(kv_idx3),
+         _p(_i32(docs.reshape(-1))), _p(_i32(ds_tok_end)), _p(table), _p(_f32(coeff_cos)), _p(_f32(coeff_sin)),
+         _p(_f32(b0)), _p(_f32(slope)), _p(_f32(delta_main)), _p(_f32(width)), _p(out), _p(lse), _stream(dev))
+    return out, lse
+
+
+def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
+             beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
+             slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
+             ramp_lambda=0.0, tau=64.0, need_coeff_grads: bool = True):
+    """Block-sparse attention backward -> dict of gradients."""
+    dev = _gpu("attn_bwd", q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list)
+    kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
+    m = BIAS_MODES[bias_mode]
+    K = coeff_cos.shape[-1] if (m and coeff_cos is not None) else 0
+    dq, dk, dv = empty_like_layout(q), empty_like_layout(k), empty_like_layout(v)
+    prm = _attn_params(q, k, v, dq, bs=bs, maxkv=kv_idx3.shape[-1], scale=scale, beta=beta, bias_mode=m, K=K,
+                       use_slope=use_slope, subtract_b0=subtract_b0, gate_kind=GATE_KINDS[gate_kind],
+                       ramp_lambda=ramp_lambda, tau=tau)
+    for name, a_, b_ in (("k", k, dk), ("v", v, dv), ("out", out, dout)):
+        if a_.stride() != b_.stride():
+            raise RuntimeError(f"attn_bwd: {name} and its gradient must share strides")
+    if dout.stride() != q.stride() or out.stride() != q.stride():
+        raise RuntimeError("attn_bwd: out and dout must share q's strides")
+    H, T = prm.H, prm.T
+    z = dict(dtype=torch.float32, device=dev)
+    dcc = torch.empty((1, H, T, K), **z) if (m and need_coeff_grads) else None
+    dcs = torch.empty((1, H, T, K), **z) if (m and need_coeff_grads) else None
+    tok = m == 2 and need_coeff_grads
+    db0 = torch.empty((1, H, T), **z) if (tok and subtract_b0) else None
+    dsl = torch.empty((1, H, T), **z) if (tok and use_slope) else None
+    gate = tok and GATE_KINDS[gate_kind] != 0
+    ddm = torch.empty((1, H, T), **z) if gate else None
+    dwd = torch.empty((1, H, T), **z) if gate else None
+    ws = torch.empty(max(16, query("scope_attn_bwd_workspace_bytes", C.byref(prm))), dtype=torch.uint8, device=dev)
+    call("scope_attn_bwd", C.byref(prm), _p(q), _p(k), _p(v), _p(out), _p(dout), _p(_f32(lse)), _p(_i32(kv_num)),
+         _p(kv_idx3), _p(_i32(q_off)), _p(_i32(q_list)), _p(_i32(docs.reshape(-1))), _p(_i32(ds_tok_end)),
+         _p(table), _p(_f32(coeff_cos)), _p(_f32(coeff_sin)), _p(_f32(b0)), _p(_f32(slope)), _p(_f32(delta_main)),
+         _p(_f32(width)), _p(dq), _p(dk), _p(dv), _p(dcc), _p(dcs), _p(db0), _p(dsl), _p(ddm), _p(dwd), _p(ws),
+         _stream(dev))
+    return dict(dq=dq, dk=dk, dv=dv, dcoeff_cos=dcc, dcoeff_sin=dcs, db0=db0, dslope=dsl, ddelta_main=ddm,
+                dwidth=dwd)
+
+
+def log2e() -> float:
+    return 1.0 / math.log(2.0)

@@ -1,0 +1,453 @@
+"""``SpectralBias``: the call surface of ``model/attn_bias.py:68-874`` with the
+pointer mask, its statistics and the attention running on the gfx950 kernels.
+
+* constructor, configuration checks and schedule setters mirror
+  ``model/attn_bias.py:75-377`` (same keyword names, same ValueErrors);
+* ``forward`` is the coefficient head (``:379-478``, torch ops, any device)
+  plus the regularisers (``:480-508``); its debug statistics (``:510-606``)
+  run in the fused statistics kernel (GPU only) without host syncs;
+* ``build_pointer_blockmask`` (``:623-873``) runs the doc-start and
+  reference-mode pointer kernels and returns a ``ScopeBlockMask``;
+* ``build_blockscore_mask`` is the block-mean q·k selection (this project's
+  block-scoring mode).
+
+The scheduled state lives both in the reference's int buffers and in Python
+integers, so that no kernel argument needs a ``.item()`` sync.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from . import ops
+from .attention import SpectralTerms
+from .blockmask import ScopeBlockMask
+
+TOKEN_EDGES = [0, 127, 255, 511, 1023, 2047, 4095, 8191, 16383, 32767, 65535, 131071, 262143, 524287, 1048575]
+BLOCK_EDGES = [0, 1, 3, 7, 15, 31, 63, 127, 255, 511, 1023, 2047, 4095, 8191]
+
+
+class SpectralBias(nn.Module):
+    """Query-conditioned Fourier bias over Δ = q_idx - kv_idx plus the
+    pointer-driven block mask (model/attn_bias.py:68-73)."""
+
+    def __init__(self, *, head_dim: int, num_heads: int, L_train: int, L_max: int = 1_000_000, K: int = 6,
+                 M: int = 2, beta: float = 0.5, ramp_lambda: float = 0.2, tau: float = 64.0,
+                 w_min: float | None = None, w_max: float | None = None, share_across_heads: bool = True,
+                 use_slope: bool = True, gate_kind: str = "softplus", c_scale: float = 0.01,
+                 width_min: float = 32.0, width_max: float = 256.0, delta_star_max: int | None = None,
+                 detach_q: bool = False, subtract_b0: bool = True, eps: float = 1e-9,
+                 use_pointer_mask: bool = False, pointer_local_blocks: int = 16, pointer_half_blocks: int = 4,
+                 pointer_global_blocks: int = 0, pointer_budget_blocks: int = 0,
+                 pointer_budget_is_total: bool = True, pointer_budget_temp: float = 1.0,
+                 pointer_radius_mode: str = "pi", pointer_qblock_rep: str = "last", pointer_doc_clamp: bool = True,
+                 gumbel_topk: bool = False, gumbel_topk_k: int = 0, gumbel_topk_tau: float = 1.0,
+                 gumbel_topk_seed: int = 0, pointer_reset_len: int = 0, lambda_omega: float = 1e-5,
+                 lambda_zero_mean: float = 1e-4, lambda_entropy: float = 1e-4, pi_entropy_floor_frac: float = 0.25,
+                 lambda_delta_edge: float = 0.0, delta_edge_eps: float = 0.0, debug_stats: bool = False,
+                 enabled: bool = True):
+        super().__init__()
+        # configuration checks: model/attn_bias.py:124-131, 159-163, 222-223
+        if K <= 0:
+            raise ValueError("K must be positive")
+        if M <= 0:
+            raise ValueError("M must be positive")
+        if gate_kind not in {"none", "softplus", "relu"}:
+            raise ValueError("gate_kind must be one of: none|softplus|relu")
+        if not share_across_heads and num_heads <= 0:
+            raise ValueError("num_heads must be set when share_across_heads=False")
+        self.enabled = enabled
+        self.head_dim, self.num_heads, self.K, self.M = head_dim, num_heads, K, M
+        self.beta, self.ramp_lambda, self.tau = float(beta), float(ramp_lambda), float(tau)
+        self.gate_kind = gate_kind
+        self.share_across_heads = share_across_heads
+        self.use_slope = use_slope
+        self.c_scale = float(c_scale)
+        self.width_min, self.width_max = float(width_min), float(width_max)
+        self.delta_star_max = int(delta_star_max) if delta_star_max is not None else int(L_train - 1)
+        self.detach_q, self.subtract_b0, self.eps = detach_q, subtract_b0, float(eps)
+        self.use_pointer_mask = bool(use_pointer_mask)
+        self.pointer_local_blocks = int(pointer_local_blocks)
+        self.pointer_half_blocks = int(pointer_half_blocks)
+        self.pointer_global_blocks = int(pointer_global_blocks)
+        self.pointer_budget_blocks = int(pointer_budget_blocks)
+        self.pointer_budget_is_total = bool(pointer_budget_is_total)
+        self.pointer_budget_temp = float(pointer_budget_temp)
+        self.pointer_radius_mode = str(pointer_radius_mode).strip().lower()
+        if self.pointer_radius_mode not in {"fixed", "pi"}:
+            raise ValueError("pointer_radius_mode must be one of: fixed|pi")
+        self.pointer_qblock_rep = str(pointer_qblock_rep)
+        if self.pointer_qblock_rep not in {"last", "mean"}:
+            raise ValueError("pointer_qblock_rep must be one of: last|mean")
+        self.pointer_doc_clamp = bool(pointer_doc_clamp)
+        self.gumbel_topk = bool(gumbel_topk)
+        self.gumbel_topk_k = int(gumbel_topk_k)
+        self.gumbel_topk_tau = float(gumbel_topk_tau)
+        self.gumbel_topk_seed = int(gumbel_topk_seed)
+        self.pointer_reset_len = int(pointer_reset_len)
+        self.debug_stats = bool(debug_stats)
+        # scheduled state: buffers (model/attn_bias.py:171-206) + host mirror
+        self._st = dict(mask=1 if self.use_pointer_mask else 0,
+                        half=self.pointer_half_blocks if self.use_pointer_mask else 0,
+                        glob=self.pointer_global_blocks if self.use_pointer_mask else 0,
+                        reset=0, reset_len=max(0, self.pointer_reset_len), seed=self.gumbel_topk_seed,
+                        dmax=self.delta_star_max, edge_eps=float(delta_edge_eps))
+        i32 = dict(dtype=torch.int32)
+        self.register_buffer("_pointer_mask_active", torch.tensor(self._st["mask"], **i32), persistent=False)
+        self.register_buffer("_pointer_half_blocks_active", torch.tensor(self._st["half"], **i32), persistent=False)
+        self.register_buffer("_pointer_global_blocks_active", torch.tensor(self._st["glob"], **i32), persistent=False)
+        self.register_buffer("_pointer_reset_active", torch.tensor(0, **i32), persistent=False)
+        self.register_buffer("_pointer_reset_len_active", torch.tensor(self._st["reset_len"], **i32),
+                             persistent=False)
+        self.register_buffer("_gumbel_seed", torch.tensor(self.gumbel_topk_seed, dtype=torch.int64), persistent=False)
+        self.register_buffer("_delta_star_max_active", torch.tensor(self.delta_star_max, **i32), persistent=False)
+        self.lambda_omega, self.lambda_zero_mean = float(lambda_omega), float(lambda_zero_mean)
+        self.lambda_entropy, self.pi_entropy_floor_frac = float(lambda_entropy), float(pi_entropy_floor_frac)
+        self.lambda_delta_edge, self.delta_edge_eps = float(lambda_delta_edge), float(delta_edge_eps)
+        self.register_buffer("_delta_edge_eps_active", torch.tensor(self.delta_edge_eps, dtype=torch.float32),
+                             persistent=False)
+
+        w_min = float(w_min) if w_min is not None else (2 * math.pi / L_max)
+        w_max = float(w_max) if w_max is not None else (2 * math.pi / L_train)
+        if not (w_min > 0 and w_max > 0 and w_min < w_max):
+            raise ValueError(f"invalid (w_min, w_max)=({w_min}, {w_max})")
+        omegas = torch.logspace(math.log10(w_min), math.log10(w_max), K, dtype=torch.float32)  # :225
+        self.register_buffer("omegas", omegas, persistent=False)
+        self.register_buffer("log_omegas", omegas.log(), persistent=False)
+        self.register_buffer("omega_sq", omegas.square(), persistent=False)
+        self.register_buffer("logw_min", torch.tensor(math.log(w_min), dtype=torch.float32), persistent=False)
+        self.register_buffer("logw_max", torch.tensor(math.log(w_max), dtype=torch.float32), persistent=False)
+        self._trig_cache: dict = {}
+
+        # debug statistics buffers (model/attn_bias.py:239-265)
+        self.register_buffer("_dbg_token_edges", torch.tensor(TOKEN_EDGES, dtype=torch.int64), persistent=False)
+        self.register_buffer("_dbg_block_edges", torch.tensor(BLOCK_EDGES, dtype=torch.int64), persistent=False)
+        z32 = lambda n: torch.zeros(n, dtype=torch.int32)  # noqa: E731
+        self.register_buffer("_dbg_delta_tokens_hist", z32(len(TOKEN_EDGES) + 1), persistent=False)
+        self.register_buffer("_dbg_delta_blocks_hist", z32(len(BLOCK_EDGES) + 1), persistent=False)
+        self.register_buffer("_dbg_ptr_center_hist", z32(len(BLOCK_EDGES) + 1), persistent=False)
+        max_kv = int(self.pointer_local_blocks + (2 * self.pointer_half_blocks + 1) * self.M + self.pointer_global_blocks)
+        self.register_buffer("_dbg_kv_unique_hist", z32(max_kv + 1), persistent=False)
+        for name in ("ptr_outside_local_frac", "ptr_block0_frac", "ptr_block0_frac_excl", "ptr_docstart_frac"):
+            self.register_buffer("_dbg_" + name, torch.zeros((), dtype=torch.float32), persistent=False)
+        self.register_buffer("_dbg_ptr_radius_hist", z32(self.pointer_half_blocks + 1), persistent=False)
+        max_extra = max(1, int(self.pointer_half_blocks * self.M))
+        self.register_buffer("_dbg_ptr_extra_sum_hist", z32(max_extra + 1), persistent=False)
+        for name in ("ptr_radius0_frac", "pi_entropy_mean", "reg_omega", "reg_entropy", "reg_delta_edge",
+                     "reg_zero_mean", "reg_total"):
+            self.register_buffer("_dbg_" + name, torch.zeros((), dtype=torch.float32), persistent=False)
+
+        hidden = max(128, 2 * head_dim)
+        out = 5 * M + (1 if use_slope else 0)
+        if share_across_heads:
+            self.mlp = nn.Sequential(nn.Linear(head_dim, hidden), nn.SiLU(), nn.Linear(hidden, out))
+        else:
+            self.w1 = nn.Parameter(torch.empty(num_heads, hidden, head_dim))
+            self.b1 = nn.Parameter(torch.zeros(num_heads, hidden))
+            self.w2 = nn.Parameter(torch.empty(num_heads, out, hidden))
+            self.b2 = nn.Parameter(torch.zeros(num_heads, out))
+            self._init_per_head_weights()
+        self._init_outputs()
+
+    # ---- initialisation (model/attn_bias.py:280-304)
+    def _init_per_head_weights(self):
+        std1 = 0.5 * (self.head_dim ** -0.5)
+        std2 = 0.5 * (self.w1.size(1) ** -0.5)
+        with torch.no_grad():
+            self.w1.uniform_(-(3 ** 0.5) * std1, (3 ** 0.5) * std1)
+            self.w2.uniform_(-(3 ** 0.5) * std2, (3 ** 0.5) * std2)
+
+    def _init_outputs(self):
+        delta_biases = torch.linspace(-6.0, -4.0, steps=self.M)
+        with torch.no_grad():
+            if self.share_across_heads:
+                last: nn.Linear = self.mlp[-1]
+                last.weight.zero_()
+                last.bias.zero_()
+                last.bias[: self.M].copy_(delta_biases)
+            else:
+                self.w2.zero_()
+                self.b2.zero_()
+                self.b2[:, : self.M].copy_(delta_biases.view(1, self.M).expand(self.num_heads, -1))
+
+    # ---- schedule setters (model/attn_bias.py:342-377)
+    def set_pointer_mask_state(self, *, enabled: bool, half_blocks: int, global_blocks: int | None = None):
+        half_blocks = int(half_blocks)
+        if half_blocks < 0:
+            raise ValueError("half_blocks must be >= 0")
+        half_blocks = min(half_blocks, self.pointer_half_blocks)
+        self._st["mask"] = 1 if enabled else 0
+        self._st["half"] = half_blocks
+        self._pointer_mask_active.fill_(self._st["mask"])
+        self._pointer_half_blocks_active.fill_(half_blocks)
+        if global_blocks is not None:
+            gb = int(global_blocks)
+            if gb < 0:
+                raise ValueError("global_blocks must be >= 0")
+            gb = min(gb, self.pointer_global_blocks)
+            self._st["glob"] = gb
+            self._pointer_global_blocks_active.fill_(gb)
+
+    def set_pointer_reset_state(self, *, enabled: bool, reset_len: int):
+        reset_len = int(reset_len)
+        if reset_len < 0:
+            raise ValueError("reset_len must be >= 0")
+        self._st["reset"] = 1 if enabled else 0
+        self._st["reset_len"] = reset_len if enabled else 0
+        self._pointer_reset_active.fill_(self._st["reset"])
+        self._pointer_reset_len_active.fill_(self._st["reset_len"])
+
+    def set_gumbel_seed(self, *, seed: int):
+        self._st["seed"] = int(seed)
+        self._gumbel_seed.fill_(int(seed))
+
+    def set_delta_star_max_active(self, *, max_tokens: int):
+        max_tokens = int(max_tokens)
+        if max_tokens < 0:
+            raise ValueError("max_tokens must be >= 0")
+        max_tokens = min(max_tokens, int(self.delta_star_max))
+        self._st["dmax"] = max_tokens
+        self._delta_star_max_active.fill_(max_tokens)
+
+    def set_delta_edge_eps_active(self, *, eps: float):
+        eps = float(eps)
+        if eps < 0:
+            raise ValueError("eps must be >= 0")
+        self._st["edge_eps"] = eps
+        self._delta_edge_eps_active.fill_(eps)
+
+    # ---- coefficient head (model/attn_bias.py:306-340, 379-478)
+    def _mlp_forward(self, q: Tensor) -> Tensor:
+        if self.detach_q:
+            q = q.detach()
+        dt = q.dtype
+        if self.share_across_heads:
+            fc1: nn.Linear = self.mlp[0]
+            fc2: nn.Linear = self.mlp[2]
+            x = F.silu(F.linear(q, fc1.weight.to(dt), fc1.bias.to(dt)))
+            return F.linear(x, fc2.weight.to(dt), fc2.bias.to(dt))
+        x = torch.einsum("bhld,hkd->bhlk", q, self.w1.to(dt)) + self.b1.to(dt)[None, :, None, :]
+        x = F.silu(x)
+        return torch.einsum("bhlk,hok->bhlo", x, self.w2.to(dt)) + self.b2.to(dt)[None, :, None, :]
+
+    def _get_trig_tables(self, L: int, device: torch.device):
+        key = (L, device)
+        if key not in self._trig_cache:
+            D = torch.arange(L, device=device, dtype=torch.float32)
+            w = self.omegas.to(device=device)
+            c32 = torch.cos(w[:, None] * D[None, :])
+            s32 = torch.sin(w[:, None] * D[None, :])
+            self._trig_cache = {key: (c32.to(torch.bfloat16), s32.to(torch.bfloat16), c32.mean(-1), s32.mean(-1))}
+        return self._trig_cache[key]
+
+    def forward(self, q: Tensor, *, docs: Tensor | None = None) -> tuple[Tensor, ...]:
+        """q [B,H,L,D] -> the reference's 12-tuple (model/attn_bias.py:385-401)."""
+        B, H, L, Dh = q.shape
+        if H != self.num_heads:
+            raise ValueError(f"expected H={self.num_heads}, got {H}")
+        if Dh != self.head_dim:
+            raise ValueError(f"expected head_dim={self.head_dim}, got {Dh}")
+        device = q.device
+        cos_wD, sin_wD, cos_mean, sin_mean = self._get_trig_tables(L, device)
+        if not self.enabled:
+            z_k = q.new_zeros((B, H, L, self.K), dtype=torch.float32)
+            z_l = q.new_zeros((B, H, L), dtype=torch.float32)
+            z_m = q.new_zeros((B, H, L, self.M), dtype=torch.float32)
+            z_pi = q.new_full((B, H, L, self.M), 1.0 / self.M, dtype=torch.float32)
+            return z_k, z_k, z_l, z_l, z_m, z_pi, z_m, z_l, z_l, cos_wD, sin_wD, q.new_zeros((), dtype=torch.float32)
+        y = self._mlp_forward(q).float()
+        M, K = self.M, self.K
+        delta_raw, mu_raw, sigma_raw, pi_logits, budget_logits = (y[..., i * M:(i + 1) * M] for i in range(5))
+        delta_cap = torch.clamp(self._delta_star_max_active.to(device=device, dtype=torch.float32), 0.0, float(L - 1))
+        delta_star = torch.sigmoid(delta_raw) * delta_cap
+        logw_min, logw_max = self.logw_min.to(device), self.logw_max.to(device)
+        mu = logw_min + (logw_max - logw_min) * torch.sigmoid(mu_raw)
+        sigma = 0.25 + 1.75 * torch.sigmoid(sigma_raw)
+        pi = torch.softmax(pi_logits, dim=-1)
+        if self.use_slope:
+            slope = self.c_scale * torch.tanh(y[..., 5 * M:5 * M + 1]).squeeze(-1)
+        else:
+            slope = q.new_zeros((B, H, L), dtype=torch.float32)
+        logw = self.log_omegas.to(device).view(1, 1, 1, 1, K)
+        a_mk = torch.exp(-((logw - mu.unsqueeze(-1)) ** 2) / (2 * (sigma.unsqueeze(-1) ** 2)))
+        a_mk = a_mk / (a_mk.sum(dim=-1, keepdim=True) + self.eps)
+        phase = self.omegas.to(device).view(1, 1, 1, 1, K) * delta_star.unsqueeze(-1)
+        pi_e = pi.unsqueeze(-1)
+        coeff_cos = (pi_e * a_mk * torch.cos(phase)).sum(dim=3)
+        coeff_sin = (pi_e * a_mk * torch.sin(phase)).sum(dim=3)
+        b0 = coeff_cos.sum(dim=-1) if self.subtract_b0 else q.new_zeros((B, H, L), dtype=torch.float32)
+        main_idx = pi.argmax(dim=-1)
+        delta_main = torch.gather(delta_star, -1, main_idx.unsqueeze(-1)).squeeze(-1)
+        width = self.width_min + (self.width_max - self.width_min) * torch.sigmoid(mu.mean(dim=-1))
+
+        z = q.new_zeros((), dtype=torch.float32)
+        reg_omega = reg_entropy = reg_delta_edge = reg_zero_mean = z
+        if self.training:  # model/attn_bias.py:485-506
+            if self.lambda_omega > 0:
+                reg_omega = self.lambda_omega * (self.omega_sq.to(device).view(1, 1, 1, 1, K) * a_mk.square()).sum(-1).mean()
+            if self.lambda_entropy > 0:
+                entropy = -(pi * (pi + self.eps).log()).sum(dim=-1)
+                h_floor = float(self.pi_entropy_floor_frac) * math.log(M)
+                if h_floor > 0:
+                    reg_entropy = self.lambda_entropy * F.relu(entropy.new_tensor(h_floor) - entropy).mean()
+            if self.lambda_zero_mean > 0:
+                mean_b = ((coeff_cos * cos_mean.to(device)).sum(-1) + (coeff_sin * sin_mean.to(device)).sum(-1)
+                          + slope * (0.5 * float(L - 1)) - b0)
+                reg_zero_mean = self.lambda_zero_mean * mean_b.mean().square()
+            if self.lambda_delta_edge > 0:
+                edge_eps = self._delta_edge_eps_active.to(device=device, dtype=torch.float32)
+                u = (delta_star / torch.clamp(delta_cap, min=1.0)).clamp(0.0, 1.0)
+                edge = F.relu(edge_eps - u) + F.relu(u - (1.0 - edge_eps))
+                reg_delta_edge = self.lambda_delta_edge * edge.mean()
+        reg_loss = reg_omega + reg_entropy + reg_delta_edge + reg_zero_mean
+
+        if self.debug_stats:
+            if B == 1 and L % 128 == 0:
+                self._forward_stats(delta_star.detach(), pi.detach(), docs, L)
+            for name, val in (("reg_omega", reg_omega), ("reg_entropy", reg_entropy),
+                              ("reg_delta_edge", reg_delta_edge), ("reg_zero_mean", reg_zero_mean),
+                              ("reg_total", reg_loss)):
+                getattr(self, "_dbg_" + name).copy_(val.detach())
+        return (coeff_cos, coeff_sin, slope, b0, delta_star, pi, budget_logits, delta_main, width, cos_wD, sin_wD,
+                reg_loss)
+
+    def _forward_stats(self, delta_star: Tensor, pi: Tensor, docs: Tensor | None, L: int, bs: int = 128):
+        """model/attn_bias.py:510-600 in the fused statistics kernel."""
+        QB = L // bs
+        has_docs = docs is not None
+        reset_on = bool(self._st["reset"]) and self._st["reset_len"] > 0
+        ds_ptr = ds_local = None
+        if has_docs:
+            ds_ptr, ds_local, _ = ops.doc_starts(docs, bs, doc_clamp=self.pointer_doc_clamp,
+                                                 reset_len=self._st["reset_len"] if reset_on else 0)
+        counts, values = ops.mask_stats(H=self.num_heads, QB=QB, bs=bs, delta_star=delta_star, pi=pi,
+                                        rep_mode=self.pointer_qblock_rep, has_docs=has_docs,
+                                        docstart_enabled=has_docs and (self.pointer_doc_clamp or bool(self._st["reset"])),
+                                        local_blocks_cfg=self.pointer_local_blocks, eps=self.eps,
+                                        ds_ptr_fwd=ds_ptr, ds_local_fwd=ds_local)
+        c = ops.unpack_counts(counts, 1, 1)
+        self._dbg_delta_tokens_hist.copy_(c["delta_tokens_hist"])
+        self._dbg_delta_blocks_hist.copy_(c["delta_blocks_hist"])
+        self._dbg_ptr_center_hist.copy_(c["ptr_center_hist"])
+        for i, name in enumerate(ops.SV_NAMES[:5]):
+            getattr(self, "_dbg_" + name).copy_(values[i])
+
+    # ---- pointer mask, reference mode (model/attn_bias.py:623-873)
+    @torch.no_grad()
+    def build_pointer_blockmask(self, *, input_seq: Tensor | None = None, docs: Tensor | None = None,
+                                delta_star: Tensor, pi: Tensor, budget_logits: Tensor, block_size: int = 128,
+                                local_blocks: int | None = None, ptr_half_blocks: int | None = None,
+                                pointer_budget_blocks: int | None = None, global_blocks: int | None = None,
+                                eod_token_id: int = 50256, gumbel_u: Tensor | None = None) -> ScopeBlockMask:
+        """Same arguments and assertions as the reference; ``gumbel_u``
+        optionally replaces the internal draw of the Gumbel uniforms."""
+        assert (input_seq is None) != (docs is None), "pass exactly one of: input_seq|docs"
+        if docs is None:
+            assert input_seq is not None and input_seq.ndim == 1
+            docs = (input_seq == eod_token_id).cumsum(0)
+        assert docs is not None and docs.ndim == 1
+        device = docs.device
+        T = int(docs.numel())
+        assert T % block_size == 0
+        B, H, TT, M = delta_star.shape
+        assert B == 1
+        assert TT == T
+        assert H == self.num_heads
+        assert M == self.M
+        assert pi.shape == (B, H, T, M)
+        assert budget_logits.shape == (B, H, T, M)
+        local = self.pointer_local_blocks if local_blocks is None else int(local_blocks)
+        p = self.pointer_half_blocks if ptr_half_blocks is None else int(ptr_half_blocks)
+        local, p = max(1, local), max(0, p)
+        NB = T // block_size
+        local = min(local, NB)
+        budget_val = self.pointer_budget_blocks if pointer_budget_blocks is None else int(pointer_budget_blocks)
+        budget_val = max(0, int(budget_val))
+        if self.pointer_budget_is_total:
+            cap = int(local + M + 2 * M * p)
+            extra = max(min(budget_val, cap) - local - M, 0)
+        else:
+            extra = budget_val
+        budget_rem = min(extra // 2, M * p)
+        k = self.gumbel_topk_k
+        if k <= 0 or k > M:
+            k = M
+        gumbel_k = k if (self.training and self.gumbel_topk and p > 0 and k < M) else 0
+        if gumbel_k and gumbel_u is None:
+            gen = torch.Generator(device=device)
+            gen.manual_seed(int(self._st["seed"]))
+            gumbel_u = torch.rand((H, NB, M), device=device, generator=gen, dtype=torch.float32)
+        reset_on = bool(self._st["reset"]) and self._st["reset_len"] > 0
+        docs32 = docs.to(torch.int32)
+        ds_ptr, ds_local, ds_tok_end = ops.doc_starts(docs32, block_size, doc_clamp=self.pointer_doc_clamp,
+                                                      reset_len=self._st["reset_len"] if reset_on else 0)
+        ga = self._st["glob"] if global_blocks is None else int(global_blocks)
+        kv_num, kv_idx, radius, centre = ops.pointer_mask_ref(
+            delta_star, budget_logits, ds_ptr, ds_local, bs=block_size, local_blocks=local, ptr_half_blocks=p,
+            global_blocks_cfg=self.pointer_global_blocks, global_active=ga, radius_mode=self.pointer_radius_mode,
+            budget_rem=budget_rem, budget_temp=self.pointer_budget_temp, mask_active=bool(self._st["mask"]),
+            half_active=self._st["half"], rep_mode=self.pointer_qblock_rep, gumbel_k=gumbel_k,
+            gumbel_tau=self.gumbel_topk_tau, gumbel_u=gumbel_u, eps=self.eps)
+        if self.debug_stats:
+            mk = self._dbg_kv_unique_hist.numel()
+            if kv_idx.shape[-1] + 1 > mk:
+                raise RuntimeError(f"kv_unique histogram has {mk} bins, list width is {kv_idx.shape[-1]}")
+            rb, eb = self._dbg_ptr_radius_hist.numel(), self._dbg_ptr_extra_sum_hist.numel()
+            counts, values = ops.mask_stats(H=H, QB=NB, bs=block_size, M=M, kv_num=kv_num, radius=radius,
+                                            maxkv_bins=mk, radius_bins=rb, extra_bins=eb)
+            c = ops.unpack_counts(counts, mk, rb)
+            self._dbg_kv_unique_hist.copy_(c["kv_unique_hist"])
+            self._dbg_ptr_radius_hist.copy_(c["ptr_radius_hist"])
+            self._dbg_ptr_extra_sum_hist.copy_(c["ptr_extra_sum_hist"])
+            self._dbg_ptr_radius0_frac.copy_(values[5])
+        return ScopeBlockMask(kv_num_blocks=kv_num[None], kv_indices=kv_idx[None], BLOCK_SIZE=block_size,
+                              docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local,
+                              extras=dict(radius=radius, centre=centre))
+
+    # ---- pointer mask, block-scoring mode
+    @torch.no_grad()
+    def build_blockscore_mask(self, q: Tensor, k: Tensor, *, docs: Tensor, block_size: int = 128,
+                              window_blocks: int = 4, global_blocks: int = 1, budget_blocks: int = 4,
+                              budget_temp: float | None = None, logit_scale: float | None = None,
+                              prior: Tensor | None = None, noise: str = "counter", gumbel_u: Tensor | None = None,
+                              seed: int | None = None, logits: Tensor | None = None,
+                              return_logits: bool = False) -> ScopeBlockMask:
+        """window ∪ top-``budget_blocks`` block-mean q·k pointers ∪ global
+        anchors.  q, k: [1,H,T,D] bf16.  ``noise``: "none" | "uniform"
+        (explicit ``gumbel_u`` [H,QB,NB]) | "counter" (in-kernel draw from the
+        Gumbel seed; only while training, like the reference's Gumbel)."""
+        T = int(docs.numel())
+        H = q.shape[1]
+        NB = T // block_size
+        docs32 = docs.to(torch.int32)
+        ds_ptr, ds_local, ds_tok_end = ops.doc_starts(docs32, block_size, doc_clamp=self.pointer_doc_clamp)
+        qbar = kbar = None
+        if logits is None:
+            qbar, kbar = ops.block_means(q, k, block_size)
+        if noise == "counter" and not self.training:
+            noise = "none"
+        scale = float(block_size) / math.sqrt(q.shape[-1]) if logit_scale is None else float(logit_scale)
+        res = ops.pointer_select(ds_ptr, ds_local, bs=block_size, NB=NB, H=H, window=window_blocks,
+                                 n_global=global_blocks, budget=budget_blocks, qbar=qbar, kbar=kbar,
+                                 logits_in=logits, prior=prior,
+                                 temp=self.pointer_budget_temp if budget_temp is None else budget_temp,
+                                 logit_scale=scale, noise=noise, gumbel_u=gumbel_u,
+                                 seed=self._st["seed"] if seed is None else seed, eps=self.eps,
+                                 return_logits=return_logits)
+        kv_num, kv_idx, picks = res[:3]
+        extras = dict(picks=picks)
+        if return_logits:
+            extras["logits"] = res[3]
+        return ScopeBlockMask(kv_num_blocks=kv_num[None], kv_indices=kv_idx[None], BLOCK_SIZE=block_size,
+                              docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local, extras=extras)
+
+    def score_terms(self, outputs: tuple, *, offset: str = "token") -> SpectralTerms:
+        """SpectralTerms for ``scope_attention`` from the 12-tuple of forward()."""
+        coeff_cos, coeff_sin, slope, b0, _, _, _, delta_main, width = outputs[:9]
+        return SpectralTerms(coeff_cos=coeff_cos, coeff_sin=coeff_sin, omegas=self.omegas.to(coeff_cos.device),
+                             offset=offset, beta=self.beta, b0=b0, slope=slope, delta_main=delta_main, width=width,
+                             use_slope=self.use_slope, subtract_b0=self.subtract_b0, gate_kind=self.gate_kind,
+                             ramp_lambda=self.ramp_lambda, tau=self.tau)

@@ -1,0 +1,306 @@
+"""GPU parity of kernel 1 (pointer selection), the q-list transpose and
+kernel 3 (statistics) against the reference's golden vectors and the oracle.
+Bar: bit-exact for every index list and integer statistic."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pointer as OP
+from oracle import stats as OS
+from tests.golden import load_cases, pointer_case_args, pointer_case_reps
+from tests.helpers import docs_with_boundaries, qkv
+
+pytestmark = pytest.mark.gpu
+
+POINTER_CASES = load_cases("pointer_ref_vectors.npz")
+FORWARD_CASES = load_cases("forward_stats_vectors.npz")
+DEV = "cuda"
+
+
+def _full(rep: np.ndarray, T: int, bs: int) -> torch.Tensor:
+    H, NB, M = rep.shape
+    full = torch.zeros((1, H, T, M), dtype=torch.float32)
+    t_rep = (torch.arange(NB) + 1) * bs - 1
+    full[0, :, t_rep, :] = torch.from_numpy(rep)
+    return full
+
+
+def _spectral_bias_for(c: dict):
+    from scope_amd import SpectralBias
+
+    sb = SpectralBias(head_dim=32, num_heads=int(c["H"]), L_train=int(c["T"]), M=int(c["M"]), K=6,
+                      use_pointer_mask=True, pointer_qblock_rep=str(c["rep_mode"]), debug_stats=True,
+                      pointer_local_blocks=int(c["cfg_pointer_local_blocks"]),
+                      pointer_half_blocks=int(c["cfg_pointer_half_blocks"]),
+                      pointer_global_blocks=int(c["cfg_pointer_global_blocks"]),
+                      pointer_budget_blocks=int(c["cfg_pointer_budget_blocks"]),
+                      pointer_budget_is_total=bool(c["cfg_pointer_budget_is_total"]),
+                      pointer_budget_temp=float(c["cfg_pointer_budget_temp"]),
+                      pointer_radius_mode=str(c["cfg_pointer_radius_mode"]),
+                      pointer_doc_clamp=bool(c["cfg_pointer_doc_clamp"]), gumbel_topk=bool(c["cfg_gumbel_topk"]),
+                      gumbel_topk_k=int(c["cfg_gumbel_topk_k"]), gumbel_topk_tau=float(c["cfg_gumbel_topk_tau"]))
+    sb.set_pointer_mask_state(enabled=bool(c["cfg_mask_active"]), half_blocks=int(c["cfg_half_active"]),
+                              global_blocks=int(c["cfg_global_active"]))
+    sb.set_pointer_reset_state(enabled=bool(c["cfg_reset_active"]), reset_len=int(c["cfg_reset_len_active"]))
+    sb.set_gumbel_seed(seed=int(c["cfg_gumbel_seed"]))
+    sb.train(bool(c["training"]))
+    return sb.to(DEV)
+
+
+@pytest.mark.parametrize("name", sorted(POINTER_CASES))
+def test_build_pointer_blockmask_matches_reference_vectors(name):
+    """SpectralBias.build_pointer_blockmask on the GPU vs the reference's own
+    outputs (kv lists, NB-wide export, q lists, debug statistics)."""
+    c = POINTER_CASES[name]
+    T, bs, M, H = int(c["T"]), int(c["bs"]), int(c["M"]), int(c["H"])
+    print(f"case {name}: H={H} T={T} bs={bs} M={M}", flush=True)
+    sb = _spectral_bias_for(c)
+    if c["rep_mode"] == "last":
+        delta_star = _full(c["delta_rep"], T, bs)
+        budget = _full(c["budget_rep"], T, bs)
+    else:
+        delta_star = torch.from_numpy(c["delta_star"])[None]
+        budget = torch.from_numpy(c["budget_logits"])[None]
+    pi = torch.full_like(delta_star, 1.0 / M)
+    kw = {}
+    for key, arg in (("cfg_build_local_blocks", "local_blocks"), ("cfg_build_ptr_half_blocks", "ptr_half_blocks"),
+                     ("cfg_build_budget_blocks", "pointer_budget_blocks"),
+                     ("cfg_build_global_blocks", "global_blocks")):
+        if int(c[key]) >= 0:
+            kw[arg] = int(c[key])
+    bm = sb.build_pointer_blockmask(docs=torch.from_numpy(c["docs"]).long().to(DEV), delta_star=delta_star.to(DEV),
+                                    pi=pi.to(DEV), budget_logits=budget.to(DEV), block_size=bs,
+                                    gumbel_u=torch.from_numpy(c["gumbel_u"]).to(DEV), **kw)
+    torch.cuda.synchronize()
+    assert np.array_equal(bm.kv_num_blocks.cpu().numpy(), c["kv_num_blocks"])
+    assert np.array_equal(bm.kv_indices_export().cpu().numpy(), c["kv_indices"])
+    tbm = bm.to_torch_blockmask()
+    assert np.array_equal(tbm.q_num_blocks.cpu().numpy(), c["q_num_blocks"])
+    assert np.array_equal(tbm.q_indices.cpu().numpy(), c["q_indices"])
+    for key in ("kv_unique_hist", "ptr_radius_hist", "ptr_extra_sum_hist"):
+        assert np.array_equal(getattr(sb, "_dbg_" + key).cpu().numpy(), c["dbg_" + key]), key
+    assert sb._dbg_ptr_radius0_frac.item() == float(c["dbg_ptr_radius0_frac"])
+
+
+@pytest.mark.parametrize("seed,H,T,bs,M,n_docs", [(0, 8, 65536, 128, 8, 1), (1, 8, 131072, 256, 8, 16),
+                                                  (2, 6, 4096, 128, 4, 5)])
+def test_pointer_mask_ref_vs_oracle_large(seed, H, T, bs, M, n_docs):
+    """Reference mode at training shapes (T up to 128k) vs the oracle."""
+    from scope_amd import ops
+
+    print(f"ref-mode seed={seed} H={H} T={T} bs={bs} M={M}", flush=True)
+    rng = np.random.default_rng(seed)
+    NB = T // bs
+    docs = docs_with_boundaries(T, n_docs, seed)
+    t_rep = (np.arange(NB) + 1) * bs - 1
+    delta_rep = (rng.random((H, NB, M)) * (t_rep[None, :, None] + bs)).astype(np.float32)
+    budget_rep = (rng.standard_normal((H, NB, M)) * 1.5).astype(np.float32)
+    u = rng.random((H, NB, M)).astype(np.float32)
+    budget_blocks = 4 + M + 18
+    rem = OP.budget_rem_blocks(M=M, local_blocks=4, ptr_half_blocks=3, budget_blocks=budget_blocks,
+                               budget_is_total=True)
+    ref = OP.pointer_mask_reference(delta_rep, budget_rep, docs.numpy(), bs=bs, M=M, local_blocks=4,
+                                    ptr_half_blocks=3, global_blocks_cfg=2, global_active=2,
+                                    budget_blocks=budget_blocks, budget_is_total=True, budget_temp=0.5,
+                                    radius_mode="pi", doc_clamp=True, mask_active=True, half_active=3,
+                                    gumbel_active=True, gumbel_k=M // 2, gumbel_tau=1.0, gumbel_u=u)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
+    kv_num, kv_idx, radius, centre = ops.pointer_mask_ref(
+        _full(delta_rep, T, bs).to(DEV), _full(budget_rep, T, bs).to(DEV), ds_ptr, ds_local, bs=bs,
+        local_blocks=4, ptr_half_blocks=3, global_blocks_cfg=2, global_active=2, radius_mode="pi",
+        budget_rem=rem, budget_temp=0.5, mask_active=True, half_active=3, gumbel_k=M // 2, gumbel_tau=1.0,
+        gumbel_u=torch.from_numpy(u).to(DEV))
+    assert np.array_equal(radius.cpu().numpy(), ref["radius"])
+    assert np.array_equal(centre.cpu().numpy(), ref["centre"])
+    assert np.array_equal(kv_num.cpu().numpy(), ref["kv_num"])
+    assert np.array_equal(kv_idx.cpu().numpy(), ref["packed"])
+
+
+def test_doc_starts_vs_oracle():
+    from scope_amd import ops
+
+    for T, bs, n_docs, clamp, reset in ((4096, 128, 7, True, 0), (131072, 256, 16, True, 0),
+                                        (8192, 128, 40, False, 0), (8192, 256, 9, True, 1000)):
+        docs = docs_with_boundaries(T, n_docs, T + n_docs)
+        got = [x.cpu().numpy() for x in ops.doc_starts(docs.to(DEV), bs, doc_clamp=clamp, reset_len=reset)]
+        ref = OP.doc_start_blocks(docs.numpy(), bs, doc_clamp=clamp, reset_active=reset > 0, reset_len=reset)
+        for g, r in zip(got, ref):
+            assert np.array_equal(g, r), (T, bs, n_docs, clamp, reset)
+
+
+# ---------------------------------------------------------------------------
+# block-scoring mode
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("H,T,bs,W,G,B,n_docs", [(6, 4096, 128, 3, 1, 2, 1), (8, 65536, 128, 4, 1, 4, 1),
+                                                 (8, 131072, 256, 2, 2, 8, 16), (2, 8192, 256, 2, 2, 16, 5)])
+def test_pointer_select_given_logits_exact(H, T, bs, W, G, B, n_docs):
+    """Selection given the same fp32 logits (with ties) is bit-exact."""
+    from scope_amd import ops
+
+    print(f"select H={H} T={T} bs={bs} W={W} G={G} B={B}", flush=True)
+    NB = T // bs
+    rng = np.random.default_rng(T + B)
+    logits = (np.round(rng.standard_normal((H, NB, NB)) * 4) / 4).astype(np.float32)  # many ties
+    docs = docs_with_boundaries(T, n_docs, 3)
+    ref = OP.pointer_select_blockscore(logits, docs.numpy(), bs=bs, window=W, n_global=G, budget=B, temp=0.5)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
+    kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=NB, H=H, window=W, n_global=G, budget=B,
+                                               logits_in=torch.from_numpy(logits).to(DEV), temp=0.5)
+    assert np.array_equal(picks.cpu().numpy(), ref["picks"])
+    assert np.array_equal(kv_num.cpu().numpy(), ref["kv_num"])
+    assert np.array_equal(kv_idx.cpu().numpy(), ref["packed"])
+
+
+@pytest.mark.parametrize("noise", ["uniform", "counter"])
+def test_pointer_select_gumbel_exact(noise):
+    from scope_amd import ops
+
+    H, T, bs, W, G, B = 4, 16384, 128, 4, 1, 4
+    NB = T // bs
+    rng = np.random.default_rng(7)
+    logits = rng.standard_normal((H, NB, NB)).astype(np.float32)
+    docs = docs_with_boundaries(T, 3, 11)
+    seed = 0x1234_5678_9ABC
+    if noise == "uniform":
+        u = rng.random((H, NB, NB)).astype(np.float32)
+    else:
+        hh, qq, kk = np.meshgrid(np.arange(H), np.arange(NB), np.arange(NB), indexing="ij")
+        u = OP.counter_uniform(seed, hh, qq, kk)
+    g = OP.gumbel_from_u(u)
+    ref = OP.pointer_select_blockscore(logits, docs.numpy(), bs=bs, window=W, n_global=G, budget=B, gumbel=g)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
+    kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=NB, H=H, window=W, n_global=G, budget=B,
+                                               logits_in=torch.from_numpy(logits).to(DEV), noise=noise,
+                                               gumbel_u=torch.from_numpy(u).to(DEV) if noise == "uniform" else None,
+                                               seed=seed)
+    assert np.array_equal(picks.cpu().numpy(), ref["picks"])
+    assert np.array_equal(kv_idx.cpu().numpy(), ref["packed"])
+
+
+@pytest.mark.parametrize("H,T,bs", [(6, 4096, 128), (8, 131072, 256)])
+def test_block_means_and_logits(H, T, bs):
+    """Fused block means + q̄·k̄ logits vs fp64; selection exact given the kernel's logits."""
+    from scope_amd import ops
+
+    q, k, _ = qkv(H, T, seed=5)
+    NB = T // bs
+    docs = docs_with_boundaries(T, 4, 2)
+    qbar, kbar = ops.block_means(q.to(DEV), k.to(DEV), bs)
+    rq = OP.block_means(q[0].double().numpy(), bs)
+    rk = OP.block_means(k[0].double().numpy(), bs)
+    assert np.abs(qbar.cpu().numpy() - rq).max() < 1e-6
+    assert np.abs(kbar.cpu().numpy() - rk).max() < 1e-6
+    prior = (-0.05 * np.log1p(np.arange(NB))).astype(np.float32)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
+    scale = bs / np.sqrt(128.0)
+    kv_num, kv_idx, picks, lg = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=NB, H=H, window=2, n_global=1,
+                                                   budget=4, qbar=qbar, kbar=kbar, prior=torch.from_numpy(prior).to(DEV),
+                                                   logit_scale=scale, return_logits=True)
+    lg = lg.cpu().numpy()
+    ref_lg = OP.pointer_logits(rq, rk, logit_scale=scale, prior=prior)
+    ds = ds_ptr.cpu().numpy()
+    causal = (np.arange(NB)[None, :] <= np.arange(NB)[:, None]) & (np.arange(NB)[None, :] >= ds[:, None])
+    diff = np.abs(lg - ref_lg)[:, causal]
+    assert diff.max() < 1e-4 * (1 + np.abs(ref_lg[:, causal]).max())
+    assert np.all(np.isneginf(lg[:, ~causal]))
+    ref = OP.pointer_select_blockscore(lg, docs.numpy(), bs=bs, window=2, n_global=1, budget=4)
+    assert np.array_equal(picks.cpu().numpy(), ref["picks"])
+    assert np.array_equal(kv_idx.cpu().numpy(), ref["packed"])
+
+
+def test_planted_needle_is_selected():
+    """C3-style needle: a key block = 3 × a query block's mean query, ≥64
+    blocks back; the noise-free selection must pick it for that q-block."""
+    from scope_amd import ops
+
+    H, T, bs = 2, 65536, 256
+    NB = T // bs
+    q, k, _ = qkv(H, T, seed=9)
+    qb, kb = 200, 100
+    mq = q[0, :, qb * bs:(qb + 1) * bs].float().mean(dim=1)  # [H,D]
+    k[0, :, kb * bs:(kb + 1) * bs] = (3.0 * mq[:, None, :]).to(k.dtype)
+    docs = torch.zeros(T, dtype=torch.int32)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
+    qbar, kbar = ops.block_means(q.to(DEV), k.to(DEV), bs)
+    _, _, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=NB, H=H, window=2, n_global=2, budget=2,
+                                     qbar=qbar, kbar=kbar, logit_scale=bs / np.sqrt(128.0))
+    assert all(kb in picks[h, qb].tolist() for h in range(H))
+
+
+# ---------------------------------------------------------------------------
+# transpose and statistics
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("H,T,bs,W,G,B", [(2, 8192, 128, 3, 1, 2), (8, 131072, 256, 2, 2, 8)])
+def test_transpose_blocks_vs_oracle(H, T, bs, W, G, B):
+    from scope_amd import ops
+
+    NB = T // bs
+    rng = np.random.default_rng(1)
+    logits = rng.standard_normal((H, NB, NB)).astype(np.float32)
+    docs = docs_with_boundaries(T, 6, 1)
+    sel = OP.pointer_select_blockscore(logits, docs.numpy(), bs=bs, window=W, n_global=G, budget=B)
+    q_num, q_off, q_list = OP.transpose_blocks(sel["kv_num"], sel["packed"], NB)
+    got_off, got_list = ops.transpose_blocks(torch.from_numpy(sel["kv_num"]).to(DEV),
+                                             torch.from_numpy(sel["packed"]).to(DEV), NB)
+    got_off, got_list = got_off.cpu().numpy(), got_list.cpu().numpy()
+    assert np.array_equal(got_off, q_off)
+    for h in range(H):
+        n = q_off[h, -1]
+        assert np.array_equal(got_list[h, :n], q_list[h, :n])
+
+
+@pytest.mark.parametrize("name", sorted(FORWARD_CASES))
+def test_forward_stats_match_reference_vectors(name):
+    from scope_amd import ops
+
+    c = FORWARD_CASES[name]
+    H, T, M = int(c["H"]), int(c["T"]), int(c["M"])
+    has_docs = bool(c["with_docs"])
+    clamp, reset_on = bool(c["cfg_pointer_doc_clamp"]), bool(c["cfg_reset_active"])
+    rl = int(c["cfg_reset_len_active"]) if reset_on else 0
+    ds_ptr = ds_local = None
+    if has_docs:
+        ds_ptr, ds_local, _ = ops.doc_starts(torch.from_numpy(c["docs"]).to(DEV), 128, doc_clamp=clamp, reset_len=rl)
+    counts, values = ops.mask_stats(H=H, QB=T // 128, bs=128, delta_star=torch.from_numpy(c["delta_star"]).to(DEV),
+                                    pi=torch.from_numpy(c["pi"]).to(DEV), rep_mode=str(c["rep_mode"]),
+                                    has_docs=has_docs, docstart_enabled=has_docs and (clamp or reset_on),
+                                    local_blocks_cfg=int(c["cfg_pointer_local_blocks"]), eps=float(c["cfg_eps"]),
+                                    ds_ptr_fwd=ds_ptr, ds_local_fwd=ds_local)
+    u = ops.unpack_counts(counts.cpu(), 1, 1)
+    for key in ("delta_tokens_hist", "delta_blocks_hist", "ptr_center_hist"):
+        assert np.array_equal(u[key].numpy(), c["dbg_" + key]), key
+    v = values.cpu().numpy()
+    for i, key in enumerate(["pi_entropy_mean", "ptr_docstart_frac", "ptr_outside_local_frac", "ptr_block0_frac",
+                             "ptr_block0_frac_excl"]):
+        if key == "pi_entropy_mean":
+            assert abs(v[i] - float(c["dbg_" + key])) <= 1e-5 * max(1.0, abs(float(c["dbg_" + key]))), key
+        else:
+            assert v[i] == float(c["dbg_" + key]), key
+
+
+def test_blockscore_stats_vs_oracle():
+    from scope_amd import ops
+
+    H, T, bs, W, G, B = 8, 131072, 256, 2, 2, 8
+    NB = T // bs
+    rng = np.random.default_rng(3)
+    logits = rng.standard_normal((H, NB, NB)).astype(np.float32)
+    docs = docs_with_boundaries(T, 16, 4)
+    sel = OP.pointer_select_blockscore(logits, docs.numpy(), bs=bs, window=W, n_global=G, budget=B)
+    ref = OS.blockscore_stats(sel["kv_num"], sel["picks"], sel["ds_ptr"], sel["ds_local"], maxkv=sel["maxkv"],
+                              local_blocks=W)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
+    counts, values = ops.mask_stats(H=H, QB=NB, bs=bs, kv_num=torch.from_numpy(sel["kv_num"]).to(DEV),
+                                    picks=torch.from_numpy(sel["picks"]).to(DEV), ds_ptr=ds_ptr, ds_local=ds_local,
+                                    maxkv_bins=sel["maxkv"] + 1, bs_local_blocks=W)
+    u = ops.unpack_counts(counts.cpu(), sel["maxkv"] + 1, 0)
+    assert np.array_equal(u["kv_unique_hist"].numpy(), ref["kv_unique_hist"])
+    assert np.array_equal(u["ptr_dist_hist"].numpy(), ref["ptr_dist_hist"])
+    assert int(u["bs_n"]) == int(ref["n_picks"])
+    v = values.cpu().numpy()
+    assert v[6] == ref["ptr_outside_local_frac"]
+    assert v[7] == ref["ptr_block0_frac"]
+    assert v[8] == ref["ptr_block0_frac_excl"]
+    assert v[9] == ref["ptr_docstart_frac"]

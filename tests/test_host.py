@@ -1,0 +1,108 @@
+"""CPU: the host-side mirror of the reference interface — configuration
+errors, schedule setters, the coefficient head against the reference's
+golden vectors, shape assertions, and the BlockMask export logic."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pointer as P
+from scope_amd import ScopeBlockMask, SpectralBias
+from tests.golden import load_cases, load_flat
+
+
+def test_config_errors_match_reference():
+    kw = dict(head_dim=32, num_heads=2, L_train=128)
+    with pytest.raises(ValueError, match="K must be positive"):
+        SpectralBias(K=0, **kw)
+    with pytest.raises(ValueError, match="M must be positive"):
+        SpectralBias(M=0, **kw)
+    with pytest.raises(ValueError, match="gate_kind"):
+        SpectralBias(gate_kind="tanh", **kw)
+    with pytest.raises(ValueError, match="pointer_radius_mode"):
+        SpectralBias(pointer_radius_mode="budget", **kw)
+    with pytest.raises(ValueError, match="pointer_qblock_rep"):
+        SpectralBias(pointer_qblock_rep="first", **kw)
+    with pytest.raises(ValueError, match="invalid"):
+        SpectralBias(w_min=1.0, w_max=0.5, **kw)
+
+
+def test_setters_clamp_and_validate():
+    sb = SpectralBias(head_dim=32, num_heads=2, L_train=128, use_pointer_mask=True, pointer_half_blocks=3,
+                      pointer_global_blocks=2)
+    sb.set_pointer_mask_state(enabled=True, half_blocks=10, global_blocks=9)
+    assert sb._pointer_half_blocks_active.item() == 3 and sb._st["half"] == 3
+    assert sb._pointer_global_blocks_active.item() == 2 and sb._st["glob"] == 2
+    with pytest.raises(ValueError):
+        sb.set_pointer_mask_state(enabled=True, half_blocks=-1)
+    with pytest.raises(ValueError):
+        sb.set_pointer_reset_state(enabled=True, reset_len=-3)
+    sb.set_pointer_reset_state(enabled=False, reset_len=50)
+    assert sb._pointer_reset_len_active.item() == 0
+    sb.set_delta_star_max_active(max_tokens=10 ** 9)
+    assert sb._delta_star_max_active.item() == 127
+    with pytest.raises(ValueError):
+        sb.set_delta_edge_eps_active(eps=-1.0)
+    sb.set_gumbel_seed(seed=77)
+    assert sb._gumbel_seed.item() == 77 and sb._st["seed"] == 77
+
+
+def test_coefficient_head_matches_reference_vectors():
+    g = load_flat("coeff_head_vectors.npz")
+    sb = SpectralBias(head_dim=int(g["Dh"]), num_heads=int(g["H"]), L_train=int(g["L_train"]), L_max=int(g["L_max"]),
+                      M=int(g["M"]), K=int(g["K"]))
+    with torch.no_grad():
+        sb.mlp[0].weight.copy_(torch.from_numpy(g["w1"]))
+        sb.mlp[0].bias.copy_(torch.from_numpy(g["b1"]))
+        sb.mlp[2].weight.copy_(torch.from_numpy(g["w2"]))
+        sb.mlp[2].bias.copy_(torch.from_numpy(g["b2"]))
+    sb.eval()
+    assert np.allclose(sb.omegas.numpy(), g["omegas"])
+    out = sb(torch.from_numpy(g["q"])[None])
+    names = ["coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits", "delta_main", "width"]
+    for i, n in enumerate(names):
+        ref = torch.from_numpy(g[n])
+        assert torch.allclose(out[i][0], ref, rtol=1e-5, atol=1e-6), n
+
+
+def test_disabled_forward_returns_zeros_and_uniform_pi():
+    sb = SpectralBias(head_dim=16, num_heads=2, L_train=64, M=3, enabled=False)
+    out = sb(torch.randn(1, 2, 64, 16))
+    assert torch.all(out[0] == 0) and torch.allclose(out[5], torch.full_like(out[5], 1 / 3))
+
+
+def test_build_pointer_blockmask_shape_assertions():
+    sb = SpectralBias(head_dim=16, num_heads=2, L_train=256, M=2, use_pointer_mask=True)
+    docs = torch.zeros(256, dtype=torch.long)
+    x = torch.zeros(1, 2, 256, 2)
+    with pytest.raises(AssertionError):
+        sb.build_pointer_blockmask(docs=docs, input_seq=docs, delta_star=x, pi=x, budget_logits=x)
+    with pytest.raises(AssertionError):
+        sb.build_pointer_blockmask(docs=torch.zeros(200, dtype=torch.long), delta_star=x, pi=x, budget_logits=x)
+    with pytest.raises(AssertionError):
+        sb.build_pointer_blockmask(docs=docs, delta_star=torch.zeros(1, 3, 256, 2), pi=x, budget_logits=x)
+    with pytest.raises(AssertionError):
+        sb.build_pointer_blockmask(docs=docs, delta_star=torch.zeros(2, 2, 256, 2), pi=x, budget_logits=x)
+
+
+def test_blockmask_export_matches_reference():
+    """ScopeBlockMask.kv_indices_export / to_torch_blockmask (pure torch, CPU)
+    reproduce the reference's NB-wide export and q lists."""
+    cases = load_cases("pointer_ref_vectors.npz")
+    from tests.golden import pointer_case_args, pointer_case_reps
+
+    for name in ("c1_pi_single_doc", "export_truncation", "gumbel_multi_doc"):
+        c = cases[name]
+        a = pointer_case_args(c)
+        dr, br = pointer_case_reps(c)
+        out = P.pointer_mask_reference(dr, br, c["docs"], gumbel_u=c["gumbel_u"], **a)
+        bs = int(c["bs"])
+        docs = torch.from_numpy(c["docs"])
+        bm = ScopeBlockMask(kv_num_blocks=torch.from_numpy(out["kv_num"])[None],
+                            kv_indices=torch.from_numpy(out["packed"])[None], BLOCK_SIZE=bs, docs=docs,
+                            ds_tok_end=torch.from_numpy(P.doc_start_blocks(c["docs"], bs)[2]))
+        assert np.array_equal(bm.kv_indices_export().numpy(), c["kv_indices"])
+        tbm = bm.to_torch_blockmask()
+        assert np.array_equal(tbm.q_indices.numpy(), c["q_indices"])
+        assert tbm.BLOCK_SIZE == (bs, bs)
