@@ -219,7 +219,8 @@ typedef struct {
 } scope_attn_params;
 
 /* Spectral tables: block mode [NB][16] fp32 (cos ω_k r, sin ω_k r);
- * token mode [T][16] bf16 (cos ω_k j, sin ω_k j).  Replaces
+ * token mode [T][32] bf16 (cos ω_k j, sin ω_k j as bf16 hi parts, then the
+ * bf16 lo parts x - hi).  Replaces
  * SpectralBias._get_trig_tables, model/attn_bias.py:326-340. */
 int64_t scope_spectral_table_bytes(int bias_mode, int64_t T, int bs);
 int scope_spectral_table(int bias_mode, const float* omegas, int K, int64_t T, int bs, void* table,

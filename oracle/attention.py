@@ -145,6 +145,21 @@ def attention_blocksparse(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: floa
     return res
 
 
+def scope_attention_blocksparse(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: float, beta: float = 0.5,
+                                bias_mode: str = "none", coeff_cos=None, coeff_sin=None, omegas=None,
+                                token_kwargs: dict | None = None):
+    """Differentiable block-sparse reference: (out [H,T,D], lse [H,T]) built
+    from the per-(h, q-block) gathers, so autograd gives every gradient
+    without a [T,T] tensor."""
+    H, T, D = q.shape
+    QB = T // bs
+    res = attention_blocksparse(q, k, v, kv_num, kv_idx, docs, bs=bs, scale=scale, beta=beta, bias_mode=bias_mode,
+                                coeff_cos=coeff_cos, coeff_sin=coeff_sin, omegas=omegas, token_kwargs=token_kwargs)
+    out = torch.stack([torch.cat([res[(h, qb)][0] for qb in range(QB)], 0) for h in range(H)], 0)
+    lse = torch.stack([torch.cat([res[(h, qb)][1] for qb in range(QB)], 0) for h in range(H)], 0)
+    return out, lse
+
+
 def scope_attention_reference(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: float, beta: float = 0.5,
                               bias_mode: str = "none", coeff_cos=None, coeff_sin=None, omegas=None,
                               token_kwargs: dict | None = None):

@@ -28,7 +28,8 @@ int check_launch(const char* what) {
 }
 
 // Block mode: row r of [NB][16] fp32 holds cos(ω_k r) for k < 8, then sin(ω_k r).
-// Token mode: row j of [T][16] bf16 holds cos(ω_k j), then sin(ω_k j).
+// Token mode: row j of [T][32] bf16 holds cos(ω_k j) and sin(ω_k j) as bf16
+// hi parts, then the bf16 lo parts (x - hi).
 // Phases are reduced in double precision so that large offsets keep full
 // fp32 accuracy; unused bands (k >= K) are zero.
 __global__ void spectral_table_kernel(const float* __restrict__ omegas, int K, int64_t rows,
@@ -49,11 +50,21 @@ __global__ void spectral_table_kernel(const float* __restrict__ omegas, int K, i
     }
   }
   if (bf16_out) {
-    uint32_t* o = reinterpret_cast<uint32_t*>(table) + r * 8;
+    // hi = bf16(x), lo = bf16(x - hi): [cos hi, sin hi, cos lo, sin lo]
+    uint32_t* o = reinterpret_cast<uint32_t*>(table) + r * 16;
+    float cl[8], sl[8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) o[k] = pack_bf16x2(c[2 * k], c[2 * k + 1]);
+    for (int k = 0; k < 8; ++k) {
+      cl[k] = c[k] - bf16_to_f32(f32_to_bf16(c[k]));
+      sl[k] = s[k] - bf16_to_f32(f32_to_bf16(s[k]));
+    }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) o[4 + k] = pack_bf16x2(s[2 * k], s[2 * k + 1]);
+    for (int k = 0; k < 4; ++k) {
+      o[k] = pack_bf16x2(c[2 * k], c[2 * k + 1]);
+      o[4 + k] = pack_bf16x2(s[2 * k], s[2 * k + 1]);
+      o[8 + k] = pack_bf16x2(cl[2 * k], cl[2 * k + 1]);
+      o[12 + k] = pack_bf16x2(sl[2 * k], sl[2 * k + 1]);
+    }
   } else {
     float* o = reinterpret_cast<float*>(table) + r * 16;
 #pragma unroll
@@ -76,7 +87,7 @@ const char* scope_last_error(void) { return g_last_error.c_str(); }
 
 int64_t scope_spectral_table_bytes(int bias_mode, int64_t T, int bs) {
   if (bias_mode == SCOPE_BIAS_BLOCK) return (T / bs) * 16 * 4;
-  if (bias_mode == SCOPE_BIAS_TOKEN) return T * 16 * 2;
+  if (bias_mode == SCOPE_BIAS_TOKEN) return T * 32 * 2;
   return 0;
 }
 

@@ -1,9 +1,814 @@
-// Kernel 2 (backward): not built yet in this revision.
+// Kernel 2 (backward): gradients of the block-sparse attention with the
+// SCOPE spectral bias, bf16 MFMA on gfx950.  Replaces the FlexAttention
+// backward (torch:_inductor/kernel/flex/templates/flex_backwards.py.jinja;
+// eager semantics torch:_higher_order_ops/flex_attention.py:826-975),
+// including the gradients of the score_mod's captured coefficient tensors.
+//
+//   dS = P ∘ (dP - Δ),  P = exp(s - lse),  dP = dO·V^T,  Δ = rowsum(dO ∘ O)
+//   dQ = scale·dS·K,  dK = scale·dS^T·Q,  dV = P^T·dO
+//
+// Pass A (q-major, one workgroup per (head, q-block), like the forward):
+//   Δ, dQ, and the bias gradients: block mode dA_k = β Σ_tiles cos(ω_k r)·Σ_j dS,
+//   token mode through extra MFMAs over the key features (bf16 hi + lo)
+//   (C_k = Σ_j dS cos ω_k j, S_k = Σ_j dS sin ω_k j), slope / b0 / gate per element.
+// Plan: per key block, its q-list is cut into chunks of kChunk q-blocks.
+// Pass B (kv-major, one workgroup per (head, key block, chunk)): dK, dV over
+//   the q-list; a block with one chunk writes bf16 directly, longer lists
+//   write fp32 partials that a reduce kernel sums in chunk order
+//   (deterministic, no floating-point atomics).
+#include <math.h>
+
 #include "attn_common.h"
+
+namespace scope {
+
+constexpr int kChunk = 16;  // q-blocks per dK/dV work item
+
+// ---------------------------------------------------------------------------
+// pass A
+// ---------------------------------------------------------------------------
+template <int BS, int MODE>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
+  constexpr int NT = 256;          // 4 waves = 128 query rows per workgroup
+  constexpr int SPLIT = BS / 128;  // workgroups per q-block
+  constexpr int D = 128;
+  constexpr int BN = 64;
+  constexpr int KSTR = D + 8;
+  constexpr int TSTR = BN + 4;
+  constexpr int FSTR = 40;
+  constexpr int NSUB = BS / BN;
+  constexpr int MB = BN / 32;
+  constexpr int KCH = BN * 16;
+  constexpr int KL = (KCH + NT - 1) / NT;
+
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[BN * KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[D * TSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Fs[MODE == 2 ? BN * FSTR : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t Ft[MODE == 2 ? 32 * TSTR : 8];
+  __shared__ __attribute__((aligned(16))) int docs_s[BN];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = tile / (a.QB * SPLIT), qb = (tile / SPLIT) % a.QB, part = tile % SPLIT;
+  const int64_t q0 = static_cast<int64_t>(qb) * BS + part * 128;
+  const int64_t wrow_lo = q0 + wave * 32;
+  const int64_t row = wrow_lo + lr;
+  const int64_t hT = static_cast<int64_t>(h) * a.T;
+
+  uint4 qreg[8], doreg[8];
+  float delta;
+  {
+    const uint16_t* qp = a.q + h * a.q_sh + row * a.q_st + g * 8;
+    const uint16_t* op = a.o + h * a.o_sh + row * a.o_st + g * 8;
+    const uint16_t* dp = a.dout + h * a.o_sh + row * a.o_st + g * 8;
+    float dsum = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
+      doreg[ks] = *reinterpret_cast<const uint4*>(dp + ks * 16);
+      const uint4 ov = *reinterpret_cast<const uint4*>(op + ks * 16);
+      const uint32_t dw[4] = {doreg[ks].x, doreg[ks].y, doreg[ks].z, doreg[ks].w};
+      const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dsum += __uint_as_float(dw[i] << 16) * __uint_as_float(ow[i] << 16);
+        dsum += __uint_as_float(dw[i] & 0xffff0000u) * __uint_as_float(ow[i] & 0xffff0000u);
+      }
+    }
+    delta = dsum + __shfl_xor(dsum, 32, 64);
+    if (g == 0) a.delta[hT + row] = delta;
+  }
+  const float lse_nat = a.lse[hT + row];
+  const float lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
+
+  // ---- bias set-up (as in the forward)
+  float ca[8], sa[8];
+  uint4 qf = make_uint4(0, 0, 0, 0), qfl = make_uint4(0, 0, 0, 0);
+  float rowc = 0.f, slp = 0.f, dm = 0.f, wd = 0.f, glam = 0.f;
+  float cos_i[4], sin_i[4];  // token mode: cos/sin(ω_k row) for k = 4g..4g+3
+  if (MODE == 1) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      ca[k] = k < a.K ? a.coeff_cos[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
+      sa[k] = k < a.K ? a.coeff_sin[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
+    }
+  }
+  if (MODE == 2) {
+    token_qfeat(a, hT, row, g, qf, qfl, cos_i, sin_i);
+    if (a.subtract_b0) rowc = -a.beta_log2 * a.b0[hT + row];
+    if (a.use_slope) slp = a.beta_log2 * a.slope[hT + row];
+    if (a.gate_kind != SCOPE_GATE_NONE) {
+      dm = a.delta_main[hT + row];
+      wd = a.width[hT + row];
+      glam = a.beta_log2 * a.ramp_lambda;
+    }
+  }
+  const bool gate = MODE == 2 && a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
+  const bool extra = MODE == 2 && (a.use_slope || gate);
+
+  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
+  const int n = a.kv_num[lrow];
+  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
+  const int total = n * NSUB;
+  const int ds_end = a.ds_tok_end[qb];
+  const int doc_row = a.docs[row];
+  const float cs = a.scale_log2;
+
+  f32x16_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = zero16();
+  // Bias gradients use Δ_true = Σ_j P dP rather than the Δ of the bf16
+  // output: since Σ_j P = 1, the row total Σ_j dS equals Δ_true - Δ, so each
+  // per-tile sum is corrected by subtracting that total times the tile's
+  // probability mass (the *_p accumulators hold the P-weighted sums).
+  f32x16_t facc = zero16(), facc_p = zero16();
+  float accA[8], accB[8], accPA[8], accPB[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) accA[k] = accB[k] = accPA[k] = accPB[k] = 0.f;
+  float rs_tot = 0.f, sl_tot = 0.f, gdm_tot = 0.f, gwd_tot = 0.f;
+  float pm_tot = 0.f, psl_tot = 0.f, pgdm_tot = 0.f, pgwd_tot = 0.f;
+
+  for (int it = 0; it < total; ++it) {
+    const int t = it / NSUB, st = it % NSUB;
+    const int kb = lst[t];
+    const int64_t kv0 = static_cast<int64_t>(kb) * BS + st * BN;
+    // ---- stage K, V (rows), docs, key features; then K^T / F^T in LDS
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int idx = tid + i * NT;
+      if (KCH % NT == 0 || idx < KCH) {
+        const int r = idx / 16, c = idx % 16;
+        *reinterpret_cast<uint4*>(&Ks[r * KSTR + c * 8]) =
+            *reinterpret_cast<const uint4*>(a.k + h * a.k_sh + (kv0 + r) * a.k_st + c * 8);
+        *reinterpret_cast<uint4*>(&Vs[r * KSTR + c * 8]) =
+            *reinterpret_cast<const uint4*>(a.v + h * a.v_sh + (kv0 + r) * a.v_st + c * 8);
+      }
+    }
+    if (tid < BN) docs_s[tid] = a.docs[kv0 + tid];
+    if (MODE == 2)
+      for (int idx = tid; idx < BN * 4; idx += NT)
+        *reinterpret_cast<uint4*>(&Fs[(idx / 4) * FSTR + (idx % 4) * 8]) = *reinterpret_cast<const uint4*>(
+            static_cast<const uint16_t*>(a.table) + (kv0 + idx / 4) * kTokRow + (idx % 4) * 8);
+    __syncthreads();
+    // K^T from Ks: 4 keys x 8 dims per thread (BN/4 * 16 blocks)
+    for (int idx = tid; idx < BN * 4; idx += NT) {
+      const int c = idx % 16, kvg = idx / 16;
+      uint32_t w[4][4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const uint4 u = *reinterpret_cast<const uint4*>(&Ks[(kvg * 4 + rr) * KSTR + c * 8]);
+        w[rr][0] = u.x;
+        w[rr][1] = u.y;
+        w[rr][2] = u.z;
+        w[rr][3] = u.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint2 val;
+        if (e & 1) {
+          val.x = pack_hi16(w[0][e / 2], w[1][e / 2]);
+          val.y = pack_hi16(w[2][e / 2], w[3][e / 2]);
+        } else {
+          val.x = pack_lo16(w[0][e / 2], w[1][e / 2]);
+          val.y = pack_lo16(w[2][e / 2], w[3][e / 2]);
+        }
+        *reinterpret_cast<uint2*>(&Kt[(c * 8 + e) * TSTR + kvg * 4]) = val;
+      }
+    }
+    if (MODE == 2) {
+      // F^T: rows 0..15 = hi features, rows 16..31 = lo features
+      for (int idx = tid; idx < 32 * BN; idx += NT) {
+        const int f = idx / BN, j = idx % BN;
+        Ft[f * TSTR + j] = Fs[j * FSTR + f];
+      }
+    }
+    __syncthreads();
+
+    if (kv0 > wrow_lo + 31) continue;
+    const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
+    float tconst = rowc;
+    float crow[8], srow[8];
+    if (MODE == 1) {
+      const float* tr = static_cast<const float*>(a.table) + static_cast<int64_t>(qb - kb) * 16;
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        crow[k] = tr[k];
+        srow[k] = tr[8 + k];
+        acc += ca[k] * crow[k] + sa[k] * srow[k];
+      }
+      tconst = acc;
+    }
+
+    // S^T and dP^T
+    f32x16_t s[MB], dpv[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      s[mb] = zero16();
+      dpv[mb] = zero16();
+      const uint16_t* kr = &Ks[(mb * 32 + lr) * KSTR + g * 8];
+      const uint16_t* vr = &Vs[(mb * 32 + lr) * KSTR + g * 8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        s[mb] = mfma32(*reinterpret_cast<const uint4*>(kr + ks * 16), qreg[ks], s[mb]);
+        dpv[mb] = mfma32(*reinterpret_cast<const uint4*>(vr + ks * 16), doreg[ks], dpv[mb]);
+      }
+      if (MODE == 2) {
+        const uint4 fh = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + g * 8]);
+        const uint4 fl = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + 16 + g * 8]);
+        s[mb] = mfma32(fh, qf, s[mb]);
+        s[mb] = mfma32(fh, qfl, s[mb]);
+        s[mb] = mfma32(fl, qf, s[mb]);
+      }
+    }
+    if (!full) {
+      const int lim = static_cast<int>(row - kv0);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int j0 = mb * 32 + 8 * rq + 4 * g;
+          const int4 d4 = *reinterpret_cast<const int4*>(&docs_s[j0]);
+          const int dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool ok = (j0 + i <= lim) & (dv[i] == doc_row);
+            s[mb][4 * rq + i] = ok ? s[mb][4 * rq + i] : -INFINITY;
+          }
+        }
+    }
+    // P, dS (natural units), per-row reductions
+    const float off = tconst - lse2;
+    uint4 dsb[2 * MB], pbv[2 * MB];
+    float rs = 0.f, slv = 0.f, gdm = 0.f, gwd = 0.f;
+    float pm = 0.f, psl = 0.f, pgdm = 0.f, pgwd = 0.f;
+    const int dbase = static_cast<int>(row - kv0);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float dsv[8], pvv[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int r = hf * 8 + jj;
+          float x = s[mb][r];
+          float sig = 0.f, sgn = 0.f, df = 0.f;
+          if (extra) {
+            const int j = mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+            df = static_cast<float>(dbase - j);
+            float e = slp * df;
+            if (gate) {
+              const float dd = df - dm;
+              const float xx = (fabsf(dd) - wd) * a.inv_tau;
+              float gt;
+              if (a.gate_kind == SCOPE_GATE_SOFTPLUS) {
+                const float ex = __expf(-fabsf(xx));
+                gt = fmaxf(xx, 0.f) + log1pf(ex);
+                sig = xx >= 0.f ? 1.f / (1.f + ex) : ex / (1.f + ex);
+              } else {
+                gt = fmaxf(xx, 0.f);
+                sig = xx > 0.f ? 1.f : 0.f;
+              }
+              sgn = dd > 0.f ? 1.f : (dd < 0.f ? -1.f : 0.f);
+              e -= glam * gt;
+            }
+            x = fmaf(x, cs, e);
+          } else {
+            x = x * cs;
+          }
+          const float p = exp2f(x + off);
+          const float d = p * (dpv[mb][r] - delta);
+          dsv[jj] = d;
+          pvv[jj] = p;
+          rs += d;
+          pm += p;
+          if (extra) {
+            slv += d * df;
+            gdm += d * sig * sgn;
+            gwd += d * sig;
+            psl += p * df;
+            pgdm += p * sig * sgn;
+            pgwd += p * sig;
+          }
+        }
+        dsb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(dsv[0], dsv[1]), cvt_pk_bf16(dsv[2], dsv[3]),
+                                      cvt_pk_bf16(dsv[4], dsv[5]), cvt_pk_bf16(dsv[6], dsv[7]));
+        if (MODE == 2)
+          pbv[mb * 2 + hf] = make_uint4(cvt_pk_bf16(pvv[0], pvv[1]), cvt_pk_bf16(pvv[2], pvv[3]),
+                                        cvt_pk_bf16(pvv[4], pvv[5]), cvt_pk_bf16(pvv[6], pvv[7]));
+      }
+    // dQ^T += K^T dS^T (and the token-mode feature sums)
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+      const uint16_t* kt = &Kt[(md * 32 + lr) * TSTR + 4 * g];
+#pragma unroll
+      for (int s2 = 0; s2 < 2 * MB; ++s2) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(kt + 16 * s2);
+        const uint2 hi = *reinterpret_cast<const uint2*>(kt + 16 * s2 + 8);
+        o[md] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), dsb[s2], o[md]);
+      }
+    }
+    if (MODE == 2) {
+      const uint16_t* ft = &Ft[lr * TSTR + 4 * g];
+#pragma unroll
+      for (int s2 = 0; s2 < 2 * MB; ++s2) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(ft + 16 * s2);
+        const uint2 hi = *reinterpret_cast<const uint2*>(ft + 16 * s2 + 8);
+        facc = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), dsb[s2], facc);
+        facc_p = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pbv[s2], facc_p);
+      }
+    }
+    rs += __shfl_xor(rs, 32, 64);
+    pm += __shfl_xor(pm, 32, 64);
+    if (MODE == 1) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        accA[k] += rs * crow[k];
+        accB[k] += rs * srow[k];
+        accPA[k] += pm * crow[k];
+        accPB[k] += pm * srow[k];
+      }
+    }
+    rs_tot += rs;
+    pm_tot += pm;
+    if (extra) {
+      sl_tot += slv + __shfl_xor(slv, 32, 64);
+      gdm_tot += gdm + __shfl_xor(gdm, 32, 64);
+      gwd_tot += gwd + __shfl_xor(gwd, 32, 64);
+      psl_tot += psl + __shfl_xor(psl, 32, 64);
+      pgdm_tot += pgdm + __shfl_xor(pgdm, 32, 64);
+      pgwd_tot += pgwd + __shfl_xor(pgwd, 32, 64);
+    }
+  }
+  const float dd_err = rs_tot;  // Δ_true - Δ
+
+  // ---- epilogue: dQ = scale·o
+  uint16_t* dqp = a.dq + h * a.q_sh + row * a.q_st + 4 * g;
+#pragma unroll
+  for (int md = 0; md < 4; ++md)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      uint2 val;
+      val.x = cvt_pk_bf16(o[md][4 * rq] * a.scale, o[md][4 * rq + 1] * a.scale);
+      val.y = cvt_pk_bf16(o[md][4 * rq + 2] * a.scale, o[md][4 * rq + 3] * a.scale);
+      *reinterpret_cast<uint2*>(dqp + md * 32 + 8 * rq) = val;
+    }
+  const float beta = a.beta;
+  if (MODE == 1 && a.dcoeff_cos && g == 0) {
+    for (int k = 0; k < a.K; ++k) {
+      a.dcoeff_cos[(hT + row) * a.K + k] = beta * (accA[k] - dd_err * accPA[k]);
+      a.dcoeff_sin[(hT + row) * a.K + k] = beta * (accB[k] - dd_err * accPB[k]);
+    }
+  }
+  if (MODE == 2) {
+    if (a.dcoeff_cos) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = 4 * g + i;
+        if (k < a.K) {
+          // feature rows: 4g+i (cos hi), 8+4g+i (sin hi), 16+4g+i (cos lo), 24+4g+i (sin lo)
+          const float C = (facc[i] + facc[8 + i]) - dd_err * (facc_p[i] + facc_p[8 + i]);
+          const float S = (facc[4 + i] + facc[12 + i]) - dd_err * (facc_p[4 + i] + facc_p[12 + i]);
+          a.dcoeff_cos[(hT + row) * a.K + k] = beta * (cos_i[i] * C + sin_i[i] * S);
+          a.dcoeff_sin[(hT + row) * a.K + k] = beta * (sin_i[i] * C - cos_i[i] * S);
+        }
+      }
+    }
+    if (g == 0) {
+      if (a.db0) a.db0[hT + row] = -beta * (rs_tot - dd_err * pm_tot);
+      if (a.dslope) a.dslope[hT + row] = beta * (sl_tot - dd_err * psl_tot);
+      if (a.ddelta_main) a.ddelta_main[hT + row] = beta * a.ramp_lambda * a.inv_tau * (gdm_tot - dd_err * pgdm_tot);
+      if (a.dwidth) a.dwidth[hT + row] = beta * a.ramp_lambda * a.inv_tau * (gwd_tot - dd_err * pgwd_tot);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// plan: chunked work items for the kv-major pass
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, const int32_t* __restrict__ q_off,
+                                                         int32_t* __restrict__ items_start,
+                                                         int32_t* __restrict__ slots_start) {
+  const int h = blockIdx.x;
+  const int32_t* off = q_off + static_cast<int64_t>(h) * (NB + 1);
+  int32_t* it = items_start + static_cast<int64_t>(h) * (NB + 1);
+  int32_t* sl = slots_start + static_cast<int64_t>(h) * (NB + 1);
+  __shared__ int s_it[1024], s_sl[1024];
+  __shared__ int carry_it, carry_sl;
+  if (threadIdx.x == 0) carry_it = carry_sl = 0;
+  __syncthreads();
+  for (int base = 0; base < NB; base += 1024) {
+    const int kb = base + threadIdx.x;
+    int nit = 0, nsl = 0;
+    if (kb < NB) {
+      const int n = off[kb + 1] - off[kb];
+      const int nch = max(1, (n + kChunk - 1) / kChunk);
+      nit = nch;
+      nsl = nch > 1 ? nch : 0;
+    }
+    s_it[threadIdx.x] = nit;
+    s_sl[threadIdx.x] = nsl;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+      const int ai = threadIdx.x >= o ? s_it[threadIdx.x - o] : 0;
+      const int as = threadIdx.x >= o ? s_sl[threadIdx.x - o] : 0;
+      __syncthreads();
+      s_it[threadIdx.x] += ai;
+      s_sl[threadIdx.x] += as;
+      __syncthreads();
+    }
+    const int ci = carry_it, cl = carry_sl;
+    if (kb < NB) {
+      it[kb] = ci + s_it[threadIdx.x] - nit;
+      sl[kb] = cl + s_sl[threadIdx.x] - nsl;
+    }
+    __syncthreads();
+    if (threadIdx.x == 1023) {
+      carry_it = ci + s_it[1023];
+      carry_sl = cl + s_sl[1023];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    it[NB] = carry_it;
+    sl[NB] = carry_sl;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// pass B
+// ---------------------------------------------------------------------------
+struct KvPlan {
+  const int32_t* items_start;
+  const int32_t* slots_start;
+  float* part_dk;
+  float* part_dv;
+  int64_t max_slots;  // per head
+};
+
+template <int BS, int MODE>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl) {
+  constexpr int NT = 256;  // 4 waves = 128 key rows per workgroup (blockIdx.z selects the part)
+  constexpr int D = 128;
+  constexpr int BM = 32;         // q rows per staged sub-tile
+  constexpr int KSTR = D + 8;    // row-major Q / dO
+  constexpr int TSTR = BM + 4;   // transposed Q / dO rows (18 dwords: conflict-free b64 reads)
+  constexpr int FSTR = 40;
+
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[BM * KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Ds[BM * KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Qt[D * TSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Dt[D * TSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Qf[MODE == 2 ? BM * FSTR : 8];
+  __shared__ __attribute__((aligned(16))) float offq[BM];
+  __shared__ __attribute__((aligned(16))) float dltq[BM];
+  __shared__ __attribute__((aligned(16))) int docq[BM];
+  __shared__ __attribute__((aligned(16))) float slq[BM];
+  __shared__ __attribute__((aligned(16))) float dmq[BM];
+  __shared__ __attribute__((aligned(16))) float wdq[BM];
+
+  const int NB = a.QB;
+  const int h = blockIdx.y;
+  const int x = blockIdx.x;
+  const int32_t* its = pl.items_start + static_cast<int64_t>(h) * (NB + 1);
+  if (x >= its[NB]) return;
+  // key block owning item x: largest kb with its[kb] <= x
+  int lo = 0, hi = NB - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (its[mid] <= x) lo = mid;
+    else hi = mid - 1;
+  }
+  const int kb = lo;
+  const int chunk = x - its[kb];
+  const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
+  const int nq = qo[kb + 1] - qo[kb];
+  const int nch = max(1, (nq + kChunk - 1) / kChunk);
+  const int i0 = chunk * kChunk, i1 = min(nq, i0 + kChunk);
+  const int32_t* ql = a.q_list + static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
+  const int64_t kv0 = static_cast<int64_t>(kb) * BS + blockIdx.z * 128;  // first key row of this workgroup
+  const int64_t wkv_lo = kv0 + wave * 32;
+  const int64_t wkv = wkv_lo + lr;
+  const int krow = blockIdx.z * 128 + wave * 32 + lr;  // key row within the block
+  const int64_t hT = static_cast<int64_t>(h) * a.T;
+  const float cs = a.scale_log2;
+
+  uint4 kreg[8], vreg[8];
+  {
+    const uint16_t* kp = a.k + h * a.k_sh + wkv * a.k_st + g * 8;
+    const uint16_t* vp = a.v + h * a.v_sh + wkv * a.v_st + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      kreg[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16);
+      vreg[ks] = *reinterpret_cast<const uint4*>(vp + ks * 16);
+    }
+  }
+  uint4 kf = make_uint4(0, 0, 0, 0), kfl = make_uint4(0, 0, 0, 0);
+  if (MODE == 2) {
+    kf = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + wkv * kTokRow + g * 8);
+    kfl = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + wkv * kTokRow + 16 + g * 8);
+  }
+  const int doc_kv = a.docs[wkv];
+  const bool gate = MODE == 2 && a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
+  const bool extra = MODE == 2 && (a.use_slope || gate);
+  const float glam = a.beta_log2 * a.ramp_lambda;
+
+  f32x16_t dvT[4], dkT[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dvT[i] = zero16();
+    dkT[i] = zero16();
+  }
+
+  for (int i = i0; i < i1; ++i) {
+    const int qb = ql[i];
+    const int ds_end = a.ds_tok_end[qb];
+    for (int sub = 0; sub < BS / BM; ++sub) {
+      const int64_t q0 = static_cast<int64_t>(qb) * BS + sub * BM;
+      if (q0 + BM - 1 < kv0) continue;  // every query row before every key of the block
+      __syncthreads();
+      // ---- stage Q, dO rows (+ transposes), per-query constants
+      for (int idx = tid; idx < BM * 16; idx += NT) {
+        const int r = idx / 16, c = idx % 16;
+        *reinterpret_cast<uint4*>(&Qs[r * KSTR + c * 8]) =
+            *reinterpret_cast<const uint4*>(a.q + h * a.q_sh + (q0 + r) * a.q_st + c * 8);
+        *reinterpret_cast<uint4*>(&Ds[r * KSTR + c * 8]) =
+            *reinterpret_cast<const uint4*>(a.dout + h * a.o_sh + (q0 + r) * a.o_st + c * 8);
+      }
+      if (tid < BM) {
+        const int64_t q = q0 + tid;
+        const float l = a.lse[hT + q];
+        float c = 0.f;
+        if (MODE == 1) {
+          const float* tr = static_cast<const float*>(a.table) + static_cast<int64_t>(qb - kb) * 16;
+          for (int k = 0; k < a.K; ++k)
+            c += a.coeff_cos[(hT + q) * a.K + k] * tr[k] + a.coeff_sin[(hT + q) * a.K + k] * tr[8 + k];
+          c *= a.beta_log2;
+        }
+        if (MODE == 2 && a.subtract_b0) c = -a.beta_log2 * a.b0[hT + q];
+        offq[tid] = l == -INFINITY ? -INFINITY : c - l * kLog2e;
+        dltq[tid] = a.delta[hT + q];
+        docq[tid] = a.docs[q];
+        if (MODE == 2) {
+          slq[tid] = a.use_slope ? a.beta_log2 * a.slope[hT + q] : 0.f;
+          dmq[tid] = gate ? a.delta_main[hT + q] : 0.f;
+          wdq[tid] = gate ? a.width[hT + q] : 0.f;
+        }
+      }
+      if (MODE == 2 && tid >= 64 && tid < 64 + 2 * BM) {
+        const int r = (tid - 64) / 2, gg = (tid - 64) % 2;
+        const int64_t q = q0 + r;
+        uint4 fh, fl;
+        token_qfeat(a, hT, q, gg, fh, fl, nullptr, nullptr);
+        *reinterpret_cast<uint4*>(&Qf[r * FSTR + gg * 8]) = fh;
+        *reinterpret_cast<uint4*>(&Qf[r * FSTR + 16 + gg * 8]) = fl;
+      }
+      __syncthreads();
+      // transposes Q -> Qt, dO -> Dt (4 rows x 8 dims per thread)
+      for (int idx = tid; idx < 2 * (BM / 4) * 16; idx += NT) {
+        const int which = idx / ((BM / 4) * 16);
+        const int rem = idx % ((BM / 4) * 16);
+        const int c = rem % 16, rg = rem / 16;
+        const uint16_t* src = which ? Ds : Qs;
+        uint16_t* dst = which ? Dt : Qt;
+        uint32_t w[4][4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const uint4 u = *reinterpret_cast<const uint4*>(&src[(rg * 4 + rr) * KSTR + c * 8]);
+          w[rr][0] = u.x;
+          w[rr][1] = u.y;
+          w[rr][2] = u.z;
+          w[rr][3] = u.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          uint2 val;
+          if (e & 1) {
+            val.x = pack_hi16(w[0][e / 2], w[1][e / 2]);
+            val.y = pack_hi16(w[2][e / 2], w[3][e / 2]);
+          } else {
+            val.x = pack_lo16(w[0][e / 2], w[1][e / 2]);
+            val.y = pack_lo16(w[2][e / 2], w[3][e / 2]);
+          }
+          *reinterpret_cast<uint2*>(&dst[(c * 8 + e) * TSTR + rg * 4]) = val;
+        }
+      }
+      __syncthreads();
+
+      if (q0 + BM - 1 < wkv_lo) continue;  // this wave's keys all after the rows
+      const bool full = (wkv_lo + 31 <= q0) && (ds_end <= wkv_lo);
+      // S = Q K^T, dP = dO V^T   (rows: queries, columns: this wave's keys)
+      f32x16_t s = zero16(), dp = zero16();
+      const uint16_t* qr = &Qs[lr * KSTR + g * 8];
+      const uint16_t* dr = &Ds[lr * KSTR + g * 8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        s = mfma32(*reinterpret_cast<const uint4*>(qr + ks * 16), kreg[ks], s);
+        dp = mfma32(*reinterpret_cast<const uint4*>(dr + ks * 16), vreg[ks], dp);
+      }
+      if (MODE == 2) {
+        const uint4 qh = *reinterpret_cast<const uint4*>(&Qf[lr * FSTR + g * 8]);
+        const uint4 qlo = *reinterpret_cast<const uint4*>(&Qf[lr * FSTR + 16 + g * 8]);
+        s = mfma32(qh, kf, s);
+        s = mfma32(qlo, kf, s);
+        s = mfma32(qh, kfl, s);
+      }
+      uint4 pb[2], dsb[2];
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int qi0 = 8 * rq + 4 * g;  // 4 consecutive query rows of this register quad
+        const float4 of4 = *reinterpret_cast<const float4*>(&offq[qi0]);
+        const float4 dl4 = *reinterpret_cast<const float4*>(&dltq[qi0]);
+        const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
+        const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
+        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+        const int dcv[4] = {dc4.x, dc4.y, dc4.z, dc4.w};
+        float pv[4], dsv[4];
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+          const int r = 4 * rq + i2;
+          const int64_t q = q0 + qi0 + i2;
+          float x = s[r];
+          if (!full) {
+            const bool ok = (wkv <= q) & (dcv[i2] == doc_kv);
+            x = ok ? x : -INFINITY;
+          }
+          if (extra) {
+            const float df = static_cast<float>(q - wkv);
+            float e = slq[qi0 + i2] * df;
+            if (gate) {
+              const float xx = (fabsf(df - dmq[qi0 + i2]) - wdq[qi0 + i2]) * a.inv_tau;
+              const float gt = a.gate_kind == SCOPE_GATE_SOFTPLUS ? fmaxf(xx, 0.f) + log1pf(__expf(-fabsf(xx)))
+                                                                  : fmaxf(xx, 0.f);
+              e -= glam * gt;
+            }
+            x = fmaf(x, cs, e);
+          } else {
+            x = x * cs;
+          }
+          const float p = exp2f(x + ofv[i2]);
+          pv[i2] = p;
+          dsv[i2] = p * (dp[r] - dlv[i2]);
+        }
+        // register quad rq -> k-step rq/2, slots 4*(rq%2) .. +3
+        const uint32_t p01 = cvt_pk_bf16(pv[0], pv[1]), p23 = cvt_pk_bf16(pv[2], pv[3]);
+        const uint32_t d01 = cvt_pk_bf16(dsv[0], dsv[1]), d23 = cvt_pk_bf16(dsv[2], dsv[3]);
+        if (rq % 2 == 0) {
+          pb[rq / 2].x = p01;
+          pb[rq / 2].y = p23;
+          dsb[rq / 2].x = d01;
+          dsb[rq / 2].y = d23;
+        } else {
+          pb[rq / 2].z = p01;
+          pb[rq / 2].w = p23;
+          dsb[rq / 2].z = d01;
+          dsb[rq / 2].w = d23;
+        }
+      }
+      // dV^T += dO^T P,  dK^T += Q^T dS
+#pragma unroll
+      for (int md = 0; md < 4; ++md) {
+        const uint16_t* dt = &Dt[(md * 32 + lr) * TSTR + 4 * g];
+        const uint16_t* qt = &Qt[(md * 32 + lr) * TSTR + 4 * g];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const uint2 dlo = *reinterpret_cast<const uint2*>(dt + 16 * s2);
+          const uint2 dhi = *reinterpret_cast<const uint2*>(dt + 16 * s2 + 8);
+          dvT[md] = mfma32(make_uint4(dlo.x, dlo.y, dhi.x, dhi.y), pb[s2], dvT[md]);
+          const uint2 qlo = *reinterpret_cast<const uint2*>(qt + 16 * s2);
+          const uint2 qhi = *reinterpret_cast<const uint2*>(qt + 16 * s2 + 8);
+          dkT[md] = mfma32(make_uint4(qlo.x, qlo.y, qhi.x, qhi.y), dsb[s2], dkT[md]);
+        }
+      }
+    }
+  }
+
+  // ---- write dK = scale·dkT^T, dV = dvT^T
+  if (nch == 1) {
+    uint16_t* dkp = a.dk + h * a.k_sh + wkv * a.k_st + 4 * g;
+    uint16_t* dvp = a.dv + h * a.v_sh + wkv * a.v_st + 4 * g;
+#pragma unroll
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        uint2 vk, vv;
+        vk.x = cvt_pk_bf16(dkT[md][4 * rq] * a.scale, dkT[md][4 * rq + 1] * a.scale);
+        vk.y = cvt_pk_bf16(dkT[md][4 * rq + 2] * a.scale, dkT[md][4 * rq + 3] * a.scale);
+        vv.x = cvt_pk_bf16(dvT[md][4 * rq], dvT[md][4 * rq + 1]);
+        vv.y = cvt_pk_bf16(dvT[md][4 * rq + 2], dvT[md][4 * rq + 3]);
+        *reinterpret_cast<uint2*>(dkp + md * 32 + 8 * rq) = vk;
+        *reinterpret_cast<uint2*>(dvp + md * 32 + 8 * rq) = vv;
+      }
+  } else {
+    const int64_t slot = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb] + chunk;
+    float* pk = pl.part_dk + (slot * BS + krow) * D + 4 * g;
+    float* pv = pl.part_dv + (slot * BS + krow) * D + 4 * g;
+#pragma unroll
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        *reinterpret_cast<float4*>(pk + md * 32 + 8 * rq) =
+            make_float4(dkT[md][4 * rq], dkT[md][4 * rq + 1], dkT[md][4 * rq + 2], dkT[md][4 * rq + 3]);
+        *reinterpret_cast<float4*>(pv + md * 32 + 8 * rq) =
+            make_float4(dvT[md][4 * rq], dvT[md][4 * rq + 1], dvT[md][4 * rq + 2], dvT[md][4 * rq + 3]);
+      }
+  }
+}
+
+// Sum the chunk partials of every multi-chunk key block in chunk order.
+__global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl, int BS) {
+  constexpr int D = 128;
+  const int NB = a.QB;
+  const int kb = blockIdx.x, h = blockIdx.y;
+  const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
+  const int nq = qo[kb + 1] - qo[kb];
+  const int nch = max(1, (nq + kChunk - 1) / kChunk);
+  if (nch <= 1) return;
+  const int64_t slot0 = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb];
+  const int64_t kv0 = static_cast<int64_t>(kb) * BS;
+  for (int e4 = threadIdx.x; e4 < BS * D / 4; e4 += blockDim.x) {
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+    for (int c = 0; c < nch; ++c) {
+      const float4 pk = reinterpret_cast<const float4*>(pl.part_dk + (slot0 + c) * BS * D)[e4];
+      const float4 pv = reinterpret_cast<const float4*>(pl.part_dv + (slot0 + c) * BS * D)[e4];
+      sk.x += pk.x; sk.y += pk.y; sk.z += pk.z; sk.w += pk.w;
+      sv.x += pv.x; sv.y += pv.y; sv.z += pv.z; sv.w += pv.w;
+    }
+    const int r = (e4 * 4) / D, d = (e4 * 4) % D;
+    uint2 vk, vv;
+    vk.x = cvt_pk_bf16(sk.x * a.scale, sk.y * a.scale);
+    vk.y = cvt_pk_bf16(sk.z * a.scale, sk.w * a.scale);
+    vv.x = cvt_pk_bf16(sv.x, sv.y);
+    vv.y = cvt_pk_bf16(sv.z, sv.w);
+    *reinterpret_cast<uint2*>(a.dk + h * a.k_sh + (kv0 + r) * a.k_st + d) = vk;
+    *reinterpret_cast<uint2*>(a.dv + h * a.v_sh + (kv0 + r) * a.v_st + d) = vv;
+  }
+}
+
+struct BwdLayout {
+  int64_t delta, items, slots, part_dk, part_dv, total, max_slots;
+  int max_items;
+};
+
+static BwdLayout bwd_layout(const scope_attn_params* p) {
+  BwdLayout L = {};
+  const int64_t QB = p->T / p->bs, NB = QB;
+  const int64_t per_head_items = NB + (QB * p->maxkv + kChunk - 1) / kChunk;
+  L.max_items = static_cast<int>(per_head_items);
+  L.max_slots = (2 * QB * p->maxkv + kChunk - 1) / kChunk + 1;
+  auto al = [](int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); };
+  int64_t o = 0;
+  L.delta = o;
+  o += al(static_cast<int64_t>(p->H) * p->T * 4);
+  L.items = o;
+  o += al(static_cast<int64_t>(p->H) * (NB + 1) * 4);
+  L.slots = o;
+  o += al(static_cast<int64_t>(p->H) * (NB + 1) * 4);
+  const int64_t part = static_cast<int64_t>(p->H) * L.max_slots * p->bs * 128 * 4;
+  L.part_dk = o;
+  o += al(part);
+  L.part_dv = o;
+  o += al(part);
+  L.total = o;
+  return L;
+}
+
+template <int BS>
+static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int grid_q, int max_items, hipStream_t s) {
+  dim3 gq(grid_q * (BS / 128)), gk(max_items, a.H, BS / 128), gr(a.QB, a.H);
+  if (mode == SCOPE_BIAS_BLOCK) {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 1>), gq, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
+                       const_cast<int32_t*>(pl.slots_start));
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
+  } else if (mode == SCOPE_BIAS_TOKEN) {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 2>), gq, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
+                       const_cast<int32_t*>(pl.slots_start));
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2>), gk, dim3(256), 0, s, a, pl);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 0>), gq, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
+                       const_cast<int32_t*>(pl.slots_start));
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 0>), gk, dim3(256), 0, s, a, pl);
+  }
+  hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
+}
+
+}  // namespace scope
 
 using namespace scope;
 
-extern "C" int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p) { return 0; }
+extern "C" int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p) {
+  if (!p || p->bs <= 0 || p->T <= 0) return 0;
+  return bwd_layout(p).total;
+}
 
 extern "C" int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               const uint16_t* out, const uint16_t* dout, const float* lse, const int32_t* kv_num,
@@ -13,5 +818,56 @@ extern "C" int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, con
                               const float* width, uint16_t* dq, uint16_t* dk, uint16_t* dv, float* dcoeff_cos,
                               float* dcoeff_sin, float* db0, float* dslope, float* ddelta_main, float* dwidth,
                               void* workspace, void* stream) {
-  return set_error(SCOPE_EINVAL, "scope_attn_bwd: backward not available in this build");
+  int rc = validate_attn(p, q, k, v, kv_num, kv_idx, docs, ds_tok_end, table, coeff_cos, coeff_sin, b0, slope,
+                         delta_main, width, "scope_attn_bwd");
+  if (rc) return rc;
+  SCOPE_REQUIRE(out && dout && lse && q_off && q_list && dq && dk && dv && workspace,
+                "scope_attn_bwd: null pointer");
+  SCOPE_REQUIRE(!dcoeff_cos == !dcoeff_sin, "scope_attn_bwd: dcoeff_cos and dcoeff_sin go together");
+  AttnArgs a = make_args(p);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = out;
+  a.dout = dout;
+  a.lse = lse;
+  a.kv_num = kv_num;
+  a.kv_idx = kv_idx;
+  a.q_off = q_off;
+  a.q_list = q_list;
+  a.docs = docs;
+  a.ds_tok_end = ds_tok_end;
+  a.table = table;
+  a.coeff_cos = coeff_cos;
+  a.coeff_sin = coeff_sin;
+  a.b0 = b0;
+  a.slope = slope;
+  a.delta_main = delta_main;
+  a.width = width;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.dcoeff_cos = p->bias_mode != SCOPE_BIAS_NONE ? dcoeff_cos : nullptr;
+  a.dcoeff_sin = p->bias_mode != SCOPE_BIAS_NONE ? dcoeff_sin : nullptr;
+  const bool tok = p->bias_mode == SCOPE_BIAS_TOKEN;
+  a.db0 = tok && p->subtract_b0 ? db0 : nullptr;
+  a.dslope = tok && p->use_slope ? dslope : nullptr;
+  a.ddelta_main = tok && p->gate_kind != SCOPE_GATE_NONE ? ddelta_main : nullptr;
+  a.dwidth = tok && p->gate_kind != SCOPE_GATE_NONE ? dwidth : nullptr;
+  const BwdLayout L = bwd_layout(p);
+  char* ws = static_cast<char*>(workspace);
+  a.delta = reinterpret_cast<float*>(ws + L.delta);
+  KvPlan pl;
+  pl.items_start = reinterpret_cast<const int32_t*>(ws + L.items);
+  pl.slots_start = reinterpret_cast<const int32_t*>(ws + L.slots);
+  pl.part_dk = reinterpret_cast<float*>(ws + L.part_dk);
+  pl.part_dv = reinterpret_cast<float*>(ws + L.part_dv);
+  pl.max_slots = L.max_slots;
+  hipStream_t s = as_stream(stream);
+  const int grid_q = p->H * a.QB;
+  if (p->bs == 256)
+    launch_bwd<256>(a, pl, p->bias_mode, grid_q, L.max_items, s);
+  else
+    launch_bwd<128>(a, pl, p->bias_mode, grid_q, L.max_items, s);
+  return check_launch("attention backward kernels");
 }

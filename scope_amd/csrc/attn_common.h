@@ -59,6 +59,31 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Token-mode table row (one per token j): 32 bf16 = cos(ω_k j) hi[8], sin hi[8],
+// cos lo[8], sin lo[8], where hi = bf16(x) and lo = bf16(x - hi).  The band
+// term runs as three MFMA k-steps (hi·hi + hi·lo + lo·hi), which carries the
+// features at about 16 mantissa bits.
+constexpr int kTokRow = 32;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// cos/sin(ω_k j) (hi + lo) for band k from a table row
+__device__ __forceinline__ void tok_trig(const uint32_t* row32, int k, float& c, float& s) {
+  const uint32_t ch = row32[k / 2], sh = row32[4 + k / 2], cl = row32[8 + k / 2], sl = row32[12 + k / 2];
+  c = (k & 1) ? bf16_hi(ch) + bf16_hi(cl) : bf16_lo(ch) + bf16_lo(cl);
+  s = (k & 1) ? bf16_hi(sh) + bf16_hi(sl) : bf16_lo(sh) + bf16_lo(sl);
+}
+
+// 8 fp32 -> (hi, lo) bf16x8 pairs
+__device__ __forceinline__ void split8(const float* f, uint4& hi, uint4& lo) {
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = f[i] - static_cast<float>(static_cast<__bf16>(f[i]));
+  hi = make_uint4(cvt_pk_bf16(f[0], f[1]), cvt_pk_bf16(f[2], f[3]), cvt_pk_bf16(f[4], f[5]), cvt_pk_bf16(f[6], f[7]));
+  lo = make_uint4(cvt_pk_bf16(r[0], r[1]), cvt_pk_bf16(r[2], r[3]), cvt_pk_bf16(r[4], r[5]), cvt_pk_bf16(r[6], r[7]));
+}
 constexpr float kLn2 = 0.6931471805599453f;
 
 struct AttnArgs {
@@ -105,11 +130,37 @@ struct AttnArgs {
   float ramp_lambda, inv_tau;
 };
 
+// Query-side token features of one row for lane group g (0: A cos + B sin,
+// 1: A sin - B cos, k = 0..7) scaled by feat_scale, split hi/lo; also returns
+// cos/sin(ω_k row) for k = 4g..4g+3 (for the coefficient gradients).
+struct AttnArgs;
+__device__ __forceinline__ void token_qfeat(const AttnArgs& a, int64_t hT, int64_t row, int g, uint4& hi, uint4& lo,
+                                            float* cos_g, float* sin_g);
+
 // host helpers shared by the forward and backward entry points (attn_fwd.hip)
 int validate_attn(const scope_attn_params* p, const void* q, const void* k, const void* v, const int32_t* kv_num,
                   const int32_t* kv_idx, const int32_t* docs, const int32_t* ds_tok_end, const void* table,
                   const float* cc, const float* cs, const float* b0, const float* slope, const float* dm,
                   const float* wd, const char* who);
 AttnArgs make_args(const scope_attn_params* p);
+
+__device__ __forceinline__ void token_qfeat(const AttnArgs& a, int64_t hT, int64_t row, int g, uint4& hi, uint4& lo,
+                                            float* cos_g, float* sin_g) {
+  const uint32_t* tb = static_cast<const uint32_t*>(a.table) + row * (kTokRow / 2);
+  float f[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float c, s;
+    tok_trig(tb, k, c, s);
+    const float A = k < a.K ? a.coeff_cos[(hT + row) * a.K + k] : 0.f;
+    const float B = k < a.K ? a.coeff_sin[(hT + row) * a.K + k] : 0.f;
+    f[k] = (g == 0 ? (A * c + B * s) : (A * s - B * c)) * a.feat_scale;
+    if (cos_g && (k >> 2) == g) {
+      cos_g[k & 3] = c;
+      sin_g[k & 3] = s;
+    }
+  }
+  split8(f, hi, lo);
+}
 
 }  // namespace scope

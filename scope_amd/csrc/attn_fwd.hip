@@ -14,10 +14,11 @@
 //   0 none
 //   1 block offsets: β Σ_k A_k(i) cos(ω_k r) + B_k(i) sin(ω_k r), r = qb - kb,
 //     a per-(row, key block) constant folded into the softmax offset
-//   2 token offsets (the reference's score_mod): the band term enters as one
-//     extra MFMA k-step over 16 bf16 features (cos/sin(ω_k j) on the key side,
-//     the angle-addition coefficients on the query side); -b0 is a row
-//     constant; slope·Δ and the softplus/relu gate are evaluated per element.
+//   2 token offsets (the reference's score_mod): the band term enters as
+//     extra MFMA k-steps over 16 features (cos/sin(ω_k j) on the key side,
+//     the angle-addition coefficients on the query side), each split into
+//     bf16 hi + lo; -b0 is a row constant; slope·Δ and the softplus/relu gate
+//     are evaluated per element.
 //
 // Masking: a sub-tile is unmasked when it ends at or before the wave's first
 // row and no document starts between its first key and the block's last
@@ -36,13 +37,15 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
   constexpr int D = 128;
   constexpr int KSTR = D + 8;   // bf16 per K row in LDS   (68 dwords: conflict-free b128 reads)
   constexpr int VSTR = BN + 4;  // bf16 per V^T row in LDS (conflict-free b64 reads)
-  constexpr int FSTR = 24;      // bf16 per feature row    (12 dwords: conflict-free b128 reads)
+  constexpr int FSTR = 40;      // bf16 per feature row    (20 dwords: conflict-free b128 reads)
   constexpr int NSUB = BS / BN;
   constexpr int MB = BN / 32;
   constexpr int KCH = BN * 16;             // 16-byte K chunks per sub-tile
   constexpr int VBL = BN * 4;              // 4x8 V blocks per sub-tile
   constexpr int KL = (KCH + NT - 1) / NT;  // per thread
   constexpr int VL = (VBL + NT - 1) / NT;
+  constexpr int FCH = BN * 4;              // 16-byte feature chunks per sub-tile (token mode)
+  constexpr int FL = (FCH + NT - 1) / NT;
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KSTR];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VSTR];
@@ -67,7 +70,7 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
 
   // ---- bias set-up (per row)
   float ca[8], sa[8];
-  uint4 qf = make_uint4(0, 0, 0, 0);
+  uint4 qf = make_uint4(0, 0, 0, 0), qfl = make_uint4(0, 0, 0, 0);
   float rowc = 0.f, slp = 0.f, dm = 0.f, wd = 0.f, glam = 0.f;
   if (MODE == 1) {
 #pragma unroll
@@ -77,19 +80,7 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
     }
   }
   if (MODE == 2) {
-    const uint32_t* tb = static_cast<const uint32_t*>(a.table) + row * 8;
-    float f[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t cw = tb[k / 2], sw = tb[4 + k / 2];
-      const float c = (k & 1) ? __uint_as_float(cw & 0xffff0000u) : __uint_as_float(cw << 16);
-      const float s = (k & 1) ? __uint_as_float(sw & 0xffff0000u) : __uint_as_float(sw << 16);
-      const float A = k < a.K ? a.coeff_cos[(hT + row) * a.K + k] : 0.f;
-      const float B = k < a.K ? a.coeff_sin[(hT + row) * a.K + k] : 0.f;
-      f[k] = (g == 0 ? (A * c + B * s) : (A * s - B * c)) * a.feat_scale;
-    }
-    qf = make_uint4(cvt_pk_bf16(f[0], f[1]), cvt_pk_bf16(f[2], f[3]), cvt_pk_bf16(f[4], f[5]),
-                    cvt_pk_bf16(f[6], f[7]));
+    token_qfeat(a, hT, row, g, qf, qfl, nullptr, nullptr);
     if (a.subtract_b0) rowc = -a.beta_log2 * a.b0[hT + row];
     if (a.use_slope) slp = a.beta_log2 * a.slope[hT + row];
     if (a.gate_kind != SCOPE_GATE_NONE) {
@@ -111,7 +102,7 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
   uint4 kpre[KL];
   uint4 vpre[VL][4];
   int dpre = 0;
-  uint4 fpre = make_uint4(0, 0, 0, 0);
+  uint4 fpre[FL];
   auto load = [&](int it) {
     const int kb = lst[it / NSUB];
     const int64_t kv0 = static_cast<int64_t>(kb) * BS + (it % NSUB) * BN;
@@ -133,9 +124,15 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
       }
     }
     if (tid < BN) dpre = a.docs[kv0 + tid];
-    if (MODE == 2 && tid < 2 * BN)
-      fpre = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + (kv0 + tid / 2) * 16 +
-                                             (tid % 2) * 8);
+    if (MODE == 2) {
+#pragma unroll
+      for (int i = 0; i < FL; ++i) {
+        const int idx = tid + i * NT;
+        if (FCH % NT == 0 || idx < FCH)
+          fpre[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + (kv0 + idx / 4) * kTokRow +
+                                                    (idx % 4) * 8);
+      }
+    }
   };
   auto store = [&]() {
 #pragma unroll
@@ -168,7 +165,13 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
       }
     }
     if (tid < BN) docs_s[tid] = dpre;
-    if (MODE == 2 && tid < 2 * BN) *reinterpret_cast<uint4*>(&Fs[(tid / 2) * FSTR + (tid % 2) * 8]) = fpre;
+    if (MODE == 2) {
+#pragma unroll
+      for (int i = 0; i < FL; ++i) {
+        const int idx = tid + i * NT;
+        if (FCH % NT == 0 || idx < FCH) *reinterpret_cast<uint4*>(&Fs[(idx / 4) * FSTR + (idx % 4) * 8]) = fpre[i];
+      }
+    }
   };
 
   f32x16_t o[4];
@@ -208,7 +211,13 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
       const uint16_t* kr = &Ks[(mb * 32 + lr) * KSTR + g * 8];
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) s[mb] = mfma32(*reinterpret_cast<const uint4*>(kr + ks * 16), qreg[ks], s[mb]);
-      if (MODE == 2) s[mb] = mfma32(*reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + g * 8]), qf, s[mb]);
+      if (MODE == 2) {
+        const uint4 fh = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + g * 8]);
+        const uint4 fl = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + 16 + g * 8]);
+        s[mb] = mfma32(fh, qf, s[mb]);
+        s[mb] = mfma32(fh, qfl, s[mb]);
+        s[mb] = mfma32(fl, qf, s[mb]);
+      }
     }
 
     if (!full) {

@@ -1,0 +1,121 @@
+"""GPU parity of kernel 2's backward against fp64 autograd through the
+block-sparse oracle.  Bar written in every comparison:
+|got - ref| <= 2e-2 + 1e-2·|ref| elementwise (dq, dk, dv, coefficient grads)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle.pointer import doc_start_blocks
+from tests.helpers import band_coefficients, docs_with_boundaries, omegas_block, qkv, random_blockscore_mask, tol_check
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ATOL, RTOL = 2e-2, 1e-2
+SCALE, BETA = 0.12, 0.5
+
+
+def _terms(mode, q, H, T, seed):
+    if mode == "block":
+        A, B = band_coefficients(q)
+        return dict(coeff_cos=A, coeff_sin=B, omegas=omegas_block(8))
+    if mode == "token":
+        g = torch.Generator().manual_seed(seed)
+        K = 6
+        cc = torch.randn((1, H, T, K), generator=g) * 0.3
+        cs = torch.randn((1, H, T, K), generator=g) * 0.3
+        return dict(coeff_cos=cc, coeff_sin=cs, omegas=OA.omegas_logspaced(K, 1024, 1 << 20), b0=cc.sum(-1),
+                    slope=torch.randn((1, H, T), generator=g) * 0.002,
+                    delta_main=torch.rand((1, H, T), generator=g) * 300,
+                    width=32 + torch.rand((1, H, T), generator=g) * 200)
+    return {}
+
+
+def _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms):
+    import scope_amd
+    from scope_amd.blockmask import ScopeBlockMask
+
+    bm = ScopeBlockMask(kv_num_blocks=kv_num[None].to(DEV), kv_indices=kv_idx[None].to(DEV), BLOCK_SIZE=bs,
+                        docs=docs.to(DEV), ds_tok_end=torch.from_numpy(doc_start_blocks(docs.numpy(), bs)[2]).to(DEV))
+    qd, kd, vd = (x.to(DEV).requires_grad_() for x in (q, k, v))
+    sp = None
+    leaves = []
+    if mode != "none":
+        t = {n: (x.to(DEV).requires_grad_() if (torch.is_tensor(x) and n != "omegas") else x) for n, x in terms.items()}
+        sp = scope_amd.SpectralTerms(coeff_cos=t["coeff_cos"], coeff_sin=t["coeff_sin"], omegas=t["omegas"].to(DEV),
+                                     offset=mode, beta=BETA)
+        leaves = [t["coeff_cos"], t["coeff_sin"]]
+        if mode == "token":
+            sp.b0, sp.slope, sp.delta_main, sp.width = t["b0"], t["slope"], t["delta_main"], t["width"]
+            sp.use_slope = sp.subtract_b0 = True
+            sp.gate_kind, sp.ramp_lambda, sp.tau = "softplus", 0.2, 64.0
+            leaves += [t["b0"], t["slope"], t["delta_main"], t["width"]]
+    out = scope_amd.scope_attention(qd, kd, vd, block_mask=bm, scale=SCALE, spectral=sp)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    grads = [qd.grad, kd.grad, vd.grad] + [x.grad for x in leaves]
+    return [gr.float().cpu() for gr in grads]
+
+
+def _ref_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms):
+    qq, kk, vv = (x[0].double().requires_grad_() for x in (q, k, v))
+    kw = dict(bias_mode=mode)
+    leaves = []
+    if mode != "none":
+        cc = terms["coeff_cos"][0].double().requires_grad_()
+        cs = terms["coeff_sin"][0].double().requires_grad_()
+        kw.update(coeff_cos=cc, coeff_sin=cs, omegas=terms["omegas"].double())
+        leaves = [cc, cs]
+    if mode == "token":
+        b0, sl, dm, wd = (terms[n][0].double().requires_grad_() for n in ("b0", "slope", "delta_main", "width"))
+        kw["token_kwargs"] = dict(b0=b0, slope=sl, delta_main=dm, width=wd, gate="softplus", ramp_lambda=0.2,
+                                  tau=64.0)
+        leaves += [b0, sl, dm, wd]
+    out, _ = OA.scope_attention_blocksparse(qq, kk, vv, kv_num, kv_idx, docs, bs=bs, scale=SCALE, beta=BETA, **kw)
+    out.backward(dout[0].double())
+    return [x.grad[None] for x in (qq, kk, vv)] + [x.grad[None] for x in leaves]
+
+
+NAMES = ["dq", "dk", "dv", "dcoeff_cos", "dcoeff_sin", "db0", "dslope", "ddelta_main", "dwidth"]
+CASES = [
+    # (H, T, bs, mode, n_docs, W, G, B)
+    (2, 1024, 128, "none", 1, 2, 1, 2),
+    (2, 1024, 128, "block", 3, 2, 1, 2),
+    (2, 2048, 256, "block", 3, 2, 2, 3),
+    (1, 1024, 128, "token", 2, 2, 1, 2),
+    (1, 2048, 256, "token", 2, 2, 1, 2),
+    (2, 4096, 128, "block", 1, 2, 1, 3),   # q-list of the global block (32 q-blocks) -> chunked dK/dV
+    (1, 8192, 256, "none", 2, 2, 2, 4),    # chunked dK/dV at bs=256
+]
+
+
+@pytest.mark.parametrize("H,T,bs,mode,n_docs,W,G,B", CASES)
+def test_attn_bwd_vs_fp64_autograd(H, T, bs, mode, n_docs, W, G, B):
+    print(f"bwd H={H} T={T} bs={bs} mode={mode} docs={n_docs}", flush=True)
+    q, k, v = qkv(H, T, seed=T + 7 * bs)
+    dout = torch.randn((1, H, T, 128), generator=torch.Generator().manual_seed(99)).to(torch.bfloat16)
+    docs = docs_with_boundaries(T, n_docs, seed=bs + 1)
+    kv_num, kv_idx = random_blockscore_mask(H, T, bs, docs, window=W, n_global=G, budget=B, seed=T)
+    terms = _terms(mode, q, H, T, seed=T)
+    got = _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms)
+    ref = _ref_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms)
+    assert len(got) == len(ref)
+    for name, gg, rr in zip(NAMES, got, ref):
+        ok, worst = tol_check(gg, rr, ATOL, RTOL)
+        print(f"  {name}: worst ratio {worst:.3f} (max |ref| {rr.abs().max().item():.3g})")
+        assert ok, f"{name} violates 2e-2 abs / 1e-2 rel: worst ratio {worst:.3f}"
+
+
+def test_attn_bwd_deterministic():
+    """Two backward runs give identical bits (no floating-point atomics)."""
+    H, T, bs = 2, 4096, 128
+    q, k, v = qkv(H, T, seed=1)
+    dout = torch.randn((1, H, T, 128), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    docs = docs_with_boundaries(T, 2, seed=3)
+    kv_num, kv_idx = random_blockscore_mask(H, T, bs, docs, window=2, n_global=1, budget=3, seed=4)
+    terms = _terms("block", q, H, T, 0)
+    g1 = _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, "block", terms)
+    g2 = _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, "block", terms)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
