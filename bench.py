@@ -1,0 +1,307 @@
+"""Benchmark of the SCOPE attention hot path on one MI355X.
+
+One step = one pass of the hot path over one synthetic batch:
+doc starts -> block means -> pointer selection (block-mean q·k + Gumbel top-k
+under the budget) -> mask statistics -> q-list transpose -> block-sparse
+attention forward -> backward (dq, dk, dv and the spectral coefficient
+gradients).  Inputs are resident in HBM before the timed region.
+
+Workload (long-context prefill, one layer): B=1, H=8, T=131072, D=128 bf16,
+block 256 (512 blocks), window 2, 2 doc-local global blocks, pointer budget 8
+(sweep {2,4,8} with --sweep), 8 spectral bands ω_k = π·2^-k over block
+offsets with coefficients q·W_b (W_b ~ N(0, 0.02) [D,16]), documents starting
+at seeded positions (~1 per 8192 tokens), a planted needle (a key block equal
+to 3 × a query block's mean query, ≥ 64 blocks back), seeded in-kernel Gumbel
+noise, dO ~ N(0,1).
+
+value = active-block TFLOP/s = (F_fwd + F_bwd) / step time, with
+F_fwd = 4·bs²·D·N_act, F_bwd = 10·bs²·D·N_act, N_act = Σ kv_num_blocks.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "SCOPE attn fwd+bwd active-block TFLOP/s & tokens/s at T=128k, 1 MI355X"
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--budget", type=int, default=8)
+    ap.add_argument("--T", type=int, default=131072)
+    ap.add_argument("--H", type=int, default=8)
+    ap.add_argument("--bs", type=int, default=256)
+    ap.add_argument("--window", type=int, default=2)
+    ap.add_argument("--n-global", type=int, default=2)
+    ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def make_inputs(H, T, D, bs, seed=0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((1, H, T, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, H, T, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, H, T, D), generator=g).to(torch.bfloat16)
+    dout = torch.randn((1, H, T, D), generator=g).to(torch.bfloat16)
+    n_docs = max(1, T // 8192)
+    cuts = torch.randperm(T - 1, generator=g)[: n_docs - 1] + 1
+    flag = torch.zeros(T, dtype=torch.int64)
+    flag[cuts] = 1
+    docs = flag.cumsum(0).to(torch.int32)
+    NB = T // bs
+    # planted needle: key block kb = 3 × mean query of block qb, ≥ 64 blocks back
+    qb_n = int(torch.randint(min(64, NB - 1), NB, (1,), generator=g))
+    dist = int(torch.randint(min(64, qb_n), qb_n + 1, (1,), generator=g)) if qb_n >= 64 else qb_n
+    kb_n = qb_n - dist
+    mq = q[0, :, qb_n * bs:(qb_n + 1) * bs].float().mean(dim=1)
+    k[0, :, kb_n * bs:(kb_n + 1) * bs] = (3.0 * mq[:, None, :]).to(torch.bfloat16)
+    W = torch.randn((D, 16), generator=g) * 0.02
+    c = q.float() @ W
+    coeff_cos, coeff_sin = c[..., :8].contiguous(), c[..., 8:].contiguous()
+    omegas = torch.tensor([math.pi * 2.0 ** (-i) for i in range(8)], dtype=torch.float32)
+    return dict(q=q, k=k, v=v, dout=dout, docs=docs, coeff_cos=coeff_cos, coeff_sin=coeff_sin, omegas=omegas,
+                needle=(qb_n, kb_n))
+
+
+class Step:
+    """The hot path on GPU-resident inputs; phase events on the current stream."""
+
+    def __init__(self, inp, *, bs, window, n_global, budget, seed=1234):
+        import torch
+
+        from scope_amd import ops
+        from scope_amd.attention import spectral_table
+
+        self.t = {k_: (v_.cuda() if torch.is_tensor(v_) else v_) for k_, v_ in inp.items()}
+        self.bs, self.window, self.n_global, self.budget, self.seed = bs, window, n_global, budget, seed
+        self.H, self.T = self.t["q"].shape[1], self.t["q"].shape[2]
+        self.NB = self.T // bs
+        self.table = spectral_table(self.t["omegas"], self.T, bs, "block")
+        self.ops = ops
+        self.phases = ["pointer", "stats", "transpose", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"]
+        self.ev = {p: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for p in self.phases}
+        self.acc = {p: 0.0 for p in self.phases}
+
+    def __call__(self, record=False):
+        ops, t, bs = self.ops, self.t, self.bs
+        ev = self.ev
+
+        def mark(p, i):
+            if record:
+                ev[p][i].record()
+
+        mark("pointer", 0)
+        ds_ptr, ds_local, ds_tok_end = ops.doc_starts(t["docs"], bs)
+        qbar, kbar = ops.block_means(t["q"], t["k"], bs)
+        kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=self.NB, H=self.H,
+                                                   window=self.window, n_global=self.n_global, budget=self.budget,
+                                                   qbar=qbar, kbar=kbar, temp=1.0,
+                                                   logit_scale=bs / math.sqrt(t["q"].shape[-1]), noise="counter",
+                                                   seed=self.seed)
+        mark("pointer", 1)
+        mark("stats", 0)
+        counts, values = ops.mask_stats(H=self.H, QB=self.NB, bs=bs, kv_num=kv_num, picks=picks, ds_ptr=ds_ptr,
+                                        ds_local=ds_local, maxkv_bins=kv_idx.shape[-1] + 1,
+                                        bs_local_blocks=self.window)
+        mark("stats", 1)
+        mark("transpose", 0)
+        q_off, q_list = ops.transpose_blocks(kv_num, kv_idx, self.NB)
+        mark("transpose", 1)
+        mark("attn_fwd", 0)
+        out, lse = ops.attn_fwd(t["q"], t["k"], t["v"], kv_num, kv_idx, t["docs"], ds_tok_end, bs=bs, scale=0.12,
+                                beta=0.5, bias_mode="block", table=self.table, coeff_cos=t["coeff_cos"],
+                                coeff_sin=t["coeff_sin"])
+        mark("attn_fwd", 1)
+        def hook(phase):
+            if phase == "dq":
+                mark("attn_bwd_dq", 0)
+            elif phase == "dkv":
+                mark("attn_bwd_dq", 1)
+                mark("attn_bwd_dkv", 0)
+            else:
+                mark("attn_bwd_dkv", 1)
+
+        grads = ops.attn_bwd(t["q"], t["k"], t["v"], out, t["dout"], lse, kv_num, kv_idx, q_off, q_list, t["docs"],
+                             ds_tok_end, bs=bs, scale=0.12, beta=0.5, bias_mode="block", table=self.table,
+                             coeff_cos=t["coeff_cos"], coeff_sin=t["coeff_sin"], phase_hook=hook)
+        self.last = dict(kv_num=kv_num, kv_idx=kv_idx, picks=picks, counts=counts, values=values, out=out, lse=lse,
+                         grads=grads, q_off=q_off, q_list=q_list, ds_tok_end=ds_tok_end)
+
+    def collect(self):
+        for p in self.phases:
+            self.acc[p] += self.ev[p][0].elapsed_time(self.ev[p][1])
+
+
+def time_steps(step, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(record=True)
+        torch.cuda.synchronize()
+        step.collect()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def time_region(step, steps, warmup):
+    """Whole-step time with events bracketing exactly `steps` back-to-back steps."""
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps / 1000.0
+
+
+def cpu_baseline(inp, step, seconds: float, bs: int):
+    """The oracle's block-sparse attention fwd+bwd (torch fp32, all host
+    threads) on a bounded sample of q-blocks of head 0 with their real lists."""
+    import torch
+
+    from oracle import attention as OA
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    kv_num = step.last["kv_num"].cpu()
+    kv_idx = step.last["kv_idx"].cpu()
+    docs = inp["docs"]
+    H, T, D = inp["q"].shape[1:]
+    QB = T // bs
+    q, k, v = (inp[n][0].float() for n in ("q", "k", "v"))
+    dout = inp["dout"][0].float()
+    cc, cs, om = inp["coeff_cos"][0].float(), inp["coeff_sin"][0].float(), inp["omegas"].float()
+    done_tiles, t_used, n_rows = 0, 0.0, 0
+    i = 0
+    while t_used < seconds and i < H * QB:
+        h, qb = (i * 7) % H, (QB - 1 - (i * 37) % QB)  # spread the sample over heads and the sequence
+        i += 1
+        qq = q[h:h + 1].clone().requires_grad_()
+        kk = k[h:h + 1].clone().requires_grad_()
+        vv = v[h:h + 1].clone().requires_grad_()
+        t0 = time.perf_counter()
+        res = OA.attention_blocksparse(qq, kk, vv, kv_num[h:h + 1], kv_idx[h:h + 1], docs, bs=bs, scale=0.12,
+                                       beta=0.5, bias_mode="block", coeff_cos=cc[h:h + 1], coeff_sin=cs[h:h + 1],
+                                       omegas=om, heads=[0], qblocks=[qb])
+        o, _ = res[(0, qb)]
+        o.backward(dout[h, qb * bs:(qb + 1) * bs])
+        t_used += time.perf_counter() - t0
+        done_tiles += int(kv_num[h, qb])
+        n_rows += 1
+    flops = 14.0 * bs * bs * D * done_tiles
+    return dict(value=flops / t_used / 1e12, unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"oracle block-sparse attention fwd+bwd (torch fp32 on CPU) for {n_rows} (head, q-block) "
+                       f"rows of the same mask ({done_tiles} active {bs}x{bs} tiles, {t_used:.1f} s)",
+                seconds=round(t_used, 2), cpu_count=os.cpu_count())
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: the SCOPE hot path is sharded by head across GPUs "
+                                   "(no exchange inside the layer), multi-GPU runs are out of scope",
+                          "n_gpus": args.gpus}))
+        sys.exit(1)
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    H, T, D, bs = args.H, args.T, 128, args.bs
+    inp = make_inputs(H, T, D, bs)
+    step = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=args.budget)
+    step()
+    torch.cuda.synchronize()
+    n_act = int(step.last["kv_num"].sum())
+    F_fwd = 4.0 * bs * bs * D * n_act
+    F_bwd = 10.0 * bs * bs * D * n_act
+
+    t_step = time_region(step, args.steps, args.warmup)
+    time_steps(step, args.steps, 0)  # per-phase breakdown (events around each phase)
+    ph = {p: step.acc[p] / args.steps for p in step.phases}
+
+    # Algorithmic FLOPs per kernel: the forward does 2 GEMMs (4·bs²·D per tile);
+    # of the backward's 5 GEMMs (10·bs²·D) the q-major pass owns S, dP, dQ
+    # (6·bs²·D) and the kv-major pass dK, dV (4·bs²·D); its S/dP recompute is
+    # not counted.
+    per_kernel = {"attn_fwd": (F_fwd, "attn_fwd_kernel"),
+                  "attn_bwd_dq": (6.0 * bs * bs * D * n_act, "attn_bwd_dq_kernel"),
+                  "attn_bwd_dkv": (4.0 * bs * bs * D * n_act, "attn_bwd_dkv_kernel")}
+    dom = max(per_kernel, key=lambda p: ph[p])
+    flops, kname = per_kernel[dom]
+    achieved = flops / (ph[dom] / 1e3) / 1e12
+    roofline = dict(bound="mfma", kernel=kname, achieved=round(achieved, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                    frac=round(achieved / PEAK_BF16_TFLOPS, 4), traffic=None,
+                    flops_per_launch=flops, launch_ms=round(ph[dom], 4))
+    qb_n, kb_n = inp["needle"]
+    picks = step.last["picks"]
+    needle_sel = bool((picks[:, qb_n] == kb_n).any().item())
+    res = {
+        "metric": METRIC,
+        "value": round((F_fwd + F_bwd) / t_step / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "long-context prefill, one SCOPE layer fwd+bwd (pointer select + stats + "
+                               "block-sparse attention)", "B": 1, "H": H, "T": T, "D": D, "block": bs,
+                   "window": args.window, "global": args.n_global, "budget": args.budget, "bands": 8,
+                   "bias": "block offsets", "docs": max(1, T // 8192)},
+        "tokens_per_s": round(T / t_step, 1),
+        "n_act": n_act,
+        "flops_fwd": F_fwd,
+        "flops_bwd": F_bwd,
+        "attn_fwd_tflops": round(F_fwd / (ph["attn_fwd"] / 1e3) / 1e12, 2),
+        "attn_bwd_tflops": round(F_bwd / ((ph["attn_bwd_dq"] + ph["attn_bwd_dkv"]) / 1e3) / 1e12, 2),
+        "breakdown_ms": {p: round(v_, 4) for p, v_ in ph.items()},
+        "needle_selected": needle_sel,
+        "roofline": roofline,
+    }
+    if args.sweep:
+        sweep = {}
+        for b in (2, 4):
+            st = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=b)
+            st()
+            torch.cuda.synchronize()
+            na = int(st.last["kv_num"].sum())
+            ts = time_region(st, args.steps, args.warmup)
+            sweep[str(b)] = dict(value=round(14.0 * bs * bs * D * na / ts / 1e12, 2), ms_per_step=round(ts * 1e3, 3),
+                                 n_act=na)
+        res["budget_sweep"] = sweep
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(inp, step, args.cpu_seconds, bs)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

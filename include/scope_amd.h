@@ -244,6 +244,22 @@ int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t
                    float* dcoeff_cos, float* dcoeff_sin, float* db0, float* dslope,
                    float* ddelta_main, float* dwidth, void* workspace, void* stream);
 
+/* The backward in two stream-ordered phases sharing one workspace:
+ * SCOPE_BWD_DQ  (q-major: Δ = rowsum(dO∘O), dQ and the coefficient gradients)
+ * then SCOPE_BWD_DKV (kv-major: dK, dV).  scope_attn_bwd runs both; the split
+ * lets a caller time or overlap the phases.  No reference counterpart beyond
+ * the FlexAttention backward that scope_attn_bwd replaces. */
+enum { SCOPE_BWD_DQ = 1, SCOPE_BWD_DKV = 2 };
+int scope_attn_bwd_phase(const scope_attn_params* p, int phases, const uint16_t* q, const uint16_t* k,
+                         const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,
+                         const int32_t* kv_num, const int32_t* kv_idx, const int32_t* q_off,
+                         const int32_t* q_list, const int32_t* docs, const int32_t* ds_tok_end,
+                         const void* table, const float* coeff_cos, const float* coeff_sin,
+                         const float* b0, const float* slope, const float* delta_main,
+                         const float* width, uint16_t* dq, uint16_t* dk, uint16_t* dv,
+                         float* dcoeff_cos, float* dcoeff_sin, float* db0, float* dslope,
+                         float* ddelta_main, float* dwidth, void* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

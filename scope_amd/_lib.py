@@ -65,6 +65,7 @@ _PROTOS = {
     "scope_attn_fwd": (c_int, [C.POINTER(AttnParams)] + [P] * 17),
     "scope_attn_bwd_workspace_bytes": (c_int64, [C.POINTER(AttnParams)]),
     "scope_attn_bwd": (c_int, [C.POINTER(AttnParams)] + [P] * 30),
+    "scope_attn_bwd_phase": (c_int, [C.POINTER(AttnParams), c_int] + [P] * 30),
 }
 
 _lib = None

@@ -780,25 +780,28 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
 }
 
 template <int BS>
-static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int grid_q, int max_items, hipStream_t s) {
+static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases, int grid_q, int max_items,
+                       hipStream_t s) {
   dim3 gq(grid_q * (BS / 128)), gk(max_items, a.H, BS / 128), gr(a.QB, a.H);
-  if (mode == SCOPE_BIAS_BLOCK) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 1>), gq, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
-                       const_cast<int32_t*>(pl.slots_start));
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
-  } else if (mode == SCOPE_BIAS_TOKEN) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 2>), gq, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
-                       const_cast<int32_t*>(pl.slots_start));
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2>), gk, dim3(256), 0, s, a, pl);
-  } else {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 0>), gq, dim3(256), 0, s, a);
-    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
-                       const_cast<int32_t*>(pl.slots_start));
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 0>), gk, dim3(256), 0, s, a, pl);
+  if (phases & SCOPE_BWD_DQ) {
+    if (mode == SCOPE_BIAS_BLOCK)
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 1>), gq, dim3(256), 0, s, a);
+    else if (mode == SCOPE_BIAS_TOKEN)
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 2>), gq, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 0>), gq, dim3(256), 0, s, a);
   }
-  hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
+  if (phases & SCOPE_BWD_DKV) {
+    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
+                       const_cast<int32_t*>(pl.slots_start));
+    if (mode == SCOPE_BIAS_BLOCK)
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
+    else if (mode == SCOPE_BIAS_TOKEN)
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2>), gk, dim3(256), 0, s, a, pl);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 0>), gk, dim3(256), 0, s, a, pl);
+    hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
+  }
 }
 
 }  // namespace scope
@@ -810,14 +813,15 @@ extern "C" int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p) {
   return bwd_layout(p).total;
 }
 
-extern "C" int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                              const uint16_t* out, const uint16_t* dout, const float* lse, const int32_t* kv_num,
-                              const int32_t* kv_idx, const int32_t* q_off, const int32_t* q_list, const int32_t* docs,
-                              const int32_t* ds_tok_end, const void* table, const float* coeff_cos,
-                              const float* coeff_sin, const float* b0, const float* slope, const float* delta_main,
-                              const float* width, uint16_t* dq, uint16_t* dk, uint16_t* dv, float* dcoeff_cos,
-                              float* dcoeff_sin, float* db0, float* dslope, float* ddelta_main, float* dwidth,
-                              void* workspace, void* stream) {
+extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, const uint16_t* q, const uint16_t* k,
+                                    const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,
+                                    const int32_t* kv_num, const int32_t* kv_idx, const int32_t* q_off,
+                                    const int32_t* q_list, const int32_t* docs, const int32_t* ds_tok_end,
+                                    const void* table, const float* coeff_cos, const float* coeff_sin, const float* b0,
+                                    const float* slope, const float* delta_main, const float* width, uint16_t* dq,
+                                    uint16_t* dk, uint16_t* dv, float* dcoeff_cos, float* dcoeff_sin, float* db0,
+                                    float* dslope, float* ddelta_main, float* dwidth, void* workspace, void* stream) {
+  SCOPE_REQUIRE(phases >= 1 && phases <= 3, "scope_attn_bwd_phase: phases must be 1, 2 or 3 (got %d)", phases);
   int rc = validate_attn(p, q, k, v, kv_num, kv_idx, docs, ds_tok_end, table, coeff_cos, coeff_sin, b0, slope,
                          delta_main, width, "scope_attn_bwd");
   if (rc) return rc;
@@ -866,8 +870,21 @@ extern "C" int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, con
   hipStream_t s = as_stream(stream);
   const int grid_q = p->H * a.QB;
   if (p->bs == 256)
-    launch_bwd<256>(a, pl, p->bias_mode, grid_q, L.max_items, s);
+    launch_bwd<256>(a, pl, p->bias_mode, phases, grid_q, L.max_items, s);
   else
-    launch_bwd<128>(a, pl, p->bias_mode, grid_q, L.max_items, s);
+    launch_bwd<128>(a, pl, p->bias_mode, phases, grid_q, L.max_items, s);
   return check_launch("attention backward kernels");
+}
+
+extern "C" int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              const uint16_t* out, const uint16_t* dout, const float* lse, const int32_t* kv_num,
+                              const int32_t* kv_idx, const int32_t* q_off, const int32_t* q_list, const int32_t* docs,
+                              const int32_t* ds_tok_end, const void* table, const float* coeff_cos,
+                              const float* coeff_sin, const float* b0, const float* slope, const float* delta_main,
+                              const float* width, uint16_t* dq, uint16_t* dk, uint16_t* dv, float* dcoeff_cos,
+                              float* dcoeff_sin, float* db0, float* dslope, float* ddelta_main, float* dwidth,
+                              void* workspace, void* stream) {
+  return scope_attn_bwd_phase(p, SCOPE_BWD_DQ | SCOPE_BWD_DKV, q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list,
+                              docs, ds_tok_end, table, coeff_cos, coeff_sin, b0, slope, delta_main, width, dq, dk, dv,
+                              dcoeff_cos, dcoeff_sin, db0, dslope, ddelta_main, dwidth, workspace, stream);
 }

@@ -296,8 +296,11 @@ def attn_fwd(q, k, v, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float
 def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
-             ramp_lambda=0.0, tau=64.0, need_coeff_grads: bool = True):
-    """Block-sparse attention backward -> dict of gradients."""
+             ramp_lambda=0.0, tau=64.0, need_coeff_grads: bool = True, phase_hook=None):
+    """Block-sparse attention backward -> dict of gradients.  With
+    ``phase_hook`` the two phases (q-major dQ pass, kv-major dK/dV pass) are
+    launched separately and the hook is called before, between and after
+    them with the phase name ("dq", "dkv", "end") (used for per-kernel timing)."""
     dev = _gpu("attn_bwd", q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list)
     kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
     m = BIAS_MODES[bias_mode]
@@ -322,11 +325,18 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
     ddm = torch.empty((1, H, T), **z) if gate else None
     dwd = torch.empty((1, H, T), **z) if gate else None
     ws = torch.empty(max(16, query("scope_attn_bwd_workspace_bytes", C.byref(prm))), dtype=torch.uint8, device=dev)
-    call("scope_attn_bwd", C.byref(prm), _p(q), _p(k), _p(v), _p(out), _p(dout), _p(_f32(lse)), _p(_i32(kv_num)),
-         _p(kv_idx3), _p(_i32(q_off)), _p(_i32(q_list)), _p(_i32(docs.reshape(-1))), _p(_i32(ds_tok_end)),
-         _p(table), _p(_f32(coeff_cos)), _p(_f32(coeff_sin)), _p(_f32(b0)), _p(_f32(slope)), _p(_f32(delta_main)),
-         _p(_f32(width)), _p(dq), _p(dk), _p(dv), _p(dcc), _p(dcs), _p(db0), _p(dsl), _p(ddm), _p(dwd), _p(ws),
-         _stream(dev))
+    args = (_p(q), _p(k), _p(v), _p(out), _p(dout), _p(_f32(lse)), _p(_i32(kv_num)), _p(kv_idx3), _p(_i32(q_off)),
+            _p(_i32(q_list)), _p(_i32(docs.reshape(-1))), _p(_i32(ds_tok_end)), _p(table), _p(_f32(coeff_cos)),
+            _p(_f32(coeff_sin)), _p(_f32(b0)), _p(_f32(slope)), _p(_f32(delta_main)), _p(_f32(width)), _p(dq),
+            _p(dk), _p(dv), _p(dcc), _p(dcs), _p(db0), _p(dsl), _p(ddm), _p(dwd), _p(ws), _stream(dev))
+    if phase_hook is None:
+        call("scope_attn_bwd", C.byref(prm), *args)
+    else:
+        phase_hook("dq")
+        call("scope_attn_bwd_phase", C.byref(prm), 1, *args)
+        phase_hook("dkv")
+        call("scope_attn_bwd_phase", C.byref(prm), 2, *args)
+        phase_hook("end")
     return dict(dq=dq, dk=dk, dv=dv, dcoeff_cos=dcc, dcoeff_sin=dcs, db0=db0, dslope=dsl, ddelta_main=ddm,
                 dwidth=dwd)
 
