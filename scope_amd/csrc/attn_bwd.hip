@@ -97,6 +97,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   }
   if (MODE == 2) {
     token_qfeat(a, hT, row, g, qf, qfl, cos_i, sin_i);
+    // kept for pass B, which stages them per query tile
+    *reinterpret_cast<uint4*>(a.qfeat + (hT + row) * kTokRow + g * 8) = qf;
+    *reinterpret_cast<uint4*>(a.qfeat + (hT + row) * kTokRow + 16 + g * 8) = qfl;
     if (a.subtract_b0) rowc = -a.beta_log2 * a.b0[hT + row];
     if (a.use_slope) slp = a.beta_log2 * a.slope[hT + row];
     if (a.gate_kind != SCOPE_GATE_NONE) {
@@ -449,26 +452,221 @@ struct KvPlan {
   int64_t max_slots;  // per head
 };
 
+// LDS staging of one 64-row query tile of pass B.  Everything arrives by
+// global_load_lds (no registers): two such buffers alternate, so the loads of
+// tile j+1 run under the MFMAs of tile j.
+template <int MODE>
+struct alignas(16) DkvBuf {
+  uint16_t q[64 * 128];            // Q rows, swizzled (swz_off)
+  uint16_t d[64 * 128];            // dO rows, swizzled
+  float ra[256];                   // lse | Δ | doc id (int32) | b0, 64 rows each
+  float rb[MODE == 0 ? 4 : 1024];  // block: cos [64][K] at 0, sin [64][K] at 512;
+                                   // token: query features [64][32] bf16 (chunk-swizzled)
+  float rc[MODE >= 2 ? 256 : 4];   // token: slope | delta_main | width
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16-byte global -> LDS copy; the LDS address is dst_wave + 16·lane, where
+// dst_wave must be the same for the whole wavefront.
+__device__ __forceinline__ void g2lds16(const void* src, void* dst_wave) {
+  __builtin_amdgcn_global_load_lds(const_cast<void*>(src), (lds_void_t*)dst_wave, 16, 0, 0);
+}
+
+// vmcnt(0): every global load of this wavefront (including global_load_lds) has landed
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Issue the copies of the 64-row query tile starting at token q0 into b.
+template <int MODE>
+__device__ __forceinline__ void dkv_issue(const AttnArgs& a, int h, int64_t hT, int64_t q0, DkvBuf<MODE>& b, int tid) {
+  const int wave = tid >> 6, lane = tid & 63;
+  {
+    // chunk jj·256 + tid: row jj·16 + tid/16, physical chunk tid%16 (holds logical chunk p ^ swz(row))
+    const int r = tid >> 4, c = (tid & 15) ^ swz(r);
+    const uint16_t* qp = a.q + h * a.q_sh + (q0 + r) * a.q_st + c * 8;
+    const uint16_t* dp = a.dout + h * a.o_sh + (q0 + r) * a.o_st + c * 8;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      g2lds16(qp + jj * 16 * a.q_st, b.q + (jj * 256 + wave * 64) * 8);
+      g2lds16(dp + jj * 16 * a.o_st, b.d + (jj * 256 + wave * 64) * 8);
+    }
+  }
+  const int arr = lane >> 4, ch = (lane & 15) * 4;
+  if (wave == 0) {
+    const void* src = arr == 0   ? static_cast<const void*>(a.lse + hT + q0 + ch)
+                      : arr == 1 ? static_cast<const void*>(a.delta + hT + q0 + ch)
+                      : arr == 2 ? static_cast<const void*>(a.docs + q0 + ch)
+                                 : static_cast<const void*>(a.b0 + hT + q0 + ch);
+    if (arr < 3 || (MODE >= 2 && a.subtract_b0)) g2lds16(src, b.ra);
+  }
+  if (MODE == 1) {
+    const int ci = (wave & 1) * 64 + lane;  // 16-byte chunk of the [64][K] coefficient rows
+    const float* src = (wave < 2 ? a.coeff_cos : a.coeff_sin) + (hT + q0) * a.K + ci * 4;
+    if (ci < 16 * a.K) g2lds16(src, b.rb + (wave >> 1) * 512 + (wave & 1) * 256);
+  }
+  if (MODE >= 2) {
+    const int r = tid >> 2, c = (tid & 3) ^ ((r >> 2) & 3);
+    g2lds16(a.qfeat + (hT + q0 + r) * kTokRow + c * 8, reinterpret_cast<uint16_t*>(b.rb) + wave * 64 * 8);
+    if (wave == 1) {
+      const float* src = arr == 0 ? a.slope : arr == 1 ? a.delta_main : a.width;
+      if ((arr == 0 && a.use_slope) || ((arr == 1 || arr == 2) && MODE == 3)) g2lds16(src + hT + q0 + ch, b.rc);
+    }
+  }
+}
+
+// P and dS of one tile as bf16 B operands (k index: the 64 query rows):
+// register quad (mq, rq) of the S / dP accumulators is k-step 2·mq + rq/2,
+// slots 4·(rq%2) .. +3.  MASK applies the causal and document masks.
+template <int MODE, bool MASK>
+__device__ __forceinline__ void dkv_probs(const AttnArgs& a, const DkvBuf<MODE>& b, const float* offw, int q0,
+                                          int lane, int wkv, int doc_kv, const f32x16_t (&s)[2],
+                                          const f32x16_t (&dp)[2], uint4 (&pb)[4], uint4 (&dsb)[4]) {
+  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
+  const int g = lane >> 5;
+  const int* docq = reinterpret_cast<const int*>(b.ra + 128);
+  const float cs = a.scale_log2;
+  const float glam = a.beta_log2 * a.ramp_lambda;
+  const float slsc = TOK && a.use_slope ? a.beta_log2 : 0.f;
+  const float spw = a.gate_kind == SCOPE_GATE_SOFTPLUS ? kLn2 : 0.f;
+#pragma unroll
+  for (int mq = 0; mq < 2; ++mq)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int qi0 = mq * 32 + 8 * rq + 4 * g;  // 4 consecutive query rows of this register quad
+      const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
+      const float4 dl4 = *reinterpret_cast<const float4*>(&b.ra[64 + qi0]);
+      const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
+      const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+      int dcv[4] = {0, 0, 0, 0};
+      if (MASK) {
+        const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
+        dcv[0] = dc4.x;
+        dcv[1] = dc4.y;
+        dcv[2] = dc4.z;
+        dcv[3] = dc4.w;
+      }
+      float pv[4], dsv[4];
+#pragma unroll
+      for (int i2 = 0; i2 < 4; ++i2) {
+        const int r = 4 * rq + i2;
+        const int q = q0 + qi0 + i2;
+        float xv;
+        if (TOK) {
+          // slope and gate terms; softplus(x) = max(x,0) + ln2·log2(1 + 2^(-|x|·log2 e))
+          const float df = static_cast<float>(q - wkv);
+          float e = slsc * b.rc[qi0 + i2] * df;
+          if (GATE) {
+            const float xx = (fabsf(df - b.rc[64 + qi0 + i2]) - b.rc[128 + qi0 + i2]) * a.inv_tau;
+            const float sp = __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e));
+            e -= glam * fmaf(spw, sp, fmaxf(xx, 0.f));
+          }
+          xv = fmaf(s[mq][r], cs, e + ofv[i2]);
+        } else {
+          xv = fmaf(s[mq][r], cs, ofv[i2]);
+        }
+        if (MASK) xv = (wkv <= q) & (dcv[i2] == doc_kv) ? xv : -INFINITY;
+        const float p = __builtin_amdgcn_exp2f(xv);
+        pv[i2] = p;
+        dsv[i2] = p * (dp[mq][r] - dlv[i2]);
+      }
+      const int ksx = 2 * mq + rq / 2;
+      const uint32_t p01 = cvt_pk_bf16(pv[0], pv[1]), p23 = cvt_pk_bf16(pv[2], pv[3]);
+      const uint32_t d01 = cvt_pk_bf16(dsv[0], dsv[1]), d23 = cvt_pk_bf16(dsv[2], dsv[3]);
+      if (rq % 2 == 0) {
+        pb[ksx].x = p01;
+        pb[ksx].y = p23;
+        dsb[ksx].x = d01;
+        dsb[ksx].y = d23;
+      } else {
+        pb[ksx].z = p01;
+        pb[ksx].w = p23;
+        dsb[ksx].z = d01;
+        dsb[ksx].w = d23;
+      }
+    }
+}
+
+// One 64-row query tile against this wavefront's 32 keys: S, dP, then
+// dV^T += dO^T·P and dK^T += Q^T·dS.
+template <int BS, int MODE>
+__device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& b, float* offw, const float* tab,
+                                         int64_t q0, int ds_end, int lane, int64_t wkv_lo, int doc_kv,
+                                         const uint4 (&kreg)[8], const uint4 (&vreg)[8], const uint4& kf,
+                                         const uint4& kfl, f32x16_t (&dvT)[4], f32x16_t (&dkT)[4]) {
+  const int g = lane >> 5, lr = lane & 31;
+  const int64_t wkv = wkv_lo + lr;
+  // per-row exponent offsets of this tile (lane = row), private to the wavefront
+  {
+    const float l = b.ra[lane];
+    float c = 0.f;
+    if (MODE == 1) {
+      if (a.K == 8) {
+        const float4* cr = reinterpret_cast<const float4*>(b.rb + lane * 8);
+        const float4* sr = reinterpret_cast<const float4*>(b.rb + 512 + lane * 8);
+        const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+        c = c0.x * tab[0] + c0.y * tab[1] + c0.z * tab[2] + c0.w * tab[3] + c1.x * tab[4] + c1.y * tab[5] +
+            c1.z * tab[6] + c1.w * tab[7] + s0.x * tab[8] + s0.y * tab[9] + s0.z * tab[10] + s0.w * tab[11] +
+            s1.x * tab[12] + s1.y * tab[13] + s1.z * tab[14] + s1.w * tab[15];
+      } else {
+        for (int k = 0; k < a.K; ++k) c += b.rb[lane * a.K + k] * tab[k] + b.rb[512 + lane * a.K + k] * tab[8 + k];
+      }
+      c *= a.beta_log2;
+    }
+    if (MODE >= 2 && a.subtract_b0) c = -a.beta_log2 * b.ra[192 + lane];
+    offw[lane] = l == -INFINITY ? -INFINITY : c - l * kLog2e;
+  }
+  const bool full = (wkv_lo + 31 <= q0) && (ds_end <= wkv_lo);
+  // S and dP, query rows in two 32-row blocks (A operand), keys as columns (B)
+  f32x16_t s[2], dp[2];
+#pragma unroll
+  for (int mq = 0; mq < 2; ++mq) {
+    s[mq] = zero16();
+    dp[mq] = zero16();
+  }
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+    for (int mq = 0; mq < 2; ++mq) {
+      s[mq] = mfma32(lds_row8(b.q, mq * 32 + lr, ks * 16 + g * 8), kreg[ks], s[mq]);
+      dp[mq] = mfma32(lds_row8(b.d, mq * 32 + lr, ks * 16 + g * 8), vreg[ks], dp[mq]);
+    }
+  if (MODE >= 2) {
+    const uint16_t* qf = reinterpret_cast<const uint16_t*>(b.rb);
+#pragma unroll
+    for (int mq = 0; mq < 2; ++mq) {
+      const int r = mq * 32 + lr, sw = (r >> 2) & 3;
+      const uint4 qh = *reinterpret_cast<const uint4*>(qf + r * kTokRow + ((g ^ sw) << 3));
+      const uint4 qlo = *reinterpret_cast<const uint4*>(qf + r * kTokRow + (((2 + g) ^ sw) << 3));
+      s[mq] = mfma32(qh, kf, s[mq]);
+      s[mq] = mfma32(qlo, kf, s[mq]);
+      s[mq] = mfma32(qh, kfl, s[mq]);
+    }
+  }
+  uint4 pb[4], dsb[4];
+  if (MODE >= 2 || !full)  // token modes always take the masked form (one copy of their longer code)
+    dkv_probs<MODE, true>(a, b, offw, static_cast<int>(q0), lane, static_cast<int>(wkv), doc_kv, s, dp, pb, dsb);
+  else
+    dkv_probs<MODE, false>(a, b, offw, static_cast<int>(q0), lane, static_cast<int>(wkv), doc_kv, s, dp, pb, dsb);
+  // dV^T += dO^T P,  dK^T += Q^T dS  (k index: the 64 query rows)
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+      dvT[md] = mfma32(lds_kmajor(b.d, 16 * s4, md * 32, lane), pb[s4], dvT[md]);
+      dkT[md] = mfma32(lds_kmajor(b.q, 16 * s4, md * 32, lane), dsb[s4], dkT[md]);
+    }
+}
+
 template <int BS, int MODE>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl) {
-  constexpr int NT = 256;  // 4 waves = 128 key rows per workgroup (blockIdx.z selects the part)
   constexpr int D = 128;
-  constexpr int BM = 32;         // q rows per staged sub-tile
-  constexpr int KSTR = D + 8;    // row-major Q / dO
-  constexpr int TSTR = BM + 4;   // transposed Q / dO rows (18 dwords: conflict-free b64 reads)
-  constexpr int FSTR = 40;
+  constexpr int BM = 64;  // query rows per staged tile
+  constexpr int NS = BS / BM;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[BM * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Ds[BM * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Qt[D * TSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Dt[D * TSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Qf[MODE == 2 ? BM * FSTR : 8];
-  __shared__ __attribute__((aligned(16))) float offq[BM];
-  __shared__ __attribute__((aligned(16))) float dltq[BM];
-  __shared__ __attribute__((aligned(16))) int docq[BM];
-  __shared__ __attribute__((aligned(16))) float slq[BM];
-  __shared__ __attribute__((aligned(16))) float dmq[BM];
-  __shared__ __attribute__((aligned(16))) float wdq[BM];
+  __shared__ DkvBuf<MODE> buf0, buf1;
+  __shared__ __attribute__((aligned(16))) float offw[4][BM];
+  __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunk * 16 : 4];
+  __shared__ int qbs[kChunk], dse[kChunk];
 
   const int NB = a.QB;
   const int h = blockIdx.y;
@@ -488,6 +686,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   const int nq = qo[kb + 1] - qo[kb];
   const int nch = max(1, (nq + kChunk - 1) / kChunk);
   const int i0 = chunk * kChunk, i1 = min(nq, i0 + kChunk);
+  const int ne = max(0, i1 - i0);
   const int32_t* ql = a.q_list + static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb];
 
   const int tid = threadIdx.x;
@@ -497,7 +696,27 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   const int64_t wkv = wkv_lo + lr;
   const int krow = blockIdx.z * 128 + wave * 32 + lr;  // key row within the block
   const int64_t hT = static_cast<int64_t>(h) * a.T;
-  const float cs = a.scale_log2;
+
+  // The q-list is ascending, so only its first entry can be the diagonal
+  // block; there the query sub-tiles that end before kv0 are skipped.
+  const int qb_first = ne > 0 ? ql[i0] : 0;
+  const int skip0 = ne > 0 && qb_first == kb ? (blockIdx.z * 128) / BM : 0;
+  const int n_it = ne * NS - skip0;
+
+  if (tid < ne) {
+    const int qb = ql[i0 + tid];
+    qbs[tid] = qb;
+    dse[tid] = a.ds_tok_end[qb];
+  }
+  if (MODE == 1 && tid < ne * 16) {
+    // block-mode table row of distance qb - kb (clamped: a later key block is fully masked anyway)
+    const int r = min(max(ql[i0 + tid / 16] - kb, 0), NB - 1);
+    tabs[tid] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + tid % 16];
+  }
+  if (n_it > 0) {
+    const int64_t q0 = static_cast<int64_t>(qb_first) * BS + (skip0 % NS) * BM;
+    dkv_issue<MODE>(a, h, hT, q0, buf0, tid);
+  }
 
   uint4 kreg[8], vreg[8];
   {
@@ -510,14 +729,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
     }
   }
   uint4 kf = make_uint4(0, 0, 0, 0), kfl = make_uint4(0, 0, 0, 0);
-  if (MODE == 2) {
+  if (MODE >= 2) {
     kf = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + wkv * kTokRow + g * 8);
     kfl = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + wkv * kTokRow + 16 + g * 8);
   }
   const int doc_kv = a.docs[wkv];
-  const bool gate = MODE == 2 && a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
-  const bool extra = MODE == 2 && (a.use_slope || gate);
-  const float glam = a.beta_log2 * a.ramp_lambda;
 
   f32x16_t dvT[4], dkT[4];
 #pragma unroll
@@ -526,164 +742,33 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
     dkT[i] = zero16();
   }
 
-  for (int i = i0; i < i1; ++i) {
-    const int qb = ql[i];
-    const int ds_end = a.ds_tok_end[qb];
-    for (int sub = 0; sub < BS / BM; ++sub) {
-      const int64_t q0 = static_cast<int64_t>(qb) * BS + sub * BM;
-      if (q0 + BM - 1 < kv0) continue;  // every query row before every key of the block
-      __syncthreads();
-      // ---- stage Q, dO rows (+ transposes), per-query constants
-      for (int idx = tid; idx < BM * 16; idx += NT) {
-        const int r = idx / 16, c = idx % 16;
-        *reinterpret_cast<uint4*>(&Qs[r * KSTR + c * 8]) =
-            *reinterpret_cast<const uint4*>(a.q + h * a.q_sh + (q0 + r) * a.q_st + c * 8);
-        *reinterpret_cast<uint4*>(&Ds[r * KSTR + c * 8]) =
-            *reinterpret_cast<const uint4*>(a.dout + h * a.o_sh + (q0 + r) * a.o_st + c * 8);
-      }
-      if (tid < BM) {
-        const int64_t q = q0 + tid;
-        const float l = a.lse[hT + q];
-        float c = 0.f;
-        if (MODE == 1) {
-          const float* tr = static_cast<const float*>(a.table) + static_cast<int64_t>(qb - kb) * 16;
-          for (int k = 0; k < a.K; ++k)
-            c += a.coeff_cos[(hT + q) * a.K + k] * tr[k] + a.coeff_sin[(hT + q) * a.K + k] * tr[8 + k];
-          c *= a.beta_log2;
+  // iteration j covers flat index f = j + skip0: list entry f / NS, sub-tile f % NS
+  auto tile_q0 = [&](int j, int& e) {
+    const int f = j + skip0;
+    e = f / NS;
+    return static_cast<int64_t>(qbs[e]) * BS + (f % NS) * BM;
+  };
+  for (int j = 0; j < n_it; j += 2) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int jj = j + half;
+      if (jj < n_it) {
+        wait_vm0();
+        __syncthreads();  // tile jj is in LDS; every wavefront is done with tile jj-1
+        int e, en;
+        if (jj + 1 < n_it) {
+          const int64_t qn = tile_q0(jj + 1, en);
+          if (half == 0) dkv_issue<MODE>(a, h, hT, qn, buf1, tid);
+          else dkv_issue<MODE>(a, h, hT, qn, buf0, tid);
         }
-        if (MODE == 2 && a.subtract_b0) c = -a.beta_log2 * a.b0[hT + q];
-        offq[tid] = l == -INFINITY ? -INFINITY : c - l * kLog2e;
-        dltq[tid] = a.delta[hT + q];
-        docq[tid] = a.docs[q];
-        if (MODE == 2) {
-          slq[tid] = a.use_slope ? a.beta_log2 * a.slope[hT + q] : 0.f;
-          dmq[tid] = gate ? a.delta_main[hT + q] : 0.f;
-          wdq[tid] = gate ? a.width[hT + q] : 0.f;
-        }
-      }
-      if (MODE == 2 && tid >= 64 && tid < 64 + 2 * BM) {
-        const int r = (tid - 64) / 2, gg = (tid - 64) % 2;
-        const int64_t q = q0 + r;
-        uint4 fh, fl;
-        token_qfeat(a, hT, q, gg, fh, fl, nullptr, nullptr);
-        *reinterpret_cast<uint4*>(&Qf[r * FSTR + gg * 8]) = fh;
-        *reinterpret_cast<uint4*>(&Qf[r * FSTR + 16 + gg * 8]) = fl;
-      }
-      __syncthreads();
-      // transposes Q -> Qt, dO -> Dt (4 rows x 8 dims per thread)
-      for (int idx = tid; idx < 2 * (BM / 4) * 16; idx += NT) {
-        const int which = idx / ((BM / 4) * 16);
-        const int rem = idx % ((BM / 4) * 16);
-        const int c = rem % 16, rg = rem / 16;
-        const uint16_t* src = which ? Ds : Qs;
-        uint16_t* dst = which ? Dt : Qt;
-        uint32_t w[4][4];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const uint4 u = *reinterpret_cast<const uint4*>(&src[(rg * 4 + rr) * KSTR + c * 8]);
-          w[rr][0] = u.x;
-          w[rr][1] = u.y;
-          w[rr][2] = u.z;
-          w[rr][3] = u.w;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          uint2 val;
-          if (e & 1) {
-            val.x = pack_hi16(w[0][e / 2], w[1][e / 2]);
-            val.y = pack_hi16(w[2][e / 2], w[3][e / 2]);
-          } else {
-            val.x = pack_lo16(w[0][e / 2], w[1][e / 2]);
-            val.y = pack_lo16(w[2][e / 2], w[3][e / 2]);
-          }
-          *reinterpret_cast<uint2*>(&dst[(c * 8 + e) * TSTR + rg * 4]) = val;
-        }
-      }
-      __syncthreads();
-
-      if (q0 + BM - 1 < wkv_lo) continue;  // this wave's keys all after the rows
-      const bool full = (wkv_lo + 31 <= q0) && (ds_end <= wkv_lo);
-      // S = Q K^T, dP = dO V^T   (rows: queries, columns: this wave's keys)
-      f32x16_t s = zero16(), dp = zero16();
-      const uint16_t* qr = &Qs[lr * KSTR + g * 8];
-      const uint16_t* dr = &Ds[lr * KSTR + g * 8];
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        s = mfma32(*reinterpret_cast<const uint4*>(qr + ks * 16), kreg[ks], s);
-        dp = mfma32(*reinterpret_cast<const uint4*>(dr + ks * 16), vreg[ks], dp);
-      }
-      if (MODE == 2) {
-        const uint4 qh = *reinterpret_cast<const uint4*>(&Qf[lr * FSTR + g * 8]);
-        const uint4 qlo = *reinterpret_cast<const uint4*>(&Qf[lr * FSTR + 16 + g * 8]);
-        s = mfma32(qh, kf, s);
-        s = mfma32(qlo, kf, s);
-        s = mfma32(qh, kfl, s);
-      }
-      uint4 pb[2], dsb[2];
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int qi0 = 8 * rq + 4 * g;  // 4 consecutive query rows of this register quad
-        const float4 of4 = *reinterpret_cast<const float4*>(&offq[qi0]);
-        const float4 dl4 = *reinterpret_cast<const float4*>(&dltq[qi0]);
-        const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
-        const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
-        const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
-        const int dcv[4] = {dc4.x, dc4.y, dc4.z, dc4.w};
-        float pv[4], dsv[4];
-#pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) {
-          const int r = 4 * rq + i2;
-          const int64_t q = q0 + qi0 + i2;
-          float x = s[r];
-          if (!full) {
-            const bool ok = (wkv <= q) & (dcv[i2] == doc_kv);
-            x = ok ? x : -INFINITY;
-          }
-          if (extra) {
-            const float df = static_cast<float>(q - wkv);
-            float e = slq[qi0 + i2] * df;
-            if (gate) {
-              const float xx = (fabsf(df - dmq[qi0 + i2]) - wdq[qi0 + i2]) * a.inv_tau;
-              const float gt = a.gate_kind == SCOPE_GATE_SOFTPLUS ? fmaxf(xx, 0.f) + log1pf(__expf(-fabsf(xx)))
-                                                                  : fmaxf(xx, 0.f);
-              e -= glam * gt;
-            }
-            x = fmaf(x, cs, e);
-          } else {
-            x = x * cs;
-          }
-          const float p = exp2f(x + ofv[i2]);
-          pv[i2] = p;
-          dsv[i2] = p * (dp[r] - dlv[i2]);
-        }
-        // register quad rq -> k-step rq/2, slots 4*(rq%2) .. +3
-        const uint32_t p01 = cvt_pk_bf16(pv[0], pv[1]), p23 = cvt_pk_bf16(pv[2], pv[3]);
-        const uint32_t d01 = cvt_pk_bf16(dsv[0], dsv[1]), d23 = cvt_pk_bf16(dsv[2], dsv[3]);
-        if (rq % 2 == 0) {
-          pb[rq / 2].x = p01;
-          pb[rq / 2].y = p23;
-          dsb[rq / 2].x = d01;
-          dsb[rq / 2].y = d23;
-        } else {
-          pb[rq / 2].z = p01;
-          pb[rq / 2].w = p23;
-          dsb[rq / 2].z = d01;
-          dsb[rq / 2].w = d23;
-        }
-      }
-      // dV^T += dO^T P,  dK^T += Q^T dS
-#pragma unroll
-      for (int md = 0; md < 4; ++md) {
-        const uint16_t* dt = &Dt[(md * 32 + lr) * TSTR + 4 * g];
-        const uint16_t* qt = &Qt[(md * 32 + lr) * TSTR + 4 * g];
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const uint2 dlo = *reinterpret_cast<const uint2*>(dt + 16 * s2);
-          const uint2 dhi = *reinterpret_cast<const uint2*>(dt + 16 * s2 + 8);
-          dvT[md] = mfma32(make_uint4(dlo.x, dlo.y, dhi.x, dhi.y), pb[s2], dvT[md]);
-          const uint2 qlo = *reinterpret_cast<const uint2*>(qt + 16 * s2);
-          const uint2 qhi = *reinterpret_cast<const uint2*>(qt + 16 * s2 + 8);
-          dkT[md] = mfma32(make_uint4(qlo.x, qlo.y, qhi.x, qhi.y), dsb[s2], dkT[md]);
+        const int64_t q0 = tile_q0(jj, e);
+        if (q0 + BM - 1 >= wkv_lo) {  // else every query row precedes this wavefront's keys
+          if (half == 0)
+            dkv_tile<BS, MODE>(a, buf0, offw[wave], tabs + (MODE == 1 ? e * 16 : 0), q0, dse[e], lane, wkv_lo,
+                               doc_kv, kreg, vreg, kf, kfl, dvT, dkT);
+          else
+            dkv_tile<BS, MODE>(a, buf1, offw[wave], tabs + (MODE == 1 ? e * 16 : 0), q0, dse[e], lane, wkv_lo,
+                               doc_kv, kreg, vreg, kf, kfl, dvT, dkT);
         }
       }
     }
@@ -752,7 +837,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl, 
 }
 
 struct BwdLayout {
-  int64_t delta, items, slots, part_dk, part_dv, total, max_slots;
+  int64_t delta, qfeat, items, slots, part_dk, part_dv, total, max_slots;
   int max_items;
 };
 
@@ -766,6 +851,8 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
   int64_t o = 0;
   L.delta = o;
   o += al(static_cast<int64_t>(p->H) * p->T * 4);
+  L.qfeat = o;
+  if (p->bias_mode == SCOPE_BIAS_TOKEN) o += al(static_cast<int64_t>(p->H) * p->T * 32 * 2);
   L.items = o;
   o += al(static_cast<int64_t>(p->H) * (NB + 1) * 4);
   L.slots = o;
@@ -794,8 +881,11 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
   if (phases & SCOPE_BWD_DKV) {
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start));
+    const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
     if (mode == SCOPE_BIAS_BLOCK)
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
+    else if (mode == SCOPE_BIAS_TOKEN && gate)
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3>), gk, dim3(256), 0, s, a, pl);
     else if (mode == SCOPE_BIAS_TOKEN)
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2>), gk, dim3(256), 0, s, a, pl);
     else
@@ -827,6 +917,10 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   if (rc) return rc;
   SCOPE_REQUIRE(out && dout && lse && q_off && q_list && dq && dk && dv && workspace,
                 "scope_attn_bwd: null pointer");
+  SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(dout) |
+                  reinterpret_cast<uintptr_t>(lse) | reinterpret_cast<uintptr_t>(workspace)) &
+                 15) == 0,
+                "scope_attn_bwd: out, dout, lse and workspace must start on a 16-byte boundary");
   SCOPE_REQUIRE(!dcoeff_cos == !dcoeff_sin, "scope_attn_bwd: dcoeff_cos and dcoeff_sin go together");
   AttnArgs a = make_args(p);
   a.q = q;
@@ -861,6 +955,7 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   const BwdLayout L = bwd_layout(p);
   char* ws = static_cast<char*>(workspace);
   a.delta = reinterpret_cast<float*>(ws + L.delta);
+  a.qfeat = reinterpret_cast<uint16_t*>(ws + L.qfeat);
   KvPlan pl;
   pl.items_start = reinterpret_cast<const int32_t*>(ws + L.items);
   pl.slots_start = reinterpret_cast<const int32_t*>(ws + L.slots);

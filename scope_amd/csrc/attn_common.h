@@ -49,6 +49,46 @@ __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// ---- swizzled row-major LDS tiles -------------------------------------------
+// A tile row holds 128 bf16 (256 bytes = all 64 banks).  The 16-byte chunk c
+// of row r is stored at chunk c ^ swz(r), swz(r) = 4·(r%4) + (r/4)%4.  With
+// this mapping both access patterns below are bank-conflict free:
+//   * row reads (16 lanes, 16 consecutive rows, same logical chunk), and
+//   * transpose reads (16 lanes, 4 rows × 4 eight-byte column groups).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+// element offset of (row r, column d) in a swizzled tile
+__device__ __forceinline__ int swz_off(int r, int d) { return r * 128 + (((d >> 3) ^ swz(r)) << 3) + (d & 7); }
+
+__device__ __forceinline__ uint4 lds_row8(const uint16_t* tile, int r, int d) {
+  return *reinterpret_cast<const uint4*>(tile + swz_off(r, d));
+}
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane j supplies an
+// 8-byte address A_j and lane i receives slot s = A_{4s + i/4}[i % 4].  With
+// lane 4s+t pointing at (row r0+s, column d0+4t), lane i gets the column
+// d0+i of rows r0..r0+3, i.e. an MFMA operand whose k index runs along rows.
+__device__ __forceinline__ uint2 lds_tr4(const uint16_t* tile, int r0, int d0, int lane16) {
+  const int s = lane16 >> 2, t = lane16 & 3;
+  const uint16_t* p = tile + swz_off(r0 + s, d0 + 4 * t);
+  // address-space cast (generic -> LDS) needs a C-style cast
+  lds_bf16x4_t* lp = (lds_bf16x4_t*)(const_cast<uint16_t*>(p));
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(lp));
+}
+
+// A/B operand of v_mfma_f32_32x32x16_bf16 whose k index runs along the rows
+// of a swizzled tile and whose m/n index is the column d = dm0 + (lane % 32):
+// k-step covering rows k0..k0+15 in the slot order used throughout
+// (slots 0-3: rows k0+4g+0..3, slots 4-7: rows k0+8+4g+0..3).
+__device__ __forceinline__ uint4 lds_kmajor(const uint16_t* tile, int k0, int dm0, int lane) {
+  const int g = lane >> 5, l16 = lane & 15, d0 = dm0 + ((lane >> 4) & 1) * 16;
+  const uint2 lo = lds_tr4(tile, k0 + 4 * g, d0, l16);
+  const uint2 hi = lds_tr4(tile, k0 + 8 + 4 * g, d0, l16);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
 // Map a linear workgroup id so that the workgroups one XCD runs (the
 // hardware deals ids round-robin over the 8 XCDs) cover consecutive tiles,
 // which then share key blocks in that XCD's L2.
@@ -117,7 +157,8 @@ struct AttnArgs {
   float* dslope;
   float* ddelta_main;
   float* dwidth;
-  float* delta;  // rowsum(dO∘O) [H,T]
+  float* delta;      // rowsum(dO∘O) [H,T]
+  uint16_t* qfeat;   // token mode: query-side features [H,T][kTokRow] (hi g0, hi g1, lo g0, lo g1)
   int H, QB, maxkv, K;
   int64_t T;
   int64_t q_sh, q_st, k_sh, k_st, v_sh, v_st, o_sh, o_st;

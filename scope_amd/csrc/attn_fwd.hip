@@ -360,6 +360,10 @@ int validate_attn(const scope_attn_params* p, const void* q, const void* k, cons
   SCOPE_REQUIRE(p->q_st % 8 == 0 && p->k_st % 8 == 0 && p->v_st % 8 == 0 && p->o_st % 8 == 0 &&
                     p->q_sh % 8 == 0 && p->k_sh % 8 == 0 && p->v_sh % 8 == 0 && p->o_sh % 8 == 0,
                 "%s: strides must be multiples of 8 elements (16-byte rows)", who);
+  auto al16 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
+  SCOPE_REQUIRE(al16(q) && al16(k) && al16(v) && al16(docs) && al16(cc) && al16(cs) && al16(b0) && al16(slope) &&
+                    al16(dm) && al16(wd) && al16(table),
+                "%s: tensors must start on a 16-byte boundary", who);
   SCOPE_REQUIRE(p->bias_mode >= 0 && p->bias_mode <= 2, "%s: bias_mode %d", who, p->bias_mode);
   if (p->bias_mode != SCOPE_BIAS_NONE) {
     SCOPE_REQUIRE(p->K >= 1 && p->K <= 8, "%s: K=%d outside [1, 8]", who, p->K);
