@@ -27,42 +27,152 @@ constexpr int kChunk = 16;  // q-blocks per dK/dV work item
 // ---------------------------------------------------------------------------
 // pass A
 // ---------------------------------------------------------------------------
+// LDS staging of one 64-key tile of pass A, filled by global_load_lds; two
+// buffers alternate so the loads of tile j+1 run under the MFMAs of tile j.
+template <int MODE>
+struct alignas(16) DqBuf {
+  uint16_t k[64 * 128];                    // K rows, swizzled (swz_off)
+  uint16_t v[64 * 128];                    // V rows, swizzled
+  int docs[64];                            // document id per key
+  float tab[16];                           // block: table row of distance qb - kb
+  uint16_t f[MODE >= 2 ? 64 * kTokRow : 8];  // token: key features [64][32], chunk-swizzled (swz32_off)
+};
+
+constexpr int kListLds = 1024;  // kv-list entries staged in LDS (longer lists read the rest from memory)
+
+template <int MODE>
+__device__ __forceinline__ void dq_issue(const AttnArgs& a, int h, int64_t kv0, int rdist, DqBuf<MODE>& b, int tid) {
+  const int wave = tid >> 6, lane = tid & 63;
+  {
+    const int r = tid >> 4, c = (tid & 15) ^ swz(r);
+    const uint16_t* kp = a.k + h * a.k_sh + (kv0 + r) * a.k_st + c * 8;
+    const uint16_t* vp = a.v + h * a.v_sh + (kv0 + r) * a.v_st + c * 8;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      g2lds16(kp + jj * 16 * a.k_st, b.k + (jj * 256 + wave * 64) * 8);
+      g2lds16(vp + jj * 16 * a.v_st, b.v + (jj * 256 + wave * 64) * 8);
+    }
+  }
+  if (wave == 0 && lane < 16) g2lds16(a.docs + kv0 + lane * 4, b.docs);
+  if (MODE == 1 && wave == 1 && lane < 4)
+    g2lds16(static_cast<const float*>(a.table) + static_cast<int64_t>(rdist) * 16 + lane * 4, b.tab);
+  if (MODE >= 2) {
+    const int r = tid >> 2, c = (tid & 3) ^ ((r >> 2) & 3);
+    g2lds16(static_cast<const uint16_t*>(a.table) + (kv0 + r) * kTokRow + c * 8, b.f + wave * 64 * 8);
+  }
+}
+
+// per-row state of pass A (one query row per lane pair l, l^32)
+struct DqRow {
+  float delta, lse2, rowc, slp, dm, wd;
+  int row, doc;
+};
+
+// Probabilities and dS^T of one tile for this lane's query row, as bf16 B
+// operands of dQ^T = K^T·dS^T (k index: the 64 keys, slot order of
+// lds_kmajor), plus the per-row sums the bias gradients need.
+template <int MODE, bool MASK>
+__device__ __forceinline__ void dq_probs(const AttnArgs& a, const DqBuf<MODE>& b, const DqRow& R, int kv0, float off,
+                                         int lane, const f32x16_t (&s)[2], const f32x16_t (&dpv)[2],
+                                         uint4 (&dsb)[4], uint4 (&pbv)[4], float& rs, float& pm, float (&ex)[6]) {
+  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
+  const int g = lane >> 5;
+  const float cs = a.scale_log2;
+  const float glam = a.beta_log2 * a.ramp_lambda;
+  const bool softplus = a.gate_kind == SCOPE_GATE_SOFTPLUS;
+  const int lim = R.row - kv0;  // keys j <= lim are causal
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      float dsv[8], pvv[8];
+      int dcv[8];
+      if (MASK) {
+        const int4 d0 = *reinterpret_cast<const int4*>(&b.docs[mb * 32 + 16 * hf + 4 * g]);
+        const int4 d1 = *reinterpret_cast<const int4*>(&b.docs[mb * 32 + 16 * hf + 8 + 4 * g]);
+        dcv[0] = d0.x, dcv[1] = d0.y, dcv[2] = d0.z, dcv[3] = d0.w;
+        dcv[4] = d1.x, dcv[5] = d1.y, dcv[6] = d1.z, dcv[7] = d1.w;
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int r = hf * 8 + jj;
+        const int j = mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);  // key within the tile
+        float x;
+        float sig = 0.f, sgn = 0.f, df = 0.f;
+        if (TOK) {
+          df = static_cast<float>(lim - j);
+          float e = R.slp * df;
+          if (GATE) {
+            const float dd = df - R.dm;
+            const float xx = (fabsf(dd) - R.wd) * a.inv_tau;
+            const float en = __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e);
+            const float inv = __builtin_amdgcn_rcpf(1.f + en);
+            const float lp = kLn2 * __builtin_amdgcn_logf(1.f + en);
+            const float gt = fmaxf(xx, 0.f) + (softplus ? lp : 0.f);
+            sig = softplus ? (xx >= 0.f ? inv : en * inv) : (xx > 0.f ? 1.f : 0.f);
+            sgn = dd > 0.f ? 1.f : (dd < 0.f ? -1.f : 0.f);
+            e -= glam * gt;
+          }
+          x = fmaf(s[mb][r], cs, e + off);
+        } else {
+          x = fmaf(s[mb][r], cs, off);
+        }
+        if (MASK) x = (j <= lim) & (dcv[jj] == R.doc) ? x : -INFINITY;
+        const float p = __builtin_amdgcn_exp2f(x);
+        const float d = p * (dpv[mb][r] - R.delta);
+        dsv[jj] = d;
+        pvv[jj] = p;
+        rs += d;
+        pm += p;
+        if (TOK) {
+          ex[0] += d * df;
+          ex[3] += p * df;
+          if (GATE) {
+            ex[1] += d * sig * sgn;
+            ex[2] += d * sig;
+            ex[4] += p * sig * sgn;
+            ex[5] += p * sig;
+          }
+        }
+      }
+      dsb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(dsv[0], dsv[1]), cvt_pk_bf16(dsv[2], dsv[3]),
+                                    cvt_pk_bf16(dsv[4], dsv[5]), cvt_pk_bf16(dsv[6], dsv[7]));
+      if (TOK)
+        pbv[mb * 2 + hf] = make_uint4(cvt_pk_bf16(pvv[0], pvv[1]), cvt_pk_bf16(pvv[2], pvv[3]),
+                                      cvt_pk_bf16(pvv[4], pvv[5]), cvt_pk_bf16(pvv[6], pvv[7]));
+    }
+}
+
 template <int BS, int MODE>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
-  constexpr int NT = 256;          // 4 waves = 128 query rows per workgroup
-  constexpr int SPLIT = BS / 128;  // workgroups per q-block
-  constexpr int D = 128;
-  constexpr int BN = 64;
-  constexpr int KSTR = D + 8;
-  constexpr int TSTR = BN + 4;
-  constexpr int FSTR = 40;
+  constexpr int SPLIT = BS / 128;  // workgroups per q-block (4 wavefronts = 128 query rows each)
+  constexpr int BN = 64;           // keys per staged tile
   constexpr int NSUB = BS / BN;
-  constexpr int MB = BN / 32;
-  constexpr int KCH = BN * 16;
-  constexpr int KL = (KCH + NT - 1) / NT;
+  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[BN * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[D * TSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Fs[MODE == 2 ? BN * FSTR : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t Ft[MODE == 2 ? 32 * TSTR : 8];
-  __shared__ __attribute__((aligned(16))) int docs_s[BN];
+  __shared__ DqBuf<MODE> buf0, buf1;
+  __shared__ int kbs[kListLds];
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
   const int h = tile / (a.QB * SPLIT), qb = (tile / SPLIT) % a.QB, part = tile % SPLIT;
   const int64_t q0 = static_cast<int64_t>(qb) * BS + part * 128;
-  const int64_t wrow_lo = q0 + wave * 32;
-  const int64_t row = wrow_lo + lr;
+  const int wrow_lo = static_cast<int>(q0) + wave * 32;
   const int64_t hT = static_cast<int64_t>(h) * a.T;
+  DqRow R;
+  R.row = wrow_lo + lr;
+
+  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
+  const int n = a.kv_num[lrow];
+  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
+  for (int t = tid; t < min(n, kListLds); t += 256) kbs[t] = lst[t];
 
   uint4 qreg[8], doreg[8];
-  float delta;
   {
-    const uint16_t* qp = a.q + h * a.q_sh + row * a.q_st + g * 8;
-    const uint16_t* op = a.o + h * a.o_sh + row * a.o_st + g * 8;
-    const uint16_t* dp = a.dout + h * a.o_sh + row * a.o_st + g * 8;
+    const uint16_t* qp = a.q + h * a.q_sh + R.row * a.q_st + g * 8;
+    const uint16_t* op = a.o + h * a.o_sh + R.row * a.o_st + g * 8;
+    const uint16_t* dp = a.dout + h * a.o_sh + R.row * a.o_st + g * 8;
     float dsum = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -77,47 +187,38 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
         dsum += __uint_as_float(dw[i] & 0xffff0000u) * __uint_as_float(ow[i] & 0xffff0000u);
       }
     }
-    delta = dsum + __shfl_xor(dsum, 32, 64);
-    if (g == 0) a.delta[hT + row] = delta;
+    R.delta = dsum + __shfl_xor(dsum, 32, 64);
+    if (g == 0) a.delta[hT + R.row] = R.delta;
   }
-  const float lse_nat = a.lse[hT + row];
-  const float lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
+  const float lse_nat = a.lse[hT + R.row];
+  R.lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
 
   // ---- bias set-up (as in the forward)
   float ca[8], sa[8];
   uint4 qf = make_uint4(0, 0, 0, 0), qfl = make_uint4(0, 0, 0, 0);
-  float rowc = 0.f, slp = 0.f, dm = 0.f, wd = 0.f, glam = 0.f;
+  R.rowc = R.slp = R.dm = R.wd = 0.f;
   float cos_i[4], sin_i[4];  // token mode: cos/sin(ω_k row) for k = 4g..4g+3
   if (MODE == 1) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      ca[k] = k < a.K ? a.coeff_cos[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
-      sa[k] = k < a.K ? a.coeff_sin[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
+      ca[k] = k < a.K ? a.coeff_cos[(hT + R.row) * a.K + k] * a.beta_log2 : 0.f;
+      sa[k] = k < a.K ? a.coeff_sin[(hT + R.row) * a.K + k] * a.beta_log2 : 0.f;
     }
   }
-  if (MODE == 2) {
-    token_qfeat(a, hT, row, g, qf, qfl, cos_i, sin_i);
+  if (TOK) {
+    token_qfeat(a, hT, R.row, g, qf, qfl, cos_i, sin_i);
     // kept for pass B, which stages them per query tile
-    *reinterpret_cast<uint4*>(a.qfeat + (hT + row) * kTokRow + g * 8) = qf;
-    *reinterpret_cast<uint4*>(a.qfeat + (hT + row) * kTokRow + 16 + g * 8) = qfl;
-    if (a.subtract_b0) rowc = -a.beta_log2 * a.b0[hT + row];
-    if (a.use_slope) slp = a.beta_log2 * a.slope[hT + row];
-    if (a.gate_kind != SCOPE_GATE_NONE) {
-      dm = a.delta_main[hT + row];
-      wd = a.width[hT + row];
-      glam = a.beta_log2 * a.ramp_lambda;
+    *reinterpret_cast<uint4*>(a.qfeat + (hT + R.row) * kTokRow + g * 8) = qf;
+    *reinterpret_cast<uint4*>(a.qfeat + (hT + R.row) * kTokRow + 16 + g * 8) = qfl;
+    if (a.subtract_b0) R.rowc = -a.beta_log2 * a.b0[hT + R.row];
+    if (a.use_slope) R.slp = a.beta_log2 * a.slope[hT + R.row];
+    if (GATE) {
+      R.dm = a.delta_main[hT + R.row];
+      R.wd = a.width[hT + R.row];
     }
   }
-  const bool gate = MODE == 2 && a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
-  const bool extra = MODE == 2 && (a.use_slope || gate);
-
-  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
-  const int n = a.kv_num[lrow];
-  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
-  const int total = n * NSUB;
   const int ds_end = a.ds_tok_end[qb];
-  const int doc_row = a.docs[row];
-  const float cs = a.scale_log2;
+  R.doc = a.docs[R.row];
 
   f32x16_t o[4];
 #pragma unroll
@@ -125,231 +226,121 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   // Bias gradients use Δ_true = Σ_j P dP rather than the Δ of the bf16
   // output: since Σ_j P = 1, the row total Σ_j dS equals Δ_true - Δ, so each
   // per-tile sum is corrected by subtracting that total times the tile's
-  // probability mass (the *_p accumulators hold the P-weighted sums).
+  // probability mass (the *P accumulators hold the P-weighted sums).  All
+  // sums stay per lane (half the keys of the row) until the epilogue.
   f32x16_t facc = zero16(), facc_p = zero16();
   float accA[8], accB[8], accPA[8], accPB[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) accA[k] = accB[k] = accPA[k] = accPB[k] = 0.f;
-  float rs_tot = 0.f, sl_tot = 0.f, gdm_tot = 0.f, gwd_tot = 0.f;
-  float pm_tot = 0.f, psl_tot = 0.f, pgdm_tot = 0.f, pgwd_tot = 0.f;
+  float rs_tot = 0.f, pm_tot = 0.f;
+  float ex[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // Σ dS·df, dS·σ·sgn, dS·σ, then the P-weighted three
 
-  for (int it = 0; it < total; ++it) {
-    const int t = it / NSUB, st = it % NSUB;
-    const int kb = lst[t];
-    const int64_t kv0 = static_cast<int64_t>(kb) * BS + st * BN;
-    // ---- stage K, V (rows), docs, key features; then K^T / F^T in LDS
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int idx = tid + i * NT;
-      if (KCH % NT == 0 || idx < KCH) {
-        const int r = idx / 16, c = idx % 16;
-        *reinterpret_cast<uint4*>(&Ks[r * KSTR + c * 8]) =
-            *reinterpret_cast<const uint4*>(a.k + h * a.k_sh + (kv0 + r) * a.k_st + c * 8);
-        *reinterpret_cast<uint4*>(&Vs[r * KSTR + c * 8]) =
-            *reinterpret_cast<const uint4*>(a.v + h * a.v_sh + (kv0 + r) * a.v_st + c * 8);
-      }
-    }
-    if (tid < BN) docs_s[tid] = a.docs[kv0 + tid];
-    if (MODE == 2)
-      for (int idx = tid; idx < BN * 4; idx += NT)
-        *reinterpret_cast<uint4*>(&Fs[(idx / 4) * FSTR + (idx % 4) * 8]) = *reinterpret_cast<const uint4*>(
-            static_cast<const uint16_t*>(a.table) + (kv0 + idx / 4) * kTokRow + (idx % 4) * 8);
-    __syncthreads();
-    // K^T from Ks: 4 keys x 8 dims per thread (BN/4 * 16 blocks)
-    for (int idx = tid; idx < BN * 4; idx += NT) {
-      const int c = idx % 16, kvg = idx / 16;
-      uint32_t w[4][4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const uint4 u = *reinterpret_cast<const uint4*>(&Ks[(kvg * 4 + rr) * KSTR + c * 8]);
-        w[rr][0] = u.x;
-        w[rr][1] = u.y;
-        w[rr][2] = u.z;
-        w[rr][3] = u.w;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        uint2 val;
-        if (e & 1) {
-          val.x = pack_hi16(w[0][e / 2], w[1][e / 2]);
-          val.y = pack_hi16(w[2][e / 2], w[3][e / 2]);
-        } else {
-          val.x = pack_lo16(w[0][e / 2], w[1][e / 2]);
-          val.y = pack_lo16(w[2][e / 2], w[3][e / 2]);
-        }
-        *reinterpret_cast<uint2*>(&Kt[(c * 8 + e) * TSTR + kvg * 4]) = val;
-      }
-    }
-    if (MODE == 2) {
-      // F^T: rows 0..15 = hi features, rows 16..31 = lo features
-      for (int idx = tid; idx < 32 * BN; idx += NT) {
-        const int f = idx / BN, j = idx % BN;
-        Ft[f * TSTR + j] = Fs[j * FSTR + f];
-      }
-    }
-    __syncthreads();
-
-    if (kv0 > wrow_lo + 31) continue;
+  // flat iteration index it = list entry · NSUB + key sub-tile; sub-tiles that
+  // start after this workgroup's last row are skipped
+  const int total = n * NSUB;
+  const int qmax = static_cast<int>(q0) + 127;
+  auto kb_at = [&](int t) { return t < kListLds ? kbs[t] : lst[t]; };
+  auto next_valid = [&](int it) {
+    while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
+    return it;
+  };
+  auto issue = [&](int it, DqBuf<MODE>& b) {
+    const int kb = kb_at(it / NSUB);
+    const int rd = min(max(qb - kb, 0), a.QB - 1);
+    dq_issue<MODE>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
+  };
+  auto run = [&](int it, const DqBuf<MODE>& b) {
+    const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
+    if (kv0 > wrow_lo + 31) return;  // every key follows this wavefront's rows
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
-    float tconst = rowc;
-    float crow[8], srow[8];
+    float tconst = R.rowc;
     if (MODE == 1) {
-      const float* tr = static_cast<const float*>(a.table) + static_cast<int64_t>(qb - kb) * 16;
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        crow[k] = tr[k];
-        srow[k] = tr[8 + k];
-        acc += ca[k] * crow[k] + sa[k] * srow[k];
-      }
+      for (int k = 0; k < 8; ++k) acc += ca[k] * b.tab[k] + sa[k] * b.tab[8 + k];
       tconst = acc;
     }
-
-    // S^T and dP^T
-    f32x16_t s[MB], dpv[MB];
+    // S^T and dP^T: keys in two 32-row blocks (A operand), this lane's query row as the column
+    f32x16_t s[2], dpv[2];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+    for (int mb = 0; mb < 2; ++mb) {
       s[mb] = zero16();
       dpv[mb] = zero16();
-      const uint16_t* kr = &Ks[(mb * 32 + lr) * KSTR + g * 8];
-      const uint16_t* vr = &Vs[(mb * 32 + lr) * KSTR + g * 8];
+    }
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        s[mb] = mfma32(*reinterpret_cast<const uint4*>(kr + ks * 16), qreg[ks], s[mb]);
-        dpv[mb] = mfma32(*reinterpret_cast<const uint4*>(vr + ks * 16), doreg[ks], dpv[mb]);
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        s[mb] = mfma32(lds_row8(b.k, mb * 32 + lr, ks * 16 + g * 8), qreg[ks], s[mb]);
+        dpv[mb] = mfma32(lds_row8(b.v, mb * 32 + lr, ks * 16 + g * 8), doreg[ks], dpv[mb]);
       }
-      if (MODE == 2) {
-        const uint4 fh = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + g * 8]);
-        const uint4 fl = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + 16 + g * 8]);
+    if (TOK) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const uint4 fh = lds_row8_32(b.f, mb * 32 + lr, g * 8);
+        const uint4 fl = lds_row8_32(b.f, mb * 32 + lr, 16 + g * 8);
         s[mb] = mfma32(fh, qf, s[mb]);
         s[mb] = mfma32(fh, qfl, s[mb]);
         s[mb] = mfma32(fl, qf, s[mb]);
       }
     }
-    if (!full) {
-      const int lim = static_cast<int>(row - kv0);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int j0 = mb * 32 + 8 * rq + 4 * g;
-          const int4 d4 = *reinterpret_cast<const int4*>(&docs_s[j0]);
-          const int dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool ok = (j0 + i <= lim) & (dv[i] == doc_row);
-            s[mb][4 * rq + i] = ok ? s[mb][4 * rq + i] : -INFINITY;
-          }
-        }
-    }
-    // P, dS (natural units), per-row reductions
-    const float off = tconst - lse2;
-    uint4 dsb[2 * MB], pbv[2 * MB];
-    float rs = 0.f, slv = 0.f, gdm = 0.f, gwd = 0.f;
-    float pm = 0.f, psl = 0.f, pgdm = 0.f, pgwd = 0.f;
-    const int dbase = static_cast<int>(row - kv0);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        float dsv[8], pvv[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int r = hf * 8 + jj;
-          float x = s[mb][r];
-          float sig = 0.f, sgn = 0.f, df = 0.f;
-          if (extra) {
-            const int j = mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-            df = static_cast<float>(dbase - j);
-            float e = slp * df;
-            if (gate) {
-              const float dd = df - dm;
-              const float xx = (fabsf(dd) - wd) * a.inv_tau;
-              float gt;
-              if (a.gate_kind == SCOPE_GATE_SOFTPLUS) {
-                const float ex = __expf(-fabsf(xx));
-                gt = fmaxf(xx, 0.f) + log1pf(ex);
-                sig = xx >= 0.f ? 1.f / (1.f + ex) : ex / (1.f + ex);
-              } else {
-                gt = fmaxf(xx, 0.f);
-                sig = xx > 0.f ? 1.f : 0.f;
-              }
-              sgn = dd > 0.f ? 1.f : (dd < 0.f ? -1.f : 0.f);
-              e -= glam * gt;
-            }
-            x = fmaf(x, cs, e);
-          } else {
-            x = x * cs;
-          }
-          const float p = exp2f(x + off);
-          const float d = p * (dpv[mb][r] - delta);
-          dsv[jj] = d;
-          pvv[jj] = p;
-          rs += d;
-          pm += p;
-          if (extra) {
-            slv += d * df;
-            gdm += d * sig * sgn;
-            gwd += d * sig;
-            psl += p * df;
-            pgdm += p * sig * sgn;
-            pgwd += p * sig;
-          }
-        }
-        dsb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(dsv[0], dsv[1]), cvt_pk_bf16(dsv[2], dsv[3]),
-                                      cvt_pk_bf16(dsv[4], dsv[5]), cvt_pk_bf16(dsv[6], dsv[7]));
-        if (MODE == 2)
-          pbv[mb * 2 + hf] = make_uint4(cvt_pk_bf16(pvv[0], pvv[1]), cvt_pk_bf16(pvv[2], pvv[3]),
-                                        cvt_pk_bf16(pvv[4], pvv[5]), cvt_pk_bf16(pvv[6], pvv[7]));
-      }
+    const float off = tconst - R.lse2;
+    uint4 dsb[4], pbv[4];
+    float rs = 0.f, pm = 0.f;
+    if (TOK || !full)
+      dq_probs<MODE, true>(a, b, R, kv0, off, lane, s, dpv, dsb, pbv, rs, pm, ex);
+    else
+      dq_probs<MODE, false>(a, b, R, kv0, off, lane, s, dpv, dsb, pbv, rs, pm, ex);
     // dQ^T += K^T dS^T (and the token-mode feature sums)
 #pragma unroll
-    for (int md = 0; md < 4; ++md) {
-      const uint16_t* kt = &Kt[(md * 32 + lr) * TSTR + 4 * g];
+    for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-      for (int s2 = 0; s2 < 2 * MB; ++s2) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(kt + 16 * s2);
-        const uint2 hi = *reinterpret_cast<const uint2*>(kt + 16 * s2 + 8);
-        o[md] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), dsb[s2], o[md]);
+      for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor(b.k, 16 * s2, md * 32, lane), dsb[s2], o[md]);
+    if (TOK) {
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const uint4 ft = lds_kmajor_32(b.f, 16 * s2, lane);
+        facc = mfma32(ft, dsb[s2], facc);
+        facc_p = mfma32(ft, pbv[s2], facc_p);
       }
     }
-    if (MODE == 2) {
-      const uint16_t* ft = &Ft[lr * TSTR + 4 * g];
-#pragma unroll
-      for (int s2 = 0; s2 < 2 * MB; ++s2) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(ft + 16 * s2);
-        const uint2 hi = *reinterpret_cast<const uint2*>(ft + 16 * s2 + 8);
-        facc = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), dsb[s2], facc);
-        facc_p = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pbv[s2], facc_p);
-      }
-    }
-    rs += __shfl_xor(rs, 32, 64);
-    pm += __shfl_xor(pm, 32, 64);
     if (MODE == 1) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        accA[k] += rs * crow[k];
-        accB[k] += rs * srow[k];
-        accPA[k] += pm * crow[k];
-        accPB[k] += pm * srow[k];
+        accA[k] += rs * b.tab[k];
+        accB[k] += rs * b.tab[8 + k];
+        accPA[k] += pm * b.tab[k];
+        accPB[k] += pm * b.tab[8 + k];
       }
     }
     rs_tot += rs;
     pm_tot += pm;
-    if (extra) {
-      sl_tot += slv + __shfl_xor(slv, 32, 64);
-      gdm_tot += gdm + __shfl_xor(gdm, 32, 64);
-      gwd_tot += gwd + __shfl_xor(gwd, 32, 64);
-      psl_tot += psl + __shfl_xor(psl, 32, 64);
-      pgdm_tot += pgdm + __shfl_xor(pgdm, 32, 64);
-      pgwd_tot += pgwd + __shfl_xor(pgwd, 32, 64);
-    }
-  }
-  const float dd_err = rs_tot;  // Δ_true - Δ
+  };
 
-  // ---- epilogue: dQ = scale·o
-  uint16_t* dqp = a.dq + h * a.q_sh + row * a.q_st + 4 * g;
+  __syncthreads();  // kbs
+  int cur = next_valid(0);
+  if (cur < total) issue(cur, buf0);
+  while (cur < total) {
+    wait_vm0();
+    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
+    int nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf1);
+    run(cur, buf0);
+    cur = nxt;
+    if (cur >= total) break;
+    wait_vm0();
+    __syncthreads();
+    nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf0);
+    run(cur, buf1);
+    cur = nxt;
+  }
+
+  // ---- epilogue: combine the lane pair's half sums, dQ = scale·o
+  rs_tot += __shfl_xor(rs_tot, 32, 64);
+  pm_tot += __shfl_xor(pm_tot, 32, 64);
+  const float dd_err = rs_tot;  // Δ_true - Δ
+  uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
 #pragma unroll
@@ -360,13 +351,21 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       *reinterpret_cast<uint2*>(dqp + md * 32 + 8 * rq) = val;
     }
   const float beta = a.beta;
-  if (MODE == 1 && a.dcoeff_cos && g == 0) {
-    for (int k = 0; k < a.K; ++k) {
-      a.dcoeff_cos[(hT + row) * a.K + k] = beta * (accA[k] - dd_err * accPA[k]);
-      a.dcoeff_sin[(hT + row) * a.K + k] = beta * (accB[k] - dd_err * accPB[k]);
+  if (MODE == 1 && a.dcoeff_cos) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      accA[k] += __shfl_xor(accA[k], 32, 64);
+      accB[k] += __shfl_xor(accB[k], 32, 64);
+      accPA[k] += __shfl_xor(accPA[k], 32, 64);
+      accPB[k] += __shfl_xor(accPB[k], 32, 64);
     }
+    if (g == 0)
+      for (int k = 0; k < a.K; ++k) {
+        a.dcoeff_cos[(hT + R.row) * a.K + k] = beta * (accA[k] - dd_err * accPA[k]);
+        a.dcoeff_sin[(hT + R.row) * a.K + k] = beta * (accB[k] - dd_err * accPB[k]);
+      }
   }
-  if (MODE == 2) {
+  if (TOK) {
     if (a.dcoeff_cos) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -375,16 +374,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
           // feature rows: 4g+i (cos hi), 8+4g+i (sin hi), 16+4g+i (cos lo), 24+4g+i (sin lo)
           const float C = (facc[i] + facc[8 + i]) - dd_err * (facc_p[i] + facc_p[8 + i]);
           const float S = (facc[4 + i] + facc[12 + i]) - dd_err * (facc_p[4 + i] + facc_p[12 + i]);
-          a.dcoeff_cos[(hT + row) * a.K + k] = beta * (cos_i[i] * C + sin_i[i] * S);
-          a.dcoeff_sin[(hT + row) * a.K + k] = beta * (sin_i[i] * C - cos_i[i] * S);
+          a.dcoeff_cos[(hT + R.row) * a.K + k] = beta * (cos_i[i] * C + sin_i[i] * S);
+          a.dcoeff_sin[(hT + R.row) * a.K + k] = beta * (sin_i[i] * C - cos_i[i] * S);
         }
       }
     }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) ex[i] += __shfl_xor(ex[i], 32, 64);
     if (g == 0) {
-      if (a.db0) a.db0[hT + row] = -beta * (rs_tot - dd_err * pm_tot);
-      if (a.dslope) a.dslope[hT + row] = beta * (sl_tot - dd_err * psl_tot);
-      if (a.ddelta_main) a.ddelta_main[hT + row] = beta * a.ramp_lambda * a.inv_tau * (gdm_tot - dd_err * pgdm_tot);
-      if (a.dwidth) a.dwidth[hT + row] = beta * a.ramp_lambda * a.inv_tau * (gwd_tot - dd_err * pgwd_tot);
+      if (a.db0) a.db0[hT + R.row] = -beta * (rs_tot - dd_err * pm_tot);
+      if (a.dslope) a.dslope[hT + R.row] = beta * (ex[0] - dd_err * ex[3]);
+      const float gsc = beta * a.ramp_lambda * a.inv_tau;
+      if (a.ddelta_main) a.ddelta_main[hT + R.row] = GATE ? gsc * (ex[1] - dd_err * ex[4]) : 0.f;
+      if (a.dwidth) a.dwidth[hT + R.row] = GATE ? gsc * (ex[2] - dd_err * ex[5]) : 0.f;
     }
   }
 }
@@ -464,17 +466,6 @@ struct alignas(16) DkvBuf {
                                    // token: query features [64][32] bf16 (chunk-swizzled)
   float rc[MODE >= 2 ? 256 : 4];   // token: slope | delta_main | width
 };
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// 16-byte global -> LDS copy; the LDS address is dst_wave + 16·lane, where
-// dst_wave must be the same for the whole wavefront.
-__device__ __forceinline__ void g2lds16(const void* src, void* dst_wave) {
-  __builtin_amdgcn_global_load_lds(const_cast<void*>(src), (lds_void_t*)dst_wave, 16, 0, 0);
-}
-
-// vmcnt(0): every global load of this wavefront (including global_load_lds) has landed
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Issue the copies of the 64-row query tile starting at token q0 into b.
 template <int MODE>
@@ -634,9 +625,8 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
     const uint16_t* qf = reinterpret_cast<const uint16_t*>(b.rb);
 #pragma unroll
     for (int mq = 0; mq < 2; ++mq) {
-      const int r = mq * 32 + lr, sw = (r >> 2) & 3;
-      const uint4 qh = *reinterpret_cast<const uint4*>(qf + r * kTokRow + ((g ^ sw) << 3));
-      const uint4 qlo = *reinterpret_cast<const uint4*>(qf + r * kTokRow + (((2 + g) ^ sw) << 3));
+      const uint4 qh = lds_row8_32(qf, mq * 32 + lr, g * 8);
+      const uint4 qlo = lds_row8_32(qf, mq * 32 + lr, 16 + g * 8);
       s[mq] = mfma32(qh, kf, s[mq]);
       s[mq] = mfma32(qlo, kf, s[mq]);
       s[mq] = mfma32(qh, kfl, s[mq]);
@@ -870,9 +860,13 @@ template <int BS>
 static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases, int grid_q, int max_items,
                        hipStream_t s) {
   dim3 gq(grid_q * (BS / 128)), gk(max_items, a.H, BS / 128), gr(a.QB, a.H);
+  // token mode with an active gate runs the kernels' MODE 3 variant
+  const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
   if (phases & SCOPE_BWD_DQ) {
     if (mode == SCOPE_BIAS_BLOCK)
       hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 1>), gq, dim3(256), 0, s, a);
+    else if (mode == SCOPE_BIAS_TOKEN && gate)
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 3>), gq, dim3(256), 0, s, a);
     else if (mode == SCOPE_BIAS_TOKEN)
       hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 2>), gq, dim3(256), 0, s, a);
     else
@@ -881,7 +875,6 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
   if (phases & SCOPE_BWD_DKV) {
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start));
-    const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
     if (mode == SCOPE_BIAS_BLOCK)
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
     else if (mode == SCOPE_BIAS_TOKEN && gate)

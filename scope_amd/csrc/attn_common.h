@@ -89,6 +89,38 @@ __device__ __forceinline__ uint4 lds_kmajor(const uint16_t* tile, int k0, int dm
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
+// ---- swizzled 32-column tiles (64-byte rows: token features) ---------------
+// The 16-byte chunk c of row r is stored at chunk c ^ ((r/4) % 4): row reads
+// of 16 consecutive rows and transpose reads of 4 rows are conflict free.
+__device__ __forceinline__ int swz32_off(int r, int d) { return r * 32 + (((d >> 3) ^ ((r >> 2) & 3)) << 3) + (d & 7); }
+
+__device__ __forceinline__ uint4 lds_row8_32(const uint16_t* tile, int r, int d) {
+  return *reinterpret_cast<const uint4*>(tile + swz32_off(r, d));
+}
+
+// A operand (32 columns x 16 rows of k) of a 32-column tile, slot order as lds_kmajor
+__device__ __forceinline__ uint4 lds_kmajor_32(const uint16_t* tile, int k0, int lane) {
+  const int g = lane >> 5, l16 = lane & 15, d0 = ((lane >> 4) & 1) * 16;
+  const int s = l16 >> 2, t = l16 & 3;
+  lds_bf16x4_t* plo = (lds_bf16x4_t*)(const_cast<uint16_t*>(tile + swz32_off(k0 + 4 * g + s, d0 + 4 * t)));
+  lds_bf16x4_t* phi = (lds_bf16x4_t*)(const_cast<uint16_t*>(tile + swz32_off(k0 + 8 + 4 * g + s, d0 + 4 * t)));
+  const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(plo));
+  const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(phi));
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// ---- direct global -> LDS copies ----------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16-byte global -> LDS copy; the LDS address is dst_wave + 16·lane, where
+// dst_wave must be the same for the whole wavefront.
+__device__ __forceinline__ void g2lds16(const void* src, void* dst_wave) {
+  __builtin_amdgcn_global_load_lds(const_cast<void*>(src), (lds_void_t*)dst_wave, 16, 0, 0);
+}
+
+// vmcnt(0): every global load of this wavefront (including global_load_lds) has landed
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Map a linear workgroup id so that the workgroups one XCD runs (the
 // hardware deals ids round-robin over the 8 XCDs) cover consecutive tiles,
 // which then share key blocks in that XCD's L2.

@@ -32,7 +32,7 @@ def _terms(mode, q, H, T, seed):
     return {}
 
 
-def _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms):
+def _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms, gate="softplus"):
     import scope_amd
     from scope_amd.blockmask import ScopeBlockMask
 
@@ -49,16 +49,16 @@ def _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms):
         if mode == "token":
             sp.b0, sp.slope, sp.delta_main, sp.width = t["b0"], t["slope"], t["delta_main"], t["width"]
             sp.use_slope = sp.subtract_b0 = True
-            sp.gate_kind, sp.ramp_lambda, sp.tau = "softplus", 0.2, 64.0
+            sp.gate_kind, sp.ramp_lambda, sp.tau = gate, 0.2 if gate != "none" else 0.0, 64.0
             leaves += [t["b0"], t["slope"], t["delta_main"], t["width"]]
     out = scope_amd.scope_attention(qd, kd, vd, block_mask=bm, scale=SCALE, spectral=sp)
     out.backward(dout.to(DEV))
     torch.cuda.synchronize()
     grads = [qd.grad, kd.grad, vd.grad] + [x.grad for x in leaves]
-    return [gr.float().cpu() for gr in grads]
+    return [None if gr is None else gr.float().cpu() for gr in grads]
 
 
-def _ref_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms):
+def _ref_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms, gate="softplus"):
     qq, kk, vv = (x[0].double().requires_grad_() for x in (q, k, v))
     kw = dict(bias_mode=mode)
     leaves = []
@@ -69,17 +69,17 @@ def _ref_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms):
         leaves = [cc, cs]
     if mode == "token":
         b0, sl, dm, wd = (terms[n][0].double().requires_grad_() for n in ("b0", "slope", "delta_main", "width"))
-        kw["token_kwargs"] = dict(b0=b0, slope=sl, delta_main=dm, width=wd, gate="softplus", ramp_lambda=0.2,
-                                  tau=64.0)
+        kw["token_kwargs"] = dict(b0=b0, slope=sl, delta_main=dm, width=wd, gate=gate,
+                                  ramp_lambda=0.2 if gate != "none" else 0.0, tau=64.0)
         leaves += [b0, sl, dm, wd]
     out, _ = OA.scope_attention_blocksparse(qq, kk, vv, kv_num, kv_idx, docs, bs=bs, scale=SCALE, beta=BETA, **kw)
     out.backward(dout[0].double())
-    return [x.grad[None] for x in (qq, kk, vv)] + [x.grad[None] for x in leaves]
+    return [x.grad[None] for x in (qq, kk, vv)] + [None if x.grad is None else x.grad[None] for x in leaves]
 
 
 NAMES = ["dq", "dk", "dv", "dcoeff_cos", "dcoeff_sin", "db0", "dslope", "ddelta_main", "dwidth"]
 CASES = [
-    # (H, T, bs, mode, n_docs, W, G, B)
+    # (H, T, bs, mode, n_docs, W, G, B); token cases use the softplus gate
     (2, 1024, 128, "none", 1, 2, 1, 2),
     (2, 1024, 128, "block", 3, 2, 1, 2),
     (2, 2048, 256, "block", 3, 2, 2, 3),
@@ -102,6 +102,28 @@ def test_attn_bwd_vs_fp64_autograd(H, T, bs, mode, n_docs, W, G, B):
     ref = _ref_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, mode, terms)
     assert len(got) == len(ref)
     for name, gg, rr in zip(NAMES, got, ref):
+        ok, worst = tol_check(gg, rr, ATOL, RTOL)
+        print(f"  {name}: worst ratio {worst:.3f} (max |ref| {rr.abs().max().item():.3g})")
+        assert ok, f"{name} violates 2e-2 abs / 1e-2 rel: worst ratio {worst:.3f}"
+
+
+@pytest.mark.parametrize("gate,bs", [("none", 128), ("relu", 256)])
+def test_attn_bwd_token_gate_kinds(gate, bs):
+    """Token mode without a gate (slope and b0 only) and with the relu gate;
+    with gate "none" the reference gradients of delta_main and width are 0."""
+    H, T = 1, 2048
+    print(f"bwd token gate={gate} bs={bs}", flush=True)
+    q, k, v = qkv(H, T, seed=11 + bs)
+    dout = torch.randn((1, H, T, 128), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    docs = docs_with_boundaries(T, 2, seed=6)
+    kv_num, kv_idx = random_blockscore_mask(H, T, bs, docs, window=2, n_global=1, budget=2, seed=7)
+    terms = _terms("token", q, H, T, seed=8)
+    got = _gpu_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, "token", terms, gate=gate)
+    ref = _ref_grads(q, k, v, dout, kv_num, kv_idx, docs, bs, "token", terms, gate=gate)
+    for name, gg, rr in zip(NAMES, got, ref):
+        if rr is None:  # no path to the parameter in the reference (gate "none")
+            assert gg is None or float(gg.abs().max()) == 0.0, name
+            continue
         ok, worst = tol_check(gg, rr, ATOL, RTOL)
         print(f"  {name}: worst ratio {worst:.3f} (max |ref| {rr.abs().max().item():.3g})")
         assert ok, f"{name} violates 2e-2 abs / 1e-2 rel: worst ratio {worst:.3f}"
