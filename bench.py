@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the run, one plain device copy of this many MiB (calibrates HBM byte counters)")
     return ap.parse_args()
 
 
@@ -94,10 +96,11 @@ class Step:
         self.NB = self.T // bs
         self.table = spectral_table(self.t["omegas"], self.T, bs, "block")
         self.ops = ops
-        self.phases = ["pointer", "stats", "transpose", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"]
+        self.phases = ["pointer", "stats", "transpose", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv", "attn_bwd_aux"]
         self.ev = {p: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for p in self.phases}
         self.acc = {p: 0.0 for p in self.phases}
+        self.aux_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
 
     def __call__(self, record=False):
         ops, t, bs = self.ops, self.t, self.bs
@@ -129,14 +132,25 @@ class Step:
                                 beta=0.5, bias_mode="block", table=self.table, coeff_cos=t["coeff_cos"],
                                 coeff_sin=t["coeff_sin"])
         mark("attn_fwd", 1)
+        # attn_bwd_dkv is the dK/dV kernel alone; attn_bwd_aux its plan and reduce kernels
+        aux = self.aux_ev
+
         def hook(phase):
             if phase == "dq":
                 mark("attn_bwd_dq", 0)
-            elif phase == "dkv":
+            elif phase == "plan":
                 mark("attn_bwd_dq", 1)
+                mark("attn_bwd_aux", 0)
+            elif phase == "dkv":
+                if record:
+                    aux[0].record()
                 mark("attn_bwd_dkv", 0)
-            else:
+            elif phase == "reduce":
                 mark("attn_bwd_dkv", 1)
+                if record:
+                    aux[1].record()
+            else:
+                mark("attn_bwd_aux", 1)
 
         grads = ops.attn_bwd(t["q"], t["k"], t["v"], out, t["dout"], lse, kv_num, kv_idx, q_off, q_list, t["docs"],
                              ds_tok_end, bs=bs, scale=0.12, beta=0.5, bias_mode="block", table=self.table,
@@ -147,6 +161,8 @@ class Step:
     def collect(self):
         for p in self.phases:
             self.acc[p] += self.ev[p][0].elapsed_time(self.ev[p][1])
+        # the aux span brackets the dK/dV kernel: remove it
+        self.acc["attn_bwd_aux"] -= self.aux_ev[0].elapsed_time(self.aux_ev[1])
 
 
 def time_steps(step, steps, warmup):
@@ -282,7 +298,8 @@ def main():
         "flops_fwd": F_fwd,
         "flops_bwd": F_bwd,
         "attn_fwd_tflops": round(F_fwd / (ph["attn_fwd"] / 1e3) / 1e12, 2),
-        "attn_bwd_tflops": round(F_bwd / ((ph["attn_bwd_dq"] + ph["attn_bwd_dkv"]) / 1e3) / 1e12, 2),
+        "attn_bwd_tflops": round(F_bwd / ((ph["attn_bwd_dq"] + ph["attn_bwd_dkv"] + ph["attn_bwd_aux"]) / 1e3) / 1e12,
+                                 2),
         "breakdown_ms": {p: round(v_, 4) for p, v_ in ph.items()},
         "needle_selected": needle_sel,
         "roofline": roofline,
@@ -300,6 +317,13 @@ def main():
         res["budget_sweep"] = sweep
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(inp, step, args.cpu_seconds, bs)
+    if args.copy_probe_mib > 0:
+        src = torch.ones(args.copy_probe_mib << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        res["copy_probe_bytes"] = src.numel() * 4
     print(json.dumps(res))
 
 

@@ -244,12 +244,22 @@ int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t
                    float* dcoeff_cos, float* dcoeff_sin, float* db0, float* dslope,
                    float* ddelta_main, float* dwidth, void* workspace, void* stream);
 
-/* The backward in two stream-ordered phases sharing one workspace:
- * SCOPE_BWD_DQ  (q-major: Δ = rowsum(dO∘O), dQ and the coefficient gradients)
- * then SCOPE_BWD_DKV (kv-major: dK, dV).  scope_attn_bwd runs both; the split
- * lets a caller time or overlap the phases.  No reference counterpart beyond
- * the FlexAttention backward that scope_attn_bwd replaces. */
-enum { SCOPE_BWD_DQ = 1, SCOPE_BWD_DKV = 2 };
+/* The backward in stream-ordered phases sharing one workspace:
+ * SCOPE_BWD_DQ  (q-major: Δ = rowsum(dO∘O), dQ and the coefficient gradients;
+ * in token mode it also stores the query features the kv-major pass reads),
+ * then SCOPE_BWD_DKV (kv-major: dK, dV), which is the three steps
+ * SCOPE_BWD_DKV_PLAN (work items), SCOPE_BWD_DKV_MAIN (the dK/dV kernel) and
+ * SCOPE_BWD_DKV_REDUCE (ordered sum of chunk partials), run in that order.
+ * scope_attn_bwd runs everything; the split lets a caller time or overlap the
+ * phases.  No reference counterpart beyond the FlexAttention backward that
+ * scope_attn_bwd replaces. */
+enum {
+  SCOPE_BWD_DQ = 1,
+  SCOPE_BWD_DKV = 2,
+  SCOPE_BWD_DKV_PLAN = 4,
+  SCOPE_BWD_DKV_MAIN = 8,
+  SCOPE_BWD_DKV_REDUCE = 16
+};
 int scope_attn_bwd_phase(const scope_attn_params* p, int phases, const uint16_t* q, const uint16_t* k,
                          const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,
                          const int32_t* kv_num, const int32_t* kv_idx, const int32_t* q_off,

@@ -27,41 +27,6 @@ constexpr int kChunk = 16;  // q-blocks per dK/dV work item
 // ---------------------------------------------------------------------------
 // pass A
 // ---------------------------------------------------------------------------
-// LDS staging of one 64-key tile of pass A, filled by global_load_lds; two
-// buffers alternate so the loads of tile j+1 run under the MFMAs of tile j.
-template <int MODE>
-struct alignas(16) DqBuf {
-  uint16_t k[64 * 128];                    // K rows, swizzled (swz_off)
-  uint16_t v[64 * 128];                    // V rows, swizzled
-  int docs[64];                            // document id per key
-  float tab[16];                           // block: table row of distance qb - kb
-  uint16_t f[MODE >= 2 ? 64 * kTokRow : 8];  // token: key features [64][32], chunk-swizzled (swz32_off)
-};
-
-constexpr int kListLds = 1024;  // kv-list entries staged in LDS (longer lists read the rest from memory)
-
-template <int MODE>
-__device__ __forceinline__ void dq_issue(const AttnArgs& a, int h, int64_t kv0, int rdist, DqBuf<MODE>& b, int tid) {
-  const int wave = tid >> 6, lane = tid & 63;
-  {
-    const int r = tid >> 4, c = (tid & 15) ^ swz(r);
-    const uint16_t* kp = a.k + h * a.k_sh + (kv0 + r) * a.k_st + c * 8;
-    const uint16_t* vp = a.v + h * a.v_sh + (kv0 + r) * a.v_st + c * 8;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      g2lds16(kp + jj * 16 * a.k_st, b.k + (jj * 256 + wave * 64) * 8);
-      g2lds16(vp + jj * 16 * a.v_st, b.v + (jj * 256 + wave * 64) * 8);
-    }
-  }
-  if (wave == 0 && lane < 16) g2lds16(a.docs + kv0 + lane * 4, b.docs);
-  if (MODE == 1 && wave == 1 && lane < 4)
-    g2lds16(static_cast<const float*>(a.table) + static_cast<int64_t>(rdist) * 16 + lane * 4, b.tab);
-  if (MODE >= 2) {
-    const int r = tid >> 2, c = (tid & 3) ^ ((r >> 2) & 3);
-    g2lds16(static_cast<const uint16_t*>(a.table) + (kv0 + r) * kTokRow + c * 8, b.f + wave * 64 * 8);
-  }
-}
-
 // per-row state of pass A (one query row per lane pair l, l^32)
 struct DqRow {
   float delta, lse2, rowc, slp, dm, wd;
@@ -72,7 +37,7 @@ struct DqRow {
 // operands of dQ^T = K^T·dS^T (k index: the 64 keys, slot order of
 // lds_kmajor), plus the per-row sums the bias gradients need.
 template <int MODE, bool MASK>
-__device__ __forceinline__ void dq_probs(const AttnArgs& a, const DqBuf<MODE>& b, const DqRow& R, int kv0, float off,
+__device__ __forceinline__ void dq_probs(const AttnArgs& a, const KvTile<MODE>& b, const DqRow& R, int kv0, float off,
                                          int lane, const f32x16_t (&s)[2], const f32x16_t (&dpv)[2],
                                          uint4 (&dsb)[4], uint4 (&pbv)[4], float& rs, float& pm, float (&ex)[6]) {
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
@@ -117,7 +82,7 @@ __device__ __forceinline__ void dq_probs(const AttnArgs& a, const DqBuf<MODE>& b
         } else {
           x = fmaf(s[mb][r], cs, off);
         }
-        if (MASK) x = (j <= lim) & (dcv[jj] == R.doc) ? x : -INFINITY;
+        if (MASK) x = mask_score(x, j, lim, dcv[jj], R.doc);
         const float p = __builtin_amdgcn_exp2f(x);
         const float d = p * (dpv[mb][r] - R.delta);
         dsv[jj] = d;
@@ -150,7 +115,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int NSUB = BS / BN;
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
 
-  __shared__ DqBuf<MODE> buf0, buf1;
+  __shared__ KvTile<MODE> buf0, buf1;
   __shared__ int kbs[kListLds];
 
   const int tid = threadIdx.x;
@@ -244,12 +209,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
     return it;
   };
-  auto issue = [&](int it, DqBuf<MODE>& b) {
+  auto issue = [&](int it, KvTile<MODE>& b) {
     const int kb = kb_at(it / NSUB);
     const int rd = min(max(qb - kb, 0), a.QB - 1);
-    dq_issue<MODE>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
+    kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
   };
-  auto run = [&](int it, const DqBuf<MODE>& b) {
+  auto run = [&](int it, const KvTile<MODE>& b) {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (kv0 > wrow_lo + 31) return;  // every key follows this wavefront's rows
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
@@ -555,7 +520,7 @@ __device__ __forceinline__ void dkv_probs(const AttnArgs& a, const DkvBuf<MODE>&
         } else {
           xv = fmaf(s[mq][r], cs, ofv[i2]);
         }
-        if (MASK) xv = (wkv <= q) & (dcv[i2] == doc_kv) ? xv : -INFINITY;
+        if (MASK) xv = mask_score(xv, wkv, q, doc_kv, dcv[i2]);
         const float p = __builtin_amdgcn_exp2f(xv);
         pv[i2] = p;
         dsv[i2] = p * (dp[mq][r] - dlv[i2]);
@@ -872,9 +837,11 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
     else
       hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 0>), gq, dim3(256), 0, s, a);
   }
-  if (phases & SCOPE_BWD_DKV) {
+  if (phases & SCOPE_BWD_DKV) phases |= SCOPE_BWD_DKV_PLAN | SCOPE_BWD_DKV_MAIN | SCOPE_BWD_DKV_REDUCE;
+  if (phases & SCOPE_BWD_DKV_PLAN)
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start));
+  if (phases & SCOPE_BWD_DKV_MAIN) {
     if (mode == SCOPE_BIAS_BLOCK)
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
     else if (mode == SCOPE_BIAS_TOKEN && gate)
@@ -883,8 +850,8 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2>), gk, dim3(256), 0, s, a, pl);
     else
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 0>), gk, dim3(256), 0, s, a, pl);
-    hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
   }
+  if (phases & SCOPE_BWD_DKV_REDUCE) hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
 }
 
 }  // namespace scope
@@ -904,7 +871,8 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
                                     const float* slope, const float* delta_main, const float* width, uint16_t* dq,
                                     uint16_t* dk, uint16_t* dv, float* dcoeff_cos, float* dcoeff_sin, float* db0,
                                     float* dslope, float* ddelta_main, float* dwidth, void* workspace, void* stream) {
-  SCOPE_REQUIRE(phases >= 1 && phases <= 3, "scope_attn_bwd_phase: phases must be 1, 2 or 3 (got %d)", phases);
+  SCOPE_REQUIRE(phases >= 1 && phases <= 31, "scope_attn_bwd_phase: phases must be a non-empty set of SCOPE_BWD_* bits (got %d)",
+                phases);
   int rc = validate_attn(p, q, k, v, kv_num, kv_idx, docs, ds_tok_end, table, coeff_cos, coeff_sin, b0, slope,
                          delta_main, width, "scope_attn_bwd");
   if (rc) return rc;

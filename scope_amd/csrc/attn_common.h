@@ -121,6 +121,16 @@ __device__ __forceinline__ void g2lds16(const void* src, void* dst_wave) {
 // vmcnt(0): every global load of this wavefront (including global_load_lds) has landed
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// x where key j is visible from a row (j <= lim and the same document), else
+// -inf, with integer sign-bit arithmetic only: comparisons would each take an
+// SGPR pair, and a tile's worth of them exhausts the scalar registers.
+__device__ __forceinline__ float mask_score(float x, int j, int lim, int doc_key, int doc_row) {
+  const uint32_t d = static_cast<uint32_t>(doc_key ^ doc_row);
+  const int ne = static_cast<int>(d | (0u - d));  // sign bit set iff the documents differ
+  const int bad = ((lim - j) | ne) >> 31;         // all ones when j > lim or the documents differ
+  return __int_as_float((__float_as_int(x) & ~bad) | (static_cast<int>(0xff800000u) & bad));
+}
+
 // Map a linear workgroup id so that the workgroups one XCD runs (the
 // hardware deals ids round-robin over the 8 XCDs) cover consecutive tiles,
 // which then share key blocks in that XCD's L2.
@@ -236,4 +246,45 @@ __device__ __forceinline__ void token_qfeat(const AttnArgs& a, int64_t hT, int64
   split8(f, hi, lo);
 }
 
+
+// ---- one 64-key tile staged in LDS (q-major passes: forward, dQ) -----------
+// Filled by global_load_lds; two buffers alternate so the copies of tile j+1
+// run under the MFMAs of tile j.
+template <int MODE>
+struct alignas(16) KvTile {
+  uint16_t k[64 * 128];                      // K rows, swizzled (swz_off)
+  uint16_t v[64 * 128];                      // V rows, swizzled
+  int docs[64];                              // document id per key
+  float tab[16];                             // block mode: table row of distance qb - kb
+  uint16_t f[MODE >= 2 ? 64 * kTokRow : 8];  // token modes: key features [64][32] (swz32_off)
+};
+
+constexpr int kListLds = 1024;  // kv-list entries staged in LDS (longer lists read the rest from memory)
+
+// Issue the copies of keys kv0 .. kv0+63 (and the block-table row rdist) into
+// b; NT threads (128, 256 or 512) take part.
+template <int MODE, int NT>
+__device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, int rdist, KvTile<MODE>& b, int tid) {
+  static_assert(NT == 128 || NT == 256 || NT == 512, "kv_issue: 128, 256 or 512 threads");
+  const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+  for (int jj = 0; jj < 1024 / NT; ++jj) {
+    // 16-byte chunk idx sits at LDS byte 16·idx: row idx/16, physical chunk
+    // idx%16, which holds the logical chunk (idx%16) ^ swz(row)
+    const int idx = jj * NT + tid;
+    const int r = idx >> 4, c = (idx & 15) ^ swz(r);
+    g2lds16(a.k + h * a.k_sh + (kv0 + r) * a.k_st + c * 8, b.k + (idx - lane) * 8);
+    g2lds16(a.v + h * a.v_sh + (kv0 + r) * a.v_st + c * 8, b.v + (idx - lane) * 8);
+  }
+  if (wave == 0 && lane < 16) g2lds16(a.docs + kv0 + lane * 4, b.docs);
+  if (MODE == 1 && wave == 1 && lane < 4)
+    g2lds16(static_cast<const float*>(a.table) + static_cast<int64_t>(rdist) * 16 + lane * 4, b.tab);
+  if (MODE >= 2) {
+#pragma unroll
+    for (int idx = tid; idx < 256; idx += NT) {
+      const int r = idx >> 2, c = (idx & 3) ^ ((r >> 2) & 3);
+      g2lds16(static_cast<const uint16_t*>(a.table) + (kv0 + r) * kTokRow + c * 8, b.f + (idx - lane) * 8);
+    }
+  }
+}
 }  // namespace scope

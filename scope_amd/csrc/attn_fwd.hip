@@ -6,23 +6,27 @@
 //
 // One workgroup per (head, q-block) of BS rows (BS = block size, 128 or 256),
 // one wavefront per 32 query rows.  The workgroup walks only the key blocks of
-// its list, staging each BN-row sub-tile of K (row-major) and V (transposed)
-// in LDS; the next sub-tile's global loads are in flight while the current
-// one is computed.  Scores are kept in the log2 domain (exp2).
+// its list in 64-key tiles.  Each tile (K and V rows, document ids, the block
+// table row or the key features) is copied straight into LDS by
+// global_load_lds, two buffers alternating so that tile j+1 is in flight while
+// tile j is computed.  S^T = K·Q^T reads K rows; O^T += V^T·P^T reads V through
+// transpose loads (ds_read_b64_tr_b16), so no tile is ever rearranged.  Scores
+// are kept in the log2 domain (exp2) and the running maximum is only raised
+// when a row's tile maximum exceeds it by more than 2^kLazy.
 //
-// Bias modes:
+// Bias modes (template MODE):
 //   0 none
 //   1 block offsets: β Σ_k A_k(i) cos(ω_k r) + B_k(i) sin(ω_k r), r = qb - kb,
 //     a per-(row, key block) constant folded into the softmax offset
 //   2 token offsets (the reference's score_mod): the band term enters as
 //     extra MFMA k-steps over 16 features (cos/sin(ω_k j) on the key side,
 //     the angle-addition coefficients on the query side), each split into
-//     bf16 hi + lo; -b0 is a row constant; slope·Δ and the softplus/relu gate
-//     are evaluated per element.
+//     bf16 hi + lo; -b0 is a row constant; slope·Δ is evaluated per element
+//   3 as 2 with the softplus/relu gate on |Δ - Δmain| - width
 //
-// Masking: a sub-tile is unmasked when it ends at or before the wave's first
-// row and no document starts between its first key and the block's last
-// token; sub-tiles entirely after the wave's rows are skipped; the rest apply
+// Masking: a tile is unmasked when it ends at or before the wave's first row
+// and no document starts between its first key and the block's last token;
+// tiles entirely after the wave's rows are skipped; the rest apply
 // kv <= q && docs[kv] == docs[q] per element.
 #include <math.h>
 #include <stdlib.h>
@@ -31,287 +35,242 @@
 
 namespace scope {
 
-template <int BS, int BN, int MODE>
+constexpr float kLazy = 8.f;  // log2 headroom before the running maximum is raised
+
+// per-row state of the forward (one query row per lane pair l, l^32)
+struct FwdRow {
+  float rowc, slp, dm, wd;
+  int row, doc;
+};
+
+// Bias and mask terms of one tile's scores in place: on return s holds the
+// log2-domain score minus the row offset (x·scale·log2e + per-element terms),
+// -inf where masked.
+template <int MODE, bool MASK>
+__device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>& b, const FwdRow& R, int kv0,
+                                           int lane, f32x16_t (&s)[2]) {
+  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
+  const int g = lane >> 5;
+  const float cs = a.scale_log2;
+  const float glam = a.beta_log2 * a.ramp_lambda;
+  const float spw = a.gate_kind == SCOPE_GATE_SOFTPLUS ? kLn2 : 0.f;
+  const int lim = R.row - kv0;  // keys j <= lim are causal
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int j0 = mb * 32 + 8 * rq + 4 * g;
+      int dcv[4] = {0, 0, 0, 0};
+      if (MASK) {
+        const int4 d4 = *reinterpret_cast<const int4*>(&b.docs[j0]);
+        dcv[0] = d4.x, dcv[1] = d4.y, dcv[2] = d4.z, dcv[3] = d4.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * rq + i, j = j0 + i;
+        float x;
+        if (TOK) {
+          const float df = static_cast<float>(lim - j);
+          float e = R.slp * df;
+          if (GATE) {
+            // softplus(x) = max(x,0) + ln2·log2(1 + 2^(-|x|·log2 e)); relu drops the second term
+            const float xx = (fabsf(df - R.dm) - R.wd) * a.inv_tau;
+            const float sp = __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e));
+            e -= glam * fmaf(spw, sp, fmaxf(xx, 0.f));
+          }
+          x = fmaf(s[mb][r], cs, e);
+        } else {
+          x = s[mb][r] * cs;
+        }
+        if (MASK) x = mask_score(x, j, lim, dcv[i], R.doc);
+        s[mb][r] = x;
+      }
+    }
+}
+
+template <int BS, int MODE>
 __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
   constexpr int NT = 2 * BS;
-  constexpr int D = 128;
-  constexpr int KSTR = D + 8;   // bf16 per K row in LDS   (68 dwords: conflict-free b128 reads)
-  constexpr int VSTR = BN + 4;  // bf16 per V^T row in LDS (conflict-free b64 reads)
-  constexpr int FSTR = 40;      // bf16 per feature row    (20 dwords: conflict-free b128 reads)
+  constexpr int BN = 64;  // keys per staged tile
   constexpr int NSUB = BS / BN;
-  constexpr int MB = BN / 32;
-  constexpr int KCH = BN * 16;             // 16-byte K chunks per sub-tile
-  constexpr int VBL = BN * 4;              // 4x8 V blocks per sub-tile
-  constexpr int KL = (KCH + NT - 1) / NT;  // per thread
-  constexpr int VL = (VBL + NT - 1) / NT;
-  constexpr int FCH = BN * 4;              // 16-byte feature chunks per sub-tile (token mode)
-  constexpr int FL = (FCH + NT - 1) / NT;
+  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Fs[MODE == 2 ? BN * FSTR : 8];
-  __shared__ __attribute__((aligned(16))) int docs_s[BN];
+  __shared__ KvTile<MODE> buf0, buf1;
+  __shared__ int kbs[kListLds];
+  // block mode: β·log2e-scaled coefficient rows of the block's queries, [BS][16] (cos 0..7, sin 8..15)
+  __shared__ __attribute__((aligned(16))) float coef[MODE == 1 ? BS * 16 : 4];
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
   const int h = tile / a.QB, qb = tile % a.QB;
   const int64_t q0 = static_cast<int64_t>(qb) * BS;
-  const int64_t wrow_lo = q0 + wave * 32;
-  const int64_t row = wrow_lo + lr;
+  const int wrow_lo = static_cast<int>(q0) + wave * 32;
   const int64_t hT = static_cast<int64_t>(h) * a.T;
+  FwdRow R;
+  R.row = wrow_lo + lr;
+
+  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
+  const int n = a.kv_num[lrow];
+  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
+  for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
 
   uint4 qreg[8];
   {
-    const uint16_t* qp = a.q + h * a.q_sh + row * a.q_st + g * 8;
+    const uint16_t* qp = a.q + h * a.q_sh + R.row * a.q_st + g * 8;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
   }
 
   // ---- bias set-up (per row)
-  float ca[8], sa[8];
   uint4 qf = make_uint4(0, 0, 0, 0), qfl = make_uint4(0, 0, 0, 0);
-  float rowc = 0.f, slp = 0.f, dm = 0.f, wd = 0.f, glam = 0.f;
+  R.rowc = R.slp = R.dm = R.wd = 0.f;
   if (MODE == 1) {
+    // lane pair (l, l^32) fills the cos (g = 0) or sin (g = 1) half of its row
+    const float* cf = (g == 0 ? a.coeff_cos : a.coeff_sin) + (hT + R.row) * a.K;
+    float* dst = coef + (wave * 32 + lr) * 16 + g * 8;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      ca[k] = k < a.K ? a.coeff_cos[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
-      sa[k] = k < a.K ? a.coeff_sin[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
+    for (int k = 0; k < 8; ++k) dst[k] = k < a.K ? cf[k] * a.beta_log2 : 0.f;
+  }
+  if (TOK) {
+    token_qfeat(a, hT, R.row, g, qf, qfl, nullptr, nullptr);
+    if (a.subtract_b0) R.rowc = -a.beta_log2 * a.b0[hT + R.row];
+    if (a.use_slope) R.slp = a.beta_log2 * a.slope[hT + R.row];
+    if (GATE) {
+      R.dm = a.delta_main[hT + R.row];
+      R.wd = a.width[hT + R.row];
     }
   }
-  if (MODE == 2) {
-    token_qfeat(a, hT, row, g, qf, qfl, nullptr, nullptr);
-    if (a.subtract_b0) rowc = -a.beta_log2 * a.b0[hT + row];
-    if (a.use_slope) slp = a.beta_log2 * a.slope[hT + row];
-    if (a.gate_kind != SCOPE_GATE_NONE) {
-      dm = a.delta_main[hT + row];
-      wd = a.width[hT + row];
-      glam = a.beta_log2 * a.ramp_lambda;
-    }
-  }
-  const bool extra = MODE == 2 && (a.use_slope || (a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f));
-
-  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
-  const int n = a.kv_num[lrow];
-  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
-  const int total = n * NSUB;
   const int ds_end = a.ds_tok_end[qb];
-  const int doc_row = a.docs[row];
-
-  // ---- global -> register prefetch of one sub-tile
-  uint4 kpre[KL];
-  uint4 vpre[VL][4];
-  int dpre = 0;
-  uint4 fpre[FL];
-  auto load = [&](int it) {
-    const int kb = lst[it / NSUB];
-    const int64_t kv0 = static_cast<int64_t>(kb) * BS + (it % NSUB) * BN;
-#pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int idx = tid + i * NT;
-      const int r = idx / 16, c = idx % 16;
-      if (KCH % NT == 0 || idx < KCH)
-        kpre[i] = *reinterpret_cast<const uint4*>(a.k + h * a.k_sh + (kv0 + r) * a.k_st + c * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int idx = tid + i * NT;
-      const int c = idx % 16, kvg = idx / 16;
-      if (VBL % NT == 0 || idx < VBL) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          vpre[i][rr] = *reinterpret_cast<const uint4*>(a.v + h * a.v_sh + (kv0 + kvg * 4 + rr) * a.v_st + c * 8);
-      }
-    }
-    if (tid < BN) dpre = a.docs[kv0 + tid];
-    if (MODE == 2) {
-#pragma unroll
-      for (int i = 0; i < FL; ++i) {
-        const int idx = tid + i * NT;
-        if (FCH % NT == 0 || idx < FCH)
-          fpre[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + (kv0 + idx / 4) * kTokRow +
-                                                    (idx % 4) * 8);
-      }
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int idx = tid + i * NT;
-      const int r = idx / 16, c = idx % 16;
-      if (KCH % NT == 0 || idx < KCH) *reinterpret_cast<uint4*>(&Ks[r * KSTR + c * 8]) = kpre[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int idx = tid + i * NT;
-      const int c = idx % 16, kvg = idx / 16;
-      if (!(VBL % NT == 0 || idx < VBL)) continue;
-      const uint32_t w0[4] = {vpre[i][0].x, vpre[i][0].y, vpre[i][0].z, vpre[i][0].w};
-      const uint32_t w1[4] = {vpre[i][1].x, vpre[i][1].y, vpre[i][1].z, vpre[i][1].w};
-      const uint32_t w2[4] = {vpre[i][2].x, vpre[i][2].y, vpre[i][2].z, vpre[i][2].w};
-      const uint32_t w3[4] = {vpre[i][3].x, vpre[i][3].y, vpre[i][3].z, vpre[i][3].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int w = e / 2;
-        uint2 val;
-        if (e & 1) {
-          val.x = pack_hi16(w0[w], w1[w]);
-          val.y = pack_hi16(w2[w], w3[w]);
-        } else {
-          val.x = pack_lo16(w0[w], w1[w]);
-          val.y = pack_lo16(w2[w], w3[w]);
-        }
-        *reinterpret_cast<uint2*>(&Vt[(c * 8 + e) * VSTR + kvg * 4]) = val;
-      }
-    }
-    if (tid < BN) docs_s[tid] = dpre;
-    if (MODE == 2) {
-#pragma unroll
-      for (int i = 0; i < FL; ++i) {
-        const int idx = tid + i * NT;
-        if (FCH % NT == 0 || idx < FCH) *reinterpret_cast<uint4*>(&Fs[(idx / 4) * FSTR + (idx % 4) * 8]) = fpre[i];
-      }
-    }
-  };
+  R.doc = a.docs[R.row];
 
   f32x16_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
-  float bt = 0.f;
-  const float cs = a.scale_log2;
 
-  if (total > 0) load(0);
-  for (int it = 0; it < total; ++it) {
-    __syncthreads();
-    store();
-    __syncthreads();
-    if (it + 1 < total) load(it + 1);
-
-    const int t = it / NSUB, st = it % NSUB;
-    const int kb = lst[t];
-    const int64_t kv0 = static_cast<int64_t>(kb) * BS + st * BN;
-    if (kv0 > wrow_lo + 31) continue;  // every key after every row of this wave
+  // flat iteration index it = list entry · NSUB + key tile; tiles that start
+  // after the block's last row are skipped
+  const int total = n * NSUB;
+  const int qmax = static_cast<int>(q0) + BS - 1;
+  auto kb_at = [&](int t) { return t < kListLds ? kbs[t] : lst[t]; };
+  auto next_valid = [&](int it) {
+    while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
+    return it;
+  };
+  auto issue = [&](int it, KvTile<MODE>& b) {
+    const int kb = kb_at(it / NSUB);
+    const int rd = min(max(qb - kb, 0), a.QB - 1);
+    kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
+  };
+  auto run = [&](int it, const KvTile<MODE>& b) {
+    const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
+    if (kv0 > wrow_lo + 31) return;  // every key follows this wavefront's rows
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
-
-    if (MODE == 1 && st == 0) {
-      const float* tr = static_cast<const float*>(a.table) + static_cast<int64_t>(qb - kb) * 16;
+    float tconst = R.rowc;
+    if (MODE == 1) {
+      const float4* cr = reinterpret_cast<const float4*>(coef + (wave * 32 + lr) * 16);
+      const float4* tr = reinterpret_cast<const float4*>(b.tab);
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc += ca[k] * tr[k] + sa[k] * tr[8 + k];
-      bt = acc;
+      for (int i = 0; i < 4; ++i) {
+        const float4 c4 = cr[i], t4 = tr[i];
+        acc += c4.x * t4.x + c4.y * t4.y + c4.z * t4.z + c4.w * t4.w;
+      }
+      tconst = acc;
     }
-    const float tconst = MODE == 1 ? bt : rowc;
-
-    // S^T = K Q^T  (+ token features)
-    f32x16_t s[MB];
+    // S^T = K Q^T (+ token features): keys in two 32-row blocks, this lane's row as the column
+    f32x16_t s[2];
+    s[0] = zero16();
+    s[1] = zero16();
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      s[mb] = zero16();
-      const uint16_t* kr = &Ks[(mb * 32 + lr) * KSTR + g * 8];
+    for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) s[mb] = mfma32(*reinterpret_cast<const uint4*>(kr + ks * 16), qreg[ks], s[mb]);
-      if (MODE == 2) {
-        const uint4 fh = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + g * 8]);
-        const uint4 fl = *reinterpret_cast<const uint4*>(&Fs[(mb * 32 + lr) * FSTR + 16 + g * 8]);
+      for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32(lds_row8(b.k, mb * 32 + lr, ks * 16 + g * 8), qreg[ks], s[mb]);
+    if (TOK) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const uint4 fh = lds_row8_32(b.f, mb * 32 + lr, g * 8);
+        const uint4 fl = lds_row8_32(b.f, mb * 32 + lr, 16 + g * 8);
         s[mb] = mfma32(fh, qf, s[mb]);
         s[mb] = mfma32(fh, qfl, s[mb]);
         s[mb] = mfma32(fl, qf, s[mb]);
       }
     }
+    if (TOK || !full)
+      fwd_scores<MODE, true>(a, b, R, kv0, lane, s);
+    else
+      fwd_scores<MODE, false>(a, b, R, kv0, lane, s);
 
-    if (!full) {
-      // branch-free: per-element control flow around accumulator updates
-      // is both slow and fragile, so read the documents unconditionally and
-      // select
-      const int lim = static_cast<int>(row - kv0);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int j0 = mb * 32 + 8 * rq + 4 * g;
-          const int4 d4 = *reinterpret_cast<const int4*>(&docs_s[j0]);
-          const int dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool ok = (j0 + i <= lim) & (dv[i] == doc_row);
-            s[mb][4 * rq + i] = ok ? s[mb][4 * rq + i] : -INFINITY;
-          }
-        }
-    }
-    if (extra) {
-      const int dbase = static_cast<int>(row - kv0);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-          const float df = static_cast<float>(dbase - j);
-          float e = slp * df;
-          if (a.gate_kind != SCOPE_GATE_NONE) {
-            const float x = (fabsf(df - dm) - wd) * a.inv_tau;
-            const float gt = a.gate_kind == SCOPE_GATE_SOFTPLUS ? fmaxf(x, 0.f) + log1pf(__expf(-fabsf(x)))
-                                                                : fmaxf(x, 0.f);
-            e -= glam * gt;
-          }
-          s[mb][r] = fmaf(s[mb][r], cs, e);
-        }
-    }
-
+    // online softmax (log2 domain); the running maximum moves only by more than kLazy
     float mx = -INFINITY;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_t = (extra ? mx : mx * cs) + tconst;
-    const float m_new = fmaxf(m_run, m_t);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    const float off = tconst - m_use;
+    const float m_t = mx + tconst;
+    const bool raise = m_t > m_run + kLazy;
+    if (__ballot(raise)) {
+      // rows that do not raise keep alpha = 1 (their m_run may still be -inf,
+      // where exp2(m_run - m_run) would be NaN); raised rows from -inf get 0
+      const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_t) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      m_run = raise ? m_t : m_run;
+    }
+    const float off = m_run == -INFINITY ? -INFINITY : tconst - m_run;
 
-    uint4 pb[2 * MB];
+    uint4 pb[4];
     float psum = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         float p[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float x = s[mb][hf * 8 + j];
-          p[j] = exp2f(extra ? x + off : fmaf(x, cs, off));
+          p[j] = __builtin_amdgcn_exp2f(s[mb][hf * 8 + j] + off);
           psum += p[j];
         }
         pb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
                                      cvt_pk_bf16(p[6], p[7]));
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    if (__ballot(alpha != 1.f)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-    }
+    l_run += psum;
 
     // O^T += V^T P^T
 #pragma unroll
-    for (int md = 0; md < 4; ++md) {
-      const uint16_t* vr = &Vt[(md * 32 + lr) * VSTR + 4 * g];
+    for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-      for (int s2 = 0; s2 < 2 * MB; ++s2) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr + 16 * s2);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16 * s2 + 8);
-        o[md] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pb[s2], o[md]);
-      }
-    }
+      for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor(b.v, 16 * s2, md * 32, lane), pb[s2], o[md]);
+  };
+
+  __syncthreads();  // kbs
+  int cur = next_valid(0);
+  if (cur < total) issue(cur, buf0);
+  while (cur < total) {
+    wait_vm0();
+    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
+    int nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf1);
+    run(cur, buf0);
+    cur = nxt;
+    if (cur >= total) break;
+    wait_vm0();
+    __syncthreads();
+    nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf0);
+    run(cur, buf1);
+    cur = nxt;
   }
 
   // ---- epilogue
   const float l_row = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
-  uint16_t* op = a.out + h * a.o_sh + row * a.o_st + 4 * g;
+  uint16_t* op = a.out + h * a.o_sh + R.row * a.o_st + 4 * g;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
 #pragma unroll
@@ -321,29 +280,20 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
       val.y = cvt_pk_bf16(o[md][4 * rq + 2] * inv, o[md][4 * rq + 3] * inv);
       *reinterpret_cast<uint2*>(op + md * 32 + 8 * rq) = val;
     }
-  if (g == 0) a.lse_out[hT + row] = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
+  if (g == 0) a.lse_out[hT + R.row] = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
 }
 
-template <int BS, int BN>
-static void launch_fwd_bn(const AttnArgs& a, int mode, int grid, hipStream_t s) {
+template <int BS>
+static void launch_fwd(const AttnArgs& a, int mode, int grid, hipStream_t s) {
+  const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
   if (mode == SCOPE_BIAS_BLOCK)
-    hipLaunchKernelGGL((attn_fwd_kernel<BS, BN, 1>), dim3(grid), dim3(2 * BS), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 1>), dim3(grid), dim3(2 * BS), 0, s, a);
+  else if (mode == SCOPE_BIAS_TOKEN && gate)
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 3>), dim3(grid), dim3(2 * BS), 0, s, a);
   else if (mode == SCOPE_BIAS_TOKEN)
-    hipLaunchKernelGGL((attn_fwd_kernel<BS, BN, 2>), dim3(grid), dim3(2 * BS), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 2>), dim3(grid), dim3(2 * BS), 0, s, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<BS, BN, 0>), dim3(grid), dim3(2 * BS), 0, s, a);
-}
-
-// Key sub-tile rows staged per LDS round (64 or 128); SCOPE_FWD_BN overrides
-// the default for tuning sweeps.
-static int fwd_tile_bn(int bs) {
-  static int env = -1;
-  if (env < 0) {
-    const char* e = getenv("SCOPE_FWD_BN");
-    env = e ? atoi(e) : 0;
-  }
-  if (env == 64 || env == 128) return env;
-  return bs == 256 ? 128 : 64;
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 0>), dim3(grid), dim3(2 * BS), 0, s, a);
 }
 
 int validate_attn(const scope_attn_params* p, const void* q, const void* k, const void* v, const int32_t* kv_num,
@@ -439,17 +389,9 @@ extern "C" int scope_attn_fwd(const scope_attn_params* p, const uint16_t* q, con
   a.lse_out = lse;
   const int grid = p->H * a.QB;
   hipStream_t s = as_stream(stream);
-  const int bn = fwd_tile_bn(p->bs);
-  if (p->bs == 256) {
-    if (bn == 64)
-      launch_fwd_bn<256, 64>(a, p->bias_mode, grid, s);
-    else
-      launch_fwd_bn<256, 128>(a, p->bias_mode, grid, s);
-  } else {
-    if (bn == 128)
-      launch_fwd_bn<128, 128>(a, p->bias_mode, grid, s);
-    else
-      launch_fwd_bn<128, 64>(a, p->bias_mode, grid, s);
-  }
+  if (p->bs == 256)
+    launch_fwd<256>(a, p->bias_mode, grid, s);
+  else
+    launch_fwd<128>(a, p->bias_mode, grid, s);
   return check_launch("attn_fwd_kernel");
 }

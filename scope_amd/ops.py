@@ -298,9 +298,10 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
              ramp_lambda=0.0, tau=64.0, need_coeff_grads: bool = True, phase_hook=None):
     """Block-sparse attention backward -> dict of gradients.  With
-    ``phase_hook`` the two phases (q-major dQ pass, kv-major dK/dV pass) are
-    launched separately and the hook is called before, between and after
-    them with the phase name ("dq", "dkv", "end") (used for per-kernel timing)."""
+    ``phase_hook`` the phases (q-major dQ pass; kv-major plan, dK/dV kernel
+    and reduce) are launched separately and the hook is called before, between
+    and after them with the phase name ("dq", "plan", "dkv", "reduce", "end")
+    (used for per-kernel timing)."""
     dev = _gpu("attn_bwd", q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list)
     kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
     m = BIAS_MODES[bias_mode]
@@ -334,8 +335,12 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
     else:
         phase_hook("dq")
         call("scope_attn_bwd_phase", C.byref(prm), 1, *args)
+        phase_hook("plan")
+        call("scope_attn_bwd_phase", C.byref(prm), 4, *args)
         phase_hook("dkv")
-        call("scope_attn_bwd_phase", C.byref(prm), 2, *args)
+        call("scope_attn_bwd_phase", C.byref(prm), 8, *args)
+        phase_hook("reduce")
+        call("scope_attn_bwd_phase", C.byref(prm), 16, *args)
         phase_hook("end")
     return dict(dq=dq, dk=dk, dv=dv, dcoeff_cos=dcc, dcoeff_sin=dcs, db0=db0, dslope=dsl, ddelta_main=ddm,
                 dwidth=dwd)
