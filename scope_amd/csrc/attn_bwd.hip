@@ -232,6 +232,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       s[mb] = zero16();
       dpv[mb] = zero16();
     }
+    // four independent accumulator chains interleaved (dependent MFMAs stall)
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
@@ -579,6 +580,7 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
     s[mq] = zero16();
     dp[mq] = zero16();
   }
+  // four independent accumulator chains interleaved (dependent MFMAs stall)
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks)
 #pragma unroll

@@ -43,9 +43,10 @@ struct FwdRow {
   int row, doc;
 };
 
-// Bias and mask terms of one tile's scores in place: on return s holds the
-// log2-domain score minus the row offset (x·scale·log2e + per-element terms),
-// -inf where masked.
+// Bias and mask terms of one tile's scores in place.  Token modes: on return
+// s holds the log2-domain score without the row offset (x·scale·log2e + the
+// per-element terms).  Modes 0 and 1 leave the raw q·k (the scale is applied
+// inside the exponent's FMA) and only mask.  Masked entries are -inf.
 template <int MODE, bool MASK>
 __device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>& b, const FwdRow& R, int kv0,
                                            int lane, f32x16_t (&s)[2]) {
@@ -80,7 +81,7 @@ __device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>
           }
           x = fmaf(s[mb][r], cs, e);
         } else {
-          x = s[mb][r] * cs;
+          x = s[mb][r];
         }
         if (MASK) x = mask_score(x, j, lim, dcv[i], R.doc);
         s[mb][r] = x;
@@ -148,6 +149,7 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
+  float bt = 0.f;  // block mode: β·bias of the current key block (log2 units)
 
   // flat iteration index it = list entry · NSUB + key tile; tiles that start
   // after the block's last row are skipped
@@ -167,8 +169,8 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (kv0 > wrow_lo + 31) return;  // every key follows this wavefront's rows
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
-    float tconst = R.rowc;
-    if (MODE == 1) {
+    if (MODE == 1 && it % NSUB == 0) {
+      // block term of this key block (a key block's first tile is never skipped)
       const float4* cr = reinterpret_cast<const float4*>(coef + (wave * 32 + lr) * 16);
       const float4* tr = reinterpret_cast<const float4*>(b.tab);
       float acc = 0.f;
@@ -177,8 +179,9 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
         const float4 c4 = cr[i], t4 = tr[i];
         acc += c4.x * t4.x + c4.y * t4.y + c4.z * t4.z + c4.w * t4.w;
       }
-      tconst = acc;
+      bt = acc;
     }
+    const float tconst = MODE == 1 ? bt : R.rowc;
     // S^T = K Q^T (+ token features): keys in two 32-row blocks, this lane's row as the column
     f32x16_t s[2];
     s[0] = zero16();
@@ -197,10 +200,9 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
         s[mb] = mfma32(fl, qf, s[mb]);
       }
     }
-    if (TOK || !full)
-      fwd_scores<MODE, true>(a, b, R, kv0, lane, s);
-    else
-      fwd_scores<MODE, false>(a, b, R, kv0, lane, s);
+    if (TOK || !full) fwd_scores<MODE, true>(a, b, R, kv0, lane, s);
+    // exponent = s·csm + off: modes 0/1 keep raw scores (csm = scale·log2e > 0)
+    const float csm = TOK ? 1.f : a.scale_log2;
 
     // online softmax (log2 domain); the running maximum moves only by more than kLazy
     float mx = -INFINITY;
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_t = mx + tconst;
+    const float m_t = mx * csm + tconst;
     const bool raise = m_t > m_run + kLazy;
     if (__ballot(raise)) {
       // rows that do not raise keep alpha = 1 (their m_run may still be -inf,
@@ -233,7 +235,7 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
         float p[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(s[mb][hf * 8 + j] + off);
+          p[j] = __builtin_amdgcn_exp2f(fmaf(s[mb][hf * 8 + j], csm, off));
           psum += p[j];
         }
         pb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
@@ -314,6 +316,8 @@ int validate_attn(const scope_attn_params* p, const void* q, const void* k, cons
   SCOPE_REQUIRE(al16(q) && al16(k) && al16(v) && al16(docs) && al16(cc) && al16(cs) && al16(b0) && al16(slope) &&
                     al16(dm) && al16(wd) && al16(table),
                 "%s: tensors must start on a 16-byte boundary", who);
+  SCOPE_REQUIRE(p->scale > 0.f && p->scale < 1e30f, "%s: scale must be positive and finite (got %g)", who,
+                static_cast<double>(p->scale));
   SCOPE_REQUIRE(p->bias_mode >= 0 && p->bias_mode <= 2, "%s: bias_mode %d", who, p->bias_mode);
   if (p->bias_mode != SCOPE_BIAS_NONE) {
     SCOPE_REQUIRE(p->K >= 1 && p->K <= 8, "%s: K=%d outside [1, 8]", who, p->K);
