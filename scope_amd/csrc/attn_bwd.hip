@@ -433,51 +433,76 @@ struct alignas(16) DkvBuf {
   float rc[MODE >= 2 ? 256 : 4];   // token: slope | delta_main | width
 };
 
-// Issue the copies of the 64-row query tile starting at token q0 into b.
+// Issue part `part` (0..9) of the copies of the 64-row query tile starting at
+// token q0 into b: 0-3 Q rows, 4-7 dO rows, 8 per-row constants, 9 block
+// coefficients or token features.  The parts are spread over the MFMAs of the
+// current tile, so that no wavefront stalls on a burst of memory instructions.
 template <int MODE>
-__device__ __forceinline__ void dkv_issue(const AttnArgs& a, int h, int64_t hT, int64_t q0, DkvBuf<MODE>& b, int tid) {
-  const int wave = tid >> 6, lane = tid & 63;
-  {
+__device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t hT, int64_t q0v, DkvBuf<MODE>& b,
+                                               int tid, int part) {
+  // q0 and the wavefront index are the same in every lane: keep them, and
+  // every row base below, in scalar registers (global_load_lds with a scalar
+  // base and a 32-bit lane byte offset)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int64_t q0 = __builtin_amdgcn_readfirstlane(static_cast<int>(q0v));
+  if (part < 8) {
     // chunk jj·256 + tid: row jj·16 + tid/16, physical chunk tid%16 (holds logical chunk p ^ swz(row))
-    const int r = tid >> 4, c = (tid & 15) ^ swz(r);
-    const uint16_t* qp = a.q + h * a.q_sh + (q0 + r) * a.q_st + c * 8;
-    const uint16_t* dp = a.dout + h * a.o_sh + (q0 + r) * a.o_st + c * 8;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      g2lds16(qp + jj * 16 * a.q_st, b.q + (jj * 256 + wave * 64) * 8);
-      g2lds16(dp + jj * 16 * a.o_st, b.d + (jj * 256 + wave * 64) * 8);
+    const int jj = part & 3;
+    const int r = (tid >> 4) + jj * 16, c = (tid & 15) ^ swz(r);
+    if (part < 4) {
+      const char* base = reinterpret_cast<const char*>(a.q + h * a.q_sh + q0 * a.q_st);
+      g2lds16(base + static_cast<uint32_t>((r * static_cast<int>(a.q_st) + c * 8) * 2), b.q + (jj * 256 + wave * 64) * 8);
+    } else {
+      const char* base = reinterpret_cast<const char*>(a.dout + h * a.o_sh + q0 * a.o_st);
+      g2lds16(base + static_cast<uint32_t>((r * static_cast<int>(a.o_st) + c * 8) * 2), b.d + (jj * 256 + wave * 64) * 8);
     }
+    return;
   }
-  const int arr = lane >> 4, ch = (lane & 15) * 4;
-  if (wave == 0) {
-    const void* src = arr == 0   ? static_cast<const void*>(a.lse + hT + q0 + ch)
-                      : arr == 1 ? static_cast<const void*>(a.delta + hT + q0 + ch)
-                      : arr == 2 ? static_cast<const void*>(a.docs + q0 + ch)
-                                 : static_cast<const void*>(a.b0 + hT + q0 + ch);
-    if (arr < 3 || (MODE >= 2 && a.subtract_b0)) g2lds16(src, b.ra);
+  const uint32_t lo = static_cast<uint32_t>(lane) * 16;  // 16 lanes x 16 bytes = one 64-row float array
+  if (part == 8) {
+    // wavefront w copies per-row array w: lse, Δ, document ids, b0
+    const char* base = wave == 0   ? reinterpret_cast<const char*>(a.lse + hT + q0)
+                       : wave == 1 ? reinterpret_cast<const char*>(a.delta + hT + q0)
+                       : wave == 2 ? reinterpret_cast<const char*>(a.docs + q0)
+                                   : reinterpret_cast<const char*>(a.b0 + hT + q0);
+    if (lane < 16 && (wave < 3 || (MODE >= 2 && a.subtract_b0))) g2lds16(base + lo, b.ra + wave * 64);
+    if (MODE >= 2) {
+      // token terms: slope, delta_main, width on wavefronts 0, 1, 2
+      const char* tb = wave == 0   ? reinterpret_cast<const char*>(a.slope + hT + q0)
+                       : wave == 1 ? reinterpret_cast<const char*>(a.delta_main + hT + q0)
+                                   : reinterpret_cast<const char*>(a.width + hT + q0);
+      const bool need = wave == 0 ? a.use_slope != 0 : (wave < 3 && MODE == 3);
+      if (lane < 16 && need) g2lds16(tb + lo, b.rc + wave * 64);
+    }
+    return;
   }
   if (MODE == 1) {
-    const int ci = (wave & 1) * 64 + lane;  // 16-byte chunk of the [64][K] coefficient rows
-    const float* src = (wave < 2 ? a.coeff_cos : a.coeff_sin) + (hT + q0) * a.K + ci * 4;
-    if (ci < 16 * a.K) g2lds16(src, b.rb + (wave >> 1) * 512 + (wave & 1) * 256);
+    // [64][K] cos rows on wavefronts 0-1, sin rows on 2-3
+    const int ci = (wave & 1) * 64 + lane;
+    const char* base = reinterpret_cast<const char*>((wave < 2 ? a.coeff_cos : a.coeff_sin) + (hT + q0) * a.K);
+    if (ci < 16 * a.K) g2lds16(base + static_cast<uint32_t>(ci) * 16, b.rb + (wave >> 1) * 512 + (wave & 1) * 256);
   }
   if (MODE >= 2) {
     const int r = tid >> 2, c = (tid & 3) ^ ((r >> 2) & 3);
-    g2lds16(a.qfeat + (hT + q0 + r) * kTokRow + c * 8, reinterpret_cast<uint16_t*>(b.rb) + wave * 64 * 8);
-    if (wave == 1) {
-      const float* src = arr == 0 ? a.slope : arr == 1 ? a.delta_main : a.width;
-      if ((arr == 0 && a.use_slope) || ((arr == 1 || arr == 2) && MODE == 3)) g2lds16(src + hT + q0 + ch, b.rc);
-    }
+    const char* base = reinterpret_cast<const char*>(a.qfeat + (hT + q0) * kTokRow);
+    g2lds16(base + static_cast<uint32_t>((r * kTokRow + c * 8) * 2), reinterpret_cast<uint16_t*>(b.rb) + wave * 64 * 8);
   }
 }
 
-// P and dS of one tile as bf16 B operands (k index: the 64 query rows):
-// register quad (mq, rq) of the S / dP accumulators is k-step 2·mq + rq/2,
-// slots 4·(rq%2) .. +3.  MASK applies the causal and document masks.
+template <int MODE>
+__device__ __forceinline__ void dkv_issue(const AttnArgs& a, int h, int64_t hT, int64_t q0, DkvBuf<MODE>& b, int tid) {
+#pragma unroll
+  for (int part = 0; part < 10; ++part) dkv_issue_part<MODE>(a, h, hT, q0, b, tid, part);
+}
+
+// P and dS of register quad (mq, rq) of one tile as bf16 B operands (k index:
+// the 64 query rows): the quad is k-step 2·mq + rq/2, slots 4·(rq%2) .. +3.
+// MASK applies the causal and document masks.
 template <int MODE, bool MASK>
-__device__ __forceinline__ void dkv_probs(const AttnArgs& a, const DkvBuf<MODE>& b, const float* offw, int q0,
-                                          int lane, int wkv, int doc_kv, const f32x16_t (&s)[2],
-                                          const f32x16_t (&dp)[2], uint4 (&pb)[4], uint4 (&dsb)[4]) {
+__device__ __forceinline__ void dkv_probs_quad(const AttnArgs& a, const DkvBuf<MODE>& b, const float* offw, int q0,
+                                               int lane, int wkv, int doc_kv, const f32x16_t (&s)[2],
+                                               const f32x16_t (&dp)[2], uint4 (&pb)[4], uint4 (&dsb)[4], int mq,
+                                               int rq) {
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
   const int g = lane >> 5;
   const int* docq = reinterpret_cast<const int*>(b.ra + 128);
@@ -485,94 +510,96 @@ __device__ __forceinline__ void dkv_probs(const AttnArgs& a, const DkvBuf<MODE>&
   const float glam = a.beta_log2 * a.ramp_lambda;
   const float slsc = TOK && a.use_slope ? a.beta_log2 : 0.f;
   const float spw = a.gate_kind == SCOPE_GATE_SOFTPLUS ? kLn2 : 0.f;
+  const int qi0 = mq * 32 + 8 * rq + 4 * g;  // 4 consecutive query rows of this register quad
+  const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
+  const float4 dl4 = *reinterpret_cast<const float4*>(&b.ra[64 + qi0]);
+  const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
+  const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+  int dcv[4] = {0, 0, 0, 0};
+  if (MASK) {
+    const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
+    dcv[0] = dc4.x;
+    dcv[1] = dc4.y;
+    dcv[2] = dc4.z;
+    dcv[3] = dc4.w;
+  }
+  float pv[4], dsv[4];
 #pragma unroll
-  for (int mq = 0; mq < 2; ++mq)
-#pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      const int qi0 = mq * 32 + 8 * rq + 4 * g;  // 4 consecutive query rows of this register quad
-      const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
-      const float4 dl4 = *reinterpret_cast<const float4*>(&b.ra[64 + qi0]);
-      const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
-      const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
-      int dcv[4] = {0, 0, 0, 0};
-      if (MASK) {
-        const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
-        dcv[0] = dc4.x;
-        dcv[1] = dc4.y;
-        dcv[2] = dc4.z;
-        dcv[3] = dc4.w;
+  for (int i2 = 0; i2 < 4; ++i2) {
+    const int r = 4 * rq + i2;
+    const int q = q0 + qi0 + i2;
+    float xv;
+    if (TOK) {
+      // slope and gate terms; softplus(x) = max(x,0) + ln2·log2(1 + 2^(-|x|·log2 e))
+      const float df = static_cast<float>(q - wkv);
+      float e = slsc * b.rc[qi0 + i2] * df;
+      if (GATE) {
+        const float xx = (fabsf(df - b.rc[64 + qi0 + i2]) - b.rc[128 + qi0 + i2]) * a.inv_tau;
+        const float sp = __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e));
+        e -= glam * fmaf(spw, sp, fmaxf(xx, 0.f));
       }
-      float pv[4], dsv[4];
-#pragma unroll
-      for (int i2 = 0; i2 < 4; ++i2) {
-        const int r = 4 * rq + i2;
-        const int q = q0 + qi0 + i2;
-        float xv;
-        if (TOK) {
-          // slope and gate terms; softplus(x) = max(x,0) + ln2·log2(1 + 2^(-|x|·log2 e))
-          const float df = static_cast<float>(q - wkv);
-          float e = slsc * b.rc[qi0 + i2] * df;
-          if (GATE) {
-            const float xx = (fabsf(df - b.rc[64 + qi0 + i2]) - b.rc[128 + qi0 + i2]) * a.inv_tau;
-            const float sp = __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e));
-            e -= glam * fmaf(spw, sp, fmaxf(xx, 0.f));
-          }
-          xv = fmaf(s[mq][r], cs, e + ofv[i2]);
-        } else {
-          xv = fmaf(s[mq][r], cs, ofv[i2]);
-        }
-        if (MASK) xv = mask_score(xv, wkv, q, doc_kv, dcv[i2]);
-        const float p = __builtin_amdgcn_exp2f(xv);
-        pv[i2] = p;
-        dsv[i2] = p * (dp[mq][r] - dlv[i2]);
-      }
-      const int ksx = 2 * mq + rq / 2;
-      const uint32_t p01 = cvt_pk_bf16(pv[0], pv[1]), p23 = cvt_pk_bf16(pv[2], pv[3]);
-      const uint32_t d01 = cvt_pk_bf16(dsv[0], dsv[1]), d23 = cvt_pk_bf16(dsv[2], dsv[3]);
-      if (rq % 2 == 0) {
-        pb[ksx].x = p01;
-        pb[ksx].y = p23;
-        dsb[ksx].x = d01;
-        dsb[ksx].y = d23;
-      } else {
-        pb[ksx].z = p01;
-        pb[ksx].w = p23;
-        dsb[ksx].z = d01;
-        dsb[ksx].w = d23;
-      }
+      xv = fmaf(s[mq][r], cs, e + ofv[i2]);
+    } else {
+      xv = fmaf(s[mq][r], cs, ofv[i2]);
     }
+    if (MASK) xv = mask_score(xv, wkv, q, doc_kv, dcv[i2]);
+    const float p = __builtin_amdgcn_exp2f(xv);
+    pv[i2] = p;
+    dsv[i2] = p * (dp[mq][r] - dlv[i2]);
+  }
+  const int ksx = 2 * mq + rq / 2;
+  const uint32_t p01 = cvt_pk_bf16(pv[0], pv[1]), p23 = cvt_pk_bf16(pv[2], pv[3]);
+  const uint32_t d01 = cvt_pk_bf16(dsv[0], dsv[1]), d23 = cvt_pk_bf16(dsv[2], dsv[3]);
+  if (rq % 2 == 0) {
+    pb[ksx].x = p01;
+    pb[ksx].y = p23;
+    dsb[ksx].x = d01;
+    dsb[ksx].y = d23;
+  } else {
+    pb[ksx].z = p01;
+    pb[ksx].w = p23;
+    dsb[ksx].z = d01;
+    dsb[ksx].w = d23;
+  }
+}
+
+// Per-row exponent offsets of a tile (lane = row), private to the wavefront.
+template <int MODE>
+__device__ __forceinline__ void dkv_offsets(const AttnArgs& a, const DkvBuf<MODE>& b, float* offw, const float* tab,
+                                            int lane) {
+  const float l = b.ra[lane];
+  float c = 0.f;
+  if (MODE == 1) {
+    if (a.K == 8) {
+      const float4* cr = reinterpret_cast<const float4*>(b.rb + lane * 8);
+      const float4* sr = reinterpret_cast<const float4*>(b.rb + 512 + lane * 8);
+      const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+      c = c0.x * tab[0] + c0.y * tab[1] + c0.z * tab[2] + c0.w * tab[3] + c1.x * tab[4] + c1.y * tab[5] +
+          c1.z * tab[6] + c1.w * tab[7] + s0.x * tab[8] + s0.y * tab[9] + s0.z * tab[10] + s0.w * tab[11] +
+          s1.x * tab[12] + s1.y * tab[13] + s1.z * tab[14] + s1.w * tab[15];
+    } else {
+      for (int k = 0; k < a.K; ++k) c += b.rb[lane * a.K + k] * tab[k] + b.rb[512 + lane * a.K + k] * tab[8 + k];
+    }
+    c *= a.beta_log2;
+  }
+  if (MODE >= 2 && a.subtract_b0) c = -a.beta_log2 * b.ra[192 + lane];
+  offw[lane] = l == -INFINITY ? -INFINITY : c - l * kLog2e;
 }
 
 // One 64-row query tile against this wavefront's 32 keys: S, dP, then
-// dV^T += dO^T·P and dK^T += Q^T·dS.
+// dV^T += dO^T·P and dK^T += Q^T·dS.  (The copies of the next tile are issued
+// by the caller: issued in here, through a reference, the compiler cannot
+// tell the two buffers apart and waits for every copy before the next LDS
+// read.)
 template <int BS, int MODE>
-__device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& b, float* offw, const float* tab,
-                                         int64_t q0, int ds_end, int lane, int64_t wkv_lo, int doc_kv,
+__device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, float* offw,
+                                         const float* tab,
+                                         int64_t q0, int lane, int64_t wkv_lo, int doc_kv,
                                          const uint4 (&kreg)[8], const uint4 (&vreg)[8], const uint4& kf,
                                          const uint4& kfl, f32x16_t (&dvT)[4], f32x16_t (&dkT)[4]) {
   const int g = lane >> 5, lr = lane & 31;
-  const int64_t wkv = wkv_lo + lr;
-  // per-row exponent offsets of this tile (lane = row), private to the wavefront
-  {
-    const float l = b.ra[lane];
-    float c = 0.f;
-    if (MODE == 1) {
-      if (a.K == 8) {
-        const float4* cr = reinterpret_cast<const float4*>(b.rb + lane * 8);
-        const float4* sr = reinterpret_cast<const float4*>(b.rb + 512 + lane * 8);
-        const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
-        c = c0.x * tab[0] + c0.y * tab[1] + c0.z * tab[2] + c0.w * tab[3] + c1.x * tab[4] + c1.y * tab[5] +
-            c1.z * tab[6] + c1.w * tab[7] + s0.x * tab[8] + s0.y * tab[9] + s0.z * tab[10] + s0.w * tab[11] +
-            s1.x * tab[12] + s1.y * tab[13] + s1.z * tab[14] + s1.w * tab[15];
-      } else {
-        for (int k = 0; k < a.K; ++k) c += b.rb[lane * a.K + k] * tab[k] + b.rb[512 + lane * a.K + k] * tab[8 + k];
-      }
-      c *= a.beta_log2;
-    }
-    if (MODE >= 2 && a.subtract_b0) c = -a.beta_log2 * b.ra[192 + lane];
-    offw[lane] = l == -INFINITY ? -INFINITY : c - l * kLog2e;
-  }
-  const bool full = (wkv_lo + 31 <= q0) && (ds_end <= wkv_lo);
+  const int wkv = static_cast<int>(wkv_lo) + lr;
+  dkv_offsets<MODE>(a, b, offw, tab, lane);
   // S and dP, query rows in two 32-row blocks (A operand), keys as columns (B)
   f32x16_t s[2], dp[2];
 #pragma unroll
@@ -580,14 +607,27 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
     s[mq] = zero16();
     dp[mq] = zero16();
   }
-  // four independent accumulator chains interleaved (dependent MFMAs stall)
+  // four independent accumulator chains; the A operands of k-step ks+1 are
+  // read from LDS while k-step ks runs (the fences stop the compiler from
+  // hoisting every read, which would exhaust the registers)
+  uint4 qa0 = lds_row8(b.q, lr, g * 8), qa1 = lds_row8(b.q, 32 + lr, g * 8);
+  uint4 da0 = lds_row8(b.d, lr, g * 8), da1 = lds_row8(b.d, 32 + lr, g * 8);
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-    for (int mq = 0; mq < 2; ++mq) {
-      s[mq] = mfma32(lds_row8(b.q, mq * 32 + lr, ks * 16 + g * 8), kreg[ks], s[mq]);
-      dp[mq] = mfma32(lds_row8(b.d, mq * 32 + lr, ks * 16 + g * 8), vreg[ks], dp[mq]);
+  for (int ks = 0; ks < 8; ++ks) {
+    uint4 qn0 = qa0, qn1 = qa1, dn0 = da0, dn1 = da1;
+    if (ks < 7) {
+      qn0 = lds_row8(b.q, lr, (ks + 1) * 16 + g * 8);
+      qn1 = lds_row8(b.q, 32 + lr, (ks + 1) * 16 + g * 8);
+      dn0 = lds_row8(b.d, lr, (ks + 1) * 16 + g * 8);
+      dn1 = lds_row8(b.d, 32 + lr, (ks + 1) * 16 + g * 8);
     }
+    s[0] = mfma32(qa0, kreg[ks], s[0]);
+    dp[0] = mfma32(da0, vreg[ks], dp[0]);
+    s[1] = mfma32(qa1, kreg[ks], s[1]);
+    dp[1] = mfma32(da1, vreg[ks], dp[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    qa0 = qn0, qa1 = qn1, da0 = dn0, da1 = dn1;
+  }
   if (MODE >= 2) {
     const uint16_t* qf = reinterpret_cast<const uint16_t*>(b.rb);
 #pragma unroll
@@ -600,18 +640,35 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
     }
   }
   uint4 pb[4], dsb[4];
-  if (MODE >= 2 || !full)  // token modes always take the masked form (one copy of their longer code)
-    dkv_probs<MODE, true>(a, b, offw, static_cast<int>(q0), lane, static_cast<int>(wkv), doc_kv, s, dp, pb, dsb);
-  else
-    dkv_probs<MODE, false>(a, b, offw, static_cast<int>(q0), lane, static_cast<int>(wkv), doc_kv, s, dp, pb, dsb);
-  // dV^T += dO^T P,  dK^T += Q^T dS  (k index: the 64 query rows)
+  if (MODE >= 2 || masked) {  // token modes always take the masked form (one copy of their longer code)
 #pragma unroll
-  for (int s4 = 0; s4 < 4; ++s4)
+    for (int mq = 0; mq < 2; ++mq)
 #pragma unroll
-    for (int md = 0; md < 4; ++md) {
-      dvT[md] = mfma32(lds_kmajor(b.d, 16 * s4, md * 32, lane), pb[s4], dvT[md]);
-      dkT[md] = mfma32(lds_kmajor(b.q, 16 * s4, md * 32, lane), dsb[s4], dkT[md]);
+      for (int rq = 0; rq < 4; ++rq)
+        dkv_probs_quad<MODE, true>(a, b, offw, static_cast<int>(q0), lane, wkv, doc_kv, s, dp, pb, dsb, mq, rq);
+  } else {
+#pragma unroll
+    for (int mq = 0; mq < 2; ++mq)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+        dkv_probs_quad<MODE, false>(a, b, offw, static_cast<int>(q0), lane, wkv, doc_kv, s, dp, pb, dsb, mq, rq);
+  }
+  // dV^T += dO^T P,  dK^T += Q^T dS  (k index: the 64 query rows), operands one step ahead
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 ta = lds_kmajor(b.d, 0, 0, lane), tb = lds_kmajor(b.q, 0, 0, lane);
+#pragma unroll
+  for (int st = 0; st < 16; ++st) {
+    const int s4 = st / 4, md = st % 4;
+    uint4 tna = ta, tnb = tb;
+    if (st < 15) {
+      tna = lds_kmajor(b.d, 16 * ((st + 1) / 4), ((st + 1) % 4) * 32, lane);
+      tnb = lds_kmajor(b.q, 16 * ((st + 1) / 4), ((st + 1) % 4) * 32, lane);
     }
+    dvT[md] = mfma32(ta, pb[s4], dvT[md]);
+    dkT[md] = mfma32(tb, dsb[s4], dkT[md]);
+    __builtin_amdgcn_sched_barrier(0);
+    ta = tna, tb = tnb;
+  }
 }
 
 template <int BS, int MODE>
@@ -719,13 +776,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
           else dkv_issue<MODE>(a, h, hT, qn, buf0, tid);
         }
         const int64_t q0 = tile_q0(jj, e);
+        const float* tab = tabs + (MODE == 1 ? e * 16 : 0);
         if (q0 + BM - 1 >= wkv_lo) {  // else every query row precedes this wavefront's keys
+          const bool masked = !((wkv_lo + 31 <= q0) && (dse[e] <= wkv_lo));
           if (half == 0)
-            dkv_tile<BS, MODE>(a, buf0, offw[wave], tabs + (MODE == 1 ? e * 16 : 0), q0, dse[e], lane, wkv_lo,
-                               doc_kv, kreg, vreg, kf, kfl, dvT, dkT);
+            dkv_tile<BS, MODE>(a, buf0, masked, offw[wave], tab, q0, lane, wkv_lo, doc_kv, kreg, vreg, kf, kfl, dvT,
+                               dkT);
           else
-            dkv_tile<BS, MODE>(a, buf1, offw[wave], tabs + (MODE == 1 ? e * 16 : 0), q0, dse[e], lane, wkv_lo,
-                               doc_kv, kreg, vreg, kf, kfl, dvT, dkT);
+            dkv_tile<BS, MODE>(a, buf1, masked, offw[wave], tab, q0, lane, wkv_lo, doc_kv, kreg, vreg, kf, kfl, dvT,
+                               dkT);
         }
       }
     }
