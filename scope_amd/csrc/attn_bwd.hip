@@ -418,6 +418,7 @@ struct KvPlan {
   float* part_dk;
   float* part_dv;
   int64_t max_slots;  // per head
+  int max_items;      // work items per head (upper bound)
 };
 
 // LDS staging of one 64-row query tile of pass B.  Everything arrives by
@@ -682,9 +683,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunk * 16 : 4];
   __shared__ int qbs[kChunk], dse[kChunk];
 
+  constexpr int P = BS / 128;  // workgroups (128 keys each) per key block
   const int NB = a.QB;
-  const int h = blockIdx.y;
-  const int x = blockIdx.x;
+  // 1-D grid, XCD-aware: the hardware deals workgroup ids round-robin over the
+  // 8 XCDs, so id L runs on XCD L % 8.  Each XCD takes a contiguous range of
+  // (head, item) pairs, and the P parts of one item get consecutive slots on
+  // the same XCD: they read the same query tiles, which then come from its L2.
+  const int L = blockIdx.x;
+  const int per_xcd = gridDim.x / 8 / P;  // items per XCD (the grid is a multiple of 8·P)
+  const int pair = (L / 8) / P, zpart = (L / 8) % P;
+  const int item = (L % 8) * per_xcd + pair;
+  if (item >= a.H * pl.max_items) return;
+  const int h = item / pl.max_items;
+  const int x = item % pl.max_items;
   const int32_t* its = pl.items_start + static_cast<int64_t>(h) * (NB + 1);
   if (x >= its[NB]) return;
   // key block owning item x: largest kb with its[kb] <= x
@@ -705,16 +716,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
-  const int64_t kv0 = static_cast<int64_t>(kb) * BS + blockIdx.z * 128;  // first key row of this workgroup
+  const int64_t kv0 = static_cast<int64_t>(kb) * BS + zpart * 128;  // first key row of this workgroup
   const int64_t wkv_lo = kv0 + wave * 32;
   const int64_t wkv = wkv_lo + lr;
-  const int krow = blockIdx.z * 128 + wave * 32 + lr;  // key row within the block
+  const int krow = zpart * 128 + wave * 32 + lr;  // key row within the block
   const int64_t hT = static_cast<int64_t>(h) * a.T;
 
   // The q-list is ascending, so only its first entry can be the diagonal
   // block; there the query sub-tiles that end before kv0 are skipped.
   const int qb_first = ne > 0 ? ql[i0] : 0;
-  const int skip0 = ne > 0 && qb_first == kb ? (blockIdx.z * 128) / BM : 0;
+  const int skip0 = ne > 0 && qb_first == kb ? (zpart * 128) / BM : 0;
   const int n_it = ne * NS - skip0;
 
   if (tid < ne) {
@@ -885,7 +896,9 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
 template <int BS>
 static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases, int grid_q, int max_items,
                        hipStream_t s) {
-  dim3 gq(grid_q * (BS / 128)), gk(max_items, a.H, BS / 128), gr(a.QB, a.H);
+  constexpr int P = BS / 128;
+  const int per_xcd = (a.H * max_items + 7) / 8;
+  dim3 gq(grid_q * P), gk(8 * per_xcd * P), gr(a.QB, a.H);
   // token mode with an active gate runs the kernels' MODE 3 variant
   const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
   if (phases & SCOPE_BWD_DQ) {
@@ -984,6 +997,7 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   pl.part_dk = reinterpret_cast<float*>(ws + L.part_dk);
   pl.part_dv = reinterpret_cast<float*>(ws + L.part_dv);
   pl.max_slots = L.max_slots;
+  pl.max_items = L.max_items;
   hipStream_t s = as_stream(stream);
   const int grid_q = p->H * a.QB;
   if (p->bs == 256)
