@@ -67,9 +67,17 @@ def make_inputs(H, T, D, bs, seed=0):
     flag[cuts] = 1
     docs = flag.cumsum(0).to(torch.int32)
     NB = T // bs
-    # planted needle: key block kb = 3 × mean query of block qb, ≥ 64 blocks back
-    qb_n = int(torch.randint(min(64, NB - 1), NB, (1,), generator=g))
-    dist = int(torch.randint(min(64, qb_n), qb_n + 1, (1,), generator=g)) if qb_n >= 64 else qb_n
+    # planted needle: key block kb = 3 × mean query of block qb, 64 blocks back
+    # (pointer candidates are document-local, so both sit in the longest
+    # document: qb its last whole block, kb clear of its global blocks; when
+    # the document is shorter than 64 + 4 blocks, as far back as it allows)
+    bd = docs[::bs]  # document of each block's first token
+    starts = [0] + [b for b in range(1, NB) if bd[b] != bd[b - 1]] + [NB]
+    # whole blocks of document i: from its first block whose first token is in it
+    spans = [(starts[i], starts[i + 1] - 1) for i in range(len(starts) - 1)]
+    fb, lb = max(spans, key=lambda sp: sp[1] - sp[0])
+    qb_n = lb - 1  # block lb may hold the next document's first tokens
+    dist = max(4, min(64, qb_n - (fb + 3)))
     kb_n = qb_n - dist
     mq = q[0, :, qb_n * bs:(qb_n + 1) * bs].float().mean(dim=1)
     k[0, :, kb_n * bs:(kb_n + 1) * bs] = (3.0 * mq[:, None, :]).to(torch.bfloat16)
@@ -101,6 +109,8 @@ class Step:
                    for p in self.phases}
         self.acc = {p: 0.0 for p in self.phases}
         self.aux_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        self.means_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        self.means_ms = 0.0
 
     def __call__(self, record=False):
         ops, t, bs = self.ops, self.t, self.bs
@@ -112,7 +122,11 @@ class Step:
 
         mark("pointer", 0)
         ds_ptr, ds_local, ds_tok_end = ops.doc_starts(t["docs"], bs)
+        if record:
+            self.means_ev[0].record()
         qbar, kbar = ops.block_means(t["q"], t["k"], bs)
+        if record:
+            self.means_ev[1].record()
         kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=self.NB, H=self.H,
                                                    window=self.window, n_global=self.n_global, budget=self.budget,
                                                    qbar=qbar, kbar=kbar, temp=1.0,
@@ -163,6 +177,7 @@ class Step:
             self.acc[p] += self.ev[p][0].elapsed_time(self.ev[p][1])
         # the aux span brackets the dK/dV kernel: remove it
         self.acc["attn_bwd_aux"] -= self.aux_ev[0].elapsed_time(self.aux_ev[1])
+        self.means_ms += self.means_ev[0].elapsed_time(self.means_ev[1])
 
 
 def time_steps(step, steps, warmup):
@@ -194,6 +209,21 @@ def time_region(step, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps / 1000.0
+
+
+def measured_traffic(kernel: str, H: int, T: int, bs: int, budget: int):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary of
+    this workload (FETCH_SIZE + WRITE_SIZE, each scaled by a calibration copy),
+    or (None, None) when no summary for this exact workload is present."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_T{T}_H{H}_bs{bs}_b{budget}.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as fh:
+        data = json.load(fh)
+    k = data.get("kernels", {}).get(kernel)
+    if not k:
+        return None, None
+    return int(k["bytes"]), os.path.relpath(path, ROOT)
 
 
 def cpu_baseline(inp, step, seconds: float, bs: int):
@@ -270,12 +300,25 @@ def main():
     dom = max(per_kernel, key=lambda p: ph[p])
     flops, kname = per_kernel[dom]
     achieved = flops / (ph[dom] / 1e3) / 1e12
+    traffic, tsrc = measured_traffic(kname, H, T, bs, args.budget)
     roofline = dict(bound="mfma", kernel=kname, achieved=round(achieved, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
-                    frac=round(achieved / PEAK_BF16_TFLOPS, 4), traffic=None,
+                    frac=round(achieved / PEAK_BF16_TFLOPS, 4), traffic=traffic, traffic_source=tsrc,
                     flops_per_launch=flops, launch_ms=round(ph[dom], 4))
+    # the pointer path is HBM-bound: q and k read once (bf16), the document ids,
+    # and the compact lists written (the byte count of the workload definition)
+    maxkv = int(step.last["kv_idx"].shape[-1])
+    ptr_bytes = 2 * H * T * D * 2 + T * 8 + H * (T // bs) * (1 + maxkv) * 4
+    means_ms = step.means_ms / args.steps
+    pointer = dict(bound="hbm", unit="GB/s", peak=PEAK_HBM_GBS, bytes=ptr_bytes,
+                   phase_ms=round(ph["pointer"], 4), phase_achieved=round(ptr_bytes / (ph["pointer"] / 1e3) / 1e9, 1),
+                   phase_frac=round(ptr_bytes / (ph["pointer"] / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                   block_means_ms=round(means_ms, 4),
+                   block_means_achieved=round(2 * H * T * D * 2 / (means_ms / 1e3) / 1e9, 1),
+                   block_means_frac=round(2 * H * T * D * 2 / (means_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4))
     qb_n, kb_n = inp["needle"]
     picks = step.last["picks"]
-    needle_sel = bool((picks[:, qb_n] == kb_n).any().item())
+    needle_sel = dict(q_block=qb_n, key_block=kb_n, distance_blocks=qb_n - kb_n,
+                      selected_heads=int((picks[:, qb_n] == kb_n).any(dim=-1).sum().item()), heads=H)
     res = {
         "metric": METRIC,
         "value": round((F_fwd + F_bwd) / t_step / 1e12, 2),
@@ -301,8 +344,9 @@ def main():
         "attn_bwd_tflops": round(F_bwd / ((ph["attn_bwd_dq"] + ph["attn_bwd_dkv"] + ph["attn_bwd_aux"]) / 1e3) / 1e12,
                                  2),
         "breakdown_ms": {p: round(v_, 4) for p, v_ in ph.items()},
-        "needle_selected": needle_sel,
+        "needle": needle_sel,
         "roofline": roofline,
+        "pointer_roofline": pointer,
     }
     if args.sweep:
         sweep = {}
