@@ -359,6 +359,13 @@ def main():
             sweep[str(b)] = dict(value=round(14.0 * bs * bs * D * na / ts / 1e12, 2), ms_per_step=round(ts * 1e3, 3),
                                  n_act=na)
         res["budget_sweep"] = sweep
+    # measured ceilings next to the vendor figures used as `peak`
+    mp = step.ops.measure_peaks("cuda")
+    res["measured_peaks"] = mp
+    roofline["peak_measured"] = mp["mfma_bf16_tflops"]
+    roofline["frac_of_measured"] = round(achieved / mp["mfma_bf16_tflops"], 4)
+    pointer["peak_measured"] = mp["hbm_copy_gbs"]
+    pointer["block_means_frac_of_measured"] = round(pointer["block_means_achieved"] / mp["hbm_copy_gbs"], 4)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(inp, step, args.cpu_seconds, bs)
     if args.copy_probe_mib > 0:

@@ -66,6 +66,9 @@ _PROTOS = {
     "scope_attn_bwd_workspace_bytes": (c_int64, [C.POINTER(AttnParams)]),
     "scope_attn_bwd": (c_int, [C.POINTER(AttnParams)] + [P] * 30),
     "scope_attn_bwd_phase": (c_int, [C.POINTER(AttnParams), c_int] + [P] * 30),
+    "scope_probe_mfma_flops": (c_int64, [c_int, c_int]),
+    "scope_probe_mfma": (c_int, [P, c_int, c_int, P]),
+    "scope_probe_copy": (c_int, [P, P, c_int64, P]),
 }
 
 _lib = None

@@ -214,17 +214,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     const int rd = min(max(qb - kb, 0), a.QB - 1);
     kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
   };
-  auto run = [&](int it, const KvTile<MODE>& b) {
-    const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
-    if (kv0 > wrow_lo + 31) return;  // every key follows this wavefront's rows
+  // block mode: the bias term and the per-row sums dS, P change per key block
+  // (four 64-key tiles), not per tile
+  float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
+  auto compute = [&](int kv0, const KvTile<MODE>& b) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
-    float tconst = R.rowc;
-    if (MODE == 1) {
-      float acc = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) acc += ca[k] * b.tab[k] + sa[k] * b.tab[8 + k];
-      tconst = acc;
-    }
+    const float tconst = MODE == 1 ? bt : R.rowc;
     // S^T and dP^T: keys in two 32-row blocks (A operand), this lane's query row as the column
     f32x16_t s[2], dpv[2];
 #pragma unroll
@@ -270,17 +265,37 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
         facc_p = mfma32(ft, pbv[s2], facc_p);
       }
     }
-    if (MODE == 1) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        accA[k] += rs * b.tab[k];
-        accB[k] += rs * b.tab[8 + k];
-        accPA[k] += pm * b.tab[k];
-        accPB[k] += pm * b.tab[8 + k];
-      }
-    }
+    rs_kb += rs;
+    pm_kb += pm;
     rs_tot += rs;
     pm_tot += pm;
+  };
+  auto run = [&](int it, int nxt, const KvTile<MODE>& b) {
+    const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
+    if (MODE == 1 && it % NSUB == 0) {
+      // a key block's first tile is never skipped (it starts at or before every row)
+      const float4* t4 = reinterpret_cast<const float4*>(b.tab);
+      const float4 c0 = t4[0], c1 = t4[1], s0 = t4[2], s1 = t4[3];
+      bt = (ca[0] * c0.x + ca[1] * c0.y + ca[2] * c0.z + ca[3] * c0.w) +
+           (ca[4] * c1.x + ca[5] * c1.y + ca[6] * c1.z + ca[7] * c1.w) +
+           (sa[0] * s0.x + sa[1] * s0.y + sa[2] * s0.z + sa[3] * s0.w) +
+           (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
+    }
+    if (kv0 <= wrow_lo + 31) compute(kv0, b);  // else every key follows this wavefront's rows
+    if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
+      // last tile of this key block: fold its sums into the coefficient gradients
+      const float4* t4 = reinterpret_cast<const float4*>(b.tab);
+      const float tb[16] = {t4[0].x, t4[0].y, t4[0].z, t4[0].w, t4[1].x, t4[1].y, t4[1].z, t4[1].w,
+                            t4[2].x, t4[2].y, t4[2].z, t4[2].w, t4[3].x, t4[3].y, t4[3].z, t4[3].w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        accA[k] += rs_kb * tb[k];
+        accB[k] += rs_kb * tb[8 + k];
+        accPA[k] += pm_kb * tb[k];
+        accPB[k] += pm_kb * tb[8 + k];
+      }
+      rs_kb = pm_kb = 0.f;
+    }
   };
 
   __syncthreads();  // kbs
@@ -291,14 +306,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
     int nxt = next_valid(cur + 1);
     if (nxt < total) issue(nxt, buf1);
-    run(cur, buf0);
+    run(cur, nxt, buf0);
     cur = nxt;
     if (cur >= total) break;
     wait_vm0();
     __syncthreads();
     nxt = next_valid(cur + 1);
     if (nxt < total) issue(nxt, buf0);
-    run(cur, buf1);
+    run(cur, nxt, buf1);
     cur = nxt;
   }
 

@@ -266,24 +266,35 @@ constexpr int kListLds = 1024;  // kv-list entries staged in LDS (longer lists r
 template <int MODE, int NT>
 __device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, int rdist, KvTile<MODE>& b, int tid) {
   static_assert(NT == 128 || NT == 256 || NT == 512, "kv_issue: 128, 256 or 512 threads");
-  const int wave = tid >> 6, lane = tid & 63;
+  // kv0, rdist and the wavefront index are the same in every lane: the row
+  // bases live in scalar registers and each lane adds a 32-bit byte offset
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int64_t k0 = __builtin_amdgcn_readfirstlane(static_cast<int>(kv0));
+  const char* kbase = reinterpret_cast<const char*>(a.k + h * a.k_sh + k0 * a.k_st);
+  const char* vbase = reinterpret_cast<const char*>(a.v + h * a.v_sh + k0 * a.v_st);
 #pragma unroll
   for (int jj = 0; jj < 1024 / NT; ++jj) {
     // 16-byte chunk idx sits at LDS byte 16·idx: row idx/16, physical chunk
     // idx%16, which holds the logical chunk (idx%16) ^ swz(row)
     const int idx = jj * NT + tid;
     const int r = idx >> 4, c = (idx & 15) ^ swz(r);
-    g2lds16(a.k + h * a.k_sh + (kv0 + r) * a.k_st + c * 8, b.k + (idx - lane) * 8);
-    g2lds16(a.v + h * a.v_sh + (kv0 + r) * a.v_st + c * 8, b.v + (idx - lane) * 8);
+    g2lds16(kbase + static_cast<uint32_t>((r * static_cast<int>(a.k_st) + c * 8) * 2), b.k + (jj * NT + wave * 64) * 8);
+    g2lds16(vbase + static_cast<uint32_t>((r * static_cast<int>(a.v_st) + c * 8) * 2), b.v + (jj * NT + wave * 64) * 8);
   }
-  if (wave == 0 && lane < 16) g2lds16(a.docs + kv0 + lane * 4, b.docs);
-  if (MODE == 1 && wave == 1 && lane < 4)
-    g2lds16(static_cast<const float*>(a.table) + static_cast<int64_t>(rdist) * 16 + lane * 4, b.tab);
+  if (wave == 0 && lane < 16) g2lds16(reinterpret_cast<const char*>(a.docs + k0) + lane * 16, b.docs);
+  if (MODE == 1 && wave == 1 && lane < 4) {
+    const int rd = __builtin_amdgcn_readfirstlane(rdist);
+    g2lds16(reinterpret_cast<const char*>(static_cast<const float*>(a.table) + static_cast<int64_t>(rd) * 16) + lane * 16,
+            b.tab);
+  }
   if (MODE >= 2) {
+    const char* fbase = reinterpret_cast<const char*>(static_cast<const uint16_t*>(a.table) + k0 * kTokRow);
 #pragma unroll
-    for (int idx = tid; idx < 256; idx += NT) {
+    for (int idx0 = 0; idx0 < 256; idx0 += NT) {
+      const int idx = idx0 + tid;
       const int r = idx >> 2, c = (idx & 3) ^ ((r >> 2) & 3);
-      g2lds16(static_cast<const uint16_t*>(a.table) + (kv0 + r) * kTokRow + c * 8, b.f + (idx - lane) * 8);
+      if (idx < 256)
+        g2lds16(fbase + static_cast<uint32_t>((r * kTokRow + c * 8) * 2), b.f + (idx0 + wave * 64) * 8);
     }
   }
 }

@@ -312,6 +312,9 @@ int validate_attn(const scope_attn_params* p, const void* q, const void* k, cons
   SCOPE_REQUIRE(p->q_st % 8 == 0 && p->k_st % 8 == 0 && p->v_st % 8 == 0 && p->o_st % 8 == 0 &&
                     p->q_sh % 8 == 0 && p->k_sh % 8 == 0 && p->v_sh % 8 == 0 && p->o_sh % 8 == 0,
                 "%s: strides must be multiples of 8 elements (16-byte rows)", who);
+  // tile copies address a 64-row tile with 32-bit byte offsets from its first row
+  SCOPE_REQUIRE(p->q_st < (1 << 24) && p->k_st < (1 << 24) && p->v_st < (1 << 24) && p->o_st < (1 << 24),
+                "%s: token strides must be below 2^24 elements", who);
   auto al16 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
   SCOPE_REQUIRE(al16(q) && al16(k) && al16(v) && al16(docs) && al16(cc) && al16(cs) && al16(b0) && al16(slope) &&
                     al16(dm) && al16(wd) && al16(table),

@@ -348,3 +348,39 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
 
 def log2e() -> float:
     return 1.0 / math.log(2.0)
+
+
+def measure_peaks(device: torch.device | str = "cuda", *, mfma_iters: int = 16384, copy_mib: int = 1024,
+                  repeats: int = 5) -> dict:
+    """Measured ceilings on this GPU: bf16 dense MFMA TFLOP/s (independent
+    32x32x16 chains on every SIMD) and HBM copy GB/s (2 x bytes per copy).
+    The best of `repeats` timed launches is reported."""
+    dev = torch.device(device)
+    _gpu("measure_peaks", torch.empty(1, device=dev))
+    lib = _lib.load()
+    st = _stream(dev)
+    props = torch.cuda.get_device_properties(dev)
+    blocks = props.multi_processor_count * 2  # 8 wavefronts per CU: 2 per SIMD
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    flops = lib.scope_probe_mfma_flops(blocks, mfma_iters)
+    src = torch.ones(copy_mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    nbytes = src.numel() * 4
+
+    def best(fn):
+        fn()
+        ts = []
+        for _ in range(repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize(dev)
+            ts.append(e0.elapsed_time(e1) / 1e3)
+        return min(ts)
+
+    t_mfma = best(lambda: call("scope_probe_mfma", _p(out), blocks, mfma_iters, st))
+    t_copy = best(lambda: call("scope_probe_copy", _p(src), _p(dst), nbytes, st))
+    return dict(mfma_bf16_tflops=round(flops / t_mfma / 1e12, 1), hbm_copy_gbs=round(2 * nbytes / t_copy / 1e9, 1),
+                mfma_probe=f"{blocks} workgroups x 4 wavefronts x 4 chains x {mfma_iters} steps",
+                copy_probe=f"{copy_mib} MiB copy (read + write)")
