@@ -373,6 +373,233 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// pass A, two wavefronts per SIMD (block size 256, no bias or block bias)
+// ---------------------------------------------------------------------------
+// Probabilities and dS^T of one 32-key half (mb) of a tile for this lane's
+// query row: dsb[hf] is k-step 2·mb + hf of dQ^T = K^T·dS^T.
+template <int MODE, bool MASK>
+__device__ __forceinline__ void dq2_probs(const KvTile<MODE>& b, const DqRow& R, int kv0, float off, float cs,
+                                          int lane, int mb, const f32x16_t& s, const f32x16_t& dp, uint4 (&dsb)[2],
+                                          float& rs, float& pm) {
+  const int g = lane >> 5;
+  const int lim = R.row - kv0;  // keys j <= lim are causal
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    float dsv[8];
+    int dcv[8];
+    if (MASK) {
+      const int4 d0 = *reinterpret_cast<const int4*>(&b.docs[mb * 32 + 16 * hf + 4 * g]);
+      const int4 d1 = *reinterpret_cast<const int4*>(&b.docs[mb * 32 + 16 * hf + 8 + 4 * g]);
+      dcv[0] = d0.x, dcv[1] = d0.y, dcv[2] = d0.z, dcv[3] = d0.w;
+      dcv[4] = d1.x, dcv[5] = d1.y, dcv[6] = d1.z, dcv[7] = d1.w;
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int r = hf * 8 + jj;
+      const int j = mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);  // key within the tile
+      float x = fmaf(s[r], cs, off);
+      if (MASK) x = mask_score(x, j, lim, dcv[jj], R.doc);
+      const float p = __builtin_amdgcn_exp2f(x);
+      const float d = p * (dp[r] - R.delta);
+      dsv[jj] = d;
+      rs += d;
+      pm += p;
+    }
+    dsb[hf] = make_uint4(cvt_pk_bf16(dsv[0], dsv[1]), cvt_pk_bf16(dsv[2], dsv[3]), cvt_pk_bf16(dsv[4], dsv[5]),
+                         cvt_pk_bf16(dsv[6], dsv[7]));
+  }
+}
+
+template <int BS, int MODE>
+__global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
+  static_assert(MODE <= 1, "token modes use attn_bwd_dq_kernel");
+  constexpr int NT = 2 * BS;  // BS/32 wavefronts of 32 query rows: the whole q-block
+  constexpr int BN = 64;      // keys per staged tile, processed in two 32-key halves
+  constexpr int NSUB = BS / BN;
+
+  __shared__ KvTile<MODE> buf0, buf1;
+  __shared__ int kbs[kListLds];
+  // block mode: β·log2e-scaled coefficients [BS][cos 8 | sin 8] and the
+  // coefficient-gradient sums [BS][Σrs·cos 8 | Σpm·cos 8 | Σrs·sin 8 | Σpm·sin 8]
+  __shared__ __attribute__((aligned(16))) float coef[MODE == 1 ? BS * 16 : 4];
+  __shared__ __attribute__((aligned(16))) float gacc[MODE == 1 ? BS * 32 : 4];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = tile / a.QB, qb = tile % a.QB;
+  const int64_t q0 = static_cast<int64_t>(qb) * BS;
+  const int wrow_lo = static_cast<int>(q0) + wave * 32;
+  const int64_t hT = static_cast<int64_t>(h) * a.T;
+  const int lrow_ = wave * 32 + lr;  // row within the block
+  DqRow R;
+  R.row = wrow_lo + lr;
+
+  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
+  const int n = a.kv_num[lrow];
+  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
+  for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
+
+  uint4 qreg[8], doreg[8];
+  {
+    const uint16_t* qp = a.q + h * a.q_sh + R.row * a.q_st + g * 8;
+    const uint16_t* op = a.o + h * a.o_sh + R.row * a.o_st + g * 8;
+    const uint16_t* dp = a.dout + h * a.o_sh + R.row * a.o_st + g * 8;
+    float dsum = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
+      doreg[ks] = *reinterpret_cast<const uint4*>(dp + ks * 16);
+      const uint4 ov = *reinterpret_cast<const uint4*>(op + ks * 16);
+      const uint32_t dw[4] = {doreg[ks].x, doreg[ks].y, doreg[ks].z, doreg[ks].w};
+      const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dsum += __uint_as_float(dw[i] << 16) * __uint_as_float(ow[i] << 16);
+        dsum += __uint_as_float(dw[i] & 0xffff0000u) * __uint_as_float(ow[i] & 0xffff0000u);
+      }
+    }
+    R.delta = dsum + __shfl_xor(dsum, 32, 64);
+    if (g == 0) a.delta[hT + R.row] = R.delta;
+  }
+  const float lse_nat = a.lse[hT + R.row];
+  R.lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
+  R.rowc = R.slp = R.dm = R.wd = 0.f;
+  if (MODE == 1) {
+    // lane pair (l, l^32): g = 0 fills the cos half of its row, g = 1 the sin half
+    const float* cf = (g == 0 ? a.coeff_cos : a.coeff_sin) + (hT + R.row) * a.K;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) coef[lrow_ * 16 + g * 8 + k] = k < a.K ? cf[k] * a.beta_log2 : 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) gacc[lrow_ * 32 + g * 16 + k] = 0.f;
+  }
+  const int ds_end = a.ds_tok_end[qb];
+  R.doc = a.docs[R.row];
+  const float cs = a.scale_log2;
+
+  f32x16_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = zero16();
+  float rs_tot = 0.f, pm_tot = 0.f;  // per lane (half the keys of the row) until the epilogue
+  float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
+
+  const int total = n * NSUB;
+  const int qmax = static_cast<int>(q0) + BS - 1;
+  auto kb_at = [&](int t) { return t < kListLds ? kbs[t] : lst[t]; };
+  auto next_valid = [&](int it) {
+    while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
+    return it;
+  };
+  auto issue = [&](int it, KvTile<MODE>& b) {
+    const int kb = kb_at(it / NSUB);
+    const int rd = min(max(qb - kb, 0), a.QB - 1);
+    kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
+  };
+  auto compute = [&](int kv0, const KvTile<MODE>& b) {
+    const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
+    const float off = (MODE == 1 ? bt : 0.f) - R.lse2;
+    float rs = 0.f, pm = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      // S^T and dP^T of keys mb·32 .. +31 (A operand) against this lane's row (B)
+      f32x16_t s = zero16(), dp = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        s = mfma32(lds_row8(b.k, mb * 32 + lr, ks * 16 + g * 8), qreg[ks], s);
+        dp = mfma32(lds_row8(b.v, mb * 32 + lr, ks * 16 + g * 8), doreg[ks], dp);
+      }
+      uint4 dsb[2];
+      if (!full)
+        dq2_probs<MODE, true>(b, R, kv0, off, cs, lane, mb, s, dp, dsb, rs, pm);
+      else
+        dq2_probs<MODE, false>(b, R, kv0, off, cs, lane, mb, s, dp, dsb, rs, pm);
+      // dQ^T += K^T dS^T over these 32 keys
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int md = 0; md < 4; ++md)
+          o[md] = mfma32(lds_kmajor(b.k, 16 * (2 * mb + hf), md * 32, lane), dsb[hf], o[md]);
+    }
+    rs_kb += rs;
+    pm_kb += pm;
+    rs_tot += rs;
+    pm_tot += pm;
+  };
+  auto run = [&](int it, int nxt, const KvTile<MODE>& b) {
+    const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
+    if (MODE == 1 && it % NSUB == 0) {
+      // block term of this key block (its first tile is never skipped)
+      const float4* cr = reinterpret_cast<const float4*>(coef + lrow_ * 16);
+      const float4* t4 = reinterpret_cast<const float4*>(b.tab);
+      float acc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 c4 = cr[i], tt = t4[i];
+        acc[i] = c4.x * tt.x + c4.y * tt.y + c4.z * tt.z + c4.w * tt.w;
+      }
+      bt = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    if (kv0 <= wrow_lo + 31) compute(kv0, b);  // else every key follows this wavefront's rows
+    if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
+      // last tile of this key block: fold the row sums (combined over the lane
+      // pair) into the gradient sums; g = 0 keeps the cos half, g = 1 the sin half
+      const float rsr = rs_kb + __shfl_xor(rs_kb, 32, 64), pmr = pm_kb + __shfl_xor(pm_kb, 32, 64);
+      const float4* t4 = reinterpret_cast<const float4*>(b.tab + g * 8);
+      float4* ga = reinterpret_cast<float4*>(gacc + lrow_ * 32 + g * 16);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float4 tt = t4[i];
+        float4 ar = ga[i], ap = ga[2 + i];
+        ar.x += rsr * tt.x, ar.y += rsr * tt.y, ar.z += rsr * tt.z, ar.w += rsr * tt.w;
+        ap.x += pmr * tt.x, ap.y += pmr * tt.y, ap.z += pmr * tt.z, ap.w += pmr * tt.w;
+        ga[i] = ar;
+        ga[2 + i] = ap;
+      }
+      rs_kb = pm_kb = 0.f;
+    }
+  };
+
+  __syncthreads();  // kbs
+  int cur = next_valid(0);
+  if (cur < total) issue(cur, buf0);
+  while (cur < total) {
+    wait_vm0();
+    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
+    int nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf1);
+    run(cur, nxt, buf0);
+    cur = nxt;
+    if (cur >= total) break;
+    wait_vm0();
+    __syncthreads();
+    nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf0);
+    run(cur, nxt, buf1);
+    cur = nxt;
+  }
+
+  // ---- epilogue: dQ = scale·o, coefficient gradients
+  rs_tot += __shfl_xor(rs_tot, 32, 64);
+  const float dd_err = rs_tot;  // Δ_true - Δ
+  uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
+#pragma unroll
+  for (int md = 0; md < 4; ++md)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      uint2 val;
+      val.x = cvt_pk_bf16(o[md][4 * rq] * a.scale, o[md][4 * rq + 1] * a.scale);
+      val.y = cvt_pk_bf16(o[md][4 * rq + 2] * a.scale, o[md][4 * rq + 3] * a.scale);
+      *reinterpret_cast<uint2*>(dqp + md * 32 + 8 * rq) = val;
+    }
+  if (MODE == 1 && a.dcoeff_cos) {
+    // g = 0 writes the cos coefficients of its row, g = 1 the sin ones
+    const float* ga = gacc + lrow_ * 32 + g * 16;
+    float* dst = (g == 0 ? a.dcoeff_cos : a.dcoeff_sin) + (hT + R.row) * a.K;
+    for (int k = 0; k < a.K; ++k) dst[k] = a.beta * (ga[k] - dd_err * ga[8 + k]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // plan: chunked work items for the kv-major pass
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, const int32_t* __restrict__ q_off,
@@ -916,7 +1143,18 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
   dim3 gq(grid_q * P), gk(8 * per_xcd * P), gr(a.QB, a.H);
   // token mode with an active gate runs the kernels' MODE 3 variant
   const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
-  if (phases & SCOPE_BWD_DQ) {
+  bool dq_done = false;
+  if constexpr (BS == 256) {
+    if ((phases & SCOPE_BWD_DQ) && mode != SCOPE_BIAS_TOKEN) {
+      // one workgroup per q-block, two wavefronts per SIMD
+      if (mode == SCOPE_BIAS_BLOCK)
+        hipLaunchKernelGGL((attn_bwd_dq2_kernel<BS, 1>), dim3(grid_q), dim3(2 * BS), 0, s, a);
+      else
+        hipLaunchKernelGGL((attn_bwd_dq2_kernel<BS, 0>), dim3(grid_q), dim3(2 * BS), 0, s, a);
+      dq_done = true;
+    }
+  }
+  if ((phases & SCOPE_BWD_DQ) && !dq_done) {
     if (mode == SCOPE_BIAS_BLOCK)
       hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 1>), gq, dim3(256), 0, s, a);
     else if (mode == SCOPE_BIAS_TOKEN && gate)
