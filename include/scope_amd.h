@@ -128,6 +128,28 @@ int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, 
                            void* stream);
 
 /* ------------------------------------------------------------------------
+ * Sliding-window block masks of the layers without the pointer mask.
+ * Replaces GPT.create_blockmasks (scoped_medium.py:535-576): the long (W)
+ * and short (W // 2) masks of a window of W blocks.
+ *   counts [6][NB]: n_partial, n_full (dense_to_ordered counts, :562-563),
+ *     then the window-clamped partial / full counts of the long mask
+ *     (:568, :570) and of the short mask (the BlockMask's kv_num_blocks and
+ *     full_kv_num_blocks; a full count is negative for W = 0, like the
+ *     reference's clamp_max(n_full, W - 1)).
+ *   partial_idx, full_idx [NB][NB] (or NULL): the ordered rows of
+ *     dense_to_ordered (:545-548), shared by both masks.
+ *   kv_num_long [NB], kv_idx_long [NB][scope_swa_width(T, bs, W)] and the
+ *     short pair [NB][scope_swa_width(T, bs, W / 2)]: the compact lists the
+ *     attention kernels read (kept full entries, then kept partial entries,
+ *     each descending; the row tail repeats the first entry).
+ * ---------------------------------------------------------------------- */
+/* row width of a compact list: max(1, min(window_blocks, NB + 1)) */
+int scope_swa_width(int64_t T, int bs, int window_blocks);
+int scope_swa_blockmask(const int32_t* docs, int64_t T, int bs, int window_blocks, int32_t* counts,
+                        int32_t* partial_idx, int32_t* full_idx, int32_t* kv_num_long, int32_t* kv_idx_long,
+                        int32_t* kv_num_short, int32_t* kv_idx_short, void* stream);
+
+/* ------------------------------------------------------------------------
  * Fused mask statistics.  Replaces model/attn_bias.py:510-600 (forward debug
  * statistics) and :839-849 (mask debug statistics) and defines the same
  * histograms for the block-scoring mode.  Integer counts go to `counts`

@@ -13,8 +13,8 @@ hand-written HIP kernels behind a C ABI (``include/scope_amd.h``,
 from . import ops
 from ._lib import ScopeLibraryError, load as load_library
 from .attention import SpectralTerms, scope_attention
-from .blockmask import ScopeBlockMask
+from .blockmask import ScopeBlockMask, create_blockmasks
 from .spectral_bias import SpectralBias
 
-__all__ = ["ops", "ScopeLibraryError", "load_library", "SpectralTerms", "scope_attention", "ScopeBlockMask",
+__all__ = ["ops", "ScopeLibraryError", "load_library", "SpectralTerms", "scope_attention", "ScopeBlockMask", "create_blockmasks",
            "SpectralBias"]

@@ -57,6 +57,8 @@ _PROTOS = {
     "scope_pointer_select": (c_int, [C.POINTER(PtrScoreParams), P, P, P, P, P, P, P, P, P, P, P, P]),
     "scope_transpose_workspace_bytes": (c_int64, [c_int, c_int]),
     "scope_transpose_blocks": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P, P, P]),
+    "scope_swa_width": (c_int, [c_int64, c_int, c_int]),
+    "scope_swa_blockmask": (c_int, [P, c_int64, c_int, c_int, P, P, P, P, P, P, P, P]),
     "scope_stats_counts_len": (c_int64, [C.POINTER(StatsParams)]),
     "scope_stats_workspace_bytes": (c_int64, [C.POINTER(StatsParams)]),
     "scope_mask_stats": (c_int, [C.POINTER(StatsParams), P, P, P, P, P, P, P, P, P, P, P, P, P]),

@@ -182,6 +182,35 @@ def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int):
     return q_off, q_list
 
 
+def swa_blockmask(docs: torch.Tensor, bs: int, window_blocks: int, *, export: bool = False) -> dict:
+    """Sliding-window block lists of the long (W) and short (W // 2) masks
+    (scoped_medium.py:535-576) from int document ids [T].
+
+    Returns ``counts`` [6, NB] (n_partial, n_full, then the BlockMask counts
+    kv_num_blocks / full_kv_num_blocks of the long and the short mask),
+    ``long`` / ``short`` = (kv_num [NB], kv_idx [NB, width]) compact lists,
+    and, with ``export``, the ordered rows ``partial_idx`` / ``full_idx``
+    [NB, NB] of dense_to_ordered."""
+    dev = _gpu("swa_blockmask", docs)
+    docs = _i32(docs.reshape(-1))
+    T = docs.numel()
+    if T % bs:
+        raise RuntimeError(f"swa_blockmask: T={T} not a multiple of bs={bs}")
+    NB = T // bs
+    W = int(window_blocks)
+    wl, ws = query("scope_swa_width", T, int(bs), W), query("scope_swa_width", T, int(bs), W // 2)
+    counts = torch.empty((6, NB), dtype=torch.int32, device=dev)
+    pidx = torch.empty((NB, NB), dtype=torch.int32, device=dev) if export else None
+    fidx = torch.empty((NB, NB), dtype=torch.int32, device=dev) if export else None
+    kvl = torch.empty(NB, dtype=torch.int32, device=dev)
+    kil = torch.empty((NB, wl), dtype=torch.int32, device=dev)
+    kvs = torch.empty(NB, dtype=torch.int32, device=dev)
+    kis = torch.empty((NB, ws), dtype=torch.int32, device=dev)
+    call("scope_swa_blockmask", _p(docs), T, int(bs), W, _p(counts), _p(pidx), _p(fidx), _p(kvl), _p(kil), _p(kvs),
+         _p(kis), _stream(dev))
+    return dict(counts=counts, partial_idx=pidx, full_idx=fidx, long=(kvl, kil), short=(kvs, kis))
+
+
 def mask_stats(*, H: int, QB: int, bs: int, M: int = 0, delta_star: torch.Tensor | None = None,
                pi: torch.Tensor | None = None, rep_mode: str = "last", has_docs: bool = False,
                docstart_enabled: bool = False, local_blocks_cfg: int = 1, eps: float = 1e-9,
