@@ -16,6 +16,12 @@ noise, dO ~ N(0,1).
 
 value = active-block TFLOP/s = (F_fwd + F_bwd) / step time, with
 F_fwd = 4·bs²·D·N_act, F_bwd = 10·bs²·D·N_act, N_act = Σ kv_num_blocks.
+
+``--workload swa`` times instead a layer without the pointer mask: the long
+sliding-window mask (scoped_medium.py:535-576, window 14 blocks of 128 = the
+reference's final 1792-token window) built from the document ids, the q-list
+transpose and the attention forward and backward without a bias, at
+T=65536, H=8, D=128 (the training shape).
 """
 from __future__ import annotations
 
@@ -48,6 +54,8 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--workload", choices=["pointer", "swa"], default="pointer")
+    ap.add_argument("--swa-window", type=int, default=14, help="long-mask window in blocks (--workload swa)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, one plain device copy of this many MiB (calibrates HBM byte counters)")
     return ap.parse_args()
@@ -180,6 +188,96 @@ class Step:
         self.means_ms += self.means_ev[0].elapsed_time(self.means_ev[1])
 
 
+class SwaStep:
+    """A layer without the pointer mask: sliding-window lists, transpose,
+    attention forward and backward (no bias)."""
+
+    def __init__(self, inp, *, bs, window):
+        import torch
+
+        from scope_amd import ops
+
+        self.t = {k_: (v_.cuda() if torch.is_tensor(v_) else v_) for k_, v_ in inp.items()}
+        self.bs, self.window, self.ops = bs, window, ops
+        self.H, self.T = self.t["q"].shape[1], self.t["q"].shape[2]
+        self.NB = self.T // bs
+        self.phases = ["swa_mask", "transpose", "attn_fwd", "attn_bwd"]
+        self.ev = {p: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for p in self.phases}
+        self.acc = {p: 0.0 for p in self.phases}
+
+    def __call__(self, record=False):
+        ops, t, bs = self.ops, self.t, self.bs
+
+        def mark(p, i):
+            if record:
+                self.ev[p][i].record()
+
+        mark("swa_mask", 0)
+        r = ops.swa_blockmask(t["docs"], bs, self.window)
+        _, _, ds_tok_end = ops.doc_starts(t["docs"], bs)
+        kv_num = r["long"][0].expand(self.H, -1).contiguous()
+        kv_idx = r["long"][1].expand(self.H, -1, -1).contiguous()
+        mark("swa_mask", 1)
+        mark("transpose", 0)
+        q_off, q_list = ops.transpose_blocks(kv_num, kv_idx, self.NB)
+        mark("transpose", 1)
+        mark("attn_fwd", 0)
+        out, lse = ops.attn_fwd(t["q"], t["k"], t["v"], kv_num, kv_idx, t["docs"], ds_tok_end, bs=bs, scale=0.12,
+                                bias_mode="none")
+        mark("attn_fwd", 1)
+        mark("attn_bwd", 0)
+        grads = ops.attn_bwd(t["q"], t["k"], t["v"], out, t["dout"], lse, kv_num, kv_idx, q_off, q_list, t["docs"],
+                             ds_tok_end, bs=bs, scale=0.12, bias_mode="none")
+        mark("attn_bwd", 1)
+        self.last = dict(kv_num=kv_num, kv_idx=kv_idx, out=out, lse=lse, grads=grads)
+
+    def collect(self):
+        for p in self.phases:
+            self.acc[p] += self.ev[p][0].elapsed_time(self.ev[p][1])
+
+
+def main_swa(args):
+    import torch
+
+    H, T, D, bs = args.H, args.T, 128, args.bs
+    inp = make_inputs(H, T, D, bs)
+    step = SwaStep(inp, bs=bs, window=args.swa_window)
+    step()
+    torch.cuda.synchronize()
+    n_act = int(step.last["kv_num"].sum())
+    F_fwd, F_bwd = 4.0 * bs * bs * D * n_act, 10.0 * bs * bs * D * n_act
+    t_step = time_region(step, args.steps, args.warmup)
+    time_steps(step, args.steps, 0)
+    ph = {p: step.acc[p] / args.steps for p in step.phases}
+    fwd_tf = F_fwd / (ph["attn_fwd"] / 1e3) / 1e12
+    res = {
+        "metric": "SWA attn fwd+bwd active-block TFLOP/s (layer without the pointer mask), 1 MI355X",
+        "value": round((F_fwd + F_bwd) / t_step / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "one attention layer fwd+bwd over the long sliding-window mask (mask build + "
+                               "transpose + attention, no bias)", "B": 1, "H": H, "T": T, "D": D, "block": bs,
+                   "window_blocks": args.swa_window, "docs": max(1, T // 8192)},
+        "tokens_per_s": round(T / t_step, 1),
+        "n_act": n_act,
+        "breakdown_ms": {p: round(v_, 4) for p, v_ in ph.items()},
+        "attn_fwd_tflops": round(fwd_tf, 2),
+        "attn_bwd_tflops": round(F_bwd / (ph["attn_bwd"] / 1e3) / 1e12, 2),
+        "roofline": dict(bound="mfma", kernel="attn_fwd_kernel", achieved=round(fwd_tf, 2), peak=PEAK_BF16_TFLOPS,
+                         unit="TFLOP/s", frac=round(fwd_tf / PEAK_BF16_TFLOPS, 4), traffic=None),
+    }
+    print(json.dumps(res))
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -277,6 +375,11 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.workload == "swa":
+        if args.T == 131072 and args.bs == 256:  # the pointer workload's defaults -> the training shape
+            args.T, args.bs = 65536, 128
+        main_swa(args)
+        return
     H, T, D, bs = args.H, args.T, 128, args.bs
     inp = make_inputs(H, T, D, bs)
     step = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=args.budget)
