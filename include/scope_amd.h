@@ -128,6 +128,51 @@ int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, 
                            void* stream);
 
 /* ------------------------------------------------------------------------
+ * Fused coefficient head.  Replaces the [B,H,L,M,K] mixture of
+ * SpectralBias.forward between the MLP output and the returned terms
+ * (model/attn_bias.py:419-478), its regularisers (:480-506) and, through
+ * autograd, their backward.  The two MLP GEMMs stay with the caller (BLAS).
+ *   y [rows, y_stride] (fp32, or bf16 bits with y_bf16): the MLP output,
+ *     columns delta_raw | mu_raw | sigma_raw | pi_logits | budget_logits
+ *     (M each) | c_raw (with use_slope); rows = B·H·L.
+ *   outputs: coeff_cos, coeff_sin [rows, K]; slope, b0, delta_main, width
+ *     [rows]; delta_star, pi, budget_logits [rows, M] (all fp32).
+ *   reg [6] (training): total, omega, entropy, delta_edge, zero_mean, and
+ *     the mean of b̄ that the backward of zero_mean needs.
+ * The backward writes dy (same dtype and stride as y) from the upstream
+ * gradients of the outputs (each may be NULL = zero) and of reg[0] (g_reg,
+ * a device scalar, or NULL).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int M, K;                      /* peaks (<= 8), bands (<= 16)                        */
+  int64_t rows;                  /* B·H·L                                               */
+  int64_t L;                     /* sequence length                                     */
+  int y_cols, y_stride;          /* 5M + use_slope; elements between rows of y / dy      */
+  int y_bf16;                    /* 1: y and dy are bf16 bits, 0: fp32                  */
+  int use_slope, subtract_b0;
+  int training;                  /* regularisers on                                     */
+  float delta_cap;               /* clamp(_delta_star_max_active, 0, L-1)               */
+  float logw_min, logw_max;      /* log ω bounds of μ                                   */
+  float c_scale, width_min, width_max, eps;
+  float lambda_omega, lambda_entropy, lambda_zero_mean, lambda_delta_edge;
+  float entropy_floor;           /* pi_entropy_floor_frac · log M                       */
+  float delta_edge_eps;          /* _delta_edge_eps_active                              */
+} scope_coeff_params;
+
+int64_t scope_coeff_head_workspace_bytes(const scope_coeff_params* p);
+int scope_coeff_head_fwd(const scope_coeff_params* p, const void* y, const float* omegas /* [K] */,
+                         const float* log_omegas /* [K] */, const float* cos_mean /* [K] or NULL */,
+                         const float* sin_mean /* [K] or NULL */, float* coeff_cos, float* coeff_sin, float* slope,
+                         float* b0, float* delta_star, float* pi, float* budget_logits, float* delta_main,
+                         float* width, float* reg /* [6] or NULL */, void* workspace, void* stream);
+int scope_coeff_head_bwd(const scope_coeff_params* p, const void* y, const float* omegas, const float* log_omegas,
+                         const float* cos_mean, const float* sin_mean, const float* g_coeff_cos,
+                         const float* g_coeff_sin, const float* g_slope, const float* g_b0,
+                         const float* g_delta_star, const float* g_pi, const float* g_budget_logits,
+                         const float* g_delta_main, const float* g_width, const float* g_reg, const float* reg,
+                         void* dy, void* stream);
+
+/* ------------------------------------------------------------------------
  * Sliding-window block masks of the layers without the pointer mask.
  * Replaces GPT.create_blockmasks (scoped_medium.py:535-576): the long (W)
  * and short (W // 2) masks of a window of W blocks.

@@ -46,6 +46,15 @@ class AttnParams(C.Structure):
                 ("v_st", c_int64), ("o_sh", c_int64), ("o_st", c_int64)]
 
 
+class CoeffParams(C.Structure):
+    _fields_ = [("M", c_int), ("K", c_int), ("rows", c_int64), ("L", c_int64), ("y_cols", c_int),
+                ("y_stride", c_int), ("y_bf16", c_int), ("use_slope", c_int), ("subtract_b0", c_int),
+                ("training", c_int), ("delta_cap", c_float), ("logw_min", c_float), ("logw_max", c_float),
+                ("c_scale", c_float), ("width_min", c_float), ("width_max", c_float), ("eps", c_float),
+                ("lambda_omega", c_float), ("lambda_entropy", c_float), ("lambda_zero_mean", c_float),
+                ("lambda_delta_edge", c_float), ("entropy_floor", c_float), ("delta_edge_eps", c_float)]
+
+
 P = c_void_p
 _PROTOS = {
     "scope_abi_version": (c_int, []),
@@ -57,6 +66,9 @@ _PROTOS = {
     "scope_pointer_select": (c_int, [C.POINTER(PtrScoreParams), P, P, P, P, P, P, P, P, P, P, P, P]),
     "scope_transpose_workspace_bytes": (c_int64, [c_int, c_int]),
     "scope_transpose_blocks": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P, P, P]),
+    "scope_coeff_head_workspace_bytes": (c_int64, [C.POINTER(CoeffParams)]),
+    "scope_coeff_head_fwd": (c_int, [C.POINTER(CoeffParams)] + [P] * 17),
+    "scope_coeff_head_bwd": (c_int, [C.POINTER(CoeffParams)] + [P] * 18),
     "scope_swa_width": (c_int, [c_int64, c_int, c_int]),
     "scope_swa_blockmask": (c_int, [P, c_int64, c_int, c_int, P, P, P, P, P, P, P, P]),
     "scope_stats_counts_len": (c_int64, [C.POINTER(StatsParams)]),

@@ -182,6 +182,72 @@ def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int):
     return q_off, q_list
 
 
+def _coeff_prm(y: torch.Tensor, prm: dict):
+    from ._lib import CoeffParams
+
+    Y = y.shape[-1]
+    rows = y.numel() // Y
+    c = CoeffParams(M=int(prm["M"]), K=int(prm["K"]), rows=rows, L=int(prm["L"]), y_cols=Y, y_stride=Y,
+                    y_bf16=int(y.dtype == torch.bfloat16), use_slope=int(bool(prm["use_slope"])),
+                    subtract_b0=int(bool(prm["subtract_b0"])), training=int(bool(prm["training"])),
+                    delta_cap=float(prm["delta_cap"]), logw_min=float(prm["logw_min"]),
+                    logw_max=float(prm["logw_max"]), c_scale=float(prm["c_scale"]),
+                    width_min=float(prm["width_min"]), width_max=float(prm["width_max"]), eps=float(prm["eps"]),
+                    lambda_omega=float(prm["lambda_omega"]), lambda_entropy=float(prm["lambda_entropy"]),
+                    lambda_zero_mean=float(prm["lambda_zero_mean"]),
+                    lambda_delta_edge=float(prm["lambda_delta_edge"]), entropy_floor=float(prm["entropy_floor"]),
+                    delta_edge_eps=float(prm["delta_edge_eps"]))
+    return c, rows
+
+
+def coeff_head_fwd(y: torch.Tensor, prm: dict, omegas: torch.Tensor, log_omegas: torch.Tensor,
+                   cos_mean: torch.Tensor | None, sin_mean: torch.Tensor | None) -> dict:
+    """Fused coefficient head (model/attn_bias.py:419-506) on the MLP output
+    y [..., 5M (+1)] (fp32 or bf16): the nine per-row outputs, shaped like y's
+    leading dimensions, and ``reg`` [6] (total, omega, entropy, delta_edge,
+    zero_mean, mean b̄) when ``prm["training"]``."""
+    dev = _gpu("coeff_head_fwd", y, omegas, log_omegas)
+    if y.dtype not in (torch.float32, torch.bfloat16):
+        y = y.float()
+    y = y.contiguous()
+    c, rows = _coeff_prm(y, prm)
+    lead = tuple(y.shape[:-1])
+    M, K = c.M, c.K
+    f = dict(dtype=torch.float32, device=dev)
+    out = dict(coeff_cos=torch.empty(lead + (K,), **f), coeff_sin=torch.empty(lead + (K,), **f),
+               slope=torch.empty(lead, **f), b0=torch.empty(lead, **f), delta_star=torch.empty(lead + (M,), **f),
+               pi=torch.empty(lead + (M,), **f), budget_logits=torch.empty(lead + (M,), **f),
+               delta_main=torch.empty(lead, **f), width=torch.empty(lead, **f))
+    reg = torch.zeros(6, **f)
+    ws = torch.empty(max(1, int(query("scope_coeff_head_workspace_bytes", C.byref(c)))), dtype=torch.uint8,
+                     device=dev)
+    call("scope_coeff_head_fwd", C.byref(c), _p(y), _p(_f32(omegas)), _p(_f32(log_omegas)), _p(_f32(cos_mean)),
+         _p(_f32(sin_mean)), *(_p(out[n]) for n in ("coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi",
+                                                     "budget_logits", "delta_main", "width")),
+         _p(reg), _p(ws), _stream(dev))
+    out["reg"] = reg
+    return out
+
+
+def coeff_head_bwd(y: torch.Tensor, prm: dict, omegas: torch.Tensor, log_omegas: torch.Tensor,
+                   cos_mean: torch.Tensor | None, sin_mean: torch.Tensor | None, grads: dict,
+                   g_reg: torch.Tensor | None = None, reg: torch.Tensor | None = None) -> torch.Tensor:
+    """dy (y's dtype and shape) from the upstream gradients of the outputs
+    (``grads[name]``, missing = zero) and of reg[0] (``g_reg``)."""
+    dev = _gpu("coeff_head_bwd", y, omegas, log_omegas)
+    if y.dtype not in (torch.float32, torch.bfloat16):
+        y = y.float()
+    y = y.contiguous()
+    c, rows = _coeff_prm(y, prm)
+    dy = torch.empty_like(y)
+    g = [_f32(grads.get(n)) for n in ("coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits",
+                                       "delta_main", "width")]
+    gr = None if g_reg is None else _f32(g_reg.reshape(1))
+    call("scope_coeff_head_bwd", C.byref(c), _p(y), _p(_f32(omegas)), _p(_f32(log_omegas)), _p(_f32(cos_mean)),
+         _p(_f32(sin_mean)), *(_p(x) for x in g), _p(gr), _p(reg), _p(dy), _stream(dev))
+    return dy
+
+
 def swa_blockmask(docs: torch.Tensor, bs: int, window_blocks: int, *, export: bool = False) -> dict:
     """Sliding-window block lists of the long (W) and short (W // 2) masks
     (scoped_medium.py:535-576) from int document ids [T].

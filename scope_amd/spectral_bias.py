@@ -3,8 +3,11 @@ pointer mask, its statistics and the attention running on the gfx950 kernels.
 
 * constructor, configuration checks and schedule setters mirror
   ``model/attn_bias.py:75-377`` (same keyword names, same ValueErrors);
-* ``forward`` is the coefficient head (``:379-478``, torch ops, any device)
-  plus the regularisers (``:480-508``); its debug statistics (``:510-606``)
+* ``forward`` is the coefficient head (``:379-478``) plus the regularisers
+  (``:480-508``).  On the GPU the MLP GEMMs run in torch (BLAS) and
+  everything after them in the fused coefficient-head kernels, forward and
+  backward (``scope_coeff_head_fwd`` / ``_bwd``); CPU tensors take the same
+  steps as the reference's torch ops.  The debug statistics (``:510-606``)
   run in the fused statistics kernel (GPU only) without host syncs;
 * ``build_pointer_blockmask`` (``:623-873``) runs the doc-start and
   reference-mode pointer kernels and returns a ``ScopeBlockMask``;
@@ -120,6 +123,9 @@ class SpectralBias(nn.Module):
         self.register_buffer("omega_sq", omegas.square(), persistent=False)
         self.register_buffer("logw_min", torch.tensor(math.log(w_min), dtype=torch.float32), persistent=False)
         self.register_buffer("logw_max", torch.tensor(math.log(w_max), dtype=torch.float32), persistent=False)
+        # the same fp32 values on the host (kernel arguments without a device read)
+        self._logw = (float(torch.tensor(math.log(w_min), dtype=torch.float32)),
+                      float(torch.tensor(math.log(w_max), dtype=torch.float32)))
         self._trig_cache: dict = {}
 
         # debug statistics buffers (model/attn_bias.py:239-265)
@@ -243,8 +249,26 @@ class SpectralBias(nn.Module):
             self._trig_cache = {key: (c32.to(torch.bfloat16), s32.to(torch.bfloat16), c32.mean(-1), s32.mean(-1))}
         return self._trig_cache[key]
 
+    def _head_params(self, L: int) -> dict:
+        """Scalar arguments of the fused coefficient head (host values only)."""
+        return dict(M=self.M, K=self.K, L=L, use_slope=self.use_slope, subtract_b0=self.subtract_b0,
+                    training=self.training, delta_cap=min(max(float(self._st["dmax"]), 0.0), float(L - 1)),
+                    logw_min=self._logw[0], logw_max=self._logw[1], c_scale=self.c_scale, width_min=self.width_min,
+                    width_max=self.width_max, eps=self.eps, lambda_omega=self.lambda_omega,
+                    lambda_entropy=self.lambda_entropy, lambda_zero_mean=self.lambda_zero_mean,
+                    lambda_delta_edge=self.lambda_delta_edge,
+                    entropy_floor=float(self.pi_entropy_floor_frac) * math.log(self.M),
+                    delta_edge_eps=self._st["edge_eps"])
+
     def forward(self, q: Tensor, *, docs: Tensor | None = None) -> tuple[Tensor, ...]:
-        """q [B,H,L,D] -> the reference's 12-tuple (model/attn_bias.py:385-401)."""
+        """q [B,H,L,D] -> the reference's 12-tuple (model/attn_bias.py:385-401):
+        the fused kernels for GPU tensors, torch ops for CPU tensors."""
+        if q.is_cuda and self.enabled:
+            return self._forward_fused(q, docs)
+        return self._forward_torch(q, docs=docs)
+
+    def _forward_torch(self, q: Tensor, *, docs: Tensor | None = None) -> tuple[Tensor, ...]:
+        """The reference's steps in torch ops (any device)."""
         B, H, L, Dh = q.shape
         if H != self.num_heads:
             raise ValueError(f"expected H={self.num_heads}, got {H}")
@@ -311,6 +335,28 @@ class SpectralBias(nn.Module):
                               ("reg_delta_edge", reg_delta_edge), ("reg_zero_mean", reg_zero_mean),
                               ("reg_total", reg_loss)):
                 getattr(self, "_dbg_" + name).copy_(val.detach())
+        return (coeff_cos, coeff_sin, slope, b0, delta_star, pi, budget_logits, delta_main, width, cos_wD, sin_wD,
+                reg_loss)
+
+    def _forward_fused(self, q: Tensor, docs: Tensor | None) -> tuple[Tensor, ...]:
+        """GPU forward: the MLP in torch, then the fused coefficient head."""
+        B, H, L, Dh = q.shape
+        if H != self.num_heads:
+            raise ValueError(f"expected H={self.num_heads}, got {H}")
+        if Dh != self.head_dim:
+            raise ValueError(f"expected head_dim={self.head_dim}, got {Dh}")
+        cos_wD, sin_wD, cos_mean, sin_mean = self._get_trig_tables(L, q.device)
+        y = self._mlp_forward(q)
+        prm = self._head_params(L)
+        outs = _CoeffHeadFn.apply(y, self.omegas, self.log_omegas, cos_mean, sin_mean, prm)
+        coeff_cos, coeff_sin, slope, b0, delta_star, pi, budget_logits, delta_main, width, reg_all = outs
+        reg_loss = reg_all[0] if self.training else q.new_zeros((), dtype=torch.float32)
+        if self.debug_stats:
+            if B == 1 and L % 128 == 0:
+                self._forward_stats(delta_star.detach(), pi.detach(), docs, L)
+            r = reg_all.detach()
+            for i, name in enumerate(("reg_total", "reg_omega", "reg_entropy", "reg_delta_edge", "reg_zero_mean")):
+                getattr(self, "_dbg_" + name).copy_(r[i] if self.training else torch.zeros_like(r[i]))
         return (coeff_cos, coeff_sin, slope, b0, delta_star, pi, budget_logits, delta_main, width, cos_wD, sin_wD,
                 reg_loss)
 
@@ -451,3 +497,27 @@ class SpectralBias(nn.Module):
                              offset=offset, beta=self.beta, b0=b0, slope=slope, delta_main=delta_main, width=width,
                              use_slope=self.use_slope, subtract_b0=self.subtract_b0, gate_kind=self.gate_kind,
                              ramp_lambda=self.ramp_lambda, tau=self.tau)
+
+
+_HEAD_NAMES = ("coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits", "delta_main", "width")
+
+
+class _CoeffHeadFn(torch.autograd.Function):
+    """MLP output y -> the coefficient head's outputs and regularisers
+    (scope_coeff_head_fwd), with the fused backward (scope_coeff_head_bwd)."""
+
+    @staticmethod
+    def forward(ctx, y, omegas, log_omegas, cos_mean, sin_mean, prm):
+        o = ops.coeff_head_fwd(y, prm, omegas, log_omegas, cos_mean, sin_mean)
+        ctx.save_for_backward(y, omegas, log_omegas, cos_mean, sin_mean, o["reg"])
+        ctx.prm = prm
+        return tuple(o[n] for n in _HEAD_NAMES) + (o["reg"],)
+
+    @staticmethod
+    def backward(ctx, *g):
+        y, omegas, log_omegas, cos_mean, sin_mean, reg = ctx.saved_tensors
+        grads = {n: g[i] for i, n in enumerate(_HEAD_NAMES) if g[i] is not None}
+        g_reg = g[len(_HEAD_NAMES)]
+        g_reg = None if g_reg is None else g_reg[0]
+        dy = ops.coeff_head_bwd(y, ctx.prm, omegas, log_omegas, cos_mean, sin_mean, grads, g_reg, reg)
+        return dy, None, None, None, None, None

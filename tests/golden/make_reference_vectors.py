@@ -16,7 +16,9 @@ What is pinned here, and why an import is needed for it:
 * its debug statistics (``:839-849``) and the forward debug statistics
   (``:510-606``).
 * the coefficient head of ``SpectralBias.forward`` (``:379-478``), used to pin
-  the host-side restatement of the coefficient head.
+  the host-side restatement of the coefficient head and the fused kernel; in
+  training mode also its regularisers (``:480-506``) and the gradients of the
+  head (through autograd) w.r.t. q and the MLP weights.
 
 Usage (build container only)::
 
@@ -213,6 +215,59 @@ def coeff_case(SpectralBias, *, seed: int = 5) -> dict:
     return rec
 
 
+def coeff_train_case(SpectralBias, *, seed: int = 6) -> dict:
+    """Training-mode coefficient head: outputs, reg_loss with every
+    regulariser on and with each one alone, and the gradients w.r.t. q and
+    the MLP weights of (a) Σ_i <out_i, G_i> for random G_i and (b) reg_loss.
+    The lambdas are raised above their defaults so that each term carries
+    weight in the gradient."""
+    gen = torch.Generator().manual_seed(seed)
+    H, T, Dh, M, K = 2, 256, 32, 3, 6
+    lam = dict(lambda_omega=1e-2, lambda_zero_mean=1e-1, lambda_entropy=1e-1, lambda_delta_edge=1e-1)
+    base = dict(head_dim=Dh, num_heads=H, L_train=128, L_max=4096, M=M, K=K, pi_entropy_floor_frac=0.9,
+                delta_edge_eps=0.2)
+    sb = SpectralBias(**base, **lam)
+    with torch.no_grad():
+        for p_ in sb.mlp.parameters():
+            p_.copy_(torch.randn(p_.shape, generator=gen) * 0.3)
+    weights = {n: p_.detach().clone() for n, p_ in sb.mlp.named_parameters()}
+    q0 = torch.randn((1, H, T, Dh), generator=gen, dtype=torch.float32)
+    names = ["coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits", "delta_main", "width"]
+    rec = dict(q=q0[0].numpy(), H=H, T=T, Dh=Dh, M=M, K=K, L_train=128, L_max=4096, pi_entropy_floor_frac=0.9,
+               delta_edge_eps=0.2, omegas=sb.omegas.numpy(), **{k: np.asarray(v) for k, v in lam.items()},
+               w1=weights["0.weight"].numpy(), b1=weights["0.bias"].numpy(), w2=weights["2.weight"].numpy(),
+               b2=weights["2.bias"].numpy())
+
+    def run(lams: dict, tag: str, with_outputs: bool):
+        m = SpectralBias(**base, **lams)
+        with torch.no_grad():
+            for n, p_ in m.mlp.named_parameters():
+                p_.copy_(weights[n])
+        m.train()
+        q = q0.clone().requires_grad_()
+        out = m(q)
+        params = [q] + [p_ for _, p_ in m.mlp.named_parameters()]
+        if with_outputs:
+            for i, n in enumerate(names):
+                rec[n] = out[i][0].detach().numpy()
+            G = [torch.randn(out[i].shape, generator=gen) for i in range(len(names))]
+            rec.update({f"G_{n}": G[i][0].numpy() for i, n in enumerate(names)})
+            lo = sum((out[i] * G[i]).sum() for i in range(len(names)))
+            go = torch.autograd.grad(lo, params, retain_graph=True)
+            rec.update({f"gout_{n}": g_.numpy() for n, g_ in zip(("q", "w1", "b1", "w2", "b2"), go)})
+        reg = out[11]
+        rec[f"reg_{tag}"] = reg.detach().numpy()
+        gr = torch.autograd.grad(reg, params, allow_unused=True)
+        rec.update({f"greg_{tag}_{n}": (np.zeros(p_.shape, np.float32) if g_ is None else g_.numpy())
+                    for n, g_, p_ in zip(("q", "w1", "b1", "w2", "b2"), gr, params)})
+
+    run(lam, "all", True)
+    zero = {k: 0.0 for k in lam}
+    for k in lam:
+        run({**zero, k: lam[k]}, k.replace("lambda_", ""), False)
+    return rec
+
+
 def main() -> None:
     ref_root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     SpectralBias = _load_reference(ref_root)
@@ -272,6 +327,7 @@ def main() -> None:
                         **{f"{c['name']}__{k}": v for c in fcases for k, v in c.items()})
 
     np.savez_compressed(os.path.join(HERE, "coeff_head_vectors.npz"), **coeff_case(SpectralBias))
+    np.savez_compressed(os.path.join(HERE, "coeff_head_train_vectors.npz"), **coeff_train_case(SpectralBias))
     print("wrote", sorted(f for f in os.listdir(HERE) if f.endswith(".npz")))
 
 

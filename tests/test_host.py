@@ -106,3 +106,57 @@ def test_blockmask_export_matches_reference():
         tbm = bm.to_torch_blockmask()
         assert np.array_equal(tbm.q_indices.numpy(), c["q_indices"])
         assert tbm.BLOCK_SIZE == (bs, bs)
+
+
+def _coeff_train_run(g: dict, lams: dict, G=None):
+    """The host coefficient head in training mode on the recorded inputs:
+    (outputs, reg_loss, grads of Σ<out_i, G_i> (if G), grads of reg_loss)."""
+    sb = SpectralBias(head_dim=int(g["Dh"]), num_heads=int(g["H"]), L_train=int(g["L_train"]),
+                      L_max=int(g["L_max"]), M=int(g["M"]), K=int(g["K"]),
+                      pi_entropy_floor_frac=float(g["pi_entropy_floor_frac"]),
+                      delta_edge_eps=float(g["delta_edge_eps"]), **lams)
+    with torch.no_grad():
+        sb.mlp[0].weight.copy_(torch.from_numpy(g["w1"]))
+        sb.mlp[0].bias.copy_(torch.from_numpy(g["b1"]))
+        sb.mlp[2].weight.copy_(torch.from_numpy(g["w2"]))
+        sb.mlp[2].bias.copy_(torch.from_numpy(g["b2"]))
+    sb.train()
+    q = torch.from_numpy(g["q"])[None].clone().requires_grad_()
+    out = sb(q)
+    params = [q, sb.mlp[0].weight, sb.mlp[0].bias, sb.mlp[2].weight, sb.mlp[2].bias]
+    go = None
+    if G is not None:
+        lo = sum((out[i] * G[i]).sum() for i in range(len(G)))
+        go = torch.autograd.grad(lo, params, retain_graph=True)
+    gr = torch.autograd.grad(out[11], params, allow_unused=True)
+    gr = [torch.zeros_like(p_) if x is None else x for x, p_ in zip(gr, params)]
+    return out, out[11], go, gr
+
+
+COEFF_NAMES = ["coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits", "delta_main", "width"]
+PARAM_NAMES = ("q", "w1", "b1", "w2", "b2")
+
+
+def test_coefficient_head_training_regularisers_and_grads_match_reference():
+    g = load_flat("coeff_head_train_vectors.npz")
+    lam = {k: float(g[k]) for k in ("lambda_omega", "lambda_zero_mean", "lambda_entropy", "lambda_delta_edge")}
+    G = [torch.from_numpy(g[f"G_{n}"])[None] for n in COEFF_NAMES]
+    out, reg, go, gr = _coeff_train_run(g, lam, G)
+    for i, n in enumerate(COEFF_NAMES):
+        assert torch.allclose(out[i][0], torch.from_numpy(g[n]), rtol=1e-5, atol=1e-6), n
+    assert np.isclose(reg.item(), g["reg_all"], rtol=1e-5, atol=1e-9)
+    for n, x in zip(PARAM_NAMES, go):
+        ref = torch.from_numpy(g[f"gout_{n}"])
+        assert torch.allclose(x.reshape(ref.shape), ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item()), n
+    for n, x in zip(PARAM_NAMES, gr):
+        ref = torch.from_numpy(g[f"greg_all_{n}"])
+        assert torch.allclose(x.reshape(ref.shape), ref, rtol=1e-4, atol=1e-5 * ref.abs().max().item()), n
+    # each regulariser alone
+    for k in lam:
+        tag = k.replace("lambda_", "")
+        _, reg1, _, gr1 = _coeff_train_run(g, {**{k2: 0.0 for k2 in lam}, k: lam[k]})
+        assert np.isclose(reg1.item(), g[f"reg_{tag}"], rtol=1e-5, atol=1e-9), tag
+        assert abs(float(g[f"reg_{tag}"])) > 0, tag
+        for n, x in zip(PARAM_NAMES, gr1):
+            ref = torch.from_numpy(g[f"greg_{tag}_{n}"])
+            assert torch.allclose(x.reshape(ref.shape), ref, rtol=1e-4, atol=1e-5 * max(ref.abs().max().item(), 1e-30)), (tag, n)
