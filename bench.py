@@ -22,6 +22,11 @@ sliding-window mask (scoped_medium.py:535-576, window 14 blocks of 128 = the
 reference's final 1792-token window) built from the document ids, the q-list
 transpose and the attention forward and backward without a bias, at
 T=65536, H=8, D=128 (the training shape).
+
+``--workload coeff`` times the coefficient head of SpectralBias.forward after
+its MLP (model/attn_bias.py:419-506, M=8 peaks, K=8 bands, regularisers on)
+forward and backward at T=131072, H=8: the fused kernels against the same
+module's torch steps on the same GPU.
 """
 from __future__ import annotations
 
@@ -54,7 +59,7 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["pointer", "swa"], default="pointer")
+    ap.add_argument("--workload", choices=["pointer", "swa", "coeff"], default="pointer")
     ap.add_argument("--swa-window", type=int, default=14, help="long-mask window in blocks (--workload swa)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, one plain device copy of this many MiB (calibrates HBM byte counters)")
@@ -278,6 +283,68 @@ def main_swa(args):
     print(json.dumps(res))
 
 
+def main_coeff(args):
+    import torch
+
+    from scope_amd import SpectralBias, ops
+
+    H, T, M, K = args.H, args.T, 8, 8
+    sb = SpectralBias(head_dim=128, num_heads=H, L_train=T, M=M, K=K).cuda().train()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    Y = 5 * M + 1
+    y = (torch.randn((1, H, T, Y), generator=g, device="cuda") * 2).to(torch.bfloat16)
+    _, _, cm, sm = sb._get_trig_tables(T, y.device)
+    prm = sb._head_params(T)
+    names = ("coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits", "delta_main", "width")
+    o = ops.coeff_head_fwd(y, prm, sb.omegas, sb.log_omegas, cm, sm)
+    grads = {n: torch.randn(o[n].shape, generator=g, device="cuda") for n in names}
+    g_reg = torch.ones((), device="cuda")
+
+    def fused():
+        r = ops.coeff_head_fwd(y, prm, sb.omegas, sb.log_omegas, cm, sm)
+        ops.coeff_head_bwd(y, prm, sb.omegas, sb.log_omegas, cm, sm, grads, g_reg, r["reg"])
+
+    # the reference's steps: torch ops from y (requires grad) to the outputs, then autograd
+    class _Torch:
+        def __call__(self):
+            yy = y.detach().requires_grad_()
+            sb._mlp_forward = lambda q: yy  # the head only: the MLP is the same in both
+            out = sb._forward_torch(torch.empty((1, H, T, 128), device="cuda", dtype=torch.bfloat16))
+            loss = sum((out[i] * grads[n]).sum() for i, n in enumerate(names)) + out[11]
+            loss.backward()
+
+    t_fused = time_region(fused, args.steps, args.warmup)
+    t_torch = time_region(_Torch(), args.steps, args.warmup)
+    rows = H * T
+    # algorithmic bytes: fwd reads y (bf16) and writes the outputs (fp32); bwd reads y and the
+    # upstream gradients of the outputs and writes dy (bf16)
+    out_b = (2 * K + 4 + 3 * M) * 4
+    bytes_ = rows * (Y * 2 + out_b + Y * 2 + out_b + Y * 2)
+    ach = bytes_ / t_fused / 1e9
+    res = {
+        "metric": "coefficient head (after the MLP) fwd+bwd rows/s, 1 MI355X",
+        "value": round(rows / t_fused, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_fused * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "SpectralBias coefficient head after the MLP, fwd+bwd with regularisers", "B": 1,
+                   "H": H, "T": T, "M": M, "K": K, "y_dtype": "bf16"},
+        "torch_steps_ms": round(t_torch * 1e3, 4),
+        "speedup_vs_torch_steps": round(t_torch / t_fused, 2),
+        "roofline": dict(bound="hbm", kernel="coeff_fwd_kernel+coeff_bwd_kernel", achieved=round(ach, 1),
+                         peak=PEAK_HBM_GBS, unit="GB/s", frac=round(ach / PEAK_HBM_GBS, 4), traffic=None,
+                         bytes_per_step=bytes_),
+    }
+    print(json.dumps(res))
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -375,6 +442,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.workload == "coeff":
+        main_coeff(args)
+        return
     if args.workload == "swa":
         if args.T == 131072 and args.bs == 256:  # the pointer workload's defaults -> the training shape
             args.T, args.bs = 65536, 128
