@@ -300,6 +300,21 @@ int scope_attn_fwd(const scope_attn_params* p, const uint16_t* q, const uint16_t
                    const float* slope, const float* delta_main, const float* width, uint16_t* out,
                    float* lse, void* stream);
 
+/* Block mass of the attention probabilities: mass[h][qb][kb] = the sum over
+ * the q-block's rows i and the key block's keys j of P_ij, for every listed
+ * kb (other entries untouched: zero mass first).  Replaces the teacher's
+ * per-q-block loop (scoped_medium.py:1799-1819: dense softmax, row sum,
+ * scatter_add per key block) for any list — the teacher passes the dense
+ * document-causal one.  Two passes over the lists: the LSE of every row
+ * (written to lse [H,T]), then the masses; no P·V.  MAXKV <= 1024.
+ * mass: fp32 [H, QB, NB]. */
+int scope_attn_block_mass(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
+                          const int32_t* kv_num, const int32_t* kv_idx, const int32_t* docs,
+                          const int32_t* ds_tok_end, const void* table, const float* coeff_cos,
+                          const float* coeff_sin, const float* b0, const float* slope,
+                          const float* delta_main, const float* width, float* lse, float* mass,
+                          void* stream);
+
 int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
 int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
                    const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,

@@ -174,6 +174,45 @@ def scope_attention_reference(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: 
     return attention_dense(q, k, v, allowed, bias, scale=scale, beta=beta)
 
 
+def block_mass(q, k, docs, *, bs: int, scale: float, beta: float = 0.5, bias_mode: str = "none", coeff_cos=None,
+               coeff_sin=None, omegas=None, token_kwargs: dict | None = None, kv_num=None, kv_idx=None):
+    """Teacher block mass (scoped_medium.py:1799-1819): for every head, q-block
+    qb and key block kb, the softmax probability mass summed over the
+    q-block's rows and the key block's keys -> [H, NB, NB].
+
+    Without lists the attention is the dense document-causal one (the
+    teacher's); with (kv_num, kv_idx) it is restricted to the listed blocks.
+    One q-block at a time, like the reference's loop.  Parity pin
+    (tests/test_oracle_attention.py): ``attention_dense`` with V = the one-hot
+    key-block indicator gives the same numbers summed over the rows; the
+    row-sum invariant Σ_kb mass = bs; the uniform closed form for q = 0."""
+    H, T, D = q.shape
+    NB = T // bs
+    docs = torch.as_tensor(docs).long()
+    mass = torch.zeros((H, NB, NB), dtype=q.dtype)
+    cols = torch.arange(T)
+    for qb in range(NB):
+        rows = torch.arange(qb * bs, (qb + 1) * bs)
+        s = scale * torch.einsum("hrd,hcd->hrc", q[:, rows], k)
+        if bias_mode == "token":
+            tk = dict(token_kwargs or {})
+            s = s + beta * bias_token(coeff_cos, coeff_sin, omegas, rows=rows, cols=cols, **tk)
+        elif bias_mode == "block":
+            s = s + beta * bias_block(coeff_cos, coeff_sin, omegas, bs, rows, cols)
+        ok = (rows[:, None] >= cols[None, :]) & (docs[rows][:, None] == docs[cols][None, :])
+        ok = ok[None].expand(H, -1, -1)
+        if kv_num is not None:
+            blk = torch.zeros((H, NB), dtype=torch.bool)
+            for h in range(H):
+                blk[h, torch.as_tensor(kv_idx)[h, qb, :int(kv_num[h, qb])].long()] = True
+            ok = ok & blk.repeat_interleave(bs, dim=1)[:, None, :]
+        s = s.masked_fill(~ok, float("-inf"))
+        lse = torch.logsumexp(s, dim=-1, keepdim=True)
+        p = torch.exp(s - torch.where(torch.isinf(lse), torch.zeros_like(lse), lse))
+        mass[:, qb] = p.sum(dim=1).reshape(H, NB, bs).sum(dim=-1)
+    return mass
+
+
 def flops_active(kv_num, bs: int, D: int) -> tuple[float, float]:
     """(F_fwd, F_bwd) counting every listed tile as a full bs×bs tile."""
     n_act = float(torch.as_tensor(kv_num).sum())

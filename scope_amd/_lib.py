@@ -77,6 +77,7 @@ _PROTOS = {
     "scope_spectral_table_bytes": (c_int64, [c_int, c_int64, c_int]),
     "scope_spectral_table": (c_int, [c_int, P, c_int, c_int64, c_int, P, P]),
     "scope_attn_fwd": (c_int, [C.POINTER(AttnParams)] + [P] * 17),
+    "scope_attn_block_mass": (c_int, [C.POINTER(AttnParams)] + [P] * 16),
     "scope_attn_bwd_workspace_bytes": (c_int64, [C.POINTER(AttnParams)]),
     "scope_attn_bwd": (c_int, [C.POINTER(AttnParams)] + [P] * 30),
     "scope_attn_bwd_phase": (c_int, [C.POINTER(AttnParams), c_int] + [P] * 30),

@@ -119,3 +119,36 @@ def scope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block_
                 dm, wd = sp.delta_main, sp.width
     out, lse = _ScopeAttnFn.apply(q, k, v, cc, cs, b0, sl, dm, wd, block_mask, sp, float(scale))
     return (out, lse) if return_lse else out
+
+
+def teacher_block_mass(q: torch.Tensor, k: torch.Tensor, docs: torch.Tensor, *, scale: float,
+                       spectral: SpectralTerms | None = None, block_size: int = 128) -> torch.Tensor:
+    """The teacher's block mass (scoped_medium.py:1799-1819): for every head,
+    q-block qb and key block kb, the softmax probability mass of the dense
+    document-causal attention summed over the q-block's rows and the key
+    block's keys -> [H, NB, NB] fp32.  The reference builds the same scores
+    from bf16 q / k and augmented q_pos / k_pos features (the band term and
+    slope of ``spectral``, offset="token"); here the bias is evaluated as in
+    ``scope_attention``.  q, k: [1,H,T,D] bf16 (the teacher's selected heads)."""
+    from .blockmask import ScopeBlockMask  # noqa: F401  (same mask conventions)
+
+    T = q.shape[-2]
+    bs = block_size
+    NB = T // bs
+    docs = docs.reshape(-1).to(torch.int32).contiguous()
+    _, ds_local, ds_tok_end = ops.doc_starts(docs, bs)
+    # dense document-causal list: key blocks from the q-block's first document start to the diagonal
+    qb = torch.arange(NB, device=q.device, dtype=torch.int32)
+    first = ds_local.to(torch.int32)
+    kv_num = (qb - first + 1)[None].expand(q.shape[1], -1).contiguous()
+    kv_idx = torch.minimum(first[:, None] + torch.arange(NB, device=q.device, dtype=torch.int32)[None],
+                           qb[:, None])[None].expand(q.shape[1], -1, -1).contiguous()
+    kw = dict(bias_mode="none")
+    if spectral is not None:
+        if spectral.offset != "token":
+            raise ValueError("teacher_block_mass: the teacher's bias uses token offsets")
+        kw = dict(bias_mode="token", beta=spectral.beta, table=spectral_table(spectral.omegas, T, bs, "token"),
+                  coeff_cos=spectral.coeff_cos, coeff_sin=spectral.coeff_sin,
+                  slope=spectral.slope if spectral.use_slope else None, use_slope=spectral.use_slope)
+    mass, _ = ops.attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, bs=bs, scale=scale, **kw)
+    return mass

@@ -201,6 +201,7 @@ struct AttnArgs {
   float* dwidth;
   float* delta;      // rowsum(dO∘O) [H,T]
   uint16_t* qfeat;   // token mode: query-side features [H,T][kTokRow] (hi g0, hi g1, lo g0, lo g1)
+  float* mass;       // block mass [H,QB,NB] (forward mass pass)
   int H, QB, maxkv, K;
   int64_t T;
   int64_t q_sh, q_st, k_sh, k_st, v_sh, v_st, o_sh, o_st;

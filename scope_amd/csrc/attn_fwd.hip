@@ -89,15 +89,24 @@ __device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>
     }
 }
 
-template <int BS, int MODE>
+// What the forward kernel produces: the attention output and its LSE; the
+// LSE alone (no P·V); or, given the LSE, the probability mass of every
+// listed key block summed over the q-block's rows (no P·V either).
+enum FwdKind { kFwdAttn = 0, kFwdLse = 1, kFwdMass = 2 };
+
+template <int BS, int MODE, int KIND = kFwdAttn>
 __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
   constexpr int NT = 2 * BS;
+  constexpr int NW = NT / 64;  // wavefronts
   constexpr int BN = 64;  // keys per staged tile
   constexpr int NSUB = BS / BN;
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
+  constexpr bool MASS = KIND == kFwdMass, PV = KIND == kFwdAttn;
 
   __shared__ KvTile<MODE> buf0, buf1;
   __shared__ int kbs[kListLds];
+  // mass: per list entry and wavefront, the wavefront's share (each slot has one writer)
+  __shared__ float mslot[MASS ? kListLds * NW : 1];
   // block mode: β·log2e-scaled coefficient rows of the block's queries, [BS][16] (cos 0..7, sin 8..15)
   __shared__ __attribute__((aligned(16))) float coef[MODE == 1 ? BS * 16 : 4];
 
@@ -115,6 +124,8 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
   const int n = a.kv_num[lrow];
   const int32_t* lst = a.kv_idx + lrow * a.maxkv;
   for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
+  if (MASS)
+    for (int t = tid; t < n * NW; t += NT) mslot[t] = 0.f;  // n <= kListLds (checked on the host)
 
   uint4 qreg[8];
   {
@@ -149,6 +160,8 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
+  float lse2 = 0.f;  // mass: the row's LSE in log2 units
+  if (MASS) lse2 = a.lse[hT + R.row] * kLog2e;
   float bt = 0.f;  // block mode: β·bias of the current key block (log2 units)
 
   // flat iteration index it = list entry · NSUB + key tile; tiles that start
@@ -203,6 +216,19 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
     if (TOK || !full) fwd_scores<MODE, true>(a, b, R, kv0, lane, s);
     // exponent = s·csm + off: modes 0/1 keep raw scores (csm = scale·log2e > 0)
     const float csm = TOK ? 1.f : a.scale_log2;
+    if (MASS) {
+      // P = 2^(s·csm + tconst - lse2); a row without visible keys (lse = -inf) has none
+      const float off = lse2 == -INFINITY ? -INFINITY : tconst - lse2;
+      float ps = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ps += __builtin_amdgcn_exp2f(fmaf(s[mb][r], csm, off));
+#pragma unroll
+      for (int o2 = 32; o2 > 0; o2 >>= 1) ps += __shfl_xor(ps, o2, 64);
+      if (lane == 0) mslot[(it / NSUB) * NW + wave] += ps;
+      return;
+    }
 
     // online softmax (log2 domain); the running maximum moves only by more than kLazy
     float mx = -INFINITY;
@@ -218,10 +244,12 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
       // where exp2(m_run - m_run) would be NaN); raised rows from -inf get 0
       const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_t) : 1.f;
       l_run *= alpha;
+      if (PV) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      }
       m_run = raise ? m_t : m_run;
     }
     const float off = m_run == -INFINITY ? -INFINITY : tconst - m_run;
@@ -244,10 +272,12 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
     l_run += psum;
 
     // O^T += V^T P^T
+    if (PV) {
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
+      for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-      for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor(b.v, 16 * s2, md * 32, lane), pb[s2], o[md]);
+        for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor(b.v, 16 * s2, md * 32, lane), pb[s2], o[md]);
+    }
   };
 
   __syncthreads();  // kbs
@@ -270,32 +300,45 @@ __global__ __launch_bounds__(2 * BS) void attn_fwd_kernel(AttnArgs a) {
   }
 
   // ---- epilogue
+  if (MASS) {
+    __syncthreads();  // every wavefront's shares are in mslot
+    float* mrow = a.mass + lrow * a.QB;
+    for (int e = tid; e < n; e += NT) {
+      float m = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) m += mslot[e * NW + w];
+      mrow[kbs[e]] = m;
+    }
+    return;
+  }
   const float l_row = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
-  uint16_t* op = a.out + h * a.o_sh + R.row * a.o_st + 4 * g;
+  if (PV) {
+    uint16_t* op = a.out + h * a.o_sh + R.row * a.o_st + 4 * g;
 #pragma unroll
-  for (int md = 0; md < 4; ++md)
+    for (int md = 0; md < 4; ++md)
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      uint2 val;
-      val.x = cvt_pk_bf16(o[md][4 * rq] * inv, o[md][4 * rq + 1] * inv);
-      val.y = cvt_pk_bf16(o[md][4 * rq + 2] * inv, o[md][4 * rq + 3] * inv);
-      *reinterpret_cast<uint2*>(op + md * 32 + 8 * rq) = val;
-    }
+      for (int rq = 0; rq < 4; ++rq) {
+        uint2 val;
+        val.x = cvt_pk_bf16(o[md][4 * rq] * inv, o[md][4 * rq + 1] * inv);
+        val.y = cvt_pk_bf16(o[md][4 * rq + 2] * inv, o[md][4 * rq + 3] * inv);
+        *reinterpret_cast<uint2*>(op + md * 32 + 8 * rq) = val;
+      }
+  }
   if (g == 0) a.lse_out[hT + R.row] = l_row > 0.f ? (m_run + log2f(l_row)) * kLn2 : -INFINITY;
 }
 
-template <int BS>
+template <int BS, int KIND = kFwdAttn>
 static void launch_fwd(const AttnArgs& a, int mode, int grid, hipStream_t s) {
   const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
   if (mode == SCOPE_BIAS_BLOCK)
-    hipLaunchKernelGGL((attn_fwd_kernel<BS, 1>), dim3(grid), dim3(2 * BS), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 1, KIND>), dim3(grid), dim3(2 * BS), 0, s, a);
   else if (mode == SCOPE_BIAS_TOKEN && gate)
-    hipLaunchKernelGGL((attn_fwd_kernel<BS, 3>), dim3(grid), dim3(2 * BS), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 3, KIND>), dim3(grid), dim3(2 * BS), 0, s, a);
   else if (mode == SCOPE_BIAS_TOKEN)
-    hipLaunchKernelGGL((attn_fwd_kernel<BS, 2>), dim3(grid), dim3(2 * BS), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 2, KIND>), dim3(grid), dim3(2 * BS), 0, s, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<BS, 0>), dim3(grid), dim3(2 * BS), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<BS, 0, KIND>), dim3(grid), dim3(2 * BS), 0, s, a);
 }
 
 int validate_attn(const scope_attn_params* p, const void* q, const void* k, const void* v, const int32_t* kv_num,
@@ -401,4 +444,50 @@ extern "C" int scope_attn_fwd(const scope_attn_params* p, const uint16_t* q, con
   else
     launch_fwd<128>(a, p->bias_mode, grid, s);
   return check_launch("attn_fwd_kernel");
+}
+
+extern "C" int scope_attn_block_mass(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
+                                     const int32_t* kv_num, const int32_t* kv_idx, const int32_t* docs,
+                                     const int32_t* ds_tok_end, const void* table, const float* coeff_cos,
+                                     const float* coeff_sin, const float* b0, const float* slope,
+                                     const float* delta_main, const float* width, float* lse, float* mass,
+                                     void* stream) {
+  int rc = validate_attn(p, q, k, k, kv_num, kv_idx, docs, ds_tok_end, table, coeff_cos, coeff_sin, b0, slope,
+                         delta_main, width, "scope_attn_block_mass");
+  if (rc) return rc;
+  SCOPE_REQUIRE(lse && mass, "scope_attn_block_mass: null output");
+  SCOPE_REQUIRE(p->maxkv <= kListLds, "scope_attn_block_mass: MAXKV=%d above %d listed blocks per q-block",
+                p->maxkv, kListLds);
+  AttnArgs a = make_args(p);
+  a.q = q;
+  a.k = k;
+  a.v = k;  // staged with the keys but never read
+  a.kv_num = kv_num;
+  a.kv_idx = kv_idx;
+  a.docs = docs;
+  a.ds_tok_end = ds_tok_end;
+  a.table = table;
+  a.coeff_cos = coeff_cos;
+  a.coeff_sin = coeff_sin;
+  a.b0 = b0;
+  a.slope = slope;
+  a.delta_main = delta_main;
+  a.width = width;
+  a.lse_out = lse;
+  a.lse = lse;
+  a.mass = mass;
+  const int grid = p->H * a.QB;
+  hipStream_t s = as_stream(stream);
+  // pass 1: the LSE of every row; pass 2: the block masses from it
+  if (p->bs == 256)
+    launch_fwd<256, kFwdLse>(a, p->bias_mode, grid, s);
+  else
+    launch_fwd<128, kFwdLse>(a, p->bias_mode, grid, s);
+  rc = check_launch("attn_fwd_kernel (lse)");
+  if (rc) return rc;
+  if (p->bs == 256)
+    launch_fwd<256, kFwdMass>(a, p->bias_mode, grid, s);
+  else
+    launch_fwd<128, kFwdMass>(a, p->bias_mode, grid, s);
+  return check_launch("attn_fwd_kernel (mass)");
 }

@@ -388,6 +388,29 @@ def attn_fwd(q, k, v, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float
     return out, lse
 
 
+def attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float, beta: float = 0.5,
+                    bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None, slope=None,
+                    delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
+                    ramp_lambda=0.0, tau=64.0):
+    """Attention probability mass per (head, q-block, listed key block),
+    summed over the q-block's rows -> (mass [H, QB, NB] fp32, lse [1,H,T])."""
+    dev = _gpu("attn_block_mass", q, k, kv_num, kv_idx, docs, ds_tok_end)
+    kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
+    m = BIAS_MODES[bias_mode]
+    K = coeff_cos.shape[-1] if (m and coeff_cos is not None) else 0
+    prm = _attn_params(q, k, k, q, bs=bs, maxkv=kv_idx3.shape[-1], scale=scale, beta=beta, bias_mode=m, K=K,
+                       use_slope=use_slope, subtract_b0=subtract_b0, gate_kind=GATE_KINDS[gate_kind],
+                       ramp_lambda=ramp_lambda, tau=tau)
+    H, T = prm.H, prm.T
+    NB = T // bs
+    lse = torch.empty((1, H, T), dtype=torch.float32, device=dev)
+    mass = torch.zeros((H, NB, NB), dtype=torch.float32, device=dev)
+    call("scope_attn_block_mass", C.byref(prm), _p(q), _p(k), _p(_i32(kv_num)), _p(kv_idx3),
+         _p(_i32(docs.reshape(-1))), _p(_i32(ds_tok_end)), _p(table), _p(_f32(coeff_cos)), _p(_f32(coeff_sin)),
+         _p(_f32(b0)), _p(_f32(slope)), _p(_f32(delta_main)), _p(_f32(width)), _p(lse), _p(mass), _stream(dev))
+    return mass, lse
+
+
 def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",

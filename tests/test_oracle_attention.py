@@ -190,3 +190,37 @@ def test_gradcheck_token_and_block_modes():
 
     assert torch.autograd.gradcheck(f_tok, (q, k, v, cc, cs, sl, dm, wd), eps=1e-6, atol=1e-5)
     assert torch.autograd.gradcheck(f_blk, (q, k, v, cc, cs), eps=1e-6, atol=1e-5)
+
+
+def test_block_mass_pins():
+    """oracle.attention.block_mass: (1) the dense attention with V = the
+    one-hot key-block indicator, summed over the q-block's rows; (2) every
+    row's probabilities sum to 1; (3) q = 0 without a bias gives the uniform
+    closed form (visible keys of a row in kb / visible keys of the row)."""
+    H, T, D, bs = 2, 256, 16, 32
+    NB = T // bs
+    g = torch.Generator().manual_seed(4)
+    docs = torch.zeros(T, dtype=torch.long)
+    docs[70:] = 1
+    docs[161:] = 2
+    q, k = (torch.randn((H, T, D), generator=g, dtype=torch.float64) for _ in range(2))
+    K = 4
+    cc = torch.randn((H, T, K), generator=g, dtype=torch.float64) * 0.3
+    cs = torch.randn((H, T, K), generator=g, dtype=torch.float64) * 0.3
+    om = A.omegas_logspaced(K, 64, 4096).double()
+    sl = torch.randn((H, T), generator=g, dtype=torch.float64) * 0.01
+    tk = dict(slope=sl)
+    m = A.block_mass(q, k, docs, bs=bs, scale=0.2, bias_mode="token", coeff_cos=cc, coeff_sin=cs, omegas=om,
+                     token_kwargs=tk)
+    i = torch.arange(T)
+    allowed = ((i[:, None] >= i[None, :]) & (docs[:, None] == docs[None, :]))[None].expand(H, -1, -1)
+    onehot = torch.nn.functional.one_hot(i // bs, NB).double()[None].expand(H, -1, -1)
+    bias = A.bias_token(cc, cs, om, **tk)
+    out, _ = A.attention_dense(q, k, onehot, allowed, bias, scale=0.2)
+    want = out.reshape(H, NB, bs, NB).sum(dim=2)
+    assert torch.allclose(m, want, atol=1e-12)
+    assert torch.allclose(m.sum(-1), torch.full((H, NB), float(bs), dtype=torch.float64), atol=1e-10)
+    mu = A.block_mass(torch.zeros_like(q), k, docs, bs=bs, scale=0.2)
+    vis = allowed[0].double()
+    closed = (vis / vis.sum(-1, keepdim=True)).reshape(NB, bs, NB, bs).sum(dim=(1, 3))
+    assert torch.allclose(mu[0], closed, atol=1e-12) and torch.allclose(mu[1], closed, atol=1e-12)
