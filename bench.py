@@ -27,6 +27,11 @@ T=65536, H=8, D=128 (the training shape).
 its MLP (model/attn_bias.py:419-506, M=8 peaks, K=8 bands, regularisers on)
 forward and backward at T=131072, H=8: the fused kernels against the same
 module's torch steps on the same GPU.
+
+``--workload teacher`` times the teacher's block mass (scoped_medium.py:
+1799-1819: dense document-causal attention with the token-offset band term
+and slope, probabilities summed per q-block and key block) at the teacher's
+length T=4096 (8 heads, bs 128) and at T=65536.
 """
 from __future__ import annotations
 
@@ -59,7 +64,7 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["pointer", "swa", "coeff"], default="pointer")
+    ap.add_argument("--workload", choices=["pointer", "swa", "coeff", "teacher"], default="pointer")
     ap.add_argument("--swa-window", type=int, default=14, help="long-mask window in blocks (--workload swa)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, one plain device copy of this many MiB (calibrates HBM byte counters)")
@@ -345,6 +350,57 @@ def main_coeff(args):
     print(json.dumps(res))
 
 
+def main_teacher(args):
+    import torch
+
+    import scope_amd
+
+    H, D, bs, K = args.H, 128, 128, 8
+    lines = {}
+    for T in (4096, 65536):
+        inp = make_inputs(H, T, D, bs)
+        q, k, docs = inp["q"].cuda(), inp["k"].cuda(), inp["docs"].cuda()
+        g = torch.Generator().manual_seed(7)
+        sp = scope_amd.SpectralTerms(coeff_cos=(torch.randn((1, H, T, K), generator=g) * 0.3).cuda(),
+                                     coeff_sin=(torch.randn((1, H, T, K), generator=g) * 0.3).cuda(),
+                                     omegas=torch.logspace(-5.0, -1.3, K).cuda(), offset="token", beta=0.5,
+                                     slope=(torch.randn((1, H, T), generator=g) * 0.002).cuda(), use_slope=True)
+
+        def step():
+            scope_amd.attention.teacher_block_mass(q, k, docs, scale=0.12, spectral=sp, block_size=bs)
+
+        t = time_region(step, args.steps, args.warmup)
+        # active tiles of the dense document-causal lists: Σ_qb (qb - first + 1)
+        from scope_amd import ops
+
+        _, ds_local, _ = ops.doc_starts(docs, bs)
+        nb = T // bs
+        n_act = H * int((torch.arange(nb, device="cuda") - ds_local + 1).sum())
+        flops = 2 * (2.0 * bs * bs * D) * n_act  # two passes of S = q·k^T over every listed tile
+        lines[str(T)] = dict(ms=round(t * 1e3, 4), n_act=n_act, tflops=round(flops / t / 1e12, 2))
+    res = {
+        "metric": "teacher block mass (dense document-causal attention probabilities per block) TFLOP/s, 1 MI355X",
+        "value": lines["4096"]["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": lines["4096"]["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "teacher block mass (LSE pass + mass pass, token band term + slope)", "B": 1, "H": H,
+                   "T": 4096, "D": D, "block": bs, "bands": K},
+        "by_length": lines,
+        "roofline": dict(bound="mfma", kernel="attn_fwd_kernel (lse + mass)", achieved=lines["65536"]["tflops"],
+                         peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                         frac=round(lines["65536"]["tflops"] / PEAK_BF16_TFLOPS, 4), traffic=None, at_T=65536),
+    }
+    print(json.dumps(res))
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -442,6 +498,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.workload == "teacher":
+        main_teacher(args)
+        return
     if args.workload == "coeff":
         main_coeff(args)
         return
