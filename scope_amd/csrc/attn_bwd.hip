@@ -469,9 +469,9 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     // lane pair (l, l^32): g = 0 fills the cos half of its row, g = 1 the sin half
     const float* cf = (g == 0 ? a.coeff_cos : a.coeff_sin) + (hT + R.row) * a.K;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) coef[lrow_ * 16 + g * 8 + k] = k < a.K ? cf[k] * a.beta_log2 : 0.f;
+    for (int k = 0; k < 8; ++k) coef[row16_off(lrow_, 2 * g + k / 4) + k % 4] = k < a.K ? cf[k] * a.beta_log2 : 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) gacc[lrow_ * 32 + g * 16 + k] = 0.f;
+    for (int k = 0; k < 16; ++k) gacc[row32_off(lrow_, 4 * g + k / 4) + k % 4] = 0.f;
   }
   const int ds_end = a.ds_tok_end[qb];
   R.doc = a.docs[R.row];
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   f32x16_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = zero16();
-  float rs_tot = 0.f, pm_tot = 0.f;  // per lane (half the keys of the row) until the epilogue
+  float rs_tot = 0.f;  // per lane (half the keys of the row) until the epilogue
   float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
 
   const int total = n * NSUB;
@@ -523,18 +523,16 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     rs_kb += rs;
     pm_kb += pm;
     rs_tot += rs;
-    pm_tot += pm;
   };
   auto run = [&](int it, int nxt, const KvTile<MODE>& b) {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (MODE == 1 && it % NSUB == 0) {
       // block term of this key block (its first tile is never skipped)
-      const float4* cr = reinterpret_cast<const float4*>(coef + lrow_ * 16);
       const float4* t4 = reinterpret_cast<const float4*>(b.tab);
       float acc[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float4 c4 = cr[i], tt = t4[i];
+        const float4 c4 = *reinterpret_cast<const float4*>(coef + row16_off(lrow_, i)), tt = t4[i];
         acc[i] = c4.x * tt.x + c4.y * tt.y + c4.z * tt.z + c4.w * tt.w;
       }
       bt = (acc[0] + acc[1]) + (acc[2] + acc[3]);
@@ -545,15 +543,16 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
       // pair) into the gradient sums; g = 0 keeps the cos half, g = 1 the sin half
       const float rsr = rs_kb + __shfl_xor(rs_kb, 32, 64), pmr = pm_kb + __shfl_xor(pm_kb, 32, 64);
       const float4* t4 = reinterpret_cast<const float4*>(b.tab + g * 8);
-      float4* ga = reinterpret_cast<float4*>(gacc + lrow_ * 32 + g * 16);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const float4 tt = t4[i];
-        float4 ar = ga[i], ap = ga[2 + i];
+        float4* gr = reinterpret_cast<float4*>(gacc + row32_off(lrow_, 4 * g + i));
+        float4* gp = reinterpret_cast<float4*>(gacc + row32_off(lrow_, 4 * g + 2 + i));
+        float4 ar = *gr, ap = *gp;
         ar.x += rsr * tt.x, ar.y += rsr * tt.y, ar.z += rsr * tt.z, ar.w += rsr * tt.w;
         ap.x += pmr * tt.x, ap.y += pmr * tt.y, ap.z += pmr * tt.z, ap.w += pmr * tt.w;
-        ga[i] = ar;
-        ga[2 + i] = ap;
+        *gr = ar;
+        *gp = ap;
       }
       rs_kb = pm_kb = 0.f;
     }
@@ -593,9 +592,12 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     }
   if (MODE == 1 && a.dcoeff_cos) {
     // g = 0 writes the cos coefficients of its row, g = 1 the sin ones
-    const float* ga = gacc + lrow_ * 32 + g * 16;
     float* dst = (g == 0 ? a.dcoeff_cos : a.dcoeff_sin) + (hT + R.row) * a.K;
-    for (int k = 0; k < a.K; ++k) dst[k] = a.beta * (ga[k] - dd_err * ga[8 + k]);
+    for (int k = 0; k < a.K; ++k) {
+      const float rs = gacc[row32_off(lrow_, 4 * g + k / 4) + k % 4];
+      const float pm = gacc[row32_off(lrow_, 4 * g + 2 + k / 4) + k % 4];
+      dst[k] = a.beta * (rs - dd_err * pm);
+    }
   }
 }
 

@@ -59,6 +59,14 @@ __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 
 // element offset of (row r, column d) in a swizzled tile
 __device__ __forceinline__ int swz_off(int r, int d) { return r * 128 + (((d >> 3) ^ swz(r)) << 3) + (d & 7); }
 
+// Per-row fp32 arrays that each lane reads as float4 chunks of its own row
+// (coefficients, gradient sums).  Row strides of 64 or 128 bytes would put
+// 4 or 8 of 16 consecutive rows on the same banks; the chunk index is XORed
+// with row bits so that 16 consecutive rows reading the same chunk hit
+// distinct banks.  Offsets in floats; chunk c covers floats 4c..4c+3.
+__device__ __forceinline__ int row16_off(int r, int c) { return r * 16 + ((c ^ ((r >> 2) & 3)) << 2); }
+__device__ __forceinline__ int row32_off(int r, int c) { return r * 32 + ((c ^ ((r >> 1) & 7)) << 2); }
+
 __device__ __forceinline__ uint4 lds_row8(const uint16_t* tile, int r, int d) {
   return *reinterpret_cast<const uint4*>(tile + swz_off(r, d));
 }

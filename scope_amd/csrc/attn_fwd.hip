@@ -144,9 +144,9 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
   if (MODE == 1) {
     // lane pair (l, l^32) fills the cos (g = 0) or sin (g = 1) half of its row
     const float* cf = (g == 0 ? a.coeff_cos : a.coeff_sin) + (hT + R.row) * a.K;
-    float* dst = coef + (wave * 32 + lr) * 16 + g * 8;
+    const int cr = wave * 32 + lr;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) dst[k] = k < a.K ? cf[k] * a.beta_log2 : 0.f;
+    for (int k = 0; k < 8; ++k) coef[row16_off(cr, 2 * g + k / 4) + k % 4] = k < a.K ? cf[k] * a.beta_log2 : 0.f;
   }
   if (TOK) {
     token_qfeat(a, hT, R.row, g, qf, qfl, nullptr, nullptr);
@@ -188,12 +188,11 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
     if (MODE == 1 && it % NSUB == 0) {
       // block term of this key block (a key block's first tile is never skipped)
-      const float4* cr = reinterpret_cast<const float4*>(coef + (wave * 32 + lr) * 16);
       const float4* tr = reinterpret_cast<const float4*>(b.tab);
       float acc = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float4 c4 = cr[i], t4 = tr[i];
+        const float4 c4 = *reinterpret_cast<const float4*>(coef + row16_off(wave * 32 + lr, i)), t4 = tr[i];
         acc += c4.x * t4.x + c4.y * t4.y + c4.z * t4.z + c4.w * t4.w;
       }
       bt = acc;

@@ -205,17 +205,25 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_fwd_kernel(
   }
 }
 
-// reg = [total, omega, entropy, delta_edge, zero_mean, mean_b]
-__global__ __launch_bounds__(64) void coeff_reg_kernel(scope_coeff_params p, int nblk, const double* __restrict__ partial,
-                                                       float* __restrict__ reg) {
-  __shared__ double tot[4];
-  if (threadIdx.x < 4) {
-    double s = 0.0;
-    for (int b = 0; b < nblk; ++b) s += partial[static_cast<int64_t>(b) * 4 + threadIdx.x];
-    tot[threadIdx.x] = s;
-  }
+// reg = [total, omega, entropy, delta_edge, zero_mean, mean_b]; one workgroup:
+// thread t sums the workgroup partials t, t + 256, ... in order, then a fixed
+// tree over the threads
+__global__ __launch_bounds__(256) void coeff_reg_kernel(scope_coeff_params p, int nblk, const double* __restrict__ partial,
+                                                        float* __restrict__ reg) {
+  __shared__ double red[4][256];
+  const int t = threadIdx.x;
+  double v[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int b = t; b < nblk; b += 256)
+    for (int i = 0; i < 4; ++i) v[i] += partial[static_cast<int64_t>(b) * 4 + i];
+  for (int i = 0; i < 4; ++i) red[i][t] = v[i];
   __syncthreads();
-  if (threadIdx.x != 0) return;
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o)
+      for (int i = 0; i < 4; ++i) red[i][t] += red[i][t + o];
+    __syncthreads();
+  }
+  if (t != 0) return;
+  const double tot[4] = {red[0][0], red[1][0], red[2][0], red[3][0]};
   const double N = static_cast<double>(p.rows), NM = N * p.M;
   const float omega = p.lambda_omega > 0.f ? static_cast<float>(p.lambda_omega * (tot[0] / NM)) : 0.f;
   const float ent = p.lambda_entropy > 0.f && p.entropy_floor > 0.f ? static_cast<float>(p.lambda_entropy * (tot[1] / N)) : 0.f;
@@ -431,7 +439,7 @@ extern "C" int scope_coeff_head_fwd(const scope_coeff_params* p, const void* y, 
   else go(coeff_fwd_kernel<kMaxM, kMaxK>);
   rc = check_launch("coeff_fwd_kernel");
   if (rc || !p->training) return rc;
-  hipLaunchKernelGGL(coeff_reg_kernel, dim3(1), dim3(64), 0, s, *p, nblk, static_cast<const double*>(workspace), reg);
+  hipLaunchKernelGGL(coeff_reg_kernel, dim3(1), dim3(256), 0, s, *p, nblk, static_cast<const double*>(workspace), reg);
   return check_launch("coeff_reg_kernel");
 }
 

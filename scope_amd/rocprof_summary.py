@@ -28,14 +28,22 @@ import json
 import os
 import sys
 
-KERNELS = ("attn_fwd_kernel", "attn_bwd_dq_kernel", "attn_bwd_dkv_kernel", "bwd_reduce_kernel", "block_means_kernel",
-           "ptr_score_kernel", "stats_kernel", "tr_fill_kernel", "tr_sort_kernel", "tr_count_kernel")
+KERNELS = ("attn_fwd_kernel", "attn_fwd_kernel(lse)", "attn_fwd_kernel(mass)", "attn_bwd_dq2_kernel",
+           "attn_bwd_dq_kernel", "attn_bwd_dkv_kernel", "bwd_reduce_kernel", "block_means_kernel", "ptr_score_kernel",
+           "stats_kernel", "tr_fill_kernel", "tr_sort_kernel", "tr_count_kernel", "swa_count_kernel",
+           "swa_rows_kernel", "swa_pad_kernel", "coeff_fwd_kernel", "coeff_bwd_kernel", "coeff_reg_kernel",
+           "probe_mfma_kernel", "probe_copy_kernel")
 COPY = "copyBuffer"
+FWD_KINDS = {"0": "", "1": "(lse)", "2": "(mass)"}
 
 
 def _short(name: str) -> str:
+    if "attn_fwd_kernel<" in name:
+        args = name.split("attn_fwd_kernel<", 1)[1].split(">", 1)[0].split(",")
+        kind = args[2].strip() if len(args) > 2 else "0"
+        return "attn_fwd_kernel" + FWD_KINDS.get(kind, "")
     for k in KERNELS + (COPY,):
-        if k in name:
+        if "(" not in k and k in name:
             return k
     return name.split("(")[0][-60:]
 
