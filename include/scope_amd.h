@@ -315,6 +315,30 @@ int scope_attn_block_mass(const scope_attn_params* p, const uint16_t* q, const u
                           const float* delta_main, const float* width, float* lse, float* mass,
                           void* stream);
 
+/* ------------------------------------------------------------------------
+ * Decode: the attention of one new token (position t) against the KV cache,
+ * over its q-block's listed key blocks with the document-causal mask.  No
+ * reference counterpart (the reference has no decode path); it serves the
+ * token loop of the 16-layer decoder (scoped_medium.py:266-639 forward, one
+ * position at a time).  q [H, D] (head stride q_sh); k_cache / v_cache
+ * [H, T_cap, D] with (head, token) strides; kv_num [H], kv_idx [H, maxkv];
+ * docs [T_cap] (entries up to t are read); out [H, D] bf16 (head stride
+ * o_sh); lse [H] natural log (or NULL).  The workspace holds one partial
+ * (max, sum, P·V row) per (head, list entry).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int H, D, bs, maxkv;
+  int64_t T_cap;                 /* tokens the cache holds (multiple of bs)  */
+  int64_t t;                     /* position of the query                    */
+  float scale;
+  int64_t q_sh, k_sh, k_st, v_sh, v_st, o_sh;
+} scope_decode_params;
+
+int64_t scope_decode_workspace_bytes(const scope_decode_params* p);
+int scope_decode_attn(const scope_decode_params* p, const uint16_t* q, const uint16_t* k_cache,
+                      const uint16_t* v_cache, const int32_t* kv_num, const int32_t* kv_idx,
+                      const int32_t* docs, void* workspace, uint16_t* out, float* lse, void* stream);
+
 int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
 int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
                    const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,

@@ -213,6 +213,28 @@ def block_mass(q, k, docs, *, bs: int, scale: float, beta: float = 0.5, bias_mod
     return mass
 
 
+def decode_attention(q, k_cache, v_cache, kv_num, kv_idx, docs, t: int, *, bs: int, scale: float):
+    """One query at position t (q [H, D]) against the cache [H, T_cap, D] over
+    the listed blocks (kv_num [H], kv_idx [H, maxkv]) with the document-causal
+    mask -> (out [H, D], lse [H]).  Pinned (tests/test_oracle_attention.py)
+    by ``attention_blocksparse``'s row t with the same list."""
+    H, T_cap, D = k_cache.shape
+    docs = torch.as_tensor(docs).long()
+    out = torch.zeros((H, D), dtype=q.dtype)
+    lse = torch.full((H,), float("-inf"), dtype=q.dtype)
+    for h in range(H):
+        blocks = torch.as_tensor(kv_idx)[h, :int(kv_num[h])].long()
+        cols = (blocks[:, None] * bs + torch.arange(bs)[None]).reshape(-1)
+        cols = cols[(cols <= t)]
+        cols = cols[docs[cols] == docs[t]]
+        if cols.numel() == 0:
+            continue
+        s = scale * (k_cache[h, cols] @ q[h])
+        lse[h] = torch.logsumexp(s, 0)
+        out[h] = torch.softmax(s, 0) @ v_cache[h, cols]
+    return out, lse
+
+
 def flops_active(kv_num, bs: int, D: int) -> tuple[float, float]:
     """(F_fwd, F_bwd) counting every listed tile as a full bs×bs tile."""
     n_act = float(torch.as_tensor(kv_num).sum())

@@ -55,6 +55,12 @@ class CoeffParams(C.Structure):
                 ("lambda_delta_edge", c_float), ("entropy_floor", c_float), ("delta_edge_eps", c_float)]
 
 
+class DecodeParams(C.Structure):
+    _fields_ = [("H", c_int), ("D", c_int), ("bs", c_int), ("maxkv", c_int), ("T_cap", c_int64), ("t", c_int64),
+                ("scale", c_float), ("q_sh", c_int64), ("k_sh", c_int64), ("k_st", c_int64), ("v_sh", c_int64),
+                ("v_st", c_int64), ("o_sh", c_int64)]
+
+
 P = c_void_p
 _PROTOS = {
     "scope_abi_version": (c_int, []),
@@ -79,6 +85,8 @@ _PROTOS = {
     "scope_attn_fwd": (c_int, [C.POINTER(AttnParams)] + [P] * 17),
     "scope_attn_block_mass": (c_int, [C.POINTER(AttnParams)] + [P] * 16),
     "scope_attn_bwd_workspace_bytes": (c_int64, [C.POINTER(AttnParams)]),
+    "scope_decode_workspace_bytes": (c_int64, [C.POINTER(DecodeParams)]),
+    "scope_decode_attn": (c_int, [C.POINTER(DecodeParams)] + [P] * 10),
     "scope_attn_bwd": (c_int, [C.POINTER(AttnParams)] + [P] * 30),
     "scope_attn_bwd_phase": (c_int, [C.POINTER(AttnParams), c_int] + [P] * 30),
     "scope_probe_mfma_flops": (c_int64, [c_int, c_int]),

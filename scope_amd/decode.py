@@ -1,0 +1,254 @@
+"""Token-loop decoding of the 16-layer SCOPE decoder on one MI355X.
+
+The model mirrors ``GPT`` of scoped_medium.py:266-639 — token and value
+embeddings (the 012 ... 012 pattern, :592), per block ``lambdas`` mixing with
+x0, QK-norm, half-truncated rotary, value-embedding mix, ReLU² MLP, the
+U-net skip connections with ``skip_weights``, no attention in block 7
+(:499), and the soft-capped logits ``30·σ(logits/7.5)`` (:618) over the
+vocabulary padded to a multiple of 128 (:529).  Every attention layer is a
+SCOPE layer with the block-scoring pointer mask (window W, budget B, G
+document-start globals) and no spectral bias.  Weights are random (the
+reference zero-initialises its output projections and lm_head, which would
+make greedy decoding trivial).
+
+* ``prefill(tokens)``: one forward over the prompt (T a multiple of the
+  block size) with the block-sparse attention kernel; fills every layer's KV
+  cache and key-block means.
+* ``step(token)``: one new position t.  When t opens a q-block, every layer
+  reselects that block's list over its cache (the query block mean is the
+  new token's query, the only one known), and keeps it for the block's other
+  positions; the attention of the token runs ``scope_decode_attn`` over the
+  list.  When t closes a block, its key mean joins the candidates.
+
+The reference has no decode path; this is the row of the scope table that
+puts the hot-path kernels under a token loop.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+
+EOT = 50256
+
+
+@dataclass
+class DecoderConfig:
+    vocab_size: int = 50257
+    num_layers: int = 16
+    num_heads: int = 8
+    model_dim: int = 1024
+    head_dim: int = 128
+    block_size: int = 128
+    window: int = 4
+    budget: int = 4
+    n_global: int = 1
+    attn_scale: float = 0.12
+    no_attn_layer: int = 7
+
+    @property
+    def vocab_padded(self) -> int:
+        return ((self.vocab_size + 127) // 128) * 128
+
+
+def _norm(x: torch.Tensor) -> torch.Tensor:
+    return F.rms_norm(x, (x.size(-1),))
+
+
+class _Rotary:
+    """Half-truncated RoPE tables (scoped_medium.py:282-299)."""
+
+    def __init__(self, dim: int, max_len: int, device):
+        freq = (1 / 1024) ** torch.linspace(0, 1, steps=dim // 4, dtype=torch.float32)
+        freq = torch.cat([freq, freq.new_zeros(dim // 4)])
+        theta = torch.arange(max_len, dtype=torch.float32)[:, None] * freq[None]
+        self.cos, self.sin = theta.cos().to(device), theta.sin().to(device)
+
+    def __call__(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """x [T, H, D] at positions pos [T]."""
+        cos, sin = self.cos[pos][:, None, :], self.sin[pos][:, None, :]
+        x1, x2 = x.float().chunk(2, dim=-1)
+        return torch.cat((x1 * cos + x2 * sin, x1 * (-sin) + x2 * cos), -1).type_as(x)
+
+
+class ScopeDecoder(nn.Module):
+    def __init__(self, cfg: DecoderConfig, *, max_len: int, device="cuda", seed: int = 0):
+        super().__init__()
+        self.cfg = cfg
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        d, H, D, L = cfg.model_dim, cfg.num_heads, cfg.head_dim, cfg.num_layers
+        hd = H * D
+
+        def uni(*shape, fan_in):
+            b = math.sqrt(3.0) * 0.5 * fan_in ** -0.5  # CastedLinear / qkv init bound (:270-274, :305-306)
+            return ((torch.rand(shape, generator=g) * 2 - 1) * b).to(torch.bfloat16).to(device)
+
+        self.embed = (torch.randn((cfg.vocab_size, d), generator=g)).to(torch.bfloat16).to(device)
+        self.value_embeds = [torch.randn((cfg.vocab_size, d), generator=g).to(torch.bfloat16).to(device)
+                             for _ in range(3)]
+        self.layers = []
+        for i in range(L):
+            lay = dict(lambdas=(1.0, 0.0), mlp_fc=uni(4 * d, d, fan_in=d), mlp_proj=uni(d, 4 * d, fan_in=4 * d))
+            if i != cfg.no_attn_layer:
+                lay.update(qkv=uni(3 * hd, d, fan_in=d), proj=uni(d, hd, fan_in=hd), vlam=(0.5, 0.5))
+            self.layers.append(lay)
+        self.skip_weights = [1.0] * (L // 2)
+        self.lm_head = uni(cfg.vocab_padded, d, fan_in=d)
+        self.rotary = _Rotary(D, max_len, device)
+        self.device = torch.device(device)
+        self.max_len = max_len
+        # caches
+        nbc = max_len // cfg.block_size
+        z = dict(dtype=torch.bfloat16, device=device)
+        self.k_cache = [torch.zeros((H, max_len, D), **z) if "qkv" in lay else None for lay in self.layers]
+        self.v_cache = [torch.zeros((H, max_len, D), **z) if "qkv" in lay else None for lay in self.layers]
+        self.kbar = [torch.zeros((H, nbc, D), dtype=torch.float32, device=device) if "qkv" in lay else None
+                     for lay in self.layers]
+        self.lists = [None] * L  # current q-block's (kv_num [H], kv_idx [H, maxkv]) per layer
+        self.docs = torch.zeros(max_len, dtype=torch.int32, device=device)
+        self.tokens = torch.zeros(max_len, dtype=torch.int64, device=device)
+        self.t = 0
+        self._ws = None
+
+    # ---- pieces shared by prefill and step -------------------------------------
+    def _ve(self, tok: torch.Tensor):
+        ve = [F.embedding(tok, w) for w in self.value_embeds]
+        L = self.cfg.num_layers
+        return [ve[0], ve[1], ve[2]] + [None] * (L - 6) + [ve[0], ve[1], ve[2]]
+
+    def _qkv(self, lay, x: torch.Tensor, ve, pos: torch.Tensor):
+        """x [T, d] (normed) -> q, k, v [T, H, D] (q, k normed and rotated, v mixed)."""
+        cfg = self.cfg
+        T = x.shape[0]
+        qkv = F.linear(x, lay["qkv"]).view(T, 3 * cfg.num_heads, cfg.head_dim)
+        q, k, v = qkv.chunk(3, dim=-2)
+        q, k = _norm(q), _norm(k)
+        q, k = self.rotary(q, pos), self.rotary(k, pos)
+        a, b = lay["vlam"]
+        v = a * v + b * ve.view_as(v) if ve is not None else a * v
+        return q, k, v
+
+    def _mlp(self, lay, x: torch.Tensor) -> torch.Tensor:
+        h = F.linear(_norm(x), lay["mlp_fc"])
+        return F.linear(F.relu(h).square(), lay["mlp_proj"])
+
+    def _logits(self, x: torch.Tensor) -> torch.Tensor:
+        return 30 * torch.sigmoid(F.linear(_norm(x), self.lm_head).float() / 7.5)
+
+    def _select(self, qbar: torch.Tensor, kbar: torch.Tensor, nb: int):
+        """Block-scoring lists of blocks 0..nb-1 from q̄, k̄ [H, nb, D]."""
+        cfg = self.cfg
+        T = nb * cfg.block_size
+        ds_ptr, ds_local, _ = ops.doc_starts(self.docs[:T], cfg.block_size)
+        return ops.pointer_select(ds_ptr, ds_local, bs=cfg.block_size, NB=nb, H=cfg.num_heads, window=cfg.window,
+                                  n_global=cfg.n_global, budget=cfg.budget, qbar=qbar, kbar=kbar, temp=1.0,
+                                  logit_scale=cfg.block_size / math.sqrt(cfg.head_dim), noise="none")
+
+    # ---- prefill ---------------------------------------------------------------
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor, *, all_logits: bool = False) -> torch.Tensor:
+        """Forward over the prompt; returns the logits of the last position
+        (or of every position with ``all_logits``)."""
+        cfg = self.cfg
+        T = tokens.numel()
+        bs = cfg.block_size
+        if T % bs or T > self.max_len:
+            raise ValueError(f"prefill: T={T} must be a multiple of {bs} and at most {self.max_len}")
+        tok = tokens.to(self.device).long()
+        self.tokens[:T] = tok
+        self.docs[:T] = (tok == EOT).cumsum(0).to(torch.int32)
+        docs = self.docs[:T]
+        _, _, ds_tok_end = ops.doc_starts(docs, bs)
+        pos = torch.arange(T, device=self.device)
+        ve = self._ve(tok)
+        x = x0 = _norm(F.embedding(tok, self.embed))
+        skips = []
+        n = len(self.skip_weights)
+        for i, lay in enumerate(self.layers):
+            if i >= n:
+                x = x + self.skip_weights[i - n] * skips.pop()
+            a, b = lay["lambdas"]
+            x = a * x + b * x0
+            if "qkv" in lay:
+                q, k, v = self._qkv(lay, _norm(x), ve[i], pos)
+                qh, kh, vh = (z.transpose(0, 1) for z in (q, k, v))  # [H, T, D] views
+                self.k_cache[i][:, :T] = kh
+                self.v_cache[i][:, :T] = vh
+                qbar, kbar = ops.block_means(qh, kh, bs)
+                self.kbar[i][:, :T // bs] = kbar
+                kv_num, kv_idx, _ = self._select(qbar, kbar, T // bs)
+                y, _ = ops.attn_fwd(qh[None], kh[None], vh[None], kv_num, kv_idx, docs, ds_tok_end, bs=bs,
+                                    scale=cfg.attn_scale)
+                x = x + F.linear(y[0].transpose(0, 1).reshape(T, -1), lay["proj"])
+            x = x + self._mlp(lay, x)
+            if i < n:
+                skips.append(x)
+        self.t = T
+        return self._logits(x) if all_logits else self._logits(x[-1:])[0]
+
+    # ---- one decode step ---------------------------------------------------------
+    @torch.no_grad()
+    def step(self, token: int | torch.Tensor) -> torch.Tensor:
+        """Append one token at position t; returns its logits [vocab_padded]."""
+        cfg = self.cfg
+        bs = cfg.block_size
+        t = self.t
+        if t >= self.max_len:
+            raise ValueError("step: the cache is full")
+        tok = torch.as_tensor(token, device=self.device).reshape(1).long()
+        self.tokens[t] = tok[0]
+        prev = self.docs[t - 1] if t > 0 else torch.zeros((), dtype=torch.int32, device=self.device)
+        self.docs[t] = prev + (tok[0] == EOT).to(torch.int32)
+        qb = t // bs
+        opens = t % bs == 0
+        if opens:  # positions of the new block not yet written carry the current document
+            self.docs[t + 1:(qb + 1) * bs] = self.docs[t]
+        pos = torch.tensor([t], device=self.device)
+        ve = self._ve(tok)
+        x = x0 = _norm(F.embedding(tok, self.embed))
+        skips = []
+        n = len(self.skip_weights)
+        H, D = cfg.num_heads, cfg.head_dim
+        for i, lay in enumerate(self.layers):
+            if i >= n:
+                x = x + self.skip_weights[i - n] * skips.pop()
+            a, b = lay["lambdas"]
+            x = a * x + b * x0
+            if "qkv" in lay:
+                q, k, v = self._qkv(lay, _norm(x), ve[i], pos)
+                self.k_cache[i][:, t] = k[0]
+                self.v_cache[i][:, t] = v[0]
+                if opens or self.lists[i] is None:
+                    nb = qb + 1
+                    qbar = torch.zeros((H, nb, D), dtype=torch.float32, device=self.device)
+                    qbar[:, qb] = q[0].float()
+                    kv_num, kv_idx, _ = self._select(qbar, self.kbar[i][:, :nb].contiguous(), nb)
+                    self.lists[i] = (kv_num[:, qb].contiguous(), kv_idx[:, qb].contiguous())
+                if self._ws is None:
+                    self._ws = torch.empty(H * 64 * (D + 2) * 4, dtype=torch.uint8, device=self.device)
+                y, _ = ops.decode_attn(q[0], self.k_cache[i], self.v_cache[i], self.lists[i][0], self.lists[i][1],
+                                       self.docs, t, bs=bs, scale=cfg.attn_scale, workspace=self._ws)
+                x = x + F.linear(y.reshape(1, H * D), lay["proj"])
+                if t % bs == bs - 1:  # the block is complete: its key mean joins the candidates
+                    self.kbar[i][:, qb] = self.k_cache[i][:, qb * bs:(qb + 1) * bs].float().mean(dim=1)
+            x = x + self._mlp(lay, x)
+            if i < n:
+                skips.append(x)
+        self.t = t + 1
+        return self._logits(x)[0]
+
+    @torch.no_grad()
+    def generate(self, n_steps: int, first: int | torch.Tensor) -> torch.Tensor:
+        """Greedy decoding: feeds ``first``, then each argmax, for n_steps."""
+        out = torch.empty(n_steps, dtype=torch.int64, device=self.device)
+        tok = torch.as_tensor(first, device=self.device)
+        for s in range(n_steps):
+            logits = self.step(tok)
+            tok = logits[:self.cfg.vocab_size].argmax()
+            out[s] = tok
+        return out

@@ -411,6 +411,36 @@ def attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: f
     return mass, lse
 
 
+def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_num: torch.Tensor,
+                kv_idx: torch.Tensor, docs: torch.Tensor, t: int, *, bs: int, scale: float,
+                workspace: torch.Tensor | None = None):
+    """Attention of the token at position t: q [H, D] bf16 against the cache
+    k_cache / v_cache [H, T_cap, D] over the listed blocks kv_idx [H, maxkv]
+    (kv_num [H]) -> (out [H, D] bf16, lse [H] natural log)."""
+    from ._lib import DecodeParams
+
+    dev = _gpu("decode_attn", q, k_cache, v_cache, kv_num, kv_idx, docs)
+    if q.dim() != 2 or k_cache.dim() != 3 or v_cache.dim() != 3:
+        raise RuntimeError("decode_attn: q [H, D], caches [H, T_cap, D]")
+    for n_, x in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+            raise RuntimeError(f"decode_attn: {n_} must be bfloat16 with a unit last stride")
+    H, D = q.shape
+    T_cap = k_cache.shape[1]
+    kv_idx = _i32(kv_idx)
+    prm = DecodeParams(H=H, D=D, bs=int(bs), maxkv=kv_idx.shape[-1], T_cap=T_cap, t=int(t), scale=float(scale),
+                       q_sh=q.stride(0), k_sh=k_cache.stride(0), k_st=k_cache.stride(1), v_sh=v_cache.stride(0),
+                       v_st=v_cache.stride(1), o_sh=D)
+    need = int(query("scope_decode_workspace_bytes", C.byref(prm)))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    out = torch.empty((H, D), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(H, dtype=torch.float32, device=dev)
+    call("scope_decode_attn", C.byref(prm), _p(q), _p(k_cache), _p(v_cache), _p(_i32(kv_num)), _p(kv_idx),
+         _p(_i32(docs.reshape(-1))), _p(workspace), _p(out), _p(lse), _stream(dev))
+    return out, lse
+
+
 def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",

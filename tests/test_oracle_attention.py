@@ -224,3 +224,26 @@ def test_block_mass_pins():
     vis = allowed[0].double()
     closed = (vis / vis.sum(-1, keepdim=True)).reshape(NB, bs, NB, bs).sum(dim=(1, 3))
     assert torch.allclose(mu[0], closed, atol=1e-12) and torch.allclose(mu[1], closed, atol=1e-12)
+
+
+def test_decode_attention_is_a_row_of_the_blocksparse_oracle():
+    H, T, D, bs = 2, 256, 16, 32
+    NB = T // bs
+    g = torch.Generator().manual_seed(8)
+    docs = torch.zeros(T, dtype=torch.long)
+    docs[100:] = 1
+    q, k, v = (torch.randn((H, T, D), generator=g, dtype=torch.float64) for _ in range(3))
+    for t in (0, 99, 100, 131, 255):
+        qb = t // bs
+        kv_idx = torch.zeros((H, NB, 4), dtype=torch.int32)
+        kv_num = torch.zeros((H, NB), dtype=torch.int32)
+        lists = [sorted({qb, max(qb - 1, 0), 0}), sorted({qb, max(qb - 2, 0)})]
+        for h in range(H):
+            kv_num[h, qb] = len(lists[h])
+            kv_idx[h, qb, :len(lists[h])] = torch.tensor(lists[h])
+        res = A.attention_blocksparse(q, k, v, kv_num, kv_idx, docs, bs=bs, scale=0.3, qblocks=[qb])
+        o, l = A.decode_attention(q[:, t], k, v, kv_num[:, qb], kv_idx[:, qb], docs, t, bs=bs, scale=0.3)
+        for h in range(H):
+            ro, rl = res[(h, qb)]
+            assert torch.allclose(o[h], ro[t % bs], atol=1e-12)
+            assert torch.allclose(l[h], rl[t % bs], atol=1e-12)
