@@ -32,6 +32,12 @@ module's torch steps on the same GPU.
 1799-1819: dense document-causal attention with the token-offset band term
 and slope, probabilities summed per q-block and key block) at the teacher's
 length T=4096 (8 heads, bs 128) and at T=65536.
+
+``--workload decode`` runs the 16-layer decoder (d_model 1024, 8 heads of
+128, MLP 4096 ReLU², vocabulary 50304, bf16, random weights): a prefill of
+131072 seeded uniform-random tokens, then 256 greedy decode steps with the
+pointer lists (window 4 blocks of 128, budget 4, 1 global) reselected at every
+new q-block.  value = decode tokens/s; the prefill time is reported beside it.
 """
 from __future__ import annotations
 
@@ -64,7 +70,8 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["pointer", "swa", "coeff", "teacher"], default="pointer")
+    ap.add_argument("--workload", choices=["pointer", "swa", "coeff", "teacher", "decode"], default="pointer")
+    ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--swa-window", type=int, default=14, help="long-mask window in blocks (--workload swa)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, one plain device copy of this many MiB (calibrates HBM byte counters)")
@@ -401,6 +408,58 @@ def main_teacher(args):
     print(json.dumps(res))
 
 
+def main_decode(args):
+    import torch
+
+    from scope_amd.decode import DecoderConfig, ScopeDecoder
+
+    T0 = args.T if args.T != 131072 or args.bs != 256 else 131072
+    n = args.decode_steps
+    cfg = DecoderConfig()
+    m = ScopeDecoder(cfg, max_len=T0 + ((n + cfg.block_size) // cfg.block_size) * cfg.block_size, device="cuda",
+                     seed=0)
+    g = torch.Generator().manual_seed(0)
+    toks = torch.randint(0, cfg.vocab_size, (T0 + 1,), generator=g)
+    # warm-up on a short prompt (kernels, allocator), then the measured run
+    w = ScopeDecoder(cfg, max_len=1024, device="cuda", seed=1)
+    w.prefill(toks[:512])
+    w.generate(8, int(toks[512]))
+    del w
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = m.prefill(toks[:T0])
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter() - t0
+    first = int(logits[:cfg.vocab_size].argmax())
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = m.generate(n, first)
+    torch.cuda.synchronize()
+    t_dec = time.perf_counter() - t0
+    res = {
+        "metric": "SCOPE decoder greedy decode tokens/s after a 131072-token prefill (16 layers), 1 MI355X",
+        "value": round(n / t_dec, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": 8,
+        "ms_per_step": round(t_dec / n * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "16-layer decoder: prefill + greedy token loop", "layers": cfg.num_layers,
+                   "d_model": cfg.model_dim, "H": cfg.num_heads, "D": cfg.head_dim, "mlp": 4 * cfg.model_dim,
+                   "vocab": cfg.vocab_padded, "prefill_tokens": T0, "decode_steps": n, "block": cfg.block_size,
+                   "window": cfg.window, "budget": cfg.budget, "global": cfg.n_global},
+        "prefill_ms": round(t_pre * 1e3, 2),
+        "prefill_tokens_per_s": round(T0 / t_pre, 1),
+        "generated_head": out[:8].tolist(),
+    }
+    print(json.dumps(res))
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -498,6 +557,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.workload == "decode":
+        main_decode(args)
+        return
     if args.workload == "teacher":
         main_teacher(args)
         return
