@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   R.row = wrow_lo + lr;
 
   const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
-  const int n = a.kv_num[lrow];
+  const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
   const int32_t* lst = a.kv_idx + lrow * a.maxkv;
   for (int t = tid; t < min(n, kListLds); t += 256) kbs[t] = lst[t];
 
@@ -204,12 +204,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   // start after this workgroup's last row are skipped
   const int total = n * NSUB;
   const int qmax = static_cast<int>(q0) + 127;
-  auto kb_at = [&](int t) { return t < kListLds ? kbs[t] : lst[t]; };
-  auto next_valid = [&](int it) {
+  // the list lives in LDS (width <= kListLds, checked on the host): a read that
+  // could also reach global memory would be a flat load, whose wait also waits
+  // for the tile copies in flight
+  auto kb_at = [&](int t) __attribute__((always_inline)) { return kbs[t]; };
+  auto next_valid = [&](int it) __attribute__((always_inline)) {
     while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
     return it;
   };
-  auto issue = [&](int it, KvTile<MODE>& b) {
+  auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
     const int kb = kb_at(it / NSUB);
     const int rd = min(max(qb - kb, 0), a.QB - 1);
     kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   // block mode: the bias term and the per-row sums dS, P change per key block
   // (four 64-key tiles), not per tile
   float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
-  auto compute = [&](int kv0, const KvTile<MODE>& b) {
+  auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
     const float tconst = MODE == 1 ? bt : R.rowc;
     // S^T and dP^T: keys in two 32-row blocks (A operand), this lane's query row as the column
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     rs_tot += rs;
     pm_tot += pm;
   };
-  auto run = [&](int it, int nxt, const KvTile<MODE>& b) {
+  auto run = [&](int it, int nxt, const KvTile<MODE>& b) __attribute__((always_inline)) {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (MODE == 1 && it % NSUB == 0) {
       // a key block's first tile is never skipped (it starts at or before every row)
@@ -436,7 +439,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   R.row = wrow_lo + lr;
 
   const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
-  const int n = a.kv_num[lrow];
+  const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
   const int32_t* lst = a.kv_idx + lrow * a.maxkv;
   for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
 
@@ -485,17 +488,20 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
 
   const int total = n * NSUB;
   const int qmax = static_cast<int>(q0) + BS - 1;
-  auto kb_at = [&](int t) { return t < kListLds ? kbs[t] : lst[t]; };
-  auto next_valid = [&](int it) {
+  // the list lives in LDS (width <= kListLds, checked on the host): a read that
+  // could also reach global memory would be a flat load, whose wait also waits
+  // for the tile copies in flight
+  auto kb_at = [&](int t) __attribute__((always_inline)) { return kbs[t]; };
+  auto next_valid = [&](int it) __attribute__((always_inline)) {
     while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
     return it;
   };
-  auto issue = [&](int it, KvTile<MODE>& b) {
+  auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
     const int kb = kb_at(it / NSUB);
     const int rd = min(max(qb - kb, 0), a.QB - 1);
     kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
   };
-  auto compute = [&](int kv0, const KvTile<MODE>& b) {
+  auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
     const float off = (MODE == 1 ? bt : 0.f) - R.lse2;
     float rs = 0.f, pm = 0.f;
@@ -524,7 +530,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     pm_kb += pm;
     rs_tot += rs;
   };
-  auto run = [&](int it, int nxt, const KvTile<MODE>& b) {
+  auto run = [&](int it, int nxt, const KvTile<MODE>& b) __attribute__((always_inline)) {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (MODE == 1 && it % NSUB == 0) {
       // block term of this key block (its first tile is never skipped)
@@ -1012,7 +1018,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   }
 
   // iteration j covers flat index f = j + skip0: list entry f / NS, sub-tile f % NS
-  auto tile_q0 = [&](int j, int& e) {
+  auto tile_q0 = [&](int j, int& e) __attribute__((always_inline)) {
     const int f = j + skip0;
     e = f / NS;
     return static_cast<int64_t>(qbs[e]) * BS + (f % NS) * BM;

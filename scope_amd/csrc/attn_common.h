@@ -97,6 +97,45 @@ __device__ __forceinline__ uint4 lds_kmajor(const uint16_t* tile, int k0, int dm
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
+// Lane byte offsets of the swizzled-tile reads, computed once per kernel.
+// swz(r) depends only on r mod 16, so a read at row offset r0 (a multiple of
+// 16: a k-step, or the second 32-row block) is the lane's offset for r0 = 0
+// plus the constant r0·256 bytes.  The inner loops then issue ds_reads whose
+// only per-read term is an immediate: no swizzle arithmetic per read.
+struct TileOffs {
+  uint32_t row[8];              // lds_row8(tile, lane % 32, 16·ks + 8·(lane / 32)), ks = 0..7
+  uint32_t tr_lo[4], tr_hi[4];  // the two transpose reads of lds_kmajor(tile, 0, 32·md, lane), md = 0..3
+};
+
+__device__ __forceinline__ TileOffs tile_offs(int lane) {
+  TileOffs o;
+  const int g = lane >> 5, lr = lane & 31, l16 = lane & 15, s = l16 >> 2, t = l16 & 3, hf = (lane >> 4) & 1;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) o.row[ks] = 2u * static_cast<uint32_t>(swz_off(lr, ks * 16 + g * 8));
+#pragma unroll
+  for (int md = 0; md < 4; ++md) {
+    const int d = md * 32 + hf * 16 + 4 * t;
+    o.tr_lo[md] = 2u * static_cast<uint32_t>(swz_off(4 * g + s, d));
+    o.tr_hi[md] = 2u * static_cast<uint32_t>(swz_off(8 + 4 * g + s, d));
+  }
+  return o;
+}
+
+// lds_row8(tile, r0 + lane % 32, 16·ks + 8·(lane / 32)) for r0 a multiple of 16
+__device__ __forceinline__ uint4 lds_row8_o(const uint16_t* tile, const TileOffs& o, int r0, int ks) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tile) + r0 * 256 + o.row[ks]);
+}
+
+// lds_kmajor(tile, k0, 32·md, lane) for k0 a multiple of 16
+__device__ __forceinline__ uint4 lds_kmajor_o(const uint16_t* tile, const TileOffs& o, int k0, int md) {
+  const char* base = reinterpret_cast<const char*>(tile) + k0 * 256;
+  lds_bf16x4_t* plo = (lds_bf16x4_t*)(const_cast<char*>(base + o.tr_lo[md]));
+  lds_bf16x4_t* phi = (lds_bf16x4_t*)(const_cast<char*>(base + o.tr_hi[md]));
+  const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(plo));
+  const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(phi));
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
 // ---- swizzled 32-column tiles (64-byte rows: token features) ---------------
 // The 16-byte chunk c of row r is stored at chunk c ^ ((r/4) % 4): row reads
 // of 16 consecutive rows and transpose reads of 4 rows are conflict free.
@@ -268,7 +307,7 @@ struct alignas(16) KvTile {
   uint16_t f[MODE >= 2 ? 64 * kTokRow : 8];  // token modes: key features [64][32] (swz32_off)
 };
 
-constexpr int kListLds = 1024;  // kv-list entries staged in LDS (longer lists read the rest from memory)
+constexpr int kListLds = 1024;  // kv-list entries staged in LDS: the widest list the q-major kernels take
 
 // Issue the copies of keys kv0 .. kv0+63 (and the block-table row rdist) into
 // b; NT threads (128, 256 or 512) take part.

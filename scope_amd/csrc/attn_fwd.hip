@@ -31,6 +31,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "attn_common.h"
 
 namespace scope {
@@ -106,8 +108,12 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
   constexpr int NSUB = BS / BN;
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
   constexpr bool MASS = KIND == kFwdMass, PV = KIND == kFwdAttn;
+  // bs=256 attention: wavefronts 4-7 run half a tile behind wavefronts 0-3
+  // (see the loop below), which needs a third tile buffer
+  constexpr bool STAGGER = PV && BS == 256;
 
   __shared__ KvTile<MODE> buf0, buf1;
+  __shared__ typename std::conditional<STAGGER, KvTile<MODE>, int>::type buf2;
   __shared__ int kbs[kListLds];
   // mass: per list entry and wavefront, the wavefront's share (each slot has one writer)
   __shared__ float mslot[MASS ? kListLds * NW : 1];
@@ -125,12 +131,13 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
   R.row = wrow_lo + lr;
 
   const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
-  const int n = a.kv_num[lrow];
+  const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
   const int32_t* lst = a.kv_idx + lrow * a.maxkv;
   for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
   if (MASS)
     for (int t = tid; t < n * NW; t += NT) mslot[t] = 0.f;  // n <= kListLds (checked on the host)
 
+  const TileOffs to = tile_offs(lane);
   uint4 qreg[8];
   {
     const uint16_t* qp = a.q + h * a.q_sh + R.row * a.q_st + g * 8;
@@ -172,19 +179,24 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
   // after the block's last row are skipped
   const int total = n * NSUB;
   const int qmax = static_cast<int>(q0) + BS - 1;
-  auto kb_at = [&](int t) { return t < kListLds ? kbs[t] : lst[t]; };
-  auto next_valid = [&](int it) {
+  // the list lives in LDS (width <= kListLds, checked on the host): a read that
+  // could also reach global memory would be a flat load, whose wait also waits
+  // for the tile copies in flight
+  auto kb_at = [&](int t) __attribute__((always_inline)) { return kbs[t]; };
+  auto next_valid = [&](int it) __attribute__((always_inline)) {
     while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
     return it;
   };
-  auto issue = [&](int it, KvTile<MODE>& b) {
+  auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
     const int kb = kb_at(it / NSUB);
     const int rd = min(max(qb - kb, 0), a.QB - 1);
     kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
   };
-  auto run = [&](int it, const KvTile<MODE>& b) {
+  // one tile in two parts: scores and probabilities (P^T as bf16 B operands
+  // in pb; false when the wavefront has nothing to do), then O^T += V^T P^T
+  auto run_a = [&](int it, const KvTile<MODE>& b, uint4 (&pb)[4]) __attribute__((always_inline)) -> bool {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
-    if (kv0 > wrow_lo + 31) return;  // every key follows this wavefront's rows
+    if (kv0 > wrow_lo + 31) return false;  // every key follows this wavefront's rows
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
     if (MODE == 1 && it % NSUB == 0) {
       // block term of this key block (a key block's first tile is never skipped)
@@ -205,7 +217,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32(lds_row8(b.k, mb * 32 + lr, ks * 16 + g * 8), qreg[ks], s[mb]);
+      for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32(lds_row8_o(b.k, to, mb * 32, ks), qreg[ks], s[mb]);
     if (TOK) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
@@ -230,7 +242,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
 #pragma unroll
       for (int o2 = 32; o2 > 0; o2 >>= 1) ps += __shfl_xor(ps, o2, 64);
       if (lane == 0) mslot[(it / NSUB) * NW + wave] += ps;
-      return;
+      return false;
     }
 
     // online softmax (log2 domain); the running maximum moves only by more than kLazy
@@ -257,7 +269,6 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
     }
     const float off = m_run == -INFINITY ? -INFINITY : tconst - m_run;
 
-    uint4 pb[4];
     float psum = 0.f;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -273,33 +284,90 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
                                      cvt_pk_bf16(p[6], p[7]));
       }
     l_run += psum;
-
-    // O^T += V^T P^T
-    if (PV) {
+    return PV;
+  };
+  auto run_b = [&](const KvTile<MODE>& b, const uint4 (&pb)[4]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2)
+    for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-        for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor(b.v, 16 * s2, md * 32, lane), pb[s2], o[md]);
-    }
+      for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor_o(b.v, to, 16 * s2, md), pb[s2], o[md]);
+  };
+  auto run = [&](int it, const KvTile<MODE>& b) __attribute__((always_inline)) {
+    uint4 pb[4];
+    if (run_a(it, b, pb)) run_b(b, pb);
   };
 
   __syncthreads();  // kbs
-  int cur = next_valid(0);
-  if (cur < total) issue(cur, buf0);
-  while (cur < total) {
-    wait_vm0();
-    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
-    int nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf1);
-    run(cur, buf0);
-    cur = nxt;
-    if (cur >= total) break;
-    wait_vm0();
-    __syncthreads();
-    nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf0);
-    run(cur, buf1);
-    cur = nxt;
+  if constexpr (STAGGER) {
+    // Wavefronts 0-3 (one per SIMD) process whole tiles; wavefronts 4-7 run
+    // half a tile behind them: their k-th barrier falls between the scores
+    // and the P·V of tile k-1.  Each SIMD then holds one wavefront in its
+    // score/softmax phase while the other runs MFMAs, instead of both in
+    // the same phase.  The leading group alone copies the tiles (256
+    // threads), into three rotating buffers: at its k-th barrier the lagging
+    // group is done with tile k-2, whose buffer then takes tile k+1.  Both
+    // groups pass n+1 barriers for n tiles.
+    const int tid4 = tid & 255;
+    auto issue4 = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
+      const int kb = kb_at(it / NSUB);
+      const int rd = min(max(qb - kb, 0), a.QB - 1);
+      kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid4);
+    };
+    if (wave < 4) {
+      int cur = next_valid(0);
+      if (cur < total) issue4(cur, buf0);
+      auto lead = [&](KvTile<MODE>& bc, KvTile<MODE>& bn) __attribute__((always_inline)) {
+        wait_vm0();
+        __syncthreads();  // tile cur is in bc for everyone; the lagging group is done with bn
+        const int nxt = next_valid(cur + 1);
+        if (nxt < total) issue4(nxt, bn);
+        run(cur, bc);
+        cur = nxt;
+      };
+      while (cur < total) {
+        lead(buf0, buf1);
+        if (cur >= total) break;
+        lead(buf1, buf2);
+        if (cur >= total) break;
+        lead(buf2, buf0);
+      }
+      __syncthreads();  // matches the lagging group's last barrier
+    } else {
+      __syncthreads();  // tile 0 is in buf0
+      int cur = next_valid(0);
+      auto lag = [&](const KvTile<MODE>& bc) __attribute__((always_inline)) {
+        uint4 pb[4];
+        const bool act = run_a(cur, bc, pb);
+        __syncthreads();  // the leading group starts the next tile
+        if (act) run_b(bc, pb);
+        cur = next_valid(cur + 1);
+      };
+      while (cur < total) {
+        lag(buf0);
+        if (cur >= total) break;
+        lag(buf1);
+        if (cur >= total) break;
+        lag(buf2);
+      }
+    }
+  } else {
+    int cur = next_valid(0);
+    if (cur < total) issue(cur, buf0);
+    while (cur < total) {
+      wait_vm0();
+      __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
+      int nxt = next_valid(cur + 1);
+      if (nxt < total) issue(nxt, buf1);
+      run(cur, buf0);
+      cur = nxt;
+      if (cur >= total) break;
+      wait_vm0();
+      __syncthreads();
+      nxt = next_valid(cur + 1);
+      if (nxt < total) issue(nxt, buf0);
+      run(cur, buf1);
+      cur = nxt;
+    }
   }
 
   // ---- epilogue
@@ -355,6 +423,7 @@ int validate_attn(const scope_attn_params* p, const void* q, const void* k, cons
                 (long long)p->T, p->bs);
   SCOPE_REQUIRE(p->T < (1ll << 31), "%s: T=%lld exceeds int32 token indices", who, (long long)p->T);
   SCOPE_REQUIRE(p->H >= 1 && p->maxkv >= 1, "%s: bad H/maxkv", who);
+  SCOPE_REQUIRE(p->maxkv <= kListLds, "%s: MAXKV=%d above %d listed blocks per q-block", who, p->maxkv, kListLds);
   SCOPE_REQUIRE(p->q_st % 8 == 0 && p->k_st % 8 == 0 && p->v_st % 8 == 0 && p->o_st % 8 == 0 &&
                     p->q_sh % 8 == 0 && p->k_sh % 8 == 0 && p->v_sh % 8 == 0 && p->o_sh % 8 == 0,
                 "%s: strides must be multiples of 8 elements (16-byte rows)", who);
