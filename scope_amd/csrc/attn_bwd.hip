@@ -184,6 +184,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   }
   const int ds_end = a.ds_tok_end[qb];
   R.doc = a.docs[R.row];
+  const TileOffs to = tile_offs(lane);
 
   f32x16_t o[4];
 #pragma unroll
@@ -230,14 +231,31 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       s[mb] = zero16();
       dpv[mb] = zero16();
     }
-    // four independent accumulator chains interleaved (dependent MFMAs stall)
+    // four independent accumulator chains interleaved (dependent MFMAs stall);
+    // operands one k-step ahead, each step's reads issued before its MFMAs
+    uint4 ka[2][2], va[2][2];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int mb = 0; mb < 2; ++mb) {
+      ka[0][mb] = lds_row8_o(b.k, to, mb * 32, 0);
+      va[0][mb] = lds_row8_o(b.v, to, mb * 32, 0);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        if (ks + 1 < 8) {
+          ka[(ks + 1) % 2][mb] = lds_row8_o(b.k, to, mb * 32, ks + 1);
+          va[(ks + 1) % 2][mb] = lds_row8_o(b.v, to, mb * 32, ks + 1);
+        }
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        s[mb] = mfma32(lds_row8(b.k, mb * 32 + lr, ks * 16 + g * 8), qreg[ks], s[mb]);
-        dpv[mb] = mfma32(lds_row8(b.v, mb * 32 + lr, ks * 16 + g * 8), doreg[ks], dpv[mb]);
+        s[mb] = mfma32(ka[ks % 2][mb], qreg[ks], s[mb]);
+        dpv[mb] = mfma32(va[ks % 2][mb], doreg[ks], dpv[mb]);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (TOK) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
@@ -255,11 +273,21 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       dq_probs<MODE, true>(a, b, R, kv0, off, lane, s, dpv, dsb, pbv, rs, pm, ex);
     else
       dq_probs<MODE, false>(a, b, R, kv0, off, lane, s, dpv, dsb, pbv, rs, pm, ex);
-    // dQ^T += K^T dS^T (and the token-mode feature sums)
+    // dQ^T += K^T dS^T (and the token-mode feature sums); step st: k-step
+    // st/4, columns 32·(st%4), operands two steps ahead
+    {
+      uint4 ta[3];
+      ta[0] = lds_kmajor_o(b.k, to, 0, 0);
+      ta[1] = lds_kmajor_o(b.k, to, 0, 1);
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
-#pragma unroll
-      for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor(b.k, 16 * s2, md * 32, lane), dsb[s2], o[md]);
+      for (int st = 0; st < 16; ++st) {
+        if (st + 2 < 16) ta[(st + 2) % 3] = lds_kmajor_o(b.k, to, 16 * ((st + 2) / 4), (st + 2) % 4);
+        o[st % 4] = mfma32(ta[st % 3], dsb[st / 4], o[st % 4]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     if (TOK) {
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
@@ -479,6 +507,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   const int ds_end = a.ds_tok_end[qb];
   R.doc = a.docs[R.row];
   const float cs = a.scale_log2;
+  const TileOffs to = tile_offs(lane);
 
   f32x16_t o[4];
 #pragma unroll
@@ -508,23 +537,39 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       // S^T and dP^T of keys mb·32 .. +31 (A operand) against this lane's row (B)
+      // (operands one k-step ahead; each step's reads go out before its MFMAs)
       f32x16_t s = zero16(), dp = zero16();
+      uint4 ka[2], va[2];
+      ka[0] = lds_row8_o(b.k, to, mb * 32, 0);
+      va[0] = lds_row8_o(b.v, to, mb * 32, 0);
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        s = mfma32(lds_row8(b.k, mb * 32 + lr, ks * 16 + g * 8), qreg[ks], s);
-        dp = mfma32(lds_row8(b.v, mb * 32 + lr, ks * 16 + g * 8), doreg[ks], dp);
+        if (ks + 1 < 8) {
+          ka[(ks + 1) % 2] = lds_row8_o(b.k, to, mb * 32, ks + 1);
+          va[(ks + 1) % 2] = lds_row8_o(b.v, to, mb * 32, ks + 1);
+        }
+        s = mfma32(ka[ks % 2], qreg[ks], s);
+        dp = mfma32(va[ks % 2], doreg[ks], dp);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
       uint4 dsb[2];
       if (!full)
         dq2_probs<MODE, true>(b, R, kv0, off, cs, lane, mb, s, dp, dsb, rs, pm);
       else
         dq2_probs<MODE, false>(b, R, kv0, off, cs, lane, mb, s, dp, dsb, rs, pm);
-      // dQ^T += K^T dS^T over these 32 keys
+      // dQ^T += K^T dS^T over these 32 keys (step st: k-step 2·mb + st/4, columns 32·(st%4))
+      uint4 ta[2];
+      ta[0] = lds_kmajor_o(b.k, to, 32 * mb, 0);
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int md = 0; md < 4; ++md)
-          o[md] = mfma32(lds_kmajor(b.k, 16 * (2 * mb + hf), md * 32, lane), dsb[hf], o[md]);
+      for (int st = 0; st < 8; ++st) {
+        if (st + 1 < 8) ta[(st + 1) % 2] = lds_kmajor_o(b.k, to, 16 * (2 * mb + (st + 1) / 4), (st + 1) % 4);
+        o[st % 4] = mfma32(ta[st % 2], dsb[st / 4], o[st % 4]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     rs_kb += rs;
     pm_kb += pm;
@@ -838,16 +883,15 @@ __device__ __forceinline__ void dkv_offsets(const AttnArgs& a, const DkvBuf<MODE
 }
 
 // One 64-row query tile against this wavefront's 32 keys: S, dP, then
-// dV^T += dO^T·P and dK^T += Q^T·dS.  (The copies of the next tile are issued
-// by the caller: issued in here, through a reference, the compiler cannot
-// tell the two buffers apart and waits for every copy before the next LDS
-// read.)
+// dV^T += dO^T·P and dK^T += Q^T·dS.  The copies of the next tile are issued
+// by the caller, before this tile's reads.
 template <int BS, int MODE>
 __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, float* offw,
                                          const float* tab,
                                          int64_t q0, int lane, int64_t wkv_lo, int doc_kv,
                                          const uint4 (&kreg)[8], const uint4 (&vreg)[8], const uint4& kf,
-                                         const uint4& kfl, f32x16_t (&dvT)[4], f32x16_t (&dkT)[4]) {
+                                         const uint4& kfl, f32x16_t (&dvT)[4], f32x16_t (&dkT)[4],
+                                         const TileOffs& to) {
   const int g = lane >> 5, lr = lane & 31;
   const int wkv = static_cast<int>(wkv_lo) + lr;
   dkv_offsets<MODE>(a, b, offw, tab, lane);
@@ -861,21 +905,24 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
   // four independent accumulator chains; the A operands of k-step ks+1 are
   // read from LDS while k-step ks runs (the fences stop the compiler from
   // hoisting every read, which would exhaust the registers)
-  uint4 qa0 = lds_row8(b.q, lr, g * 8), qa1 = lds_row8(b.q, 32 + lr, g * 8);
-  uint4 da0 = lds_row8(b.d, lr, g * 8), da1 = lds_row8(b.d, 32 + lr, g * 8);
+  uint4 qa0 = lds_row8_o(b.q, to, 0, 0), qa1 = lds_row8_o(b.q, to, 32, 0);
+  uint4 da0 = lds_row8_o(b.d, to, 0, 0), da1 = lds_row8_o(b.d, to, 32, 0);
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
     uint4 qn0 = qa0, qn1 = qa1, dn0 = da0, dn1 = da1;
     if (ks < 7) {
-      qn0 = lds_row8(b.q, lr, (ks + 1) * 16 + g * 8);
-      qn1 = lds_row8(b.q, 32 + lr, (ks + 1) * 16 + g * 8);
-      dn0 = lds_row8(b.d, lr, (ks + 1) * 16 + g * 8);
-      dn1 = lds_row8(b.d, 32 + lr, (ks + 1) * 16 + g * 8);
+      qn0 = lds_row8_o(b.q, to, 0, ks + 1);
+      qn1 = lds_row8_o(b.q, to, 32, ks + 1);
+      dn0 = lds_row8_o(b.d, to, 0, ks + 1);
+      dn1 = lds_row8_o(b.d, to, 32, ks + 1);
     }
     s[0] = mfma32(qa0, kreg[ks], s[0]);
     dp[0] = mfma32(da0, vreg[ks], dp[0]);
     s[1] = mfma32(qa1, kreg[ks], s[1]);
     dp[1] = mfma32(da1, vreg[ks], dp[1]);
+    // the next k-step's reads go out before this k-step's MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     __builtin_amdgcn_sched_barrier(0);
     qa0 = qn0, qa1 = qn1, da0 = dn0, da1 = dn1;
   }
@@ -904,21 +951,28 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
       for (int rq = 0; rq < 4; ++rq)
         dkv_probs_quad<MODE, false>(a, b, offw, static_cast<int>(q0), lane, wkv, doc_kv, s, dp, pb, dsb, mq, rq);
   }
-  // dV^T += dO^T P,  dK^T += Q^T dS  (k index: the 64 query rows), operands one step ahead
+  // dV^T += dO^T P,  dK^T += Q^T dS  (k index: the 64 query rows); a step is
+  // two MFMAs, so the operands are read TPD steps ahead into a ring
   __builtin_amdgcn_sched_barrier(0);
-  uint4 ta = lds_kmajor(b.d, 0, 0, lane), tb = lds_kmajor(b.q, 0, 0, lane);
+  constexpr int TPD = 3;
+  uint4 ta[TPD + 1], tb[TPD + 1];
+#pragma unroll
+  for (int i = 0; i < TPD; ++i) {
+    ta[i] = lds_kmajor_o(b.d, to, 16 * (i / 4), i % 4);
+    tb[i] = lds_kmajor_o(b.q, to, 16 * (i / 4), i % 4);
+  }
 #pragma unroll
   for (int st = 0; st < 16; ++st) {
     const int s4 = st / 4, md = st % 4;
-    uint4 tna = ta, tnb = tb;
-    if (st < 15) {
-      tna = lds_kmajor(b.d, 16 * ((st + 1) / 4), ((st + 1) % 4) * 32, lane);
-      tnb = lds_kmajor(b.q, 16 * ((st + 1) / 4), ((st + 1) % 4) * 32, lane);
+    if (st + TPD < 16) {
+      ta[(st + TPD) % (TPD + 1)] = lds_kmajor_o(b.d, to, 16 * ((st + TPD) / 4), (st + TPD) % 4);
+      tb[(st + TPD) % (TPD + 1)] = lds_kmajor_o(b.q, to, 16 * ((st + TPD) / 4), (st + TPD) % 4);
     }
-    dvT[md] = mfma32(ta, pb[s4], dvT[md]);
-    dkT[md] = mfma32(tb, dsb[s4], dkT[md]);
+    dvT[md] = mfma32(ta[st % (TPD + 1)], pb[s4], dvT[md]);
+    dkT[md] = mfma32(tb[st % (TPD + 1)], dsb[s4], dkT[md]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
-    ta = tna, tb = tnb;
   }
 }
 
@@ -1009,6 +1063,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
     kfl = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.table) + wkv * kTokRow + 16 + g * 8);
   }
   const int doc_kv = a.docs[wkv];
+  const TileOffs to = tile_offs(lane);
 
   f32x16_t dvT[4], dkT[4];
 #pragma unroll
@@ -1042,10 +1097,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
           const bool masked = !((wkv_lo + 31 <= q0) && (dse[e] <= wkv_lo));
           if (half == 0)
             dkv_tile<BS, MODE>(a, buf0, masked, offw[wave], tab, q0, lane, wkv_lo, doc_kv, kreg, vreg, kf, kfl, dvT,
-                               dkT);
+                               dkT, to);
           else
             dkv_tile<BS, MODE>(a, buf1, masked, offw[wave], tab, q0, lane, wkv_lo, doc_kv, kreg, vreg, kf, kfl, dvT,
-                               dkT);
+                               dkT, to);
         }
       }
     }

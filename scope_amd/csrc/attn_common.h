@@ -161,8 +161,30 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // 16-byte global -> LDS copy; the LDS address is dst_wave + 16·lane, where
 // dst_wave must be the same for the whole wavefront.
+//
+// Issued as inline assembly rather than through __builtin_amdgcn_global_load_lds:
+// while a builtin copy is in flight, the compiler's wait insertion treats the
+// LDS counter as out of order and waits with lgkmcnt(0) before every LDS
+// operand, so an operand read one step ahead is waited for at once together
+// with every younger read.  Hidden from the compiler, the copies leave the
+// LDS reads with exact lgkmcnt(N) waits.  The price is that the compiler
+// knows nothing of the copies: every reader of a copied buffer is ordered
+// after them by wait_vm0() and a barrier (each tile loop does both before it
+// touches the tile), and a workgroup waits for its copies before it exits.
+// M0 (the LDS base of the copy) is saved and restored around the copy.
 __device__ __forceinline__ void g2lds16(const void* src, void* dst_wave) {
-  __builtin_amdgcn_global_load_lds(const_cast<void*>(src), (lds_void_t*)dst_wave, 16, 0, 0);
+  const uint32_t m0v =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)dst_wave)));
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(keep)
+      : "v"(src), "s"(m0v)
+      : "memory");
 }
 
 // vmcnt(0): every global load of this wavefront (including global_load_lds) has landed
