@@ -747,10 +747,10 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
     const int r = (tid >> 4) + jj * 16, c = (tid & 15) ^ swz(r);
     if (part < 4) {
       const char* base = reinterpret_cast<const char*>(a.q + h * a.q_sh + q0 * a.q_st);
-      g2lds16(base + static_cast<uint32_t>((r * static_cast<int>(a.q_st) + c * 8) * 2), b.q + (jj * 256 + wave * 64) * 8);
+      g2lds16(base, static_cast<uint32_t>((r * static_cast<int>(a.q_st) + c * 8) * 2), b.q + (jj * 256 + wave * 64) * 8);
     } else {
       const char* base = reinterpret_cast<const char*>(a.dout + h * a.o_sh + q0 * a.o_st);
-      g2lds16(base + static_cast<uint32_t>((r * static_cast<int>(a.o_st) + c * 8) * 2), b.d + (jj * 256 + wave * 64) * 8);
+      g2lds16(base, static_cast<uint32_t>((r * static_cast<int>(a.o_st) + c * 8) * 2), b.d + (jj * 256 + wave * 64) * 8);
     }
     return;
   }
@@ -761,14 +761,14 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
                        : wave == 1 ? reinterpret_cast<const char*>(a.delta + hT + q0)
                        : wave == 2 ? reinterpret_cast<const char*>(a.docs + q0)
                                    : reinterpret_cast<const char*>(a.b0 + hT + q0);
-    if (lane < 16 && (wave < 3 || (MODE >= 2 && a.subtract_b0))) g2lds16(base + lo, b.ra + wave * 64);
+    if (lane < 16 && (wave < 3 || (MODE >= 2 && a.subtract_b0))) g2lds16(base, lo, b.ra + wave * 64);
     if (MODE >= 2) {
       // token terms: slope, delta_main, width on wavefronts 0, 1, 2
       const char* tb = wave == 0   ? reinterpret_cast<const char*>(a.slope + hT + q0)
                        : wave == 1 ? reinterpret_cast<const char*>(a.delta_main + hT + q0)
                                    : reinterpret_cast<const char*>(a.width + hT + q0);
       const bool need = wave == 0 ? a.use_slope != 0 : (wave < 3 && MODE == 3);
-      if (lane < 16 && need) g2lds16(tb + lo, b.rc + wave * 64);
+      if (lane < 16 && need) g2lds16(tb, lo, b.rc + wave * 64);
     }
     return;
   }
@@ -776,12 +776,12 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
     // [64][K] cos rows on wavefronts 0-1, sin rows on 2-3
     const int ci = (wave & 1) * 64 + lane;
     const char* base = reinterpret_cast<const char*>((wave < 2 ? a.coeff_cos : a.coeff_sin) + (hT + q0) * a.K);
-    if (ci < 16 * a.K) g2lds16(base + static_cast<uint32_t>(ci) * 16, b.rb + (wave >> 1) * 512 + (wave & 1) * 256);
+    if (ci < 16 * a.K) g2lds16(base, static_cast<uint32_t>(ci) * 16, b.rb + (wave >> 1) * 512 + (wave & 1) * 256);
   }
   if (MODE >= 2) {
     const int r = tid >> 2, c = (tid & 3) ^ ((r >> 2) & 3);
     const char* base = reinterpret_cast<const char*>(a.qfeat + (hT + q0) * kTokRow);
-    g2lds16(base + static_cast<uint32_t>((r * kTokRow + c * 8) * 2), reinterpret_cast<uint16_t*>(b.rb) + wave * 64 * 8);
+    g2lds16(base, static_cast<uint32_t>((r * kTokRow + c * 8) * 2), reinterpret_cast<uint16_t*>(b.rb) + wave * 64 * 8);
   }
 }
 

@@ -159,8 +159,9 @@ __device__ __forceinline__ uint4 lds_kmajor_32(const uint16_t* tile, int k0, int
 // ---- direct global -> LDS copies ----------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// 16-byte global -> LDS copy; the LDS address is dst_wave + 16·lane, where
-// dst_wave must be the same for the whole wavefront.
+// 16-byte global -> LDS copy of base + off (off per lane, base the same for
+// the whole wavefront) to LDS address dst_wave + 16·lane (dst_wave the same
+// for the whole wavefront): global_load_lds_dwordx4 with a scalar base.
 //
 // Issued as inline assembly rather than through __builtin_amdgcn_global_load_lds:
 // while a builtin copy is in flight, the compiler's wait insertion treats the
@@ -172,18 +173,24 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // after them by wait_vm0() and a barrier (each tile loop does both before it
 // touches the tile), and a workgroup waits for its copies before it exits.
 // M0 (the LDS base of the copy) is saved and restored around the copy.
-__device__ __forceinline__ void g2lds16(const void* src, void* dst_wave) {
+__device__ __forceinline__ void g2lds16(const void* base, uint32_t off, void* dst_wave) {
+  // (readfirstlane returns int: each half goes through uint32_t before widening,
+  // or the low half would be sign-extended into the high one)
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
   const uint32_t m0v =
       __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)dst_wave)));
   uint32_t keep;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
+      "s_mov_b32 m0, %3\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(keep)
-      : "v"(src), "s"(m0v)
+      : "v"(off), "s"(sb), "s"(m0v)
       : "memory");
 }
 
@@ -348,14 +355,13 @@ __device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, 
     // idx%16, which holds the logical chunk (idx%16) ^ swz(row)
     const int idx = jj * NT + tid;
     const int r = idx >> 4, c = (idx & 15) ^ swz(r);
-    g2lds16(kbase + static_cast<uint32_t>((r * static_cast<int>(a.k_st) + c * 8) * 2), b.k + (jj * NT + wave * 64) * 8);
-    g2lds16(vbase + static_cast<uint32_t>((r * static_cast<int>(a.v_st) + c * 8) * 2), b.v + (jj * NT + wave * 64) * 8);
+    g2lds16(kbase, static_cast<uint32_t>((r * static_cast<int>(a.k_st) + c * 8) * 2), b.k + (jj * NT + wave * 64) * 8);
+    g2lds16(vbase, static_cast<uint32_t>((r * static_cast<int>(a.v_st) + c * 8) * 2), b.v + (jj * NT + wave * 64) * 8);
   }
-  if (wave == 0 && lane < 16) g2lds16(reinterpret_cast<const char*>(a.docs + k0) + lane * 16, b.docs);
+  if (wave == 0 && lane < 16) g2lds16(a.docs + k0, lane * 16, b.docs);
   if (MODE == 1 && wave == 1 && lane < 4) {
     const int rd = __builtin_amdgcn_readfirstlane(rdist);
-    g2lds16(reinterpret_cast<const char*>(static_cast<const float*>(a.table) + static_cast<int64_t>(rd) * 16) + lane * 16,
-            b.tab);
+    g2lds16(static_cast<const float*>(a.table) + static_cast<int64_t>(rd) * 16, lane * 16, b.tab);
   }
   if (MODE >= 2) {
     const char* fbase = reinterpret_cast<const char*>(static_cast<const uint16_t*>(a.table) + k0 * kTokRow);
@@ -364,7 +370,7 @@ __device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, 
       const int idx = idx0 + tid;
       const int r = idx >> 2, c = (idx & 3) ^ ((r >> 2) & 3);
       if (idx < 256)
-        g2lds16(fbase + static_cast<uint32_t>((r * kTokRow + c * 8) * 2), b.f + (idx0 + wave * 64) * 8);
+        g2lds16(fbase, static_cast<uint32_t>((r * kTokRow + c * 8) * 2), b.f + (idx0 + wave * 64) * 8);
     }
   }
 }
