@@ -589,8 +589,8 @@ def main():
     # (6·bs²·D) and the kv-major pass dK, dV (4·bs²·D); its S/dP recompute is
     # not counted.
     per_kernel = {"attn_fwd": (F_fwd, "attn_fwd_kernel"),
-                  "attn_bwd_dq": (6.0 * bs * bs * D * n_act, "attn_bwd_dq_kernel"),
-                  "attn_bwd_dkv": (4.0 * bs * bs * D * n_act, "attn_bwd_dkv_kernel")}
+                  "attn_bwd_dq": (6.0 * bs * bs * D * n_act, "attn_bwd_dq2_kernel" if bs == 256 else "attn_bwd_dq_kernel"),
+                  "attn_bwd_dkv": (4.0 * bs * bs * D * n_act, "attn_bwd_dkv16_kernel")}
     dom = max(per_kernel, key=lambda p: ph[p])
     flops, kname = per_kernel[dom]
     achieved = flops / (ph[dom] / 1e3) / 1e12

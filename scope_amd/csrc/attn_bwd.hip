@@ -12,10 +12,13 @@
 //   token mode through extra MFMAs over the key features (bf16 hi + lo)
 //   (C_k = Σ_j dS cos ω_k j, S_k = Σ_j dS sin ω_k j), slope / b0 / gate per element.
 // Plan: per key block, its q-list is cut into chunks of kChunk q-blocks.
-// Pass B (kv-major, one workgroup per (head, key block, chunk)): dK, dV over
-//   the q-list; a block with one chunk writes bf16 directly, longer lists
-//   write fp32 partials that a reduce kernel sums in chunk order
-//   (deterministic, no floating-point atomics).
+// Pass B (kv-major, one workgroup per (head, 128 keys of a key block, chunk)):
+//   dK, dV over the q-list; a block with one chunk writes bf16 directly,
+//   longer lists write fp32 partials that a reduce kernel sums in chunk order
+//   (deterministic, no floating-point atomics).  Modes 0 and 1 run 16 keys
+//   per wavefront on v_mfma_f32_16x16x32_bf16, eight wavefronts in two
+//   staggered groups (attn_bwd_dkv16_kernel); the token modes run 32 keys per
+//   wavefront on the 32x32x16 form, four wavefronts (attn_bwd_dkv_kernel).
 #include <math.h>
 
 #include "attn_common.h"
@@ -1138,6 +1141,338 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   }
 }
 
+// ---------------------------------------------------------------------------
+// pass B, 16 keys per wavefront (modes 0 and 1)
+// ---------------------------------------------------------------------------
+// Eight wavefronts of 16 keys share a workgroup of 128 keys, two wavefronts
+// per SIMD, so that one wavefront's probabilities run under the other's
+// matrix products.  Per 64-row query tile a wavefront computes, with
+// v_mfma_f32_16x16x32_bf16:
+//   S = Q·K^T, dP = dO·V^T   (M = 16 query rows × 4, N = its 16 keys, K and V
+//                             of those keys held in registers as B operands)
+//   dV^T += dO^T·P, dK^T += Q^T·dS   (M = 16 columns of D × 8, K = 64 rows)
+// The S accumulator of row block mb holds rows 16mb + 4g + r (g = lane / 16)
+// for key lane % 16, so P and dS are the B operands of the second pair with
+// no data movement: k-step kk takes slots 0-3 from row block 2kk and slots
+// 4-7 from row block 2kk+1; the transpose reads of dO^T and Q^T use the same
+// row order.
+
+// P and dS of one tile for this lane's key as the B operands of the
+// transposed products (pb[kk], dsb[kk]: k-step kk, see above).
+template <int MODE, bool MASK>
+__device__ __forceinline__ void dkv16_probs(const DkvBuf<MODE>& b, const float* offw, float cs, int q0, int wkv,
+                                            int doc_kv, int g, const f32x4_t (&s)[4], const f32x4_t (&dp)[4],
+                                            uint4 (&pb)[2], uint4 (&dsb)[2]) {
+  const int* docq = reinterpret_cast<const int*>(b.ra + 128);
+  uint32_t pw[8], dw[8];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int qi0 = 16 * mb + 4 * g;  // rows qi0 .. qi0+3 of the tile
+    const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
+    const float4 dl4 = *reinterpret_cast<const float4*>(&b.ra[64 + qi0]);
+    const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
+    const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
+    int dcv[4] = {0, 0, 0, 0};
+    if (MASK) {
+      const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
+      dcv[0] = dc4.x, dcv[1] = dc4.y, dcv[2] = dc4.z, dcv[3] = dc4.w;
+    }
+    float pv[4], dv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = fmaf(s[mb][i], cs, ofv[i]);
+      if (MASK) x = mask_score(x, wkv, q0 + qi0 + i, doc_kv, dcv[i]);
+      const float p = __builtin_amdgcn_exp2f(x);
+      pv[i] = p;
+      dv[i] = p * (dp[mb][i] - dlv[i]);
+    }
+    pw[2 * mb] = cvt_pk_bf16(pv[0], pv[1]);
+    pw[2 * mb + 1] = cvt_pk_bf16(pv[2], pv[3]);
+    dw[2 * mb] = cvt_pk_bf16(dv[0], dv[1]);
+    dw[2 * mb + 1] = cvt_pk_bf16(dv[2], dv[3]);
+  }
+  pb[0] = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+  pb[1] = make_uint4(pw[4], pw[5], pw[6], pw[7]);
+  dsb[0] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+  dsb[1] = make_uint4(dw[4], dw[5], dw[6], dw[7]);
+}
+
+// Lane byte offsets of the 16x16 operand reads of a swizzled tile.
+// Row reads: at k-step ks lane group g takes columns 32g + 8ks .. +7 (the
+// k order of the contraction is free as long as both operands follow it; with
+// 4ks + g instead, the b128 reads of 64 lanes conflict two ways).
+struct TileOffs16 {
+  uint32_t row[4];  // row c = lane % 16, columns 32g + 8·ks .. +7 (g = lane / 16)
+  uint32_t tr[8];   // transpose read: row 4g + (c / 4), columns 16·md + 4·(c % 4) .. +3
+};
+
+__device__ __forceinline__ TileOffs16 tile_offs16(int lane) {
+  TileOffs16 o;
+  const int g = lane >> 4, c = lane & 15, s = c >> 2, t = c & 3;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) o.row[ks] = 2u * static_cast<uint32_t>(swz_off(c, 32 * g + 8 * ks));
+#pragma unroll
+  for (int md = 0; md < 8; ++md) o.tr[md] = 2u * static_cast<uint32_t>(swz_off(4 * g + s, 16 * md + 4 * t));
+  return o;
+}
+
+// A operand of k-step kk whose m index is column 16·md + lane % 16: rows
+// 32kk + 4g + 0..3 (slots 0-3) and 32kk + 16 + 4g + 0..3 (slots 4-7).
+__device__ __forceinline__ uint4 lds_kmajor16(const uint16_t* tile, const TileOffs16& o, int kk, int md) {
+  const char* base = reinterpret_cast<const char*>(tile) + kk * 32 * 256;
+  lds_bf16x4_t* plo = (lds_bf16x4_t*)(const_cast<char*>(base + o.tr[md]));
+  lds_bf16x4_t* phi = (lds_bf16x4_t*)(const_cast<char*>(base + 16 * 256 + o.tr[md]));
+  const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(plo));
+  const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(phi));
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+__device__ __forceinline__ uint4 lds_row16(const uint16_t* tile, const TileOffs16& o, int mb, int ks) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(tile) + mb * 16 * 256 + o.row[ks]);
+}
+
+// One 64-row query tile against this wavefront's 16 keys, first part:
+// per-row offsets, S and dP, then P and dS as bf16 B operands.
+template <int MODE>
+__device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, float* offw,
+                                        const float* tab, int q0, int lane, int wkv, int doc_kv,
+                                        const uint4 (&kreg)[4], const uint4 (&vreg)[4], const TileOffs16& to,
+                                        uint4 (&pb)[2], uint4 (&dsb)[2]) {
+  const int g = lane >> 4;
+  dkv_offsets<MODE>(a, b, offw, tab, lane);
+  f32x4_t s[4], dp[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    s[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    dp[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // step st = 4·ks + mb; operands read RA steps ahead into a ring
+  constexpr int RA = 2;
+  uint4 qa[RA + 1], da[RA + 1];
+#pragma unroll
+  for (int i = 0; i < RA; ++i) {
+    qa[i] = lds_row16(b.q, to, i % 4, i / 4);
+    da[i] = lds_row16(b.d, to, i % 4, i / 4);
+  }
+#pragma unroll
+  for (int st = 0; st < 16; ++st) {
+    const int ks = st / 4, mb = st % 4;
+    if (st + RA < 16) {
+      qa[(st + RA) % (RA + 1)] = lds_row16(b.q, to, (st + RA) % 4, (st + RA) / 4);
+      da[(st + RA) % (RA + 1)] = lds_row16(b.d, to, (st + RA) % 4, (st + RA) / 4);
+    }
+    s[mb] = mfma16(qa[st % (RA + 1)], kreg[ks], s[mb]);
+    dp[mb] = mfma16(da[st % (RA + 1)], vreg[ks], dp[mb]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (masked)
+    dkv16_probs<MODE, true>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb);
+  else
+    dkv16_probs<MODE, false>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb);
+}
+
+// Second part: dV^T += dO^T P, dK^T += Q^T dS (step st = 8·kk + md).
+template <int MODE>
+__device__ __forceinline__ void dkv16_b(const DkvBuf<MODE>& b, const TileOffs16& to, const uint4 (&pb)[2],
+                                        const uint4 (&dsb)[2], f32x4_t (&dvT)[8], f32x4_t (&dkT)[8]) {
+  constexpr int RB = 2;
+  uint4 ta[RB + 1], tb[RB + 1];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    ta[i] = lds_kmajor16(b.d, to, i / 8, i % 8);
+    tb[i] = lds_kmajor16(b.q, to, i / 8, i % 8);
+  }
+#pragma unroll
+  for (int st = 0; st < 16; ++st) {
+    const int kk = st / 8, md = st % 8;
+    if (st + RB < 16) {
+      ta[(st + RB) % (RB + 1)] = lds_kmajor16(b.d, to, (st + RB) / 8, (st + RB) % 8);
+      tb[(st + RB) % (RB + 1)] = lds_kmajor16(b.q, to, (st + RB) / 8, (st + RB) % 8);
+    }
+    dvT[md] = mfma16(ta[st % (RB + 1)], pb[kk], dvT[md]);
+    dkT[md] = mfma16(tb[st % (RB + 1)], dsb[kk], dkT[md]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int BS, int MODE>
+__global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan pl) {
+  static_assert(MODE <= 1, "token modes use attn_bwd_dkv_kernel");
+  constexpr int D = 128;
+  constexpr int BM = 64;  // query rows per staged tile
+  constexpr int NS = BS / BM;
+
+  __shared__ DkvBuf<MODE> buf0, buf1, buf2;
+  __shared__ __attribute__((aligned(16))) float offw[8][BM];
+  __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunk * 16 : 4];
+  __shared__ int qbs[kChunk], dse[kChunk];
+
+  constexpr int P = BS / 128;  // workgroups (128 keys each) per key block
+  const int NB = a.QB;
+  // 1-D grid, XCD-aware, as attn_bwd_dkv_kernel
+  const int L = blockIdx.x;
+  const int per_xcd = gridDim.x / 8 / P;
+  const int pair = (L / 8) / P, zpart = (L / 8) % P;
+  const int item = (L % 8) * per_xcd + pair;
+  if (item >= a.H * pl.max_items) return;
+  const int h = item / pl.max_items;
+  const int x = item % pl.max_items;
+  const int32_t* its = pl.items_start + static_cast<int64_t>(h) * (NB + 1);
+  if (x >= its[NB]) return;
+  int lo = 0, hi = NB - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (its[mid] <= x) lo = mid;
+    else hi = mid - 1;
+  }
+  const int kb = lo;
+  const int chunk = x - its[kb];
+  const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
+  const int nq = qo[kb + 1] - qo[kb];
+  const int nch = max(1, (nq + kChunk - 1) / kChunk);
+  const int i0 = chunk * kChunk, i1 = min(nq, i0 + kChunk);
+  const int ne = max(0, i1 - i0);
+  const int32_t* ql = a.q_list + static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64, g = lane / 16, c = lane % 16;
+  const int64_t kv0 = static_cast<int64_t>(kb) * BS + zpart * 128;  // first key row of this workgroup
+  const int wkv_lo = static_cast<int>(kv0) + wave * 16;
+  const int wkv = wkv_lo + c;
+  const int krow = zpart * 128 + wave * 16 + c;  // key row within the block
+  const int64_t hT = static_cast<int64_t>(h) * a.T;
+
+  const int qb_first = ne > 0 ? ql[i0] : 0;
+  const int skip0 = ne > 0 && qb_first == kb ? (zpart * 128) / BM : 0;
+  const int n_it = ne * NS - skip0;
+
+  if (tid < ne) {
+    const int qb = ql[i0 + tid];
+    qbs[tid] = qb;
+    dse[tid] = a.ds_tok_end[qb];
+  }
+  if (MODE == 1 && tid < ne * 16) {
+    const int r = min(max(ql[i0 + tid / 16] - kb, 0), NB - 1);
+    tabs[tid] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + tid % 16];
+  }
+  if (n_it > 0 && wave < 4) {
+    const int64_t q0 = static_cast<int64_t>(qb_first) * BS + (skip0 % NS) * BM;
+    dkv_issue<MODE>(a, h, hT, q0, buf0, tid);
+  }
+
+  uint4 kreg[4], vreg[4];
+  {
+    // k-step ks: columns 32g + 8ks .. +7, the order of the row reads
+    const uint16_t* kp = a.k + h * a.k_sh + static_cast<int64_t>(wkv) * a.k_st + g * 32;
+    const uint16_t* vp = a.v + h * a.v_sh + static_cast<int64_t>(wkv) * a.v_st + g * 32;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      kreg[ks] = *reinterpret_cast<const uint4*>(kp + ks * 8);
+      vreg[ks] = *reinterpret_cast<const uint4*>(vp + ks * 8);
+    }
+  }
+  const int doc_kv = a.docs[wkv];
+  const TileOffs16 to = tile_offs16(lane);
+
+  f32x4_t dvT[8], dkT[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    dvT[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    dkT[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  auto tile_q0 = [&](int j, int& e) __attribute__((always_inline)) {
+    const int f = j + skip0;
+    e = f / NS;
+    return qbs[e] * BS + (f % NS) * BM;
+  };
+  // Wavefronts 0-3 (one per SIMD) process whole tiles and copy them into
+  // three rotating buffers (256 threads); wavefronts 4-7 run half a tile
+  // behind: their k-th barrier falls between the first and the second part
+  // of tile k-1, so each SIMD holds one wavefront in its probabilities while
+  // the other runs MFMAs.  At the leading group's k-th barrier the lagging
+  // group is done with tile k-2, whose buffer then takes tile k+1.  Both
+  // groups pass n_it + 1 barriers.
+  auto part_a = [&](const DkvBuf<MODE>& bc, int j, uint4 (&pb)[2], uint4 (&dsb)[2]) __attribute__((always_inline)) {
+    int e;
+    const int q0 = tile_q0(j, e);
+    if (q0 + BM - 1 < wkv_lo) return false;  // every query row precedes this wavefront's keys
+    const bool masked = !((wkv_lo + 15 <= q0) && (dse[e] <= wkv_lo));
+    const float* tab = tabs + (MODE == 1 ? e * 16 : 0);
+    dkv16_a<MODE>(a, bc, masked, offw[wave], tab, q0, lane, wkv, doc_kv, kreg, vreg, to, pb, dsb);
+    return true;
+  };
+  if (wave < 4) {
+    int j = 0;
+    auto lead = [&](const DkvBuf<MODE>& bc, DkvBuf<MODE>& bn) __attribute__((always_inline)) {
+      wait_vm0();
+      __syncthreads();  // tile j is in bc for everyone; the lagging group is done with bn
+      if (j + 1 < n_it) {
+        int en;
+        dkv_issue<MODE>(a, h, hT, tile_q0(j + 1, en), bn, tid);
+      }
+      uint4 pb[2], dsb[2];
+      if (part_a(bc, j, pb, dsb)) dkv16_b<MODE>(bc, to, pb, dsb, dvT, dkT);
+      ++j;
+    };
+    while (j < n_it) {
+      lead(buf0, buf1);
+      if (j >= n_it) break;
+      lead(buf1, buf2);
+      if (j >= n_it) break;
+      lead(buf2, buf0);
+    }
+    __syncthreads();  // matches the lagging group's last barrier
+  } else {
+    __syncthreads();  // tile 0 is in buf0
+    int j = 0;
+    auto lag = [&](const DkvBuf<MODE>& bc) __attribute__((always_inline)) {
+      uint4 pb[2], dsb[2];
+      const bool act = part_a(bc, j, pb, dsb);
+      __syncthreads();  // the leading group starts the next tile
+      if (act) dkv16_b<MODE>(bc, to, pb, dsb, dvT, dkT);
+      ++j;
+    };
+    while (j < n_it) {
+      lag(buf0);
+      if (j >= n_it) break;
+      lag(buf1);
+      if (j >= n_it) break;
+      lag(buf2);
+    }
+  }
+  wait_vm0();  // no copy may still target LDS when the workgroup exits
+
+  // ---- write dK = scale·dkT^T, dV = dvT^T: lane holds columns 16md + 4g .. +3 of key wkv
+  if (nch == 1) {
+    uint16_t* dkp = a.dk + h * a.k_sh + static_cast<int64_t>(wkv) * a.k_st + 4 * g;
+    uint16_t* dvp = a.dv + h * a.v_sh + static_cast<int64_t>(wkv) * a.v_st + 4 * g;
+#pragma unroll
+    for (int md = 0; md < 8; ++md) {
+      uint2 vk, vv;
+      vk.x = cvt_pk_bf16(dkT[md][0] * a.scale, dkT[md][1] * a.scale);
+      vk.y = cvt_pk_bf16(dkT[md][2] * a.scale, dkT[md][3] * a.scale);
+      vv.x = cvt_pk_bf16(dvT[md][0], dvT[md][1]);
+      vv.y = cvt_pk_bf16(dvT[md][2], dvT[md][3]);
+      *reinterpret_cast<uint2*>(dkp + md * 16) = vk;
+      *reinterpret_cast<uint2*>(dvp + md * 16) = vv;
+    }
+  } else {
+    const int64_t slot = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb] + chunk;
+    float* pk = pl.part_dk + (slot * BS + krow) * D + 4 * g;
+    float* pv = pl.part_dv + (slot * BS + krow) * D + 4 * g;
+#pragma unroll
+    for (int md = 0; md < 8; ++md) {
+      *reinterpret_cast<float4*>(pk + md * 16) = make_float4(dkT[md][0], dkT[md][1], dkT[md][2], dkT[md][3]);
+      *reinterpret_cast<float4*>(pv + md * 16) = make_float4(dvT[md][0], dvT[md][1], dvT[md][2], dvT[md][3]);
+    }
+  }
+}
+
 // Sum the chunk partials of every multi-chunk key block in chunk order.
 __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl, int BS) {
   constexpr int D = 128;
@@ -1231,7 +1566,13 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
   if (phases & SCOPE_BWD_DKV_PLAN)
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start));
-  if (phases & SCOPE_BWD_DKV_MAIN) {
+  if ((phases & SCOPE_BWD_DKV_MAIN) && mode != SCOPE_BIAS_TOKEN) {
+    // 16 keys per wavefront, 8 wavefronts (two per SIMD) per 128 keys
+    if (mode == SCOPE_BIAS_BLOCK)
+      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1>), gk, dim3(512), 0, s, a, pl);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0>), gk, dim3(512), 0, s, a, pl);
+  } else if (phases & SCOPE_BWD_DKV_MAIN) {
     if (mode == SCOPE_BIAS_BLOCK)
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
     else if (mode == SCOPE_BIAS_TOKEN && gate)

@@ -27,6 +27,16 @@ __device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, const
                                                  0, 0, 0);
 }
 
+// v_mfma_f32_16x16x32_bf16 (wave64), lane l, g = l / 16, c = l % 16:
+//   A (16 x 32, M x K): row c, k = 8g .. 8g+7;  B (32 x 16, K x N): col c,
+//   k = 8g .. 8g+7;  C (16 x 16): col c, register r -> row 4g + r.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                 0, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   bf16x2_t v;
   v[0] = static_cast<__bf16>(lo);
@@ -51,11 +61,17 @@ __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
 
 // ---- swizzled row-major LDS tiles -------------------------------------------
 // A tile row holds 128 bf16 (256 bytes = all 64 banks).  The 16-byte chunk c
-// of row r is stored at chunk c ^ swz(r), swz(r) = 4·(r%4) + (r/4)%4.  With
-// this mapping both access patterns below are bank-conflict free:
-//   * row reads (16 lanes, 16 consecutive rows, same logical chunk), and
-//   * transpose reads (16 lanes, 4 rows × 4 eight-byte column groups).
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+// of row r is stored at chunk c ^ swz(r), swz(r) = 4·(r%4) + 2·b2 + b3 with
+// b2, b3 the bits 2 and 3 of r.  With this mapping these access patterns are
+// bank-conflict free:
+//   * row reads (16 lanes, 16 consecutive rows, same logical chunk),
+//   * transpose reads of the 32x32 operands (32 lanes, 4 rows × 8 eight-byte
+//     column groups), and
+//   * transpose reads of the 16x16 operands (32 lanes: rows 4g .. 4g+3 of
+//     lane group g = 0, 1, the same 4 column groups): bits 1-3 of swz(r)
+//     encode r mod 8, so the 8 rows of the two groups land on 8 distinct
+//     chunk pairs.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
 // element offset of (row r, column d) in a swizzled tile
 __device__ __forceinline__ int swz_off(int r, int d) { return r * 128 + (((d >> 3) ^ swz(r)) << 3) + (d & 7); }
 
