@@ -451,7 +451,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   constexpr int BN = 64;      // keys per staged tile, processed in two 32-key halves
   constexpr int NSUB = BS / BN;
 
-  __shared__ KvTile<MODE> buf0, buf1;
+  __shared__ KvTile<MODE> buf0, buf1, buf2;
   __shared__ int kbs[kListLds];
   // block mode: β·log2e-scaled coefficients [BS][cos 8 | sin 8] and the
   // coefficient-gradient sums [BS][Σrs·cos 8 | Σpm·cos 8 | Σrs·sin 8 | Σpm·sin 8]
@@ -533,7 +533,23 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     const int rd = min(max(qb - kb, 0), a.QB - 1);
     kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
   };
-  auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
+  // One tile in two parts.  Part A: scores, probabilities and dQ of the
+  // first 32-key half, then scores and probabilities of the second (its dS^T
+  // returned in dsb1); part B: the second half's dQ.
+  auto dq_half = [&](const KvTile<MODE>& b, int mb, const uint4 (&dsb)[2]) __attribute__((always_inline)) {
+    // dQ^T += K^T dS^T over keys mb·32 .. +31 (step st: k-step 2·mb + st/4, columns 32·(st%4))
+    uint4 ta[2];
+    ta[0] = lds_kmajor_o(b.k, to, 32 * mb, 0);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      if (st + 1 < 8) ta[(st + 1) % 2] = lds_kmajor_o(b.k, to, 16 * (2 * mb + (st + 1) / 4), (st + 1) % 4);
+      o[st % 4] = mfma32(ta[st % 2], dsb[st / 4], o[st % 4]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto compute_a = [&](int kv0, const KvTile<MODE>& b, uint4 (&dsb1)[2]) __attribute__((always_inline)) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
     const float off = (MODE == 1 ? bt : 0.f) - R.lse2;
     float rs = 0.f, pm = 0.f;
@@ -562,23 +578,20 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
         dq2_probs<MODE, true>(b, R, kv0, off, cs, lane, mb, s, dp, dsb, rs, pm);
       else
         dq2_probs<MODE, false>(b, R, kv0, off, cs, lane, mb, s, dp, dsb, rs, pm);
-      // dQ^T += K^T dS^T over these 32 keys (step st: k-step 2·mb + st/4, columns 32·(st%4))
-      uint4 ta[2];
-      ta[0] = lds_kmajor_o(b.k, to, 32 * mb, 0);
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        if (st + 1 < 8) ta[(st + 1) % 2] = lds_kmajor_o(b.k, to, 16 * (2 * mb + (st + 1) / 4), (st + 1) % 4);
-        o[st % 4] = mfma32(ta[st % 2], dsb[st / 4], o[st % 4]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_barrier(0);
+      if (mb == 0) {
+        dq_half(b, 0, dsb);
+      } else {
+        dsb1[0] = dsb[0];
+        dsb1[1] = dsb[1];
       }
     }
     rs_kb += rs;
     pm_kb += pm;
     rs_tot += rs;
   };
-  auto run = [&](int it, int nxt, const KvTile<MODE>& b) __attribute__((always_inline)) {
+  // part A of tile it with the block-mode bookkeeping; false when the
+  // wavefront has nothing to do for this tile
+  auto run_a = [&](int it, int nxt, const KvTile<MODE>& b, uint4 (&dsb1)[2]) __attribute__((always_inline)) -> bool {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (MODE == 1 && it % NSUB == 0) {
       // block term of this key block (its first tile is never skipped)
@@ -591,7 +604,8 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
       }
       bt = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     }
-    if (kv0 <= wrow_lo + 31) compute(kv0, b);  // else every key follows this wavefront's rows
+    const bool act = kv0 <= wrow_lo + 31;  // else every key follows this wavefront's rows
+    if (act) compute_a(kv0, b, dsb1);
     if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
       // last tile of this key block: fold the row sums (combined over the lane
       // pair) into the gradient sums; g = 0 keeps the cos half, g = 1 the sin half
@@ -610,25 +624,60 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
       }
       rs_kb = pm_kb = 0.f;
     }
+    return act;
   };
 
   __syncthreads();  // kbs
+  // Wavefronts 0-3 (one per SIMD) process whole tiles and copy them (256
+  // threads) into three rotating buffers; wavefronts 4-7 run part of a tile
+  // behind: their k-th barrier falls between part A and part B of tile k-1,
+  // so the two wavefronts of a SIMD are not in the same phase.  At the
+  // leading group's k-th barrier the lagging group is done with tile k-2,
+  // whose buffer then takes tile k+1.  Both groups pass n+1 barriers for n
+  // tiles.
+  const int tid4 = tid & 255;
+  auto issue4 = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
+    const int kb = kb_at(it / NSUB);
+    const int rd = min(max(qb - kb, 0), a.QB - 1);
+    kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid4);
+  };
   int cur = next_valid(0);
-  if (cur < total) issue(cur, buf0);
-  while (cur < total) {
-    wait_vm0();
-    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
-    int nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf1);
-    run(cur, nxt, buf0);
-    cur = nxt;
-    if (cur >= total) break;
-    wait_vm0();
-    __syncthreads();
-    nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf0);
-    run(cur, nxt, buf1);
-    cur = nxt;
+  if (wave < 4) {
+    if (cur < total) issue4(cur, buf0);
+    auto lead = [&](const KvTile<MODE>& bc, KvTile<MODE>& bn) __attribute__((always_inline)) {
+      wait_vm0();
+      __syncthreads();  // tile cur is in bc for everyone; the lagging group is done with bn
+      const int nxt = next_valid(cur + 1);
+      if (nxt < total) issue4(nxt, bn);
+      uint4 dsb1[2];
+      if (run_a(cur, nxt, bc, dsb1)) dq_half(bc, 1, dsb1);
+      cur = nxt;
+    };
+    while (cur < total) {
+      lead(buf0, buf1);
+      if (cur >= total) break;
+      lead(buf1, buf2);
+      if (cur >= total) break;
+      lead(buf2, buf0);
+    }
+    __syncthreads();  // matches the lagging group's last barrier
+  } else {
+    __syncthreads();  // tile 0 is in buf0
+    auto lag = [&](const KvTile<MODE>& bc) __attribute__((always_inline)) {
+      const int nxt = next_valid(cur + 1);
+      uint4 dsb1[2];
+      const bool act = run_a(cur, nxt, bc, dsb1);
+      __syncthreads();  // the leading group starts the next tile
+      if (act) dq_half(bc, 1, dsb1);
+      cur = nxt;
+    };
+    while (cur < total) {
+      lag(buf0);
+      if (cur >= total) break;
+      lag(buf1);
+      if (cur >= total) break;
+      lag(buf2);
+    }
   }
 
   // ---- epilogue: dQ = scale·o, coefficient gradients
