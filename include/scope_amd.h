@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SCOPE_ABI_VERSION 1
+#define SCOPE_ABI_VERSION 2
 
 enum {
   SCOPE_OK = 0,
@@ -115,6 +115,37 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
                          const int32_t* ds_ptr, const int32_t* ds_local, int32_t* kv_num,
                          int32_t* kv_idx /* [H,QB,W+budget+G] */, int32_t* picks /* [H,QB,budget] */,
                          float* logits_out /* [H,QB,NB] or NULL */, void* stream);
+
+/* Soft pointer weights (no reference counterpart: build_pointer_blockmask
+ * selects under torch.no_grad, model/attn_bias.py:623; this is the
+ * differentiable inclusion weight the block-scoring specification asks for).
+ * pair_bias [H,QB,W+budget+G] aligned with kv_idx: log σ(z/soft_temp) for
+ * the pick entries (z the noise-free selection logit, computed like
+ * scope_pointer_select computes it), 0 for window, global and padding
+ * entries.  It is the scope_attn_params.pair_bias input of the attention. */
+int scope_pointer_pair_bias(const scope_ptr_score_params* p, float soft_temp, const float* qbar,
+                            const float* kbar, const float* logits_in /* [H,QB,NB] or NULL */,
+                            const float* prior /* or NULL */, const int32_t* kv_num, const int32_t* kv_idx,
+                            const int32_t* picks /* [H,QB,budget] */, float* pair_bias, void* stream);
+
+/* Backward of the soft pointer weights: given dpair_bias (the attention
+ * backward's gradient of pair_bias), dz = dpair·(1 - e^pair)/soft_temp and
+ * the block-mean chain z = logit_scale·q̄·k̄ + prior add
+ *   dq[i] += logit_scale/bs · Σ_e dz[qb(i),e] k̄[kv_idx[qb(i),e]]
+ *   dk[j] += logit_scale/bs · Σ_{qb lists kb(j)} dz[qb, pos of kb(j)] q̄[qb]
+ * to dq, dk (bf16, in place; fixed summation order).  The prior is treated as
+ * a constant schedule (no gradient).  workspace: scope_pointer_bwd_workspace_bytes. */
+typedef struct {
+  int H, NB, D, bs, maxkv;
+  float logit_scale, soft_temp;
+  int64_t q_sh, q_st, k_sh, k_st; /* element strides of dq, dk [H, T, D] */
+} scope_ptr_bwd_params;
+
+int64_t scope_pointer_bwd_workspace_bytes(const scope_ptr_bwd_params* p);
+int scope_pointer_bwd(const scope_ptr_bwd_params* p, const float* qbar, const float* kbar,
+                      const int32_t* kv_num, const int32_t* kv_idx, const int32_t* q_off,
+                      const int32_t* q_list, const float* pair_bias, const float* dpair_bias, uint16_t* dq,
+                      uint16_t* dk, void* workspace, void* stream);
 
 /* ------------------------------------------------------------------------
  * Transposed (q-major) lists.  Replaces BlockMask.from_kv_blocks ->
@@ -283,6 +314,14 @@ typedef struct {
   int use_slope, subtract_b0, gate_kind;
   float ramp_lambda, tau;
   int64_t q_sh, q_st, k_sh, k_st, v_sh, v_st, o_sh, o_st;  /* element strides */
+  /* Soft pointer weights (no reference counterpart: the reference selects
+   * under torch.no_grad, model/attn_bias.py:623).  pair_bias [H, QB, maxkv]
+   * fp32, aligned with kv_idx, is added (natural-log units, not scaled by
+   * beta) to every score of the tile (q-block qb, key block kv_idx[h,qb,e]);
+   * NULL = none.  The backward writes its gradient, the tile sum of dS, to
+   * dpair_bias [H, QB, maxkv] (entries e >= kv_num: 0) when non-NULL. */
+  const float* pair_bias;
+  float* dpair_bias;
 } scope_attn_params;
 
 /* Spectral tables: block mode [NB][16] fp32 (cos ω_k r, sin ω_k r);

@@ -94,11 +94,14 @@ def bias_token(coeff_cos, coeff_sin, omegas, *, b0=None, slope=None, delta_main=
     return bias
 
 
-def attention_dense(q, k, v, allowed, bias=None, *, scale: float, beta: float = 0.5):
-    """q,k,v [H,T,D]; allowed [H,T,T] bool; bias [H,T,T] or None -> (out [H,T,D], lse [H,T])."""
+def attention_dense(q, k, v, allowed, bias=None, *, scale: float, beta: float = 0.5, extra=None):
+    """q,k,v [H,T,D]; allowed [H,T,T] bool; bias [H,T,T] or None (scaled by
+    beta); extra [H,T,T] or None (added as is) -> (out [H,T,D], lse [H,T])."""
     s = scale * torch.einsum("hid,hjd->hij", q, k)
     if bias is not None:
         s = s + beta * bias
+    if extra is not None:
+        s = s + extra
     s = s.masked_fill(~allowed, float("-inf"))
     lse = torch.logsumexp(s, dim=-1)
     safe = torch.where(torch.isinf(lse), torch.zeros_like(lse), lse)
@@ -109,10 +112,12 @@ def attention_dense(q, k, v, allowed, bias=None, *, scale: float, beta: float = 
 
 def attention_blocksparse(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: float, beta: float = 0.5,
                           bias_mode: str = "none", coeff_cos=None, coeff_sin=None, omegas=None,
-                          token_kwargs: dict | None = None, heads=None, qblocks=None):
+                          token_kwargs: dict | None = None, heads=None, qblocks=None, pair_bias=None):
     """Per (h, qb) gather of the listed key blocks; same semantics as
     ``attention_dense`` without a [T,T] tensor.  Returns dicts keyed by
-    (h, qb) -> (out [bs,D], lse [bs]) for the requested heads / q-blocks."""
+    (h, qb) -> (out [bs,D], lse [bs]) for the requested heads / q-blocks.
+    ``pair_bias`` [H,QB,L] (aligned with kv_idx) adds b[h,qb,e] to every
+    score of the tile (q-block qb, key block kv_idx[h,qb,e])."""
     H, T, D = q.shape
     docs = torch.as_tensor(docs).long()
     kv_num = torch.as_tensor(kv_num)
@@ -136,6 +141,8 @@ def attention_blocksparse(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: floa
                     if tk.get(key) is not None:
                         tk[key] = tk[key][h:h + 1]
                 s = s + beta * bias_token(coeff_cos[h:h + 1], coeff_sin[h:h + 1], omegas, rows=rows, cols=cols, **tk)[0]
+            if pair_bias is not None:
+                s = s + pair_bias[h, qb, :n].repeat_interleave(bs)[None, :]
             ok = (rows[:, None] >= cols[None, :]) & (docs[rows][:, None] == docs[cols][None, :])
             s = s.masked_fill(~ok, float("-inf"))
             lse = torch.logsumexp(s, dim=-1)
@@ -147,22 +154,36 @@ def attention_blocksparse(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: floa
 
 def scope_attention_blocksparse(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: float, beta: float = 0.5,
                                 bias_mode: str = "none", coeff_cos=None, coeff_sin=None, omegas=None,
-                                token_kwargs: dict | None = None):
+                                token_kwargs: dict | None = None, pair_bias=None):
     """Differentiable block-sparse reference: (out [H,T,D], lse [H,T]) built
     from the per-(h, q-block) gathers, so autograd gives every gradient
     without a [T,T] tensor."""
     H, T, D = q.shape
     QB = T // bs
     res = attention_blocksparse(q, k, v, kv_num, kv_idx, docs, bs=bs, scale=scale, beta=beta, bias_mode=bias_mode,
-                                coeff_cos=coeff_cos, coeff_sin=coeff_sin, omegas=omegas, token_kwargs=token_kwargs)
+                                coeff_cos=coeff_cos, coeff_sin=coeff_sin, omegas=omegas, token_kwargs=token_kwargs,
+                                pair_bias=pair_bias)
     out = torch.stack([torch.cat([res[(h, qb)][0] for qb in range(QB)], 0) for h in range(H)], 0)
     lse = torch.stack([torch.cat([res[(h, qb)][1] for qb in range(QB)], 0) for h in range(H)], 0)
     return out, lse
 
 
+def pair_bias_dense(pair_bias, kv_num, kv_idx, bs: int, T: int):
+    """[H,QB,L] per-list-entry bias -> dense [H,T,T] (zero off the lists)."""
+    H, QB, L = pair_bias.shape
+    NB = T // bs
+    blk = torch.zeros((H, QB, NB), dtype=pair_bias.dtype)
+    for h in range(H):
+        for qb in range(QB):
+            n = int(kv_num[h, qb])
+            idx = torch.as_tensor(kv_idx[h, qb, :n]).long()
+            blk = blk.index_put((torch.full_like(idx, h), torch.full_like(idx, qb), idx), pair_bias[h, qb, :n])
+    return blk.repeat_interleave(bs, dim=1).repeat_interleave(bs, dim=2)
+
+
 def scope_attention_reference(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: float, beta: float = 0.5,
                               bias_mode: str = "none", coeff_cos=None, coeff_sin=None, omegas=None,
-                              token_kwargs: dict | None = None):
+                              token_kwargs: dict | None = None, pair_bias=None):
     """Dense-masked reference with autograd: returns (out, lse)."""
     H, T, D = q.shape
     allowed = allowed_mask(kv_num, kv_idx, docs, bs, T)
@@ -171,7 +192,9 @@ def scope_attention_reference(q, k, v, kv_num, kv_idx, docs, *, bs: int, scale: 
         bias = bias_block(coeff_cos, coeff_sin, omegas, bs)
     elif bias_mode == "token":
         bias = bias_token(coeff_cos, coeff_sin, omegas, **(token_kwargs or {}))
-    return attention_dense(q, k, v, allowed, bias, scale=scale, beta=beta)
+    out, lse = attention_dense(q, k, v, allowed, bias, scale=scale, beta=beta,
+                               extra=None if pair_bias is None else pair_bias_dense(pair_bias, kv_num, kv_idx, bs, T))
+    return out, lse
 
 
 def block_mass(q, k, docs, *, bs: int, scale: float, beta: float = 0.5, bias_mode: str = "none", coeff_cos=None,
@@ -251,3 +274,29 @@ def omegas_logspaced(K: int, L_train: int, L_max: int) -> torch.Tensor:
     w_min = 2 * math.pi / L_max
     w_max = 2 * math.pi / L_train
     return torch.logspace(math.log10(w_min), math.log10(w_max), K, dtype=torch.float32)
+
+
+def soft_pointer_pair_bias(q, k, kv_num, kv_idx, picks, *, bs: int, logit_scale: float, soft_temp: float,
+                           prior=None):
+    """Differentiable soft top-k weights of the block-scoring picks (a
+    specification of this project): q̄, k̄ = block means of q, k [H,T,D];
+    z = logit_scale · q̄·k̄ + prior[qb-kb]; b = log σ(z/τ_w) on the pick
+    entries of the packed lists, 0 elsewhere.  Returns b [H,QB,L] with the
+    autograd graph back to q and k (the prior is a constant schedule)."""
+    H, T, D = q.shape
+    NB = T // bs
+    qbar = q.reshape(H, NB, bs, D).mean(dim=2)
+    kbar = k.reshape(H, NB, bs, D).mean(dim=2)
+    kv_idx = torch.as_tensor(kv_idx).long()
+    kv_num = torch.as_tensor(kv_num)
+    picks = torch.as_tensor(picks).long()
+    L = kv_idx.shape[-1]
+    hh = torch.arange(H)[:, None, None].expand(H, NB, L)
+    qq = torch.arange(NB)[None, :, None].expand(H, NB, L)
+    z = logit_scale * (qbar[hh, qq] * kbar[hh, kv_idx.clamp(0, NB - 1)]).sum(-1)
+    if prior is not None:
+        pr = torch.as_tensor(prior, dtype=z.dtype).reshape(-1, NB).expand(H, NB)
+        z = z + pr[hh, (qq - kv_idx).clamp(0, NB - 1)]
+    e = torch.arange(L)[None, None, :]
+    is_pick = (kv_idx[..., :, None] == picks[..., None, :]).any(-1) & (e < kv_num[..., None])
+    return torch.where(is_pick, torch.nn.functional.logsigmoid(z / soft_temp), torch.zeros_like(z))

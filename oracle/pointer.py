@@ -400,3 +400,27 @@ def pointer_select_blockscore(logits: np.ndarray, docs: np.ndarray, *, bs: int, 
             raw[h, qb] = np.asarray(win + sel + glb, dtype=np.int32)
     kv_num, packed = pack_sorted_unique(raw)
     return dict(kv_num=kv_num, packed=packed, picks=picks, ds_ptr=ds_ptr, ds_local=ds_local, maxkv=maxkv)
+
+
+def soft_pair_bias(logits: np.ndarray, kv_num: np.ndarray, kv_idx: np.ndarray, picks: np.ndarray, *,
+                   soft_temp: float) -> np.ndarray:
+    """Soft top-k weights of the pointer picks as an additive score bias per
+    list entry (a specification of this project; the reference selects under
+    ``torch.no_grad``, model/attn_bias.py:623).
+
+        b[h,qb,e] = log σ(logit[h,qb,kb]/τ_w)   for e < kv_num and kb = kv_idx[h,qb,e] a pick
+        b[h,qb,e] = 0                           for window, global and padding entries
+
+    ``logits`` are the noise-free block-scoring logits [H,QB,NB] (fp64)."""
+    H, QB, L = kv_idx.shape
+    out = np.zeros((H, QB, L), dtype=np.float64)
+    t = float(soft_temp)
+    for h in range(H):
+        for qb in range(QB):
+            pk = set(int(x) for x in picks[h, qb] if x >= 0)
+            for e in range(int(kv_num[h, qb])):
+                kb = int(kv_idx[h, qb, e])
+                if kb in pk:
+                    x = float(logits[h, qb, kb]) / t
+                    out[h, qb, e] = -np.logaddexp(0.0, -x)  # log σ(x)
+    return out

@@ -12,7 +12,7 @@ import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCOPE_AMD_LIB", os.path.join(HERE, "libscope_amd.so"))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 c_int, c_int64, c_float, c_void_p, c_char_p, c_uint64 = C.c_int, C.c_int64, C.c_float, C.c_void_p, C.c_char_p, C.c_uint64
 
@@ -43,7 +43,14 @@ class AttnParams(C.Structure):
                 ("beta", c_float), ("bias_mode", c_int), ("K", c_int), ("use_slope", c_int),
                 ("subtract_b0", c_int), ("gate_kind", c_int), ("ramp_lambda", c_float), ("tau", c_float),
                 ("q_sh", c_int64), ("q_st", c_int64), ("k_sh", c_int64), ("k_st", c_int64), ("v_sh", c_int64),
-                ("v_st", c_int64), ("o_sh", c_int64), ("o_st", c_int64)]
+                ("v_st", c_int64), ("o_sh", c_int64), ("o_st", c_int64), ("pair_bias", c_void_p),
+                ("dpair_bias", c_void_p)]
+
+
+class PtrBwdParams(C.Structure):
+    _fields_ = [("H", c_int), ("NB", c_int), ("D", c_int), ("bs", c_int), ("maxkv", c_int),
+                ("logit_scale", c_float), ("soft_temp", c_float), ("q_sh", c_int64), ("q_st", c_int64),
+                ("k_sh", c_int64), ("k_st", c_int64)]
 
 
 class CoeffParams(C.Structure):
@@ -70,6 +77,9 @@ _PROTOS = {
     "scope_pointer_mask_ref": (c_int, [C.POINTER(PtrRefParams), P, P, P, P, P, P, P, P, P, P]),
     "scope_block_means": (c_int, [P, P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int64, c_int64, P, P, P]),
     "scope_pointer_select": (c_int, [C.POINTER(PtrScoreParams), P, P, P, P, P, P, P, P, P, P, P, P]),
+    "scope_pointer_pair_bias": (c_int, [C.POINTER(PtrScoreParams), c_float, P, P, P, P, P, P, P, P, P]),
+    "scope_pointer_bwd_workspace_bytes": (c_int64, [C.POINTER(PtrBwdParams)]),
+    "scope_pointer_bwd": (c_int, [C.POINTER(PtrBwdParams)] + [P] * 12),
     "scope_transpose_workspace_bytes": (c_int64, [c_int, c_int]),
     "scope_transpose_blocks": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P, P, P]),
     "scope_coeff_head_workspace_bytes": (c_int64, [C.POINTER(CoeffParams)]),

@@ -70,30 +70,75 @@ def _kwargs(sp: SpectralTerms | None, bm: ScopeBlockMask):
 
 class _ScopeAttnFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, cc, cs, b0, slope, dm, wd, bm: ScopeBlockMask, sp: SpectralTerms | None, scale: float):
+    def forward(ctx, q, k, v, cc, cs, b0, slope, dm, wd, pb, bm: ScopeBlockMask, sp: SpectralTerms | None,
+                scale: float):
         kw = _kwargs(sp, bm)
         out, lse = ops.attn_fwd(q, k, v, bm.kv_num_blocks[0], bm.kv_indices[0], bm.docs, bm.ds_tok_end,
                                 bs=bm.BLOCK_SIZE, scale=scale, coeff_cos=cc, coeff_sin=cs, b0=b0, slope=slope,
-                                delta_main=dm, width=wd, **kw)
-        ctx.save_for_backward(q, k, v, out, lse, cc, cs, b0, slope, dm, wd)
+                                delta_main=dm, width=wd, pair_bias=pb, **kw)
+        ctx.save_for_backward(q, k, v, out, lse, cc, cs, b0, slope, dm, wd, pb)
         ctx.bm, ctx.sp, ctx.scale = bm, sp, scale
         ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, _dlse):
-        q, k, v, out, lse, cc, cs, b0, slope, dm, wd = ctx.saved_tensors
+        q, k, v, out, lse, cc, cs, b0, slope, dm, wd, pb = ctx.saved_tensors
         bm, sp = ctx.bm, ctx.sp
         kw = _kwargs(sp, bm)
         q_off, q_list = bm.q_lists()
         dout = dout if dout.stride() == q.stride() else _match(dout, q)
         out_m = out if out.stride() == q.stride() else _match(out, q)
         need_c = sp is not None and any(ctx.needs_input_grad[3:9])
+        need_p = pb is not None and ctx.needs_input_grad[9]
         g = ops.attn_bwd(q, k, v, out_m, dout, lse, bm.kv_num_blocks[0], bm.kv_indices[0], q_off, q_list, bm.docs,
                          bm.ds_tok_end, bs=bm.BLOCK_SIZE, scale=ctx.scale, coeff_cos=cc, coeff_sin=cs, b0=b0,
-                         slope=slope, delta_main=dm, width=wd, need_coeff_grads=need_c, **kw)
+                         slope=slope, delta_main=dm, width=wd, need_coeff_grads=need_c, pair_bias=pb,
+                         need_pair_grad=need_p, **kw)
+        dpb = g["dpair_bias"].reshape(pb.shape) if need_p else None
         return (g["dq"], g["dk"], g["dv"], g["dcoeff_cos"], g["dcoeff_sin"], g["db0"], g["dslope"],
-                g["ddelta_main"], g["dwidth"], None, None, None)
+                g["ddelta_main"], g["dwidth"], dpb, None, None, None)
+
+
+class _SoftPointerFn(torch.autograd.Function):
+    """Soft weights of the block-scoring picks as a per-list-entry score
+    bias: b = log σ(z/τ_w), z = logit_scale·q̄·k̄ + prior (noise-free), on the
+    pick entries (scope_pointer_pair_bias).  Backward: the block-mean chain
+    into q and k (scope_pointer_bwd).  No reference counterpart: the
+    reference's selection runs under torch.no_grad (model/attn_bias.py:623)."""
+
+    @staticmethod
+    def forward(ctx, q, k, bm: ScopeBlockMask, window: int, n_global: int, logit_scale: float, soft_temp: float,
+                prior):
+        bs = bm.BLOCK_SIZE
+        qbar, kbar = ops.block_means(q, k, bs)
+        picks = bm.extras["picks"]
+        pb = ops.pointer_pair_bias(bm.kv_num_blocks[0], bm.kv_indices[0], picks, bs=bs, window=window,
+                                   n_global=n_global, soft_temp=soft_temp, qbar=qbar, kbar=kbar, prior=prior,
+                                   logit_scale=logit_scale)
+        ctx.save_for_backward(qbar, kbar, pb)
+        ctx.bm, ctx.logit_scale, ctx.soft_temp = bm, logit_scale, soft_temp
+        ctx.q_like, ctx.k_like = (q.shape, q.stride()), (k.shape, k.stride())
+        return pb
+
+    @staticmethod
+    def backward(ctx, dpb):
+        qbar, kbar, pb = ctx.saved_tensors
+        bm = ctx.bm
+        q_off, q_list = bm.q_lists()
+        dq = torch.empty_strided(*ctx.q_like, dtype=torch.bfloat16, device=pb.device).zero_()
+        dk = torch.empty_strided(*ctx.k_like, dtype=torch.bfloat16, device=pb.device).zero_()
+        ops.pointer_bwd(qbar, kbar, bm.kv_num_blocks[0], bm.kv_indices[0], q_off, q_list, pb, dpb.contiguous(), dq,
+                        dk, bs=bm.BLOCK_SIZE, logit_scale=ctx.logit_scale, soft_temp=ctx.soft_temp)
+        return dq, dk, None, None, None, None, None, None
+
+
+def soft_pointer_bias(q: torch.Tensor, k: torch.Tensor, block_mask: ScopeBlockMask, *, window: int, n_global: int,
+                      logit_scale: float, soft_temp: float, prior: torch.Tensor | None = None) -> torch.Tensor:
+    """Differentiable soft weights [H,QB,MAXKV] of a block-scoring mask's
+    picks (q, k the tensors the mask was selected from)."""
+    return _SoftPointerFn.apply(q, k, block_mask, int(window), int(n_global), float(logit_scale),
+                                float(soft_temp), prior)
 
 
 def _match(x: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
@@ -107,7 +152,9 @@ def scope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block_
     """Block-sparse attention over ``block_mask`` with the document-causal
     mask and the optional spectral bias.  q, k, v: [1,H,T,D] bf16 (any
     head/token strides, unit last stride).  Returns out [1,H,T,D] (and
-    lse [1,H,T], natural log, if ``return_lse``)."""
+    lse [1,H,T], natural log, if ``return_lse``).  A mask built with soft
+    pointer weights carries them in ``extras["pair_bias"]``; they are added
+    to the listed tiles' scores and receive gradients."""
     sp = spectral
     cc = cs = b0 = sl = dm = wd = None
     if sp is not None:
@@ -117,7 +164,8 @@ def scope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block_
             sl = sp.slope if sp.use_slope else None
             if sp.gate_kind != "none":
                 dm, wd = sp.delta_main, sp.width
-    out, lse = _ScopeAttnFn.apply(q, k, v, cc, cs, b0, sl, dm, wd, block_mask, sp, float(scale))
+    pb = block_mask.extras.get("pair_bias")
+    out, lse = _ScopeAttnFn.apply(q, k, v, cc, cs, b0, sl, dm, wd, pb, block_mask, sp, float(scale))
     return (out, lse) if return_lse else out
 
 

@@ -21,6 +21,8 @@
 //   wavefront on the 32x32x16 form, four wavefronts (attn_bwd_dkv_kernel).
 #include <math.h>
 
+#include <algorithm>
+
 #include "attn_common.h"
 
 namespace scope {
@@ -120,6 +122,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 
   __shared__ KvTile<MODE> buf0, buf1;
   __shared__ int kbs[kListLds];
+  __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
@@ -135,6 +138,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
   const int32_t* lst = a.kv_idx + lrow * a.maxkv;
   for (int t = tid; t < min(n, kListLds); t += 256) kbs[t] = lst[t];
+  const bool pbias = a.pair_bias != nullptr;
+  if (pbias)
+    for (int t = tid; t < min(n, kListLds); t += 256) kbias[t] = a.pair_bias[lrow * a.maxkv + t] * kLog2e;
 
   uint4 qreg[8], doreg[8];
   {
@@ -156,7 +162,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       }
     }
     R.delta = dsum + __shfl_xor(dsum, 32, 64);
-    if (g == 0) a.delta[hT + R.row] = R.delta;
   }
   const float lse_nat = a.lse[hT + R.row];
   R.lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
@@ -224,9 +229,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   // block mode: the bias term and the per-row sums dS, P change per key block
   // (four 64-key tiles), not per tile
   float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
+  float eb = 0.f;  // pair bias of the current list entry (log2 units)
   auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
-    const float tconst = MODE == 1 ? bt : R.rowc;
+    const float tconst = (MODE == 1 ? bt : R.rowc) + eb;
     // S^T and dP^T: keys in two 32-row blocks (A operand), this lane's query row as the column
     f32x16_t s[2], dpv[2];
 #pragma unroll
@@ -315,6 +321,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
            (sa[0] * s0.x + sa[1] * s0.y + sa[2] * s0.z + sa[3] * s0.w) +
            (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
     }
+    if (it % NSUB == 0) eb = pbias ? kbias[it / NSUB] : 0.f;  // per key block (its first tile is never skipped)
     if (kv0 <= wrow_lo + 31) compute(kv0, b);  // else every key follows this wavefront's rows
     if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
       // last tile of this key block: fold its sums into the coefficient gradients
@@ -355,6 +362,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   rs_tot += __shfl_xor(rs_tot, 32, 64);
   pm_tot += __shfl_xor(pm_tot, 32, 64);
   const float dd_err = rs_tot;  // Δ_true - Δ
+  // the kv-major pass reads Δ_true = Δ + (Δ_true - Δ): its dS, dK and the
+  // pair-bias sums then do not carry the bf16 rounding of the output
+  if (g == 0) a.delta[hT + R.row] = R.delta + dd_err;
   uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
@@ -453,6 +463,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
 
   __shared__ KvTile<MODE> buf0, buf1, buf2;
   __shared__ int kbs[kListLds];
+  __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
   // block mode: β·log2e-scaled coefficients [BS][cos 8 | sin 8] and the
   // coefficient-gradient sums [BS][Σrs·cos 8 | Σpm·cos 8 | Σrs·sin 8 | Σpm·sin 8]
   __shared__ __attribute__((aligned(16))) float coef[MODE == 1 ? BS * 16 : 4];
@@ -473,6 +484,9 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
   const int32_t* lst = a.kv_idx + lrow * a.maxkv;
   for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
+  const bool pbias = a.pair_bias != nullptr;
+  if (pbias)
+    for (int t = tid; t < min(n, kListLds); t += NT) kbias[t] = a.pair_bias[lrow * a.maxkv + t] * kLog2e;
 
   uint4 qreg[8], doreg[8];
   {
@@ -494,7 +508,6 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
       }
     }
     R.delta = dsum + __shfl_xor(dsum, 32, 64);
-    if (g == 0) a.delta[hT + R.row] = R.delta;
   }
   const float lse_nat = a.lse[hT + R.row];
   R.lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
@@ -517,6 +530,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   for (int i = 0; i < 4; ++i) o[i] = zero16();
   float rs_tot = 0.f;  // per lane (half the keys of the row) until the epilogue
   float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
+  float eb = 0.f;  // pair bias of the current key block (log2 units)
 
   const int total = n * NSUB;
   const int qmax = static_cast<int>(q0) + BS - 1;
@@ -549,9 +563,9 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  auto compute_a = [&](int kv0, const KvTile<MODE>& b, uint4 (&dsb1)[2]) __attribute__((always_inline)) {
+  auto compute_a = [&](int kv0, const KvTile<MODE>& b, float eb, uint4 (&dsb1)[2]) __attribute__((always_inline)) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
-    const float off = (MODE == 1 ? bt : 0.f) - R.lse2;
+    const float off = (MODE == 1 ? bt : 0.f) + eb - R.lse2;
     float rs = 0.f, pm = 0.f;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
@@ -604,8 +618,9 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
       }
       bt = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     }
+    if (it % NSUB == 0) eb = pbias ? kbias[it / NSUB] : 0.f;  // per key block
     const bool act = kv0 <= wrow_lo + 31;  // else every key follows this wavefront's rows
-    if (act) compute_a(kv0, b, dsb1);
+    if (act) compute_a(kv0, b, eb, dsb1);
     if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
       // last tile of this key block: fold the row sums (combined over the lane
       // pair) into the gradient sums; g = 0 keeps the cos half, g = 1 the sin half
@@ -683,6 +698,9 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   // ---- epilogue: dQ = scale·o, coefficient gradients
   rs_tot += __shfl_xor(rs_tot, 32, 64);
   const float dd_err = rs_tot;  // Δ_true - Δ
+  // the kv-major pass reads Δ_true = Δ + (Δ_true - Δ): its dS, dK and the
+  // pair-bias sums then do not carry the bf16 rounding of the output
+  if (g == 0) a.delta[hT + R.row] = R.delta + dd_err;
   uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
@@ -768,6 +786,34 @@ struct KvPlan {
   int max_items;      // work items per head (upper bound)
 };
 
+// Pair bias of the item's list entries: for each listed q-block qb, the
+// position of key block kb in qb's kv list (its first kv_num entries are
+// unique and ascending) and the bias there (log2 units; 0 without one).
+__device__ __forceinline__ void dkv_entry_bias(const AttnArgs& a, int h, int kb, int qb, float& eb, int& pos) {
+  const int64_t row = static_cast<int64_t>(h) * a.QB + qb;
+  const int32_t* lst = a.kv_idx + row * a.maxkv;
+  int lo = 0, hi = min(a.kv_num[row], a.maxkv) - 1;
+  pos = -1;
+  while (lo <= hi) {
+    const int mid = (lo + hi) >> 1;
+    const int v = lst[mid];
+    if (v == kb) {
+      pos = mid;
+      break;
+    }
+    if (v < kb) lo = mid + 1;
+    else hi = mid - 1;
+  }
+  eb = (a.pair_bias && pos >= 0) ? a.pair_bias[row * a.maxkv + pos] * kLog2e : 0.f;
+}
+
+// Sum of x over the 64 lanes of the wavefront.
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
 // LDS staging of one 64-row query tile of pass B.  Everything arrives by
 // global_load_lds (no registers): two such buffers alternate, so the loads of
 // tile j+1 run under the MFMAs of tile j.
@@ -846,11 +892,11 @@ __device__ __forceinline__ void dkv_issue(const AttnArgs& a, int h, int64_t hT, 
 // P and dS of register quad (mq, rq) of one tile as bf16 B operands (k index:
 // the 64 query rows): the quad is k-step 2·mq + rq/2, slots 4·(rq%2) .. +3.
 // MASK applies the causal and document masks.
-template <int MODE, bool MASK>
+template <int MODE, bool MASK, bool DP>
 __device__ __forceinline__ void dkv_probs_quad(const AttnArgs& a, const DkvBuf<MODE>& b, const float* offw, int q0,
                                                int lane, int wkv, int doc_kv, const f32x16_t (&s)[2],
                                                const f32x16_t (&dp)[2], uint4 (&pb)[4], uint4 (&dsb)[4], int mq,
-                                               int rq) {
+                                               int rq, float& dsum) {
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
   const int g = lane >> 5;
   const int* docq = reinterpret_cast<const int*>(b.ra + 128);
@@ -894,6 +940,7 @@ __device__ __forceinline__ void dkv_probs_quad(const AttnArgs& a, const DkvBuf<M
     const float p = __builtin_amdgcn_exp2f(xv);
     pv[i2] = p;
     dsv[i2] = p * (dp[mq][r] - dlv[i2]);
+    if (DP) dsum += dsv[i2];
   }
   const int ksx = 2 * mq + rq / 2;
   const uint32_t p01 = cvt_pk_bf16(pv[0], pv[1]), p23 = cvt_pk_bf16(pv[2], pv[3]);
@@ -914,7 +961,7 @@ __device__ __forceinline__ void dkv_probs_quad(const AttnArgs& a, const DkvBuf<M
 // Per-row exponent offsets of a tile (lane = row), private to the wavefront.
 template <int MODE>
 __device__ __forceinline__ void dkv_offsets(const AttnArgs& a, const DkvBuf<MODE>& b, float* offw, const float* tab,
-                                            int lane) {
+                                            float eb, int lane) {
   const float l = b.ra[lane];
   float c = 0.f;
   if (MODE == 1) {
@@ -931,22 +978,22 @@ __device__ __forceinline__ void dkv_offsets(const AttnArgs& a, const DkvBuf<MODE
     c *= a.beta_log2;
   }
   if (MODE >= 2 && a.subtract_b0) c = -a.beta_log2 * b.ra[192 + lane];
-  offw[lane] = l == -INFINITY ? -INFINITY : c - l * kLog2e;
+  offw[lane] = l == -INFINITY ? -INFINITY : c + eb - l * kLog2e;
 }
 
 // One 64-row query tile against this wavefront's 32 keys: S, dP, then
 // dV^T += dO^T·P and dK^T += Q^T·dS.  The copies of the next tile are issued
 // by the caller, before this tile's reads.
-template <int BS, int MODE>
+template <int BS, int MODE, bool DP>
 __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, float* offw,
-                                         const float* tab,
+                                         const float* tab, float eb,
                                          int64_t q0, int lane, int64_t wkv_lo, int doc_kv,
                                          const uint4 (&kreg)[8], const uint4 (&vreg)[8], const uint4& kf,
                                          const uint4& kfl, f32x16_t (&dvT)[4], f32x16_t (&dkT)[4],
-                                         const TileOffs& to) {
+                                         const TileOffs& to, float* slot) {
   const int g = lane >> 5, lr = lane & 31;
   const int wkv = static_cast<int>(wkv_lo) + lr;
-  dkv_offsets<MODE>(a, b, offw, tab, lane);
+  dkv_offsets<MODE>(a, b, offw, tab, eb, lane);
   // S and dP, query rows in two 32-row blocks (A operand), keys as columns (B)
   f32x16_t s[2], dp[2];
 #pragma unroll
@@ -990,18 +1037,25 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
     }
   }
   uint4 pb[4], dsb[4];
+  float dsum = 0.f;
   if (MODE >= 2 || masked) {  // token modes always take the masked form (one copy of their longer code)
 #pragma unroll
     for (int mq = 0; mq < 2; ++mq)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq)
-        dkv_probs_quad<MODE, true>(a, b, offw, static_cast<int>(q0), lane, wkv, doc_kv, s, dp, pb, dsb, mq, rq);
+        dkv_probs_quad<MODE, true, DP>(a, b, offw, static_cast<int>(q0), lane, wkv, doc_kv, s, dp, pb, dsb, mq, rq,
+                                       dsum);
   } else {
 #pragma unroll
     for (int mq = 0; mq < 2; ++mq)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq)
-        dkv_probs_quad<MODE, false>(a, b, offw, static_cast<int>(q0), lane, wkv, doc_kv, s, dp, pb, dsb, mq, rq);
+        dkv_probs_quad<MODE, false, DP>(a, b, offw, static_cast<int>(q0), lane, wkv, doc_kv, s, dp, pb, dsb, mq, rq,
+                                        dsum);
+  }
+  if (DP) {
+    dsum = wave_sum(dsum);
+    if (lane == 0) *slot += dsum;
   }
   // dV^T += dO^T P,  dK^T += Q^T dS  (k index: the 64 query rows); a step is
   // two MFMAs, so the operands are read TPD steps ahead into a ring
@@ -1028,7 +1082,7 @@ __device__ __forceinline__ void dkv_tile(const AttnArgs& a, const DkvBuf<MODE>& 
   }
 }
 
-template <int BS, int MODE>
+template <int BS, int MODE, bool DP>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl) {
   constexpr int D = 128;
   constexpr int BM = 64;  // query rows per staged tile
@@ -1037,7 +1091,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   __shared__ DkvBuf<MODE> buf0, buf1;
   __shared__ __attribute__((aligned(16))) float offw[4][BM];
   __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunk * 16 : 4];
-  __shared__ int qbs[kChunk], dse[kChunk];
+  __shared__ int qbs[kChunk], dse[kChunk], epos[kChunk];
+  __shared__ float ebias[kChunk];
+  __shared__ float pslot[kChunk][4];  // pair-bias gradient: per entry and wavefront
 
   constexpr int P = BS / 128;  // workgroups (128 keys each) per key block
   const int NB = a.QB;
@@ -1088,7 +1144,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
     const int qb = ql[i0 + tid];
     qbs[tid] = qb;
     dse[tid] = a.ds_tok_end[qb];
+    float eb = 0.f;
+    int pos = -1;
+    if (a.pair_bias || a.dpair) dkv_entry_bias(a, h, kb, qb, eb, pos);
+    ebias[tid] = eb;
+    epos[tid] = pos;
   }
+  if (DP && tid < kChunk * 4) pslot[tid / 4][tid % 4] = 0.f;
   if (MODE == 1 && tid < ne * 16) {
     // block-mode table row of distance qb - kb (clamped: a later key block is fully masked anyway)
     const int r = min(max(ql[i0 + tid / 16] - kb, 0), NB - 1);
@@ -1147,14 +1209,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
         const float* tab = tabs + (MODE == 1 ? e * 16 : 0);
         if (q0 + BM - 1 >= wkv_lo) {  // else every query row precedes this wavefront's keys
           const bool masked = !((wkv_lo + 31 <= q0) && (dse[e] <= wkv_lo));
-          if (half == 0)
-            dkv_tile<BS, MODE>(a, buf0, masked, offw[wave], tab, q0, lane, wkv_lo, doc_kv, kreg, vreg, kf, kfl, dvT,
-                               dkT, to);
-          else
-            dkv_tile<BS, MODE>(a, buf1, masked, offw[wave], tab, q0, lane, wkv_lo, doc_kv, kreg, vreg, kf, kfl, dvT,
-                               dkT, to);
+          const DkvBuf<MODE>& bc = half == 0 ? buf0 : buf1;
+          dkv_tile<BS, MODE, DP>(a, bc, masked, offw[wave], tab, ebias[e], q0, lane, wkv_lo, doc_kv, kreg, vreg, kf,
+                                 kfl, dvT, dkT, to, &pslot[e][wave]);
         }
       }
+    }
+  }
+
+  if (DP) {
+    __syncthreads();  // every wavefront's slots are final
+    if (tid < ne && epos[tid] >= 0) {
+      const float t = (pslot[tid][0] + pslot[tid][1]) + (pslot[tid][2] + pslot[tid][3]);
+      const int64_t row = static_cast<int64_t>(h) * a.QB + qbs[tid];
+      a.dpair[(static_cast<int64_t>(zpart) * a.H * a.QB + row) * a.maxkv + epos[tid]] = t;
     }
   }
 
@@ -1208,10 +1276,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
 
 // P and dS of one tile for this lane's key as the B operands of the
 // transposed products (pb[kk], dsb[kk]: k-step kk, see above).
-template <int MODE, bool MASK>
+template <int MODE, bool MASK, bool DP>
 __device__ __forceinline__ void dkv16_probs(const DkvBuf<MODE>& b, const float* offw, float cs, int q0, int wkv,
                                             int doc_kv, int g, const f32x4_t (&s)[4], const f32x4_t (&dp)[4],
-                                            uint4 (&pb)[2], uint4 (&dsb)[2]) {
+                                            uint4 (&pb)[2], uint4 (&dsb)[2], float& dsum) {
   const int* docq = reinterpret_cast<const int*>(b.ra + 128);
   uint32_t pw[8], dw[8];
 #pragma unroll
@@ -1234,6 +1302,7 @@ __device__ __forceinline__ void dkv16_probs(const DkvBuf<MODE>& b, const float* 
       const float p = __builtin_amdgcn_exp2f(x);
       pv[i] = p;
       dv[i] = p * (dp[mb][i] - dlv[i]);
+      if (DP) dsum += dv[i];
     }
     pw[2 * mb] = cvt_pk_bf16(pv[0], pv[1]);
     pw[2 * mb + 1] = cvt_pk_bf16(pv[2], pv[3]);
@@ -1282,13 +1351,15 @@ __device__ __forceinline__ uint4 lds_row16(const uint16_t* tile, const TileOffs1
 
 // One 64-row query tile against this wavefront's 16 keys, first part:
 // per-row offsets, S and dP, then P and dS as bf16 B operands.
-template <int MODE>
+// With DP, the tile's sum of dS over this wavefront's keys is added to *slot
+// (one writer per slot: the wavefront's own entry).
+template <int MODE, bool DP>
 __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, float* offw,
-                                        const float* tab, int q0, int lane, int wkv, int doc_kv,
+                                        const float* tab, float eb, int q0, int lane, int wkv, int doc_kv,
                                         const uint4 (&kreg)[4], const uint4 (&vreg)[4], const TileOffs16& to,
-                                        uint4 (&pb)[2], uint4 (&dsb)[2]) {
+                                        uint4 (&pb)[2], uint4 (&dsb)[2], float* slot) {
   const int g = lane >> 4;
-  dkv_offsets<MODE>(a, b, offw, tab, lane);
+  dkv_offsets<MODE>(a, b, offw, tab, eb, lane);
   f32x4_t s[4], dp[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
@@ -1316,10 +1387,15 @@ __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
+  float dsum = 0.f;
   if (masked)
-    dkv16_probs<MODE, true>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb);
+    dkv16_probs<MODE, true, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dsum);
   else
-    dkv16_probs<MODE, false>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb);
+    dkv16_probs<MODE, false, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dsum);
+  if (DP) {
+    dsum = wave_sum(dsum);
+    if (lane == 0) *slot += dsum;
+  }
 }
 
 // Second part: dV^T += dO^T P, dK^T += Q^T dS (step st = 8·kk + md).
@@ -1348,7 +1424,7 @@ __device__ __forceinline__ void dkv16_b(const DkvBuf<MODE>& b, const TileOffs16&
   }
 }
 
-template <int BS, int MODE>
+template <int BS, int MODE, bool DP>
 __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan pl) {
   static_assert(MODE <= 1, "token modes use attn_bwd_dkv_kernel");
   constexpr int D = 128;
@@ -1358,7 +1434,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   __shared__ DkvBuf<MODE> buf0, buf1, buf2;
   __shared__ __attribute__((aligned(16))) float offw[8][BM];
   __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunk * 16 : 4];
-  __shared__ int qbs[kChunk], dse[kChunk];
+  __shared__ int qbs[kChunk], dse[kChunk], epos[kChunk];
+  __shared__ float ebias[kChunk];
+  __shared__ float pslot[kChunk][8];  // pair-bias gradient: per entry and wavefront
 
   constexpr int P = BS / 128;  // workgroups (128 keys each) per key block
   const int NB = a.QB;
@@ -1403,7 +1481,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     const int qb = ql[i0 + tid];
     qbs[tid] = qb;
     dse[tid] = a.ds_tok_end[qb];
+    float eb = 0.f;
+    int pos = -1;
+    if (a.pair_bias || a.dpair) dkv_entry_bias(a, h, kb, qb, eb, pos);
+    ebias[tid] = eb;
+    epos[tid] = pos;
   }
+  if (DP && tid < kChunk * 8) pslot[tid / 8][tid % 8] = 0.f;
   if (MODE == 1 && tid < ne * 16) {
     const int r = min(max(ql[i0 + tid / 16] - kb, 0), NB - 1);
     tabs[tid] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + tid % 16];
@@ -1452,7 +1536,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     if (q0 + BM - 1 < wkv_lo) return false;  // every query row precedes this wavefront's keys
     const bool masked = !((wkv_lo + 15 <= q0) && (dse[e] <= wkv_lo));
     const float* tab = tabs + (MODE == 1 ? e * 16 : 0);
-    dkv16_a<MODE>(a, bc, masked, offw[wave], tab, q0, lane, wkv, doc_kv, kreg, vreg, to, pb, dsb);
+    dkv16_a<MODE, DP>(a, bc, masked, offw[wave], tab, ebias[e], q0, lane, wkv, doc_kv, kreg, vreg, to, pb, dsb,
+                      &pslot[e][wave]);
     return true;
   };
   if (wave < 4) {
@@ -1495,6 +1580,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     }
   }
   wait_vm0();  // no copy may still target LDS when the workgroup exits
+  if (DP && tid < ne && epos[tid] >= 0) {
+    // every slot was last written before the final barrier of the loop above
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) t += pslot[tid][w];
+    const int64_t row = static_cast<int64_t>(h) * a.QB + qbs[tid];
+    a.dpair[(static_cast<int64_t>(zpart) * a.H * a.QB + row) * a.maxkv + epos[tid]] = t;
+  }
 
   // ---- write dK = scale·dkT^T, dV = dvT^T: lane holds columns 16md + 4g .. +3 of key wkv
   if (nch == 1) {
@@ -1553,7 +1646,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl, 
 }
 
 struct BwdLayout {
-  int64_t delta, qfeat, items, slots, part_dk, part_dv, total, max_slots;
+  int64_t delta, qfeat, items, slots, part_dk, part_dv, dpair, total, max_slots;
   int max_items;
 };
 
@@ -1578,13 +1671,32 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
   o += al(part);
   L.part_dv = o;
   o += al(part);
+  // pair-bias gradient partials, one per 128-key part of a key block
+  L.dpair = o;
+  if (p->dpair_bias) o += al(static_cast<int64_t>(p->bs / 128) * p->H * QB * p->maxkv * 4);
   L.total = o;
   return L;
 }
 
+// dpair_bias[h][qb][e] = the sum of the key-block parts' tile sums for the
+// listed entries (in part order), 0 for e >= kv_num.
+__global__ __launch_bounds__(256) void dpair_sum_kernel(AttnArgs a, int parts, float* __restrict__ out) {
+  const int64_t rows = static_cast<int64_t>(a.H) * a.QB;
+  const int64_t n = rows * a.maxkv;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t row = i / a.maxkv;
+    const int e = static_cast<int>(i % a.maxkv);
+    float t = 0.f;
+    if (e < min(a.kv_num[row], a.maxkv))
+      for (int pp = 0; pp < parts; ++pp) t += a.dpair[pp * n + i];
+    out[i] = t;
+  }
+}
+
 template <int BS>
 static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases, int grid_q, int max_items,
-                       hipStream_t s) {
+                       float* dpair_out, hipStream_t s) {
   constexpr int P = BS / 128;
   const int per_xcd = (a.H * max_items + 7) / 8;
   dim3 gq(grid_q * P), gk(8 * per_xcd * P), gr(a.QB, a.H);
@@ -1615,23 +1727,35 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
   if (phases & SCOPE_BWD_DKV_PLAN)
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start));
+  const bool dp = a.dpair != nullptr;  // the pair-bias gradient runs in its own instantiation
   if ((phases & SCOPE_BWD_DKV_MAIN) && mode != SCOPE_BIAS_TOKEN) {
     // 16 keys per wavefront, 8 wavefronts (two per SIMD) per 128 keys
-    if (mode == SCOPE_BIAS_BLOCK)
-      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1>), gk, dim3(512), 0, s, a, pl);
+    if (mode == SCOPE_BIAS_BLOCK && dp)
+      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1, true>), gk, dim3(512), 0, s, a, pl);
+    else if (mode == SCOPE_BIAS_BLOCK)
+      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1, false>), gk, dim3(512), 0, s, a, pl);
+    else if (dp)
+      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0, true>), gk, dim3(512), 0, s, a, pl);
     else
-      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0>), gk, dim3(512), 0, s, a, pl);
+      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0, false>), gk, dim3(512), 0, s, a, pl);
   } else if (phases & SCOPE_BWD_DKV_MAIN) {
-    if (mode == SCOPE_BIAS_BLOCK)
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 1>), gk, dim3(256), 0, s, a, pl);
-    else if (mode == SCOPE_BIAS_TOKEN && gate)
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3>), gk, dim3(256), 0, s, a, pl);
-    else if (mode == SCOPE_BIAS_TOKEN)
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2>), gk, dim3(256), 0, s, a, pl);
+    if (gate && dp)
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3, true>), gk, dim3(256), 0, s, a, pl);
+    else if (gate)
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3, false>), gk, dim3(256), 0, s, a, pl);
+    else if (dp)
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2, true>), gk, dim3(256), 0, s, a, pl);
     else
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 0>), gk, dim3(256), 0, s, a, pl);
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2, false>), gk, dim3(256), 0, s, a, pl);
   }
-  if (phases & SCOPE_BWD_DKV_REDUCE) hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
+  if (phases & SCOPE_BWD_DKV_REDUCE) {
+    hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
+    if (a.dpair && dpair_out) {
+      const int64_t n = static_cast<int64_t>(a.H) * a.QB * a.maxkv;
+      const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
+      hipLaunchKernelGGL(dpair_sum_kernel, dim3(blocks), dim3(256), 0, s, a, P, dpair_out);
+    }
+  }
 }
 
 }  // namespace scope
@@ -1706,10 +1830,11 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   pl.max_items = L.max_items;
   hipStream_t s = as_stream(stream);
   const int grid_q = p->H * a.QB;
+  a.dpair = p->dpair_bias ? reinterpret_cast<float*>(ws + L.dpair) : nullptr;
   if (p->bs == 256)
-    launch_bwd<256>(a, pl, p->bias_mode, phases, grid_q, L.max_items, s);
+    launch_bwd<256>(a, pl, p->bias_mode, phases, grid_q, L.max_items, p->dpair_bias, s);
   else
-    launch_bwd<128>(a, pl, p->bias_mode, phases, grid_q, L.max_items, s);
+    launch_bwd<128>(a, pl, p->bias_mode, phases, grid_q, L.max_items, p->dpair_bias, s);
   return check_launch("attention backward kernels");
 }
 

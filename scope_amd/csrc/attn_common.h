@@ -294,6 +294,8 @@ struct AttnArgs {
   float* delta;      // rowsum(dO∘O) [H,T]
   uint16_t* qfeat;   // token mode: query-side features [H,T][kTokRow] (hi g0, hi g1, lo g0, lo g1)
   float* mass;       // block mass [H,QB,NB] (forward mass pass)
+  const float* pair_bias;  // per-list-entry score bias [H,QB,maxkv] (natural log) or null
+  float* dpair;            // backward: tile sums of dS per (key-block part, h, qb, entry) [P][H][QB][maxkv] or null
   int H, QB, maxkv, K;
   int64_t T;
   int64_t q_sh, q_st, k_sh, k_st, v_sh, v_st, o_sh, o_st;

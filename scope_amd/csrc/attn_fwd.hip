@@ -115,6 +115,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
   __shared__ KvTile<MODE> buf0, buf1;
   __shared__ typename std::conditional<STAGGER, KvTile<MODE>, int>::type buf2;
   __shared__ int kbs[kListLds];
+  __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
   // mass: per list entry and wavefront, the wavefront's share (each slot has one writer)
   __shared__ float mslot[MASS ? kListLds * NW : 1];
   // block mode: β·log2e-scaled coefficient rows of the block's queries, [BS][16] (cos 0..7, sin 8..15)
@@ -134,6 +135,9 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
   const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
   const int32_t* lst = a.kv_idx + lrow * a.maxkv;
   for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
+  const bool pbias = a.pair_bias != nullptr;
+  if (pbias)
+    for (int t = tid; t < min(n, kListLds); t += NT) kbias[t] = a.pair_bias[lrow * a.maxkv + t] * kLog2e;
   if (MASS)
     for (int t = tid; t < n * NW; t += NT) mslot[t] = 0.f;  // n <= kListLds (checked on the host)
 
@@ -174,6 +178,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
   float lse2 = 0.f;  // mass: the row's LSE in log2 units
   if (MASS) lse2 = a.lse[hT + R.row] * kLog2e;
   float bt = 0.f;  // block mode: β·bias of the current key block (log2 units)
+  float eb = 0.f;  // pair bias of the current key block (log2 units)
 
   // flat iteration index it = list entry · NSUB + key tile; tiles that start
   // after the block's last row are skipped
@@ -209,7 +214,8 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
       }
       bt = acc;
     }
-    const float tconst = MODE == 1 ? bt : R.rowc;
+    if (it % NSUB == 0) eb = pbias ? kbias[it / NSUB] : 0.f;  // per key block (its first tile is never skipped)
+    const float tconst = (MODE == 1 ? bt : R.rowc) + eb;
     // S^T = K Q^T (+ token features): keys in two 32-row blocks, this lane's row as the column
     f32x16_t s[2];
     s[0] = zero16();
@@ -476,6 +482,7 @@ AttnArgs make_args(const scope_attn_params* p) {
   a.gate_kind = p->gate_kind;
   a.ramp_lambda = p->ramp_lambda;
   a.inv_tau = p->tau > 0.f ? 1.f / p->tau : 0.f;
+  a.pair_bias = p->pair_bias;
   return a;
 }
 

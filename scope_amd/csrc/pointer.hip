@@ -551,6 +551,181 @@ __global__ __launch_bounds__(256) void ptr_score_kernel(ScoreLaunch A, const flo
   if (active && lane == 0) kv_num[rowq] = n;
 }
 
+
+// two floats -> packed bf16 pair (round to nearest even; lo in the low half)
+__device__ __forceinline__ uint32_t bf16_pack(float lo, float hi) {
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  bf16x2_v v;
+  v[0] = static_cast<__bf16>(lo);
+  v[1] = static_cast<__bf16>(hi);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// ---------------------------------------------------------------------------
+// soft pointer weights (no reference counterpart: model/attn_bias.py:623
+// selects under torch.no_grad)
+// ---------------------------------------------------------------------------
+// b[h,qb,e] = log σ(z/τ_w) for the pick entries of the packed list (e <
+// kv_num and kv_idx[e] one of the picks), 0 otherwise; z is the noise-free
+// selection logit, computed exactly as ptr_score_kernel computes it (the
+// same fmaf chain over d, then the prior), so b follows the ranked value.
+// One wavefront per (h, qb), one lane per list entry.
+template <int D>
+__global__ __launch_bounds__(256) void pair_bias_kernel(ScoreLaunch A, float soft_temp, const float* __restrict__ qbar,
+                                                         const float* __restrict__ kbar,
+                                                         const float* __restrict__ logits_in,
+                                                         const float* __restrict__ prior,
+                                                         const int32_t* __restrict__ kv_num,
+                                                         const int32_t* __restrict__ kv_idx,
+                                                         const int32_t* __restrict__ picks, float* __restrict__ out) {
+  const scope_ptr_score_params& P = A.p;
+  const int NB = P.NB, B = P.budget, L = A.L;
+  const int lane = lane_id();
+  const int qb = blockIdx.x * 4 + threadIdx.x / kWave;
+  const int h = blockIdx.y;
+  if (qb >= NB || lane >= L) return;
+  const int64_t row = static_cast<int64_t>(h) * NB + qb;
+  const int n = kv_num[row];
+  const int kb = kv_idx[row * L + lane];
+  bool pick = false;
+  for (int i = 0; i < B; ++i) pick = pick || (picks[row * B + i] == kb);
+  float b = 0.f;
+  if (lane < n && pick) {
+    float logit;
+    if (logits_in) {
+      logit = logits_in[row * NB + kb];
+    } else {
+      const float* qr = qbar + row * D;
+      const float* kr = kbar + (static_cast<int64_t>(h) * NB + kb) * D;
+      float acc = 0.f;
+#pragma unroll 8
+      for (int d = 0; d < D; ++d) acc = fmaf(qr[d], kr[d], acc);
+      logit = P.logit_scale * acc;
+      if (prior) logit = logit + prior[h * P.prior_head_stride + (qb - kb)];
+    }
+    const float x = logit / soft_temp;
+    b = fminf(x, 0.f) - log1pf(expf(-fabsf(x)));  // log σ(x)
+  }
+  out[row * L + lane] = b;
+}
+
+// Pointer backward, q side: per (h, qb), dz_e = db_e·(1 - e^b_e)/τ_w for the
+// listed entries (0 where b = 0), stored for the k side; dq̄ = ls·Σ_e dz_e·k̄_kb
+// (entries in list order), and every row of the q-block gets dq̄/bs.
+__global__ __launch_bounds__(256) void ptr_bwd_q_kernel(scope_ptr_bwd_params P, const float* __restrict__ kbar,
+                                                        const int32_t* __restrict__ kv_num,
+                                                        const int32_t* __restrict__ kv_idx,
+                                                        const float* __restrict__ pair_bias,
+                                                        const float* __restrict__ dpair, float* __restrict__ dz,
+                                                        uint16_t* __restrict__ dq) {
+  __shared__ float dzs[64];
+  __shared__ int kbs[64];
+  __shared__ float dqb[128];
+  const int qb = blockIdx.x, h = blockIdx.y;
+  const int64_t row = static_cast<int64_t>(h) * P.NB + qb;
+  const int L = P.maxkv;
+  const int n = min(kv_num[row], L);
+  for (int e = threadIdx.x; e < L; e += blockDim.x) {
+    float v = 0.f;
+    if (e < n) {
+      const float b = pair_bias[row * L + e];
+      v = b != 0.f ? dpair[row * L + e] * (1.f - expf(b)) / P.soft_temp : 0.f;
+    }
+    dz[row * L + e] = v;
+    if (e < 64) {
+      dzs[e] = v;
+      kbs[e] = e < n ? kv_idx[row * L + e] : 0;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < P.D) {
+    const int d = threadIdx.x;
+    float acc = 0.f;
+    for (int e = 0; e < n; ++e)
+      if (dzs[e] != 0.f) acc += dzs[e] * kbar[(static_cast<int64_t>(h) * P.NB + kbs[e]) * P.D + d];
+    dqb[d] = P.logit_scale * acc / static_cast<float>(P.bs);
+  }
+  __syncthreads();
+  // rows of the q-block: 8 bf16 per thread step
+  const int chunks = P.bs * P.D / 8;
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+    const int r = c / (P.D / 8), d0 = (c % (P.D / 8)) * 8;
+    uint16_t* ptr = dq + h * P.q_sh + (static_cast<int64_t>(qb) * P.bs + r) * P.q_st + d0;
+    uint4 v = *reinterpret_cast<const uint4*>(ptr);
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = __uint_as_float(w[i] << 16) + dqb[d0 + 2 * i];
+      const float hi = __uint_as_float(w[i] & 0xffff0000u) + dqb[d0 + 2 * i + 1];
+      w[i] = bf16_pack(lo, hi);
+    }
+    *reinterpret_cast<uint4*>(ptr) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Pointer backward, k side: per (h, kb), dk̄ = ls·Σ dz·q̄_qb over the q-blocks
+// that list kb (the transposed list, ascending), and every row of the key
+// block gets dk̄/bs.
+__global__ __launch_bounds__(256) void ptr_bwd_k_kernel(scope_ptr_bwd_params P, const float* __restrict__ qbar,
+                                                        const int32_t* __restrict__ kv_num,
+                                                        const int32_t* __restrict__ kv_idx,
+                                                        const int32_t* __restrict__ q_off,
+                                                        const int32_t* __restrict__ q_list,
+                                                        const float* __restrict__ dz, uint16_t* __restrict__ dk) {
+  __shared__ float dks[128];
+  __shared__ float part[2][128];
+  const int kb = blockIdx.x, h = blockIdx.y;
+  const int NB = P.NB, L = P.maxkv;
+  const int32_t* qo = q_off + static_cast<int64_t>(h) * (NB + 1);
+  const int32_t* ql = q_list + static_cast<int64_t>(h) * NB * L + qo[kb];
+  const int nq = qo[kb + 1] - qo[kb];
+  // two halves of the q-list in parallel (threads 0-127 and 128-255), each in list order
+  const int d = threadIdx.x & 127, half = threadIdx.x >> 7;
+  float acc = 0.f;
+  if (d < P.D) {
+    const int mid = (nq + 1) / 2;
+    const int i0 = half == 0 ? 0 : mid, i1 = half == 0 ? mid : nq;
+    for (int i = i0; i < i1; ++i) {
+      const int qb = ql[i];
+      const int64_t row = static_cast<int64_t>(h) * NB + qb;
+      // position of kb in qb's list (unique and ascending in its first kv_num entries)
+      int lo = 0, hi = min(kv_num[row], L) - 1, pos = -1;
+      while (lo <= hi) {
+        const int m = (lo + hi) >> 1;
+        const int v = kv_idx[row * L + m];
+        if (v == kb) {
+          pos = m;
+          break;
+        }
+        if (v < kb) lo = m + 1;
+        else hi = m - 1;
+      }
+      if (pos < 0) continue;
+      const float z = dz[row * L + pos];
+      if (z != 0.f) acc += z * qbar[row * P.D + d];
+    }
+    part[half][d] = acc;
+  }
+  __syncthreads();
+  if (threadIdx.x < P.D) dks[threadIdx.x] = P.logit_scale * (part[0][threadIdx.x] + part[1][threadIdx.x]) /
+                                           static_cast<float>(P.bs);
+  __syncthreads();
+  const int chunks = P.bs * P.D / 8;
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+    const int r = c / (P.D / 8), d0 = (c % (P.D / 8)) * 8;
+    uint16_t* ptr = dk + h * P.k_sh + (static_cast<int64_t>(kb) * P.bs + r) * P.k_st + d0;
+    uint4 v = *reinterpret_cast<const uint4*>(ptr);
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = __uint_as_float(w[i] << 16) + dks[d0 + 2 * i];
+      const float hi = __uint_as_float(w[i] & 0xffff0000u) + dks[d0 + 2 * i + 1];
+      w[i] = bf16_pack(lo, hi);
+    }
+    *reinterpret_cast<uint4*>(ptr) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 }  // namespace scope
 
 using namespace scope;
@@ -656,6 +831,59 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
     hipLaunchKernelGGL(ptr_score_kernel<64>, grid, dim3(256), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
                        gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, picks, logits_out);
   return check_launch("ptr_score_kernel");
+}
+
+
+int scope_pointer_pair_bias(const scope_ptr_score_params* p, float soft_temp, const float* qbar, const float* kbar,
+                            const float* logits_in, const float* prior, const int32_t* kv_num, const int32_t* kv_idx,
+                            const int32_t* picks, float* pair_bias, void* stream) {
+  SCOPE_REQUIRE(p && kv_num && kv_idx && picks && pair_bias, "scope_pointer_pair_bias: null pointer");
+  SCOPE_REQUIRE(logits_in || (qbar && kbar), "scope_pointer_pair_bias: need logits_in or qbar/kbar");
+  SCOPE_REQUIRE(p->D == 64 || p->D == 128, "scope_pointer_pair_bias: D=%d (supported: 64, 128)", p->D);
+  SCOPE_REQUIRE(p->budget >= 1 && p->budget <= kMaxBudget, "scope_pointer_pair_bias: budget=%d outside [1, %d]",
+                p->budget, kMaxBudget);
+  SCOPE_REQUIRE(soft_temp > 0.f, "scope_pointer_pair_bias: soft_temp must be > 0");
+  ScoreLaunch A;
+  A.p = *p;
+  A.L = min(p->window, p->NB) + p->budget + min(p->n_global, p->NB);
+  A.N = next_pow2(A.L);
+  SCOPE_REQUIRE(A.L <= 64, "scope_pointer_pair_bias: list length %d exceeds 64", A.L);
+  dim3 grid(ceil_div(p->NB, 4), p->H);
+  if (p->D == 128)
+    hipLaunchKernelGGL(pair_bias_kernel<128>, grid, dim3(256), 0, as_stream(stream), A, soft_temp, qbar, kbar,
+                       logits_in, prior, kv_num, kv_idx, picks, pair_bias);
+  else
+    hipLaunchKernelGGL(pair_bias_kernel<64>, grid, dim3(256), 0, as_stream(stream), A, soft_temp, qbar, kbar,
+                       logits_in, prior, kv_num, kv_idx, picks, pair_bias);
+  return check_launch("pair_bias_kernel");
+}
+
+int64_t scope_pointer_bwd_workspace_bytes(const scope_ptr_bwd_params* p) {
+  if (!p) return 0;
+  return static_cast<int64_t>(p->H) * p->NB * p->maxkv * 4;
+}
+
+int scope_pointer_bwd(const scope_ptr_bwd_params* p, const float* qbar, const float* kbar, const int32_t* kv_num,
+                      const int32_t* kv_idx, const int32_t* q_off, const int32_t* q_list, const float* pair_bias,
+                      const float* dpair_bias, uint16_t* dq, uint16_t* dk, void* workspace, void* stream) {
+  SCOPE_REQUIRE(p && qbar && kbar && kv_num && kv_idx && q_off && q_list && pair_bias && dpair_bias && dq && dk &&
+                    workspace,
+                "scope_pointer_bwd: null pointer");
+  SCOPE_REQUIRE(p->D == 64 || p->D == 128, "scope_pointer_bwd: D=%d (supported: 64, 128)", p->D);
+  SCOPE_REQUIRE(p->maxkv >= 1 && p->maxkv <= 64, "scope_pointer_bwd: maxkv=%d outside [1, 64]", p->maxkv);
+  SCOPE_REQUIRE(p->soft_temp > 0.f && p->bs > 0 && p->NB >= 1 && p->H >= 1, "scope_pointer_bwd: bad parameters");
+  SCOPE_REQUIRE(p->bs * p->D % 8 == 0 && p->q_st % 8 == 0 && p->k_st % 8 == 0 && p->q_sh % 8 == 0 && p->k_sh % 8 == 0,
+                "scope_pointer_bwd: dq/dk rows must stay 16-byte aligned");
+  SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(dq) | reinterpret_cast<uintptr_t>(dk)) & 15) == 0,
+                "scope_pointer_bwd: dq and dk must start on a 16-byte boundary");
+  float* dz = static_cast<float*>(workspace);
+  hipStream_t s = as_stream(stream);
+  dim3 grid(p->NB, p->H);
+  hipLaunchKernelGGL(ptr_bwd_q_kernel, grid, dim3(256), 0, s, *p, kbar, kv_num, kv_idx, pair_bias, dpair_bias, dz, dq);
+  int rc = check_launch("ptr_bwd_q_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(ptr_bwd_k_kernel, grid, dim3(256), 0, s, *p, qbar, kv_num, kv_idx, q_off, q_list, dz, dk);
+  return check_launch("ptr_bwd_k_kernel");
 }
 
 }  // extern "C"

@@ -167,6 +167,53 @@ def pointer_select(ds_ptr: torch.Tensor, ds_local: torch.Tensor, *, bs: int, NB:
     return (kv_num, kv_idx, picks, logits) if return_logits else (kv_num, kv_idx, picks)
 
 
+def pointer_pair_bias(kv_num: torch.Tensor, kv_idx: torch.Tensor, picks: torch.Tensor, *, bs: int, window: int,
+                      n_global: int, soft_temp: float, qbar: torch.Tensor | None = None,
+                      kbar: torch.Tensor | None = None, logits_in: torch.Tensor | None = None,
+                      prior: torch.Tensor | None = None, logit_scale: float = 1.0) -> torch.Tensor:
+    """Soft pointer weights as a per-list-entry score bias [H,QB,L] (log σ(z/τ_w)
+    on the pick entries, 0 elsewhere), aligned with kv_idx."""
+    dev = _gpu("pointer_pair_bias", kv_num, kv_idx, picks, qbar, kbar, logits_in, prior)
+    H, NB = kv_num.shape[-2], kv_num.shape[-1]
+    L = kv_idx.shape[-1]
+    budget = picks.shape[-1]
+    D = qbar.shape[-1] if qbar is not None else 128
+    pstride = 0
+    if prior is not None:
+        prior = _f32(prior)
+        pstride = NB if prior.dim() == 2 else 0
+    prm = PtrScoreParams(H=H, NB=NB, D=D, bs=bs, window=window, n_global=n_global, budget=budget, temp=1.0,
+                         logit_scale=float(logit_scale), noise_mode=0, seed=0, eps=1e-9, prior_head_stride=pstride)
+    if min(window, NB) + budget + min(n_global, NB) != L:
+        raise RuntimeError("pointer_pair_bias: kv_idx width does not match window + budget + global")
+    out = torch.empty((H, NB, L), dtype=torch.float32, device=dev)
+    call("scope_pointer_pair_bias", C.byref(prm), float(soft_temp), _p(_f32(qbar)), _p(_f32(kbar)),
+         _p(_f32(logits_in)), _p(prior), _p(_i32(kv_num.reshape(H, NB))), _p(_i32(kv_idx.reshape(H, NB, L))),
+         _p(_i32(picks.reshape(H, NB, budget))), _p(out), _stream(dev))
+    return out
+
+
+def pointer_bwd(qbar: torch.Tensor, kbar: torch.Tensor, kv_num: torch.Tensor, kv_idx: torch.Tensor,
+                q_off: torch.Tensor, q_list: torch.Tensor, pair_bias: torch.Tensor, dpair_bias: torch.Tensor,
+                dq: torch.Tensor, dk: torch.Tensor, *, bs: int, logit_scale: float, soft_temp: float) -> None:
+    """Add the soft pointer weights' gradient path (through the block means)
+    to dq and dk [1,H,T,D] bf16 in place."""
+    from ._lib import PtrBwdParams
+
+    dev = _gpu("pointer_bwd", qbar, kbar, kv_num, kv_idx, q_off, q_list, pair_bias, dpair_bias, dq, dk)
+    H, NB, D = qbar.shape
+    L = kv_idx.shape[-1]
+    _, _, _, qsh, qst = _bhtd("pointer_bwd dq", dq)
+    _, _, _, ksh, kst = _bhtd("pointer_bwd dk", dk)
+    prm = PtrBwdParams(H=H, NB=NB, D=D, bs=int(bs), maxkv=L, logit_scale=float(logit_scale),
+                       soft_temp=float(soft_temp), q_sh=qsh, q_st=qst, k_sh=ksh, k_st=kst)
+    ws = torch.empty(max(16, query("scope_pointer_bwd_workspace_bytes", C.byref(prm))), dtype=torch.uint8,
+                     device=dev)
+    call("scope_pointer_bwd", C.byref(prm), _p(_f32(qbar)), _p(_f32(kbar)), _p(_i32(kv_num.reshape(H, NB))),
+         _p(_i32(kv_idx.reshape(H, NB, L))), _p(_i32(q_off)), _p(_i32(q_list)), _p(_f32(pair_bias)),
+         _p(_f32(dpair_bias)), _p(dq), _p(dk), _p(ws), _stream(dev))
+
+
 def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int):
     """q lists (CSR): q_off [H, NB+1], q_list [H, QB*MAXKV]."""
     dev = _gpu("transpose_blocks", kv_num, kv_idx)
@@ -362,6 +409,13 @@ def _attn_params(q, k, v, out, *, bs, maxkv, scale, beta, bias_mode, K, use_slop
                       tau=float(tau), q_sh=qsh, q_st=qst, k_sh=ksh, k_st=kst, v_sh=vsh, v_st=vst, o_sh=osh, o_st=ost)
 
 
+def _pair_bias(pair_bias, kv_idx3):
+    if pair_bias is None:
+        return None
+    pb = _f32(pair_bias.reshape(kv_idx3.shape))
+    return pb
+
+
 def empty_like_layout(x: torch.Tensor) -> torch.Tensor:
     """New tensor with x's shape and memory order (like FlexAttention's output)."""
     return torch.empty_like(x)
@@ -370,9 +424,11 @@ def empty_like_layout(x: torch.Tensor) -> torch.Tensor:
 def attn_fwd(q, k, v, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float, beta: float = 0.5,
              bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None, slope=None,
              delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
-             ramp_lambda=0.0, tau=64.0, out=None):
-    """Block-sparse attention forward -> (out like q, lse [1,H,T] fp32, natural log)."""
-    dev = _gpu("attn_fwd", q, k, v, kv_num, kv_idx, docs, ds_tok_end)
+             ramp_lambda=0.0, tau=64.0, out=None, pair_bias=None):
+    """Block-sparse attention forward -> (out like q, lse [1,H,T] fp32, natural log).
+    ``pair_bias`` [H,QB,MAXKV] (aligned with kv_idx) is added to every score of
+    each listed tile."""
+    dev = _gpu("attn_fwd", q, k, v, kv_num, kv_idx, docs, ds_tok_end, pair_bias)
     out = empty_like_layout(q) if out is None else out
     kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
     m = BIAS_MODES[bias_mode]
@@ -381,6 +437,8 @@ def attn_fwd(q, k, v, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float
                        use_slope=use_slope, subtract_b0=subtract_b0, gate_kind=GATE_KINDS[gate_kind],
                        ramp_lambda=ramp_lambda, tau=tau)
     H, T = prm.H, prm.T
+    pb = _pair_bias(pair_bias, kv_idx3)
+    prm.pair_bias = _p(pb)
     lse = torch.empty((1, H, T), dtype=torch.float32, device=dev)
     call("scope_attn_fwd", C.byref(prm), _p(q), _p(k), _p(v), _p(_i32(kv_num)), _p(kv_idx3),
          _p(_i32(docs.reshape(-1))), _p(_i32(ds_tok_end)), _p(table), _p(_f32(coeff_cos)), _p(_f32(coeff_sin)),
@@ -444,7 +502,8 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
 def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
-             ramp_lambda=0.0, tau=64.0, need_coeff_grads: bool = True, phase_hook=None):
+             ramp_lambda=0.0, tau=64.0, need_coeff_grads: bool = True, phase_hook=None, pair_bias=None,
+             need_pair_grad: bool = False):
     """Block-sparse attention backward -> dict of gradients.  With
     ``phase_hook`` the phases (q-major dQ pass; kv-major plan, dK/dV kernel
     and reduce) are launched separately and the hook is called before, between
@@ -465,6 +524,10 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
         raise RuntimeError("attn_bwd: out and dout must share q's strides")
     H, T = prm.H, prm.T
     z = dict(dtype=torch.float32, device=dev)
+    pb = _pair_bias(pair_bias, kv_idx3)
+    dpb = torch.empty(kv_idx3.shape, **z) if need_pair_grad else None
+    prm.pair_bias = _p(pb)
+    prm.dpair_bias = _p(dpb)
     dcc = torch.empty((1, H, T, K), **z) if (m and need_coeff_grads) else None
     dcs = torch.empty((1, H, T, K), **z) if (m and need_coeff_grads) else None
     tok = m == 2 and need_coeff_grads
@@ -491,7 +554,7 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
         call("scope_attn_bwd_phase", C.byref(prm), 16, *args)
         phase_hook("end")
     return dict(dq=dq, dk=dk, dv=dv, dcoeff_cos=dcc, dcoeff_sin=dcs, db0=db0, dslope=dsl, ddelta_main=ddm,
-                dwidth=dwd)
+                dwidth=dwd, dpair_bias=dpb)
 
 
 def log2e() -> float:

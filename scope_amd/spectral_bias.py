@@ -460,11 +460,16 @@ class SpectralBias(nn.Module):
                               budget_temp: float | None = None, logit_scale: float | None = None,
                               prior: Tensor | None = None, noise: str = "counter", gumbel_u: Tensor | None = None,
                               seed: int | None = None, logits: Tensor | None = None,
-                              return_logits: bool = False) -> ScopeBlockMask:
+                              return_logits: bool = False, soft_temp: float | None = None) -> ScopeBlockMask:
         """window ∪ top-``budget_blocks`` block-mean q·k pointers ∪ global
         anchors.  q, k: [1,H,T,D] bf16.  ``noise``: "none" | "uniform"
         (explicit ``gumbel_u`` [H,QB,NB]) | "counter" (in-kernel draw from the
-        Gumbel seed; only while training, like the reference's Gumbel)."""
+        Gumbel seed; only while training, like the reference's Gumbel).
+        ``soft_temp`` > 0 attaches the soft pointer weights log σ(z/soft_temp)
+        of the picks (z the noise-free logit) as ``extras["pair_bias"]``:
+        ``scope_attention`` adds them to the picked tiles' scores, and their
+        gradient flows back to q and k through the block means (with
+        ``logits`` given instead of q̄·k̄, the weights are constants)."""
         T = int(docs.numel())
         H = q.shape[1]
         NB = T // block_size
@@ -487,8 +492,21 @@ class SpectralBias(nn.Module):
         extras = dict(picks=picks)
         if return_logits:
             extras["logits"] = res[3]
-        return ScopeBlockMask(kv_num_blocks=kv_num[None], kv_indices=kv_idx[None], BLOCK_SIZE=block_size,
-                              docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local, extras=extras)
+        bm = ScopeBlockMask(kv_num_blocks=kv_num[None], kv_indices=kv_idx[None], BLOCK_SIZE=block_size,
+                            docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local, extras=extras)
+        if soft_temp is not None and soft_temp > 0 and budget_blocks > 0:
+            if logits is None:
+                from .attention import soft_pointer_bias
+
+                with torch.enable_grad():
+                    extras["pair_bias"] = soft_pointer_bias(q, k, bm, window=window_blocks, n_global=global_blocks,
+                                                            logit_scale=scale, soft_temp=float(soft_temp),
+                                                            prior=prior)
+            else:
+                extras["pair_bias"] = ops.pointer_pair_bias(kv_num, kv_idx, picks, bs=block_size,
+                                                            window=window_blocks, n_global=global_blocks,
+                                                            soft_temp=float(soft_temp), logits_in=logits)
+        return bm
 
     def score_terms(self, outputs: tuple, *, offset: str = "token") -> SpectralTerms:
         """SpectralTerms for ``scope_attention`` from the 12-tuple of forward()."""
