@@ -33,6 +33,15 @@ module's torch steps on the same GPU.
 and slope, probabilities summed per q-block and key block) at the teacher's
 length T=4096 (8 heads, bs 128) and at T=65536.
 
+``--workload train`` times the training-shape layer: T=65536, H=8, D=128,
+block 128 (512 blocks), window 4, 1 global block, pointer budget 4, one
+document, seeded in-kernel Gumbel noise, no needle, the same spectral bias,
+with the soft pointer weights on (``--soft-temp``, default 4): each pick's
+weight log σ(z/τ_w) enters its tile's scores, and the backward carries their
+gradient through the block means into dq and dk (pointer backward timed as
+its own phase).  ``--soft-temp`` also turns the weights on for the default
+workload.
+
 ``--workload decode`` runs the 16-layer decoder (d_model 1024, 8 heads of
 128, MLP 4096 ReLU², vocabulary 50304, bf16, random weights): a prefill of
 131072 seeded uniform-random tokens, then 256 greedy decode steps with the
@@ -70,7 +79,10 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["pointer", "swa", "coeff", "teacher", "decode"], default="pointer")
+    ap.add_argument("--workload", choices=["pointer", "train", "swa", "coeff", "teacher", "decode"],
+                    default="pointer")
+    ap.add_argument("--soft-temp", type=float, default=0.0,
+                    help="soft pointer weights log σ(z/τ) on the picks (0: default, off except --workload train: 4; < 0: off)")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--swa-window", type=int, default=14, help="long-mask window in blocks (--workload swa)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -78,7 +90,7 @@ def parse():
     return ap.parse_args()
 
 
-def make_inputs(H, T, D, bs, seed=0):
+def make_inputs(H, T, D, bs, seed=0, n_docs=None, needle=True):
     import torch
 
     g = torch.Generator().manual_seed(seed)
@@ -86,7 +98,7 @@ def make_inputs(H, T, D, bs, seed=0):
     k = torch.randn((1, H, T, D), generator=g).to(torch.bfloat16)
     v = torch.randn((1, H, T, D), generator=g).to(torch.bfloat16)
     dout = torch.randn((1, H, T, D), generator=g).to(torch.bfloat16)
-    n_docs = max(1, T // 8192)
+    n_docs = max(1, T // 8192) if n_docs is None else n_docs
     cuts = torch.randperm(T - 1, generator=g)[: n_docs - 1] + 1
     flag = torch.zeros(T, dtype=torch.int64)
     flag[cuts] = 1
@@ -104,8 +116,9 @@ def make_inputs(H, T, D, bs, seed=0):
     qb_n = lb - 1  # block lb may hold the next document's first tokens
     dist = max(4, min(64, qb_n - (fb + 3)))
     kb_n = qb_n - dist
-    mq = q[0, :, qb_n * bs:(qb_n + 1) * bs].float().mean(dim=1)
-    k[0, :, kb_n * bs:(kb_n + 1) * bs] = (3.0 * mq[:, None, :]).to(torch.bfloat16)
+    if needle:
+        mq = q[0, :, qb_n * bs:(qb_n + 1) * bs].float().mean(dim=1)
+        k[0, :, kb_n * bs:(kb_n + 1) * bs] = (3.0 * mq[:, None, :]).to(torch.bfloat16)
     W = torch.randn((D, 16), generator=g) * 0.02
     c = q.float() @ W
     coeff_cos, coeff_sin = c[..., :8].contiguous(), c[..., 8:].contiguous()
@@ -117,7 +130,7 @@ def make_inputs(H, T, D, bs, seed=0):
 class Step:
     """The hot path on GPU-resident inputs; phase events on the current stream."""
 
-    def __init__(self, inp, *, bs, window, n_global, budget, seed=1234):
+    def __init__(self, inp, *, bs, window, n_global, budget, seed=1234, soft_temp=0.0):
         import torch
 
         from scope_amd import ops
@@ -129,7 +142,10 @@ class Step:
         self.NB = self.T // bs
         self.table = spectral_table(self.t["omegas"], self.T, bs, "block")
         self.ops = ops
+        self.soft_temp = float(soft_temp)
         self.phases = ["pointer", "stats", "transpose", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv", "attn_bwd_aux"]
+        if self.soft_temp > 0:
+            self.phases.append("pointer_bwd")
         self.ev = {p: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for p in self.phases}
         self.acc = {p: 0.0 for p in self.phases}
@@ -152,11 +168,16 @@ class Step:
         qbar, kbar = ops.block_means(t["q"], t["k"], bs)
         if record:
             self.means_ev[1].record()
+        ls = bs / math.sqrt(t["q"].shape[-1])
         kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=self.NB, H=self.H,
                                                    window=self.window, n_global=self.n_global, budget=self.budget,
-                                                   qbar=qbar, kbar=kbar, temp=1.0,
-                                                   logit_scale=bs / math.sqrt(t["q"].shape[-1]), noise="counter",
+                                                   qbar=qbar, kbar=kbar, temp=1.0, logit_scale=ls, noise="counter",
                                                    seed=self.seed)
+        soft = self.soft_temp > 0
+        pb = None
+        if soft:
+            pb = ops.pointer_pair_bias(kv_num, kv_idx, picks, bs=bs, window=self.window, n_global=self.n_global,
+                                       soft_temp=self.soft_temp, qbar=qbar, kbar=kbar, logit_scale=ls)
         mark("pointer", 1)
         mark("stats", 0)
         counts, values = ops.mask_stats(H=self.H, QB=self.NB, bs=bs, kv_num=kv_num, picks=picks, ds_ptr=ds_ptr,
@@ -169,7 +190,7 @@ class Step:
         mark("attn_fwd", 0)
         out, lse = ops.attn_fwd(t["q"], t["k"], t["v"], kv_num, kv_idx, t["docs"], ds_tok_end, bs=bs, scale=0.12,
                                 beta=0.5, bias_mode="block", table=self.table, coeff_cos=t["coeff_cos"],
-                                coeff_sin=t["coeff_sin"])
+                                coeff_sin=t["coeff_sin"], pair_bias=pb)
         mark("attn_fwd", 1)
         # attn_bwd_dkv is the dK/dV kernel alone; attn_bwd_aux its plan and reduce kernels
         aux = self.aux_ev
@@ -193,9 +214,15 @@ class Step:
 
         grads = ops.attn_bwd(t["q"], t["k"], t["v"], out, t["dout"], lse, kv_num, kv_idx, q_off, q_list, t["docs"],
                              ds_tok_end, bs=bs, scale=0.12, beta=0.5, bias_mode="block", table=self.table,
-                             coeff_cos=t["coeff_cos"], coeff_sin=t["coeff_sin"], phase_hook=hook)
+                             coeff_cos=t["coeff_cos"], coeff_sin=t["coeff_sin"], phase_hook=hook, pair_bias=pb,
+                             need_pair_grad=soft)
+        if soft:
+            mark("pointer_bwd", 0)
+            ops.pointer_bwd(qbar, kbar, kv_num, kv_idx, q_off, q_list, pb, grads["dpair_bias"], grads["dq"],
+                            grads["dk"], bs=bs, logit_scale=ls, soft_temp=self.soft_temp)
+            mark("pointer_bwd", 1)
         self.last = dict(kv_num=kv_num, kv_idx=kv_idx, picks=picks, counts=counts, values=values, out=out, lse=lse,
-                         grads=grads, q_off=q_off, q_list=q_list, ds_tok_end=ds_tok_end)
+                         grads=grads, q_off=q_off, q_list=q_list, ds_tok_end=ds_tok_end, pair_bias=pb)
 
     def collect(self):
         for p in self.phases:
@@ -516,6 +543,8 @@ def cpu_baseline(inp, step, seconds: float, bs: int):
     torch.set_num_threads(os.cpu_count() or 1)
     kv_num = step.last["kv_num"].cpu()
     kv_idx = step.last["kv_idx"].cpu()
+    pb = step.last.get("pair_bias")
+    pb = None if pb is None else pb.float().cpu()
     docs = inp["docs"]
     H, T, D = inp["q"].shape[1:]
     QB = T // bs
@@ -533,7 +562,8 @@ def cpu_baseline(inp, step, seconds: float, bs: int):
         t0 = time.perf_counter()
         res = OA.attention_blocksparse(qq, kk, vv, kv_num[h:h + 1], kv_idx[h:h + 1], docs, bs=bs, scale=0.12,
                                        beta=0.5, bias_mode="block", coeff_cos=cc[h:h + 1], coeff_sin=cs[h:h + 1],
-                                       omegas=om, heads=[0], qblocks=[qb])
+                                       omegas=om, heads=[0], qblocks=[qb],
+                                       pair_bias=None if pb is None else pb[h:h + 1])
         o, _ = res[(0, qb)]
         o.backward(dout[h, qb * bs:(qb + 1) * bs])
         t_used += time.perf_counter() - t0
@@ -571,9 +601,14 @@ def main():
             args.T, args.bs = 65536, 128
         main_swa(args)
         return
+    train = args.workload == "train"
+    if train and (args.T, args.bs, args.window, args.n_global, args.budget) == (131072, 256, 2, 2, 8):
+        # the pointer workload's defaults -> the training shape
+        args.T, args.bs, args.window, args.n_global, args.budget = 65536, 128, 4, 1, 4
+    soft = args.soft_temp if args.soft_temp != 0 else (4.0 if train else 0.0)  # < 0: off
     H, T, D, bs = args.H, args.T, 128, args.bs
-    inp = make_inputs(H, T, D, bs)
-    step = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=args.budget)
+    inp = make_inputs(H, T, D, bs, n_docs=1 if train else None, needle=not train)
+    step = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=args.budget, soft_temp=soft)
     step()
     torch.cuda.synchronize()
     n_act = int(step.last["kv_num"].sum())
@@ -609,12 +644,18 @@ def main():
                    block_means_ms=round(means_ms, 4),
                    block_means_achieved=round(2 * H * T * D * 2 / (means_ms / 1e3) / 1e9, 1),
                    block_means_frac=round(2 * H * T * D * 2 / (means_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4))
-    qb_n, kb_n = inp["needle"]
-    picks = step.last["picks"]
-    needle_sel = dict(q_block=qb_n, key_block=kb_n, distance_blocks=qb_n - kb_n,
-                      selected_heads=int((picks[:, qb_n] == kb_n).any(dim=-1).sum().item()), heads=H)
+    needle_sel = None
+    if not train:
+        qb_n, kb_n = inp["needle"]
+        picks = step.last["picks"]
+        needle_sel = dict(q_block=qb_n, key_block=kb_n, distance_blocks=qb_n - kb_n,
+                          selected_heads=int((picks[:, qb_n] == kb_n).any(dim=-1).sum().item()), heads=H)
+    workload = ("training-shape layer, one SCOPE layer fwd+bwd (pointer select + stats + block-sparse attention "
+                "+ soft pointer weights and their backward)") if train else (
+        "long-context prefill, one SCOPE layer fwd+bwd (pointer select + stats + block-sparse attention)")
     res = {
-        "metric": METRIC,
+        "metric": ("SCOPE attn fwd+bwd active-block TFLOP/s & tokens/s at T=64k with soft pointer weights, 1 MI355X"
+                   if train else METRIC),
         "value": round((F_fwd + F_bwd) / t_step / 1e12, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -626,10 +667,10 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "long-context prefill, one SCOPE layer fwd+bwd (pointer select + stats + "
-                               "block-sparse attention)", "B": 1, "H": H, "T": T, "D": D, "block": bs,
+        "config": {"workload": workload, "B": 1, "H": H, "T": T, "D": D, "block": bs,
                    "window": args.window, "global": args.n_global, "budget": args.budget, "bands": 8,
-                   "bias": "block offsets", "docs": max(1, T // 8192)},
+                   "bias": "block offsets", "docs": 1 if train else max(1, T // 8192),
+                   "soft_pointer_temp": soft if soft > 0 else None},
         "tokens_per_s": round(T / t_step, 1),
         "n_act": n_act,
         "flops_fwd": F_fwd,
@@ -639,13 +680,14 @@ def main():
                                  2),
         "breakdown_ms": {p: round(v_, 4) for p, v_ in ph.items()},
         "needle": needle_sel,
+        "pointer_bwd_ms": round(ph["pointer_bwd"], 4) if soft > 0 else None,
         "roofline": roofline,
         "pointer_roofline": pointer,
     }
     if args.sweep:
         sweep = {}
         for b in (2, 4):
-            st = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=b)
+            st = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=b, soft_temp=soft)
             st()
             torch.cuda.synchronize()
             na = int(st.last["kv_num"].sum())

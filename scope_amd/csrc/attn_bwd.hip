@@ -780,31 +780,31 @@ __global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, const int32_t* _
 struct KvPlan {
   const int32_t* items_start;
   const int32_t* slots_start;
+  const int32_t* q_pos;  // with a pair bias: for each q-list entry, kb's position in that q-block's kv list
   float* part_dk;
   float* part_dv;
   int64_t max_slots;  // per head
   int max_items;      // work items per head (upper bound)
 };
 
-// Pair bias of the item's list entries: for each listed q-block qb, the
-// position of key block kb in qb's kv list (its first kv_num entries are
-// unique and ascending) and the bias there (log2 units; 0 without one).
-__device__ __forceinline__ void dkv_entry_bias(const AttnArgs& a, int h, int kb, int qb, float& eb, int& pos) {
-  const int64_t row = static_cast<int64_t>(h) * a.QB + qb;
-  const int32_t* lst = a.kv_idx + row * a.maxkv;
-  int lo = 0, hi = min(a.kv_num[row], a.maxkv) - 1;
-  pos = -1;
-  while (lo <= hi) {
-    const int mid = (lo + hi) >> 1;
-    const int v = lst[mid];
-    if (v == kb) {
-      pos = mid;
-      break;
-    }
-    if (v < kb) lo = mid + 1;
-    else hi = mid - 1;
+// q_pos[h][i] = the position of key block kb in the kv list of q-block
+// q_list[h][i], for every entry i of kb's q-list (its first kv_num entries
+// are unique; a scan of independent loads).  One workgroup per (kb, h).
+__global__ __launch_bounds__(64) void qpos_kernel(AttnArgs a, int32_t* __restrict__ q_pos) {
+  const int kb = blockIdx.x, h = blockIdx.y;
+  const int NB = a.QB;
+  const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
+  const int64_t base = static_cast<int64_t>(h) * a.QB * a.maxkv;
+  for (int i = qo[kb] + threadIdx.x; i < qo[kb + 1]; i += blockDim.x) {
+    const int qb = a.q_list[base + i];
+    const int64_t row = static_cast<int64_t>(h) * a.QB + qb;
+    const int n = min(a.kv_num[row], a.maxkv);
+    const int32_t* lst = a.kv_idx + row * a.maxkv;
+    int pos = -1;
+    for (int e = 0; e < n; ++e)
+      if (lst[e] == kb) pos = e;
+    q_pos[base + i] = pos;
   }
-  eb = (a.pair_bias && pos >= 0) ? a.pair_bias[row * a.maxkv + pos] * kLog2e : 0.f;
 }
 
 // Sum of x over the 64 lanes of the wavefront.
@@ -1146,7 +1146,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
     dse[tid] = a.ds_tok_end[qb];
     float eb = 0.f;
     int pos = -1;
-    if (a.pair_bias || a.dpair) dkv_entry_bias(a, h, kb, qb, eb, pos);
+    if (pl.q_pos) {
+      pos = pl.q_pos[static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb] + i0 + tid];
+      if (a.pair_bias && pos >= 0) eb = a.pair_bias[(static_cast<int64_t>(h) * a.QB + qb) * a.maxkv + pos] * kLog2e;
+    }
     ebias[tid] = eb;
     epos[tid] = pos;
   }
@@ -1351,13 +1354,13 @@ __device__ __forceinline__ uint4 lds_row16(const uint16_t* tile, const TileOffs1
 
 // One 64-row query tile against this wavefront's 16 keys, first part:
 // per-row offsets, S and dP, then P and dS as bf16 B operands.
-// With DP, the tile's sum of dS over this wavefront's keys is added to *slot
-// (one writer per slot: the wavefront's own entry).
+// With DP, the tile's dS values are added to this lane's running sum dacc
+// (reduced over the wavefront once per list entry by the caller).
 template <int MODE, bool DP>
 __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, float* offw,
                                         const float* tab, float eb, int q0, int lane, int wkv, int doc_kv,
                                         const uint4 (&kreg)[4], const uint4 (&vreg)[4], const TileOffs16& to,
-                                        uint4 (&pb)[2], uint4 (&dsb)[2], float* slot) {
+                                        uint4 (&pb)[2], uint4 (&dsb)[2], float& dacc) {
   const int g = lane >> 4;
   dkv_offsets<MODE>(a, b, offw, tab, eb, lane);
   f32x4_t s[4], dp[4];
@@ -1387,15 +1390,10 @@ __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
-  float dsum = 0.f;
   if (masked)
-    dkv16_probs<MODE, true, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dsum);
+    dkv16_probs<MODE, true, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
   else
-    dkv16_probs<MODE, false, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dsum);
-  if (DP) {
-    dsum = wave_sum(dsum);
-    if (lane == 0) *slot += dsum;
-  }
+    dkv16_probs<MODE, false, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
 }
 
 // Second part: dV^T += dO^T P, dK^T += Q^T dS (step st = 8·kk + md).
@@ -1483,7 +1481,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     dse[tid] = a.ds_tok_end[qb];
     float eb = 0.f;
     int pos = -1;
-    if (a.pair_bias || a.dpair) dkv_entry_bias(a, h, kb, qb, eb, pos);
+    if (pl.q_pos) {
+      pos = pl.q_pos[static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb] + i0 + tid];
+      if (a.pair_bias && pos >= 0) eb = a.pair_bias[(static_cast<int64_t>(h) * a.QB + qb) * a.maxkv + pos] * kLog2e;
+    }
     ebias[tid] = eb;
     epos[tid] = pos;
   }
@@ -1530,14 +1531,30 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   // the other runs MFMAs.  At the leading group's k-th barrier the lagging
   // group is done with tile k-2, whose buffer then takes tile k+1.  Both
   // groups pass n_it + 1 barriers.
+  // pair-bias gradient: this lane's running dS sum of list entry dcur,
+  // reduced over the wavefront when the entry changes (a wavefront takes the
+  // entries in order, each entry's tiles back to back)
+  float dacc = 0.f;
+  int dcur = -1;
+  auto flush = [&]() __attribute__((always_inline)) {
+    if (dcur >= 0) {
+      const float t = wave_sum(dacc);
+      if (lane == 0) pslot[dcur][wave] += t;
+    }
+    dacc = 0.f;
+  };
   auto part_a = [&](const DkvBuf<MODE>& bc, int j, uint4 (&pb)[2], uint4 (&dsb)[2]) __attribute__((always_inline)) {
     int e;
     const int q0 = tile_q0(j, e);
     if (q0 + BM - 1 < wkv_lo) return false;  // every query row precedes this wavefront's keys
+    if (DP && e != dcur) {
+      flush();
+      dcur = e;
+    }
     const bool masked = !((wkv_lo + 15 <= q0) && (dse[e] <= wkv_lo));
     const float* tab = tabs + (MODE == 1 ? e * 16 : 0);
     dkv16_a<MODE, DP>(a, bc, masked, offw[wave], tab, ebias[e], q0, lane, wkv, doc_kv, kreg, vreg, to, pb, dsb,
-                      &pslot[e][wave]);
+                      dacc);
     return true;
   };
   if (wave < 4) {
@@ -1580,8 +1597,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     }
   }
   wait_vm0();  // no copy may still target LDS when the workgroup exits
+  if (DP) {
+    flush();
+    __syncthreads();  // every wavefront's slots are final
+  }
   if (DP && tid < ne && epos[tid] >= 0) {
-    // every slot was last written before the final barrier of the loop above
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < 8; ++w) t += pslot[tid][w];
@@ -1626,7 +1646,8 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl, 
   if (nch <= 1) return;
   const int64_t slot0 = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb];
   const int64_t kv0 = static_cast<int64_t>(kb) * BS;
-  for (int e4 = threadIdx.x; e4 < BS * D / 4; e4 += blockDim.x) {
+  // gridDim.z workgroups share a key block's elements (a long q-list has many chunks)
+  for (int e4 = blockIdx.z * blockDim.x + threadIdx.x; e4 < BS * D / 4; e4 += gridDim.z * blockDim.x) {
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
     for (int c = 0; c < nch; ++c) {
       const float4 pk = reinterpret_cast<const float4*>(pl.part_dk + (slot0 + c) * BS * D)[e4];
@@ -1646,7 +1667,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl, 
 }
 
 struct BwdLayout {
-  int64_t delta, qfeat, items, slots, part_dk, part_dv, dpair, total, max_slots;
+  int64_t delta, qfeat, items, slots, part_dk, part_dv, q_pos, dpair, total, max_slots;
   int max_items;
 };
 
@@ -1671,6 +1692,8 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
   o += al(part);
   L.part_dv = o;
   o += al(part);
+  L.q_pos = o;
+  if (p->pair_bias || p->dpair_bias) o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * 4);
   // pair-bias gradient partials, one per 128-key part of a key block
   L.dpair = o;
   if (p->dpair_bias) o += al(static_cast<int64_t>(p->bs / 128) * p->H * QB * p->maxkv * 4);
@@ -1699,7 +1722,7 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
                        float* dpair_out, hipStream_t s) {
   constexpr int P = BS / 128;
   const int per_xcd = (a.H * max_items + 7) / 8;
-  dim3 gq(grid_q * P), gk(8 * per_xcd * P), gr(a.QB, a.H);
+  dim3 gq(grid_q * P), gk(8 * per_xcd * P), gr(a.QB, a.H, 8);
   // token mode with an active gate runs the kernels' MODE 3 variant
   const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
   bool dq_done = false;
@@ -1724,9 +1747,12 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
       hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 0>), gq, dim3(256), 0, s, a);
   }
   if (phases & SCOPE_BWD_DKV) phases |= SCOPE_BWD_DKV_PLAN | SCOPE_BWD_DKV_MAIN | SCOPE_BWD_DKV_REDUCE;
-  if (phases & SCOPE_BWD_DKV_PLAN)
+  if (phases & SCOPE_BWD_DKV_PLAN) {
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start));
+    if (pl.q_pos)
+      hipLaunchKernelGGL(qpos_kernel, dim3(a.QB, a.H), dim3(64), 0, s, a, const_cast<int32_t*>(pl.q_pos));
+  }
   const bool dp = a.dpair != nullptr;  // the pair-bias gradient runs in its own instantiation
   if ((phases & SCOPE_BWD_DKV_MAIN) && mode != SCOPE_BIAS_TOKEN) {
     // 16 keys per wavefront, 8 wavefronts (two per SIMD) per 128 keys
@@ -1826,6 +1852,7 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   pl.slots_start = reinterpret_cast<const int32_t*>(ws + L.slots);
   pl.part_dk = reinterpret_cast<float*>(ws + L.part_dk);
   pl.part_dv = reinterpret_cast<float*>(ws + L.part_dv);
+  pl.q_pos = (p->pair_bias || p->dpair_bias) ? reinterpret_cast<const int32_t*>(ws + L.q_pos) : nullptr;
   pl.max_slots = L.max_slots;
   pl.max_items = L.max_items;
   hipStream_t s = as_stream(stream);

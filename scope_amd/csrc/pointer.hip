@@ -665,13 +665,18 @@ __global__ __launch_bounds__(256) void ptr_bwd_q_kernel(scope_ptr_bwd_params P, 
 
 // Pointer backward, k side: per (h, kb), dk̄ = ls·Σ dz·q̄_qb over the q-blocks
 // that list kb (the transposed list, ascending), and every row of the key
-// block gets dk̄/bs.
+// block gets dk̄/bs.  The list is taken in chunks of 256 entries: first each
+// thread finds its entry's dz (kb's position in that q-block's list, a scan
+// of at most 64 contiguous entries), then the columns are summed over the
+// chunk in list order.
 __global__ __launch_bounds__(256) void ptr_bwd_k_kernel(scope_ptr_bwd_params P, const float* __restrict__ qbar,
                                                         const int32_t* __restrict__ kv_num,
                                                         const int32_t* __restrict__ kv_idx,
                                                         const int32_t* __restrict__ q_off,
                                                         const int32_t* __restrict__ q_list,
                                                         const float* __restrict__ dz, uint16_t* __restrict__ dk) {
+  __shared__ float wz[256];
+  __shared__ int wq[256];
   __shared__ float dks[128];
   __shared__ float part[2][128];
   const int kb = blockIdx.x, h = blockIdx.y;
@@ -679,33 +684,33 @@ __global__ __launch_bounds__(256) void ptr_bwd_k_kernel(scope_ptr_bwd_params P, 
   const int32_t* qo = q_off + static_cast<int64_t>(h) * (NB + 1);
   const int32_t* ql = q_list + static_cast<int64_t>(h) * NB * L + qo[kb];
   const int nq = qo[kb + 1] - qo[kb];
-  // two halves of the q-list in parallel (threads 0-127 and 128-255), each in list order
   const int d = threadIdx.x & 127, half = threadIdx.x >> 7;
   float acc = 0.f;
-  if (d < P.D) {
-    const int mid = (nq + 1) / 2;
-    const int i0 = half == 0 ? 0 : mid, i1 = half == 0 ? mid : nq;
-    for (int i = i0; i < i1; ++i) {
-      const int qb = ql[i];
+  for (int c0 = 0; c0 < nq; c0 += 256) {
+    const int cn = min(256, nq - c0);
+    __syncthreads();  // the previous chunk's wz / wq are consumed
+    if (threadIdx.x < cn) {
+      const int qb = ql[c0 + threadIdx.x];
       const int64_t row = static_cast<int64_t>(h) * NB + qb;
-      // position of kb in qb's list (unique and ascending in its first kv_num entries)
-      int lo = 0, hi = min(kv_num[row], L) - 1, pos = -1;
-      while (lo <= hi) {
-        const int m = (lo + hi) >> 1;
-        const int v = kv_idx[row * L + m];
-        if (v == kb) {
-          pos = m;
-          break;
-        }
-        if (v < kb) lo = m + 1;
-        else hi = m - 1;
-      }
-      if (pos < 0) continue;
-      const float z = dz[row * L + pos];
-      if (z != 0.f) acc += z * qbar[row * P.D + d];
+      const int n = min(kv_num[row], L);
+      float z = 0.f;
+      for (int e = 0; e < n; ++e)
+        if (kv_idx[row * L + e] == kb) z = dz[row * L + e];
+      wz[threadIdx.x] = z;
+      wq[threadIdx.x] = qb;
     }
-    part[half][d] = acc;
+    __syncthreads();
+    if (d < P.D) {
+      // the two halves of the chunk, each in list order
+      const int mid = (cn + 1) / 2;
+      const int i0 = half == 0 ? 0 : mid, i1 = half == 0 ? mid : cn;
+      for (int i = i0; i < i1; ++i) {
+        const float z = wz[i];
+        if (z != 0.f) acc += z * qbar[(static_cast<int64_t>(h) * NB + wq[i]) * P.D + d];
+      }
+    }
   }
+  if (d < P.D) part[half][d] = acc;
   __syncthreads();
   if (threadIdx.x < P.D) dks[threadIdx.x] = P.logit_scale * (part[0][threadIdx.x] + part[1][threadIdx.x]) /
                                            static_cast<float>(P.bs);
