@@ -17,6 +17,10 @@ noise, dO ~ N(0,1).
 value = active-block TFLOP/s = (F_fwd + F_bwd) / step time, with
 F_fwd = 4·bs²·D·N_act, F_bwd = 10·bs²·D·N_act, N_act = Σ kv_num_blocks.
 
+The million-token layer (T=1048576, 4096 blocks of 256, window 2, one global
+block, budget 8, one document, no needle) is the same workload with
+``--T 1048576 --n-global 1 --docs 1 --no-needle``.
+
 ``--workload swa`` times instead a layer without the pointer mask: the long
 sliding-window mask (scoped_medium.py:535-576, window 14 blocks of 128 = the
 reference's final 1792-token window) built from the document ids, the q-list
@@ -84,6 +88,9 @@ def parse():
     ap.add_argument("--soft-temp", type=float, default=0.0,
                     help="soft pointer weights log σ(z/τ) on the picks (0: default, off except --workload train: 4; < 0: off)")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--docs", type=int, default=0,
+                    help="documents at seeded positions (0: one per 8192 tokens; the training shape: 1)")
+    ap.add_argument("--no-needle", action="store_true", help="no planted needle block")
     ap.add_argument("--swa-window", type=int, default=14, help="long-mask window in blocks (--workload swa)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the run, one plain device copy of this many MiB (calibrates HBM byte counters)")
@@ -124,7 +131,7 @@ def make_inputs(H, T, D, bs, seed=0, n_docs=None, needle=True):
     coeff_cos, coeff_sin = c[..., :8].contiguous(), c[..., 8:].contiguous()
     omegas = torch.tensor([math.pi * 2.0 ** (-i) for i in range(8)], dtype=torch.float32)
     return dict(q=q, k=k, v=v, dout=dout, docs=docs, coeff_cos=coeff_cos, coeff_sin=coeff_sin, omegas=omegas,
-                needle=(qb_n, kb_n))
+                needle=(qb_n, kb_n) if needle else None)
 
 
 class Step:
@@ -607,7 +614,9 @@ def main():
         args.T, args.bs, args.window, args.n_global, args.budget = 65536, 128, 4, 1, 4
     soft = args.soft_temp if args.soft_temp != 0 else (4.0 if train else 0.0)  # < 0: off
     H, T, D, bs = args.H, args.T, 128, args.bs
-    inp = make_inputs(H, T, D, bs, n_docs=1 if train else None, needle=not train)
+    n_docs = args.docs if args.docs > 0 else (1 if train else max(1, T // 8192))
+    inp = make_inputs(H, T, D, bs, n_docs=n_docs, needle=not (train or args.no_needle))
+    print(f"inputs ready: H={H} T={T} bs={bs} docs={n_docs}", file=sys.stderr, flush=True)
     step = Step(inp, bs=bs, window=args.window, n_global=args.n_global, budget=args.budget, soft_temp=soft)
     step()
     torch.cuda.synchronize()
@@ -645,7 +654,7 @@ def main():
                    block_means_achieved=round(2 * H * T * D * 2 / (means_ms / 1e3) / 1e9, 1),
                    block_means_frac=round(2 * H * T * D * 2 / (means_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4))
     needle_sel = None
-    if not train:
+    if inp.get("needle") is not None:
         qb_n, kb_n = inp["needle"]
         picks = step.last["picks"]
         needle_sel = dict(q_block=qb_n, key_block=kb_n, distance_blocks=qb_n - kb_n,
@@ -669,7 +678,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": workload, "B": 1, "H": H, "T": T, "D": D, "block": bs,
                    "window": args.window, "global": args.n_global, "budget": args.budget, "bands": 8,
-                   "bias": "block offsets", "docs": 1 if train else max(1, T // 8192),
+                   "bias": "block offsets", "docs": n_docs,
                    "soft_pointer_temp": soft if soft > 0 else None},
         "tokens_per_s": round(T / t_step, 1),
         "n_act": n_act,

@@ -27,7 +27,11 @@
 
 namespace scope {
 
-constexpr int kChunk = 16;  // q-blocks per dK/dV work item
+// q-blocks per dK/dV work item: q-lists of up to kChunk entries (the window,
+// the pointer picks and the global blocks of documents up to kChunk blocks
+// long) are one item and write bf16 directly; only longer lists pay for fp32
+// partials and their reduce
+constexpr int kChunk = 32;
 
 // ---------------------------------------------------------------------------
 // pass A
@@ -727,50 +731,59 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, const int32_t* __restrict__ q_off,
                                                          int32_t* __restrict__ items_start,
-                                                         int32_t* __restrict__ slots_start) {
+                                                         int32_t* __restrict__ slots_start,
+                                                         int32_t* __restrict__ multi) {
   const int h = blockIdx.x;
   const int32_t* off = q_off + static_cast<int64_t>(h) * (NB + 1);
   int32_t* it = items_start + static_cast<int64_t>(h) * (NB + 1);
   int32_t* sl = slots_start + static_cast<int64_t>(h) * (NB + 1);
-  __shared__ int s_it[1024], s_sl[1024];
-  __shared__ int carry_it, carry_sl;
-  if (threadIdx.x == 0) carry_it = carry_sl = 0;
+  int32_t* ml = multi + static_cast<int64_t>(h) * (NB + 1);
+  __shared__ int s_it[1024], s_sl[1024], s_ml[1024];
+  __shared__ int carry_it, carry_sl, carry_ml;
+  if (threadIdx.x == 0) carry_it = carry_sl = carry_ml = 0;
   __syncthreads();
   for (int base = 0; base < NB; base += 1024) {
     const int kb = base + threadIdx.x;
-    int nit = 0, nsl = 0;
+    int nit = 0, nsl = 0, nml = 0;
     if (kb < NB) {
       const int n = off[kb + 1] - off[kb];
       const int nch = max(1, (n + kChunk - 1) / kChunk);
       nit = nch;
       nsl = nch > 1 ? nch : 0;
+      nml = nch > 1 ? 1 : 0;
     }
     s_it[threadIdx.x] = nit;
     s_sl[threadIdx.x] = nsl;
+    s_ml[threadIdx.x] = nml;
     __syncthreads();
     for (int o = 1; o < 1024; o <<= 1) {
       const int ai = threadIdx.x >= o ? s_it[threadIdx.x - o] : 0;
       const int as = threadIdx.x >= o ? s_sl[threadIdx.x - o] : 0;
+      const int am = threadIdx.x >= o ? s_ml[threadIdx.x - o] : 0;
       __syncthreads();
       s_it[threadIdx.x] += ai;
       s_sl[threadIdx.x] += as;
+      s_ml[threadIdx.x] += am;
       __syncthreads();
     }
-    const int ci = carry_it, cl = carry_sl;
+    const int ci = carry_it, cl = carry_sl, cm = carry_ml;
     if (kb < NB) {
       it[kb] = ci + s_it[threadIdx.x] - nit;
       sl[kb] = cl + s_sl[threadIdx.x] - nsl;
+      if (nml) ml[1 + cm + s_ml[threadIdx.x] - 1] = kb;  // ascending key blocks
     }
     __syncthreads();
     if (threadIdx.x == 1023) {
       carry_it = ci + s_it[1023];
       carry_sl = cl + s_sl[1023];
+      carry_ml = cm + s_ml[1023];
     }
     __syncthreads();
   }
   if (threadIdx.x == 0) {
     it[NB] = carry_it;
     sl[NB] = carry_sl;
+    ml[0] = carry_ml;
   }
 }
 
@@ -780,6 +793,7 @@ __global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, const int32_t* _
 struct KvPlan {
   const int32_t* items_start;
   const int32_t* slots_start;
+  const int32_t* multi;  // per head [NB+1]: the count, then the key blocks with more than one chunk
   const int32_t* q_pos;  // with a pair bias: for each q-list entry, kb's position in that q-block's kv list
   float* part_dk;
   float* part_dv;
@@ -1153,11 +1167,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
     ebias[tid] = eb;
     epos[tid] = pos;
   }
-  if (DP && tid < kChunk * 4) pslot[tid / 4][tid % 4] = 0.f;
-  if (MODE == 1 && tid < ne * 16) {
-    // block-mode table row of distance qb - kb (clamped: a later key block is fully masked anyway)
-    const int r = min(max(ql[i0 + tid / 16] - kb, 0), NB - 1);
-    tabs[tid] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + tid % 16];
+  for (int t = tid; DP && t < kChunk * 4; t += blockDim.x) pslot[t / 4][t % 4] = 0.f;
+  // block-mode table row of distance qb - kb (clamped: a later key block is fully masked anyway)
+  for (int t = tid; MODE == 1 && t < ne * 16; t += blockDim.x) {
+    const int r = min(max(ql[i0 + t / 16] - kb, 0), NB - 1);
+    tabs[t] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + t % 16];
   }
   if (n_it > 0) {
     const int64_t q0 = static_cast<int64_t>(qb_first) * BS + (skip0 % NS) * BM;
@@ -1488,10 +1502,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     ebias[tid] = eb;
     epos[tid] = pos;
   }
-  if (DP && tid < kChunk * 8) pslot[tid / 8][tid % 8] = 0.f;
-  if (MODE == 1 && tid < ne * 16) {
-    const int r = min(max(ql[i0 + tid / 16] - kb, 0), NB - 1);
-    tabs[tid] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + tid % 16];
+  for (int t = tid; DP && t < kChunk * 8; t += blockDim.x) pslot[t / 8][t % 8] = 0.f;
+  for (int t = tid; MODE == 1 && t < ne * 16; t += blockDim.x) {
+    const int r = min(max(ql[i0 + t / 16] - kb, 0), NB - 1);
+    tabs[t] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + t % 16];
   }
   if (n_it > 0 && wave < 4) {
     const int64_t q0 = static_cast<int64_t>(qb_first) * BS + (skip0 % NS) * BM;
@@ -1635,39 +1649,85 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   }
 }
 
-// Sum the chunk partials of every multi-chunk key block in chunk order.
-__global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl, int BS) {
-  constexpr int D = 128;
+// dK and dV of the key blocks whose q-list spans several chunks: the sum of
+// the chunks' fp32 partials in chunk order, dK scaled, rounded to bf16.  A
+// fixed grid walks the work units (multi-chunk key block of any head, one of
+// kSlices column slices), so no workgroup is launched for a single-chunk
+// block and a long q-list (a global block listed by every q-block of a long
+// document) is summed by many workgroups.  Each thread sums PT float4
+// columns, two chunks at a time (2·2·PT loads in flight), which spreads the
+// unit's dependent index loads over many data loads.
+template <int BS>
+__global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) {
+  constexpr int D = 128, kSlices = 8, PT = BS * D / 4 / kSlices / 256;
+  constexpr int64_t per_slot = static_cast<int64_t>(BS) * D / 4;  // float4 per partial
   const int NB = a.QB;
-  const int kb = blockIdx.x, h = blockIdx.y;
-  const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
-  const int nq = qo[kb + 1] - qo[kb];
-  const int nch = max(1, (nq + kChunk - 1) / kChunk);
-  if (nch <= 1) return;
-  const int64_t slot0 = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb];
-  const int64_t kv0 = static_cast<int64_t>(kb) * BS;
-  // gridDim.z workgroups share a key block's elements (a long q-list has many chunks)
-  for (int e4 = blockIdx.z * blockDim.x + threadIdx.x; e4 < BS * D / 4; e4 += gridDim.z * blockDim.x) {
-    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
-    for (int c = 0; c < nch; ++c) {
-      const float4 pk = reinterpret_cast<const float4*>(pl.part_dk + (slot0 + c) * BS * D)[e4];
-      const float4 pv = reinterpret_cast<const float4*>(pl.part_dv + (slot0 + c) * BS * D)[e4];
-      sk.x += pk.x; sk.y += pk.y; sk.z += pk.z; sk.w += pk.w;
-      sv.x += pv.x; sv.y += pv.y; sv.z += pv.z; sv.w += pv.w;
+  int total = 0;
+  for (int h = 0; h < a.H; ++h) total += pl.multi[static_cast<int64_t>(h) * (NB + 1)];
+  const int64_t units = static_cast<int64_t>(total) * kSlices;
+  for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
+    int m = static_cast<int>(u / kSlices);
+    const int e0 = static_cast<int>(u % kSlices) * PT * 256 + threadIdx.x;
+    int h = 0;
+    for (int c = pl.multi[0]; m >= c && h + 1 < a.H; c = pl.multi[static_cast<int64_t>(h) * (NB + 1)]) {
+      m -= c;
+      ++h;
     }
-    const int r = (e4 * 4) / D, d = (e4 * 4) % D;
-    uint2 vk, vv;
-    vk.x = cvt_pk_bf16(sk.x * a.scale, sk.y * a.scale);
-    vk.y = cvt_pk_bf16(sk.z * a.scale, sk.w * a.scale);
-    vv.x = cvt_pk_bf16(sv.x, sv.y);
-    vv.y = cvt_pk_bf16(sv.z, sv.w);
-    *reinterpret_cast<uint2*>(a.dk + h * a.k_sh + (kv0 + r) * a.k_st + d) = vk;
-    *reinterpret_cast<uint2*>(a.dv + h * a.v_sh + (kv0 + r) * a.v_st + d) = vv;
+    const int kb = pl.multi[static_cast<int64_t>(h) * (NB + 1) + 1 + m];
+    const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
+    const int nch = (qo[kb + 1] - qo[kb] + kChunk - 1) / kChunk;
+    const int64_t slot0 = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb];
+    const float4* pk = reinterpret_cast<const float4*>(pl.part_dk) + slot0 * per_slot + e0;
+    const float4* pv = reinterpret_cast<const float4*>(pl.part_dv) + slot0 * per_slot + e0;
+    float4 sk[PT], sv[PT];
+#pragma unroll
+    for (int t = 0; t < PT; ++t) sk[t] = sv[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [](float4& acc, const float4 x) __attribute__((always_inline)) {
+      acc.x += x.x;
+      acc.y += x.y;
+      acc.z += x.z;
+      acc.w += x.w;
+    };
+    for (int c = 0; c < nch; c += 2) {
+      const bool two = c + 1 < nch;
+      float4 xk[2][PT], xv[2][PT];
+#pragma unroll
+      for (int t = 0; t < PT; ++t) {
+        xk[0][t] = pk[c * per_slot + t * 256];
+        xv[0][t] = pv[c * per_slot + t * 256];
+        if (two) {
+          xk[1][t] = pk[(c + 1) * per_slot + t * 256];
+          xv[1][t] = pv[(c + 1) * per_slot + t * 256];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < PT; ++t) {
+        add(sk[t], xk[0][t]);
+        add(sv[t], xv[0][t]);
+        if (two) {
+          add(sk[t], xk[1][t]);
+          add(sv[t], xv[1][t]);
+        }
+      }
+    }
+    const int64_t kv0 = static_cast<int64_t>(kb) * BS;
+#pragma unroll
+    for (int t = 0; t < PT; ++t) {
+      const int e4 = e0 + t * 256;
+      const int r = (e4 * 4) / D, d = (e4 * 4) % D;
+      uint2 vk, vv;
+      vk.x = cvt_pk_bf16(sk[t].x * a.scale, sk[t].y * a.scale);
+      vk.y = cvt_pk_bf16(sk[t].z * a.scale, sk[t].w * a.scale);
+      vv.x = cvt_pk_bf16(sv[t].x, sv[t].y);
+      vv.y = cvt_pk_bf16(sv[t].z, sv[t].w);
+      *reinterpret_cast<uint2*>(a.dk + h * a.k_sh + (kv0 + r) * a.k_st + d) = vk;
+      *reinterpret_cast<uint2*>(a.dv + h * a.v_sh + (kv0 + r) * a.v_st + d) = vv;
+    }
   }
 }
 
 struct BwdLayout {
-  int64_t delta, qfeat, items, slots, part_dk, part_dv, q_pos, dpair, total, max_slots;
+  int64_t delta, qfeat, items, slots, multi, part_dk, part_dv, q_pos, dpair, total, max_slots;
   int max_items;
 };
 
@@ -1686,6 +1746,8 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
   L.items = o;
   o += al(static_cast<int64_t>(p->H) * (NB + 1) * 4);
   L.slots = o;
+  o += al(static_cast<int64_t>(p->H) * (NB + 1) * 4);
+  L.multi = o;
   o += al(static_cast<int64_t>(p->H) * (NB + 1) * 4);
   const int64_t part = static_cast<int64_t>(p->H) * L.max_slots * p->bs * 128 * 4;
   L.part_dk = o;
@@ -1722,7 +1784,7 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
                        float* dpair_out, hipStream_t s) {
   constexpr int P = BS / 128;
   const int per_xcd = (a.H * max_items + 7) / 8;
-  dim3 gq(grid_q * P), gk(8 * per_xcd * P), gr(a.QB, a.H, 8);
+  dim3 gq(grid_q * P), gk(8 * per_xcd * P), gr(4096);
   // token mode with an active gate runs the kernels' MODE 3 variant
   const bool gate = a.gate_kind != SCOPE_GATE_NONE && a.ramp_lambda > 0.f;
   bool dq_done = false;
@@ -1749,7 +1811,7 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
   if (phases & SCOPE_BWD_DKV) phases |= SCOPE_BWD_DKV_PLAN | SCOPE_BWD_DKV_MAIN | SCOPE_BWD_DKV_REDUCE;
   if (phases & SCOPE_BWD_DKV_PLAN) {
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
-                       const_cast<int32_t*>(pl.slots_start));
+                       const_cast<int32_t*>(pl.slots_start), const_cast<int32_t*>(pl.multi));
     if (pl.q_pos)
       hipLaunchKernelGGL(qpos_kernel, dim3(a.QB, a.H), dim3(64), 0, s, a, const_cast<int32_t*>(pl.q_pos));
   }
@@ -1775,7 +1837,7 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2, false>), gk, dim3(256), 0, s, a, pl);
   }
   if (phases & SCOPE_BWD_DKV_REDUCE) {
-    hipLaunchKernelGGL(bwd_reduce_kernel, gr, dim3(256), 0, s, a, pl, BS);
+    hipLaunchKernelGGL(bwd_reduce_kernel<BS>, gr, dim3(256), 0, s, a, pl);
     if (a.dpair && dpair_out) {
       const int64_t n = static_cast<int64_t>(a.H) * a.QB * a.maxkv;
       const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
@@ -1850,6 +1912,7 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   KvPlan pl;
   pl.items_start = reinterpret_cast<const int32_t*>(ws + L.items);
   pl.slots_start = reinterpret_cast<const int32_t*>(ws + L.slots);
+  pl.multi = reinterpret_cast<const int32_t*>(ws + L.multi);
   pl.part_dk = reinterpret_cast<float*>(ws + L.part_dk);
   pl.part_dv = reinterpret_cast<float*>(ws + L.part_dv);
   pl.q_pos = (p->pair_bias || p->dpair_bias) ? reinterpret_cast<const int32_t*>(ws + L.q_pos) : nullptr;
