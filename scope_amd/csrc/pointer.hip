@@ -401,25 +401,37 @@ __device__ __forceinline__ bool better(float za, int ka, float zb, int kb) {
   return za > zb || (za == zb && ka < kb);
 }
 
+// One wavefront per q-block, kScoreQ q-blocks per workgroup.  The workgroup
+// walks the key blocks of its range in chunks of 64 (one candidate per lane):
+// each chunk's k̄ rows are staged in LDS once for all kScoreQ wavefronts, the
+// next chunk's rows load into registers while the current one is scored, and
+// the workgroups are issued last q-blocks first (they have the most
+// candidates).
+constexpr int kScoreQ = 8;
+
 template <int D>
-__global__ __launch_bounds__(256) void ptr_score_kernel(ScoreLaunch A, const float* __restrict__ qbar,
-                                                         const float* __restrict__ kbar,
-                                                         const float* __restrict__ logits_in,
-                                                         const float* __restrict__ prior,
-                                                         const float* __restrict__ gumbel_u,
-                                                         const int32_t* __restrict__ ds_ptr_a,
-                                                         const int32_t* __restrict__ ds_local_a,
-                                                         int32_t* __restrict__ kv_num, int32_t* __restrict__ kv_idx,
-                                                         int32_t* __restrict__ picks, float* __restrict__ logits_out) {
+__global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, const float* __restrict__ qbar,
+                                                                 const float* __restrict__ kbar,
+                                                                 const float* __restrict__ logits_in,
+                                                                 const float* __restrict__ prior,
+                                                                 const float* __restrict__ gumbel_u,
+                                                                 const int32_t* __restrict__ ds_ptr_a,
+                                                                 const int32_t* __restrict__ ds_local_a,
+                                                                 int32_t* __restrict__ kv_num,
+                                                                 int32_t* __restrict__ kv_idx,
+                                                                 int32_t* __restrict__ picks,
+                                                                 float* __restrict__ logits_out) {
   constexpr int kStride = D + 4;  // padded k̄ row in LDS (16-byte aligned, conflict-free float4 reads)
-  __shared__ float ks[kWave * kStride];
-  __shared__ int lists[4 * 64];
+  constexpr int NT = kScoreQ * kWave;
+  constexpr int PF = (kWave * D / 4 + NT - 1) / NT;  // float4 of a chunk per thread
+  __shared__ float ks[2][kWave * kStride];
+  __shared__ int lists[kScoreQ * 64];
   const scope_ptr_score_params& P = A.p;
   const int NB = P.NB;
   const int wave = threadIdx.x / kWave;
   const int lane = lane_id();
   const int h = blockIdx.y;
-  const int qb0 = blockIdx.x * 4;
+  const int qb0 = (gridDim.x - 1 - blockIdx.x) * kScoreQ;
   const int qb = __builtin_amdgcn_readfirstlane(qb0 + wave);
   const bool active = qb < NB;
   const int qbc = active ? qb : NB - 1;
@@ -449,17 +461,36 @@ __global__ __launch_bounds__(256) void ptr_score_kernel(ScoreLaunch A, const flo
 
   // kb range of the workgroup: [ds_ptr of its first q-block, its last q-block]
   const int lo_wg = ds_ptr_a[qb0];
-  const int hi_wg = min(qb0 + 3, NB - 1);
+  const int hi_wg = min(qb0 + kScoreQ - 1, NB - 1);
+  float4 pf[PF];
+  // rows kb0 .. min(kb0 + 63, hi_wg) of k̄ into registers, then into buffer b
+  auto fetch = [&](int kb0) __attribute__((always_inline)) {
+    const int nrow = min(kWave, hi_wg - kb0 + 1);
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = threadIdx.x + j * NT, rr = i / (D / 4), cc = i % (D / 4);
+      pf[j] = i < kWave * D / 4 && rr < nrow
+                  ? *reinterpret_cast<const float4*>(kbar + (static_cast<int64_t>(h) * NB + kb0 + rr) * D + cc * 4)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stash = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = threadIdx.x + j * NT, rr = i / (D / 4), cc = i % (D / 4);
+      if (i < kWave * D / 4) *reinterpret_cast<float4*>(&ks[b][rr * kStride + cc * 4]) = pf[j];
+    }
+  };
+  if (!logits_in) {
+    fetch(lo_wg);
+    stash(0);
+  }
+  int buf = 0;
   for (int kb0 = lo_wg; kb0 <= hi_wg; kb0 += kWave) {
+    const bool more = kb0 + kWave <= hi_wg;
     if (!logits_in) {
-      __syncthreads();
-      const int nrow = min(kWave, hi_wg - kb0 + 1);
-      for (int i = threadIdx.x; i < nrow * (D / 4); i += blockDim.x) {
-        const int rr = i / (D / 4), cc = i % (D / 4);
-        const float4 v = *reinterpret_cast<const float4*>(kbar + (static_cast<int64_t>(h) * NB + kb0 + rr) * D + cc * 4);
-        *reinterpret_cast<float4*>(&ks[rr * kStride + cc * 4]) = v;
-      }
-      __syncthreads();
+      __syncthreads();  // ks[buf] is complete; every wavefront is done with ks[buf ^ 1]
+      if (more) fetch(kb0 + kWave);
     }
     const int kb = kb0 + lane;
     const bool cand = active && kb >= ds_p && kb <= qbc && !(kb >= wlo) && !(G > 0 && kb <= ghi);
@@ -470,7 +501,7 @@ __global__ __launch_bounds__(256) void ptr_score_kernel(ScoreLaunch A, const flo
         logit = logits_in[rowq * NB + kb];
       } else {
         float acc = 0.f;
-        const float* kr = &ks[lane * kStride];
+        const float* kr = &ks[buf][lane * kStride];
 #pragma unroll
         for (int d = 0; d < D; d += 4) {
           const float4 kv4 = *reinterpret_cast<const float4*>(kr + d);
@@ -506,6 +537,10 @@ __global__ __launch_bounds__(256) void ptr_score_kernel(ScoreLaunch A, const flo
           ck = k2;
         }
       }
+    }
+    if (!logits_in && more) {
+      stash(buf ^ 1);
+      buf ^= 1;
     }
   }
   if (logits_out && active) {
@@ -828,12 +863,12 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
   A.L = min(p->window, p->NB) + p->budget + min(p->n_global, p->NB);
   A.N = next_pow2(A.L);
   SCOPE_REQUIRE(A.N <= 64, "scope_pointer_select: list length %d exceeds 64", A.L);
-  dim3 grid(ceil_div(p->NB, 4), p->H);
+  dim3 grid(ceil_div(p->NB, kScoreQ), p->H);
   if (p->D == 128)
-    hipLaunchKernelGGL(ptr_score_kernel<128>, grid, dim3(256), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
+    hipLaunchKernelGGL(ptr_score_kernel<128>, grid, dim3(kScoreQ * 64), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
                        gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, picks, logits_out);
   else
-    hipLaunchKernelGGL(ptr_score_kernel<64>, grid, dim3(256), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
+    hipLaunchKernelGGL(ptr_score_kernel<64>, grid, dim3(kScoreQ * 64), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
                        gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, picks, logits_out);
   return check_launch("ptr_score_kernel");
 }
