@@ -50,7 +50,8 @@ workload.
 128, MLP 4096 ReLU², vocabulary 50304, bf16, random weights): a prefill of
 131072 seeded uniform-random tokens, then 256 greedy decode steps with the
 pointer lists (window 4 blocks of 128, budget 4, 1 global) reselected at every
-new q-block.  value = decode tokens/s; the prefill time is reported beside it.
+new q-block (the steps inside a block replay one captured HIP graph).
+value = decode tokens/s; the prefill time is reported beside it.
 """
 from __future__ import annotations
 

@@ -377,6 +377,15 @@ int64_t scope_decode_workspace_bytes(const scope_decode_params* p);
 int scope_decode_attn(const scope_decode_params* p, const uint16_t* q, const uint16_t* k_cache,
                       const uint16_t* v_cache, const int32_t* kv_num, const int32_t* kv_idx,
                       const int32_t* docs, void* workspace, uint16_t* out, float* lse, void* stream);
+/* As scope_decode_attn with the position read from device memory (*t_dev;
+ * p->t is ignored; a position outside [0, T_cap) gives an all-zero output and
+ * lse = -inf).  No counterpart in the reference, which has no decode loop: for
+ * callers that keep the position on the device, such as a decode step
+ * captured once in a HIP graph and replayed for every token. */
+int scope_decode_attn_at(const scope_decode_params* p, const int64_t* t_dev, const uint16_t* q,
+                         const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* kv_num,
+                         const int32_t* kv_idx, const int32_t* docs, void* workspace, uint16_t* out,
+                         float* lse, void* stream);
 
 int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
 int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,

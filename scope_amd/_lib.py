@@ -97,6 +97,7 @@ _PROTOS = {
     "scope_attn_bwd_workspace_bytes": (c_int64, [C.POINTER(AttnParams)]),
     "scope_decode_workspace_bytes": (c_int64, [C.POINTER(DecodeParams)]),
     "scope_decode_attn": (c_int, [C.POINTER(DecodeParams)] + [P] * 10),
+    "scope_decode_attn_at": (c_int, [C.POINTER(DecodeParams)] + [P] * 11),
     "scope_attn_bwd": (c_int, [C.POINTER(AttnParams)] + [P] * 30),
     "scope_attn_bwd_phase": (c_int, [C.POINTER(AttnParams), c_int] + [P] * 30),
     "scope_probe_mfma_flops": (c_int64, [c_int, c_int]),

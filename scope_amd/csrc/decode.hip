@@ -27,12 +27,16 @@ __global__ __launch_bounds__(64) void decode_part_kernel(scope_decode_params p, 
                                                          const uint16_t* __restrict__ vc,
                                                          const int32_t* __restrict__ kv_num,
                                                          const int32_t* __restrict__ kv_idx,
-                                                         const int32_t* __restrict__ docs, float* __restrict__ work) {
+                                                         const int32_t* __restrict__ docs, float* __restrict__ work,
+                                                         const int64_t* __restrict__ t_dev) {
   const int e = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
   float* w = work + (static_cast<int64_t>(h) * p.maxkv + e) * (kDecD + 2);
   const int n = kv_num[h];
+  // the position: from the parameters, or from device memory (checked here:
+  // a position outside the cache gives no mass and an all-zero output)
+  const int64_t t = t_dev ? *t_dev : p.t;
   const int64_t k0 = e < n ? static_cast<int64_t>(kv_idx[static_cast<int64_t>(h) * p.maxkv + e]) * p.bs : -1;
-  if (k0 < 0 || k0 > p.t) {  // unused slot, or a block after the query: no mass
+  if (k0 < 0 || k0 > t || t < 0 || t >= p.T_cap) {  // unused slot, a block after the query, or no valid position
     if (lane == 0) {
       w[kDecD] = -INFINITY;
       w[kDecD + 1] = 0.f;
@@ -45,7 +49,6 @@ __global__ __launch_bounds__(64) void decode_part_kernel(scope_decode_params p, 
   qs[2 * lane] = bf16_to_f32(qh[2 * lane]) * p.scale * kDecLog2e;
   qs[2 * lane + 1] = bf16_to_f32(qh[2 * lane + 1]) * p.scale * kDecLog2e;
   __syncthreads();
-  const int64_t t = p.t;
   const int doc_t = docs[t];
   // scores (log2 units), one key per lane per step
   float m = -INFINITY;
@@ -128,28 +131,43 @@ extern "C" int64_t scope_decode_workspace_bytes(const scope_decode_params* p) {
   return static_cast<int64_t>(p->H) * p->maxkv * (kDecD + 2) * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int scope_decode_attn(const scope_decode_params* p, const uint16_t* q, const uint16_t* k_cache,
-                                 const uint16_t* v_cache, const int32_t* kv_num, const int32_t* kv_idx,
-                                 const int32_t* docs, void* workspace, uint16_t* out, float* lse, void* stream) {
-  SCOPE_REQUIRE(p && q && k_cache && v_cache && kv_num && kv_idx && docs && workspace && out,
-                "scope_decode_attn: null pointer");
-  SCOPE_REQUIRE(p->D == kDecD, "scope_decode_attn: head dim D=%d (supported: 128)", p->D);
-  SCOPE_REQUIRE(p->bs == 64 || p->bs == 128 || p->bs == 256, "scope_decode_attn: block size %d (64, 128, 256)", p->bs);
-  SCOPE_REQUIRE(p->H >= 1 && p->maxkv >= 1 && p->maxkv <= 65535, "scope_decode_attn: bad H=%d / maxkv=%d", p->H,
-                p->maxkv);
-  SCOPE_REQUIRE(p->t >= 0 && p->t < p->T_cap, "scope_decode_attn: position t=%lld outside the cache (%lld tokens)",
+static int decode_launch(const scope_decode_params* p, const int64_t* t_dev, const uint16_t* q,
+                         const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* kv_num,
+                         const int32_t* kv_idx, const int32_t* docs, void* workspace, uint16_t* out, float* lse,
+                         void* stream, const char* fn) {
+  SCOPE_REQUIRE(p && q && k_cache && v_cache && kv_num && kv_idx && docs && workspace && out, "%s: null pointer", fn);
+  SCOPE_REQUIRE(p->D == kDecD, "%s: head dim D=%d (supported: 128)", fn, p->D);
+  SCOPE_REQUIRE(p->bs == 64 || p->bs == 128 || p->bs == 256, "%s: block size %d (64, 128, 256)", fn, p->bs);
+  SCOPE_REQUIRE(p->H >= 1 && p->maxkv >= 1 && p->maxkv <= 65535, "%s: bad H=%d / maxkv=%d", fn, p->H, p->maxkv);
+  SCOPE_REQUIRE(t_dev || (p->t >= 0 && p->t < p->T_cap), "%s: position t=%lld outside the cache (%lld tokens)", fn,
                 (long long)p->t, (long long)p->T_cap);
-  SCOPE_REQUIRE(p->T_cap % p->bs == 0, "scope_decode_attn: cache length %lld not a multiple of bs=%d",
-                (long long)p->T_cap, p->bs);
+  SCOPE_REQUIRE(p->T_cap % p->bs == 0, "%s: cache length %lld not a multiple of bs=%d", fn, (long long)p->T_cap,
+                p->bs);
   SCOPE_REQUIRE(p->k_st % 8 == 0 && p->k_sh % 8 == 0 && p->v_st % 2 == 0 && p->v_sh % 2 == 0 &&
                     (reinterpret_cast<uintptr_t>(k_cache) & 15) == 0 && (reinterpret_cast<uintptr_t>(v_cache) & 3) == 0,
-                "scope_decode_attn: k rows must be 16-byte aligned and v rows 4-byte aligned");
+                "%s: k rows must be 16-byte aligned and v rows 4-byte aligned", fn);
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(decode_part_kernel, dim3(p->maxkv, p->H), dim3(64), 0, s, *p, q, k_cache, v_cache, kv_num,
-                     kv_idx, docs, static_cast<float*>(workspace));
+                     kv_idx, docs, static_cast<float*>(workspace), t_dev);
   int rc = check_launch("decode_part_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(p->H), dim3(kDecD), 0, s, *p, static_cast<const float*>(workspace),
                      out, lse);
   return check_launch("decode_merge_kernel");
+}
+
+extern "C" int scope_decode_attn(const scope_decode_params* p, const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, const int32_t* kv_num, const int32_t* kv_idx,
+                                 const int32_t* docs, void* workspace, uint16_t* out, float* lse, void* stream) {
+  return decode_launch(p, nullptr, q, k_cache, v_cache, kv_num, kv_idx, docs, workspace, out, lse, stream,
+                       "scope_decode_attn");
+}
+
+extern "C" int scope_decode_attn_at(const scope_decode_params* p, const int64_t* t_dev, const uint16_t* q,
+                                    const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* kv_num,
+                                    const int32_t* kv_idx, const int32_t* docs, void* workspace, uint16_t* out,
+                                    float* lse, void* stream) {
+  SCOPE_REQUIRE(t_dev, "scope_decode_attn_at: null position pointer");
+  return decode_launch(p, t_dev, q, k_cache, v_cache, kv_num, kv_idx, docs, workspace, out, lse, stream,
+                       "scope_decode_attn_at");
 }

@@ -19,6 +19,13 @@ make greedy decoding trivial).
   new token's query, the only one known), and keeps it for the block's other
   positions; the attention of the token runs ``scope_decode_attn`` over the
   list.  When t closes a block, its key mean joins the candidates.
+* The steps inside a block (neither opening nor closing it) run as one
+  captured HIP graph (``torch.cuda.CUDAGraph``), replayed per token: the
+  position lives on the device (``_t_dev``; cache and document writes index
+  with it, ``scope_decode_attn_at`` reads it), the lists sit in fixed
+  per-layer buffers that a reselection refills, so every replay sees the
+  current state.  The eager steps run the same operations, so both paths
+  give the same logits.
 
 The reference has no decode path; this is the row of the scope table that
 puts the hot-path kernels under a token loop.
@@ -77,7 +84,7 @@ class _Rotary:
 
 
 class ScopeDecoder(nn.Module):
-    def __init__(self, cfg: DecoderConfig, *, max_len: int, device="cuda", seed: int = 0):
+    def __init__(self, cfg: DecoderConfig, *, max_len: int, device="cuda", seed: int = 0, use_graph: bool = True):
         super().__init__()
         self.cfg = cfg
         g = torch.Generator(device="cpu").manual_seed(seed)
@@ -109,11 +116,24 @@ class ScopeDecoder(nn.Module):
         self.v_cache = [torch.zeros((H, max_len, D), **z) if "qkv" in lay else None for lay in self.layers]
         self.kbar = [torch.zeros((H, nbc, D), dtype=torch.float32, device=device) if "qkv" in lay else None
                      for lay in self.layers]
-        self.lists = [None] * L  # current q-block's (kv_num [H], kv_idx [H, maxkv]) per layer
+        # current q-block's list per layer, in fixed buffers of the full width
+        # (window + budget + globals) that each reselection refills
+        width = cfg.window + cfg.budget + cfg.n_global
+        self.list_num = [torch.zeros(H, dtype=torch.int32, device=device) if "qkv" in lay else None
+                         for lay in self.layers]
+        self.list_idx = [torch.zeros((H, width), dtype=torch.int32, device=device) if "qkv" in lay else None
+                         for lay in self.layers]
+        self.have_lists = False
         self.docs = torch.zeros(max_len, dtype=torch.int32, device=device)
         self.tokens = torch.zeros(max_len, dtype=torch.int64, device=device)
         self.t = 0
-        self._ws = None
+        self._t_dev = torch.zeros(1, dtype=torch.int64, device=device)  # = t, on the device
+        self._ws = torch.empty(H * width * (D + 2) * 4, dtype=torch.uint8, device=device)
+        self.use_graph = bool(use_graph) and self.device.type == "cuda"
+        self._graph = None
+        self._g_tok = None
+        self._g_out = None
+        self._g_warm = 0
 
     # ---- pieces shared by prefill and step -------------------------------------
     def _ve(self, tok: torch.Tensor):
@@ -189,26 +209,24 @@ class ScopeDecoder(nn.Module):
             if i < n:
                 skips.append(x)
         self.t = T
+        self._t_dev.fill_(T)
+        self.have_lists = False
         return self._logits(x) if all_logits else self._logits(x[-1:])[0]
 
     # ---- one decode step ---------------------------------------------------------
-    @torch.no_grad()
-    def step(self, token: int | torch.Tensor) -> torch.Tensor:
-        """Append one token at position t; returns its logits [vocab_padded]."""
+    def _body(self, tok: torch.Tensor, t: int, opens: bool, closes: bool) -> torch.Tensor:
+        """The step at the position held in ``_t_dev`` (= t), then _t_dev += 1.
+        ``opens`` / ``closes`` (eager steps only) add the block's reselection /
+        its key-mean update; with both false the body is graph-capturable."""
         cfg = self.cfg
         bs = cfg.block_size
-        t = self.t
-        if t >= self.max_len:
-            raise ValueError("step: the cache is full")
-        tok = torch.as_tensor(token, device=self.device).reshape(1).long()
-        self.tokens[t] = tok[0]
-        prev = self.docs[t - 1] if t > 0 else torch.zeros((), dtype=torch.int32, device=self.device)
-        self.docs[t] = prev + (tok[0] == EOT).to(torch.int32)
+        td = self._t_dev
+        self.tokens.index_copy_(0, td, tok)
+        prev = torch.where(td > 0, self.docs.index_select(0, (td - 1).clamp(min=0)), 0)
+        self.docs.index_copy_(0, td, (prev + (tok == EOT)).to(torch.int32))
         qb = t // bs
-        opens = t % bs == 0
         if opens:  # positions of the new block not yet written carry the current document
             self.docs[t + 1:(qb + 1) * bs] = self.docs[t]
-        pos = torch.tensor([t], device=self.device)
         ve = self._ve(tok)
         x = x0 = _norm(F.embedding(tok, self.embed))
         skips = []
@@ -220,27 +238,68 @@ class ScopeDecoder(nn.Module):
             a, b = lay["lambdas"]
             x = a * x + b * x0
             if "qkv" in lay:
-                q, k, v = self._qkv(lay, _norm(x), ve[i], pos)
-                self.k_cache[i][:, t] = k[0]
-                self.v_cache[i][:, t] = v[0]
-                if opens or self.lists[i] is None:
+                q, k, v = self._qkv(lay, _norm(x), ve[i], td)
+                self.k_cache[i].index_copy_(1, td, k.transpose(0, 1))
+                self.v_cache[i].index_copy_(1, td, v.transpose(0, 1))
+                if opens:
                     nb = qb + 1
                     qbar = torch.zeros((H, nb, D), dtype=torch.float32, device=self.device)
                     qbar[:, qb] = q[0].float()
                     kv_num, kv_idx, _ = self._select(qbar, self.kbar[i][:, :nb].contiguous(), nb)
-                    self.lists[i] = (kv_num[:, qb].contiguous(), kv_idx[:, qb].contiguous())
-                if self._ws is None:
-                    self._ws = torch.empty(H * 64 * (D + 2) * 4, dtype=torch.uint8, device=self.device)
-                y, _ = ops.decode_attn(q[0], self.k_cache[i], self.v_cache[i], self.lists[i][0], self.lists[i][1],
-                                       self.docs, t, bs=bs, scale=cfg.attn_scale, workspace=self._ws)
+                    self.list_num[i].copy_(kv_num[:, qb])
+                    self.list_idx[i].zero_()
+                    self.list_idx[i][:, :kv_idx.shape[-1]].copy_(kv_idx[:, qb])
+                y, _ = ops.decode_attn(q[0], self.k_cache[i], self.v_cache[i], self.list_num[i], self.list_idx[i],
+                                       self.docs, td, bs=bs, scale=cfg.attn_scale, workspace=self._ws)
                 x = x + F.linear(y.reshape(1, H * D), lay["proj"])
-                if t % bs == bs - 1:  # the block is complete: its key mean joins the candidates
+                if closes:  # the block is complete: its key mean joins the candidates
                     self.kbar[i][:, qb] = self.k_cache[i][:, qb * bs:(qb + 1) * bs].float().mean(dim=1)
             x = x + self._mlp(lay, x)
             if i < n:
                 skips.append(x)
+        logits = self._logits(x)[0]
+        td.add_(1)
+        return logits
+
+    @torch.no_grad()
+    def step(self, token: int | torch.Tensor) -> torch.Tensor:
+        """Append one token at position t; returns its logits [vocab_padded]."""
+        bs = self.cfg.block_size
+        t = self.t
+        if t >= self.max_len:
+            raise ValueError("step: the cache is full")
+        tok = torch.as_tensor(token, device=self.device).reshape(1).long()
+        opens = t % bs == 0 or not self.have_lists
+        closes = t % bs == bs - 1
+        if self.use_graph and not opens and not closes:
+            out = self._graph_step(tok, t)
+        else:
+            out = self._body(tok, t, opens, closes)
+            self.have_lists = True
         self.t = t + 1
-        return self._logits(x)[0]
+        return out
+
+    def _graph_step(self, tok: torch.Tensor, t: int) -> torch.Tensor:
+        """A step inside a block: one eager run of the body first (library
+        warm-up), then a capture; every later such step replays the graph."""
+        if self._graph is None and self._g_warm == 0:
+            self._g_warm = 1
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                out = self._body(tok, t, False, False)
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            return out
+        if self._graph is None:
+            self._g_tok = tok.clone()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._g_out = self._body(self._g_tok, -1, False, False)
+            self._graph = g  # the capture ran nothing: replay for this token below
+        else:
+            self._g_tok.copy_(tok)
+        self._graph.replay()
+        return self._g_out.clone()
 
     @torch.no_grad()
     def generate(self, n_steps: int, first: int | torch.Tensor) -> torch.Tensor:

@@ -470,11 +470,13 @@ def attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: f
 
 
 def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_num: torch.Tensor,
-                kv_idx: torch.Tensor, docs: torch.Tensor, t: int, *, bs: int, scale: float,
+                kv_idx: torch.Tensor, docs: torch.Tensor, t: int | torch.Tensor, *, bs: int, scale: float,
                 workspace: torch.Tensor | None = None):
     """Attention of the token at position t: q [H, D] bf16 against the cache
     k_cache / v_cache [H, T_cap, D] over the listed blocks kv_idx [H, maxkv]
-    (kv_num [H]) -> (out [H, D] bf16, lse [H] natural log)."""
+    (kv_num [H]) -> (out [H, D] bf16, lse [H] natural log).  ``t`` is an int,
+    or a one-element int64 tensor on the device that the kernel reads (no host
+    sync; what a captured decode step needs)."""
     from ._lib import DecodeParams
 
     dev = _gpu("decode_attn", q, k_cache, v_cache, kv_num, kv_idx, docs)
@@ -486,7 +488,11 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
     H, D = q.shape
     T_cap = k_cache.shape[1]
     kv_idx = _i32(kv_idx)
-    prm = DecodeParams(H=H, D=D, bs=int(bs), maxkv=kv_idx.shape[-1], T_cap=T_cap, t=int(t), scale=float(scale),
+    t_dev = t if isinstance(t, torch.Tensor) else None
+    if t_dev is not None and (t_dev.dtype != torch.int64 or t_dev.numel() != 1 or t_dev.device != q.device):
+        raise RuntimeError("decode_attn: a tensor position must be one int64 element on the device of q")
+    prm = DecodeParams(H=H, D=D, bs=int(bs), maxkv=kv_idx.shape[-1], T_cap=T_cap, t=0 if t_dev is not None else int(t),
+                       scale=float(scale),
                        q_sh=q.stride(0), k_sh=k_cache.stride(0), k_st=k_cache.stride(1), v_sh=v_cache.stride(0),
                        v_st=v_cache.stride(1), o_sh=D)
     need = int(query("scope_decode_workspace_bytes", C.byref(prm)))
@@ -494,8 +500,12 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     out = torch.empty((H, D), dtype=torch.bfloat16, device=dev)
     lse = torch.empty(H, dtype=torch.float32, device=dev)
-    call("scope_decode_attn", C.byref(prm), _p(q), _p(k_cache), _p(v_cache), _p(_i32(kv_num)), _p(kv_idx),
-         _p(_i32(docs.reshape(-1))), _p(workspace), _p(out), _p(lse), _stream(dev))
+    tail = (_p(q), _p(k_cache), _p(v_cache), _p(_i32(kv_num)), _p(kv_idx), _p(_i32(docs.reshape(-1))), _p(workspace),
+            _p(out), _p(lse), _stream(dev))
+    if t_dev is not None:
+        call("scope_decode_attn_at", C.byref(prm), _p(t_dev), *tail)
+    else:
+        call("scope_decode_attn", C.byref(prm), *tail)
     return out, lse
 
 

@@ -47,14 +47,51 @@ def test_decode_attn_vs_oracle(bs, t):
     for name, a, b in (("out", out, ro), ("lse", lse, rl)):
         ok, worst = tol_check(a.float().cpu(), b)
         assert ok, f"{name}: worst tolerance ratio {worst:.3f}"
+    # the position read from device memory (scope_decode_attn_at) gives the same result
+    args = (q.to(DEV), kc.to(DEV), vc.to(DEV), kv_num.to(DEV), kv_idx.to(DEV), docs.to(DEV))
+    out2, lse2 = ops.decode_attn(*args, torch.tensor([t], dtype=torch.int64, device=DEV), bs=bs, scale=0.12)
+    assert torch.equal(out2, out) and torch.equal(lse2, lse)
+    # a device position outside the cache: no mass, zero output (checked in the kernel)
+    out3, lse3 = ops.decode_attn(*args, torch.tensor([T_cap], dtype=torch.int64, device=DEV), bs=bs, scale=0.12)
+    assert torch.all(out3.float() == 0) and torch.all(lse3 == -float("inf"))
 
 
-def _small_model(window: int, max_len: int):
+def _small_model(window: int, max_len: int, use_graph: bool = True):
     from scope_amd.decode import DecoderConfig, ScopeDecoder
 
     cfg = DecoderConfig(vocab_size=50257, num_layers=6, num_heads=2, model_dim=256, head_dim=128, block_size=128,
                         window=window, budget=2, n_global=1, no_attn_layer=2)
-    return ScopeDecoder(cfg, max_len=max_len, device=DEV, seed=3)
+    return ScopeDecoder(cfg, max_len=max_len, device=DEV, seed=3, use_graph=use_graph)
+
+
+def test_graph_steps_equal_eager_steps():
+    """The steps inside a block run as one captured graph, replayed per
+    token; every replay gives the logits of the eager step (same operations),
+    across block opens and closes (positions 384 .. 533, blocks of 128) and
+    with end-of-text tokens before and during the loop; each replay is
+    followed by eager work (the comparison) and a synchronization."""
+    T0, n = 384, 150
+    g = torch.Generator().manual_seed(9)
+    toks = torch.randint(0, 50257, (T0 + n,), generator=g)
+    toks[[100, 450, 520]] = 50256
+    print("graph steps vs eager steps", flush=True)
+    eager = _small_model(window=8, max_len=1024, use_graph=False)
+    graph = _small_model(window=8, max_len=1024, use_graph=True)
+    eager.prefill(toks[:T0])
+    graph.prefill(toks[:T0])
+    worst = 0.0
+    for s_ in range(n):
+        a = eager.step(toks[T0 + s_])
+        b = graph.step(toks[T0 + s_])
+        torch.cuda.synchronize()
+        d = (a - b).abs().max().item()
+        worst = max(worst, d)
+        assert d <= 1e-6, f"position {T0 + s_}: |graph - eager| = {d:.3e}"
+        assert int(a.argmax()) == int(b.argmax())
+    assert graph._graph is not None, "no step ran as a graph"
+    assert torch.equal(eager.k_cache[0], graph.k_cache[0]) and torch.equal(eager.docs, graph.docs)
+    assert int(graph._t_dev.item()) == graph.t == T0 + n
+    print(f"  max |graph - eager| {worst:.3e}", flush=True)
 
 
 def test_token_loop_matches_prefill():
@@ -114,7 +151,7 @@ def test_block_start_reselection_matches_oracle_choice():
     docs = m.docs[:nb * cfg.block_size].cpu().numpy()
     ref = OP.pointer_select_blockscore(logits.astype(np.float32), docs, bs=cfg.block_size, window=cfg.window,
                                        n_global=cfg.n_global, budget=cfg.budget)
-    kv_num, kv_idx = (x.cpu() for x in m.lists[i0])
+    kv_num, kv_idx = m.list_num[i0].cpu(), m.list_idx[i0].cpu()
     for h in range(cfg.num_heads):
         want = ref["packed"][h, qb, :ref["kv_num"][h, qb]]
         assert list(kv_idx[h, :int(kv_num[h])].numpy()) == list(want), h
