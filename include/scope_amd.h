@@ -387,6 +387,22 @@ int scope_decode_attn_at(const scope_decode_params* p, const int64_t* t_dev, con
                          const int32_t* kv_idx, const int32_t* docs, void* workspace, uint16_t* out,
                          float* lse, void* stream);
 
+/* The decoder attention layer's glue for T tokens (replaces, in the token
+ * loop and the prefill, scoped_medium.py:339-345 with norm :266-267 and
+ * Rotary :291-310): from qkv [T, 3H, D] bf16 (the qkv projection), q and k
+ * RMS-normalised (eps: F.rms_norm's default for bf16 inputs is the fp32
+ * epsilon) and rotated by the rotary tables cos_t / sin_t
+ * [rot_rows, D/2] fp32 (row stride rot_st) at positions pos [T] (int64, on
+ * the device), v = va·v + vb·ve (ve [T, H·D] bf16 or NULL).  q -> q_out
+ * [T, H, D]; k, v -> row pos[t] (cache_at_pos) or row t of k_out / v_out
+ * ([H, rows, D] with the given head and row strides).  A position outside
+ * the tables or a row outside [0, rows) writes a zero q and no k/v. */
+int scope_decoder_qkv_glue(int T, int H, int D, int64_t rows, float eps, float va, float vb,
+                           const uint16_t* qkv, const uint16_t* ve, const int64_t* pos, const float* cos_t,
+                           const float* sin_t, int64_t rot_rows, int64_t rot_st, uint16_t* q_out,
+                           uint16_t* k_out, uint16_t* v_out, int64_t k_sh, int64_t k_st, int64_t v_sh,
+                           int64_t v_st, int cache_at_pos, void* stream);
+
 int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
 int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
                    const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,

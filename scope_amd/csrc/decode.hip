@@ -122,6 +122,77 @@ __global__ __launch_bounds__(kDecD) void decode_merge_kernel(scope_decode_params
   if (d == 0 && lse) lse[h] = L > 0.f ? (M + log2f(L)) * kDecLn2 : -INFINITY;
 }
 
+// The attention layer's glue of the decoder for T tokens
+// (scoped_medium.py:339-345 with norm :266-267 and Rotary :291-310): q and k
+// RMS-normalised over D (fp32, eps given: F.rms_norm's default for bf16
+// inputs is the fp32 epsilon of its compute type; rounded to bf16), rotated by the half-truncated rotary tables at
+// their positions (y1 = x1·cos + x2·sin, y2 = x1·(-sin) + x2·cos, each
+// product and sum rounded to fp32 as separate tensor ops round them, the
+// result to bf16), v = a·v + b·ve (each product and the sum rounded to bf16,
+// as bf16 tensor arithmetic does; b·ve dropped without ve).  q goes to
+// q_out [T, H, D]; k and v go to row pos[t] of the caches (cache_at_pos) or
+// to row t.  One 128-thread workgroup per (token, head).
+__global__ __launch_bounds__(kDecD) void qkv_glue_kernel(int H, int64_t rows, float eps, float va, float vb,
+                                                          const uint16_t* __restrict__ qkv,
+                                                          const uint16_t* __restrict__ ve,
+                                                          const int64_t* __restrict__ pos,
+                                                          const float* __restrict__ cos_t,
+                                                          const float* __restrict__ sin_t, int64_t rot_rows,
+                                                          int64_t rot_st, uint16_t* __restrict__ q_out,
+                                                          uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                          int64_t k_sh, int64_t k_st, int64_t v_sh, int64_t v_st,
+                                                          int cache_at_pos) {
+  constexpr int D = kDecD, HD = kDecD / 2;
+  const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const int64_t p = pos[t];
+  const int64_t w = cache_at_pos ? p : t;  // the k/v row written
+  uint16_t* qo = q_out + (static_cast<int64_t>(t) * H + h) * D + d;
+  if (p < 0 || p >= rot_rows || w < 0 || w >= rows) {  // uniform over the workgroup: no rotary row / no cache row
+    *qo = 0;
+    return;
+  }
+  const uint16_t* row = qkv + static_cast<int64_t>(t) * 3 * H * D;
+  const float q = bf16_to_f32(row[h * D + d]);
+  const float k = bf16_to_f32(row[(H + h) * D + d]);
+  const float v = bf16_to_f32(row[(2 * H + h) * D + d]);
+  __shared__ float part[2][2];
+  __shared__ float xs[2][D];
+  float sq = q * q, sk = k * k;
+  for (int o = 32; o > 0; o >>= 1) {
+    sq += __shfl_xor(sq, o, kWave);
+    sk += __shfl_xor(sk, o, kWave);
+  }
+  if ((d & 63) == 0) {
+    part[d >> 6][0] = sq;
+    part[d >> 6][1] = sk;
+  }
+  __syncthreads();
+  const float rq = 1.f / sqrtf((part[0][0] + part[1][0]) / D + eps);
+  const float rk = 1.f / sqrtf((part[0][1] + part[1][1]) / D + eps);
+  const float qn = bf16_to_f32(f32_to_bf16(__fmul_rn(q, rq)));
+  const float kn = bf16_to_f32(f32_to_bf16(__fmul_rn(k, rk)));
+  xs[0][d] = qn;
+  xs[1][d] = kn;
+  __syncthreads();
+  const float c = cos_t[p * rot_st + (d % HD)], sn = sin_t[p * rot_st + (d % HD)];
+  float yq, yk;
+  if (d < HD) {
+    yq = __fadd_rn(__fmul_rn(qn, c), __fmul_rn(xs[0][d + HD], sn));
+    yk = __fadd_rn(__fmul_rn(kn, c), __fmul_rn(xs[1][d + HD], sn));
+  } else {
+    yq = __fadd_rn(__fmul_rn(xs[0][d - HD], -sn), __fmul_rn(qn, c));
+    yk = __fadd_rn(__fmul_rn(xs[1][d - HD], -sn), __fmul_rn(kn, c));
+  }
+  *qo = f32_to_bf16(yq);
+  kc[h * k_sh + w * k_st + d] = f32_to_bf16(yk);
+  float vv = bf16_to_f32(f32_to_bf16(__fmul_rn(va, v)));
+  if (ve) {
+    const float e = bf16_to_f32(ve[static_cast<int64_t>(t) * H * D + h * D + d]);
+    vv = bf16_to_f32(f32_to_bf16(__fadd_rn(vv, bf16_to_f32(f32_to_bf16(__fmul_rn(vb, e))))));
+  }
+  vc[h * v_sh + w * v_st + d] = f32_to_bf16(vv);
+}
+
 }  // namespace scope
 
 using namespace scope;
@@ -170,4 +241,18 @@ extern "C" int scope_decode_attn_at(const scope_decode_params* p, const int64_t*
   SCOPE_REQUIRE(t_dev, "scope_decode_attn_at: null position pointer");
   return decode_launch(p, t_dev, q, k_cache, v_cache, kv_num, kv_idx, docs, workspace, out, lse, stream,
                        "scope_decode_attn_at");
+}
+
+extern "C" int scope_decoder_qkv_glue(int T, int H, int D, int64_t rows, float eps, float va, float vb,
+                                      const uint16_t* qkv, const uint16_t* ve, const int64_t* pos, const float* cos_t,
+                                      const float* sin_t, int64_t rot_rows, int64_t rot_st, uint16_t* q_out,
+                                      uint16_t* k_out, uint16_t* v_out, int64_t k_sh, int64_t k_st, int64_t v_sh,
+                                      int64_t v_st, int cache_at_pos, void* stream) {
+  SCOPE_REQUIRE(qkv && pos && cos_t && sin_t && q_out && k_out && v_out, "scope_decoder_qkv_glue: null pointer");
+  SCOPE_REQUIRE(D == kDecD, "scope_decoder_qkv_glue: head dim D=%d (supported: 128)", D);
+  SCOPE_REQUIRE(T >= 1 && T <= 2147483647 && H >= 1 && H <= 65535 && rows >= 1 && rot_rows >= 1 && rot_st >= D / 2,
+                "scope_decoder_qkv_glue: bad T=%d / H=%d / rows=%lld / rotary table", T, H, (long long)rows);
+  hipLaunchKernelGGL(qkv_glue_kernel, dim3(T, H), dim3(kDecD), 0, as_stream(stream), H, rows, eps, va, vb, qkv, ve,
+                     pos, cos_t, sin_t, rot_rows, rot_st, q_out, k_out, v_out, k_sh, k_st, v_sh, v_st, cache_at_pos);
+  return check_launch("qkv_glue_kernel");
 }

@@ -67,6 +67,16 @@ def _norm(x: torch.Tensor) -> torch.Tensor:
     return F.rms_norm(x, (x.size(-1),))
 
 
+def _mix(a: float, b: float, x: torch.Tensor, x0: torch.Tensor) -> torch.Tensor:
+    """a·x + b·x0 (scoped_medium.py:505); a = 1, b = 0 is x itself, exactly."""
+    return x if (a == 1.0 and b == 0.0) else a * x + b * x0
+
+
+def _skip(x: torch.Tensor, w: float, s: torch.Tensor) -> torch.Tensor:
+    """x + w·s (scoped_medium.py:607); w = 1 is a plain sum, exactly."""
+    return x + s if w == 1.0 else x + w * s
+
+
 class _Rotary:
     """Half-truncated RoPE tables (scoped_medium.py:282-299)."""
 
@@ -141,17 +151,18 @@ class ScopeDecoder(nn.Module):
         L = self.cfg.num_layers
         return [ve[0], ve[1], ve[2]] + [None] * (L - 6) + [ve[0], ve[1], ve[2]]
 
-    def _qkv(self, lay, x: torch.Tensor, ve, pos: torch.Tensor):
-        """x [T, d] (normed) -> q, k, v [T, H, D] (q, k normed and rotated, v mixed)."""
+    def _qkv(self, lay, x: torch.Tensor, ve, pos: torch.Tensor, i: int | None = None):
+        """x [T, d] (normed) -> q [T, H, D] (normed and rotated) and k, v: with
+        a layer index i, k and v go to rows pos of that layer's caches (which
+        are returned); otherwise they are new [T, H, D] tensors.  The glue runs
+        as one kernel (``ops.decoder_qkv_glue``)."""
         cfg = self.cfg
-        T = x.shape[0]
-        qkv = F.linear(x, lay["qkv"]).view(T, 3 * cfg.num_heads, cfg.head_dim)
-        q, k, v = qkv.chunk(3, dim=-2)
-        q, k = _norm(q), _norm(k)
-        q, k = self.rotary(q, pos), self.rotary(k, pos)
+        qkv = F.linear(x, lay["qkv"])
         a, b = lay["vlam"]
-        v = a * v + b * ve.view_as(v) if ve is not None else a * v
-        return q, k, v
+        kc = self.k_cache[i] if i is not None else None
+        vc = self.v_cache[i] if i is not None else None
+        return ops.decoder_qkv_glue(qkv, ve, pos, self.rotary.cos, self.rotary.sin, heads=cfg.num_heads, va=a,
+                                    vb=b if ve is not None else 0.0, k_out=kc, v_out=vc)
 
     def _mlp(self, lay, x: torch.Tensor) -> torch.Tensor:
         h = F.linear(_norm(x), lay["mlp_fc"])
@@ -191,14 +202,12 @@ class ScopeDecoder(nn.Module):
         n = len(self.skip_weights)
         for i, lay in enumerate(self.layers):
             if i >= n:
-                x = x + self.skip_weights[i - n] * skips.pop()
+                x = _skip(x, self.skip_weights[i - n], skips.pop())
             a, b = lay["lambdas"]
-            x = a * x + b * x0
+            x = _mix(a, b, x, x0)
             if "qkv" in lay:
-                q, k, v = self._qkv(lay, _norm(x), ve[i], pos)
-                qh, kh, vh = (z.transpose(0, 1) for z in (q, k, v))  # [H, T, D] views
-                self.k_cache[i][:, :T] = kh
-                self.v_cache[i][:, :T] = vh
+                q, kc, vc = self._qkv(lay, _norm(x), ve[i], pos, i)  # k, v into cache rows 0 .. T-1
+                qh, kh, vh = q.transpose(0, 1), kc[:, :T], vc[:, :T]  # [H, T, D] views
                 qbar, kbar = ops.block_means(qh, kh, bs)
                 self.kbar[i][:, :T // bs] = kbar
                 kv_num, kv_idx, _ = self._select(qbar, kbar, T // bs)
@@ -234,13 +243,11 @@ class ScopeDecoder(nn.Module):
         H, D = cfg.num_heads, cfg.head_dim
         for i, lay in enumerate(self.layers):
             if i >= n:
-                x = x + self.skip_weights[i - n] * skips.pop()
+                x = _skip(x, self.skip_weights[i - n], skips.pop())
             a, b = lay["lambdas"]
-            x = a * x + b * x0
+            x = _mix(a, b, x, x0)
             if "qkv" in lay:
-                q, k, v = self._qkv(lay, _norm(x), ve[i], td)
-                self.k_cache[i].index_copy_(1, td, k.transpose(0, 1))
-                self.v_cache[i].index_copy_(1, td, v.transpose(0, 1))
+                q, _, _ = self._qkv(lay, _norm(x), ve[i], td, i)  # k, v into cache row t
                 if opens:
                     nb = qb + 1
                     qbar = torch.zeros((H, nb, D), dtype=torch.float32, device=self.device)

@@ -509,6 +509,47 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
     return out, lse
 
 
+def decoder_qkv_glue(qkv: torch.Tensor, ve: torch.Tensor | None, pos: torch.Tensor, cos: torch.Tensor,
+                     sin: torch.Tensor, *, heads: int, va: float, vb: float, k_out: torch.Tensor | None = None,
+                     v_out: torch.Tensor | None = None, eps: float | None = None):
+    """The decoder attention layer's glue (scoped_medium.py:339-345): qkv
+    [T, 3·heads·D] bf16 -> q [T, heads, D] (RMS-normed, rotated at pos [T]);
+    k and v (normed + rotated / va·v + vb·ve) go to rows pos of the caches
+    k_out / v_out [heads, rows, D], or, without caches, are returned as
+    [T, heads, D] tensors.  Returns (q, k, v) with k, v the caches or the
+    new tensors."""
+    dev = _gpu("decoder_qkv_glue", qkv, ve, pos, cos, sin, k_out, v_out)
+    T = qkv.shape[0]
+    D = qkv.shape[-1] // (3 * heads)
+    if qkv.dtype != torch.bfloat16 or not qkv.is_contiguous() or qkv.shape[-1] != 3 * heads * D:
+        raise RuntimeError("decoder_qkv_glue: qkv must be a contiguous bfloat16 [T, 3*heads*D]")
+    if ve is not None and (ve.dtype != torch.bfloat16 or not ve.is_contiguous() or ve.numel() != T * heads * D):
+        raise RuntimeError("decoder_qkv_glue: ve must be a contiguous bfloat16 [T, heads*D]")
+    if pos.dtype != torch.int64 or pos.numel() != T or not pos.is_contiguous():
+        raise RuntimeError("decoder_qkv_glue: pos must be a contiguous int64 [T]")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape or cos.stride(-1) != 1 \
+            or sin.stride() != cos.stride() or cos.shape[-1] != D // 2:
+        raise RuntimeError("decoder_qkv_glue: cos/sin must be float32 [rows, D/2] with the same strides")
+    q = torch.empty((T, heads, D), dtype=torch.bfloat16, device=dev)
+    at_pos = k_out is not None
+    if at_pos:
+        if v_out is None or k_out.shape != v_out.shape or k_out.dtype != torch.bfloat16 or v_out.dtype != torch.bfloat16 \
+                or k_out.stride(-1) != 1 or v_out.stride(-1) != 1 or k_out.shape[0] != heads or k_out.shape[-1] != D:
+            raise RuntimeError("decoder_qkv_glue: caches must be bfloat16 [heads, rows, D] with a unit last stride")
+        kt, vt, rows = k_out, v_out, k_out.shape[1]
+        strides = (kt.stride(0), kt.stride(1), vt.stride(0), vt.stride(1))
+    else:
+        kt = torch.empty((T, heads, D), dtype=torch.bfloat16, device=dev)
+        vt = torch.empty((T, heads, D), dtype=torch.bfloat16, device=dev)
+        rows = T
+        strides = (D, heads * D, D, heads * D)  # head stride, row stride of a [T, heads, D] tensor
+    # F.rms_norm's default eps for bf16 inputs is the epsilon of its fp32 compute type
+    e = torch.finfo(torch.float32).eps if eps is None else float(eps)
+    call("scope_decoder_qkv_glue", T, heads, D, rows, e, float(va), float(vb), _p(qkv), _p(ve), _p(pos), _p(cos),
+         _p(sin), cos.shape[0], cos.stride(0), _p(q), _p(kt), _p(vt), *strides, 1 if at_pos else 0, _stream(dev))
+    return q, kt, vt
+
+
 def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",

@@ -56,6 +56,49 @@ def test_decode_attn_vs_oracle(bs, t):
     assert torch.all(out3.float() == 0) and torch.all(lse3 == -float("inf"))
 
 
+def test_qkv_glue_matches_torch_ops():
+    """The fused glue against the torch ops it replaces (scoped_medium.py:
+    339-345: rms_norm of q and k, the half-truncated Rotary, v = a·v + b·ve):
+    v bit-exact, q and k equal up to the norm's sum order (under 1% of the
+    elements, by at most 2^-6 on rows of RMS 1); with caches, k and v land in rows pos and nowhere else; a
+    position outside the tables writes a zero q and no cache row."""
+    from scope_amd import ops
+    from scope_amd.decode import _Rotary, _norm
+
+    H, D, T, rows = 4, 128, 300, 512
+    print(f"qkv glue T={T} H={H}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    qkv = (torch.randn((T, 3 * H * D), generator=g) * 2).to(torch.bfloat16).to(DEV)
+    ve = torch.randn((T, H * D), generator=g).to(torch.bfloat16).to(DEV)
+    pos = torch.randperm(rows, generator=g)[:T].to(DEV)
+    rot = _Rotary(D, rows, DEV)
+    q, k, v = qkv.view(T, 3 * H, D).chunk(3, dim=-2)
+    q, k = rot(_norm(q), pos), rot(_norm(k), pos)
+    v = 0.5 * v + 0.5 * ve.view_as(v)
+    q2, k2, v2 = ops.decoder_qkv_glue(qkv, ve, pos, rot.cos, rot.sin, heads=H, va=0.5, vb=0.5)
+    assert torch.equal(v2, v)
+    for name, a, b in (("q", q2, q), ("k", k2, k)):
+        # rows have RMS 1 after the norm: a one-step difference of a normed
+        # value moves a rotated one by at most ~2^-7 (more than one step of a
+        # small rotated value when its two terms cancel)
+        d = (a.float() - b.float()).abs()
+        assert d.max().item() <= 2.0 ** -6, f"{name}: max difference {d.max().item():.3e}"
+        assert (d > 0).float().mean().item() < 0.01, f"{name}: too many differing elements"
+    kc = torch.zeros((H, rows, D), dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    q3, _, _ = ops.decoder_qkv_glue(qkv, ve, pos, rot.cos, rot.sin, heads=H, va=0.5, vb=0.5, k_out=kc, v_out=vc)
+    assert torch.equal(q3, q2)
+    assert torch.equal(kc[:, pos], k2.transpose(0, 1)) and torch.equal(vc[:, pos], v2.transpose(0, 1))
+    untouched = torch.ones(rows, dtype=torch.bool, device=DEV)
+    untouched[pos] = False
+    assert torch.all(kc[:, untouched] == 0) and torch.all(vc[:, untouched] == 0)
+    bad = torch.full((T,), rows, dtype=torch.int64, device=DEV)
+    kc2 = torch.zeros_like(kc)
+    vc2 = torch.zeros_like(kc)
+    q4, _, _ = ops.decoder_qkv_glue(qkv, ve, bad, rot.cos, rot.sin, heads=H, va=0.5, vb=0.5, k_out=kc2, v_out=vc2)
+    assert torch.all(q4.float() == 0) and torch.all(kc2 == 0) and torch.all(vc2 == 0)
+
+
 def _small_model(window: int, max_len: int, use_graph: bool = True):
     from scope_amd.decode import DecoderConfig, ScopeDecoder
 
