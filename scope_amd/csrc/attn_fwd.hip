@@ -114,7 +114,9 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 
 
   __shared__ KvTile<MODE> buf0, buf1;
   __shared__ typename std::conditional<STAGGER, KvTile<MODE>, int>::type buf2;
-  __shared__ int kbs[kListLds];
+  // key-block indices of the list (< 65536, checked on the host): 16 bits keep the
+  // bs=128 workgroup under half of the CU's LDS, two workgroups per CU
+  __shared__ uint16_t kbs[kListLds];
   __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
   // mass: per list entry and wavefront, the wavefront's share (each slot has one writer)
   __shared__ float mslot[MASS ? kListLds * NW : 1];
@@ -499,6 +501,8 @@ extern "C" int scope_attn_fwd(const scope_attn_params* p, const uint16_t* q, con
                          delta_main, width, "scope_attn_fwd");
   if (rc) return rc;
   SCOPE_REQUIRE(out && lse, "scope_attn_fwd: null output");
+  SCOPE_REQUIRE(p->T / p->bs <= 65536, "scope_attn_fwd: %lld key blocks (at most 65536)",
+                (long long)(p->T / p->bs));
   AttnArgs a = make_args(p);
   a.q = q;
   a.k = k;
@@ -535,6 +539,8 @@ extern "C" int scope_attn_block_mass(const scope_attn_params* p, const uint16_t*
                          delta_main, width, "scope_attn_block_mass");
   if (rc) return rc;
   SCOPE_REQUIRE(lse && mass, "scope_attn_block_mass: null output");
+  SCOPE_REQUIRE(p->T / p->bs <= 65536, "scope_attn_block_mass: %lld key blocks (at most 65536)",
+                (long long)(p->T / p->bs));
   SCOPE_REQUIRE(p->maxkv <= kListLds, "scope_attn_block_mass: MAXKV=%d above %d listed blocks per q-block",
                 p->maxkv, kListLds);
   AttnArgs a = make_args(p);
