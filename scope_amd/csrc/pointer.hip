@@ -409,7 +409,8 @@ __device__ __forceinline__ bool better(float za, int ka, float zb, int kb) {
 // candidates).
 constexpr int kScoreQ = 8;
 
-template <int D>
+// KB: slots of the per-lane top list (the budget rounded up to 2, 4, 8 or 16)
+template <int D, int KB>
 __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, const float* __restrict__ qbar,
                                                                  const float* __restrict__ kbar,
                                                                  const float* __restrict__ logits_in,
@@ -451,10 +452,10 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
   }
 
   // per-lane top-B list, sorted best first
-  float tz[kMaxBudget];
-  int tk[kMaxBudget];
+  float tz[KB];
+  int tk[KB];
 #pragma unroll
-  for (int i = 0; i < kMaxBudget; ++i) {
+  for (int i = 0; i < KB; ++i) {
     tz[i] = -INFINITY;
     tk[i] = INT_MAX;
   }
@@ -527,7 +528,7 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
       float cz = z;
       int ck = kb;
 #pragma unroll
-      for (int i = 0; i < kMaxBudget; ++i) {
+      for (int i = 0; i < KB; ++i) {
         if (i < B && better(cz, ck, tz[i], tk[i])) {
           float z2 = tz[i];
           int k2 = tk[i];
@@ -566,12 +567,12 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
     const bool valid = bk != INT_MAX;
     if (valid && tk[0] == bk) {
 #pragma unroll
-      for (int j = 0; j < kMaxBudget - 1; ++j) {
+      for (int j = 0; j < KB - 1; ++j) {
         tz[j] = tz[j + 1];
         tk[j] = tk[j + 1];
       }
-      tz[kMaxBudget - 1] = -INFINITY;
-      tk[kMaxBudget - 1] = INT_MAX;
+      tz[KB - 1] = -INFINITY;
+      tk[KB - 1] = INT_MAX;
     }
     if (active && lane == 0) picks[rowq * B + i] = valid ? bk : -1;
     if (lane == 0) list[W + i] = valid ? bk : qbc;
@@ -864,12 +865,23 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
   A.N = next_pow2(A.L);
   SCOPE_REQUIRE(A.N <= 64, "scope_pointer_select: list length %d exceeds 64", A.L);
   dim3 grid(ceil_div(p->NB, kScoreQ), p->H);
-  if (p->D == 128)
-    hipLaunchKernelGGL(ptr_score_kernel<128>, grid, dim3(kScoreQ * 64), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
-                       gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, picks, logits_out);
-  else
-    hipLaunchKernelGGL(ptr_score_kernel<64>, grid, dim3(kScoreQ * 64), 0, as_stream(stream), A, qbar, kbar, logits_in, prior,
-                       gumbel_u, ds_ptr, ds_local, kv_num, kv_idx, picks, logits_out);
+  hipStream_t st = as_stream(stream);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(kScoreQ * 64), 0, st, A, qbar, kbar, logits_in, prior, gumbel_u, ds_ptr,
+                       ds_local, kv_num, kv_idx, picks, logits_out);
+  };
+  const int kb = p->budget <= 2 ? 2 : p->budget <= 4 ? 4 : p->budget <= 8 ? 8 : 16;
+  if (p->D == 128) {
+    if (kb == 2) go(ptr_score_kernel<128, 2>);
+    else if (kb == 4) go(ptr_score_kernel<128, 4>);
+    else if (kb == 8) go(ptr_score_kernel<128, 8>);
+    else go(ptr_score_kernel<128, 16>);
+  } else {
+    if (kb == 2) go(ptr_score_kernel<64, 2>);
+    else if (kb == 4) go(ptr_score_kernel<64, 4>);
+    else if (kb == 8) go(ptr_score_kernel<64, 8>);
+    else go(ptr_score_kernel<64, 16>);
+  }
   return check_launch("ptr_score_kernel");
 }
 
