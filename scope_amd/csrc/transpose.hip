@@ -76,8 +76,11 @@ __global__ void tr_fill_kernel(const int32_t* __restrict__ kv_num, const int32_t
   }
 }
 
-// One wavefront (one workgroup) per bucket; bitonic sort in LDS.
-__global__ __launch_bounds__(64) void tr_sort_kernel(int NB, int QB, int maxkv, const int32_t* __restrict__ q_off,
+// One workgroup of 256 threads per bucket: a list of up to 64 entries is sorted
+// in registers by the first wavefront (bitonic over the lanes); a longer one
+// (a global block listed by every q-block of a long document) by the whole
+// workgroup, bitonic in LDS.
+__global__ __launch_bounds__(256) void tr_sort_kernel(int NB, int QB, int maxkv, const int32_t* __restrict__ q_off,
                                                      int32_t* __restrict__ q_list, int cap) {
   extern __shared__ int s[];
   const int h = blockIdx.y;
@@ -87,7 +90,9 @@ __global__ __launch_bounds__(64) void tr_sort_kernel(int NB, int QB, int maxkv, 
   if (n <= 1) return;
   int32_t* b = q_list + static_cast<int64_t>(h) * QB * maxkv + o0;
   const int lane = threadIdx.x;
+  const int nt = blockDim.x;
   if (n <= kWave) {
+    if (lane >= kWave) return;
     // register bitonic over 64 lanes
     int v = lane < n ? b[lane] : INT_MAX;
 #pragma unroll
@@ -106,11 +111,11 @@ __global__ __launch_bounds__(64) void tr_sort_kernel(int NB, int QB, int maxkv, 
   }
   const int N = next_pow2(n);
   if (N > cap) return;  // guarded on the host: cap >= next_pow2(QB)
-  for (int i = lane; i < N; i += kWave) s[i] = i < n ? b[i] : INT_MAX;
+  for (int i = lane; i < N; i += nt) s[i] = i < n ? b[i] : INT_MAX;
   __syncthreads();
   for (int k = 2; k <= N; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = lane; i < (N >> 1); i += kWave) {
+      for (int i = lane; i < (N >> 1); i += nt) {
         int lo = 2 * j * (i / j) + (i % j);
         int hi = lo + j;
         bool up = (lo & k) == 0;
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(64) void tr_sort_kernel(int NB, int QB, int maxkv, 
       __syncthreads();
     }
   }
-  for (int i = lane; i < n; i += kWave) b[i] = s[i];
+  for (int i = lane; i < n; i += nt) b[i] = s[i];
 }
 
 }  // namespace scope
@@ -152,7 +157,7 @@ int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, 
   hipLaunchKernelGGL(tr_scan_kernel, dim3(H), dim3(1024), 0, s, NB, q_off);
   hipLaunchKernelGGL(tr_fill_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off, cursor, q_list);
-  hipLaunchKernelGGL(tr_sort_kernel, dim3(NB, H), dim3(64), cap * sizeof(int), s, NB, QB, maxkv, q_off, q_list, cap);
+  hipLaunchKernelGGL(tr_sort_kernel, dim3(NB, H), dim3(256), cap * sizeof(int), s, NB, QB, maxkv, q_off, q_list, cap);
   return check_launch("transpose kernels");
 }
 
