@@ -85,8 +85,9 @@ CASES = [
     (2, 2048, 256, "block", 3, 2, 2, 3),
     (1, 1024, 128, "token", 2, 2, 1, 2),
     (1, 2048, 256, "token", 2, 2, 1, 2),
-    (2, 4096, 128, "block", 1, 2, 1, 3),   # q-list of the global block (32 q-blocks) -> chunked dK/dV
-    (1, 8192, 256, "none", 2, 2, 2, 4),    # chunked dK/dV at bs=256
+    (2, 4096, 128, "block", 1, 2, 1, 3),   # the global block's q-list holds exactly 32 q-blocks: one full item
+    (1, 8192, 256, "none", 2, 2, 2, 4),    # document-start blocks with q-lists of up to 32 at bs=256
+    # (q-lists longer than 32, summed over several items and reduced: test_gpu_bwd_hot_blocks.py)
 ]
 
 

@@ -69,7 +69,8 @@ CASES = [
     (2, 2048, 128, "none", 2, 2, 1, 3),    # 16-key kernel, bs=128
     (2, 2048, 256, "block", 3, 2, 2, 3),   # 16-key kernel, bs=256, block bias
     (1, 2048, 128, "token", 2, 2, 1, 2),   # 32-key kernel (token mode)
-    (2, 4096, 128, "block", 1, 2, 1, 3),   # chunked dK/dV (global block listed by 32 q-blocks)
+    (2, 4096, 128, "block", 1, 2, 1, 3),   # global block listed by 32 q-blocks: one full dK/dV item
+    # (pair bias on q-lists longer than 32: test_gpu_bwd_hot_blocks.py)
 ]
 
 
