@@ -112,17 +112,22 @@ def make_inputs(H, T, D, bs, seed=0, n_docs=None, needle=True):
     flag[cuts] = 1
     docs = flag.cumsum(0).to(torch.int32)
     NB = T // bs
-    # planted needle: key block kb = 3 × mean query of block qb, 64 blocks back
-    # (pointer candidates are document-local, so both sit in the longest
-    # document: qb its last whole block, kb clear of its global blocks; when
-    # the document is shorter than 64 + 4 blocks, as far back as it allows)
+    # planted needle: key block kb = 3 × mean query of block qb, at a seeded
+    # distance of at least 64 blocks (pointer candidates are document-local,
+    # so both sit in the longest document: qb its last whole block, kb clear
+    # of its global blocks; when the document is shorter than 64 + 4 blocks,
+    # as far back as it allows)
     bd = docs[::bs]  # document of each block's first token
     starts = [0] + [b for b in range(1, NB) if bd[b] != bd[b - 1]] + [NB]
     # whole blocks of document i: from its first block whose first token is in it
     spans = [(starts[i], starts[i + 1] - 1) for i in range(len(starts) - 1)]
     fb, lb = max(spans, key=lambda sp: sp[1] - sp[0])
     qb_n = lb - 1  # block lb may hold the next document's first tokens
-    dist = max(4, min(64, qb_n - (fb + 3)))
+    room = qb_n - (fb + 3)  # farthest distance that stays clear of the document's global blocks
+    if room >= 64:  # seeded distance of at least 64 blocks
+        dist = 64 + int(torch.randint(0, room - 64 + 1, (1,), generator=g))
+    else:
+        dist = max(4, room)
     kb_n = qb_n - dist
     if needle:
         mq = q[0, :, qb_n * bs:(qb_n + 1) * bs].float().mean(dim=1)
@@ -135,10 +140,23 @@ def make_inputs(H, T, D, bs, seed=0, n_docs=None, needle=True):
                 needle=(qb_n, kb_n) if needle else None)
 
 
+PRIOR_SCALE = 0.5
+
+
+def radius_prior(NB: int, scale: float):
+    """Radius prior of the block-scoring logits over the block distance
+    r = qb - kb: prior[r] = -scale·ln(1 + r), a power-law preference for
+    nearer blocks (the reference spreads its pointer offsets Δ* over a
+    log-spaced range, model/attn_bias.py:220-226)."""
+    import torch
+
+    return -scale * torch.log1p(torch.arange(NB, dtype=torch.float32))
+
+
 class Step:
     """The hot path on GPU-resident inputs; phase events on the current stream."""
 
-    def __init__(self, inp, *, bs, window, n_global, budget, seed=1234, soft_temp=0.0):
+    def __init__(self, inp, *, bs, window, n_global, budget, seed=1234, soft_temp=0.0, prior_scale=PRIOR_SCALE):
         import torch
 
         from scope_amd import ops
@@ -148,6 +166,7 @@ class Step:
         self.bs, self.window, self.n_global, self.budget, self.seed = bs, window, n_global, budget, seed
         self.H, self.T = self.t["q"].shape[1], self.t["q"].shape[2]
         self.NB = self.T // bs
+        self.prior = radius_prior(self.NB, prior_scale).cuda() if prior_scale > 0 else None
         self.table = spectral_table(self.t["omegas"], self.T, bs, "block")
         self.ops = ops
         self.soft_temp = float(soft_temp)
@@ -179,13 +198,14 @@ class Step:
         ls = bs / math.sqrt(t["q"].shape[-1])
         kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=self.NB, H=self.H,
                                                    window=self.window, n_global=self.n_global, budget=self.budget,
-                                                   qbar=qbar, kbar=kbar, temp=1.0, logit_scale=ls, noise="counter",
-                                                   seed=self.seed)
+                                                   qbar=qbar, kbar=kbar, prior=self.prior, temp=1.0, logit_scale=ls,
+                                                   noise="counter", seed=self.seed)
         soft = self.soft_temp > 0
         pb = None
         if soft:
             pb = ops.pointer_pair_bias(kv_num, kv_idx, picks, bs=bs, window=self.window, n_global=self.n_global,
-                                       soft_temp=self.soft_temp, qbar=qbar, kbar=kbar, logit_scale=ls)
+                                       soft_temp=self.soft_temp, qbar=qbar, kbar=kbar, prior=self.prior,
+                                       logit_scale=ls)
         mark("pointer", 1)
         mark("stats", 0)
         counts, values = ops.mask_stats(H=self.H, QB=self.NB, bs=bs, kv_num=kv_num, picks=picks, ds_ptr=ds_ptr,
@@ -351,17 +371,7 @@ def main_coeff(args):
         r = ops.coeff_head_fwd(y, prm, sb.omegas, sb.log_omegas, cm, sm)
         ops.coeff_head_bwd(y, prm, sb.omegas, sb.log_omegas, cm, sm, grads, g_reg, r["reg"])
 
-    # the reference's steps: torch ops from y (requires grad) to the outputs, then autograd
-    class _Torch:
-        def __call__(self):
-            yy = y.detach().requires_grad_()
-            sb._mlp_forward = lambda q: yy  # the head only: the MLP is the same in both
-            out = sb._forward_torch(torch.empty((1, H, T, 128), device="cuda", dtype=torch.bfloat16))
-            loss = sum((out[i] * grads[n]).sum() for i, n in enumerate(names)) + out[11]
-            loss.backward()
-
     t_fused = time_region(fused, args.steps, args.warmup)
-    t_torch = time_region(_Torch(), args.steps, args.warmup)
     rows = H * T
     # algorithmic bytes: fwd reads y (bf16) and writes the outputs (fp32); bwd reads y and the
     # upstream gradients of the outputs and writes dy (bf16)
@@ -383,13 +393,59 @@ def main_coeff(args):
         "data": "synthetic",
         "config": {"workload": "SpectralBias coefficient head after the MLP, fwd+bwd with regularisers", "B": 1,
                    "H": H, "T": T, "M": M, "K": K, "y_dtype": "bf16"},
-        "torch_steps_ms": round(t_torch * 1e3, 4),
-        "speedup_vs_torch_steps": round(t_torch / t_fused, 2),
         "roofline": dict(bound="hbm", kernel="coeff_fwd_kernel+coeff_bwd_kernel", achieved=round(ach, 1),
                          peak=PEAK_HBM_GBS, unit="GB/s", frac=round(ach / PEAK_HBM_GBS, 4), traffic=None,
                          bytes_per_step=bytes_),
     }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_coeff(sb, names, args.cpu_seconds)
     print(json.dumps(res))
+
+
+def cpu_baseline_coeff(sb, names, seconds: float):
+    """The reference's coefficient-head steps after the MLP (the oracle's
+    torch ops, model/attn_bias.py:419-506) forward + autograd backward with
+    the regularisers on the host cores, over a bounded sample: batches of
+    4096 rows per head of random MLP outputs, until `seconds` are spent."""
+    import copy
+
+    import torch
+
+    from oracle.coeff_head import coeff_head_forward
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    cpu = copy.deepcopy(sb).cpu().float().train()
+    H, M, L = cpu.num_heads, cpu.M, 4096
+    Y = 5 * M + (1 if cpu.use_slope else 0)
+    g = torch.Generator().manual_seed(0)
+    q = torch.zeros((1, H, L, cpu.head_dim))
+    done, t_used = 0, 0.0
+    while t_used < seconds:
+        y = (torch.randn((1, H, L, Y), generator=g) * 2).requires_grad_()
+        cpu._mlp_forward = lambda _q, y=y: y  # the head alone, like the timed kernels
+        t0 = time.perf_counter()
+        out = coeff_head_forward(cpu, q)
+        loss = sum(out[i].sum() for i in range(len(names))) + out[11]
+        loss.backward()
+        t_used += time.perf_counter() - t0
+        done += H * L
+    return dict(value=round(done / t_used, 1), unit="rows/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"oracle coefficient head after the MLP (torch fp32 on CPU) fwd+bwd with regularisers "
+                       f"over {done} rows ({t_used:.1f} s)", cpu_model=cpu_model())
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 def main_teacher(args):
@@ -581,7 +637,135 @@ def cpu_baseline(inp, step, seconds: float, bs: int):
     return dict(value=flops / t_used / 1e12, unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
                 sample=f"oracle block-sparse attention fwd+bwd (torch fp32 on CPU) for {n_rows} (head, q-block) "
                        f"rows of the same mask ({done_tiles} active {bs}x{bs} tiles, {t_used:.1f} s)",
-                seconds=round(t_used, 2), cpu_count=os.cpu_count())
+                seconds=round(t_used, 2), cpu_count=os.cpu_count(), cpu_model=cpu_model())
+
+
+def c1_lists(inp, bs: int, window: int, n_global: int, budget: int, seed: int):
+    """The config-1 lists from the oracle's block-scoring selection: fp64
+    block means, logits bs/√D·q̄·k̄ + radius prior, counter Gumbel noise (τ=1)."""
+    import numpy as np
+
+    from oracle import pointer as OP
+
+    q, k, docs = inp["q"][0].float().numpy(), inp["k"][0].float().numpy(), inp["docs"].numpy()
+    H, T, D = q.shape
+    NB = T // bs
+    lg = OP.pointer_logits(OP.block_means(q, bs), OP.block_means(k, bs), logit_scale=bs / math.sqrt(D),
+                           prior=radius_prior(NB, PRIOR_SCALE).double().numpy()).astype(np.float32)
+    hh, qq, kk = np.meshgrid(np.arange(H), np.arange(NB), np.arange(NB), indexing="ij")
+    g = OP.gumbel_from_u(OP.counter_uniform(seed, hh, qq, kk))
+    sel = OP.pointer_select_blockscore(lg, docs, bs=bs, window=window, n_global=n_global, budget=budget, gumbel=g)
+    return sel["kv_num"], sel["packed"]
+
+
+def cpu_reference_path_c1(seconds: float):
+    """The reference's own CPU path (its eager FlexAttention fallback,
+    scoped_medium.py:37-38) at config 1: B=1, H=6, T=4096, D=128, bs=128,
+    window 3, global 1, budget 2, block-offset spectral bias with 8 bands,
+    forward only.  Eager flex_attention on the host cores in fp32, with the
+    block lists restated inside mask_mod (eager FlexAttention evaluates
+    mask_mod on every score and ignores kv_indices) together with
+    document_causal (model/attn_bias.py:674-679), and the band term as
+    score_mod; then dense masked SDPA in fp32 with an explicit bias.  The GPU
+    forward of the same layer and lists is timed beside them."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention.flex_attention import create_block_mask, flex_attention
+
+    from scope_amd import ops
+    from scope_amd.attention import spectral_table
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    H, T, D, bs, W, G, B = 6, 4096, 128, 128, 3, 1, 2
+    NB = T // bs
+    inp = make_inputs(H, T, D, bs, n_docs=1, needle=False)
+    kv_num, kv_idx = c1_lists(inp, bs, W, G, B, seed=1234)
+    n_act = int(kv_num.sum())
+    flops = 4.0 * bs * bs * D * n_act
+    q, k, v = (inp[n][0].float() for n in ("q", "k", "v"))
+    cc, cs = inp["coeff_cos"][0].float(), inp["coeff_sin"][0].float()
+    om = inp["omegas"].float()
+    blk = torch.zeros((H, NB, NB), dtype=torch.bool)
+    for h in range(H):
+        for qb in range(NB):
+            blk[h, qb, torch.from_numpy(kv_idx[h, qb, :kv_num[h, qb]]).long()] = True
+    docs_l = inp["docs"].long()
+    rr = torch.arange(NB, dtype=torch.float32)
+    cosR, sinR = torch.cos(om[:, None] * rr[None]), torch.sin(om[:, None] * rr[None])  # [K, NB]
+
+    def mask_mod(b, h, qi, ki):
+        return blk[h, qi // bs, ki // bs] & (qi >= ki) & (docs_l[qi] == docs_l[ki])
+
+    CC, CS = cc[None], cs[None]
+
+    def score_mod(score, b, h, q_idx, kv_idx_):  # the shape of scoped_medium.py:425-457, block offsets
+        qi = q_idx.to(torch.long).reshape(-1)
+        ki = kv_idx_.to(torch.long).reshape(-1)
+        r = (qi[:, None] // bs - ki[None, :] // bs).clamp(min=0)
+        A, Bc = CC[b, h, qi], CS[b, h, qi]
+        bias = score.new_zeros(r.shape, dtype=torch.float32)
+        for kx in range(cc.shape[-1]):
+            bias = bias + A[:, kx:kx + 1] * cosR[kx, r] + Bc[:, kx:kx + 1] * sinR[kx, r]
+        return score + 0.5 * bias.reshape_as(score).to(score.dtype)
+
+    def flex_step():
+        bm = create_block_mask(mask_mod, None, H, T, T, device="cpu", BLOCK_SIZE=bs)
+        return flex_attention(q[None], k[None], v[None], block_mask=bm, score_mod=score_mod, scale=0.12)
+
+    def sdpa_step():
+        i = torch.arange(T)
+        allowed = blk.repeat_interleave(bs, 1).repeat_interleave(bs, 2) & ((i[:, None] >= i[None, :]) &
+                                                                           (docs_l[:, None] == docs_l[None, :]))
+        r = (i[:, None] // bs - i[None, :] // bs).clamp(min=0)
+        bias = torch.zeros((H, T, T))
+        for kx in range(cc.shape[-1]):
+            bias += cc[:, :, kx, None] * cosR[kx][r][None] + cs[:, :, kx, None] * sinR[kx][r][None]
+        mask = torch.where(allowed, 0.5 * bias, torch.tensor(float("-inf")))
+        return F.scaled_dot_product_attention(q[None], k[None], v[None], attn_mask=mask[None], scale=0.12)
+
+    def timed(fn):
+        ts = []
+        while not ts or (sum(ts) < seconds / 2 and len(ts) < 5):
+            t0 = time.perf_counter()
+            out = fn()
+            ts.append(time.perf_counter() - t0)
+        return min(ts), len(ts), out
+
+    t_flex, n_flex, o_flex = timed(flex_step)
+    t_sdpa, n_sdpa, o_sdpa = timed(sdpa_step)
+    # the GPU forward of the same layer and lists
+    dev = torch.device("cuda")
+    gq, gk, gv = (inp[n].to(dev) for n in ("q", "k", "v"))
+    docs_d = inp["docs"].to(dev)
+    _, _, ds_tok_end = ops.doc_starts(docs_d, bs)
+    kn, ki = torch.from_numpy(kv_num).to(dev), torch.from_numpy(kv_idx).to(dev)
+    tab = spectral_table(inp["omegas"].to(dev), T, bs, "block")
+    gcc, gcs = inp["coeff_cos"].to(dev), inp["coeff_sin"].to(dev)
+
+    def gpu_fwd():
+        ops.attn_fwd(gq, gk, gv, kn, ki, docs_d, ds_tok_end, bs=bs, scale=0.12, beta=0.5, bias_mode="block",
+                     table=tab, coeff_cos=gcc, coeff_sin=gcs)
+
+    t_gpu = time_region(gpu_fwd, 20, 3)
+    o_gpu, _ = ops.attn_fwd(gq, gk, gv, kn, ki, docs_d, ds_tok_end, bs=bs, scale=0.12, beta=0.5, bias_mode="block",
+                            table=tab, coeff_cos=gcc, coeff_sin=gcs)
+    o_gpu = o_gpu.float().cpu()[0]
+    return dict(workload="config 1: B=1, H=6, T=4096, D=128, bs=128, window 3, global 1, budget 2, "
+                         "block-offset bias (8 bands), forward only, fp32 on the host",
+                n_act=n_act, flops_fwd=flops, cores=torch.get_num_threads(), cpu_count=os.cpu_count(),
+                cpu_model=cpu_model(),
+                eager_flex_attention=dict(ms=round(t_flex * 1e3, 1), tflops=round(flops / t_flex / 1e12, 5),
+                                          runs=n_flex, kind="reference",
+                                          source="torch eager flex_attention (the reference's fallback, "
+                                                 "scoped_medium.py:37-38) with restated mask_mod/score_mod"),
+                dense_sdpa=dict(ms=round(t_sdpa * 1e3, 1), tflops=round(flops / t_sdpa / 1e12, 5), runs=n_sdpa,
+                                kind="reference", source="F.scaled_dot_product_attention fp32 with a dense "
+                                                         "bias + mask (built inside the timed call)"),
+                gpu_fwd_ms=round(t_gpu * 1e3, 4), gpu_tflops=round(flops / t_gpu / 1e12, 2),
+                gpu_speedup_vs_eager_flex=round(t_flex / t_gpu, 1),
+                max_abs_diff=dict(flex_vs_sdpa=round(float((o_flex[0] - o_sdpa[0]).abs().max()), 6),
+                                  gpu_vs_flex=round(float((o_gpu - o_flex[0]).abs().max()), 6)))
 
 
 def main():
@@ -714,6 +898,8 @@ def main():
     pointer["block_means_frac_of_measured"] = round(pointer["block_means_achieved"] / mp["hbm_copy_gbs"], 4)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(inp, step, args.cpu_seconds, bs)
+        if not train:
+            res["cpu_baseline"]["reference_path_c1"] = cpu_reference_path_c1(args.cpu_seconds)
     if args.copy_probe_mib > 0:
         src = torch.ones(args.copy_probe_mib << 18, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)

@@ -261,82 +261,26 @@ class SpectralBias(nn.Module):
                     delta_edge_eps=self._st["edge_eps"])
 
     def forward(self, q: Tensor, *, docs: Tensor | None = None) -> tuple[Tensor, ...]:
-        """q [B,H,L,D] -> the reference's 12-tuple (model/attn_bias.py:385-401):
-        the fused kernels for GPU tensors, torch ops for CPU tensors."""
-        if q.is_cuda and self.enabled:
-            return self._forward_fused(q, docs)
-        return self._forward_torch(q, docs=docs)
-
-    def _forward_torch(self, q: Tensor, *, docs: Tensor | None = None) -> tuple[Tensor, ...]:
-        """The reference's steps in torch ops (any device)."""
-        B, H, L, Dh = q.shape
-        if H != self.num_heads:
-            raise ValueError(f"expected H={self.num_heads}, got {H}")
-        if Dh != self.head_dim:
-            raise ValueError(f"expected head_dim={self.head_dim}, got {Dh}")
-        device = q.device
-        cos_wD, sin_wD, cos_mean, sin_mean = self._get_trig_tables(L, device)
+        """q [B,H,L,D] on the GPU -> the reference's 12-tuple
+        (model/attn_bias.py:385-401): the MLP in torch, the rest in the fused
+        coefficient-head kernels.  Disabled, it returns zeros and uniform π
+        like the reference (:411-417).  There is no CPU path."""
+        if not q.is_cuda:
+            raise RuntimeError(f"SpectralBias.forward: q must live on the GPU (got {q.device}); there is no CPU path")
         if not self.enabled:
-            z_k = q.new_zeros((B, H, L, self.K), dtype=torch.float32)
-            z_l = q.new_zeros((B, H, L), dtype=torch.float32)
-            z_m = q.new_zeros((B, H, L, self.M), dtype=torch.float32)
-            z_pi = q.new_full((B, H, L, self.M), 1.0 / self.M, dtype=torch.float32)
-            return z_k, z_k, z_l, z_l, z_m, z_pi, z_m, z_l, z_l, cos_wD, sin_wD, q.new_zeros((), dtype=torch.float32)
-        y = self._mlp_forward(q).float()
-        M, K = self.M, self.K
-        delta_raw, mu_raw, sigma_raw, pi_logits, budget_logits = (y[..., i * M:(i + 1) * M] for i in range(5))
-        delta_cap = torch.clamp(self._delta_star_max_active.to(device=device, dtype=torch.float32), 0.0, float(L - 1))
-        delta_star = torch.sigmoid(delta_raw) * delta_cap
-        logw_min, logw_max = self.logw_min.to(device), self.logw_max.to(device)
-        mu = logw_min + (logw_max - logw_min) * torch.sigmoid(mu_raw)
-        sigma = 0.25 + 1.75 * torch.sigmoid(sigma_raw)
-        pi = torch.softmax(pi_logits, dim=-1)
-        if self.use_slope:
-            slope = self.c_scale * torch.tanh(y[..., 5 * M:5 * M + 1]).squeeze(-1)
-        else:
-            slope = q.new_zeros((B, H, L), dtype=torch.float32)
-        logw = self.log_omegas.to(device).view(1, 1, 1, 1, K)
-        a_mk = torch.exp(-((logw - mu.unsqueeze(-1)) ** 2) / (2 * (sigma.unsqueeze(-1) ** 2)))
-        a_mk = a_mk / (a_mk.sum(dim=-1, keepdim=True) + self.eps)
-        phase = self.omegas.to(device).view(1, 1, 1, 1, K) * delta_star.unsqueeze(-1)
-        pi_e = pi.unsqueeze(-1)
-        coeff_cos = (pi_e * a_mk * torch.cos(phase)).sum(dim=3)
-        coeff_sin = (pi_e * a_mk * torch.sin(phase)).sum(dim=3)
-        b0 = coeff_cos.sum(dim=-1) if self.subtract_b0 else q.new_zeros((B, H, L), dtype=torch.float32)
-        main_idx = pi.argmax(dim=-1)
-        delta_main = torch.gather(delta_star, -1, main_idx.unsqueeze(-1)).squeeze(-1)
-        width = self.width_min + (self.width_max - self.width_min) * torch.sigmoid(mu.mean(dim=-1))
+            return self._forward_disabled(q)
+        return self._forward_fused(q, docs)
 
-        z = q.new_zeros((), dtype=torch.float32)
-        reg_omega = reg_entropy = reg_delta_edge = reg_zero_mean = z
-        if self.training:  # model/attn_bias.py:485-506
-            if self.lambda_omega > 0:
-                reg_omega = self.lambda_omega * (self.omega_sq.to(device).view(1, 1, 1, 1, K) * a_mk.square()).sum(-1).mean()
-            if self.lambda_entropy > 0:
-                entropy = -(pi * (pi + self.eps).log()).sum(dim=-1)
-                h_floor = float(self.pi_entropy_floor_frac) * math.log(M)
-                if h_floor > 0:
-                    reg_entropy = self.lambda_entropy * F.relu(entropy.new_tensor(h_floor) - entropy).mean()
-            if self.lambda_zero_mean > 0:
-                mean_b = ((coeff_cos * cos_mean.to(device)).sum(-1) + (coeff_sin * sin_mean.to(device)).sum(-1)
-                          + slope * (0.5 * float(L - 1)) - b0)
-                reg_zero_mean = self.lambda_zero_mean * mean_b.mean().square()
-            if self.lambda_delta_edge > 0:
-                edge_eps = self._delta_edge_eps_active.to(device=device, dtype=torch.float32)
-                u = (delta_star / torch.clamp(delta_cap, min=1.0)).clamp(0.0, 1.0)
-                edge = F.relu(edge_eps - u) + F.relu(u - (1.0 - edge_eps))
-                reg_delta_edge = self.lambda_delta_edge * edge.mean()
-        reg_loss = reg_omega + reg_entropy + reg_delta_edge + reg_zero_mean
-
-        if self.debug_stats:
-            if B == 1 and L % 128 == 0:
-                self._forward_stats(delta_star.detach(), pi.detach(), docs, L)
-            for name, val in (("reg_omega", reg_omega), ("reg_entropy", reg_entropy),
-                              ("reg_delta_edge", reg_delta_edge), ("reg_zero_mean", reg_zero_mean),
-                              ("reg_total", reg_loss)):
-                getattr(self, "_dbg_" + name).copy_(val.detach())
-        return (coeff_cos, coeff_sin, slope, b0, delta_star, pi, budget_logits, delta_main, width, cos_wD, sin_wD,
-                reg_loss)
+    def _forward_disabled(self, q: Tensor) -> tuple[Tensor, ...]:
+        """model/attn_bias.py:411-417: zero coefficients, uniform π."""
+        B, H, L, _ = q.shape
+        cos_wD, sin_wD, _, _ = self._get_trig_tables(L, q.device)
+        f = dict(dtype=torch.float32, device=q.device)
+        z_k = torch.zeros((B, H, L, self.K), **f)
+        z_l = torch.zeros((B, H, L), **f)
+        z_m = torch.zeros((B, H, L, self.M), **f)
+        z_pi = torch.full((B, H, L, self.M), 1.0 / self.M, **f)
+        return z_k, z_k, z_l, z_l, z_m, z_pi, z_m, z_l, z_l, cos_wD, sin_wD, torch.zeros((), **f)
 
     def _forward_fused(self, q: Tensor, docs: Tensor | None) -> tuple[Tensor, ...]:
         """GPU forward: the MLP in torch, then the fused coefficient head."""

@@ -117,7 +117,9 @@ def test_bf16_input_equals_fp32_input(M, K):
 
 def test_fused_head_matches_torch_steps_at_training_shape():
     """T=65536, H=8, M=8, K=8 in bf16 (the module's MLP dtype follows q): the
-    fused kernels against the same module's torch steps on the same GPU."""
+    fused kernels against the oracle's torch steps with the same module's
+    parameters on the same GPU."""
+    from oracle.coeff_head import coeff_head_forward
     from scope_amd import SpectralBias
 
     torch.manual_seed(0)
@@ -128,7 +130,7 @@ def test_fused_head_matches_torch_steps_at_training_shape():
     q = torch.randn((1, 8, 65536, 128), device=DEV).to(torch.bfloat16).requires_grad_()
     out_f = sb(q)
     q2 = q.detach().clone().requires_grad_()
-    out_t = sb._forward_torch(q2)
+    out_t = coeff_head_forward(sb, q2)  # the oracle, as the checker, on the same GPU
     for i, n in enumerate(NAMES):
         a, b = out_f[i].float(), out_t[i].float()
         tol = 1e-4 * b.abs().max().item() + 1e-4 * b.abs()
@@ -144,3 +146,15 @@ def test_fused_head_matches_torch_steps_at_training_shape():
     # both run the MLP backward in bf16; the head's dy is rounded to bf16 in both
     err = (gf - gt).abs().max().item()
     assert err <= 2e-2 * gt.abs().max().item(), f"dq max err {err:.3e} vs max {gt.abs().max().item():.3e}"
+
+
+def test_disabled_forward_on_gpu():
+    """enabled=False returns zeros and uniform π like the reference
+    (model/attn_bias.py:411-417), on the GPU."""
+    from scope_amd import SpectralBias
+
+    sb = SpectralBias(head_dim=16, num_heads=2, L_train=64, M=3, enabled=False).to(DEV)
+    out = sb(torch.randn(1, 2, 64, 16, device=DEV))
+    assert len(out) == 12 and out[0].is_cuda
+    assert all(torch.all(out[i] == 0) for i in (0, 1, 2, 3, 4, 6, 7, 8, 11))
+    assert torch.allclose(out[5], torch.full_like(out[5], 1 / 3))

@@ -1,6 +1,8 @@
 """CPU: the host-side mirror of the reference interface — configuration
-errors, schedule setters, the coefficient head against the reference's
-golden vectors, shape assertions, and the BlockMask export logic."""
+errors, schedule setters, the oracle's coefficient head against the
+reference's golden vectors (the fused kernels are checked against the same
+vectors on the GPU), the GPU-only forward, shape assertions, and the
+BlockMask export logic."""
 from __future__ import annotations
 
 import numpy as np
@@ -8,6 +10,7 @@ import pytest
 import torch
 
 from oracle import pointer as P
+from oracle.coeff_head import coeff_head_forward
 from scope_amd import ScopeBlockMask, SpectralBias
 from tests.golden import load_cases, load_flat
 
@@ -59,17 +62,24 @@ def test_coefficient_head_matches_reference_vectors():
         sb.mlp[2].bias.copy_(torch.from_numpy(g["b2"]))
     sb.eval()
     assert np.allclose(sb.omegas.numpy(), g["omegas"])
-    out = sb(torch.from_numpy(g["q"])[None])
+    out = coeff_head_forward(sb, torch.from_numpy(g["q"])[None])
     names = ["coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits", "delta_main", "width"]
     for i, n in enumerate(names):
         ref = torch.from_numpy(g[n])
         assert torch.allclose(out[i][0], ref, rtol=1e-5, atol=1e-6), n
 
 
-def test_disabled_forward_returns_zeros_and_uniform_pi():
+def test_oracle_disabled_head_returns_zeros_and_uniform_pi():
     sb = SpectralBias(head_dim=16, num_heads=2, L_train=64, M=3, enabled=False)
-    out = sb(torch.randn(1, 2, 64, 16))
+    out = coeff_head_forward(sb, torch.randn(1, 2, 64, 16))
     assert torch.all(out[0] == 0) and torch.allclose(out[5], torch.full_like(out[5], 1 / 3))
+
+
+@pytest.mark.parametrize("enabled", [True, False])
+def test_forward_has_no_cpu_path(enabled):
+    sb = SpectralBias(head_dim=16, num_heads=2, L_train=64, M=3, enabled=enabled)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        sb(torch.randn(1, 2, 64, 16))
 
 
 def test_build_pointer_blockmask_shape_assertions():
@@ -109,7 +119,7 @@ def test_blockmask_export_matches_reference():
 
 
 def _coeff_train_run(g: dict, lams: dict, G=None):
-    """The host coefficient head in training mode on the recorded inputs:
+    """The oracle's coefficient head in training mode on the recorded inputs:
     (outputs, reg_loss, grads of Σ<out_i, G_i> (if G), grads of reg_loss)."""
     sb = SpectralBias(head_dim=int(g["Dh"]), num_heads=int(g["H"]), L_train=int(g["L_train"]),
                       L_max=int(g["L_max"]), M=int(g["M"]), K=int(g["K"]),
@@ -122,7 +132,7 @@ def _coeff_train_run(g: dict, lams: dict, G=None):
         sb.mlp[2].bias.copy_(torch.from_numpy(g["b2"]))
     sb.train()
     q = torch.from_numpy(g["q"])[None].clone().requires_grad_()
-    out = sb(q)
+    out = coeff_head_forward(sb, q)
     params = [q, sb.mlp[0].weight, sb.mlp[0].bias, sb.mlp[2].weight, sb.mlp[2].bias]
     go = None
     if G is not None:
