@@ -158,6 +158,20 @@ int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, 
                            int maxkv, int32_t* q_off, int32_t* q_list, void* workspace,
                            void* stream);
 
+/* scope_transpose_blocks without a workspace: it allocates nothing (no
+ * hipMalloc, no allocating library call), for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it.  No counterpart in the reference.  Same kernels
+ * and results; the fill cursors live in a static device array of the library
+ * (SCOPE_NOALLOC_MAX_HNB int32 per device, 1 MiB, held until the process
+ * ends), so H*NB must not exceed SCOPE_NOALLOC_MAX_HNB (else SCOPE_ERANGE).
+ * The array is shared by every call on a device and cleared by each call:
+ * calls that overlap on one device (concurrent streams, threads) race.  The
+ * stream must belong to the current device. */
+#define SCOPE_NOALLOC_MAX_HNB 262144
+int scope_transpose_blocks_noalloc(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB,
+                                   int maxkv, int32_t* q_off, int32_t* q_list, void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused coefficient head.  Replaces the [B,H,L,M,K] mixture of
  * SpectralBias.forward between the MLP output and the returned terms

@@ -11,7 +11,16 @@
 // the result is deterministic.
 #include <limits.h>
 
+#include <mutex>
+
 #include "common.h"
+
+// Scratch of scope_transpose_blocks_noalloc: the per-(head, key block) fill
+// cursors, in device memory the library owns, so that entry point allocates
+// nothing.  Each device holds its own copy until the process ends; host code
+// uses the device address hipGetSymbolAddress reports for the current device,
+// never this name.
+static __device__ __align__(256) int32_t scratch[SCOPE_NOALLOC_MAX_HNB];
 
 namespace scope {
 
@@ -131,22 +140,54 @@ __global__ __launch_bounds__(256) void tr_sort_kernel(int NB, int QB, int maxkv,
   for (int i = lane; i < n; i += nt) b[i] = s[i];
 }
 
-}  // namespace scope
+// Address of `scratch` on each device, looked up once per device with that
+// device current.
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch_ptr[kMaxDevices] = {};
 
-using namespace scope;
+static int noalloc_scratch(void* stream, int32_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(SCOPE_ELAUNCH, "scope_transpose_blocks_noalloc: hipGetDevice: %s",
+                                        hipGetErrorString(e));
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(as_stream(stream), &sdev);
+    if (e != hipSuccess)
+      return set_error(SCOPE_ELAUNCH, "scope_transpose_blocks_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev)
+      return set_error(SCOPE_EINVAL, "scope_transpose_blocks_noalloc: the stream belongs to device %d, the current "
+                       "device is %d", static_cast<int>(sdev), dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(SCOPE_ERANGE, "scope_transpose_blocks_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(SCOPE_ELAUNCH, "scope_transpose_blocks_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<int32_t*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return SCOPE_OK;
+}
 
-extern "C" {
+static int transpose_checks(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv,
+                            const int32_t* q_off, const int32_t* q_list, const char* fn) {
+  SCOPE_REQUIRE(kv_num && kv_idx && q_off && q_list, "%s: null pointer", fn);
+  SCOPE_REQUIRE(H >= 1 && QB >= 1 && NB >= 1 && maxkv >= 1, "%s: bad sizes", fn);
+  SCOPE_REQUIRE(next_pow2(QB) * 4 <= 64 * 1024, "%s: QB=%d exceeds the LDS sort capacity", fn, QB);
+  return SCOPE_OK;
+}
 
-int64_t scope_transpose_workspace_bytes(int H, int NB) { return static_cast<int64_t>(H) * NB * 4; }
-
-int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv,
-                           int32_t* q_off, int32_t* q_list, void* workspace, void* stream) {
-  SCOPE_REQUIRE(kv_num && kv_idx && q_off && q_list && workspace, "scope_transpose_blocks: null pointer");
-  SCOPE_REQUIRE(H >= 1 && QB >= 1 && NB >= 1 && maxkv >= 1, "scope_transpose_blocks: bad sizes");
+// count -> scan -> fill -> sort with `cursor` [H·NB] as the fill cursors
+// (zeroed here by a kernel, so the launches can be captured in a graph).
+static int transpose_launch(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv,
+                            int32_t* q_off, int32_t* q_list, int32_t* cursor, hipStream_t s) {
   const int cap = next_pow2(QB);
-  SCOPE_REQUIRE(cap * 4 <= 64 * 1024, "scope_transpose_blocks: QB=%d exceeds the LDS sort capacity", QB);
-  hipStream_t s = as_stream(stream);
-  int32_t* cursor = static_cast<int32_t*>(workspace);
   const int64_t n_off = static_cast<int64_t>(H) * (NB + 1);
   const int64_t n_cur = static_cast<int64_t>(H) * NB;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(n_off, 256)), dim3(256), 0, s, q_off, n_off, 0);
@@ -159,6 +200,37 @@ int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, 
                      q_off, cursor, q_list);
   hipLaunchKernelGGL(tr_sort_kernel, dim3(NB, H), dim3(256), cap * sizeof(int), s, NB, QB, maxkv, q_off, q_list, cap);
   return check_launch("transpose kernels");
+}
+
+}  // namespace scope
+
+using namespace scope;
+
+extern "C" {
+
+int64_t scope_transpose_workspace_bytes(int H, int NB) { return static_cast<int64_t>(H) * NB * 4; }
+
+int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv,
+                           int32_t* q_off, int32_t* q_list, void* workspace, void* stream) {
+  int rc = transpose_checks(kv_num, kv_idx, H, QB, NB, maxkv, q_off, q_list, "scope_transpose_blocks");
+  if (rc) return rc;
+  SCOPE_REQUIRE(workspace, "scope_transpose_blocks: null workspace");
+  return transpose_launch(kv_num, kv_idx, H, QB, NB, maxkv, q_off, q_list, static_cast<int32_t*>(workspace),
+                          as_stream(stream));
+}
+
+int scope_transpose_blocks_noalloc(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv,
+                                   int32_t* q_off, int32_t* q_list, void* stream) {
+  int rc = transpose_checks(kv_num, kv_idx, H, QB, NB, maxkv, q_off, q_list, "scope_transpose_blocks_noalloc");
+  if (rc) return rc;
+  if (static_cast<int64_t>(H) * NB > SCOPE_NOALLOC_MAX_HNB)
+    return set_error(SCOPE_ERANGE, "scope_transpose_blocks_noalloc: H*NB = %lld exceeds the static scratch of %d "
+                     "cursors (use scope_transpose_blocks with a workspace)",
+                     static_cast<long long>(H) * NB, SCOPE_NOALLOC_MAX_HNB);
+  int32_t* cursor = nullptr;
+  rc = noalloc_scratch(stream, &cursor);
+  if (rc) return rc;
+  return transpose_launch(kv_num, kv_idx, H, QB, NB, maxkv, q_off, q_list, cursor, as_stream(stream));
 }
 
 }  // extern "C"

@@ -229,6 +229,28 @@ def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int):
     return q_off, q_list
 
 
+NOALLOC_MAX_HNB = 262144  # include/scope_amd.h SCOPE_NOALLOC_MAX_HNB
+
+
+def transpose_blocks_noalloc(kv_num: torch.Tensor, kv_idx: torch.Tensor, q_off: torch.Tensor,
+                             q_list: torch.Tensor) -> None:
+    """``transpose_blocks`` into caller-provided q_off [H, NB+1] / q_list
+    [H, QB*MAXKV] int32 without any device allocation by the library (its
+    cursors sit in a static device array: H*NB <= 262144; calls that overlap
+    on one device race).  kv_num / kv_idx must already be contiguous int32."""
+    dev = _gpu("transpose_blocks_noalloc", kv_num, kv_idx, q_off, q_list)
+    for n_, t in (("kv_num", kv_num), ("kv_idx", kv_idx), ("q_off", q_off), ("q_list", q_list)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise RuntimeError(f"transpose_blocks_noalloc: {n_} must be a contiguous int32 tensor")
+    H, QB = kv_num.shape[-2], kv_num.shape[-1]
+    maxkv = kv_idx.shape[-1]
+    NB = q_off.shape[-1] - 1
+    if q_off.numel() != H * (NB + 1) or q_list.numel() != H * QB * maxkv or kv_idx.numel() != H * QB * maxkv:
+        raise RuntimeError("transpose_blocks_noalloc: q_off [H, NB+1], q_list [H, QB*MAXKV] do not match the lists")
+    call("scope_transpose_blocks_noalloc", _p(kv_num), _p(kv_idx), H, QB, NB, maxkv, _p(q_off), _p(q_list),
+         _stream(dev))
+
+
 def _coeff_prm(y: torch.Tensor, prm: dict):
     from ._lib import CoeffParams
 
