@@ -46,6 +46,12 @@ gradient through the block means into dq and dk (pointer backward timed as
 its own phase).  ``--soft-temp`` also turns the weights on for the default
 workload.
 
+``--workload ref`` times the reference's default layer path (its defaults:
+T=16384, bs 128, K=6 token-offset bands with slope as in qk_aug, reference-mode
+lists with local 8, half 4, M 8, budget 64 in total, temperature 0.5): the
+coefficient head, the reference-mode mask, the attention and the whole
+backward; ``--T 65536`` for the training shape.
+
 ``--workload decode`` runs the 16-layer decoder (d_model 1024, 8 heads of
 128, MLP 4096 ReLU², vocabulary 50304, bf16, random weights): a prefill of
 131072 seeded uniform-random tokens, then 256 greedy decode steps with the
@@ -84,7 +90,7 @@ def parse():
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["pointer", "train", "swa", "coeff", "teacher", "decode"],
+    ap.add_argument("--workload", choices=["pointer", "train", "swa", "coeff", "teacher", "decode", "ref"],
                     default="pointer")
     ap.add_argument("--soft-temp", type=float, default=0.0,
                     help="soft pointer weights log σ(z/τ) on the picks (0: default, off except --workload train: 4; < 0: off)")
@@ -551,6 +557,99 @@ def main_decode(args):
     print(json.dumps(res))
 
 
+def main_ref(args):
+    """The reference's default layer path (scoped_medium.py:334-466 with the
+    defaults of :692-727): SpectralBias.forward (MLP + coefficient head, K=6
+    bands, M=8 peaks), build_pointer_blockmask in reference mode (local 8,
+    half 4, budget 64 in total, temperature 0.5, "pi" radii, no global
+    blocks), the attention with the qk_aug terms (token offsets, slope, no
+    gate) and the whole backward, through scope_attention / SpectralBias as
+    the reference would call them."""
+    import torch
+
+    from scope_amd import SpectralBias, SpectralTerms, scope_attention
+
+    H, D, bs = args.H, 128, 128
+    T = args.T if args.T != 131072 else 16384
+    inp = make_inputs(H, T, D, bs, needle=False)
+    q, k, v, dout, docs = (inp[n].cuda() for n in ("q", "k", "v", "dout", "docs"))
+    sb = SpectralBias(head_dim=D, num_heads=H, L_train=4096, K=6, M=8, use_pointer_mask=True,
+                      pointer_local_blocks=8, pointer_half_blocks=4, pointer_budget_blocks=64,
+                      pointer_budget_is_total=True, pointer_budget_temp=0.5, pointer_radius_mode="pi",
+                      pointer_global_blocks=0).cuda().train()
+    sb.set_delta_star_max_active(max_tokens=T - 1)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    with torch.no_grad():  # a spread of pointer offsets (the reference zero-initialises the head's last layer)
+        for p_ in sb.mlp.parameters():
+            p_.copy_(torch.randn(p_.shape, generator=g, device="cuda") * 0.05)
+    one = torch.ones((), device="cuda")
+
+    def layer(q_, k_, v_):
+        out = sb(q_, docs=docs)
+        bm = sb.build_pointer_blockmask(docs=docs, delta_star=out[4], pi=out[5], budget_logits=out[6], block_size=bs)
+        sp = SpectralTerms(coeff_cos=out[0], coeff_sin=out[1], omegas=sb.omegas, offset="token", beta=sb.beta,
+                           slope=out[2], use_slope=True)
+        return scope_attention(q_, k_, v_, block_mask=bm, scale=0.12, spectral=sp), out[11], bm
+
+    def step():
+        qd, kd, vd = (x.detach().requires_grad_() for x in (q, k, v))
+        y, reg, _ = layer(qd, kd, vd)
+        torch.autograd.backward([y, reg], [dout, one])
+
+    with torch.no_grad():
+        _, _, bm = layer(q, k, v)
+    n_act = int(bm.kv_num_blocks.sum())
+    maxkv = bm.maxkv
+    t_step = time_region(step, args.steps, args.warmup)
+    # the attention alone on the same lists and terms
+    qd, kd, vd = (x.detach().requires_grad_() for x in (q, k, v))
+    with torch.no_grad():
+        out = sb(q, docs=docs)
+    sp = SpectralTerms(coeff_cos=out[0], coeff_sin=out[1], omegas=sb.omegas, offset="token", beta=sb.beta,
+                       slope=out[2], use_slope=True)
+
+    def attn_fwd_only():
+        with torch.no_grad():
+            scope_attention(q, k, v, block_mask=bm, scale=0.12, spectral=sp)
+
+    def attn_fwd_bwd():
+        y = scope_attention(qd, kd, vd, block_mask=bm, scale=0.12, spectral=sp)
+        y.backward(dout)
+
+    t_fwd = time_region(attn_fwd_only, args.steps, args.warmup)
+    t_attn = time_region(attn_fwd_bwd, args.steps, args.warmup)
+    F_fwd, F_bwd = 4.0 * bs * bs * D * n_act, 10.0 * bs * bs * D * n_act
+    res = {
+        "metric": "SCOPE layer fwd+bwd on the reference's default path (qk_aug terms, reference-mode lists) "
+                  "active-block TFLOP/s, 1 MI355X",
+        "value": round((F_fwd + F_bwd) / t_step / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "reference default layer: coefficient head + reference-mode pointer mask + attention "
+                               "(token offsets, K=6, slope, no gate) fwd+bwd", "B": 1, "H": H, "T": T, "D": D,
+                   "block": bs, "local": 8, "half": 4, "M": 8, "budget_total": 64, "budget_temp": 0.5,
+                   "global": 0, "maxkv": maxkv, "docs": max(1, T // 8192)},
+        "tokens_per_s": round(T / t_step, 1),
+        "n_act": n_act,
+        "attn_fwd_ms": round(t_fwd * 1e3, 4),
+        "attn_fwd_tflops": round(F_fwd / t_fwd / 1e12, 2),
+        "attn_fwd_bwd_ms": round(t_attn * 1e3, 4),
+        "attn_fwd_bwd_tflops": round((F_fwd + F_bwd) / t_attn / 1e12, 2),
+        "roofline": dict(bound="mfma", kernel="attention fwd+bwd (token mode)",
+                         achieved=round((F_fwd + F_bwd) / t_attn / 1e12, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                         frac=round((F_fwd + F_bwd) / t_attn / 1e12 / PEAK_BF16_TFLOPS, 4), traffic=None),
+    }
+    print(json.dumps(res))
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -781,6 +880,9 @@ def main():
     torch.cuda.set_device(0)
     if args.workload == "decode":
         main_decode(args)
+        return
+    if args.workload == "ref":
+        main_ref(args)
         return
     if args.workload == "teacher":
         main_teacher(args)

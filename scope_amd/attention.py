@@ -12,8 +12,9 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+from torch._subclasses.fake_tensor import FakeTensor
 
-from . import ops
+from . import library, ops
 from .blockmask import ScopeBlockMask
 
 
@@ -44,107 +45,37 @@ class SpectralTerms:
 
 
 _TABLES: dict = {}
+_MODE = {"none": 0, "block": 1, "token": 2}
+_GATE = {"none": 0, "softplus": 1, "relu": 2}
 
 
 def spectral_table(omegas: torch.Tensor, T: int, bs: int, mode: str) -> torch.Tensor:
-    """Cached cos/sin table (the analogue of SpectralBias._get_trig_tables)."""
+    """cos/sin table (the analogue of SpectralBias._get_trig_tables), cached
+    per (ω, T, bs, mode) in eager mode and rebuilt in compiled graphs."""
+    if torch.compiler.is_compiling() or isinstance(omegas, FakeTensor):  # traced: no cache keyed on pointers
+        return library.spectral_table(omegas, T, bs, _MODE[mode])
     key = (omegas.data_ptr(), omegas._version, omegas.device, T, bs, mode)
     tab = _TABLES.get(key)
     if tab is None:
         if len(_TABLES) > 16:
             _TABLES.clear()
-        tab = ops.spectral_table(omegas, T, bs, mode)
+        tab = library.spectral_table(omegas, T, bs, _MODE[mode])
         _TABLES[key] = tab
     return tab
-
-
-def _kwargs(sp: SpectralTerms | None, bm: ScopeBlockMask):
-    if sp is None:
-        return dict(bias_mode="none")
-    T = bm.seq_len
-    return dict(bias_mode=sp.offset, beta=sp.beta, table=spectral_table(sp.omegas, T, bm.BLOCK_SIZE, sp.offset),
-                use_slope=sp.use_slope and sp.offset == "token",
-                subtract_b0=sp.subtract_b0 and sp.offset == "token",
-                gate_kind=sp.gate_kind if sp.offset == "token" else "none", ramp_lambda=sp.ramp_lambda, tau=sp.tau)
-
-
-class _ScopeAttnFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, v, cc, cs, b0, slope, dm, wd, pb, bm: ScopeBlockMask, sp: SpectralTerms | None,
-                scale: float):
-        kw = _kwargs(sp, bm)
-        out, lse = ops.attn_fwd(q, k, v, bm.kv_num_blocks[0], bm.kv_indices[0], bm.docs, bm.ds_tok_end,
-                                bs=bm.BLOCK_SIZE, scale=scale, coeff_cos=cc, coeff_sin=cs, b0=b0, slope=slope,
-                                delta_main=dm, width=wd, pair_bias=pb, **kw)
-        ctx.save_for_backward(q, k, v, out, lse, cc, cs, b0, slope, dm, wd, pb)
-        ctx.bm, ctx.sp, ctx.scale = bm, sp, scale
-        ctx.mark_non_differentiable(lse)
-        return out, lse
-
-    @staticmethod
-    def backward(ctx, dout, _dlse):
-        q, k, v, out, lse, cc, cs, b0, slope, dm, wd, pb = ctx.saved_tensors
-        bm, sp = ctx.bm, ctx.sp
-        kw = _kwargs(sp, bm)
-        q_off, q_list = bm.q_lists()
-        dout = dout if dout.stride() == q.stride() else _match(dout, q)
-        out_m = out if out.stride() == q.stride() else _match(out, q)
-        need_c = sp is not None and any(ctx.needs_input_grad[3:9])
-        need_p = pb is not None and ctx.needs_input_grad[9]
-        g = ops.attn_bwd(q, k, v, out_m, dout, lse, bm.kv_num_blocks[0], bm.kv_indices[0], q_off, q_list, bm.docs,
-                         bm.ds_tok_end, bs=bm.BLOCK_SIZE, scale=ctx.scale, coeff_cos=cc, coeff_sin=cs, b0=b0,
-                         slope=slope, delta_main=dm, width=wd, need_coeff_grads=need_c, pair_bias=pb,
-                         need_pair_grad=need_p, **kw)
-        dpb = g["dpair_bias"].reshape(pb.shape) if need_p else None
-        return (g["dq"], g["dk"], g["dv"], g["dcoeff_cos"], g["dcoeff_sin"], g["db0"], g["dslope"],
-                g["ddelta_main"], g["dwidth"], dpb, None, None, None)
-
-
-class _SoftPointerFn(torch.autograd.Function):
-    """Soft weights of the block-scoring picks as a per-list-entry score
-    bias: b = log σ(z/τ_w), z = logit_scale·q̄·k̄ + prior (noise-free), on the
-    pick entries (scope_pointer_pair_bias).  Backward: the block-mean chain
-    into q and k (scope_pointer_bwd).  No reference counterpart: the
-    reference's selection runs under torch.no_grad (model/attn_bias.py:623)."""
-
-    @staticmethod
-    def forward(ctx, q, k, bm: ScopeBlockMask, window: int, n_global: int, logit_scale: float, soft_temp: float,
-                prior):
-        bs = bm.BLOCK_SIZE
-        qbar, kbar = ops.block_means(q, k, bs)
-        picks = bm.extras["picks"]
-        pb = ops.pointer_pair_bias(bm.kv_num_blocks[0], bm.kv_indices[0], picks, bs=bs, window=window,
-                                   n_global=n_global, soft_temp=soft_temp, qbar=qbar, kbar=kbar, prior=prior,
-                                   logit_scale=logit_scale)
-        ctx.save_for_backward(qbar, kbar, pb)
-        ctx.bm, ctx.logit_scale, ctx.soft_temp = bm, logit_scale, soft_temp
-        ctx.q_like, ctx.k_like = (q.shape, q.stride()), (k.shape, k.stride())
-        return pb
-
-    @staticmethod
-    def backward(ctx, dpb):
-        qbar, kbar, pb = ctx.saved_tensors
-        bm = ctx.bm
-        q_off, q_list = bm.q_lists()
-        dq = torch.empty_strided(*ctx.q_like, dtype=torch.bfloat16, device=pb.device).zero_()
-        dk = torch.empty_strided(*ctx.k_like, dtype=torch.bfloat16, device=pb.device).zero_()
-        ops.pointer_bwd(qbar, kbar, bm.kv_num_blocks[0], bm.kv_indices[0], q_off, q_list, pb, dpb.contiguous(), dq,
-                        dk, bs=bm.BLOCK_SIZE, logit_scale=ctx.logit_scale, soft_temp=ctx.soft_temp)
-        return dq, dk, None, None, None, None, None, None
 
 
 def soft_pointer_bias(q: torch.Tensor, k: torch.Tensor, block_mask: ScopeBlockMask, *, window: int, n_global: int,
                       logit_scale: float, soft_temp: float, prior: torch.Tensor | None = None) -> torch.Tensor:
     """Differentiable soft weights [H,QB,MAXKV] of a block-scoring mask's
-    picks (q, k the tensors the mask was selected from)."""
-    return _SoftPointerFn.apply(q, k, block_mask, int(window), int(n_global), float(logit_scale),
-                                float(soft_temp), prior)
-
-
-def _match(x: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
-    y = torch.empty_like(like)
-    y.copy_(x)
-    return y
+    picks (q, k the tensors the mask was selected from): b = log σ(z/τ_w),
+    z = logit_scale·q̄·k̄ + prior (noise-free), on the pick entries; the
+    backward carries the block-mean chain into q and k.  No reference
+    counterpart: the reference's selection runs under torch.no_grad
+    (model/attn_bias.py:623)."""
+    pb, _, _ = library.soft_pointer_bias(q, k, block_mask.kv_num_blocks[0], block_mask.kv_indices[0],
+                                         block_mask.extras["picks"], prior, block_mask.BLOCK_SIZE, int(window),
+                                         int(n_global), float(logit_scale), float(soft_temp))
+    return pb
 
 
 def scope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block_mask: ScopeBlockMask,
@@ -154,18 +85,33 @@ def scope_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, block_
     head/token strides, unit last stride).  Returns out [1,H,T,D] (and
     lse [1,H,T], natural log, if ``return_lse``).  A mask built with soft
     pointer weights carries them in ``extras["pair_bias"]``; they are added
-    to the listed tiles' scores and receive gradients."""
-    sp = spectral
-    cc = cs = b0 = sl = dm = wd = None
+    to the listed tiles' scores and receive gradients.  Runs the
+    ``scope::attn_fwd`` operator (its autograd formula is ``scope::attn_bwd``),
+    so it traces under torch.compile without a graph break."""
+    bm, sp = block_mask, spectral
+    bs = bm.BLOCK_SIZE
+    cc = cs = b0 = sl = dm = wd = table = None
+    mode, gate, beta, use_slope, sub_b0, lam, tau = 0, 0, 0.5, False, False, 0.0, 64.0
     if sp is not None:
         cc, cs = sp.coeff_cos, sp.coeff_sin
+        mode, beta, lam, tau = _MODE[sp.offset], float(sp.beta), float(sp.ramp_lambda), float(sp.tau)
+        table = spectral_table(sp.omegas, bm.seq_len, bs, sp.offset)
         if sp.offset == "token":
-            b0 = sp.b0 if sp.subtract_b0 else None
-            sl = sp.slope if sp.use_slope else None
-            if sp.gate_kind != "none":
+            use_slope, sub_b0, gate = bool(sp.use_slope), bool(sp.subtract_b0), _GATE[sp.gate_kind]
+            b0 = sp.b0 if sub_b0 else None
+            sl = sp.slope if use_slope else None
+            if gate:
                 dm, wd = sp.delta_main, sp.width
-    pb = block_mask.extras.get("pair_bias")
-    out, lse = _ScopeAttnFn.apply(q, k, v, cc, cs, b0, sl, dm, wd, pb, block_mask, sp, float(scale))
+    pb = bm.extras.get("pair_bias")
+    kv_num, kv_idx = bm.kv_num_blocks[0], bm.kv_indices[0]
+    grad = torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                           for t in (q, k, v, cc, cs, b0, sl, dm, wd, pb))
+    if grad:
+        q_off, q_list = bm.q_lists()
+    else:  # no backward: the transposed lists are not needed
+        q_off = q_list = kv_num.new_empty(0)
+    out, lse = library.attn_fwd(q, k, v, kv_num, kv_idx, bm.docs, bm.ds_tok_end, q_off, q_list, table, cc, cs, b0,
+                                sl, dm, wd, pb, bs, float(scale), beta, mode, use_slope, sub_b0, gate, lam, tau)
     return (out, lse) if return_lse else out
 
 

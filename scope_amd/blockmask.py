@@ -23,7 +23,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-from . import ops
+from . import library, ops
 
 
 @dataclass
@@ -61,7 +61,7 @@ class ScopeBlockMask:
     def q_lists(self) -> tuple[torch.Tensor, torch.Tensor]:
         """Transposed lists (CSR): q_off [H, NB+1], q_list [H, QB*MAXKV]."""
         if self._q_lists is None:
-            self._q_lists = ops.transpose_blocks(self.kv_num_blocks[0], self.kv_indices[0], self.num_blocks)
+            self._q_lists = library.transpose_blocks(self.kv_num_blocks[0], self.kv_indices[0], self.num_blocks)
         return self._q_lists
 
     def kv_indices_export(self) -> torch.Tensor:

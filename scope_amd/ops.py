@@ -85,7 +85,7 @@ def doc_starts(docs: torch.Tensor, bs: int, *, doc_clamp: bool = True, reset_len
     if T % bs:
         raise RuntimeError(f"doc_starts: T={T} not a multiple of bs={bs}")
     NB = T // bs
-    out = torch.empty((3, NB), dtype=torch.int32, device=dev)
+    out = [torch.empty(NB, dtype=torch.int32, device=dev) for _ in range(3)]
     call("scope_doc_starts", _p(docs), T, int(bs), int(bool(doc_clamp)), int(max(0, reset_len)), _p(out[0]),
          _p(out[1]), _p(out[2]), _stream(dev))
     return out[0], out[1], out[2]
@@ -214,15 +214,19 @@ def pointer_bwd(qbar: torch.Tensor, kbar: torch.Tensor, kv_num: torch.Tensor, kv
          _p(_f32(dpair_bias)), _p(dq), _p(dk), _p(ws), _stream(dev))
 
 
-def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int):
-    """q lists (CSR): q_off [H, NB+1], q_list [H, QB*MAXKV]."""
+def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int, tail: int | None = None):
+    """q lists (CSR): q_off [H, NB+1], q_list [H, QB*MAXKV].  Entries of a
+    head's q_list past q_off[h, NB] are left as allocated, or set to ``tail``."""
     dev = _gpu("transpose_blocks", kv_num, kv_idx)
     kv_num = _i32(kv_num.reshape(kv_num.shape[-2], kv_num.shape[-1]))
     H, QB = kv_num.shape
     kv_idx = _i32(kv_idx.reshape(H, QB, kv_idx.shape[-1]))
     maxkv = kv_idx.shape[-1]
     q_off = torch.empty((H, NB + 1), dtype=torch.int32, device=dev)
-    q_list = torch.empty((H, QB * maxkv), dtype=torch.int32, device=dev)
+    if tail is None:
+        q_list = torch.empty((H, QB * maxkv), dtype=torch.int32, device=dev)
+    else:
+        q_list = torch.full((H, QB * maxkv), int(tail), dtype=torch.int32, device=dev)
     ws = torch.empty(max(1, query("scope_transpose_workspace_bytes", H, NB)), dtype=torch.uint8, device=dev)
     call("scope_transpose_blocks", _p(kv_num), _p(kv_idx), H, QB, NB, maxkv, _p(q_off), _p(q_list), _p(ws),
          _stream(dev))

@@ -4,11 +4,11 @@ pointer mask, its statistics and the attention running on the gfx950 kernels.
 * constructor, configuration checks and schedule setters mirror
   ``model/attn_bias.py:75-377`` (same keyword names, same ValueErrors);
 * ``forward`` is the coefficient head (``:379-478``) plus the regularisers
-  (``:480-508``).  On the GPU the MLP GEMMs run in torch (BLAS) and
-  everything after them in the fused coefficient-head kernels, forward and
-  backward (``scope_coeff_head_fwd`` / ``_bwd``); CPU tensors take the same
-  steps as the reference's torch ops.  The debug statistics (``:510-606``)
-  run in the fused statistics kernel (GPU only) without host syncs;
+  (``:480-508``): the MLP GEMMs run in torch (BLAS) and everything after them
+  in the fused coefficient-head kernels, forward and backward
+  (``scope::coeff_head_fwd`` / ``_bwd``).  GPU tensors only: there is no CPU
+  path.  The debug statistics (``:510-606``) run in the fused statistics
+  kernel without host syncs;
 * ``build_pointer_blockmask`` (``:623-873``) runs the doc-start and
   reference-mode pointer kernels and returns a ``ScopeBlockMask``;
 * ``build_blockscore_mask`` is the block-mean q·k selection (this project's
@@ -21,11 +21,12 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from . import ops
+from . import library, ops
 from .attention import SpectralTerms
 from .blockmask import ScopeBlockMask
 
@@ -124,8 +125,7 @@ class SpectralBias(nn.Module):
         self.register_buffer("logw_min", torch.tensor(math.log(w_min), dtype=torch.float32), persistent=False)
         self.register_buffer("logw_max", torch.tensor(math.log(w_max), dtype=torch.float32), persistent=False)
         # the same fp32 values on the host (kernel arguments without a device read)
-        self._logw = (float(torch.tensor(math.log(w_min), dtype=torch.float32)),
-                      float(torch.tensor(math.log(w_max), dtype=torch.float32)))
+        self._logw = (float(np.float32(math.log(w_min))), float(np.float32(math.log(w_max))))
         self._trig_cache: dict = {}
 
         # debug statistics buffers (model/attn_bias.py:239-265)
@@ -291,8 +291,8 @@ class SpectralBias(nn.Module):
             raise ValueError(f"expected head_dim={self.head_dim}, got {Dh}")
         cos_wD, sin_wD, cos_mean, sin_mean = self._get_trig_tables(L, q.device)
         y = self._mlp_forward(q)
-        prm = self._head_params(L)
-        outs = _CoeffHeadFn.apply(y, self.omegas, self.log_omegas, cos_mean, sin_mean, prm)
+        iprm, fprm = library.pack_head_params(self._head_params(L))
+        outs = library.coeff_head_fwd(y, self.omegas, self.log_omegas, cos_mean, sin_mean, iprm, fprm)
         coeff_cos, coeff_sin, slope, b0, delta_star, pi, budget_logits, delta_main, width, reg_all = outs
         reg_loss = reg_all[0] if self.training else q.new_zeros((), dtype=torch.float32)
         if self.debug_stats:
@@ -311,13 +311,13 @@ class SpectralBias(nn.Module):
         reset_on = bool(self._st["reset"]) and self._st["reset_len"] > 0
         ds_ptr = ds_local = None
         if has_docs:
-            ds_ptr, ds_local, _ = ops.doc_starts(docs, bs, doc_clamp=self.pointer_doc_clamp,
-                                                 reset_len=self._st["reset_len"] if reset_on else 0)
-        counts, values = ops.mask_stats(H=self.num_heads, QB=QB, bs=bs, delta_star=delta_star, pi=pi,
-                                        rep_mode=self.pointer_qblock_rep, has_docs=has_docs,
-                                        docstart_enabled=has_docs and (self.pointer_doc_clamp or bool(self._st["reset"])),
-                                        local_blocks_cfg=self.pointer_local_blocks, eps=self.eps,
-                                        ds_ptr_fwd=ds_ptr, ds_local_fwd=ds_local)
+            ds_ptr, ds_local, _ = library.doc_starts(docs.to(torch.int32), bs, bool(self.pointer_doc_clamp),
+                                                     self._st["reset_len"] if reset_on else 0)
+        d3, p3 = (delta_star[0], pi[0]) if delta_star.dim() == 4 else (delta_star, pi)
+        counts, values = library.mask_stats(d3, p3, ds_ptr, ds_local, None, None, None, None, None, self.num_heads,
+                                            QB, bs, self.M, self.pointer_qblock_rep == "mean", has_docs,
+                                            has_docs and (self.pointer_doc_clamp or bool(self._st["reset"])),
+                                            self.pointer_local_blocks, float(self.eps), 1, 1, 1, 1)
         c = ops.unpack_counts(counts, 1, 1)
         self._dbg_delta_tokens_hist.copy_(c["delta_tokens_hist"])
         self._dbg_delta_blocks_hist.copy_(c["delta_blocks_hist"])
@@ -372,22 +372,21 @@ class SpectralBias(nn.Module):
             gumbel_u = torch.rand((H, NB, M), device=device, generator=gen, dtype=torch.float32)
         reset_on = bool(self._st["reset"]) and self._st["reset_len"] > 0
         docs32 = docs.to(torch.int32)
-        ds_ptr, ds_local, ds_tok_end = ops.doc_starts(docs32, block_size, doc_clamp=self.pointer_doc_clamp,
-                                                      reset_len=self._st["reset_len"] if reset_on else 0)
+        ds_ptr, ds_local, ds_tok_end = library.doc_starts(docs32, block_size, bool(self.pointer_doc_clamp),
+                                                          self._st["reset_len"] if reset_on else 0)
         ga = self._st["glob"] if global_blocks is None else int(global_blocks)
-        kv_num, kv_idx, radius, centre = ops.pointer_mask_ref(
-            delta_star, budget_logits, ds_ptr, ds_local, bs=block_size, local_blocks=local, ptr_half_blocks=p,
-            global_blocks_cfg=self.pointer_global_blocks, global_active=ga, radius_mode=self.pointer_radius_mode,
-            budget_rem=budget_rem, budget_temp=self.pointer_budget_temp, mask_active=bool(self._st["mask"]),
-            half_active=self._st["half"], rep_mode=self.pointer_qblock_rep, gumbel_k=gumbel_k,
-            gumbel_tau=self.gumbel_topk_tau, gumbel_u=gumbel_u, eps=self.eps)
+        kv_num, kv_idx, radius, centre = library.pointer_mask_ref(
+            delta_star, budget_logits, ds_ptr, ds_local, gumbel_u if gumbel_k else None, block_size, local, p,
+            self.pointer_global_blocks, ga, self.pointer_radius_mode == "pi", budget_rem,
+            float(self.pointer_budget_temp), bool(self._st["mask"]), self._st["half"],
+            self.pointer_qblock_rep == "mean", gumbel_k, float(self.gumbel_topk_tau), float(self.eps))
         if self.debug_stats:
             mk = self._dbg_kv_unique_hist.numel()
             if kv_idx.shape[-1] + 1 > mk:
                 raise RuntimeError(f"kv_unique histogram has {mk} bins, list width is {kv_idx.shape[-1]}")
             rb, eb = self._dbg_ptr_radius_hist.numel(), self._dbg_ptr_extra_sum_hist.numel()
-            counts, values = ops.mask_stats(H=H, QB=NB, bs=block_size, M=M, kv_num=kv_num, radius=radius,
-                                            maxkv_bins=mk, radius_bins=rb, extra_bins=eb)
+            counts, values = library.mask_stats(None, None, None, None, kv_num, radius, None, None, None, H, NB,
+                                                block_size, M, False, False, False, 1, 1e-9, mk, rb, eb, 1)
             c = ops.unpack_counts(counts, mk, rb)
             self._dbg_kv_unique_hist.copy_(c["kv_unique_hist"])
             self._dbg_ptr_radius_hist.copy_(c["ptr_radius_hist"])
@@ -418,24 +417,22 @@ class SpectralBias(nn.Module):
         H = q.shape[1]
         NB = T // block_size
         docs32 = docs.to(torch.int32)
-        ds_ptr, ds_local, ds_tok_end = ops.doc_starts(docs32, block_size, doc_clamp=self.pointer_doc_clamp)
+        ds_ptr, ds_local, ds_tok_end = library.doc_starts(docs32, block_size, bool(self.pointer_doc_clamp), 0)
         qbar = kbar = None
         if logits is None:
-            qbar, kbar = ops.block_means(q, k, block_size)
+            qbar, kbar = library.block_means(q, k, block_size)
         if noise == "counter" and not self.training:
             noise = "none"
         scale = float(block_size) / math.sqrt(q.shape[-1]) if logit_scale is None else float(logit_scale)
-        res = ops.pointer_select(ds_ptr, ds_local, bs=block_size, NB=NB, H=H, window=window_blocks,
-                                 n_global=global_blocks, budget=budget_blocks, qbar=qbar, kbar=kbar,
-                                 logits_in=logits, prior=prior,
-                                 temp=self.pointer_budget_temp if budget_temp is None else budget_temp,
-                                 logit_scale=scale, noise=noise, gumbel_u=gumbel_u,
-                                 seed=self._st["seed"] if seed is None else seed, eps=self.eps,
-                                 return_logits=return_logits)
-        kv_num, kv_idx, picks = res[:3]
+        noise_mode = {"none": 0, "uniform": 1, "counter": 2}[noise]
+        kv_num, kv_idx, picks, lg = library.pointer_select(
+            ds_ptr, ds_local, qbar, kbar, logits, prior, gumbel_u if noise_mode == 1 else None, block_size, NB, H,
+            window_blocks, global_blocks, budget_blocks,
+            float(self.pointer_budget_temp if budget_temp is None else budget_temp), scale, noise_mode,
+            library.seed_to_signed(self._st["seed"] if seed is None else seed), float(self.eps), bool(return_logits))
         extras = dict(picks=picks)
         if return_logits:
-            extras["logits"] = res[3]
+            extras["logits"] = lg
         bm = ScopeBlockMask(kv_num_blocks=kv_num[None], kv_indices=kv_idx[None], BLOCK_SIZE=block_size,
                             docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local, extras=extras)
         if soft_temp is not None and soft_temp > 0 and budget_blocks > 0:
@@ -447,9 +444,8 @@ class SpectralBias(nn.Module):
                                                             logit_scale=scale, soft_temp=float(soft_temp),
                                                             prior=prior)
             else:
-                extras["pair_bias"] = ops.pointer_pair_bias(kv_num, kv_idx, picks, bs=block_size,
-                                                            window=window_blocks, n_global=global_blocks,
-                                                            soft_temp=float(soft_temp), logits_in=logits)
+                extras["pair_bias"] = library.pair_bias_from_logits(kv_num, kv_idx, picks, logits, block_size,
+                                                                    window_blocks, global_blocks, float(soft_temp))
         return bm
 
     def score_terms(self, outputs: tuple, *, offset: str = "token") -> SpectralTerms:
@@ -459,27 +455,3 @@ class SpectralBias(nn.Module):
                              offset=offset, beta=self.beta, b0=b0, slope=slope, delta_main=delta_main, width=width,
                              use_slope=self.use_slope, subtract_b0=self.subtract_b0, gate_kind=self.gate_kind,
                              ramp_lambda=self.ramp_lambda, tau=self.tau)
-
-
-_HEAD_NAMES = ("coeff_cos", "coeff_sin", "slope", "b0", "delta_star", "pi", "budget_logits", "delta_main", "width")
-
-
-class _CoeffHeadFn(torch.autograd.Function):
-    """MLP output y -> the coefficient head's outputs and regularisers
-    (scope_coeff_head_fwd), with the fused backward (scope_coeff_head_bwd)."""
-
-    @staticmethod
-    def forward(ctx, y, omegas, log_omegas, cos_mean, sin_mean, prm):
-        o = ops.coeff_head_fwd(y, prm, omegas, log_omegas, cos_mean, sin_mean)
-        ctx.save_for_backward(y, omegas, log_omegas, cos_mean, sin_mean, o["reg"])
-        ctx.prm = prm
-        return tuple(o[n] for n in _HEAD_NAMES) + (o["reg"],)
-
-    @staticmethod
-    def backward(ctx, *g):
-        y, omegas, log_omegas, cos_mean, sin_mean, reg = ctx.saved_tensors
-        grads = {n: g[i] for i, n in enumerate(_HEAD_NAMES) if g[i] is not None}
-        g_reg = g[len(_HEAD_NAMES)]
-        g_reg = None if g_reg is None else g_reg[0]
-        dy = ops.coeff_head_bwd(y, ctx.prm, omegas, log_omegas, cos_mean, sin_mean, grads, g_reg, reg)
-        return dy, None, None, None, None, None
