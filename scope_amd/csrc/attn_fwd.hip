@@ -96,11 +96,12 @@ __device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>
 // listed key block summed over the q-block's rows (no P·V either).
 enum FwdKind { kFwdAttn = 0, kFwdLse = 1, kFwdMass = 2 };
 
-// Modes 0 and 1 run two wavefronts per SIMD at either block size (for bs=128
-// the compiler would otherwise take up to 512 registers and run one); the
-// token modes need more registers than that leaves.
+// Every mode runs two wavefronts per SIMD at either block size: for bs=128
+// the compiler would otherwise take up to 512 registers and run one (the
+// token modes then fit in 249-253 registers without spills; two 80.5 KB
+// workgroups share a CU).
 template <int BS, int MODE, int KIND = kFwdAttn>
-__global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(MODE <= 1 ? 2 : 1))) void attn_fwd_kernel(
+__global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) void attn_fwd_kernel(
     AttnArgs a) {
   constexpr int NT = 2 * BS;
   constexpr int NW = NT / 64;  // wavefronts
