@@ -430,7 +430,8 @@ int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t
 
 /* The backward in stream-ordered phases sharing one workspace:
  * SCOPE_BWD_DQ  (q-major: Δ = rowsum(dO∘O), dQ and the coefficient gradients;
- * in token mode it also stores the query features the kv-major pass reads),
+ * it also stores what the kv-major pass reads: the query features in token
+ * mode, otherwise the softmax offset of every row and listed key block),
  * then SCOPE_BWD_DKV (kv-major: dK, dV), which is the three steps
  * SCOPE_BWD_DKV_PLAN (work items), SCOPE_BWD_DKV_MAIN (the dK/dV kernel) and
  * SCOPE_BWD_DKV_REDUCE (ordered sum of chunk partials), run in that order.

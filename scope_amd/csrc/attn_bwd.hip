@@ -11,6 +11,10 @@
 //   Δ, dQ, and the bias gradients: block mode dA_k = β Σ_tiles cos(ω_k r)·Σ_j dS,
 //   token mode through extra MFMAs over the key features (bf16 hi + lo)
 //   (C_k = Σ_j dS cos ω_k j, S_k = Σ_j dS sin ω_k j), slope / b0 / gate per element.
+// Pass A also stores, for the modes without token offsets, each row's
+// softmax offset for every listed key block (block term + pair bias - lse, log2
+// units): pass B copies the 64 offsets of a query tile into LDS with the tile
+// instead of recomputing them in every wavefront.
 // Plan: per key block, its q-list is cut into chunks of kChunk q-blocks.
 // Pass B (kv-major, one workgroup per (head, 128 keys of a key block, chunk)):
 //   dK, dV over the q-list; a block with one chunk writes bf16 directly,
@@ -362,6 +366,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     cur = nxt;
   }
 
+  // ---- modes 0/1: this row's softmax offset for every listed key block (the
+  // block term as in the loop, plus the pair bias, minus lse), read per tile
+  // by the kv-major pass
+  if (MODE <= 1 && g == 0) {
+    float* rof = a.roff + lrow * a.maxkv * BS + (R.row - qb * BS);
+    for (int e = 0; e < n; ++e) {
+      float t = pbias ? kbias[e] : 0.f;
+      if (MODE == 1) {
+        const int rd = min(max(qb - kb_at(e), 0), a.QB - 1);
+        const float4* t4 = reinterpret_cast<const float4*>(static_cast<const float*>(a.table) + rd * 16);
+        const float4 c0 = t4[0], c1 = t4[1], s0 = t4[2], s1 = t4[3];
+        t += (ca[0] * c0.x + ca[1] * c0.y + ca[2] * c0.z + ca[3] * c0.w) +
+             (ca[4] * c1.x + ca[5] * c1.y + ca[6] * c1.z + ca[7] * c1.w) +
+             (sa[0] * s0.x + sa[1] * s0.y + sa[2] * s0.z + sa[3] * s0.w) +
+             (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
+      }
+      rof[e * BS] = t - R.lse2;
+    }
+  }
+
   // ---- epilogue: combine the lane pair's half sums, dQ = scale·o
   rs_tot += __shfl_xor(rs_tot, 32, 64);
   pm_tot += __shfl_xor(pm_tot, 32, 64);
@@ -699,6 +723,28 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     }
   }
 
+  // ---- this row's softmax offset for every listed key block (the block term
+  // as in the loop, plus the pair bias, minus lse), read per tile by the
+  // kv-major pass
+  if (g == 0) {
+    float* rof = a.roff + lrow * a.maxkv * BS + lrow_;
+    for (int e = 0; e < n; ++e) {
+      float t = pbias ? kbias[e] : 0.f;
+      if (MODE == 1) {
+        const int rd = min(max(qb - kb_at(e), 0), a.QB - 1);
+        const float4* t4 = reinterpret_cast<const float4*>(static_cast<const float*>(a.table) + rd * 16);
+        float acc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 c4 = *reinterpret_cast<const float4*>(coef + row16_off(lrow_, i)), tt = t4[i];
+          acc[i] = c4.x * tt.x + c4.y * tt.y + c4.z * tt.z + c4.w * tt.w;
+        }
+        t += (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      }
+      rof[e * BS] = t - R.lse2;
+    }
+  }
+
   // ---- epilogue: dQ = scale·o, coefficient gradients
   rs_tot += __shfl_xor(rs_tot, 32, 64);
   const float dd_err = rs_tot;  // Δ_true - Δ
@@ -835,9 +881,9 @@ template <int MODE>
 struct alignas(16) DkvBuf {
   uint16_t q[64 * 128];            // Q rows, swizzled (swz_off)
   uint16_t d[64 * 128];            // dO rows, swizzled
-  float ra[256];                   // lse | Δ | doc id (int32) | b0, 64 rows each
-  float rb[MODE == 0 ? 4 : 1024];  // block: cos [64][K] at 0, sin [64][K] at 512;
-                                   // token: query features [64][32] bf16 (chunk-swizzled)
+  float ra[256];                   // modes 0/1: softmax offset (log2) | Δ | doc id (int32), 64 rows each;
+                                   // token modes: lse | Δ | doc id | b0
+  float rb[MODE <= 1 ? 4 : 1024];  // token: query features [64][32] bf16 (chunk-swizzled)
   float rc[MODE >= 2 ? 256 : 4];   // token: slope | delta_main | width
 };
 
@@ -846,8 +892,8 @@ struct alignas(16) DkvBuf {
 // coefficients or token features.  The parts are spread over the MFMAs of the
 // current tile, so that no wavefront stalls on a burst of memory instructions.
 template <int MODE>
-__device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t hT, int64_t q0v, DkvBuf<MODE>& b,
-                                               int tid, int part) {
+__device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t hT, int64_t q0v, const float* rof,
+                                               DkvBuf<MODE>& b, int tid, int part) {
   // q0 and the wavefront index are the same in every lane: keep them, and
   // every row base below, in scalar registers (global_load_lds with a scalar
   // base and a 32-bit lane byte offset)
@@ -868,8 +914,9 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
   }
   const uint32_t lo = static_cast<uint32_t>(lane) * 16;  // 16 lanes x 16 bytes = one 64-row float array
   if (part == 8) {
-    // wavefront w copies per-row array w: lse, Δ, document ids, b0
-    const char* base = wave == 0   ? reinterpret_cast<const char*>(a.lse + hT + q0)
+    // wavefront w copies per-row array w: the softmax offsets (modes 0/1) or
+    // lse (token modes), Δ, document ids, b0
+    const char* base = wave == 0   ? reinterpret_cast<const char*>(MODE <= 1 ? rof : a.lse + hT + q0)
                        : wave == 1 ? reinterpret_cast<const char*>(a.delta + hT + q0)
                        : wave == 2 ? reinterpret_cast<const char*>(a.docs + q0)
                                    : reinterpret_cast<const char*>(a.b0 + hT + q0);
@@ -884,12 +931,6 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
     }
     return;
   }
-  if (MODE == 1) {
-    // [64][K] cos rows on wavefronts 0-1, sin rows on 2-3
-    const int ci = (wave & 1) * 64 + lane;
-    const char* base = reinterpret_cast<const char*>((wave < 2 ? a.coeff_cos : a.coeff_sin) + (hT + q0) * a.K);
-    if (ci < 16 * a.K) g2lds16(base, static_cast<uint32_t>(ci) * 16, b.rb + (wave >> 1) * 512 + (wave & 1) * 256);
-  }
   if (MODE >= 2) {
     const int r = tid >> 2, c = (tid & 3) ^ ((r >> 2) & 3);
     const char* base = reinterpret_cast<const char*>(a.qfeat + (hT + q0) * kTokRow);
@@ -898,9 +939,10 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
 }
 
 template <int MODE>
-__device__ __forceinline__ void dkv_issue(const AttnArgs& a, int h, int64_t hT, int64_t q0, DkvBuf<MODE>& b, int tid) {
+__device__ __forceinline__ void dkv_issue(const AttnArgs& a, int h, int64_t hT, int64_t q0, const float* rof,
+                                          DkvBuf<MODE>& b, int tid) {
 #pragma unroll
-  for (int part = 0; part < 10; ++part) dkv_issue_part<MODE>(a, h, hT, q0, b, tid, part);
+  for (int part = 0; part < 10; ++part) dkv_issue_part<MODE>(a, h, hT, q0, rof, b, tid, part);
 }
 
 // P and dS of register quad (mq, rq) of one tile as bf16 B operands (k index:
@@ -976,22 +1018,10 @@ __device__ __forceinline__ void dkv_probs_quad(const AttnArgs& a, const DkvBuf<M
 template <int MODE>
 __device__ __forceinline__ void dkv_offsets(const AttnArgs& a, const DkvBuf<MODE>& b, float* offw, const float* tab,
                                             float eb, int lane) {
+  static_assert(MODE >= 2, "modes 0/1 read the offsets the q-major pass stored");
   const float l = b.ra[lane];
   float c = 0.f;
-  if (MODE == 1) {
-    if (a.K == 8) {
-      const float4* cr = reinterpret_cast<const float4*>(b.rb + lane * 8);
-      const float4* sr = reinterpret_cast<const float4*>(b.rb + 512 + lane * 8);
-      const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
-      c = c0.x * tab[0] + c0.y * tab[1] + c0.z * tab[2] + c0.w * tab[3] + c1.x * tab[4] + c1.y * tab[5] +
-          c1.z * tab[6] + c1.w * tab[7] + s0.x * tab[8] + s0.y * tab[9] + s0.z * tab[10] + s0.w * tab[11] +
-          s1.x * tab[12] + s1.y * tab[13] + s1.z * tab[14] + s1.w * tab[15];
-    } else {
-      for (int k = 0; k < a.K; ++k) c += b.rb[lane * a.K + k] * tab[k] + b.rb[512 + lane * a.K + k] * tab[8 + k];
-    }
-    c *= a.beta_log2;
-  }
-  if (MODE >= 2 && a.subtract_b0) c = -a.beta_log2 * b.ra[192 + lane];
+  if (a.subtract_b0) c = -a.beta_log2 * b.ra[192 + lane];
   offw[lane] = l == -INFINITY ? -INFINITY : c + eb - l * kLog2e;
 }
 
@@ -1175,7 +1205,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   }
   if (n_it > 0) {
     const int64_t q0 = static_cast<int64_t>(qb_first) * BS + (skip0 % NS) * BM;
-    dkv_issue<MODE>(a, h, hT, q0, buf0, tid);
+    dkv_issue<MODE>(a, h, hT, q0, nullptr, buf0, tid);
   }
 
   uint4 kreg[8], vreg[8];
@@ -1219,8 +1249,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
         int e, en;
         if (jj + 1 < n_it) {
           const int64_t qn = tile_q0(jj + 1, en);
-          if (half == 0) dkv_issue<MODE>(a, h, hT, qn, buf1, tid);
-          else dkv_issue<MODE>(a, h, hT, qn, buf0, tid);
+          if (half == 0) dkv_issue<MODE>(a, h, hT, qn, nullptr, buf1, tid);
+          else dkv_issue<MODE>(a, h, hT, qn, nullptr, buf0, tid);
         }
         const int64_t q0 = tile_q0(jj, e);
         const float* tab = tabs + (MODE == 1 ? e * 16 : 0);
@@ -1371,12 +1401,10 @@ __device__ __forceinline__ uint4 lds_row16(const uint16_t* tile, const TileOffs1
 // With DP, the tile's dS values are added to this lane's running sum dacc
 // (reduced over the wavefront once per list entry by the caller).
 template <int MODE, bool DP>
-__device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, float* offw,
-                                        const float* tab, float eb, int q0, int lane, int wkv, int doc_kv,
-                                        const uint4 (&kreg)[4], const uint4 (&vreg)[4], const TileOffs16& to,
-                                        uint4 (&pb)[2], uint4 (&dsb)[2], float& dacc) {
+__device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, int q0, int lane,
+                                        int wkv, int doc_kv, const uint4 (&kreg)[4], const uint4 (&vreg)[4],
+                                        const TileOffs16& to, uint4 (&pb)[2], uint4 (&dsb)[2], float& dacc) {
   const int g = lane >> 4;
-  dkv_offsets<MODE>(a, b, offw, tab, eb, lane);
   f32x4_t s[4], dp[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
@@ -1404,10 +1432,11 @@ __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
+  // the tile's softmax offsets (block term, pair bias and lse per row) are in b.ra[0..63]
   if (masked)
-    dkv16_probs<MODE, true, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
+    dkv16_probs<MODE, true, DP>(b, b.ra, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
   else
-    dkv16_probs<MODE, false, DP>(b, offw, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
+    dkv16_probs<MODE, false, DP>(b, b.ra, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
 }
 
 // Second part: dV^T += dO^T P, dK^T += Q^T dS (step st = 8·kk + md).
@@ -1444,10 +1473,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   constexpr int NS = BS / BM;
 
   __shared__ DkvBuf<MODE> buf0, buf1, buf2;
-  __shared__ __attribute__((aligned(16))) float offw[8][BM];
-  __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunk * 16 : 4];
   __shared__ int qbs[kChunk], dse[kChunk], epos[kChunk];
-  __shared__ float ebias[kChunk];
   __shared__ float pslot[kChunk][8];  // pair-bias gradient: per entry and wavefront
 
   constexpr int P = BS / 128;  // workgroups (128 keys each) per key block
@@ -1493,23 +1519,19 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     const int qb = ql[i0 + tid];
     qbs[tid] = qb;
     dse[tid] = a.ds_tok_end[qb];
-    float eb = 0.f;
-    int pos = -1;
-    if (pl.q_pos) {
-      pos = pl.q_pos[static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb] + i0 + tid];
-      if (a.pair_bias && pos >= 0) eb = a.pair_bias[(static_cast<int64_t>(h) * a.QB + qb) * a.maxkv + pos] * kLog2e;
-    }
-    ebias[tid] = eb;
-    epos[tid] = pos;
+    // position of kb in this q-block's list: its offsets rows in roff
+    epos[tid] = pl.q_pos[static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb] + i0 + tid];
   }
   for (int t = tid; DP && t < kChunk * 8; t += blockDim.x) pslot[t / 8][t % 8] = 0.f;
-  for (int t = tid; MODE == 1 && t < ne * 16; t += blockDim.x) {
-    const int r = min(max(ql[i0 + t / 16] - kb, 0), NB - 1);
-    tabs[t] = static_cast<const float*>(a.table)[static_cast<int64_t>(r) * 16 + t % 16];
-  }
+  __syncthreads();  // qbs, epos
+  // the offsets of tile j (q-block qbs[e], rows (f % NS)·64 .. +63 of the list entry)
+  auto tile_rof = [&](int j) __attribute__((always_inline)) {
+    const int f = j + skip0, e = f / NS;
+    return a.roff + ((static_cast<int64_t>(h) * a.QB + qbs[e]) * a.maxkv + epos[e]) * BS + (f % NS) * BM;
+  };
   if (n_it > 0 && wave < 4) {
     const int64_t q0 = static_cast<int64_t>(qb_first) * BS + (skip0 % NS) * BM;
-    dkv_issue<MODE>(a, h, hT, q0, buf0, tid);
+    dkv_issue<MODE>(a, h, hT, q0, tile_rof(0), buf0, tid);
   }
 
   uint4 kreg[4], vreg[4];
@@ -1566,9 +1588,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
       dcur = e;
     }
     const bool masked = !((wkv_lo + 15 <= q0) && (dse[e] <= wkv_lo));
-    const float* tab = tabs + (MODE == 1 ? e * 16 : 0);
-    dkv16_a<MODE, DP>(a, bc, masked, offw[wave], tab, ebias[e], q0, lane, wkv, doc_kv, kreg, vreg, to, pb, dsb,
-                      dacc);
+    dkv16_a<MODE, DP>(a, bc, masked, q0, lane, wkv, doc_kv, kreg, vreg, to, pb, dsb, dacc);
     return true;
   };
   if (wave < 4) {
@@ -1578,7 +1598,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
       __syncthreads();  // tile j is in bc for everyone; the lagging group is done with bn
       if (j + 1 < n_it) {
         int en;
-        dkv_issue<MODE>(a, h, hT, tile_q0(j + 1, en), bn, tid);
+        dkv_issue<MODE>(a, h, hT, tile_q0(j + 1, en), tile_rof(j + 1), bn, tid);
       }
       uint4 pb[2], dsb[2];
       if (part_a(bc, j, pb, dsb)) dkv16_b<MODE>(bc, to, pb, dsb, dvT, dkT);
@@ -1727,7 +1747,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) 
 }
 
 struct BwdLayout {
-  int64_t delta, qfeat, items, slots, multi, part_dk, part_dv, q_pos, dpair, total, max_slots;
+  int64_t delta, qfeat, items, slots, multi, part_dk, part_dv, q_pos, roff, dpair, total, max_slots;
   int max_items;
 };
 
@@ -1755,7 +1775,11 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
   L.part_dv = o;
   o += al(part);
   L.q_pos = o;
-  if (p->pair_bias || p->dpair_bias) o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * 4);
+  if (p->pair_bias || p->dpair_bias || p->bias_mode != SCOPE_BIAS_TOKEN)
+    o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * 4);
+  // per-(h, qb, entry, row) softmax offsets of modes 0/1
+  L.roff = o;
+  if (p->bias_mode != SCOPE_BIAS_TOKEN) o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * p->bs * 4);
   // pair-bias gradient partials, one per 128-key part of a key block
   L.dpair = o;
   if (p->dpair_bias) o += al(static_cast<int64_t>(p->bs / 128) * p->H * QB * p->maxkv * 4);
@@ -1915,7 +1939,10 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   pl.multi = reinterpret_cast<const int32_t*>(ws + L.multi);
   pl.part_dk = reinterpret_cast<float*>(ws + L.part_dk);
   pl.part_dv = reinterpret_cast<float*>(ws + L.part_dv);
-  pl.q_pos = (p->pair_bias || p->dpair_bias) ? reinterpret_cast<const int32_t*>(ws + L.q_pos) : nullptr;
+  pl.q_pos = (p->pair_bias || p->dpair_bias || p->bias_mode != SCOPE_BIAS_TOKEN)
+                 ? reinterpret_cast<const int32_t*>(ws + L.q_pos)
+                 : nullptr;
+  a.roff = p->bias_mode != SCOPE_BIAS_TOKEN ? reinterpret_cast<float*>(ws + L.roff) : nullptr;
   pl.max_slots = L.max_slots;
   pl.max_items = L.max_items;
   hipStream_t s = as_stream(stream);

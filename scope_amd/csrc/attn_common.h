@@ -296,6 +296,10 @@ struct AttnArgs {
   float* mass;       // block mass [H,QB,NB] (forward mass pass)
   const float* pair_bias;  // per-list-entry score bias [H,QB,maxkv] (natural log) or null
   float* dpair;            // backward: tile sums of dS per (key-block part, h, qb, entry) [P][H][QB][maxkv] or null
+  // backward, no bias or block bias: the log2-domain softmax offset of every
+  // (h, qb, list entry, row), [H][QB][maxkv][bs] = block term + pair bias -
+  // lse·log2e, written by the q-major pass and read per tile by the kv-major pass
+  float* roff;
   int H, QB, maxkv, K;
   int64_t T;
   int64_t q_sh, q_st, k_sh, k_st, v_sh, v_st, o_sh, o_st;
