@@ -392,7 +392,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const float dd_err = rs_tot;  // Δ_true - Δ
   // the kv-major pass reads Δ_true = Δ + (Δ_true - Δ): its dS, dK and the
   // pair-bias sums then do not carry the bf16 rounding of the output
-  if (g == 0) a.delta[hT + R.row] = R.delta + dd_err;
+  if (g == 0) a.delta[hT + R.row] = -(R.delta + dd_err);  // stored negated: the kv-major dP accumulators start from it
   uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
@@ -750,7 +750,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   const float dd_err = rs_tot;  // Δ_true - Δ
   // the kv-major pass reads Δ_true = Δ + (Δ_true - Δ): its dS, dK and the
   // pair-bias sums then do not carry the bf16 rounding of the output
-  if (g == 0) a.delta[hT + R.row] = R.delta + dd_err;
+  if (g == 0) a.delta[hT + R.row] = -(R.delta + dd_err);  // stored negated: the kv-major dP accumulators start from it
   uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
@@ -995,7 +995,7 @@ __device__ __forceinline__ void dkv_probs_quad(const AttnArgs& a, const DkvBuf<M
     if (MASK) xv = mask_score(xv, wkv, q, doc_kv, dcv[i2]);
     const float p = __builtin_amdgcn_exp2f(xv);
     pv[i2] = p;
-    dsv[i2] = p * (dp[mq][r] - dlv[i2]);
+    dsv[i2] = p * (dp[mq][r] + dlv[i2]);  // dlv holds -Δ
     if (DP) dsum += dsv[i2];
   }
   const int ksx = 2 * mq + rq / 2;
@@ -1333,9 +1333,7 @@ __device__ __forceinline__ void dkv16_probs(const DkvBuf<MODE>& b, const float* 
   for (int mb = 0; mb < 4; ++mb) {
     const int qi0 = 16 * mb + 4 * g;  // rows qi0 .. qi0+3 of the tile
     const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
-    const float4 dl4 = *reinterpret_cast<const float4*>(&b.ra[64 + qi0]);
     const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
-    const float dlv[4] = {dl4.x, dl4.y, dl4.z, dl4.w};
     int dcv[4] = {0, 0, 0, 0};
     if (MASK) {
       const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
@@ -1348,7 +1346,7 @@ __device__ __forceinline__ void dkv16_probs(const DkvBuf<MODE>& b, const float* 
       if (MASK) x = mask_score(x, wkv, q0 + qi0 + i, doc_kv, dcv[i]);
       const float p = __builtin_amdgcn_exp2f(x);
       pv[i] = p;
-      dv[i] = p * (dp[mb][i] - dlv[i]);
+      dv[i] = p * dp[mb][i];  // the dP accumulator started from -Δ
       if (DP) dsum += dv[i];
     }
     pw[2 * mb] = cvt_pk_bf16(pv[0], pv[1]);
@@ -1409,7 +1407,8 @@ __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     s[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    dp[mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // dP - Δ: the accumulator of rows 16mb + 4g .. +3 starts from their -Δ (stored negated)
+    dp[mb] = *reinterpret_cast<const f32x4_t*>(&b.ra[64 + 16 * mb + 4 * g]);
   }
   // step st = 4·ks + mb; operands read RA steps ahead into a ring
   constexpr int RA = 2;
