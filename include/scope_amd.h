@@ -218,6 +218,32 @@ int scope_coeff_head_bwd(const scope_coeff_params* p, const void* y, const float
                          void* dy, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Weight and bias gradients of the head's MLP layers.  Replaces autograd's
+ * weight-gradient GEMM and bias-gradient reduction of the shared
+ * Linear(D, 2D) -> SiLU -> Linear(2D, 5M+1) (model/attn_bias.py:271-276,
+ * applied at :380-398 to every (b, h, t) row), whose contraction runs over
+ * all rows:  dw[m][n] = Σ_r a[r][m]·b[r][n],  db[m] = Σ_r a[r][m]
+ * with a the layer's output gradient and b its input, both bf16.  Row r is
+ * row r % seg of segment r / seg: a + (r / seg)·a_ss + (r % seg)·a_rs
+ * (elements), likewise b.  rows and seg are multiples of 64; (M, N) is
+ * (64, 128), (64, 256), (128, 128), (128, 256), (256, 64) or (256, 128).
+ * dw [M][N] and db [M] (db may be NULL) are fp32, each rounded to bf16
+ * first when round_bf16 (the gradient of a bf16 copy of an fp32 weight).
+ * Sums run in a fixed order (no atomics).  workspace:
+ * scope_linear_wgrad_workspace_bytes.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int64_t rows, seg;
+  int M, N;
+  int64_t a_ss, a_rs, b_ss, b_rs;
+  int round_bf16;
+} scope_wgrad_params;
+
+int64_t scope_linear_wgrad_workspace_bytes(const scope_wgrad_params* p);
+int scope_linear_wgrad(const scope_wgrad_params* p, const uint16_t* a, const uint16_t* b, float* dw, float* db,
+                       void* workspace, void* stream);
+
+/* ------------------------------------------------------------------------
  * Sliding-window block masks of the layers without the pointer mask.
  * Replaces GPT.create_blockmasks (scoped_medium.py:535-576): the long (W)
  * and short (W // 2) masks of a window of W blocks.

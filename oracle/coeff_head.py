@@ -1,12 +1,15 @@
 """Oracle: the coefficient head of ``SpectralBias.forward`` in torch ops.
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  The product runs the
-MLP in torch and the rest in the fused HIP kernels (``scope_coeff_head_fwd`` /
-``scope_coeff_head_bwd``); this restates the reference's steps one tensor op
-at a time, so autograd gives the reference's gradients.
+MLP's GEMMs in torch with its weight and bias gradients on a HIP kernel
+(``scope_linear_wgrad``), and the rest in the fused HIP kernels
+(``scope_coeff_head_fwd`` / ``scope_coeff_head_bwd``); this restates the
+reference's steps one tensor op at a time, so autograd gives the reference's
+gradients.
 
 Restates ``model/attn_bias.py:379-506``:
 
+* the MLP, SiLU between two linear layers (``:380-398``, ``mlp_forward``);
 * the MLP output y = [delta_raw | mu_raw | sigma_raw | pi_logits |
   budget_logits | c_raw] (``:419-431``);
 * Δ* = σ(delta_raw)·clamp(Δ*max, 0, L-1) (``:438-440``), μ, σ, π = softmax,
@@ -33,6 +36,21 @@ import torch
 import torch.nn.functional as F
 
 
+def mlp_forward(sb, q: torch.Tensor) -> torch.Tensor:
+    """The head's MLP (model/attn_bias.py:380-398): SiLU between two linear
+    layers, shared across heads or per head, with the weights cast to q's
+    dtype."""
+    if sb.detach_q:
+        q = q.detach()
+    dt = q.dtype
+    if sb.share_across_heads:
+        fc1, fc2 = sb.mlp[0], sb.mlp[2]
+        x = F.silu(F.linear(q, fc1.weight.to(dt), fc1.bias.to(dt)))
+        return F.linear(x, fc2.weight.to(dt), fc2.bias.to(dt))
+    x = F.silu(torch.einsum("bhld,hkd->bhlk", q, sb.w1.to(dt)) + sb.b1.to(dt)[None, :, None, :])
+    return torch.einsum("bhlk,hok->bhlo", x, sb.w2.to(dt)) + sb.b2.to(dt)[None, :, None, :]
+
+
 def coeff_head_forward(sb, q: torch.Tensor) -> tuple[torch.Tensor, ...]:
     """The reference's 12-tuple (model/attn_bias.py:385-401) for q [B,H,L,D]
     from the parameters and schedule buffers of ``sb`` (a
@@ -54,7 +72,7 @@ def coeff_head_forward(sb, q: torch.Tensor) -> tuple[torch.Tensor, ...]:
         z_m = q.new_zeros((B, H, L, sb.M), dtype=torch.float32)
         z_pi = q.new_full((B, H, L, sb.M), 1.0 / sb.M, dtype=torch.float32)
         return z_k, z_k, z_l, z_l, z_m, z_pi, z_m, z_l, z_l, cos_wD, sin_wD, q.new_zeros((), dtype=torch.float32)
-    y = sb._mlp_forward(q).float()
+    y = mlp_forward(sb, q).float()
     M, K = sb.M, sb.K
     delta_raw, mu_raw, sigma_raw, pi_logits, budget_logits = (y[..., i * M:(i + 1) * M] for i in range(5))
     delta_cap = torch.clamp(sb._delta_star_max_active.to(device=device, dtype=torch.float32), 0.0, float(L - 1))

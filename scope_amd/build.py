@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "libscope_amd.so")
 ARCH = os.environ.get("SCOPE_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["api.hip", "pointer.hip", "transpose.hip", "stats.hip", "swa.hip", "coeff.hip", "decode.hip",
-           "attn_fwd.hip", "attn_bwd.hip", "probe.hip"]
+           "attn_fwd.hip", "attn_bwd.hip", "mlp.hip", "probe.hip"]
 # integer/selection kernels must round exactly like the reference's fp32 tensor ops
 NO_CONTRACT = {"pointer.hip", "stats.hip"}
 

@@ -1,0 +1,246 @@
+// Weight and bias gradients of a linear layer over many rows, for the MLP of
+// SpectralBias (model/attn_bias.py:271-276, 380-398: Linear(D, 2D) -> SiLU
+// -> Linear(2D, 5M+1), shared across heads and applied to every (b, h, t)
+// row).  Autograd's weight gradient of such a layer is a GEMM whose
+// contraction runs over all B·H·T rows (131072 at T = 16384, H = 8):
+//   dW[m][n] = Σ_r A[r][m] B[r][n],   db[m] = Σ_r A[r][m]
+// with A the output gradient and B the layer input.  The contraction is
+// split over workgroups, each summing a contiguous run of 64-row chunks on
+// bf16 MFMAs into fp32 partials, which a second kernel adds in workgroup
+// order (no atomics: the result does not depend on scheduling).
+//
+// Operands: both chunks are copied into swizzled LDS tiles (rows of 128
+// columns) by global_load_lds; the MFMA operands of A^T and of B run along
+// rows (the contraction index), so both come from transpose reads
+// (lds_kmajor_o).  For v_mfma_f32_32x32x16_bf16 with A^T as the A operand
+// and B as the B operand, the accumulator of block (mb, nb) holds
+// dW[32·mb + 8(r/4) + 4g + r%4][32·nb + lane % 32] in register r.
+#include <math.h>
+
+#include "attn_common.h"
+
+namespace scope {
+
+namespace {
+
+constexpr int kWgradThreads = 256;
+constexpr int kWgradMaxGroups = 256;
+constexpr int kChunkRows = 64;
+
+struct WgradArgs {
+  const uint16_t* a;
+  const uint16_t* b;
+  int64_t rows, seg;  // rows summed over; rows per segment (row r = segment r / seg, row r % seg)
+  int64_t a_ss, a_rs, b_ss, b_rs;
+  float* part;        // [groups][M·N + M]
+  int chunks_per_group;
+};
+
+// Copy rows r0 .. r0+63 of an operand with C columns (64, 128 or 256) into
+// C/128 swizzled tiles (a 64-column operand fills the left half of one).
+template <int C>
+__device__ __forceinline__ void wgrad_copy(const uint16_t* x, int64_t ss, int64_t rs, int64_t seg, int64_t r0,
+                                           uint16_t* tiles, int tid) {
+  constexpr int NTILE = C < 128 ? 1 : C / 128;
+  const int64_t s = r0 / seg, t0 = r0 % seg;  // a chunk never spans segments (seg % 64 == 0)
+  const uint16_t* base = x + s * ss + t0 * rs;
+  const int wave = tid >> 6;
+#pragma unroll
+  for (int tl = 0; tl < NTILE; ++tl) {
+#pragma unroll
+    for (int jj = 0; jj < 1024 / kWgradThreads; ++jj) {
+      // physical 16-byte slot idx of the tile: row idx/16, holding logical chunk (idx%16) ^ swz(row)
+      const int idx = jj * kWgradThreads + tid;
+      const int r = idx >> 4, c = (idx & 15) ^ swz(r);
+      uint16_t* dst = tiles + tl * (64 * 128) + (jj * kWgradThreads + wave * 64) * 8;
+      const uint32_t off = static_cast<uint32_t>((r * rs + tl * 128 + c * 8) * 2);
+      if (C >= 128 || c < C / 8) g2lds16(base, off, dst);
+    }
+  }
+}
+
+// Which accumulator blocks a wavefront owns: the four wavefronts split the
+// MB x NB grid of 32x32 blocks by m blocks (MB % 4 == 0), else by n blocks
+// (NB % 4 == 0), else two by two.
+template <int MB, int NB>
+struct WgradSplit {
+  static constexpr bool BY_M = MB % 4 == 0;
+  static constexpr bool BY_N = !BY_M && NB % 4 == 0;
+  static constexpr int WM = BY_M ? MB / 4 : (BY_N ? MB : MB / 2);  // m blocks per wavefront
+  static constexpr int WN = BY_M ? NB : (BY_N ? NB / 4 : NB / 2);  // n blocks per wavefront
+  __device__ static int mb(int wave, int i) { return BY_M ? wave + 4 * i : (BY_N ? i : (wave / 2) * WM + i); }
+  __device__ static int nb(int wave, int j) { return BY_M ? j : (BY_N ? wave + 4 * j : (wave % 2) * WN + j); }
+  // the column sums of A are taken by the wavefronts that own n block 0
+  __device__ static bool colsum(int wave) { return BY_M ? true : (BY_N ? wave == 0 : wave % 2 == 0); }
+};
+
+template <int MB, int NB>
+__global__ __launch_bounds__(kWgradThreads) void wgrad_kernel(WgradArgs g) {
+  constexpr int M = 32 * MB, N = 32 * NB;
+  constexpr int TA = M < 128 ? 1 : M / 128, TB = N < 128 ? 1 : N / 128;
+  using S = WgradSplit<MB, NB>;
+  static_assert(S::WM * S::WN <= 8, "wgrad_kernel: at most 8 accumulator blocks per wavefront");
+  __shared__ __attribute__((aligned(16))) uint16_t sa[2][TA * 64 * 128];
+  __shared__ __attribute__((aligned(16))) uint16_t sb[2][TB * 64 * 128];
+
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const int64_t chunks = g.rows / kChunkRows;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * g.chunks_per_group;
+  const int64_t c1 = c0 + g.chunks_per_group < chunks ? c0 + g.chunks_per_group : chunks;
+  const TileOffs to = tile_offs(lane);
+
+  f32x16_t acc[S::WM][S::WN];
+#pragma unroll
+  for (int i = 0; i < S::WM; ++i)
+#pragma unroll
+    for (int j = 0; j < S::WN; ++j) acc[i][j] = zero16();
+  float cs[S::WM];
+#pragma unroll
+  for (int i = 0; i < S::WM; ++i) cs[i] = 0.f;
+  const bool do_cs = S::colsum(wave);
+
+  auto issue = [&](int64_t c, int buf) __attribute__((always_inline)) {
+    wgrad_copy<M>(g.a, g.a_ss, g.a_rs, g.seg, c * kChunkRows, sa[buf], tid);
+    wgrad_copy<N>(g.b, g.b_ss, g.b_rs, g.seg, c * kChunkRows, sb[buf], tid);
+  };
+  if (c0 < c1) issue(c0, 0);
+  for (int64_t c = c0; c < c1; ++c) {
+    const int buf = static_cast<int>((c - c0) & 1);
+    wait_vm0();
+    __syncthreads();  // chunk c is in buffer buf; every wavefront is done with the other buffer
+    if (c + 1 < c1) issue(c + 1, buf ^ 1);
+#pragma unroll
+    for (int ks = 0; ks < kChunkRows / 16; ++ks) {
+      uint4 av[S::WM], bv[S::WN];
+#pragma unroll
+      for (int i = 0; i < S::WM; ++i) {
+        const int mb = S::mb(wave, i);
+        av[i] = lds_kmajor_o(sa[buf] + (mb / 4) * (64 * 128), to, 16 * ks, mb % 4);
+      }
+#pragma unroll
+      for (int j = 0; j < S::WN; ++j) {
+        const int nb = S::nb(wave, j);
+        bv[j] = lds_kmajor_o(sb[buf] + (nb / 4) * (64 * 128), to, 16 * ks, nb % 4);
+      }
+#pragma unroll
+      for (int i = 0; i < S::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < S::WN; ++j) acc[i][j] = mfma32(av[i], bv[j], acc[i][j]);
+      if (do_cs) {
+#pragma unroll
+        for (int i = 0; i < S::WM; ++i) {
+          const uint32_t w4[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) cs[i] += bf16_lo(w4[q]) + bf16_hi(w4[q]);
+        }
+      }
+    }
+  }
+  wait_vm0();  // no copy may still target LDS when the workgroup exits
+
+  // partials of this workgroup: dW block rows as above, then the column sums
+  float* part = g.part + static_cast<int64_t>(blockIdx.x) * (M * N + M);
+  const int gq = lane / 32, c = lane % 32;
+#pragma unroll
+  for (int i = 0; i < S::WM; ++i) {
+    const int mb = S::mb(wave, i);
+#pragma unroll
+    for (int j = 0; j < S::WN; ++j) {
+      const int nb = S::nb(wave, j);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = 32 * mb + 8 * (r / 4) + 4 * gq + (r % 4);
+        part[m * N + 32 * nb + c] = acc[i][j][r];
+      }
+    }
+    if (do_cs) {
+      // lanes l and l ^ 32 hold different rows of the same column
+      const float t = cs[i] + __shfl_xor(cs[i], 32, 64);
+      if (gq == 0) part[M * N + 32 * mb + c] = t;
+    }
+  }
+}
+
+__device__ __forceinline__ float round_bf16(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
+
+// dw[m][n] (then db[m]) = the sum over workgroups, in workgroup order.
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, int groups, int MN, int M,
+                                                           int rnd, float* __restrict__ dw, float* __restrict__ db) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= MN + M || (i >= MN && !db)) return;
+  const int stride = MN + M;
+  float t = 0.f;
+  for (int w = 0; w < groups; ++w) t += part[static_cast<int64_t>(w) * stride + i];
+  if (rnd) t = round_bf16(t);
+  if (i < MN)
+    dw[i] = t;
+  else
+    db[i - MN] = t;
+}
+
+int wgrad_groups(const scope_wgrad_params* p) {
+  const int64_t chunks = p->rows / kChunkRows;
+  return static_cast<int>(chunks < kWgradMaxGroups ? chunks : kWgradMaxGroups);
+}
+
+template <int MB, int NB>
+void launch_wgrad(const WgradArgs& g, int groups, hipStream_t s) {
+  hipLaunchKernelGGL((wgrad_kernel<MB, NB>), dim3(groups), dim3(kWgradThreads), 0, s, g);
+}
+
+}  // namespace
+
+}  // namespace scope
+
+using namespace scope;
+
+extern "C" int64_t scope_linear_wgrad_workspace_bytes(const scope_wgrad_params* p) {
+  if (!p || p->rows <= 0 || p->M <= 0 || p->N <= 0) return 0;
+  return static_cast<int64_t>(wgrad_groups(p)) * (static_cast<int64_t>(p->M) * p->N + p->M) * 4;
+}
+
+extern "C" int scope_linear_wgrad(const scope_wgrad_params* p, const uint16_t* a, const uint16_t* b, float* dw,
+                                  float* db, void* workspace, void* stream) {
+  SCOPE_REQUIRE(p && a && b && dw && workspace, "scope_linear_wgrad: null pointer");
+  const int M = p->M, N = p->N;
+  const bool shape_ok = (M == 64 && (N == 128 || N == 256)) || (M == 128 && (N == 128 || N == 256)) ||
+                        (M == 256 && (N == 64 || N == 128));
+  SCOPE_REQUIRE(shape_ok, "scope_linear_wgrad: (M, N) = (%d, %d) not supported (64, 128 or 256 with M·N <= 32768)",
+                M, N);
+  SCOPE_REQUIRE(p->rows > 0 && p->rows % kChunkRows == 0, "scope_linear_wgrad: rows=%lld must be a positive multiple of %d",
+                (long long)p->rows, kChunkRows);
+  SCOPE_REQUIRE(p->seg > 0 && p->seg % kChunkRows == 0 && p->rows % p->seg == 0,
+                "scope_linear_wgrad: seg=%lld must be a multiple of %d dividing rows", (long long)p->seg, kChunkRows);
+  SCOPE_REQUIRE(p->a_rs >= M && p->b_rs >= N && p->a_rs % 8 == 0 && p->b_rs % 8 == 0 && p->a_ss % 8 == 0 &&
+                    p->b_ss % 8 == 0 && p->a_ss >= 0 && p->b_ss >= 0,
+                "scope_linear_wgrad: row strides must cover the row and all strides be multiples of 8 elements");
+  // each chunk's lane offsets are 32-bit byte offsets from the chunk's first row
+  SCOPE_REQUIRE(p->a_rs < (1 << 24) && p->b_rs < (1 << 24), "scope_linear_wgrad: row strides must be below 2^24");
+  SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                  reinterpret_cast<uintptr_t>(workspace)) & 15) == 0,
+                "scope_linear_wgrad: a, b and workspace must start on a 16-byte boundary");
+  const int groups = wgrad_groups(p);
+  const int64_t chunks = p->rows / kChunkRows;
+  WgradArgs g;
+  g.a = a;
+  g.b = b;
+  g.rows = p->rows;
+  g.seg = p->seg;
+  g.a_ss = p->a_ss;
+  g.a_rs = p->a_rs;
+  g.b_ss = p->b_ss;
+  g.b_rs = p->b_rs;
+  g.part = static_cast<float*>(workspace);
+  g.chunks_per_group = static_cast<int>((chunks + groups - 1) / groups);
+  hipStream_t s = as_stream(stream);
+  if (M == 64 && N == 128) launch_wgrad<2, 4>(g, groups, s);
+  else if (M == 64) launch_wgrad<2, 8>(g, groups, s);
+  else if (M == 128 && N == 128) launch_wgrad<4, 4>(g, groups, s);
+  else if (M == 128) launch_wgrad<4, 8>(g, groups, s);
+  else if (N == 64) launch_wgrad<8, 2>(g, groups, s);
+  else launch_wgrad<8, 4>(g, groups, s);
+  const int total = M * N + M;
+  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((total + 255) / 256), dim3(256), 0, s, g.part, groups, M * N, M,
+                     p->round_bf16, dw, db);
+  return check_launch("linear weight gradient kernels");
+}

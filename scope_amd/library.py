@@ -26,7 +26,10 @@ Operators (schemas are the decorated signatures below):
   calls (scoped_medium.py:422, 459-466, 470-476) with the spectral score_mod;
 * ``scope::coeff_head_fwd`` (+ autograd via ``scope::coeff_head_bwd``) — the
   coefficient head of SpectralBias.forward after its MLP (model/attn_bias.py:
-  419-506).
+  419-506);
+* ``scope::coeff_mlp`` (+ autograd whose weight and bias gradients run on
+  ``scope::linear_wgrad``) — the head's shared MLP (model/attn_bias.py:271-276,
+  380-386).
 
 Optional outputs that an operator cannot return as None (a gradient that is
 not asked for) are returned as empty tensors.
@@ -34,6 +37,7 @@ not asked for) are returned as empty tensors.
 from typing import Optional, Sequence
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 
 from . import ops
@@ -456,3 +460,81 @@ def _head_backward(ctx, *g):
 
 
 coeff_head_fwd.register_autograd(_head_backward, setup_context=_head_setup)
+
+
+# ---------------------------------------------------------------------------
+# The head's MLP (model/attn_bias.py:271-276, applied at :380-398)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op(f"{_NS}::linear_wgrad", mutates_args=())
+def linear_wgrad(a: Tensor, b: Tensor, round_bf16: bool) -> tuple[Tensor, Tensor]:
+    """dw [M, N] = Σ_r a[r]^T b[r], db [M] = Σ_r a[r] over the bf16 rows of
+    a [..., M] and b [..., N] (fp32, rounded to bf16 with ``round_bf16``)."""
+    return ops.linear_wgrad(a, b, round_bf16=round_bf16)
+
+
+@linear_wgrad.register_fake
+def _(a, b, round_bf16):
+    return a.new_empty((a.shape[-1], b.shape[-1]), dtype=_F32), a.new_empty(a.shape[-1], dtype=_F32)
+
+
+@torch.library.custom_op(f"{_NS}::coeff_mlp", mutates_args=())
+def coeff_mlp(q: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, b2: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """The head's shared MLP on q [..., D]: y = Linear(w2, b2)(SiLU(Linear(w1,
+    b1)(q))) with the weights cast to q's dtype (model/attn_bias.py:380-386),
+    and the pre-activation z1 and activation x1 that its backward reuses."""
+    ops._gpu("coeff_mlp", q, w1, b1, w2, b2)
+    dt = q.dtype
+    z1 = F.linear(q, w1.to(dt), b1.to(dt))
+    x1 = F.silu(z1)
+    return F.linear(x1, w2.to(dt), b2.to(dt)), z1, x1
+
+
+@coeff_mlp.register_fake
+def _(q, w1, b1, w2, b2):
+    lead = tuple(q.shape[:-1])
+    hid = lead + (w1.shape[0],)
+    return q.new_empty(lead + (w2.shape[0],)), q.new_empty(hid), q.new_empty(hid)
+
+
+def _mlp_setup(ctx, inputs, output):
+    q, w1, b1, w2, b2 = inputs
+    ctx.save_for_backward(q, w1, w2, output[1], output[2])
+    ctx.dtypes = (w1.dtype, b1.dtype, w2.dtype, b2.dtype)
+
+
+def _wgrad(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
+    """Weight and bias gradient of a linear layer (output gradient a, input b):
+    the split-row kernel for bf16, a plain product for other dtypes."""
+    if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16:
+        M = a.shape[-1]
+        Mp = 64 if M <= 64 else (128 if M <= 128 else 256)
+        if Mp != M:  # pad the output columns to a multiple the kernel takes
+            a = F.pad(a.reshape(-1, M), (0, Mp - M))
+        dw, db = linear_wgrad(a, b, True)
+        return dw[:M], db[:M]
+    a2, b2 = a.reshape(-1, a.shape[-1]), b.reshape(-1, b.shape[-1])
+    return a2.t().matmul(b2).float(), a2.sum(0).float()
+
+
+def _mlp_backward(ctx, gy, gz1, gx1):
+    """Autograd of the two F.linear and the SiLU (the reference's backward):
+    dx1 = gy·W2, dz1 = SiLU'(z1)·dx1, dq = dz1·W1 on the BLAS library; the
+    weight and bias gradients, whose contraction runs over all rows, on the
+    split-row kernel.  The weights' gradients are those of their bf16 copies
+    (rounded to bf16), in the weights' dtype."""
+    q, w1, w2, z1, x1 = ctx.saved_tensors
+    dt = q.dtype
+    dx1 = gy.to(dt).matmul(w2.to(dt))
+    if gx1 is not None:
+        dx1 = dx1 + gx1
+    dz1 = torch.ops.aten.silu_backward(dx1, z1)
+    if gz1 is not None:
+        dz1 = dz1 + gz1
+    dq = dz1.matmul(w1.to(dt)) if ctx.needs_input_grad[0] else None
+    dw2, db2 = _wgrad(gy.to(dt), x1)
+    dw1, db1 = _wgrad(dz1, q)
+    t1, tb1, t2, tb2 = ctx.dtypes
+    return dq, dw1.to(t1), db1.to(tb1), dw2.to(t2), db2.to(tb2)
+
+
+coeff_mlp.register_autograd(_mlp_backward, setup_context=_mlp_setup)

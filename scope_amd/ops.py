@@ -302,6 +302,66 @@ def coeff_head_fwd(y: torch.Tensor, prm: dict, omegas: torch.Tensor, log_omegas:
     return out
 
 
+def _row_layout(x: torch.Tensor):
+    """(rows, seg, segment stride, row stride) of x's rows (its last dimension
+    is the row, unit stride): a 2-D [R, C] tensor, or [..., S, T, C] with
+    size-1 leading dimensions (segments S of T rows, e.g. the heads of a
+    [1, H, T, D] view).  None when x has neither form."""
+    if x.stride(-1) != 1:
+        return None
+    shape, strides = list(x.shape[:-1]), list(x.stride()[:-1])
+    while len(shape) > 2 and shape[0] == 1:
+        shape.pop(0)
+        strides.pop(0)
+    if len(shape) == 1:
+        return shape[0], shape[0], 0, strides[0]
+    if len(shape) == 2:
+        return shape[0] * shape[1], shape[1], strides[0], strides[1]
+    return None
+
+
+def linear_wgrad(a: torch.Tensor, b: torch.Tensor, *, round_bf16: bool = True, want_db: bool = True):
+    """dw [M, N] = Σ_r a[r]^T b[r] and db [M] = Σ_r a[r] over the rows of a
+    [..., M] and b [..., N] (bf16, the same rows): the weight and bias
+    gradients of a linear layer with output gradient a and input b
+    (model/attn_bias.py:271-276; autograd of F.linear).  fp32 results,
+    rounded to bf16 first with ``round_bf16``; db is None without
+    ``want_db``."""
+    dev = _gpu("linear_wgrad", a, b)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise RuntimeError("linear_wgrad: a and b must be bf16")
+    M, N = a.shape[-1], b.shape[-1]
+    la, lb = _row_layout(a), _row_layout(b)
+    if la is None:
+        a = a.contiguous()
+        la = _row_layout(a)
+    if lb is None:
+        b = b.contiguous()
+        lb = _row_layout(b)
+    if la[0] != lb[0]:
+        raise RuntimeError(f"linear_wgrad: {la[0]} rows of a against {lb[0]} rows of b")
+    rows = la[0]
+    # one segment length for both: an operand with one row stride takes the other's segments
+    segs = {l[1] for l in (la, lb) if l[1] != rows}
+    if len(segs) > 1:
+        raise RuntimeError(f"linear_wgrad: segments of {sorted(segs)} rows in a and b")
+    seg = segs.pop() if segs else rows
+
+    def strides(l):
+        return (l[2], l[3]) if l[1] == seg else (seg * l[3], l[3])
+
+    a_ss, a_rs = strides(la)
+    b_ss, b_rs = strides(lb)
+    prm = _lib.WgradParams(rows=rows, seg=seg, M=M, N=N, a_ss=a_ss, a_rs=a_rs, b_ss=b_ss, b_rs=b_rs,
+                           round_bf16=int(bool(round_bf16)))
+    dw = torch.empty((M, N), dtype=torch.float32, device=dev)
+    db = torch.empty(M, dtype=torch.float32, device=dev) if want_db else None
+    ws = torch.empty(max(16, int(query("scope_linear_wgrad_workspace_bytes", C.byref(prm)))), dtype=torch.uint8,
+                     device=dev)
+    call("scope_linear_wgrad", C.byref(prm), _p(a), _p(b), _p(dw), _p(db), _p(ws), _stream(dev))
+    return dw, db
+
+
 def coeff_head_bwd(y: torch.Tensor, prm: dict, omegas: torch.Tensor, log_omegas: torch.Tensor,
                    cos_mean: torch.Tensor | None, sin_mean: torch.Tensor | None, grads: dict,
                    g_reg: torch.Tensor | None = None, reg: torch.Tensor | None = None) -> torch.Tensor:
