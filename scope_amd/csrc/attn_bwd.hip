@@ -723,28 +723,6 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     }
   }
 
-  // ---- this row's softmax offset for every listed key block (the block term
-  // as in the loop, plus the pair bias, minus lse), read per tile by the
-  // kv-major pass
-  if (g == 0) {
-    float* rof = a.roff + lrow * a.maxkv * BS + lrow_;
-    for (int e = 0; e < n; ++e) {
-      float t = pbias ? kbias[e] : 0.f;
-      if (MODE == 1) {
-        const int rd = min(max(qb - kb_at(e), 0), a.QB - 1);
-        const float4* t4 = reinterpret_cast<const float4*>(static_cast<const float*>(a.table) + rd * 16);
-        float acc[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 c4 = *reinterpret_cast<const float4*>(coef + row16_off(lrow_, i)), tt = t4[i];
-          acc[i] = c4.x * tt.x + c4.y * tt.y + c4.z * tt.z + c4.w * tt.w;
-        }
-        t += (acc[0] + acc[1]) + (acc[2] + acc[3]);
-      }
-      rof[e * BS] = t - R.lse2;
-    }
-  }
-
   // ---- epilogue: dQ = scale·o, coefficient gradients
   rs_tot += __shfl_xor(rs_tot, 32, 64);
   const float dd_err = rs_tot;  // Δ_true - Δ
@@ -768,6 +746,27 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
       const float rs = gacc[row32_off(lrow_, 4 * g + k / 4) + k % 4];
       const float pm = gacc[row32_off(lrow_, 4 * g + 2 + k / 4) + k % 4];
       dst[k] = a.beta * (rs - dd_err * pm);
+    }
+  }
+  // ---- this row's softmax offset for every listed key block (the block term
+  // as in the loop, plus the pair bias, minus lse), read per tile by the
+  // kv-major pass; after the dQ store, when its accumulators are free
+  if (g == 0) {
+    float* rof = a.roff + lrow * a.maxkv * BS + lrow_;
+    for (int e = 0; e < n; ++e) {
+      float t = pbias ? kbias[e] : 0.f;
+      if (MODE == 1) {
+        const int rd = min(max(qb - kb_at(e), 0), a.QB - 1);
+        const float4* t4 = reinterpret_cast<const float4*>(static_cast<const float*>(a.table) + rd * 16);
+        float acc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 c4 = *reinterpret_cast<const float4*>(coef + row16_off(lrow_, i)), tt = t4[i];
+          acc[i] = c4.x * tt.x + c4.y * tt.y + c4.z * tt.z + c4.w * tt.w;
+        }
+        t += (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      }
+      rof[e * BS] = t - R.lse2;
     }
   }
 }
@@ -1322,18 +1321,42 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
 // row order.
 
 // P and dS of one tile for this lane's key as the B operands of the
-// transposed products (pb[kk], dsb[kk]: k-step kk, see above).
+// transposed products (pb[kk], dsb[kk]: k-step kk, see above).  Modes 0/1:
+// the rows' softmax offsets are in b.ra[0..63].  Token modes: the offset
+// of a row is -β·b0 + the pair bias eb - lse (log2 units, b.ra: lse | Δ |
+// doc | b0), and each score adds the slope term β·slope·(i - j) and, with
+// the gate (mode 3), -β·λ·gate(|i - j - δ| - w).
 template <int MODE, bool MASK, bool DP>
-__device__ __forceinline__ void dkv16_probs(const DkvBuf<MODE>& b, const float* offw, float cs, int q0, int wkv,
-                                            int doc_kv, int g, const f32x4_t (&s)[4], const f32x4_t (&dp)[4],
-                                            uint4 (&pb)[2], uint4 (&dsb)[2], float& dsum) {
+__device__ __forceinline__ void dkv16_probs(const AttnArgs& a, const DkvBuf<MODE>& b, const float* offw, float eb,
+                                            float cs, int q0, int wkv, int doc_kv, int g, const f32x4_t (&s)[4],
+                                            const f32x4_t (&dp)[4], uint4 (&pb)[2], uint4 (&dsb)[2], float& dsum) {
+  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
   const int* docq = reinterpret_cast<const int*>(b.ra + 128);
   uint32_t pw[8], dw[8];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     const int qi0 = 16 * mb + 4 * g;  // rows qi0 .. qi0+3 of the tile
-    const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
-    const float ofv[4] = {of4.x, of4.y, of4.z, of4.w};
+    float ofv[4], slv[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (TOK) {
+      const float4 l4 = *reinterpret_cast<const float4*>(&b.ra[qi0]);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.subtract_b0) {
+        const float4 b4 = *reinterpret_cast<const float4*>(&b.ra[192 + qi0]);
+        bv[0] = b4.x, bv[1] = b4.y, bv[2] = b4.z, bv[3] = b4.w;
+      }
+      if (a.use_slope) {
+        const float4 s4 = *reinterpret_cast<const float4*>(&b.rc[qi0]);
+        slv[0] = s4.x * a.beta_log2, slv[1] = s4.y * a.beta_log2, slv[2] = s4.z * a.beta_log2,
+        slv[3] = s4.w * a.beta_log2;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ofv[i] = lv[i] == -INFINITY ? -INFINITY : fmaf(-a.beta_log2, bv[i], eb) - lv[i] * kLog2e;
+    } else {
+      const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
+      ofv[0] = of4.x, ofv[1] = of4.y, ofv[2] = of4.z, ofv[3] = of4.w;
+    }
     int dcv[4] = {0, 0, 0, 0};
     if (MASK) {
       const int4 dc4 = *reinterpret_cast<const int4*>(&docq[qi0]);
@@ -1342,7 +1365,21 @@ __device__ __forceinline__ void dkv16_probs(const DkvBuf<MODE>& b, const float* 
     float pv[4], dv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float x = fmaf(s[mb][i], cs, ofv[i]);
+      float x;
+      if constexpr (TOK) {
+        const float df = static_cast<float>(q0 + qi0 + i - wkv);
+        float e = slv[i] * df;
+        if constexpr (GATE) {
+          // softplus(x) = max(x,0) + ln2·log2(1 + 2^(-|x|·log2 e)); relu drops the second term
+          const float xx = (fabsf(df - b.rc[64 + qi0 + i]) - b.rc[128 + qi0 + i]) * a.inv_tau;
+          const float sp = __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e));
+          const float spw = a.gate_kind == SCOPE_GATE_SOFTPLUS ? kLn2 : 0.f;
+          e -= a.beta_log2 * a.ramp_lambda * fmaf(spw, sp, fmaxf(xx, 0.f));
+        }
+        x = fmaf(s[mb][i], cs, e + ofv[i]);
+      } else {
+        x = fmaf(s[mb][i], cs, ofv[i]);
+      }
       if (MASK) x = mask_score(x, wkv, q0 + qi0 + i, doc_kv, dcv[i]);
       const float p = __builtin_amdgcn_exp2f(x);
       pv[i] = p;
@@ -1398,10 +1435,15 @@ __device__ __forceinline__ uint4 lds_row16(const uint16_t* tile, const TileOffs1
 // per-row offsets, S and dP, then P and dS as bf16 B operands.
 // With DP, the tile's dS values are added to this lane's running sum dacc
 // (reduced over the wavefront once per list entry by the caller).
+// Token modes add the key-feature term: the query features [hi | lo] of a
+// row (one k=32 operand, b.rb) against [k_hi | k_hi] (kf[0]) and [k_lo | 0]
+// (kf[1]) give q_hi·k_hi + q_lo·k_hi + q_hi·k_lo in two MFMAs; eb is the
+// pair bias of the tile's list entry (log2 units).
 template <int MODE, bool DP>
 __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b, bool masked, int q0, int lane,
                                         int wkv, int doc_kv, const uint4 (&kreg)[4], const uint4 (&vreg)[4],
-                                        const TileOffs16& to, uint4 (&pb)[2], uint4 (&dsb)[2], float& dacc) {
+                                        const uint4 (&kf)[2], float eb, const TileOffs16& to, uint4 (&pb)[2],
+                                        uint4 (&dsb)[2], float& dacc) {
   const int g = lane >> 4;
   f32x4_t s[4], dp[4];
 #pragma unroll
@@ -1431,11 +1473,20 @@ __device__ __forceinline__ void dkv16_a(const AttnArgs& a, const DkvBuf<MODE>& b
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // the tile's softmax offsets (block term, pair bias and lse per row) are in b.ra[0..63]
+  if constexpr (MODE >= 2) {
+    const uint16_t* qf = reinterpret_cast<const uint16_t*>(b.rb);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const uint4 fa = lds_row8_32(qf, 16 * mb + (lane & 15), 8 * g);
+      s[mb] = mfma16(fa, kf[0], s[mb]);
+      s[mb] = mfma16(fa, kf[1], s[mb]);
+    }
+  }
+  // modes 0/1: the tile's softmax offsets (block term, pair bias and lse per row) are in b.ra[0..63]
   if (masked)
-    dkv16_probs<MODE, true, DP>(b, b.ra, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
+    dkv16_probs<MODE, true, DP>(a, b, b.ra, eb, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
   else
-    dkv16_probs<MODE, false, DP>(b, b.ra, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
+    dkv16_probs<MODE, false, DP>(a, b, b.ra, eb, a.scale_log2, q0, wkv, doc_kv, g, s, dp, pb, dsb, dacc);
 }
 
 // Second part: dV^T += dO^T P, dK^T += Q^T dS (step st = 8·kk + md).
@@ -1466,7 +1517,6 @@ __device__ __forceinline__ void dkv16_b(const DkvBuf<MODE>& b, const TileOffs16&
 
 template <int BS, int MODE, bool DP>
 __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan pl) {
-  static_assert(MODE <= 1, "token modes use attn_bwd_dkv_kernel");
   constexpr int D = 128;
   constexpr int BM = 64;  // query rows per staged tile
   constexpr int NS = BS / BM;
@@ -1524,7 +1574,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   for (int t = tid; DP && t < kChunk * 8; t += blockDim.x) pslot[t / 8][t % 8] = 0.f;
   __syncthreads();  // qbs, epos
   // the offsets of tile j (q-block qbs[e], rows (f % NS)·64 .. +63 of the list entry)
-  auto tile_rof = [&](int j) __attribute__((always_inline)) {
+  auto tile_rof = [&](int j) __attribute__((always_inline)) -> const float* {
+    if constexpr (MODE >= 2) return nullptr;  // token modes: per-row constants, no stored offsets
     const int f = j + skip0, e = f / NS;
     return a.roff + ((static_cast<int64_t>(h) * a.QB + qbs[e]) * a.maxkv + epos[e]) * BS + (f % NS) * BM;
   };
@@ -1546,6 +1597,15 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   }
   const int doc_kv = a.docs[wkv];
   const TileOffs16 to = tile_offs16(lane);
+  // token modes: this lane's key features as B operands (see dkv16_a); the
+  // table row of key j is cos hi[8], sin hi[8], cos lo[8], sin lo[8]
+  uint4 kf[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+  if constexpr (MODE >= 2) {
+    const uint16_t* tr = static_cast<const uint16_t*>(a.table) + static_cast<int64_t>(wkv) * kTokRow;
+    kf[0] = *reinterpret_cast<const uint4*>(tr + 8 * (g & 1));
+    if (g < 2) kf[1] = *reinterpret_cast<const uint4*>(tr + 16 + 8 * g);
+  }
+  const bool pbias = MODE >= 2 && a.pair_bias != nullptr;
 
   f32x4_t dvT[8], dkT[8];
 #pragma unroll
@@ -1587,7 +1647,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
       dcur = e;
     }
     const bool masked = !((wkv_lo + 15 <= q0) && (dse[e] <= wkv_lo));
-    dkv16_a<MODE, DP>(a, bc, masked, q0, lane, wkv, doc_kv, kreg, vreg, to, pb, dsb, dacc);
+    // token modes: the pair bias of the list entry (modes 0/1 have it in the stored offsets)
+    const float eb = pbias && epos[e] >= 0
+                         ? a.pair_bias[(static_cast<int64_t>(h) * a.QB + qbs[e]) * a.maxkv + epos[e]] * kLog2e
+                         : 0.f;
+    dkv16_a<MODE, DP>(a, bc, masked, q0, lane, wkv, doc_kv, kreg, vreg, kf, eb, to, pb, dsb, dacc);
     return true;
   };
   if (wave < 4) {
@@ -1774,8 +1838,7 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
   L.part_dv = o;
   o += al(part);
   L.q_pos = o;
-  if (p->pair_bias || p->dpair_bias || p->bias_mode != SCOPE_BIAS_TOKEN)
-    o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * 4);
+  o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * 4);
   // per-(h, qb, entry, row) softmax offsets of modes 0/1
   L.roff = o;
   if (p->bias_mode != SCOPE_BIAS_TOKEN) o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * p->bs * 4);
@@ -1839,25 +1902,19 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
       hipLaunchKernelGGL(qpos_kernel, dim3(a.QB, a.H), dim3(64), 0, s, a, const_cast<int32_t*>(pl.q_pos));
   }
   const bool dp = a.dpair != nullptr;  // the pair-bias gradient runs in its own instantiation
-  if ((phases & SCOPE_BWD_DKV_MAIN) && mode != SCOPE_BIAS_TOKEN) {
+  if (phases & SCOPE_BWD_DKV_MAIN) {
     // 16 keys per wavefront, 8 wavefronts (two per SIMD) per 128 keys
-    if (mode == SCOPE_BIAS_BLOCK && dp)
-      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1, true>), gk, dim3(512), 0, s, a, pl);
-    else if (mode == SCOPE_BIAS_BLOCK)
-      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1, false>), gk, dim3(512), 0, s, a, pl);
-    else if (dp)
-      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0, true>), gk, dim3(512), 0, s, a, pl);
-    else
-      hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0, false>), gk, dim3(512), 0, s, a, pl);
-  } else if (phases & SCOPE_BWD_DKV_MAIN) {
-    if (gate && dp)
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3, true>), gk, dim3(256), 0, s, a, pl);
-    else if (gate)
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3, false>), gk, dim3(256), 0, s, a, pl);
-    else if (dp)
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2, true>), gk, dim3(256), 0, s, a, pl);
-    else
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 2, false>), gk, dim3(256), 0, s, a, pl);
+    // (the gated token mode spills 20-40 registers here: it keeps the
+    // 32-keys-per-wavefront kernel, one wavefront per SIMD)
+    const int m = mode == SCOPE_BIAS_TOKEN ? (gate ? 3 : 2) : (mode == SCOPE_BIAS_BLOCK ? 1 : 0);
+    if (m == 3 && dp) hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3, true>), gk, dim3(256), 0, s, a, pl);
+    else if (m == 3) hipLaunchKernelGGL((attn_bwd_dkv_kernel<BS, 3, false>), gk, dim3(256), 0, s, a, pl);
+    else if (m == 2 && dp) hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 2, true>), gk, dim3(512), 0, s, a, pl);
+    else if (m == 2) hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 2, false>), gk, dim3(512), 0, s, a, pl);
+    else if (m == 1 && dp) hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1, true>), gk, dim3(512), 0, s, a, pl);
+    else if (m == 1) hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 1, false>), gk, dim3(512), 0, s, a, pl);
+    else if (dp) hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0, true>), gk, dim3(512), 0, s, a, pl);
+    else hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0, false>), gk, dim3(512), 0, s, a, pl);
   }
   if (phases & SCOPE_BWD_DKV_REDUCE) {
     hipLaunchKernelGGL(bwd_reduce_kernel<BS>, gr, dim3(256), 0, s, a, pl);
@@ -1938,9 +1995,7 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   pl.multi = reinterpret_cast<const int32_t*>(ws + L.multi);
   pl.part_dk = reinterpret_cast<float*>(ws + L.part_dk);
   pl.part_dv = reinterpret_cast<float*>(ws + L.part_dv);
-  pl.q_pos = (p->pair_bias || p->dpair_bias || p->bias_mode != SCOPE_BIAS_TOKEN)
-                 ? reinterpret_cast<const int32_t*>(ws + L.q_pos)
-                 : nullptr;
+  pl.q_pos = reinterpret_cast<const int32_t*>(ws + L.q_pos);
   a.roff = p->bias_mode != SCOPE_BIAS_TOKEN ? reinterpret_cast<float*>(ws + L.roff) : nullptr;
   pl.max_slots = L.max_slots;
   pl.max_items = L.max_items;

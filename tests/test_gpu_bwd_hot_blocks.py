@@ -10,8 +10,8 @@ q_indices, torch:_inductor/kernel/flex/templates/flex_backwards.py.jinja).
 Every case here has key blocks with 2 to 4 chunks, a ragged last chunk, and
 heads without any multi-chunk block (the reduce walks the heads' multi-chunk
 lists and must skip an empty one), in every dK/dV kernel family: the 16-key
-kernel (no bias, block bias, with a pair bias) and the 32-key token-mode
-kernel (with the softplus gate).  The whole dq / dk / dv (and coefficient and
+kernel (no bias, block bias, token offsets, each with a pair bias too) and
+the 32-key kernel of the gated token mode (softplus gate).  The whole dq / dk / dv (and coefficient and
 pair-bias gradients) are compared with fp64 autograd through the oracle's
 block-sparse attention.  Bar written in every comparison:
 |got - ref| <= 2e-2 + 1e-2·|ref| elementwise (dpair_bias: 2e-2·max|ref|)."""
@@ -68,7 +68,10 @@ CASES = [
     ("bs128-block", 4, 16384, 128, [100 * 128 + 5], [(2, 0, 2), (2, 1, 2), (2, 0, 3), (2, 1, 3)], "block", False),
     ("bs128-block-pair", 4, 16384, 128, [100 * 128 + 5], [(2, 1, 2), (2, 0, 2), (2, 0, 3), (2, 1, 3)], "block",
      True),
-    ("bs128-token-gate", 2, 16384, 128, [9000], [(2, 0, 2), (2, 1, 3)], "token", False),
+    ("bs128-token", 2, 16384, 128, [9000], [(2, 0, 2), (2, 1, 3)], "token", False),
+    ("bs128-token-pair", 2, 16384, 128, [9000], [(2, 1, 2), (2, 0, 3)], "token", True),
+    ("bs128-token-gate", 2, 16384, 128, [9000], [(2, 0, 2), (2, 1, 3)], "token-gate", False),
+    ("bs256-token", 2, 32768, 256, [100 * 256 + 77], [(2, 2, 3), (2, 0, 2)], "token", False),
     ("bs256-none", 2, 32768, 256, [100 * 256 + 77], [(2, 2, 3), (2, 0, 2)], "none", False),
     ("bs256-block", 3, 32768, 256, [100 * 256 + 77], [(2, 0, 3), (2, 2, 3), (2, 0, 2)], "block", False),
 ]
@@ -96,6 +99,8 @@ def test_multichunk_dkv_vs_fp64(cid, H, T, bs, cuts, per_head, mode, pair):
     print(f"  users of the hottest block per head: {users.max(axis=1).tolist()} "
           f"(chunks {nch.max(axis=1).tolist()})", flush=True)
 
+    gate = mode == "token-gate"
+    mode = "token" if gate else mode
     q, k, v = qkv(H, T, seed=T + 3 * bs + H)
     g = torch.Generator().manual_seed(41)
     dout = torch.randn((1, H, T, 128), generator=g).to(torch.bfloat16)
@@ -132,11 +137,15 @@ def test_multichunk_dkv_vs_fp64(cid, H, T, bs, cuts, per_head, mode, pair):
         sp = scope_amd.SpectralTerms(coeff_cos=cd, coeff_sin=sd, omegas=terms["omegas"].to(DEV), offset=mode, beta=BETA)
         leaves = [cd, sd]
         if mode == "token":
-            extra = {n: x.to(DEV).requires_grad_() for n, x in tok_kw.items()}
-            sp.b0, sp.slope, sp.delta_main, sp.width = extra["b0"], extra["slope"], extra["delta_main"], extra["width"]
+            # without a gate delta_main and width do not enter the scores
+            tok_names = ("b0", "slope", "delta_main", "width") if gate else ("b0", "slope")
+            extra = {n: tok_kw[n].to(DEV).requires_grad_() for n in tok_names}
+            sp.b0, sp.slope = extra["b0"], extra["slope"]
             sp.use_slope = sp.subtract_b0 = True
-            sp.gate_kind, sp.ramp_lambda, sp.tau = "softplus", 0.2, 64.0
-            leaves += [extra[n] for n in ("b0", "slope", "delta_main", "width")]
+            if gate:
+                sp.delta_main, sp.width = extra["delta_main"], extra["width"]
+                sp.gate_kind, sp.ramp_lambda, sp.tau = "softplus", 0.2, 64.0
+            leaves += [extra[n] for n in tok_names]
     out = scope_amd.scope_attention(qd, kd, vd, block_mask=bm, scale=SCALE, spectral=sp)
     out.backward(dout.to(DEV))
     torch.cuda.synchronize()
@@ -152,8 +161,9 @@ def test_multichunk_dkv_vs_fp64(cid, H, T, bs, cuts, per_head, mode, pair):
         rleaves = [rc, rs]
     if mode == "token":
         rt = {n: x[0].double().requires_grad_() for n, x in tok_kw.items()}
-        kw["token_kwargs"] = dict(gate="softplus", ramp_lambda=0.2, tau=64.0, **rt)
-        rleaves += [rt[n] for n in ("b0", "slope", "delta_main", "width")]
+        gk = dict(gate="softplus", ramp_lambda=0.2, tau=64.0) if gate else dict(gate="none")
+        kw["token_kwargs"] = dict(**gk, **rt)
+        rleaves += [rt[n] for n in tok_names]
     pr = pb.clone().requires_grad_() if pair else None
     ro, _ = OA.scope_attention_blocksparse(qq, kk, vv, kv_num, kv_idx, docs, bs=bs, scale=SCALE, beta=BETA,
                                            pair_bias=pr, **kw)
