@@ -209,9 +209,12 @@ def _soft_setup(ctx, inputs, output):
     ctx.save_for_backward(q, k, kv_num, kv_idx, pb, qbar, kbar)
     ctx.bs, ctx.logit_scale, ctx.soft_temp = bs, logit_scale, soft_temp
     ctx.mark_non_differentiable(qbar, kbar)
+    ctx.set_materialize_grads(False)  # an output's unused gradient stays None (no zero tensors)
 
 
 def _soft_backward(ctx, dpb, _dq, _dk):
+    if dpb is None:
+        return (None,) * 11
     q, k, kv_num, kv_idx, pb, qbar, kbar = ctx.saved_tensors
     q_off, q_list = transpose_blocks(kv_num, kv_idx, kv_num.shape[-1])
     dq, dk = soft_pointer_bwd(qbar, kbar, kv_num, kv_idx, q_off, q_list, pb, dpb, q, k, ctx.bs, ctx.logit_scale,
@@ -368,9 +371,12 @@ def _attn_setup(ctx, inputs, output):
                           slope, dm, wd, pb)
     ctx.cfg = (bs, scale, beta, bias_mode, use_slope, subtract_b0, gate_kind, ramp_lambda, tau)
     ctx.mark_non_differentiable(lse)
+    ctx.set_materialize_grads(False)  # lse's gradient stays None (no zero tensor)
 
 
 def _attn_backward(ctx, dout, _dlse):
+    if dout is None:
+        return (None,) * 26
     (q, k, v, out, lse, kv_num, kv_idx, docs, ds_tok_end, q_off, q_list, table, cc, cs, b0, slope, dm, wd,
      pb) = ctx.saved_tensors
     bs, scale, beta, bias_mode, use_slope, subtract_b0, gate_kind, ramp_lambda, tau = ctx.cfg
@@ -449,6 +455,7 @@ def _head_setup(ctx, inputs, output):
     y, omegas, log_omegas, cos_mean, sin_mean, iprm, fprm = inputs
     ctx.save_for_backward(y, omegas, log_omegas, cos_mean, sin_mean, output[-1])
     ctx.iprm, ctx.fprm = list(iprm), list(fprm)
+    ctx.set_materialize_grads(False)  # the unused outputs' gradients stay None (the kernel skips them)
 
 
 def _head_backward(ctx, *g):
@@ -500,6 +507,7 @@ def _mlp_setup(ctx, inputs, output):
     q, w1, b1, w2, b2 = inputs
     ctx.save_for_backward(q, w1, w2, output[1], output[2])
     ctx.dtypes = (w1.dtype, b1.dtype, w2.dtype, b2.dtype)
+    ctx.set_materialize_grads(False)  # z1 and x1 are saved for the backward, not used: their gradients stay None
 
 
 def _wgrad(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
@@ -523,18 +531,24 @@ def _mlp_backward(ctx, gy, gz1, gx1):
     split-row kernel.  The weights' gradients are those of their bf16 copies
     (rounded to bf16), in the weights' dtype."""
     q, w1, w2, z1, x1 = ctx.saved_tensors
+    if gy is None and gz1 is None and gx1 is None:
+        return None, None, None, None, None
     dt = q.dtype
-    dx1 = gy.to(dt).matmul(w2.to(dt))
-    if gx1 is not None:
-        dx1 = dx1 + gx1
-    dz1 = torch.ops.aten.silu_backward(dx1, z1)
-    if gz1 is not None:
-        dz1 = dz1 + gz1
-    dq = dz1.matmul(w1.to(dt)) if ctx.needs_input_grad[0] else None
-    dw2, db2 = _wgrad(gy.to(dt), x1)
-    dw1, db1 = _wgrad(dz1, q)
     t1, tb1, t2, tb2 = ctx.dtypes
-    return dq, dw1.to(t1), db1.to(tb1), dw2.to(t2), db2.to(tb2)
+    dw2 = db2 = None
+    dx1 = gx1
+    if gy is not None:
+        gy = gy.to(dt)
+        dx1 = gy.matmul(w2.to(dt)) if dx1 is None else dx1 + gy.matmul(w2.to(dt))
+        dw2, db2 = _wgrad(gy, x1)
+        dw2, db2 = dw2.to(t2), db2.to(tb2)
+    dz1 = gz1
+    if dx1 is not None:
+        dz = torch.ops.aten.silu_backward(dx1, z1)
+        dz1 = dz if dz1 is None else dz1 + dz
+    dq = dz1.matmul(w1.to(dt)) if ctx.needs_input_grad[0] else None
+    dw1, db1 = _wgrad(dz1, q)
+    return dq, dw1.to(t1), db1.to(tb1), dw2, db2
 
 
 coeff_mlp.register_autograd(_mlp_backward, setup_context=_mlp_setup)
