@@ -618,6 +618,7 @@ def main_ref(args):
 
     t_fwd = time_region(attn_fwd_only, args.steps, args.warmup)
     t_attn = time_region(attn_fwd_bwd, args.steps, args.warmup)
+    graph = graph_step_time(layer, q, k, v, dout, one, args.steps)
     F_fwd, F_bwd = 4.0 * bs * bs * D * n_act, 10.0 * bs * bs * D * n_act
     res = {
         "metric": "SCOPE layer fwd+bwd on the reference's default path (qk_aug terms, reference-mode lists) "
@@ -642,12 +643,58 @@ def main_ref(args):
         "attn_fwd_ms": round(t_fwd * 1e3, 4),
         "attn_fwd_tflops": round(F_fwd / t_fwd / 1e12, 2),
         "attn_fwd_bwd_ms": round(t_attn * 1e3, 4),
+        # the same step replayed from one captured HIP graph: no host launch
+        # overhead (eager, the ~45 launches of the module path can outrun a slow
+        # host's Python); equal to eager bit for bit on every replay checked
+        "graph_ms_per_step": graph["ms"], "graph_tflops": (round((F_fwd + F_bwd) / graph["ms"] / 1e9, 2)
+                                                          if graph["ms"] else None),
+        "graph_check": graph["check"],
         "attn_fwd_bwd_tflops": round((F_fwd + F_bwd) / t_attn / 1e12, 2),
         "roofline": dict(bound="mfma", kernel="attention fwd+bwd (token mode)",
                          achieved=round((F_fwd + F_bwd) / t_attn / 1e12, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                          frac=round((F_fwd + F_bwd) / t_attn / 1e12 / PEAK_BF16_TFLOPS, 4), traffic=None),
     }
     print(json.dumps(res))
+
+
+def graph_step_time(layer, q, k, v, dout, one, steps: int) -> dict:
+    """ms per fwd+bwd step of `layer` replayed from a captured HIP graph, and
+    whether each checked replay's output equals an eager step's bit for bit."""
+    import torch
+
+    qs, ks, vs = (x.detach().clone().requires_grad_() for x in (q, k, v))
+
+    def body():
+        y, reg, _ = layer(qs, ks, vs)
+        torch.autograd.backward([y, reg], [dout, one])
+        return y
+
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                body()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y_g = body()
+        with torch.no_grad():
+            y_e = layer(q, k, v)[0]
+        ok = True
+        for _ in range(3):  # replays with eager work and synchronisations between them
+            g.replay()
+            torch.cuda.synchronize()
+            ok = ok and bool(torch.equal(y_g, y_e))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return dict(ms=round(e0.elapsed_time(e1) / steps, 4), check="equal to eager" if ok else "DIFFERS from eager")
+    except Exception as ex:  # capture not possible here: report why, keep the eager numbers
+        return dict(ms=None, check=f"not captured: {type(ex).__name__}: {ex}"[:200])
 
 
 def time_steps(step, steps, warmup):

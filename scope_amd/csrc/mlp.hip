@@ -74,14 +74,19 @@ struct WgradSplit {
   __device__ static bool colsum(int wave) { return BY_M ? true : (BY_N ? wave == 0 : wave % 2 == 0); }
 };
 
+// global_load_lds copies one thread issues per chunk of an operand with C columns
+template <int C>
+constexpr int kCopiesPerChunk = (C < 128 ? 1 : C / 128) * (1024 / kWgradThreads);
+
 template <int MB, int NB>
 __global__ __launch_bounds__(kWgradThreads) void wgrad_kernel(WgradArgs g) {
   constexpr int M = 32 * MB, N = 32 * NB;
   constexpr int TA = M < 128 ? 1 : M / 128, TB = N < 128 ? 1 : N / 128;
   using S = WgradSplit<MB, NB>;
   static_assert(S::WM * S::WN <= 8, "wgrad_kernel: at most 8 accumulator blocks per wavefront");
-  __shared__ __attribute__((aligned(16))) uint16_t sa[2][TA * 64 * 128];
-  __shared__ __attribute__((aligned(16))) uint16_t sb[2][TB * 64 * 128];
+  // three chunk buffers: chunk c+2 is copied while chunk c is summed
+  __shared__ __attribute__((aligned(16))) uint16_t sa[3][TA * 64 * 128];
+  __shared__ __attribute__((aligned(16))) uint16_t sb[3][TB * 64 * 128];
 
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
   const int64_t chunks = g.rows / kChunkRows;
@@ -98,17 +103,30 @@ __global__ __launch_bounds__(kWgradThreads) void wgrad_kernel(WgradArgs g) {
 #pragma unroll
   for (int i = 0; i < S::WM; ++i) cs[i] = 0.f;
   const bool do_cs = S::colsum(wave);
+  // vmcnt counts this wavefront's copies in issue order: with chunk c+1's copies
+  // issued after chunk c's, "at most one chunk's copies outstanding" means chunk c landed
+  constexpr int kPerChunk = kCopiesPerChunk<M> + kCopiesPerChunk<N>;
+  static_assert(kPerChunk <= 15, "wgrad_kernel: vmcnt field");
+  auto wait_vm_copies_but_one_chunk = []() __attribute__((always_inline)) {
+    // s_waitcnt vmcnt(kPerChunk) (expcnt and lgkmcnt at their maximum: not waited for)
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kPerChunk);
+  };
 
   auto issue = [&](int64_t c, int buf) __attribute__((always_inline)) {
     wgrad_copy<M>(g.a, g.a_ss, g.a_rs, g.seg, c * kChunkRows, sa[buf], tid);
     wgrad_copy<N>(g.b, g.b_ss, g.b_rs, g.seg, c * kChunkRows, sb[buf], tid);
   };
   if (c0 < c1) issue(c0, 0);
+  if (c0 + 1 < c1) issue(c0 + 1, 1);
   for (int64_t c = c0; c < c1; ++c) {
-    const int buf = static_cast<int>((c - c0) & 1);
-    wait_vm0();
-    __syncthreads();  // chunk c is in buffer buf; every wavefront is done with the other buffer
-    if (c + 1 < c1) issue(c + 1, buf ^ 1);
+    const int buf = static_cast<int>((c - c0) % 3);
+    // chunk c is the older of at most two chunks in flight: wait for it alone
+    if (c + 1 < c1)
+      wait_vm_copies_but_one_chunk();
+    else
+      wait_vm0();
+    __syncthreads();  // chunk c is in buffer buf; every wavefront is done with the buffer of chunk c-1
+    if (c + 2 < c1) issue(c + 2, static_cast<int>((c + 2 - c0) % 3));
 #pragma unroll
     for (int ks = 0; ks < kChunkRows / 16; ++ks) {
       uint4 av[S::WM], bv[S::WN];
@@ -163,19 +181,39 @@ __global__ __launch_bounds__(kWgradThreads) void wgrad_kernel(WgradArgs g) {
 
 __device__ __forceinline__ float round_bf16(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
 
-// dw[m][n] (then db[m]) = the sum over workgroups, in workgroup order.
+// dw[m][n] (then db[m]) = the sum over workgroups.  A workgroup takes 64
+// consecutive elements; its four wavefronts sum a quarter of the groups each
+// with eight interleaved accumulators (eight loads in flight per lane), and
+// the quarters are added in order: a fixed association, so the result does
+// not depend on scheduling.
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, int groups, int MN, int M,
                                                            int rnd, float* __restrict__ dw, float* __restrict__ db) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= MN + M || (i >= MN && !db)) return;
+  __shared__ float qsum[4][64];
+  const int e = blockIdx.x * 64 + threadIdx.x % 64, quarter = threadIdx.x / 64;
   const int stride = MN + M;
-  float t = 0.f;
-  for (int w = 0; w < groups; ++w) t += part[static_cast<int64_t>(w) * stride + i];
+  const int per_q = (groups + 3) / 4;
+  const int w0 = quarter * per_q, w1 = min(groups, w0 + per_q);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (e < stride) {
+    int w = w0;
+    for (; w + 8 <= w1; w += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += part[static_cast<int64_t>(w + u) * stride + e];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (w + u < w1) acc[u] += part[static_cast<int64_t>(w + u) * stride + e];
+  }
+  qsum[quarter][threadIdx.x % 64] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  __syncthreads();
+  if (quarter != 0 || e >= stride || (e >= MN && !db)) return;
+  const int i = threadIdx.x;
+  float t = ((qsum[0][i] + qsum[1][i]) + qsum[2][i]) + qsum[3][i];
   if (rnd) t = round_bf16(t);
-  if (i < MN)
-    dw[i] = t;
+  if (e < MN)
+    dw[e] = t;
   else
-    db[i - MN] = t;
+    db[e - MN] = t;
 }
 
 int wgrad_groups(const scope_wgrad_params* p) {
@@ -240,7 +278,7 @@ extern "C" int scope_linear_wgrad(const scope_wgrad_params* p, const uint16_t* a
   else if (N == 64) launch_wgrad<8, 2>(g, groups, s);
   else launch_wgrad<8, 4>(g, groups, s);
   const int total = M * N + M;
-  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((total + 255) / 256), dim3(256), 0, s, g.part, groups, M * N, M,
+  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((total + 63) / 64), dim3(256), 0, s, g.part, groups, M * N, M,
                      p->round_bf16, dw, db);
   return check_launch("linear weight gradient kernels");
 }
