@@ -45,6 +45,7 @@ def _short(name: str) -> str:
     for k in KERNELS + (COPY,):
         if "(" not in k and k in name:
             return k
+    name = name.replace("(anonymous namespace)::", "")
     return name.split("(")[0][-60:]
 
 
