@@ -1732,6 +1732,433 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   }
 }
 
+// ---------------------------------------------------------------------------
+// pass A, 16 query rows per wavefront (two wavefronts per SIMD, any mode)
+// ---------------------------------------------------------------------------
+// Transpose read of a 64 x 32 feature tile (swz32_off) as the A operand of a
+// 16x16x32 MFMA: m = feature 16·fb + lane % 16, k = the keys of k-step kk in
+// the slot order of lds_kmajor16 (rows 32kk + 4g + 0..3, then 32kk + 16 + 4g
+// + 0..3).
+__device__ __forceinline__ uint4 lds_kmajor16_32(const uint16_t* tile, int kk, int fb, int lane) {
+  const int g = lane >> 4, j = lane & 15, s = j >> 2, t = j & 3;
+  const int r0 = 32 * kk + 4 * g + s, d = 16 * fb + 4 * t;
+  lds_bf16x4_t* plo = (lds_bf16x4_t*)(const_cast<uint16_t*>(tile + swz32_off(r0, d)));
+  lds_bf16x4_t* phi = (lds_bf16x4_t*)(const_cast<uint16_t*>(tile + swz32_off(r0 + 16, d)));
+  const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(plo));
+  const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(phi));
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// x summed over the four lane groups of 16 (lanes l, l ^ 16, l ^ 32, l ^ 48)
+__device__ __forceinline__ float sum_groups16(float x) {
+  x += __shfl_xor(x, 16, 64);
+  return x + __shfl_xor(x, 32, 64);
+}
+
+// The q-major pass with 16 query rows per wavefront on v_mfma_f32_16x16x32_bf16:
+// lane l owns query row l % 16 of its wavefront and, in every 16-key block of
+// a tile, the keys 4g .. 4g+3 (g = l / 16).  S^T = K·Q^T and dP^T = V·dO^T
+// per 16-key block (K, V rows from the tile, Q and dO of the lane's row in
+// registers; dP starts from -Δ), the token modes' key features as two k=32
+// MFMAs (the table row [k_hi | k_lo] against [q_hi | q_hi] and [q_lo | 0]),
+// then dQ^T += K^T·dS^T and, in token modes, the feature gradient
+// dF^T += F^T·dS^T (and its P-weighted twin for the Δ correction) from
+// transpose reads.  Eight wavefronts (128 rows) per workgroup, two per SIMD;
+// every mode, both block sizes.  The math per element, the sums and the
+// epilogue's outputs are those of attn_bwd_dq_kernel.
+template <int BS, int MODE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq16_kernel(AttnArgs a) {
+  constexpr int SPLIT = BS / 128;  // workgroups per q-block (8 wavefronts = 128 query rows each)
+  constexpr int BN = 64;           // keys per staged tile
+  constexpr int NSUB = BS / BN;
+  constexpr int NT = 512;
+  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
+
+  __shared__ KvTile<MODE> buf0, buf1;
+  __shared__ int kbs[kListLds];
+  __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64, g = lane / 16, c = lane % 16;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = tile / (a.QB * SPLIT), qb = (tile / SPLIT) % a.QB, part = tile % SPLIT;
+  const int64_t q0 = static_cast<int64_t>(qb) * BS + part * 128;
+  const int wrow_lo = static_cast<int>(q0) + wave * 16;
+  const int64_t hT = static_cast<int64_t>(h) * a.T;
+  const int row = wrow_lo + c;
+
+  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
+  const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
+  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
+  for (int t = tid; t < min(n, kListLds); t += NT) kbs[t] = lst[t];
+  const bool pbias = a.pair_bias != nullptr;
+  if (pbias)
+    for (int t = tid; t < min(n, kListLds); t += NT) kbias[t] = a.pair_bias[lrow * a.maxkv + t] * kLog2e;
+
+  // Q and dO of this lane's row, k-step ks: columns 32g + 8ks .. +7 (the order of the row reads)
+  uint4 qreg[4], doreg[4];
+  float delta;
+  {
+    const uint16_t* qp = a.q + h * a.q_sh + static_cast<int64_t>(row) * a.q_st + g * 32;
+    const uint16_t* op = a.o + h * a.o_sh + static_cast<int64_t>(row) * a.o_st + g * 32;
+    const uint16_t* dp = a.dout + h * a.o_sh + static_cast<int64_t>(row) * a.o_st + g * 32;
+    float dsum = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 8);
+      doreg[ks] = *reinterpret_cast<const uint4*>(dp + ks * 8);
+      const uint4 ov = *reinterpret_cast<const uint4*>(op + ks * 8);
+      const uint32_t dw[4] = {doreg[ks].x, doreg[ks].y, doreg[ks].z, doreg[ks].w};
+      const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dsum += __uint_as_float(dw[i] << 16) * __uint_as_float(ow[i] << 16);
+        dsum += __uint_as_float(dw[i] & 0xffff0000u) * __uint_as_float(ow[i] & 0xffff0000u);
+      }
+    }
+    delta = sum_groups16(dsum);
+  }
+  const float lse_nat = a.lse[hT + row];
+  const float lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
+  const int doc = a.docs[row];
+
+  // ---- bias set-up (as in the forward)
+  float ca[8], sa[8];
+  uint4 qf1 = make_uint4(0, 0, 0, 0), qf2 = make_uint4(0, 0, 0, 0);
+  float rowc = 0.f, slp = 0.f, dm = 0.f, wd = 0.f;
+  float cos_i[4], sin_i[4];  // token mode, lane groups 0 and 1: cos/sin(ω_k row) for k = 4g..4g+3
+  if (MODE == 1) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      ca[k] = k < a.K ? a.coeff_cos[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
+      sa[k] = k < a.K ? a.coeff_sin[(hT + row) * a.K + k] * a.beta_log2 : 0.f;
+    }
+  }
+  if (TOK) {
+    // the row's features: half g % 2 (cos half, sin half), hi and lo bf16 parts
+    uint4 hi, lo;
+    token_qfeat(a, hT, row, g & 1, hi, lo, cos_i, sin_i);
+    qf1 = hi;                                     // [q_hi | q_hi]
+    if (g < 2) qf2 = lo;                          // [q_lo | 0]
+    if (g < 2) {
+      // kept for the kv-major pass, which stages them per query tile
+      *reinterpret_cast<uint4*>(a.qfeat + (hT + row) * kTokRow + g * 8) = hi;
+      *reinterpret_cast<uint4*>(a.qfeat + (hT + row) * kTokRow + 16 + g * 8) = lo;
+    }
+    if (a.subtract_b0) rowc = -a.beta_log2 * a.b0[hT + row];
+    if (a.use_slope) slp = a.beta_log2 * a.slope[hT + row];
+    if (GATE) {
+      dm = a.delta_main[hT + row];
+      wd = a.width[hT + row];
+    }
+  }
+  const int ds_end = a.ds_tok_end[qb];
+  const TileOffs16 to = tile_offs16(lane);
+
+  f32x4_t dqT[8];  // dQ^T: D rows 16·md + 4g + r, this lane's query row
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dqT[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Δ correction of the bias gradients, as in attn_bwd_dq_kernel: every sum
+  // has a P-weighted twin; all stay per lane (a quarter of the row's keys)
+  // until the epilogue
+  f32x4_t facc[2], facc_p[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) facc[i] = facc_p[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float accA[8], accB[8], accPA[8], accPB[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) accA[k] = accB[k] = accPA[k] = accPB[k] = 0.f;
+  float rs_tot = 0.f, pm_tot = 0.f;
+  float ex[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // Σ dS·df, dS·σ·sgn, dS·σ, then the P-weighted three
+
+  const int total = n * NSUB;
+  const int qmax = static_cast<int>(q0) + 127;
+  auto kb_at = [&](int t) __attribute__((always_inline)) { return kbs[t]; };
+  auto next_valid = [&](int it) __attribute__((always_inline)) {
+    while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
+    return it;
+  };
+  auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
+    const int kb = kb_at(it / NSUB);
+    const int rd = min(max(qb - kb, 0), a.QB - 1);
+    kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
+  };
+  float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
+  float eb = 0.f;  // pair bias of the current list entry (log2 units)
+  const float cs = a.scale_log2;
+  auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
+    const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
+    const float off = (MODE == 1 ? bt : rowc) + eb - lse2;
+    // S^T and dP^T - Δ per 16-key block kb4 (step st = 4·ks + kb4), operands two steps ahead
+    f32x4_t s[4], dp[4];
+#pragma unroll
+    for (int kb4 = 0; kb4 < 4; ++kb4) {
+      s[kb4] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      dp[kb4] = f32x4_t{-delta, -delta, -delta, -delta};
+    }
+    constexpr int RA = 2;
+    uint4 ka[RA + 1], va[RA + 1];
+#pragma unroll
+    for (int i = 0; i < RA; ++i) {
+      ka[i] = lds_row16(b.k, to, i % 4, i / 4);
+      va[i] = lds_row16(b.v, to, i % 4, i / 4);
+    }
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const int ks = st / 4, kb4 = st % 4;
+      if (st + RA < 16) {
+        ka[(st + RA) % (RA + 1)] = lds_row16(b.k, to, (st + RA) % 4, (st + RA) / 4);
+        va[(st + RA) % (RA + 1)] = lds_row16(b.v, to, (st + RA) % 4, (st + RA) / 4);
+      }
+      s[kb4] = mfma16(ka[st % (RA + 1)], qreg[ks], s[kb4]);
+      dp[kb4] = mfma16(va[st % (RA + 1)], doreg[ks], dp[kb4]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (TOK) {
+#pragma unroll
+      for (int kb4 = 0; kb4 < 4; ++kb4) {
+        const uint4 fa = lds_row8_32(b.f, 16 * kb4 + c, 8 * g);
+        s[kb4] = mfma16(fa, qf1, s[kb4]);
+        s[kb4] = mfma16(fa, qf2, s[kb4]);
+      }
+    }
+    // probabilities and dS^T: key j = 16·kb4 + 4g + r of the tile
+    const int lim = row - kv0;  // keys j <= lim are causal
+    const bool softplus = a.gate_kind == SCOPE_GATE_SOFTPLUS;
+    const float glam = a.beta_log2 * a.ramp_lambda;
+    float rs = 0.f, pm = 0.f;
+    uint32_t dw[8], pw[8];
+#pragma unroll
+    for (int kb4 = 0; kb4 < 4; ++kb4) {
+      int dcv[4] = {0, 0, 0, 0};
+      if (TOK || !full) {
+        const int4 d4 = *reinterpret_cast<const int4*>(&b.docs[16 * kb4 + 4 * g]);
+        dcv[0] = d4.x, dcv[1] = d4.y, dcv[2] = d4.z, dcv[3] = d4.w;
+      }
+      float dv[4], pv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * kb4 + 4 * g + r;
+        float x;
+        float sig = 0.f, sgn = 0.f, df = 0.f;
+        if (TOK) {
+          df = static_cast<float>(lim - j);
+          float e = slp * df;
+          if (GATE) {
+            const float dd = df - dm;
+            const float xx = (fabsf(dd) - wd) * a.inv_tau;
+            const float en = __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e);
+            const float inv = __builtin_amdgcn_rcpf(1.f + en);
+            const float lp = kLn2 * __builtin_amdgcn_logf(1.f + en);
+            const float gt = fmaxf(xx, 0.f) + (softplus ? lp : 0.f);
+            sig = softplus ? (xx >= 0.f ? inv : en * inv) : (xx > 0.f ? 1.f : 0.f);
+            sgn = dd > 0.f ? 1.f : (dd < 0.f ? -1.f : 0.f);
+            e -= glam * gt;
+          }
+          x = fmaf(s[kb4][r], cs, e + off);
+        } else {
+          x = fmaf(s[kb4][r], cs, off);
+        }
+        if (TOK || !full) x = mask_score(x, j, lim, dcv[r], doc);
+        const float p = __builtin_amdgcn_exp2f(x);
+        const float d = p * dp[kb4][r];  // dP accumulator started from -Δ
+        dv[r] = d;
+        pv[r] = p;
+        rs += d;
+        pm += p;
+        if (TOK) {
+          ex[0] += d * df;
+          ex[3] += p * df;
+          if (GATE) {
+            ex[1] += d * sig * sgn;
+            ex[2] += d * sig;
+            ex[4] += p * sig * sgn;
+            ex[5] += p * sig;
+          }
+        }
+      }
+      dw[2 * kb4] = cvt_pk_bf16(dv[0], dv[1]);
+      dw[2 * kb4 + 1] = cvt_pk_bf16(dv[2], dv[3]);
+      pw[2 * kb4] = cvt_pk_bf16(pv[0], pv[1]);
+      pw[2 * kb4 + 1] = cvt_pk_bf16(pv[2], pv[3]);
+    }
+    // B operands of k-step kk: blocks 2kk (slots 0-3) and 2kk+1 (slots 4-7)
+    uint4 dsb[2], pb[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      dsb[kk] = make_uint4(dw[4 * kk], dw[4 * kk + 1], dw[4 * kk + 2], dw[4 * kk + 3]);
+      pb[kk] = make_uint4(pw[4 * kk], pw[4 * kk + 1], pw[4 * kk + 2], pw[4 * kk + 3]);
+    }
+    // dQ^T += K^T dS^T (step st = 8·kk + md), operands two steps ahead
+    {
+      constexpr int RB = 2;
+      uint4 ta[RB + 1];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) ta[i] = lds_kmajor16(b.k, to, i / 8, i % 8);
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const int kk = st / 8, md = st % 8;
+        if (st + RB < 16) ta[(st + RB) % (RB + 1)] = lds_kmajor16(b.k, to, (st + RB) / 8, (st + RB) % 8);
+        dqT[md] = mfma16(ta[st % (RB + 1)], dsb[kk], dqT[md]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (TOK) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int fb = 0; fb < 2; ++fb) {
+          const uint4 ft = lds_kmajor16_32(b.f, kk, fb, lane);
+          facc[fb] = mfma16(ft, dsb[kk], facc[fb]);
+          facc_p[fb] = mfma16(ft, pb[kk], facc_p[fb]);
+        }
+    }
+    rs_kb += rs;
+    pm_kb += pm;
+    rs_tot += rs;
+    pm_tot += pm;
+  };
+  auto run = [&](int it, int nxt, const KvTile<MODE>& b) __attribute__((always_inline)) {
+    const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
+    if (MODE == 1 && it % NSUB == 0) {
+      // a key block's first tile is never skipped (it starts at or before every row)
+      const float4* t4 = reinterpret_cast<const float4*>(b.tab);
+      const float4 c0 = t4[0], c1 = t4[1], s0 = t4[2], s1 = t4[3];
+      bt = (ca[0] * c0.x + ca[1] * c0.y + ca[2] * c0.z + ca[3] * c0.w) +
+           (ca[4] * c1.x + ca[5] * c1.y + ca[6] * c1.z + ca[7] * c1.w) +
+           (sa[0] * s0.x + sa[1] * s0.y + sa[2] * s0.z + sa[3] * s0.w) +
+           (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
+    }
+    if (it % NSUB == 0) eb = pbias ? kbias[it / NSUB] : 0.f;  // per key block (its first tile is never skipped)
+    if (kv0 <= wrow_lo + 15) compute(kv0, b);                 // else every key follows this wavefront's rows
+    if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
+      // last tile of this key block: fold its sums into the coefficient gradients
+      const float4* t4 = reinterpret_cast<const float4*>(b.tab);
+      const float tb[16] = {t4[0].x, t4[0].y, t4[0].z, t4[0].w, t4[1].x, t4[1].y, t4[1].z, t4[1].w,
+                            t4[2].x, t4[2].y, t4[2].z, t4[2].w, t4[3].x, t4[3].y, t4[3].z, t4[3].w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        accA[k] += rs_kb * tb[k];
+        accB[k] += rs_kb * tb[8 + k];
+        accPA[k] += pm_kb * tb[k];
+        accPB[k] += pm_kb * tb[8 + k];
+      }
+      rs_kb = pm_kb = 0.f;
+    }
+  };
+
+  __syncthreads();  // kbs, kbias
+  int cur = next_valid(0);
+  if (cur < total) issue(cur, buf0);
+  while (cur < total) {
+    wait_vm0();
+    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
+    int nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf1);
+    run(cur, nxt, buf0);
+    cur = nxt;
+    if (cur >= total) break;
+    wait_vm0();
+    __syncthreads();
+    nxt = next_valid(cur + 1);
+    if (nxt < total) issue(nxt, buf0);
+    run(cur, nxt, buf1);
+    cur = nxt;
+  }
+  wait_vm0();  // no copy may still target LDS when the workgroup exits
+
+  // ---- epilogue: sums over the four lane groups of a row, dQ = scale·o
+  rs_tot = sum_groups16(rs_tot);
+  pm_tot = sum_groups16(pm_tot);
+  const float dd_err = rs_tot;  // Δ_true - Δ
+  // the kv-major pass reads Δ_true = Δ + (Δ_true - Δ), stored negated (its dP accumulators start from it)
+  if (g == 0) a.delta[hT + row] = -(delta + dd_err);
+  uint16_t* dqp = a.dq + h * a.q_sh + static_cast<int64_t>(row) * a.q_st + 4 * g;
+#pragma unroll
+  for (int md = 0; md < 8; ++md) {
+    uint2 val;
+    val.x = cvt_pk_bf16(dqT[md][0] * a.scale, dqT[md][1] * a.scale);
+    val.y = cvt_pk_bf16(dqT[md][2] * a.scale, dqT[md][3] * a.scale);
+    *reinterpret_cast<uint2*>(dqp + md * 16) = val;
+  }
+  const float beta = a.beta;
+  if (MODE == 1 && a.dcoeff_cos) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      accA[k] = sum_groups16(accA[k]);
+      accB[k] = sum_groups16(accB[k]);
+      accPA[k] = sum_groups16(accPA[k]);
+      accPB[k] = sum_groups16(accPB[k]);
+    }
+    if (g == 0)
+      for (int k = 0; k < a.K; ++k) {
+        a.dcoeff_cos[(hT + row) * a.K + k] = beta * (accA[k] - dd_err * accPA[k]);
+        a.dcoeff_sin[(hT + row) * a.K + k] = beta * (accB[k] - dd_err * accPB[k]);
+      }
+  }
+  if (TOK) {
+    if (a.dcoeff_cos) {
+      // facc[fb] register r: feature 16·fb + 4g + r; features 0-7 cos hi, 8-15 sin hi,
+      // 16-23 cos lo, 24-31 sin lo (band k = feature % 8): lane groups 0, 1 hold the
+      // cos half of bands 4g .. 4g+3, lane groups 2, 3 the sin half of the same bands
+      float C[4], Cp[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        C[i] = facc[0][i] + facc[1][i];
+        Cp[i] = facc_p[0][i] + facc_p[1][i];
+      }
+      float S[4], Sp[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        S[i] = __shfl_xor(C[i], 32, 64);
+        Sp[i] = __shfl_xor(Cp[i], 32, 64);
+      }
+      if (g < 2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int k = 4 * g + i;
+          if (k < a.K) {
+            const float Cc = C[i] - dd_err * Cp[i], Sc = S[i] - dd_err * Sp[i];
+            a.dcoeff_cos[(hT + row) * a.K + k] = beta * (cos_i[i] * Cc + sin_i[i] * Sc);
+            a.dcoeff_sin[(hT + row) * a.K + k] = beta * (sin_i[i] * Cc - cos_i[i] * Sc);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) ex[i] = sum_groups16(ex[i]);
+    if (g == 0) {
+      if (a.db0) a.db0[hT + row] = -beta * (rs_tot - dd_err * pm_tot);
+      if (a.dslope) a.dslope[hT + row] = beta * (ex[0] - dd_err * ex[3]);
+      const float gsc = beta * a.ramp_lambda * a.inv_tau;
+      if (a.ddelta_main) a.ddelta_main[hT + row] = GATE ? gsc * (ex[1] - dd_err * ex[4]) : 0.f;
+      if (a.dwidth) a.dwidth[hT + row] = GATE ? gsc * (ex[2] - dd_err * ex[5]) : 0.f;
+    }
+  }
+  // ---- modes 0/1: this row's softmax offset for every listed key block (the
+  // block term, plus the pair bias, minus lse), read per tile by the kv-major
+  // pass; the four lanes of a row take every fourth entry
+  if (MODE <= 1) {
+    float* rof = a.roff + lrow * a.maxkv * BS + (row - qb * BS);
+    for (int e = g; e < n; e += 4) {
+      float t = pbias ? kbias[e] : 0.f;
+      if (MODE == 1) {
+        const int rd = min(max(qb - kb_at(e), 0), a.QB - 1);
+        const float4* t4 = reinterpret_cast<const float4*>(static_cast<const float*>(a.table) + rd * 16);
+        const float4 c0 = t4[0], c1 = t4[1], s0 = t4[2], s1 = t4[3];
+        t += (ca[0] * c0.x + ca[1] * c0.y + ca[2] * c0.z + ca[3] * c0.w) +
+             (ca[4] * c1.x + ca[5] * c1.y + ca[6] * c1.z + ca[7] * c1.w) +
+             (sa[0] * s0.x + sa[1] * s0.y + sa[2] * s0.z + sa[3] * s0.w) +
+             (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
+      }
+      rof[e * BS] = t - lse2;
+    }
+  }
+}
+
 // dK and dV of the key blocks whose q-list spans several chunks: the sum of
 // the chunks' fp32 partials in chunk order, dK scaled, rounded to bf16.  A
 // fixed grid walks the work units (multi-chunk key block of any head, one of
@@ -1885,14 +2312,17 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
     }
   }
   if ((phases & SCOPE_BWD_DQ) && !dq_done) {
+    // 16 query rows per wavefront, eight wavefronts (two per SIMD) per 128
+    // rows; the gated token mode would spill there (about 80 registers) and
+    // keeps 32 rows per wavefront, one wavefront per SIMD
     if (mode == SCOPE_BIAS_BLOCK)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 1>), gq, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((attn_bwd_dq16_kernel<BS, 1>), gq, dim3(512), 0, s, a);
     else if (mode == SCOPE_BIAS_TOKEN && gate)
       hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 3>), gq, dim3(256), 0, s, a);
     else if (mode == SCOPE_BIAS_TOKEN)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 2>), gq, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((attn_bwd_dq16_kernel<BS, 2>), gq, dim3(512), 0, s, a);
     else
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 0>), gq, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((attn_bwd_dq16_kernel<BS, 0>), gq, dim3(512), 0, s, a);
   }
   if (phases & SCOPE_BWD_DKV) phases |= SCOPE_BWD_DKV_PLAN | SCOPE_BWD_DKV_MAIN | SCOPE_BWD_DKV_REDUCE;
   if (phases & SCOPE_BWD_DKV_PLAN) {
