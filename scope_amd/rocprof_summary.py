@@ -29,7 +29,7 @@ import os
 import sys
 
 KERNELS = ("attn_fwd_kernel", "attn_fwd_kernel(lse)", "attn_fwd_kernel(mass)", "attn_bwd_dq2_kernel",
-           "attn_bwd_dq_kernel", "attn_bwd_dkv16_kernel", "attn_bwd_dkv_kernel", "bwd_reduce_kernel", "block_means_kernel", "ptr_score_kernel",
+           "attn_bwd_dq16_kernel", "attn_bwd_dq_kernel", "attn_bwd_dkv16_kernel", "attn_bwd_dkv_kernel", "bwd_reduce_kernel", "block_means_kernel", "ptr_score_kernel",
            "stats_kernel", "tr_fill_kernel", "tr_sort_kernel", "tr_count_kernel", "swa_count_kernel",
            "swa_rows_kernel", "swa_pad_kernel", "coeff_fwd_kernel", "coeff_bwd_kernel", "coeff_reg_kernel",
            "probe_mfma_kernel", "probe_copy_kernel")
