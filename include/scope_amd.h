@@ -244,6 +244,33 @@ int scope_linear_wgrad(const scope_wgrad_params* p, const uint16_t* a, const uin
                        void* workspace, void* stream);
 
 /* ------------------------------------------------------------------------
+ * The head's shared MLP, fused.  Replaces the two F.linear and the SiLU of
+ * SpectralBias._mlp_forward (model/attn_bias.py:271-276, 380-386) on bf16
+ * rows, and the row-wise part of their autograd:
+ *   forward   y = W2·SiLU(W1·q + b1) + b2               y [rows][O] bf16
+ *   backward  z1 = W1·q + b1, x1 = SiLU(z1), dx1 = gy·W2,
+ *             dz1 = SiLU'(z1)·dx1, dq = dz1·W1          dq [rows][128],
+ *             x1, dz1 [rows][256], gyp = gy padded to [rows][64] (bf16)
+ * with the weights fp32 as in the module (W1 [256][128], b1 [256],
+ * W2 [O][256], b2 [O], rounded to bf16 like the reference's .to(q.dtype))
+ * and every intermediate rounded to bf16 where the reference's tensors are;
+ * D = 128, hidden = 256, 1 <= O <= 64.  Row r of q is row r % seg of
+ * segment r / seg: q + (r / seg)·q_ss + (r % seg)·q_rs (elements); rows is
+ * a multiple of 32; y, gy, dq, dz1, x1 and gyp are contiguous.  The weight
+ * and bias gradients take x1 / gyp and dz1 / q to scope_linear_wgrad.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int64_t rows, seg, q_ss, q_rs;
+  int D, H, O;
+} scope_mlp_params;
+
+int scope_coeff_mlp_fwd(const scope_mlp_params* p, const uint16_t* q, const float* w1, const float* b1,
+                        const float* w2, const float* b2, uint16_t* y, void* stream);
+int scope_coeff_mlp_bwd(const scope_mlp_params* p, const uint16_t* q, const uint16_t* gy, const float* w1,
+                        const float* b1, const float* w2, const float* b2, uint16_t* dq, uint16_t* dz1,
+                        uint16_t* x1, uint16_t* gyp, void* stream);
+
+/* ------------------------------------------------------------------------
  * Sliding-window block masks of the layers without the pointer mask.
  * Replaces GPT.create_blockmasks (scoped_medium.py:535-576): the long (W)
  * and short (W // 2) masks of a window of W blocks.

@@ -51,10 +51,11 @@ def mlp_forward(sb, q: torch.Tensor) -> torch.Tensor:
     return torch.einsum("bhlk,hok->bhlo", x, sb.w2.to(dt)) + sb.b2.to(dt)[None, :, None, :]
 
 
-def coeff_head_forward(sb, q: torch.Tensor) -> tuple[torch.Tensor, ...]:
+def coeff_head_forward(sb, q: torch.Tensor, y: torch.Tensor | None = None) -> tuple[torch.Tensor, ...]:
     """The reference's 12-tuple (model/attn_bias.py:385-401) for q [B,H,L,D]
     from the parameters and schedule buffers of ``sb`` (a
-    ``scope_amd.SpectralBias``)."""
+    ``scope_amd.SpectralBias``); ``y`` replaces the MLP's output when given
+    (to check the head's arithmetic alone on another MLP's output)."""
     B, H, L, Dh = q.shape
     if H != sb.num_heads:
         raise ValueError(f"expected H={sb.num_heads}, got {H}")
@@ -72,7 +73,7 @@ def coeff_head_forward(sb, q: torch.Tensor) -> tuple[torch.Tensor, ...]:
         z_m = q.new_zeros((B, H, L, sb.M), dtype=torch.float32)
         z_pi = q.new_full((B, H, L, sb.M), 1.0 / sb.M, dtype=torch.float32)
         return z_k, z_k, z_l, z_l, z_m, z_pi, z_m, z_l, z_l, cos_wD, sin_wD, q.new_zeros((), dtype=torch.float32)
-    y = mlp_forward(sb, q).float()
+    y = (mlp_forward(sb, q) if y is None else y).float()
     M, K = sb.M, sb.K
     delta_raw, mu_raw, sigma_raw, pi_logits, budget_logits = (y[..., i * M:(i + 1) * M] for i in range(5))
     delta_cap = torch.clamp(sb._delta_star_max_active.to(device=device, dtype=torch.float32), 0.0, float(L - 1))

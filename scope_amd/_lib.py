@@ -67,6 +67,11 @@ class WgradParams(C.Structure):
                 ("a_rs", c_int64), ("b_ss", c_int64), ("b_rs", c_int64), ("round_bf16", c_int)]
 
 
+class MlpParams(C.Structure):
+    _fields_ = [("rows", c_int64), ("seg", c_int64), ("q_ss", c_int64), ("q_rs", c_int64), ("D", c_int), ("H", c_int),
+                ("O", c_int)]
+
+
 class DecodeParams(C.Structure):
     _fields_ = [("H", c_int), ("D", c_int), ("bs", c_int), ("maxkv", c_int), ("T_cap", c_int64), ("t", c_int64),
                 ("scale", c_float), ("q_sh", c_int64), ("k_sh", c_int64), ("k_st", c_int64), ("v_sh", c_int64),
@@ -93,6 +98,8 @@ _PROTOS = {
     "scope_coeff_head_bwd": (c_int, [C.POINTER(CoeffParams)] + [P] * 18),
     "scope_linear_wgrad_workspace_bytes": (c_int64, [C.POINTER(WgradParams)]),
     "scope_linear_wgrad": (c_int, [C.POINTER(WgradParams)] + [P] * 6),
+    "scope_coeff_mlp_fwd": (c_int, [C.POINTER(MlpParams)] + [P] * 7),
+    "scope_coeff_mlp_bwd": (c_int, [C.POINTER(MlpParams)] + [P] * 11),
     "scope_swa_width": (c_int, [c_int64, c_int, c_int]),
     "scope_swa_blockmask": (c_int, [P, c_int64, c_int, c_int, P, P, P, P, P, P, P, P]),
     "scope_stats_counts_len": (c_int64, [C.POINTER(StatsParams)]),

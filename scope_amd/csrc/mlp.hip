@@ -17,6 +17,8 @@
 // dW[32·mb + 8(r/4) + 4g + r%4][32·nb + lane % 32] in register r.
 #include <math.h>
 
+#include <algorithm>
+
 #include "attn_common.h"
 
 namespace scope {
@@ -226,6 +228,202 @@ void launch_wgrad(const WgradArgs& g, int groups, hipStream_t s) {
   hipLaunchKernelGGL((wgrad_kernel<MB, NB>), dim3(groups), dim3(kWgradThreads), 0, s, g);
 }
 
+
+// ---------------------------------------------------------------------------
+// The MLP itself, fused: forward y = W2·SiLU(W1·q + b1) + b2 per row and the
+// backward's row-wise part (model/attn_bias.py:271-276, 380-386; autograd of
+// two F.linear and a SiLU on bf16 rows).
+// ---------------------------------------------------------------------------
+// One 512-thread workgroup per CU walks tiles of 256 rows, 32 rows per
+// wavefront.  W1 [256][128] and W2^T [256][64] (the module's fp32 weights
+// rounded to bf16, as the reference's .to(q.dtype)) sit in LDS as swizzled
+// 256-byte-row tiles, so the attention kernels' operand reads serve both
+// orientations.  Per hidden block of 32 units (v_mfma_f32_32x32x16_bf16):
+//   Z^T = W1·X^T (A: W1 rows, B: the wavefront's rows of q in registers),
+//   x1 = SiLU(bf16(Z^T + b1)) in the C layout, which is directly the B
+//   operand of Y^T += W2·X1^T (A: W2^T through transpose reads).
+// The backward recomputes Z^T, takes dX1^T = W2^T·gY^T, dZ1 = SiLU'(z)·dx1
+// and dQ^T += W1^T·dZ1^T, and writes x1, dz1 and the output gradient padded
+// to 64 columns for the weight-gradient kernel above.  Every intermediate is
+// rounded to bf16 where the reference's bf16 tensors are.
+constexpr int kMlpD = 128, kMlpH = 256, kMlpOMax = 64;
+constexpr int kMlpThreads = 512;
+constexpr int kMlpTileRows = 256;  // 8 wavefronts x 32 rows
+
+struct MlpArgs {
+  const uint16_t* q;
+  int64_t rows, seg, q_ss, q_rs;  // row r of q: q + (r / seg)·q_ss + (r % seg)·q_rs (elements)
+  const float* w1;                // [256][128]
+  const float* b1;                // [256]
+  const float* w2;                // [O][256]
+  const float* b2;                // [O]
+  int O;
+  uint16_t* y;                    // forward: [rows][O]
+  const uint16_t* gy;             // backward: [rows][O]
+  uint16_t* dq;                   // [rows][128]
+  uint16_t* dz1;                  // [rows][256]
+  uint16_t* x1;                   // [rows][256]
+  uint16_t* gyp;                  // [rows][64], the output gradient padded with zeros
+};
+
+struct MlpLds {
+  uint16_t w1[kMlpH * 128];   // W1, swizzled rows of 128 (swz_off)
+  uint16_t w2t[kMlpH * 128];  // W2^T: row h holds W2[0..O-1][h], zeros up to column 63 (swz_off)
+  float b1[kMlpH];
+  float b2[kMlpOMax];
+};
+
+__device__ __forceinline__ float bf16_round(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
+
+__device__ __forceinline__ float mlp_sigmoid(float z) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
+}
+
+__device__ void mlp_load_weights(const MlpArgs& g, MlpLds& L, int tid) {
+  // W1: four consecutive columns per thread and step (one 8-byte LDS write)
+  for (int i = tid; i < kMlpH * kMlpD / 4; i += kMlpThreads) {
+    const int r = i / (kMlpD / 4), d = (i % (kMlpD / 4)) * 4;
+    const float4 w = *reinterpret_cast<const float4*>(g.w1 + r * kMlpD + d);
+    *reinterpret_cast<uint2*>(&L.w1[swz_off(r, d)]) = make_uint2(cvt_pk_bf16(w.x, w.y), cvt_pk_bf16(w.z, w.w));
+  }
+  // W2^T: element (h, o) = W2[o][h], zero for o >= O
+  for (int i = tid; i < kMlpH * kMlpOMax; i += kMlpThreads) {
+    const int h = i % kMlpH, o = i / kMlpH;
+    const float w = o < g.O ? g.w2[o * kMlpH + h] : 0.f;
+    L.w2t[swz_off(h, o)] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(w));
+  }
+  for (int i = tid; i < kMlpH; i += kMlpThreads) L.b1[i] = bf16_round(g.b1[i]);
+  for (int i = tid; i < kMlpOMax; i += kMlpThreads) L.b2[i] = i < g.O ? bf16_round(g.b2[i]) : 0.f;
+}
+
+// Z^T of hidden block hb for this wavefront's 32 rows (xb: the rows' q as B operands)
+__device__ __forceinline__ f32x16_t mlp_z(const MlpLds& L, const TileOffs& to, int hb, const uint4 (&xb)[8]) {
+  f32x16_t z = zero16();
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) z = mfma32(lds_row8_o(L.w1, to, 32 * hb, ks), xb[ks], z);
+  return z;
+}
+
+__global__ __launch_bounds__(kMlpThreads) void mlp_fwd_kernel(MlpArgs g) {
+  __shared__ MlpLds L;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, gq = lane / 32, lr = lane % 32;
+  mlp_load_weights(g, L, tid);
+  __syncthreads();
+  const TileOffs to = tile_offs(lane);
+  const int64_t tiles = (g.rows + kMlpTileRows - 1) / kMlpTileRows;
+  for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+    const int64_t row = t * kMlpTileRows + wave * 32 + lr;  // rows is a multiple of 32: whole wavefronts
+    if (t * kMlpTileRows + wave * 32 >= g.rows) break;
+    const uint16_t* qp = g.q + (row / g.seg) * g.q_ss + (row % g.seg) * g.q_rs + 8 * gq;
+    uint4 xb[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) xb[ks] = *reinterpret_cast<const uint4*>(qp + 16 * ks);
+    f32x16_t y[2] = {zero16(), zero16()};
+#pragma unroll
+    for (int hb = 0; hb < 8; ++hb) {
+      const f32x16_t z = mlp_z(L, to, hb, xb);
+      uint32_t w[8];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const int h0 = 32 * hb + 8 * (r / 4) + 4 * gq + r % 4;
+        const float z0 = bf16_round(z[r] + L.b1[h0]), z1 = bf16_round(z[r + 1] + L.b1[h0 + 1]);
+        w[r / 2] = cvt_pk_bf16(z0 * mlp_sigmoid(z0), z1 * mlp_sigmoid(z1));
+      }
+      const uint4 xp[2] = {make_uint4(w[0], w[1], w[2], w[3]), make_uint4(w[4], w[5], w[6], w[7])};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int ob = 0; ob < 2; ++ob) y[ob] = mfma32(lds_kmajor_o(L.w2t, to, 32 * hb + 16 * kk, ob), xp[kk], y[ob]);
+    }
+    uint16_t* yp = g.y + row * g.O;
+#pragma unroll
+    for (int ob = 0; ob < 2; ++ob)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = 32 * ob + 8 * (r / 4) + 4 * gq + r % 4;
+        if (o < g.O) yp[o] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y[ob][r] + L.b2[o]));
+      }
+  }
+}
+
+__global__ __launch_bounds__(kMlpThreads) void mlp_bwd_kernel(MlpArgs g) {
+  __shared__ MlpLds L;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, gq = lane / 32, lr = lane % 32;
+  mlp_load_weights(g, L, tid);
+  __syncthreads();
+  const TileOffs to = tile_offs(lane);
+  const int64_t tiles = (g.rows + kMlpTileRows - 1) / kMlpTileRows;
+  for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+    const int64_t row = t * kMlpTileRows + wave * 32 + lr;
+    if (t * kMlpTileRows + wave * 32 >= g.rows) break;
+    const uint16_t* qp = g.q + (row / g.seg) * g.q_ss + (row % g.seg) * g.q_rs + 8 * gq;
+    uint4 xb[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) xb[ks] = *reinterpret_cast<const uint4*>(qp + 16 * ks);
+    // the output gradient as B operands of dX1^T (k = outputs 16ks + 8gq .. +7), zero past O;
+    // the same values padded to 64 columns for the weight gradient
+    uint4 gb[4];
+    const uint16_t* gp = g.gy + row * g.O;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int o = 16 * ks + 8 * gq + 2 * j;
+        const uint32_t lo = o < g.O ? gp[o] : 0u, hi = o + 1 < g.O ? gp[o + 1] : 0u;
+        w[j] = lo | (hi << 16);
+      }
+      gb[ks] = make_uint4(w[0], w[1], w[2], w[3]);
+      *reinterpret_cast<uint4*>(g.gyp + row * kMlpOMax + 16 * ks + 8 * gq) = gb[ks];
+    }
+    f32x16_t dq[4] = {zero16(), zero16(), zero16(), zero16()};
+#pragma unroll
+    for (int hb = 0; hb < 8; ++hb) {
+      const f32x16_t z = mlp_z(L, to, hb, xb);
+      f32x16_t dx = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) dx = mfma32(lds_row8_o(L.w2t, to, 32 * hb, ks), gb[ks], dx);
+      uint32_t xw[8], dw[8];
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float xv[2], dv[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int h = 32 * hb + 8 * ((r + i) / 4) + 4 * gq + (r + i) % 4;
+          const float zz = bf16_round(z[r + i] + L.b1[h]);
+          const float s = mlp_sigmoid(zz);
+          xv[i] = zz * s;
+          // SiLU'(z)·dx1 with dx1 rounded to bf16 (the reference's gy·W2 is a bf16 tensor)
+          dv[i] = bf16_round(dx[r + i]) * s * (1.f + zz * (1.f - s));
+        }
+        xw[r / 2] = cvt_pk_bf16(xv[0], xv[1]);
+        dw[r / 2] = cvt_pk_bf16(dv[0], dv[1]);
+      }
+      // x1 and dz1 rows: hidden 32hb + 8q + 4gq .. +3 in register quad q
+      uint16_t* xr = g.x1 + row * kMlpH + 32 * hb + 4 * gq;
+      uint16_t* dr = g.dz1 + row * kMlpH + 32 * hb + 4 * gq;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        *reinterpret_cast<uint2*>(xr + 8 * qd) = make_uint2(xw[2 * qd], xw[2 * qd + 1]);
+        *reinterpret_cast<uint2*>(dr + 8 * qd) = make_uint2(dw[2 * qd], dw[2 * qd + 1]);
+      }
+      const uint4 dp[2] = {make_uint4(dw[0], dw[1], dw[2], dw[3]), make_uint4(dw[4], dw[5], dw[6], dw[7])};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int md = 0; md < 4; ++md) dq[md] = mfma32(lds_kmajor_o(L.w1, to, 32 * hb + 16 * kk, md), dp[kk], dq[md]);
+    }
+    // dq rows: columns 32md + 8q + 4gq .. +3 in register quad q
+    uint16_t* dqp = g.dq + row * kMlpD + 4 * gq;
+#pragma unroll
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+        *reinterpret_cast<uint2*>(dqp + 32 * md + 8 * qd) =
+            make_uint2(cvt_pk_bf16(dq[md][4 * qd], dq[md][4 * qd + 1]), cvt_pk_bf16(dq[md][4 * qd + 2], dq[md][4 * qd + 3]));
+  }
+}
+
 }  // namespace
 
 }  // namespace scope
@@ -281,4 +479,69 @@ extern "C" int scope_linear_wgrad(const scope_wgrad_params* p, const uint16_t* a
   hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((total + 63) / 64), dim3(256), 0, s, g.part, groups, M * N, M,
                      p->round_bf16, dw, db);
   return check_launch("linear weight gradient kernels");
+}
+
+static int mlp_check(const scope_mlp_params* p, const uint16_t* q, const float* w1, const float* b1, const float* w2,
+                     const float* b2, const char* who) {
+  SCOPE_REQUIRE(p && q && w1 && b1 && w2 && b2, "%s: null pointer", who);
+  SCOPE_REQUIRE(p->D == kMlpD && p->H == kMlpH && p->O >= 1 && p->O <= kMlpOMax,
+                "%s: (D, hidden, outputs) = (%d, %d, %d); the kernel takes (128, 256, 1..64)", who, p->D, p->H, p->O);
+  SCOPE_REQUIRE(p->rows > 0 && p->rows % 32 == 0, "%s: rows=%lld must be a positive multiple of 32", who,
+                (long long)p->rows);
+  SCOPE_REQUIRE(p->seg > 0 && p->rows % p->seg == 0, "%s: seg=%lld must divide rows", who, (long long)p->seg);
+  SCOPE_REQUIRE(p->q_rs >= kMlpD && p->q_rs % 8 == 0 && p->q_ss >= 0 && p->q_ss % 8 == 0,
+                "%s: q's row stride must cover a row and both strides be multiples of 8 elements", who);
+  SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(w1)) & 15) == 0,
+                "%s: q and w1 must start on a 16-byte boundary", who);
+  return 0;
+}
+
+static MlpArgs mlp_args(const scope_mlp_params* p, const uint16_t* q, const float* w1, const float* b1,
+                        const float* w2, const float* b2) {
+  MlpArgs g = {};
+  g.q = q;
+  g.rows = p->rows;
+  g.seg = p->seg;
+  g.q_ss = p->q_ss;
+  g.q_rs = p->q_rs;
+  g.w1 = w1;
+  g.b1 = b1;
+  g.w2 = w2;
+  g.b2 = b2;
+  g.O = p->O;
+  return g;
+}
+
+static int mlp_grid(int64_t rows) {
+  // one workgroup per CU (129 KB of LDS each), walking the 256-row tiles
+  const int64_t tiles = (rows + kMlpTileRows - 1) / kMlpTileRows;
+  return static_cast<int>(std::min<int64_t>(tiles, 256));
+}
+
+extern "C" int scope_coeff_mlp_fwd(const scope_mlp_params* p, const uint16_t* q, const float* w1, const float* b1,
+                                   const float* w2, const float* b2, uint16_t* y, void* stream) {
+  if (int rc = mlp_check(p, q, w1, b1, w2, b2, "scope_coeff_mlp_fwd")) return rc;
+  SCOPE_REQUIRE(y != nullptr, "scope_coeff_mlp_fwd: null output");
+  MlpArgs g = mlp_args(p, q, w1, b1, w2, b2);
+  g.y = y;
+  hipLaunchKernelGGL(mlp_fwd_kernel, dim3(mlp_grid(p->rows)), dim3(kMlpThreads), 0, as_stream(stream), g);
+  return check_launch("MLP forward kernel");
+}
+
+extern "C" int scope_coeff_mlp_bwd(const scope_mlp_params* p, const uint16_t* q, const uint16_t* gy, const float* w1,
+                                   const float* b1, const float* w2, const float* b2, uint16_t* dq, uint16_t* dz1,
+                                   uint16_t* x1, uint16_t* gyp, void* stream) {
+  if (int rc = mlp_check(p, q, w1, b1, w2, b2, "scope_coeff_mlp_bwd")) return rc;
+  SCOPE_REQUIRE(gy && dq && dz1 && x1 && gyp, "scope_coeff_mlp_bwd: null pointer");
+  SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(dq) | reinterpret_cast<uintptr_t>(dz1) | reinterpret_cast<uintptr_t>(x1) |
+                  reinterpret_cast<uintptr_t>(gyp)) & 15) == 0,
+                "scope_coeff_mlp_bwd: dq, dz1, x1 and gyp must start on a 16-byte boundary");
+  MlpArgs g = mlp_args(p, q, w1, b1, w2, b2);
+  g.gy = gy;
+  g.dq = dq;
+  g.dz1 = dz1;
+  g.x1 = x1;
+  g.gyp = gyp;
+  hipLaunchKernelGGL(mlp_bwd_kernel, dim3(mlp_grid(p->rows)), dim3(kMlpThreads), 0, as_stream(stream), g);
+  return check_launch("MLP backward kernel");
 }

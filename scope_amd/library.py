@@ -27,7 +27,8 @@ Operators (schemas are the decorated signatures below):
 * ``scope::coeff_head_fwd`` (+ autograd via ``scope::coeff_head_bwd``) — the
   coefficient head of SpectralBias.forward after its MLP (model/attn_bias.py:
   419-506);
-* ``scope::coeff_mlp`` (+ autograd whose weight and bias gradients run on
+* ``scope::coeff_mlp`` (+ autograd: the row-wise backward on one fused kernel,
+  ``scope::coeff_mlp_bwd``, the weight and bias gradients on
   ``scope::linear_wgrad``) — the head's shared MLP (model/attn_bias.py:271-276,
   380-386).
 
@@ -484,30 +485,42 @@ def _(a, b, round_bf16):
     return a.new_empty((a.shape[-1], b.shape[-1]), dtype=_F32), a.new_empty(a.shape[-1], dtype=_F32)
 
 
+@torch.library.custom_op(f"{_NS}::coeff_mlp_bwd", mutates_args=())
+def coeff_mlp_bwd(q: Tensor, gy: Tensor, w1: Tensor, b1: Tensor, w2: Tensor,
+                  b2: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The row-wise backward of the fused MLP: (dq, dz1, x1, gy padded to 64
+    columns), bf16, with z1 and x1 recomputed from q."""
+    return ops.coeff_mlp_bwd(q, gy, w1, b1, w2, b2)
+
+
+@coeff_mlp_bwd.register_fake
+def _(q, gy, w1, b1, w2, b2):
+    lead = tuple(q.shape[:-1])
+    return (q.new_empty(lead + (q.shape[-1],)), q.new_empty(lead + (w1.shape[0],)), q.new_empty(lead + (w1.shape[0],)),
+            q.new_empty(lead + (64,)))
+
+
 @torch.library.custom_op(f"{_NS}::coeff_mlp", mutates_args=())
-def coeff_mlp(q: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, b2: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+def coeff_mlp(q: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, b2: Tensor) -> Tensor:
     """The head's shared MLP on q [..., D]: y = Linear(w2, b2)(SiLU(Linear(w1,
-    b1)(q))) with the weights cast to q's dtype (model/attn_bias.py:380-386),
-    and the pre-activation z1 and activation x1 that its backward reuses."""
+    b1)(q))) with the weights cast to q's dtype (model/attn_bias.py:380-386).
+    bf16 rows of 128 with fp32 weights (the reference's default) run one fused
+    kernel; other dtypes and shapes the reference's torch steps."""
     ops._gpu("coeff_mlp", q, w1, b1, w2, b2)
+    if ops.coeff_mlp_fused(q, w1, w2):
+        return ops.coeff_mlp_fwd(q, w1, b1, w2, b2)
     dt = q.dtype
-    z1 = F.linear(q, w1.to(dt), b1.to(dt))
-    x1 = F.silu(z1)
-    return F.linear(x1, w2.to(dt), b2.to(dt)), z1, x1
+    return F.linear(F.silu(F.linear(q, w1.to(dt), b1.to(dt))), w2.to(dt), b2.to(dt))
 
 
 @coeff_mlp.register_fake
 def _(q, w1, b1, w2, b2):
-    lead = tuple(q.shape[:-1])
-    hid = lead + (w1.shape[0],)
-    return q.new_empty(lead + (w2.shape[0],)), q.new_empty(hid), q.new_empty(hid)
+    return q.new_empty(tuple(q.shape[:-1]) + (w2.shape[0],))
 
 
 def _mlp_setup(ctx, inputs, output):
-    q, w1, b1, w2, b2 = inputs
-    ctx.save_for_backward(q, w1, w2, output[1], output[2])
-    ctx.dtypes = (w1.dtype, b1.dtype, w2.dtype, b2.dtype)
-    ctx.set_materialize_grads(False)  # z1 and x1 are saved for the backward, not used: their gradients stay None
+    ctx.save_for_backward(*inputs)
+    ctx.set_materialize_grads(False)
 
 
 def _wgrad(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
@@ -524,31 +537,33 @@ def _wgrad(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
     return a2.t().matmul(b2).float(), a2.sum(0).float()
 
 
-def _mlp_backward(ctx, gy, gz1, gx1):
+def _mlp_backward(ctx, gy):
     """Autograd of the two F.linear and the SiLU (the reference's backward):
-    dx1 = gy·W2, dz1 = SiLU'(z1)·dx1, dq = dz1·W1 on the BLAS library; the
-    weight and bias gradients, whose contraction runs over all rows, on the
-    split-row kernel.  The weights' gradients are those of their bf16 copies
-    (rounded to bf16), in the weights' dtype."""
-    q, w1, w2, z1, x1 = ctx.saved_tensors
-    if gy is None and gz1 is None and gx1 is None:
+    dx1 = gy·W2, dz1 = SiLU'(z1)·dx1, dq = dz1·W1 with z1 and x1 recomputed
+    (one fused kernel for the forward's fused case, else the torch steps);
+    the weight and bias gradients, whose contraction runs over all rows, on
+    the split-row kernel.  The weights' gradients are those of their bf16
+    copies (rounded to bf16), in the weights' dtype."""
+    if gy is None:
         return None, None, None, None, None
+    q, w1, b1, w2, b2 = ctx.saved_tensors
     dt = q.dtype
-    t1, tb1, t2, tb2 = ctx.dtypes
-    dw2 = db2 = None
-    dx1 = gx1
-    if gy is not None:
+    O = w2.shape[0]
+    if ops.coeff_mlp_fused(q, w1, w2):
+        dq, dz1, x1, gyp = coeff_mlp_bwd(q, gy, w1, b1, w2, b2)
+        dw2, db2 = linear_wgrad(gyp, x1, True)
+        dw2, db2 = dw2[:O], db2[:O]
+        if not ctx.needs_input_grad[0]:
+            dq = None
+    else:
         gy = gy.to(dt)
-        dx1 = gy.matmul(w2.to(dt)) if dx1 is None else dx1 + gy.matmul(w2.to(dt))
+        z1 = F.linear(q, w1.to(dt), b1.to(dt))
+        x1 = F.silu(z1)
+        dz1 = torch.ops.aten.silu_backward(gy.matmul(w2.to(dt)), z1)
         dw2, db2 = _wgrad(gy, x1)
-        dw2, db2 = dw2.to(t2), db2.to(tb2)
-    dz1 = gz1
-    if dx1 is not None:
-        dz = torch.ops.aten.silu_backward(dx1, z1)
-        dz1 = dz if dz1 is None else dz1 + dz
-    dq = dz1.matmul(w1.to(dt)) if ctx.needs_input_grad[0] else None
+        dq = dz1.matmul(w1.to(dt)) if ctx.needs_input_grad[0] else None
     dw1, db1 = _wgrad(dz1, q)
-    return dq, dw1.to(t1), db1.to(tb1), dw2, db2
+    return dq, dw1.to(w1.dtype), db1.to(b1.dtype), dw2.to(w2.dtype), db2.to(b2.dtype)
 
 
 coeff_mlp.register_autograd(_mlp_backward, setup_context=_mlp_setup)

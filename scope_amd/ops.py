@@ -362,6 +362,57 @@ def linear_wgrad(a: torch.Tensor, b: torch.Tensor, *, round_bf16: bool = True, w
     return dw, db
 
 
+def _mlp_params(q: torch.Tensor, w2: torch.Tensor):
+    lq = _row_layout(q)
+    if lq is None:
+        q = q.contiguous()
+        lq = _row_layout(q)
+    rows, seg, ss, rs = lq
+    if seg == rows:
+        ss = 0
+    return q, _lib.MlpParams(rows=rows, seg=seg, q_ss=ss, q_rs=rs, D=q.shape[-1], H=256, O=w2.shape[0])
+
+
+def coeff_mlp_fused(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> bool:
+    """Whether the fused MLP kernels take these operands: bf16 rows of 128, fp32
+    contiguous weights [256][128] and [O][256] with O <= 64, rows a multiple of
+    32 (otherwise the operator runs the reference's torch steps)."""
+    return (q.dtype == torch.bfloat16 and q.shape[-1] == 128 and w1.dtype == torch.float32
+            and w2.dtype == torch.float32 and tuple(w1.shape) == (256, 128) and w2.dim() == 2
+            and w2.shape[1] == 256 and 1 <= w2.shape[0] <= 64 and q.numel() // 128 % 32 == 0 and q.numel() > 0)
+
+
+def coeff_mlp_fwd(q: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor,
+                  b2: torch.Tensor) -> torch.Tensor:
+    """y [..., O] = W2·SiLU(W1·q + b1) + b2 on bf16 rows of q [..., 128] with the
+    fp32 weights rounded to bf16 (model/attn_bias.py:271-276, 380-386)."""
+    dev = _gpu("coeff_mlp_fwd", q, w1, b1, w2, b2)
+    w1, b1, w2, b2 = (t.contiguous() for t in (w1, b1, w2, b2))
+    qc, prm = _mlp_params(q, w2)
+    y = torch.empty(q.shape[:-1] + (w2.shape[0],), dtype=q.dtype, device=dev)
+    call("scope_coeff_mlp_fwd", C.byref(prm), _p(qc), _p(w1), _p(b1), _p(w2), _p(b2), _p(y), _stream(dev))
+    return y
+
+
+def coeff_mlp_bwd(q: torch.Tensor, gy: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor,
+                  b2: torch.Tensor):
+    """The row-wise part of the MLP's backward: (dq [..., 128], dz1 [..., 256],
+    x1 [..., 256], gy padded to [..., 64]), bf16, from the output gradient gy
+    [..., O]; z1 and x1 are recomputed from q."""
+    dev = _gpu("coeff_mlp_bwd", q, gy, w1, b1, w2, b2)
+    w1, b1, w2, b2 = (t.contiguous() for t in (w1, b1, w2, b2))
+    qc, prm = _mlp_params(q, w2)
+    gy = gy.to(q.dtype).contiguous()
+    lead = q.shape[:-1]
+    dq = torch.empty(lead + (128,), dtype=q.dtype, device=dev)
+    dz1 = torch.empty(lead + (256,), dtype=q.dtype, device=dev)
+    x1 = torch.empty(lead + (256,), dtype=q.dtype, device=dev)
+    gyp = torch.empty(lead + (64,), dtype=q.dtype, device=dev)
+    call("scope_coeff_mlp_bwd", C.byref(prm), _p(qc), _p(gy), _p(w1), _p(b1), _p(w2), _p(b2), _p(dq), _p(dz1),
+         _p(x1), _p(gyp), _stream(dev))
+    return dq, dz1, x1, gyp
+
+
 def coeff_head_bwd(y: torch.Tensor, prm: dict, omegas: torch.Tensor, log_omegas: torch.Tensor,
                    cos_mean: torch.Tensor | None, sin_mean: torch.Tensor | None, grads: dict,
                    g_reg: torch.Tensor | None = None, reg: torch.Tensor | None = None) -> torch.Tensor:

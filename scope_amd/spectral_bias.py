@@ -231,12 +231,12 @@ class SpectralBias(nn.Module):
             q = q.detach()
         dt = q.dtype
         if self.share_across_heads:
-            # the two F.linear and the SiLU of the reference, as one operator whose
-            # backward runs the weight and bias gradients (a contraction over all
-            # B·H·T rows) on the split-row kernel
+            # the two F.linear and the SiLU of the reference, as one operator (one
+            # fused kernel each way) whose weight and bias gradients (a
+            # contraction over all B·H·T rows) run on the split-row kernel
             fc1: nn.Linear = self.mlp[0]
             fc2: nn.Linear = self.mlp[2]
-            return library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias)[0]
+            return library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias)
         x = torch.einsum("bhld,hkd->bhlk", q, self.w1.to(dt)) + self.b1.to(dt)[None, :, None, :]
         x = F.silu(x)
         return torch.einsum("bhlk,hok->bhlo", x, self.w2.to(dt)) + self.b2.to(dt)[None, :, None, :]

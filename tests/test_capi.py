@@ -51,13 +51,14 @@ def test_prototypes_cover_header():
 
 
 def test_ctypes_struct_layouts_match_c():
-    from scope_amd._lib import (AttnParams, CoeffParams, DecodeParams, PtrBwdParams, PtrRefParams, PtrScoreParams,
-                                StatsParams, WgradParams)
+    from scope_amd._lib import (AttnParams, CoeffParams, DecodeParams, MlpParams, PtrBwdParams, PtrRefParams,
+                                PtrScoreParams, StatsParams, WgradParams)
 
     structs = {"scope_ptr_ref_params": PtrRefParams, "scope_ptr_score_params": PtrScoreParams,
                "scope_stats_params": StatsParams, "scope_attn_params": AttnParams,
                "scope_ptr_bwd_params": PtrBwdParams, "scope_coeff_params": CoeffParams,
-               "scope_decode_params": DecodeParams, "scope_wgrad_params": WgradParams}
+               "scope_decode_params": DecodeParams, "scope_wgrad_params": WgradParams,
+               "scope_mlp_params": MlpParams}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')

@@ -6,12 +6,13 @@ weight-gradient kernel (``scope_linear_wgrad``) under it.
   [1, H, T, N] view (rows in head segments, as the transposed q of the
   reference) and a 2-D; the bound is 1e-5 of Σ_r |a||b| (fp32 accumulation
   of exact bf16 products) unrounded, plus half a bf16 ulp rounded.
-* ``coeff_mlp`` against autograd of the reference's steps
+* ``coeff_mlp`` (fused kernels) against autograd of the reference's steps
   (oracle.coeff_head.mlp_forward: F.linear, SiLU, F.linear with the weights
   cast to bf16), at the reference's default shape (D=128, hidden 256, 41
-  outputs): y, z1 and x1 bit for bit (the same torch ops), dq within 1e-3 of
-  max|dq| (the same BLAS calls; autograd may pick another kernel), and the
-  weight and bias gradients within a bf16 ulp plus 1e-5 of Σ|a||b|."""
+  outputs): y, dq and the weight and bias gradients at least as close to
+  fp64 arithmetic on the same bf16 operands as the torch steps are (1.5x
+  their error, max and mean); the backward's x1 and dz1 against the torch
+  steps but for one-ulp rounding flips; fp32 rows on the torch steps."""
 from __future__ import annotations
 
 import pytest
@@ -70,8 +71,27 @@ def test_linear_wgrad_rejects_bad_shapes():
         ops.linear_wgrad(a, b)
 
 
+def _mlp64(q, w1, b1, w2, b2, gy):
+    """fp64 forward and row-wise backward of the MLP from the same bf16 operands
+    (the weights rounded to bf16, no intermediate rounding): y, dq, z."""
+    q64 = q.reshape(-1, q.shape[-1]).double()
+    w1d, b1d, w2d, b2d = (t.bfloat16().double() for t in (w1, b1, w2, b2))
+    z = q64 @ w1d.t() + b1d
+    s = torch.sigmoid(z)
+    y = (z * s) @ w2d.t() + b2d
+    dx1 = gy.reshape(-1, gy.shape[-1]).double() @ w2d
+    dq = (dx1 * s * (1 + z * (1 - s))) @ w1d
+    return y, dq, z
+
+
 @pytest.mark.parametrize("T", [2048, 16384])
 def test_coeff_mlp_matches_reference_autograd(T):
+    """The fused forward and backward against autograd of the reference's torch
+    steps (F.linear, SiLU, F.linear in bf16): both are compared with fp64
+    arithmetic on the same bf16 operands, and the fused kernels must be at
+    least as accurate (within 1.5x of the torch steps' error, max and mean) —
+    bit equality is not expected, the two sum in different orders and round
+    their bf16 intermediates at different boundaries."""
     H, D = 8, 128
     sb = SpectralBias(head_dim=D, num_heads=H, L_train=T, K=6, M=8).to(DEV).train()
     g = torch.Generator(device=DEV).manual_seed(T)
@@ -92,24 +112,64 @@ def test_coeff_mlp_matches_reference_autograd(T):
         return out.detach(), q.grad, [p_.grad.clone() for p_ in params]
 
     fc1, fc2 = sb.mlp[0], sb.mlp[2]
-    y_op, dq_op, gw_op = run(lambda q: library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias)[0])
+    assert ops.coeff_mlp_fused(q0, fc1.weight, fc2.weight)
+    y_op, dq_op, gw_op = run(lambda q: library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias))
     y_ref, dq_ref, gw_ref = run(lambda q: mlp_forward(sb, q))
-    assert torch.equal(y_op, y_ref)
-    with torch.no_grad():
-        z1, x1 = library.coeff_mlp(q0, fc1.weight, fc1.bias, fc2.weight, fc2.bias)[1:]
-        z_ref = torch.nn.functional.linear(q0, fc1.weight.bfloat16(), fc1.bias.bfloat16())
-    assert torch.equal(z1, z_ref) and torch.equal(x1, torch.nn.functional.silu(z_ref))
-    tol = 1e-3 * float(dq_ref.float().abs().max())
-    assert float((dq_op.float() - dq_ref.float()).abs().max()) <= tol
-    # the gradients' inputs: gy with x1 (fc2), dz1 with q (fc1)
-    dx1 = gy.matmul(fc2.weight.bfloat16())
-    dz1 = torch.ops.aten.silu_backward(dx1, z1)
-    for got, ref, (a, b) in zip(gw_op, gw_ref, [(dz1, q0), (dz1, None), (gy, x1), (gy, None)]):
-        a64 = a.reshape(-1, a.shape[-1]).double()
-        if b is None:
-            bound = 1e-5 * a64.abs().sum(0)
-        else:
-            bound = 1e-5 * (a64.abs().t() @ b.reshape(-1, b.shape[-1]).double().abs())
-        bound = bound + ref.double().abs() * 2.0 ** -7 + 1e-30
-        err = (got.double() - ref.double()).abs()
-        assert bool((err <= bound).all()), f"worst {float((err / bound).max()):.3f} of the bound"
+    assert y_op.shape == y_ref.shape and y_op.dtype == y_ref.dtype and dq_op.shape == q0.shape
+    y64, dq64, _ = _mlp64(q0, fc1.weight, fc1.bias, fc2.weight, fc2.bias, gy)
+    for got, ref, exact in ((y_op, y_ref, y64), (dq_op, dq_ref, dq64)):
+        e_got = (got.reshape(exact.shape).double() - exact).abs()
+        e_ref = (ref.reshape(exact.shape).double() - exact).abs()
+        assert float(e_got.max()) <= 1.5 * float(e_ref.max()) + 1e-6
+        assert float(e_got.mean()) <= 1.5 * float(e_ref.mean()) + 1e-7
+    # the weight and bias gradients, likewise against fp64 from the same operands
+    q64 = q0.reshape(-1, D).double()
+    g64 = gy.reshape(-1, gy.shape[-1]).double()
+    w1d, b1d, w2d = (t.bfloat16().double() for t in (fc1.weight, fc1.bias, fc2.weight))
+    z = q64 @ w1d.t() + b1d
+    sg = torch.sigmoid(z)
+    dz = (g64 @ w2d) * sg * (1 + z * (1 - sg))
+    exact = [dz.t() @ q64, dz.sum(0), g64.t() @ (z * sg), g64.sum(0)]
+    for got, ref, ex in zip(gw_op, gw_ref, exact):
+        e_got, e_ref = (got.double() - ex).abs(), (ref.double() - ex).abs()
+        floor = 1e-6 * float(ex.abs().max())
+        assert float(e_got.max()) <= 1.5 * float(e_ref.max()) + floor
+        assert float(e_got.mean()) <= 1.5 * float(e_ref.mean()) + floor
+
+
+def test_coeff_mlp_bwd_intermediates():
+    """x1, dz1 and the padded output gradient of the fused backward against
+    the torch steps on the same rows: x1 = SiLU(bf16(q·W1 + b1)) and
+    dz1 = SiLU'(z1)·bf16(gy·W2) agree but for rare one-ulp flips at bf16
+    rounding boundaries; the padding is gy itself and zeros."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    rows, O = 4096, 41
+    q = torch.randn((rows, 128), generator=g, device=DEV).to(torch.bfloat16)
+    w1 = torch.randn((256, 128), generator=g, device=DEV) * 0.05
+    b1 = torch.randn(256, generator=g, device=DEV) * 0.05
+    w2 = torch.randn((O, 256), generator=g, device=DEV) * 0.05
+    b2 = torch.randn(O, generator=g, device=DEV) * 0.05
+    gy = torch.randn((rows, O), generator=g, device=DEV).to(torch.bfloat16)
+    dq, dz1, x1, gyp = ops.coeff_mlp_bwd(q, gy, w1, b1, w2, b2)
+    torch.cuda.synchronize()
+    z_ref = torch.nn.functional.linear(q, w1.bfloat16(), b1.bfloat16())
+    x_ref = torch.nn.functional.silu(z_ref)
+    dz_ref = torch.ops.aten.silu_backward(gy.matmul(w2.bfloat16()), z_ref)
+    assert torch.equal(gyp[:, :O], gy) and not bool(gyp[:, O:].any())
+    for got, ref in ((x1, x_ref), (dz1, dz_ref)):
+        diff = (got.float() - ref.float()).abs()
+        ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
+        assert bool((diff <= 2 * ulp + 1e-6).all())
+        assert float((diff > 0).float().mean()) < 0.02
+
+
+def test_coeff_mlp_fp32_takes_the_torch_steps():
+    """fp32 rows are not the fused kernels' case: the operator runs the
+    reference's torch steps, equal to the oracle's forward."""
+    H, D, T = 2, 128, 256
+    sb = SpectralBias(head_dim=D, num_heads=H, L_train=T, K=6, M=8).to(DEV).train()
+    q = torch.randn((1, H, T, D), device=DEV)
+    fc1, fc2 = sb.mlp[0], sb.mlp[2]
+    assert not ops.coeff_mlp_fused(q, fc1.weight, fc2.weight)
+    y = library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias)
+    assert torch.equal(y, mlp_forward(sb, q))
