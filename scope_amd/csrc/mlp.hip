@@ -244,8 +244,11 @@ void launch_wgrad(const WgradArgs& g, int groups, hipStream_t s) {
 //   operand of Y^T += W2·X1^T (A: W2^T through transpose reads).
 // The backward recomputes Z^T, takes dX1^T = W2^T·gY^T, dZ1 = SiLU'(z)·dx1
 // and dQ^T += W1^T·dZ1^T, and writes x1, dz1 and the output gradient padded
-// to 64 columns for the weight-gradient kernel above.  Every intermediate is
-// rounded to bf16 where the reference's bf16 tensors are.
+// to 64 columns for the weight-gradient kernel above.  b1 enters Z^T as one
+// more k-step (a row of ones against the bias).  Every intermediate is
+// rounded to bf16 where the reference's tensors are (z1, x1, dx1, dz1): the
+// head's outputs downstream (the peak positions among them) are not
+// continuous in y, so the MLP keeps the reference's rounding points.
 constexpr int kMlpD = 128, kMlpH = 256, kMlpOMax = 64;
 constexpr int kMlpThreads = 512;
 constexpr int kMlpTileRows = 256;  // 8 wavefronts x 32 rows
@@ -269,7 +272,7 @@ struct MlpArgs {
 struct MlpLds {
   uint16_t w1[kMlpH * 128];   // W1, swizzled rows of 128 (swz_off)
   uint16_t w2t[kMlpH * 128];  // W2^T: row h holds W2[0..O-1][h], zeros up to column 63 (swz_off)
-  float b1[kMlpH];
+  uint16_t b1[kMlpH];  // bf16 bits: the A operand of the bias k-step
   float b2[kMlpOMax];
 };
 
@@ -280,25 +283,52 @@ __device__ __forceinline__ float mlp_sigmoid(float z) {
 }
 
 __device__ void mlp_load_weights(const MlpArgs& g, MlpLds& L, int tid) {
-  // W1: four consecutive columns per thread and step (one 8-byte LDS write)
-  for (int i = tid; i < kMlpH * kMlpD / 4; i += kMlpThreads) {
-    const int r = i / (kMlpD / 4), d = (i % (kMlpD / 4)) * 4;
-    const float4 w = *reinterpret_cast<const float4*>(g.w1 + r * kMlpD + d);
-    *reinterpret_cast<uint2*>(&L.w1[swz_off(r, d)]) = make_uint2(cvt_pk_bf16(w.x, w.y), cvt_pk_bf16(w.z, w.w));
+  // every load of the thread is issued before the first conversion (a loop
+  // of load, convert, store waits one memory latency per step)
+  constexpr int N1 = kMlpH * kMlpD / 4 / kMlpThreads;  // float4 of W1 per thread: 16
+  constexpr int N2 = kMlpH * kMlpOMax / kMlpThreads;   // elements of W2^T per thread: 32
+  float4 w1v[N1];
+  float w2v[N2];
+#pragma unroll
+  for (int j = 0; j < N1; ++j) {
+    const int i = tid + j * kMlpThreads, r = i / (kMlpD / 4), d = (i % (kMlpD / 4)) * 4;
+    w1v[j] = *reinterpret_cast<const float4*>(g.w1 + r * kMlpD + d);
   }
-  // W2^T: element (h, o) = W2[o][h], zero for o >= O
-  for (int i = tid; i < kMlpH * kMlpOMax; i += kMlpThreads) {
-    const int h = i % kMlpH, o = i / kMlpH;
-    const float w = o < g.O ? g.w2[o * kMlpH + h] : 0.f;
-    L.w2t[swz_off(h, o)] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(w));
+#pragma unroll
+  for (int j = 0; j < N2; ++j) {
+    // element (h, o) of W2^T = W2[o][h]: consecutive threads read consecutive h
+    const int i = tid + j * kMlpThreads, h = i % kMlpH, o = i / kMlpH;
+    w2v[j] = o < g.O ? g.w2[o * kMlpH + h] : 0.f;
   }
-  for (int i = tid; i < kMlpH; i += kMlpThreads) L.b1[i] = bf16_round(g.b1[i]);
-  for (int i = tid; i < kMlpOMax; i += kMlpThreads) L.b2[i] = i < g.O ? bf16_round(g.b2[i]) : 0.f;
+  const float b1v = g.b1[tid % kMlpH];
+  const float b2v = tid < g.O ? g.b2[tid] : 0.f;
+#pragma unroll
+  for (int j = 0; j < N1; ++j) {
+    const int i = tid + j * kMlpThreads, r = i / (kMlpD / 4), d = (i % (kMlpD / 4)) * 4;
+    *reinterpret_cast<uint2*>(&L.w1[swz_off(r, d)]) =
+        make_uint2(cvt_pk_bf16(w1v[j].x, w1v[j].y), cvt_pk_bf16(w1v[j].z, w1v[j].w));
+  }
+#pragma unroll
+  for (int j = 0; j < N2; ++j) {
+    const int i = tid + j * kMlpThreads, h = i % kMlpH, o = i / kMlpH;
+    L.w2t[swz_off(h, o)] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(w2v[j]));
+  }
+  if (tid < kMlpH) L.b1[tid] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(b1v));
+  if (tid < kMlpOMax) L.b2[tid] = bf16_round(b2v);
 }
 
-// Z^T of hidden block hb for this wavefront's 32 rows (xb: the rows' q as B operands)
-__device__ __forceinline__ f32x16_t mlp_z(const MlpLds& L, const TileOffs& to, int hb, const uint4 (&xb)[8]) {
-  f32x16_t z = zero16();
+// The bias as one more k-step of Z^T = W1·X^T + b1·1^T: A holds b1 of the
+// lane's hidden unit in slot 0 of lane group 0 (k = 0), B a row of ones
+// (kOnes: 1.0 in k = 0, lane group 0), every other product zero.
+__device__ __forceinline__ uint4 mlp_bias_a(const MlpLds& L, int hb, int lr, int gq) {
+  return make_uint4(gq == 0 ? static_cast<uint32_t>(L.b1[32 * hb + lr]) : 0u, 0u, 0u, 0u);
+}
+__device__ __forceinline__ uint4 mlp_ones_b(int gq) { return make_uint4(gq == 0 ? 0x3F80u : 0u, 0u, 0u, 0u); }
+
+// Z^T + b1 of hidden block hb for this wavefront's 32 rows (xb: the rows' q as B operands)
+__device__ __forceinline__ f32x16_t mlp_z(const MlpLds& L, const TileOffs& to, int hb, const uint4 (&xb)[8], int lr,
+                                          int gq) {
+  f32x16_t z = mfma32(mlp_bias_a(L, hb, lr, gq), mlp_ones_b(gq), zero16());
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) z = mfma32(lds_row8_o(L.w1, to, 32 * hb, ks), xb[ks], z);
   return z;
@@ -318,22 +348,35 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_fwd_kernel(MlpArgs g) {
     uint4 xb[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) xb[ks] = *reinterpret_cast<const uint4*>(qp + 16 * ks);
+    // software pipeline over the hidden blocks: the Z^T MFMAs of block hb+1
+    // (operands read at the top of the step) run under the SiLU of block hb
     f32x16_t y[2] = {zero16(), zero16()};
+    f32x16_t z = mlp_z(L, to, 0, xb, lr, gq);
 #pragma unroll
     for (int hb = 0; hb < 8; ++hb) {
-      const f32x16_t z = mlp_z(L, to, hb, xb);
+      uint4 an[8], aw[4];
+      if (hb < 7) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) an[ks] = lds_row8_o(L.w1, to, 32 * (hb + 1), ks);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) aw[i] = lds_kmajor_o(L.w2t, to, 32 * hb + 16 * (i / 2), i % 2);
+      f32x16_t zn = zero16();
+      if (hb < 7) {
+        zn = mfma32(mlp_bias_a(L, hb + 1, lr, gq), mlp_ones_b(gq), zn);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) zn = mfma32(an[ks], xb[ks], zn);
+      }
       uint32_t w[8];
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const int h0 = 32 * hb + 8 * (r / 4) + 4 * gq + r % 4;
-        const float z0 = bf16_round(z[r] + L.b1[h0]), z1 = bf16_round(z[r + 1] + L.b1[h0 + 1]);
+        const float z0 = bf16_round(z[r]), z1 = bf16_round(z[r + 1]);  // z1 is a bf16 tensor in the reference
         w[r / 2] = cvt_pk_bf16(z0 * mlp_sigmoid(z0), z1 * mlp_sigmoid(z1));
       }
       const uint4 xp[2] = {make_uint4(w[0], w[1], w[2], w[3]), make_uint4(w[4], w[5], w[6], w[7])};
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int ob = 0; ob < 2; ++ob) y[ob] = mfma32(lds_kmajor_o(L.w2t, to, 32 * hb + 16 * kk, ob), xp[kk], y[ob]);
+      for (int i = 0; i < 4; ++i) y[i % 2] = mfma32(aw[i], xp[i / 2], y[i % 2]);
+      z = zn;
     }
     uint16_t* yp = g.y + row * g.O;
 #pragma unroll
@@ -376,25 +419,39 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_bwd_kernel(MlpArgs g) {
       gb[ks] = make_uint4(w[0], w[1], w[2], w[3]);
       *reinterpret_cast<uint4*>(g.gyp + row * kMlpOMax + 16 * ks + 8 * gq) = gb[ks];
     }
+    // per hidden block: Z^T and dX1^T, the VALU work, the dQ^T products (the
+    // other wavefront of the SIMD fills the gaps; holding the next block's
+    // accumulators as well would spill)
     f32x16_t dq[4] = {zero16(), zero16(), zero16(), zero16()};
+    auto zdx = [&](int hb, f32x16_t& z, f32x16_t& dx) __attribute__((always_inline)) {
+      uint4 an[8], ag[4];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) an[ks] = lds_row8_o(L.w1, to, 32 * hb, ks);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) ag[ks] = lds_row8_o(L.w2t, to, 32 * hb, ks);
+      z = mfma32(mlp_bias_a(L, hb, lr, gq), mlp_ones_b(gq), zero16());
+      dx = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        z = mfma32(an[ks], xb[ks], z);
+        if (ks < 4) dx = mfma32(ag[ks], gb[ks], dx);
+      }
+    };
 #pragma unroll
     for (int hb = 0; hb < 8; ++hb) {
-      const f32x16_t z = mlp_z(L, to, hb, xb);
-      f32x16_t dx = zero16();
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) dx = mfma32(lds_row8_o(L.w2t, to, 32 * hb, ks), gb[ks], dx);
+      f32x16_t z, dx;
+      zdx(hb, z, dx);
       uint32_t xw[8], dw[8];
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         float xv[2], dv[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          const int h = 32 * hb + 8 * ((r + i) / 4) + 4 * gq + (r + i) % 4;
-          const float zz = bf16_round(z[r + i] + L.b1[h]);
-          const float s = mlp_sigmoid(zz);
-          xv[i] = zz * s;
-          // SiLU'(z)·dx1 with dx1 rounded to bf16 (the reference's gy·W2 is a bf16 tensor)
-          dv[i] = bf16_round(dx[r + i]) * s * (1.f + zz * (1.f - s));
+          // z1 and dx1 = gy·W2 are bf16 tensors in the reference
+          const float zz = bf16_round(z[r + i]);
+          const float sg = mlp_sigmoid(zz);
+          xv[i] = zz * sg;
+          dv[i] = bf16_round(dx[r + i]) * (sg * fmaf(zz, 1.f - sg, 1.f));  // SiLU'(z1)·dx1
         }
         xw[r / 2] = cvt_pk_bf16(xv[0], xv[1]);
         dw[r / 2] = cvt_pk_bf16(dv[0], dv[1]);
@@ -409,9 +466,7 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_bwd_kernel(MlpArgs g) {
       }
       const uint4 dp[2] = {make_uint4(dw[0], dw[1], dw[2], dw[3]), make_uint4(dw[4], dw[5], dw[6], dw[7])};
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int md = 0; md < 4; ++md) dq[md] = mfma32(lds_kmajor_o(L.w1, to, 32 * hb + 16 * kk, md), dp[kk], dq[md]);
+      for (int i = 0; i < 8; ++i) dq[i % 4] = mfma32(lds_kmajor_o(L.w1, to, 32 * hb + 16 * (i / 4), i % 4), dp[i / 4], dq[i % 4]);
     }
     // dq rows: columns 32md + 8q + 4gq .. +3 in register quad q
     uint16_t* dqp = g.dq + row * kMlpD + 4 * gq;
