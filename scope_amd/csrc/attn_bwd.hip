@@ -1929,10 +1929,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float glam = a.beta_log2 * a.ramp_lambda;
     float rs = 0.f, pm = 0.f;
     uint32_t dw[8], pw[8];
+    // the causal and document mask only on the tiles that need it (a mask-free
+    // copy for the rest, in every mode)
+    auto probs = [&](auto mask_tag) __attribute__((always_inline)) {
+      constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int kb4 = 0; kb4 < 4; ++kb4) {
       int dcv[4] = {0, 0, 0, 0};
-      if (TOK || !full) {
+      if (MASK) {
         const int4 d4 = *reinterpret_cast<const int4*>(&b.docs[16 * kb4 + 4 * g]);
         dcv[0] = d4.x, dcv[1] = d4.y, dcv[2] = d4.z, dcv[3] = d4.w;
       }
@@ -1960,7 +1964,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         } else {
           x = fmaf(s[kb4][r], cs, off);
         }
-        if (TOK || !full) x = mask_score(x, j, lim, dcv[r], doc);
+        if (MASK) x = mask_score(x, j, lim, dcv[r], doc);
         const float p = __builtin_amdgcn_exp2f(x);
         const float d = p * dp[kb4][r];  // dP accumulator started from -Δ
         dv[r] = d;
@@ -1983,6 +1987,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       pw[2 * kb4] = cvt_pk_bf16(pv[0], pv[1]);
       pw[2 * kb4 + 1] = cvt_pk_bf16(pv[2], pv[3]);
     }
+    };
+    if (full) probs(std::false_type{});
+    else probs(std::true_type{});
     // B operands of k-step kk: blocks 2kk (slots 0-3) and 2kk+1 (slots 4-7)
     uint4 dsb[2], pb[2];
 #pragma unroll

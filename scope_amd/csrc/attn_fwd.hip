@@ -237,7 +237,9 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
         s[mb] = mfma32(fl, qf, s[mb]);
       }
     }
-    if (TOK || !full) fwd_scores<MODE, true>(a, b, R, kv0, lane, s);
+    // token modes add their per-element terms on every tile, the mask only where it is needed
+    if (!full) fwd_scores<MODE, true>(a, b, R, kv0, lane, s);
+    else if (TOK) fwd_scores<MODE, false>(a, b, R, kv0, lane, s);
     // exponent = s·csm + off: modes 0/1 keep raw scores (csm = scale·log2e > 0)
     const float csm = TOK ? 1.f : a.scale_log2;
     if (MASS) {
