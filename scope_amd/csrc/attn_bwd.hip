@@ -1363,11 +1363,12 @@ __device__ __forceinline__ void dkv16_probs(const AttnArgs& a, const DkvBuf<MODE
       dcv[0] = dc4.x, dcv[1] = dc4.y, dcv[2] = dc4.z, dcv[3] = dc4.w;
     }
     float pv[4], dv[4];
+    const float dfb = static_cast<float>(q0 + qi0 - wkv);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float x;
       if constexpr (TOK) {
-        const float df = static_cast<float>(q0 + qi0 + i - wkv);
+        const float df = dfb + static_cast<float>(i);  // q - wkv, exact in fp32
         float e = slv[i] * df;
         if constexpr (GATE) {
           // softplus(x) = max(x,0) + ln2·log2(1 + 2^(-|x|·log2 e)); relu drops the second term
@@ -1925,6 +1926,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     // probabilities and dS^T: key j = 16·kb4 + 4g + r of the tile
     const int lim = row - kv0;  // keys j <= lim are causal
+    const float dfl = static_cast<float>(lim - 4 * g);
     const bool softplus = a.gate_kind == SCOPE_GATE_SOFTPLUS;
     const float glam = a.beta_log2 * a.ramp_lambda;
     float rs = 0.f, pm = 0.f;
@@ -1947,7 +1949,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         float x;
         float sig = 0.f, sgn = 0.f, df = 0.f;
         if (TOK) {
-          df = static_cast<float>(lim - j);
+          df = dfl - static_cast<float>(16 * kb4 + r);  // lim - j, exact in fp32
           float e = slp * df;
           if (GATE) {
             const float dd = df - dm;

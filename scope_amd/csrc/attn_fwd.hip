@@ -58,6 +58,9 @@ __device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>
   const float glam = a.beta_log2 * a.ramp_lambda;
   const float spw = a.gate_kind == SCOPE_GATE_SOFTPLUS ? kLn2 : 0.f;
   const int lim = R.row - kv0;  // keys j <= lim are causal
+  // slope term slp·(lim - j), j = jc + 4g with jc a constant of the register:
+  // fma(-slp, jc, slp·(lim - 4g)) (the integers are exact in fp32)
+  const float sbase = GATE ? 0.f : R.slp * static_cast<float>(lim - 4 * g);
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -74,7 +77,7 @@ __device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>
         float x;
         if (TOK) {
           const float df = static_cast<float>(lim - j);
-          float e = R.slp * df;
+          float e = GATE ? R.slp * df : fmaf(-R.slp, static_cast<float>(mb * 32 + 8 * rq + i), sbase);
           if (GATE) {
             // softplus(x) = max(x,0) + ln2·log2(1 + 2^(-|x|·log2 e)); relu drops the second term
             const float xx = (fabsf(df - R.dm) - R.wd) * a.inv_tau;
