@@ -46,404 +46,6 @@ struct DqRow {
   int row, doc;
 };
 
-// Probabilities and dS^T of one tile for this lane's query row, as bf16 B
-// operands of dQ^T = K^T·dS^T (k index: the 64 keys, slot order of
-// lds_kmajor), plus the per-row sums the bias gradients need.
-template <int MODE, bool MASK>
-__device__ __forceinline__ void dq_probs(const AttnArgs& a, const KvTile<MODE>& b, const DqRow& R, int kv0, float off,
-                                         int lane, const f32x16_t (&s)[2], const f32x16_t (&dpv)[2],
-                                         uint4 (&dsb)[4], uint4 (&pbv)[4], float& rs, float& pm, float (&ex)[6]) {
-  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
-  const int g = lane >> 5;
-  const float cs = a.scale_log2;
-  const float glam = a.beta_log2 * a.ramp_lambda;
-  const bool softplus = a.gate_kind == SCOPE_GATE_SOFTPLUS;
-  const int lim = R.row - kv0;  // keys j <= lim are causal
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      float dsv[8], pvv[8];
-      int dcv[8];
-      if (MASK) {
-        const int4 d0 = *reinterpret_cast<const int4*>(&b.docs[mb * 32 + 16 * hf + 4 * g]);
-        const int4 d1 = *reinterpret_cast<const int4*>(&b.docs[mb * 32 + 16 * hf + 8 + 4 * g]);
-        dcv[0] = d0.x, dcv[1] = d0.y, dcv[2] = d0.z, dcv[3] = d0.w;
-        dcv[4] = d1.x, dcv[5] = d1.y, dcv[6] = d1.z, dcv[7] = d1.w;
-      }
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int r = hf * 8 + jj;
-        const int j = mb * 32 + 8 * (r / 4) + 4 * g + (r % 4);  // key within the tile
-        float x;
-        float sig = 0.f, sgn = 0.f, df = 0.f;
-        if (TOK) {
-          df = static_cast<float>(lim - j);
-          float e = R.slp * df;
-          if (GATE) {
-            const float dd = df - R.dm;
-            const float xx = (fabsf(dd) - R.wd) * a.inv_tau;
-            const float en = __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e);
-            const float inv = __builtin_amdgcn_rcpf(1.f + en);
-            const float lp = kLn2 * __builtin_amdgcn_logf(1.f + en);
-            const float gt = fmaxf(xx, 0.f) + (softplus ? lp : 0.f);
-            sig = softplus ? (xx >= 0.f ? inv : en * inv) : (xx > 0.f ? 1.f : 0.f);
-            sgn = dd > 0.f ? 1.f : (dd < 0.f ? -1.f : 0.f);
-            e -= glam * gt;
-          }
-          x = fmaf(s[mb][r], cs, e + off);
-        } else {
-          x = fmaf(s[mb][r], cs, off);
-        }
-        if (MASK) x = mask_score(x, j, lim, dcv[jj], R.doc);
-        const float p = __builtin_amdgcn_exp2f(x);
-        const float d = p * (dpv[mb][r] - R.delta);
-        dsv[jj] = d;
-        pvv[jj] = p;
-        rs += d;
-        pm += p;
-        if (TOK) {
-          ex[0] += d * df;
-          ex[3] += p * df;
-          if (GATE) {
-            ex[1] += d * sig * sgn;
-            ex[2] += d * sig;
-            ex[4] += p * sig * sgn;
-            ex[5] += p * sig;
-          }
-        }
-      }
-      dsb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(dsv[0], dsv[1]), cvt_pk_bf16(dsv[2], dsv[3]),
-                                    cvt_pk_bf16(dsv[4], dsv[5]), cvt_pk_bf16(dsv[6], dsv[7]));
-      if (TOK)
-        pbv[mb * 2 + hf] = make_uint4(cvt_pk_bf16(pvv[0], pvv[1]), cvt_pk_bf16(pvv[2], pvv[3]),
-                                      cvt_pk_bf16(pvv[4], pvv[5]), cvt_pk_bf16(pvv[6], pvv[7]));
-    }
-}
-
-template <int BS, int MODE>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
-  constexpr int SPLIT = BS / 128;  // workgroups per q-block (4 wavefronts = 128 query rows each)
-  constexpr int BN = 64;           // keys per staged tile
-  constexpr int NSUB = BS / BN;
-  constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
-
-  __shared__ KvTile<MODE> buf0, buf1;
-  __shared__ int kbs[kListLds];
-  __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
-
-  const int tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int h = tile / (a.QB * SPLIT), qb = (tile / SPLIT) % a.QB, part = tile % SPLIT;
-  const int64_t q0 = static_cast<int64_t>(qb) * BS + part * 128;
-  const int wrow_lo = static_cast<int>(q0) + wave * 32;
-  const int64_t hT = static_cast<int64_t>(h) * a.T;
-  DqRow R;
-  R.row = wrow_lo + lr;
-
-  const int64_t lrow = static_cast<int64_t>(h) * a.QB + qb;
-  const int n = min(a.kv_num[lrow], a.maxkv);  // maxkv <= kListLds
-  const int32_t* lst = a.kv_idx + lrow * a.maxkv;
-  for (int t = tid; t < min(n, kListLds); t += 256) kbs[t] = lst[t];
-  const bool pbias = a.pair_bias != nullptr;
-  if (pbias)
-    for (int t = tid; t < min(n, kListLds); t += 256) kbias[t] = a.pair_bias[lrow * a.maxkv + t] * kLog2e;
-
-  uint4 qreg[8], doreg[8];
-  {
-    const uint16_t* qp = a.q + h * a.q_sh + R.row * a.q_st + g * 8;
-    const uint16_t* op = a.o + h * a.o_sh + R.row * a.o_st + g * 8;
-    const uint16_t* dp = a.dout + h * a.o_sh + R.row * a.o_st + g * 8;
-    float dsum = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      qreg[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
-      doreg[ks] = *reinterpret_cast<const uint4*>(dp + ks * 16);
-      const uint4 ov = *reinterpret_cast<const uint4*>(op + ks * 16);
-      const uint32_t dw[4] = {doreg[ks].x, doreg[ks].y, doreg[ks].z, doreg[ks].w};
-      const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        dsum += __uint_as_float(dw[i] << 16) * __uint_as_float(ow[i] << 16);
-        dsum += __uint_as_float(dw[i] & 0xffff0000u) * __uint_as_float(ow[i] & 0xffff0000u);
-      }
-    }
-    R.delta = dsum + __shfl_xor(dsum, 32, 64);
-  }
-  const float lse_nat = a.lse[hT + R.row];
-  R.lse2 = lse_nat == -INFINITY ? INFINITY : lse_nat * kLog2e;
-
-  // ---- bias set-up (as in the forward)
-  float ca[8], sa[8];
-  uint4 qf = make_uint4(0, 0, 0, 0), qfl = make_uint4(0, 0, 0, 0);
-  R.rowc = R.slp = R.dm = R.wd = 0.f;
-  float cos_i[4], sin_i[4];  // token mode: cos/sin(ω_k row) for k = 4g..4g+3
-  if (MODE == 1) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      ca[k] = k < a.K ? a.coeff_cos[(hT + R.row) * a.K + k] * a.beta_log2 : 0.f;
-      sa[k] = k < a.K ? a.coeff_sin[(hT + R.row) * a.K + k] * a.beta_log2 : 0.f;
-    }
-  }
-  if (TOK) {
-    token_qfeat(a, hT, R.row, g, qf, qfl, cos_i, sin_i);
-    // kept for pass B, which stages them per query tile
-    *reinterpret_cast<uint4*>(a.qfeat + (hT + R.row) * kTokRow + g * 8) = qf;
-    *reinterpret_cast<uint4*>(a.qfeat + (hT + R.row) * kTokRow + 16 + g * 8) = qfl;
-    if (a.subtract_b0) R.rowc = -a.beta_log2 * a.b0[hT + R.row];
-    if (a.use_slope) R.slp = a.beta_log2 * a.slope[hT + R.row];
-    if (GATE) {
-      R.dm = a.delta_main[hT + R.row];
-      R.wd = a.width[hT + R.row];
-    }
-  }
-  const int ds_end = a.ds_tok_end[qb];
-  R.doc = a.docs[R.row];
-  const TileOffs to = tile_offs(lane);
-
-  f32x16_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = zero16();
-  // Bias gradients use Δ_true = Σ_j P dP rather than the Δ of the bf16
-  // output: since Σ_j P = 1, the row total Σ_j dS equals Δ_true - Δ, so each
-  // per-tile sum is corrected by subtracting that total times the tile's
-  // probability mass (the *P accumulators hold the P-weighted sums).  All
-  // sums stay per lane (half the keys of the row) until the epilogue.
-  f32x16_t facc = zero16(), facc_p = zero16();
-  float accA[8], accB[8], accPA[8], accPB[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) accA[k] = accB[k] = accPA[k] = accPB[k] = 0.f;
-  float rs_tot = 0.f, pm_tot = 0.f;
-  float ex[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // Σ dS·df, dS·σ·sgn, dS·σ, then the P-weighted three
-
-  // flat iteration index it = list entry · NSUB + key sub-tile; sub-tiles that
-  // start after this workgroup's last row are skipped
-  const int total = n * NSUB;
-  const int qmax = static_cast<int>(q0) + 127;
-  // the list lives in LDS (width <= kListLds, checked on the host): a read that
-  // could also reach global memory would be a flat load, whose wait also waits
-  // for the tile copies in flight
-  auto kb_at = [&](int t) __attribute__((always_inline)) { return kbs[t]; };
-  auto next_valid = [&](int it) __attribute__((always_inline)) {
-    while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
-    return it;
-  };
-  auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
-    const int kb = kb_at(it / NSUB);
-    const int rd = min(max(qb - kb, 0), a.QB - 1);
-    kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
-  };
-  // block mode: the bias term and the per-row sums dS, P change per key block
-  // (four 64-key tiles), not per tile
-  float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
-  float eb = 0.f;  // pair bias of the current list entry (log2 units)
-  auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
-    const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
-    const float tconst = (MODE == 1 ? bt : R.rowc) + eb;
-    // S^T and dP^T: keys in two 32-row blocks (A operand), this lane's query row as the column
-    f32x16_t s[2], dpv[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      s[mb] = zero16();
-      dpv[mb] = zero16();
-    }
-    // four independent accumulator chains interleaved (dependent MFMAs stall);
-    // operands one k-step ahead, each step's reads issued before its MFMAs
-    uint4 ka[2][2], va[2][2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      ka[0][mb] = lds_row8_o(b.k, to, mb * 32, 0);
-      va[0][mb] = lds_row8_o(b.v, to, mb * 32, 0);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-        if (ks + 1 < 8) {
-          ka[(ks + 1) % 2][mb] = lds_row8_o(b.k, to, mb * 32, ks + 1);
-          va[(ks + 1) % 2][mb] = lds_row8_o(b.v, to, mb * 32, ks + 1);
-        }
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        s[mb] = mfma32(ka[ks % 2][mb], qreg[ks], s[mb]);
-        dpv[mb] = mfma32(va[ks % 2][mb], doreg[ks], dpv[mb]);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (TOK) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const uint4 fh = lds_row8_32(b.f, mb * 32 + lr, g * 8);
-        const uint4 fl = lds_row8_32(b.f, mb * 32 + lr, 16 + g * 8);
-        s[mb] = mfma32(fh, qf, s[mb]);
-        s[mb] = mfma32(fh, qfl, s[mb]);
-        s[mb] = mfma32(fl, qf, s[mb]);
-      }
-    }
-    const float off = tconst - R.lse2;
-    uint4 dsb[4], pbv[4];
-    float rs = 0.f, pm = 0.f;
-    if (TOK || !full)
-      dq_probs<MODE, true>(a, b, R, kv0, off, lane, s, dpv, dsb, pbv, rs, pm, ex);
-    else
-      dq_probs<MODE, false>(a, b, R, kv0, off, lane, s, dpv, dsb, pbv, rs, pm, ex);
-    // dQ^T += K^T dS^T (and the token-mode feature sums); step st: k-step
-    // st/4, columns 32·(st%4), operands two steps ahead
-    {
-      uint4 ta[3];
-      ta[0] = lds_kmajor_o(b.k, to, 0, 0);
-      ta[1] = lds_kmajor_o(b.k, to, 0, 1);
-#pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        if (st + 2 < 16) ta[(st + 2) % 3] = lds_kmajor_o(b.k, to, 16 * ((st + 2) / 4), (st + 2) % 4);
-        o[st % 4] = mfma32(ta[st % 3], dsb[st / 4], o[st % 4]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    if (TOK) {
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const uint4 ft = lds_kmajor_32(b.f, 16 * s2, lane);
-        facc = mfma32(ft, dsb[s2], facc);
-        facc_p = mfma32(ft, pbv[s2], facc_p);
-      }
-    }
-    rs_kb += rs;
-    pm_kb += pm;
-    rs_tot += rs;
-    pm_tot += pm;
-  };
-  auto run = [&](int it, int nxt, const KvTile<MODE>& b) __attribute__((always_inline)) {
-    const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
-    if (MODE == 1 && it % NSUB == 0) {
-      // a key block's first tile is never skipped (it starts at or before every row)
-      const float4* t4 = reinterpret_cast<const float4*>(b.tab);
-      const float4 c0 = t4[0], c1 = t4[1], s0 = t4[2], s1 = t4[3];
-      bt = (ca[0] * c0.x + ca[1] * c0.y + ca[2] * c0.z + ca[3] * c0.w) +
-           (ca[4] * c1.x + ca[5] * c1.y + ca[6] * c1.z + ca[7] * c1.w) +
-           (sa[0] * s0.x + sa[1] * s0.y + sa[2] * s0.z + sa[3] * s0.w) +
-           (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
-    }
-    if (it % NSUB == 0) eb = pbias ? kbias[it / NSUB] : 0.f;  // per key block (its first tile is never skipped)
-    if (kv0 <= wrow_lo + 31) compute(kv0, b);  // else every key follows this wavefront's rows
-    if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
-      // last tile of this key block: fold its sums into the coefficient gradients
-      const float4* t4 = reinterpret_cast<const float4*>(b.tab);
-      const float tb[16] = {t4[0].x, t4[0].y, t4[0].z, t4[0].w, t4[1].x, t4[1].y, t4[1].z, t4[1].w,
-                            t4[2].x, t4[2].y, t4[2].z, t4[2].w, t4[3].x, t4[3].y, t4[3].z, t4[3].w};
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        accA[k] += rs_kb * tb[k];
-        accB[k] += rs_kb * tb[8 + k];
-        accPA[k] += pm_kb * tb[k];
-        accPB[k] += pm_kb * tb[8 + k];
-      }
-      rs_kb = pm_kb = 0.f;
-    }
-  };
-
-  __syncthreads();  // kbs
-  int cur = next_valid(0);
-  if (cur < total) issue(cur, buf0);
-  while (cur < total) {
-    wait_vm0();
-    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
-    int nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf1);
-    run(cur, nxt, buf0);
-    cur = nxt;
-    if (cur >= total) break;
-    wait_vm0();
-    __syncthreads();
-    nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf0);
-    run(cur, nxt, buf1);
-    cur = nxt;
-  }
-
-  // ---- modes 0/1: this row's softmax offset for every listed key block (the
-  // block term as in the loop, plus the pair bias, minus lse), read per tile
-  // by the kv-major pass
-  if (MODE <= 1 && g == 0) {
-    float* rof = a.roff + lrow * a.maxkv * BS + (R.row - qb * BS);
-    for (int e = 0; e < n; ++e) {
-      float t = pbias ? kbias[e] : 0.f;
-      if (MODE == 1) {
-        const int rd = min(max(qb - kb_at(e), 0), a.QB - 1);
-        const float4* t4 = reinterpret_cast<const float4*>(static_cast<const float*>(a.table) + rd * 16);
-        const float4 c0 = t4[0], c1 = t4[1], s0 = t4[2], s1 = t4[3];
-        t += (ca[0] * c0.x + ca[1] * c0.y + ca[2] * c0.z + ca[3] * c0.w) +
-             (ca[4] * c1.x + ca[5] * c1.y + ca[6] * c1.z + ca[7] * c1.w) +
-             (sa[0] * s0.x + sa[1] * s0.y + sa[2] * s0.z + sa[3] * s0.w) +
-             (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
-      }
-      rof[e * BS] = t - R.lse2;
-    }
-  }
-
-  // ---- epilogue: combine the lane pair's half sums, dQ = scale·o
-  rs_tot += __shfl_xor(rs_tot, 32, 64);
-  pm_tot += __shfl_xor(pm_tot, 32, 64);
-  const float dd_err = rs_tot;  // Δ_true - Δ
-  // the kv-major pass reads Δ_true = Δ + (Δ_true - Δ): its dS, dK and the
-  // pair-bias sums then do not carry the bf16 rounding of the output
-  if (g == 0) a.delta[hT + R.row] = -(R.delta + dd_err);  // stored negated: the kv-major dP accumulators start from it
-  uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
-#pragma unroll
-  for (int md = 0; md < 4; ++md)
-#pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      uint2 val;
-      val.x = cvt_pk_bf16(o[md][4 * rq] * a.scale, o[md][4 * rq + 1] * a.scale);
-      val.y = cvt_pk_bf16(o[md][4 * rq + 2] * a.scale, o[md][4 * rq + 3] * a.scale);
-      *reinterpret_cast<uint2*>(dqp + md * 32 + 8 * rq) = val;
-    }
-  const float beta = a.beta;
-  if (MODE == 1 && a.dcoeff_cos) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      accA[k] += __shfl_xor(accA[k], 32, 64);
-      accB[k] += __shfl_xor(accB[k], 32, 64);
-      accPA[k] += __shfl_xor(accPA[k], 32, 64);
-      accPB[k] += __shfl_xor(accPB[k], 32, 64);
-    }
-    if (g == 0)
-      for (int k = 0; k < a.K; ++k) {
-        a.dcoeff_cos[(hT + R.row) * a.K + k] = beta * (accA[k] - dd_err * accPA[k]);
-        a.dcoeff_sin[(hT + R.row) * a.K + k] = beta * (accB[k] - dd_err * accPB[k]);
-      }
-  }
-  if (TOK) {
-    if (a.dcoeff_cos) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int k = 4 * g + i;
-        if (k < a.K) {
-          // feature rows: 4g+i (cos hi), 8+4g+i (sin hi), 16+4g+i (cos lo), 24+4g+i (sin lo)
-          const float C = (facc[i] + facc[8 + i]) - dd_err * (facc_p[i] + facc_p[8 + i]);
-          const float S = (facc[4 + i] + facc[12 + i]) - dd_err * (facc_p[4 + i] + facc_p[12 + i]);
-          a.dcoeff_cos[(hT + R.row) * a.K + k] = beta * (cos_i[i] * C + sin_i[i] * S);
-          a.dcoeff_sin[(hT + R.row) * a.K + k] = beta * (sin_i[i] * C - cos_i[i] * S);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 6; ++i) ex[i] += __shfl_xor(ex[i], 32, 64);
-    if (g == 0) {
-      if (a.db0) a.db0[hT + R.row] = -beta * (rs_tot - dd_err * pm_tot);
-      if (a.dslope) a.dslope[hT + R.row] = beta * (ex[0] - dd_err * ex[3]);
-      const float gsc = beta * a.ramp_lambda * a.inv_tau;
-      if (a.ddelta_main) a.ddelta_main[hT + R.row] = GATE ? gsc * (ex[1] - dd_err * ex[4]) : 0.f;
-      if (a.dwidth) a.dwidth[hT + R.row] = GATE ? gsc * (ex[2] - dd_err * ex[5]) : 0.f;
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // pass A, two wavefronts per SIMD (block size 256, no bias or block bias)
 // ---------------------------------------------------------------------------
@@ -484,7 +86,7 @@ __device__ __forceinline__ void dq2_probs(const KvTile<MODE>& b, const DqRow& R,
 
 template <int BS, int MODE>
 __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
-  static_assert(MODE <= 1, "token modes use attn_bwd_dq_kernel");
+  static_assert(MODE <= 1, "token modes use attn_bwd_dq16_kernel");
   constexpr int NT = 2 * BS;  // BS/32 wavefronts of 32 query rows: the whole q-block
   constexpr int BN = 64;      // keys per staged tile, processed in two 32-key halves
   constexpr int NSUB = BS / BN;
@@ -1765,8 +1367,10 @@ __device__ __forceinline__ float sum_groups16(float x) {
 // then dQ^T += K^T·dS^T and, in token modes, the feature gradient
 // dF^T += F^T·dS^T (and its P-weighted twin for the Δ correction) from
 // transpose reads.  Eight wavefronts (128 rows) per workgroup, two per SIMD;
-// every mode, both block sizes.  The math per element, the sums and the
-// epilogue's outputs are those of attn_bwd_dq_kernel.
+// every mode, both block sizes (the gated mode takes a tile's four 16-key
+// blocks in two halves to fit its registers).  It stores Δ_true (negated) and,
+// in modes 0/1, every row's softmax offset per listed key block for the
+// kv-major pass, and the token modes' query features.
 template <int BS, int MODE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq16_kernel(AttnArgs a) {
   constexpr int SPLIT = BS / 128;  // workgroups per q-block (8 wavefronts = 128 query rows each)
@@ -1827,7 +1431,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float ca[8], sa[8];
   uint4 qf1 = make_uint4(0, 0, 0, 0), qf2 = make_uint4(0, 0, 0, 0);
   float rowc = 0.f, slp = 0.f, dm = 0.f, wd = 0.f;
-  float cos_i[4], sin_i[4];  // token mode, lane groups 0 and 1: cos/sin(ω_k row) for k = 4g..4g+3
+  // token mode: cos/sin(ω_k row) of the bands k = 4g..4g+3 are read again in the
+  // epilogue (keeping them live through the tile loop costs registers)
   if (MODE == 1) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -1838,7 +1443,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (TOK) {
     // the row's features: half g % 2 (cos half, sin half), hi and lo bf16 parts
     uint4 hi, lo;
-    token_qfeat(a, hT, row, g & 1, hi, lo, cos_i, sin_i);
+    token_qfeat(a, hT, row, g & 1, hi, lo, nullptr, nullptr);
     qf1 = hi;                                     // [q_hi | q_hi]
     if (g < 2) qf2 = lo;                          // [q_lo | 0]
     if (g < 2) {
@@ -1859,9 +1464,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   f32x4_t dqT[8];  // dQ^T: D rows 16·md + 4g + r, this lane's query row
 #pragma unroll
   for (int i = 0; i < 8; ++i) dqT[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // Δ correction of the bias gradients, as in attn_bwd_dq_kernel: every sum
-  // has a P-weighted twin; all stay per lane (a quarter of the row's keys)
-  // until the epilogue
+  // Bias gradients use Δ_true = Σ_j P dP rather than the Δ of the bf16
+  // output: since Σ_j P = 1, the row total Σ_j dS equals Δ_true - Δ, so each
+  // per-tile sum is corrected by subtracting that total times the tile's
+  // probability mass (every sum has a P-weighted twin).  All stay per lane
+  // (a quarter of the row's keys) until the epilogue.
   f32x4_t facc[2], facc_p[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) facc[i] = facc_p[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -1889,41 +1496,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
     const float off = (MODE == 1 ? bt : rowc) + eb - lse2;
-    // S^T and dP^T - Δ per 16-key block kb4 (step st = 4·ks + kb4), operands two steps ahead
-    f32x4_t s[4], dp[4];
-#pragma unroll
-    for (int kb4 = 0; kb4 < 4; ++kb4) {
-      s[kb4] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      dp[kb4] = f32x4_t{-delta, -delta, -delta, -delta};
-    }
-    constexpr int RA = 2;
-    uint4 ka[RA + 1], va[RA + 1];
-#pragma unroll
-    for (int i = 0; i < RA; ++i) {
-      ka[i] = lds_row16(b.k, to, i % 4, i / 4);
-      va[i] = lds_row16(b.v, to, i % 4, i / 4);
-    }
-#pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const int ks = st / 4, kb4 = st % 4;
-      if (st + RA < 16) {
-        ka[(st + RA) % (RA + 1)] = lds_row16(b.k, to, (st + RA) % 4, (st + RA) / 4);
-        va[(st + RA) % (RA + 1)] = lds_row16(b.v, to, (st + RA) % 4, (st + RA) / 4);
-      }
-      s[kb4] = mfma16(ka[st % (RA + 1)], qreg[ks], s[kb4]);
-      dp[kb4] = mfma16(va[st % (RA + 1)], doreg[ks], dp[kb4]);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (TOK) {
-#pragma unroll
-      for (int kb4 = 0; kb4 < 4; ++kb4) {
-        const uint4 fa = lds_row8_32(b.f, 16 * kb4 + c, 8 * g);
-        s[kb4] = mfma16(fa, qf1, s[kb4]);
-        s[kb4] = mfma16(fa, qf2, s[kb4]);
-      }
-    }
     // probabilities and dS^T: key j = 16·kb4 + 4g + r of the tile
     const int lim = row - kv0;  // keys j <= lim are causal
     const float dfl = static_cast<float>(lim - 4 * g);
@@ -1931,67 +1503,111 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float glam = a.beta_log2 * a.ramp_lambda;
     float rs = 0.f, pm = 0.f;
     uint32_t dw[8], pw[8];
-    // the causal and document mask only on the tiles that need it (a mask-free
-    // copy for the rest, in every mode)
-    auto probs = [&](auto mask_tag) __attribute__((always_inline)) {
-      constexpr bool MASK = decltype(mask_tag)::value;
+    // The gated mode takes the tile's four 16-key blocks in two halves (the
+    // S and dP accumulators of two blocks live at a time); the others at once.
+    constexpr int NH = GATE ? 2 : 1, KB = 4 / NH;
 #pragma unroll
-    for (int kb4 = 0; kb4 < 4; ++kb4) {
-      int dcv[4] = {0, 0, 0, 0};
-      if (MASK) {
-        const int4 d4 = *reinterpret_cast<const int4*>(&b.docs[16 * kb4 + 4 * g]);
-        dcv[0] = d4.x, dcv[1] = d4.y, dcv[2] = d4.z, dcv[3] = d4.w;
+    for (int hh = 0; hh < NH; ++hh) {
+      // S^T and dP^T - Δ per 16-key block kb4 = KB·hh + kl (step st = KB·ks + kl),
+      // operands RA steps ahead
+      f32x4_t s[KB], dp[KB];
+#pragma unroll
+      for (int kl = 0; kl < KB; ++kl) {
+        s[kl] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        dp[kl] = f32x4_t{-delta, -delta, -delta, -delta};
       }
-      float dv[4], pv[4];
+      constexpr int RA = 2;
+      constexpr int NST = 4 * KB;
+      uint4 ka[RA + 1], va[RA + 1];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * kb4 + 4 * g + r;
-        float x;
-        float sig = 0.f, sgn = 0.f, df = 0.f;
-        if (TOK) {
-          df = dfl - static_cast<float>(16 * kb4 + r);  // lim - j, exact in fp32
-          float e = slp * df;
-          if (GATE) {
-            const float dd = df - dm;
-            const float xx = (fabsf(dd) - wd) * a.inv_tau;
-            const float en = __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e);
-            const float inv = __builtin_amdgcn_rcpf(1.f + en);
-            const float lp = kLn2 * __builtin_amdgcn_logf(1.f + en);
-            const float gt = fmaxf(xx, 0.f) + (softplus ? lp : 0.f);
-            sig = softplus ? (xx >= 0.f ? inv : en * inv) : (xx > 0.f ? 1.f : 0.f);
-            sgn = dd > 0.f ? 1.f : (dd < 0.f ? -1.f : 0.f);
-            e -= glam * gt;
-          }
-          x = fmaf(s[kb4][r], cs, e + off);
-        } else {
-          x = fmaf(s[kb4][r], cs, off);
+      for (int i = 0; i < RA; ++i) {
+        ka[i] = lds_row16(b.k, to, KB * hh + i % KB, i / KB);
+        va[i] = lds_row16(b.v, to, KB * hh + i % KB, i / KB);
+      }
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const int ks = st / KB, kl = st % KB;
+        if (st + RA < NST) {
+          ka[(st + RA) % (RA + 1)] = lds_row16(b.k, to, KB * hh + (st + RA) % KB, (st + RA) / KB);
+          va[(st + RA) % (RA + 1)] = lds_row16(b.v, to, KB * hh + (st + RA) % KB, (st + RA) / KB);
         }
-        if (MASK) x = mask_score(x, j, lim, dcv[r], doc);
-        const float p = __builtin_amdgcn_exp2f(x);
-        const float d = p * dp[kb4][r];  // dP accumulator started from -Δ
-        dv[r] = d;
-        pv[r] = p;
-        rs += d;
-        pm += p;
-        if (TOK) {
-          ex[0] += d * df;
-          ex[3] += p * df;
-          if (GATE) {
-            ex[1] += d * sig * sgn;
-            ex[2] += d * sig;
-            ex[4] += p * sig * sgn;
-            ex[5] += p * sig;
-          }
+        s[kl] = mfma16(ka[st % (RA + 1)], qreg[ks], s[kl]);
+        dp[kl] = mfma16(va[st % (RA + 1)], doreg[ks], dp[kl]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (TOK) {
+#pragma unroll
+        for (int kl = 0; kl < KB; ++kl) {
+          const uint4 fa = lds_row8_32(b.f, 16 * (KB * hh + kl) + c, 8 * g);
+          s[kl] = mfma16(fa, qf1, s[kl]);
+          s[kl] = mfma16(fa, qf2, s[kl]);
         }
       }
-      dw[2 * kb4] = cvt_pk_bf16(dv[0], dv[1]);
-      dw[2 * kb4 + 1] = cvt_pk_bf16(dv[2], dv[3]);
-      pw[2 * kb4] = cvt_pk_bf16(pv[0], pv[1]);
-      pw[2 * kb4 + 1] = cvt_pk_bf16(pv[2], pv[3]);
+      // the causal and document mask only on the tiles that need it (a
+      // mask-free copy for the rest, in every mode)
+      auto probs = [&](auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+#pragma unroll
+        for (int kl = 0; kl < KB; ++kl) {
+          const int kb4 = KB * hh + kl;
+          int dcv[4] = {0, 0, 0, 0};
+          if (MASK) {
+            const int4 d4 = *reinterpret_cast<const int4*>(&b.docs[16 * kb4 + 4 * g]);
+            dcv[0] = d4.x, dcv[1] = d4.y, dcv[2] = d4.z, dcv[3] = d4.w;
+          }
+          float dv[4], pv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = 16 * kb4 + 4 * g + r;
+            float x;
+            float sig = 0.f, sgn = 0.f, df = 0.f;
+            if (TOK) {
+              df = dfl - static_cast<float>(16 * kb4 + r);  // lim - j, exact in fp32
+              float e = slp * df;
+              if (GATE) {
+                const float dd = df - dm;
+                const float xx = (fabsf(dd) - wd) * a.inv_tau;
+                const float en = __builtin_amdgcn_exp2f(-fabsf(xx) * kLog2e);
+                const float inv = __builtin_amdgcn_rcpf(1.f + en);
+                const float lp = kLn2 * __builtin_amdgcn_logf(1.f + en);
+                const float gt = fmaxf(xx, 0.f) + (softplus ? lp : 0.f);
+                sig = softplus ? (xx >= 0.f ? inv : en * inv) : (xx > 0.f ? 1.f : 0.f);
+                sgn = dd > 0.f ? 1.f : (dd < 0.f ? -1.f : 0.f);
+                e -= glam * gt;
+              }
+              x = fmaf(s[kl][r], cs, e + off);
+            } else {
+              x = fmaf(s[kl][r], cs, off);
+            }
+            if (MASK) x = mask_score(x, j, lim, dcv[r], doc);
+            const float p = __builtin_amdgcn_exp2f(x);
+            const float d = p * dp[kl][r];  // dP accumulator started from -Δ
+            dv[r] = d;
+            pv[r] = p;
+            rs += d;
+            pm += p;
+            if (TOK) {
+              ex[0] += d * df;
+              ex[3] += p * df;
+              if (GATE) {
+                ex[1] += d * sig * sgn;
+                ex[2] += d * sig;
+                ex[4] += p * sig * sgn;
+                ex[5] += p * sig;
+              }
+            }
+          }
+          dw[2 * kb4] = cvt_pk_bf16(dv[0], dv[1]);
+          dw[2 * kb4 + 1] = cvt_pk_bf16(dv[2], dv[3]);
+          pw[2 * kb4] = cvt_pk_bf16(pv[0], pv[1]);
+          pw[2 * kb4 + 1] = cvt_pk_bf16(pv[2], pv[3]);
+        }
+      };
+      if (full) probs(std::false_type{});
+      else probs(std::true_type{});
     }
-    };
-    if (full) probs(std::false_type{});
-    else probs(std::true_type{});
     // B operands of k-step kk: blocks 2kk (slots 0-3) and 2kk+1 (slots 4-7)
     uint4 dsb[2], pb[2];
 #pragma unroll
@@ -2131,8 +1747,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const int k = 4 * g + i;
           if (k < a.K) {
             const float Cc = C[i] - dd_err * Cp[i], Sc = S[i] - dd_err * Sp[i];
-            a.dcoeff_cos[(hT + row) * a.K + k] = beta * (cos_i[i] * Cc + sin_i[i] * Sc);
-            a.dcoeff_sin[(hT + row) * a.K + k] = beta * (sin_i[i] * Cc - cos_i[i] * Sc);
+            float ci, si;
+            tok_trig(static_cast<const uint32_t*>(a.table) + static_cast<int64_t>(row) * (kTokRow / 2), k, ci, si);
+            a.dcoeff_cos[(hT + row) * a.K + k] = beta * (ci * Cc + si * Sc);
+            a.dcoeff_sin[(hT + row) * a.K + k] = beta * (si * Cc - ci * Sc);
           }
         }
       }
@@ -2321,13 +1939,11 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
     }
   }
   if ((phases & SCOPE_BWD_DQ) && !dq_done) {
-    // 16 query rows per wavefront, eight wavefronts (two per SIMD) per 128
-    // rows; the gated token mode would spill there (about 80 registers) and
-    // keeps 32 rows per wavefront, one wavefront per SIMD
+    // 16 query rows per wavefront, eight wavefronts (two per SIMD) per 128 rows
     if (mode == SCOPE_BIAS_BLOCK)
       hipLaunchKernelGGL((attn_bwd_dq16_kernel<BS, 1>), gq, dim3(512), 0, s, a);
     else if (mode == SCOPE_BIAS_TOKEN && gate)
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<BS, 3>), gq, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((attn_bwd_dq16_kernel<BS, 3>), gq, dim3(512), 0, s, a);
     else if (mode == SCOPE_BIAS_TOKEN)
       hipLaunchKernelGGL((attn_bwd_dq16_kernel<BS, 2>), gq, dim3(512), 0, s, a);
     else
