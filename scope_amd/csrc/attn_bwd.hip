@@ -482,10 +482,9 @@ template <int MODE>
 struct alignas(16) DkvBuf {
   uint16_t q[64 * 128];            // Q rows, swizzled (swz_off)
   uint16_t d[64 * 128];            // dO rows, swizzled
-  float ra[256];                   // modes 0/1: softmax offset (log2) | Δ | doc id (int32), 64 rows each;
-                                   // token modes: lse | Δ | doc id | b0
+  float ra[256];                   // softmax offset without the pair bias (log2) | -Δ | doc id (int32), 64 rows each
   float rb[MODE <= 1 ? 4 : 1024];  // token: query features [64][32] bf16 (chunk-swizzled)
-  float rc[MODE >= 2 ? 256 : 4];   // token: slope | delta_main | width
+  float rc[MODE >= 2 ? 256 : 4];   // token: β·slope (log2 units) | delta_main | width
 };
 
 // Issue part `part` (0..9) of the copies of the 64-row query tile starting at
@@ -515,19 +514,19 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
   }
   const uint32_t lo = static_cast<uint32_t>(lane) * 16;  // 16 lanes x 16 bytes = one 64-row float array
   if (part == 8) {
-    // wavefront w copies per-row array w: the softmax offsets (modes 0/1) or
-    // lse (token modes), Δ, document ids, b0
-    const char* base = wave == 0   ? reinterpret_cast<const char*>(MODE <= 1 ? rof : a.lse + hT + q0)
+    // wavefront w copies per-row array w: the softmax offsets (modes 0/1: per
+    // list entry; token modes: per row, the pair bias added per tile), -Δ,
+    // document ids
+    const char* base = wave == 0   ? reinterpret_cast<const char*>(MODE <= 1 ? rof : a.rowoff + hT + q0)
                        : wave == 1 ? reinterpret_cast<const char*>(a.delta + hT + q0)
-                       : wave == 2 ? reinterpret_cast<const char*>(a.docs + q0)
-                                   : reinterpret_cast<const char*>(a.b0 + hT + q0);
-    if (lane < 16 && (wave < 3 || (MODE >= 2 && a.subtract_b0))) g2lds16(base, lo, b.ra + wave * 64);
+                                   : reinterpret_cast<const char*>(a.docs + q0);
+    if (lane < 16 && wave < 3) g2lds16(base, lo, b.ra + wave * 64);
     if (MODE >= 2) {
-      // token terms: slope, delta_main, width on wavefronts 0, 1, 2
-      const char* tb = wave == 0   ? reinterpret_cast<const char*>(a.slope + hT + q0)
+      // token terms: β·slope, delta_main, width on wavefronts 0, 1, 2
+      const char* tb = wave == 0   ? reinterpret_cast<const char*>(a.rowslope + hT + q0)
                        : wave == 1 ? reinterpret_cast<const char*>(a.delta_main + hT + q0)
                                    : reinterpret_cast<const char*>(a.width + hT + q0);
-      const bool need = wave == 0 ? a.use_slope != 0 : (wave < 3 && MODE == 3);
+      const bool need = wave == 0 || (wave < 3 && MODE == 3);
       if (lane < 16 && need) g2lds16(tb, lo, b.rc + wave * 64);
     }
     return;
@@ -559,7 +558,7 @@ __device__ __forceinline__ void dkv_probs_quad(const AttnArgs& a, const DkvBuf<M
   const int* docq = reinterpret_cast<const int*>(b.ra + 128);
   const float cs = a.scale_log2;
   const float glam = a.beta_log2 * a.ramp_lambda;
-  const float slsc = TOK && a.use_slope ? a.beta_log2 : 0.f;
+  const float slsc = TOK ? 1.f : 0.f;  // b.rc holds β·slope (zero without the slope term)
   const float spw = a.gate_kind == SCOPE_GATE_SOFTPLUS ? kLn2 : 0.f;
   const int qi0 = mq * 32 + 8 * rq + 4 * g;  // 4 consecutive query rows of this register quad
   const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
@@ -620,10 +619,7 @@ template <int MODE>
 __device__ __forceinline__ void dkv_offsets(const AttnArgs& a, const DkvBuf<MODE>& b, float* offw, const float* tab,
                                             float eb, int lane) {
   static_assert(MODE >= 2, "modes 0/1 read the offsets the q-major pass stored");
-  const float l = b.ra[lane];
-  float c = 0.f;
-  if (a.subtract_b0) c = -a.beta_log2 * b.ra[192 + lane];
-  offw[lane] = l == -INFINITY ? -INFINITY : c + eb - l * kLog2e;
+  offw[lane] = b.ra[lane] + eb;  // the row's offset (-β·b0 - lse, or -inf) and the pair bias
 }
 
 // One 64-row query tile against this wavefront's 32 keys: S, dP, then
@@ -940,21 +936,11 @@ __device__ __forceinline__ void dkv16_probs(const AttnArgs& a, const DkvBuf<MODE
     const int qi0 = 16 * mb + 4 * g;  // rows qi0 .. qi0+3 of the tile
     float ofv[4], slv[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (TOK) {
-      const float4 l4 = *reinterpret_cast<const float4*>(&b.ra[qi0]);
-      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (a.subtract_b0) {
-        const float4 b4 = *reinterpret_cast<const float4*>(&b.ra[192 + qi0]);
-        bv[0] = b4.x, bv[1] = b4.y, bv[2] = b4.z, bv[3] = b4.w;
-      }
-      if (a.use_slope) {
-        const float4 s4 = *reinterpret_cast<const float4*>(&b.rc[qi0]);
-        slv[0] = s4.x * a.beta_log2, slv[1] = s4.y * a.beta_log2, slv[2] = s4.z * a.beta_log2,
-        slv[3] = s4.w * a.beta_log2;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ofv[i] = lv[i] == -INFINITY ? -INFINITY : fmaf(-a.beta_log2, bv[i], eb) - lv[i] * kLog2e;
+      // the rows' offsets (-β·b0 - lse) and β·slope, stored by the q-major pass
+      const float4 o4 = *reinterpret_cast<const float4*>(&b.ra[qi0]);
+      const float4 s4 = *reinterpret_cast<const float4*>(&b.rc[qi0]);
+      ofv[0] = o4.x + eb, ofv[1] = o4.y + eb, ofv[2] = o4.z + eb, ofv[3] = o4.w + eb;
+      slv[0] = s4.x, slv[1] = s4.y, slv[2] = s4.z, slv[3] = s4.w;
     } else {
       const float4 of4 = *reinterpret_cast<const float4*>(&offw[qi0]);
       ofv[0] = of4.x, ofv[1] = of4.y, ofv[2] = of4.z, ofv[3] = of4.w;
@@ -1758,6 +1744,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int i = 0; i < 6; ++i) ex[i] = sum_groups16(ex[i]);
     if (g == 0) {
+      // for the kv-major pass: the row's offset without the pair bias (-inf
+      // for a row without visible keys: lse2 is +inf there) and β·slope
+      a.rowoff[hT + row] = rowc - lse2;
+      a.rowslope[hT + row] = slp;
       if (a.db0) a.db0[hT + row] = -beta * (rs_tot - dd_err * pm_tot);
       if (a.dslope) a.dslope[hT + row] = beta * (ex[0] - dd_err * ex[3]);
       const float gsc = beta * a.ramp_lambda * a.inv_tau;
@@ -1864,7 +1854,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) 
 }
 
 struct BwdLayout {
-  int64_t delta, qfeat, items, slots, multi, part_dk, part_dv, q_pos, roff, dpair, total, max_slots;
+  int64_t delta, qfeat, items, slots, multi, part_dk, part_dv, q_pos, roff, rowoff, dpair, total, max_slots;
   int max_items;
 };
 
@@ -1896,6 +1886,9 @@ static BwdLayout bwd_layout(const scope_attn_params* p) {
   // per-(h, qb, entry, row) softmax offsets of modes 0/1
   L.roff = o;
   if (p->bias_mode != SCOPE_BIAS_TOKEN) o += al(static_cast<int64_t>(p->H) * QB * p->maxkv * p->bs * 4);
+  // token modes: per-row offsets and slopes, [2][H][T]
+  L.rowoff = o;
+  if (p->bias_mode == SCOPE_BIAS_TOKEN) o += al(2 * static_cast<int64_t>(p->H) * p->T * 4);
   // pair-bias gradient partials, one per 128-key part of a key block
   L.dpair = o;
   if (p->dpair_bias) o += al(static_cast<int64_t>(p->bs / 128) * p->H * QB * p->maxkv * 4);
@@ -2052,6 +2045,8 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   pl.part_dv = reinterpret_cast<float*>(ws + L.part_dv);
   pl.q_pos = reinterpret_cast<const int32_t*>(ws + L.q_pos);
   a.roff = p->bias_mode != SCOPE_BIAS_TOKEN ? reinterpret_cast<float*>(ws + L.roff) : nullptr;
+  a.rowoff = p->bias_mode == SCOPE_BIAS_TOKEN ? reinterpret_cast<float*>(ws + L.rowoff) : nullptr;
+  a.rowslope = a.rowoff ? a.rowoff + static_cast<int64_t>(p->H) * p->T : nullptr;
   pl.max_slots = L.max_slots;
   pl.max_items = L.max_items;
   hipStream_t s = as_stream(stream);

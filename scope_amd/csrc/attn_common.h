@@ -300,6 +300,12 @@ struct AttnArgs {
   // (h, qb, list entry, row), [H][QB][maxkv][bs] = block term + pair bias -
   // lse·log2e, written by the q-major pass and read per tile by the kv-major pass
   float* roff;
+  // backward, token modes: each row's softmax offset without the pair bias,
+  // -β·b0 - lse (log2 units, -inf for a row without visible keys), and its
+  // slope β·slope (log2 units), [H][T] each, written by the q-major pass and
+  // copied per tile by the kv-major pass
+  float* rowoff;
+  float* rowslope;
   int H, QB, maxkv, K;
   int64_t T;
   int64_t q_sh, q_st, k_sh, k_st, v_sh, v_st, o_sh, o_st;
