@@ -1,8 +1,9 @@
 // Fused coefficient head of SpectralBias.forward (model/attn_bias.py:419-506):
 // the [rows, M, K] mixture that turns the MLP output y into the band
 // coefficients and the per-row pointer terms, its regularisers, and its
-// backward.  The two MLP GEMMs stay on the BLAS library; everything between
-// y and the outputs is one pass over y with a thread per (b, h, t) row.
+// backward.  The MLP that produces y runs before it (mlp.hip); everything
+// between y and the outputs is one pass over y with eight lanes per (b, h, t)
+// row, lane m taking mixture peak m.
 //
 // Per row, with y = [delta_raw | mu_raw | sigma_raw | pi_logits |
 // budget_logits | c_raw] (M columns each, c_raw only with use_slope):
@@ -40,56 +41,66 @@ __device__ __forceinline__ float load_y(const void* y, bool bf16, int64_t i) {
   return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(y)[i]) : static_cast<const float*>(y)[i];
 }
 
-// Forward quantities of one row that the backward needs again.  MM is a
-// compile-time bound on M: every loop below runs to MM with a guard, so the
-// arrays stay in registers (a runtime-indexed array would live in scratch).
-template <int MM>
-struct CoeffRow {
-  float ds[MM], sd[MM];   // Δ*, σ(delta_raw)
-  float mu[MM], sm[MM];   // μ, σ(mu_raw)
-  float sg[MM], ss[MM];   // s, σ(sigma_raw)
-  float pi[MM];
-  float th;               // tanh(c_raw)
-  int amax;               // first maximum of π
+// Lanes per row: lane m of a group of eight takes peak m (m < M <= 8); the
+// sums over the peaks are 8-lane reductions inside the group.  With a thread
+// per row the kernels would run two wavefronts per SIMD, each working through
+// M·K exp and sincos calls one after another.
+constexpr int kCoeffGroup = 8;
+constexpr int kCoeffRows = kCoeffThreads / kCoeffGroup;  // rows per workgroup
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// op over the 8 lanes of the group, the same value in every lane (op is
+// commutative): quad xor 1, quad xor 2, then the mirrored quad of the eight
+template <typename Op>
+__device__ __forceinline__ float grp_reduce(float x, Op op) {
+  x = op(x, dpp_f<0xB1>(x));
+  x = op(x, dpp_f<0x4E>(x));
+  x = op(x, dpp_f<0x141>(x));
+  return x;
+}
+__device__ __forceinline__ float grp_sum(float x) {
+  return grp_reduce(x, [](float u, float v) { return u + v; });
+}
+__device__ __forceinline__ float grp_max(float x) {
+  return grp_reduce(x, [](float u, float v) { return fmaxf(u, v); });
+}
+__device__ __forceinline__ float grp_min(float x) {
+  return grp_reduce(x, [](float u, float v) { return fminf(u, v); });
+}
+
+// One lane's peak m of a row, and the row terms every lane of the group holds.
+// Lanes m >= M read column 0 for the sigmoids (finite, unused) and carry π = 0.
+struct CoeffPeak {
+  float sd, ds;  // σ(delta_raw_m), Δ*_m
+  float sm, mu;  // σ(mu_raw_m), μ_m
+  float ss, sg;  // σ(sigma_raw_m), s_m
+  float pi;      // π_m
+  float th;      // tanh(c_raw) of the row
+  int amax;      // first maximum of π over the row
 };
 
-template <int MM>
-__device__ __forceinline__ void coeff_row(const scope_coeff_params& p, const void* y, int64_t row,
-                                          CoeffRow<MM>& R) {
+// Every lane of the group must call this (group reductions inside).
+__device__ __forceinline__ void coeff_peak(const scope_coeff_params& p, const void* y, int64_t row, int m, bool act,
+                                           CoeffPeak& R) {
   const int M = p.M;
   const bool bf = p.y_bf16 != 0;
   const int64_t base = row * p.y_stride;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    if (m >= M) break;
-    R.sd[m] = sigm(load_y(y, bf, base + m));
-    R.ds[m] = R.sd[m] * p.delta_cap;
-    R.sm[m] = sigm(load_y(y, bf, base + M + m));
-    R.mu[m] = p.logw_min + (p.logw_max - p.logw_min) * R.sm[m];
-    R.ss[m] = sigm(load_y(y, bf, base + 2 * M + m));
-    R.sg[m] = 0.25f + 1.75f * R.ss[m];
-    R.pi[m] = load_y(y, bf, base + 3 * M + m);
-    mx = fmaxf(mx, R.pi[m]);
-  }
-  float den = 0.f;
-#pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    if (m >= M) break;
-    R.pi[m] = expf(R.pi[m] - mx);
-    den += R.pi[m];
-  }
-  R.amax = 0;
-  float best = -1.f;
-#pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    if (m >= M) break;
-    R.pi[m] /= den;
-    if (R.pi[m] > best) {
-      best = R.pi[m];
-      R.amax = m;
-    }
-  }
+  const int mm = act ? m : 0;
+  R.sd = sigm(load_y(y, bf, base + mm));
+  R.ds = R.sd * p.delta_cap;
+  R.sm = sigm(load_y(y, bf, base + M + mm));
+  R.mu = p.logw_min + (p.logw_max - p.logw_min) * R.sm;
+  R.ss = sigm(load_y(y, bf, base + 2 * M + mm));
+  R.sg = 0.25f + 1.75f * R.ss;
+  const float lg = act ? load_y(y, bf, base + 3 * M + mm) : -INFINITY;
+  const float mx = grp_max(lg);
+  const float ex = act ? expf(lg - mx) : 0.f;
+  R.pi = ex / grp_sum(ex);
+  const float best = grp_max(R.pi);
+  R.amax = static_cast<int>(grp_min(act && R.pi == best ? static_cast<float>(m) : static_cast<float>(kCoeffGroup)));
   R.th = p.use_slope ? tanhf(load_y(y, bf, base + 5 * M)) : 0.f;
 }
 
@@ -101,94 +112,96 @@ __device__ __forceinline__ float coeff_e(const float* logw, int k, float mu, flo
 
 }  // namespace
 
-template <int MM, int KK>
+template <int KK>
 __global__ __launch_bounds__(kCoeffThreads) void coeff_fwd_kernel(
     scope_coeff_params p, const void* __restrict__ y, const float* __restrict__ omegas,
     const float* __restrict__ logw, const float* __restrict__ cmean, const float* __restrict__ smean,
     float* __restrict__ cc_out, float* __restrict__ cs_out, float* __restrict__ slope_out, float* __restrict__ b0_out,
     float* __restrict__ ds_out, float* __restrict__ pi_out, float* __restrict__ bl_out, float* __restrict__ dm_out,
     float* __restrict__ w_out, double* __restrict__ partial) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kCoeffThreads + threadIdx.x;
+  const int m = threadIdx.x % kCoeffGroup;
+  const int64_t row_id = static_cast<int64_t>(blockIdx.x) * kCoeffRows + threadIdx.x / kCoeffGroup;
+  const bool valid = row_id < p.rows;
+  const int64_t row = valid ? row_id : p.rows - 1;  // every lane takes part in the group reductions
   const int M = p.M, K = p.K;
-  double r_omega = 0.0, r_ent = 0.0, r_edge = 0.0, r_b = 0.0;
-  if (row < p.rows) {
-    CoeffRow<MM> R;
-    coeff_row<MM>(p, y, row, R);
-    float cc[KK], cs[KK];
-#pragma unroll
-    for (int k = 0; k < KK; ++k) cc[k] = cs[k] = 0.f;
-    float om_row = 0.f;
-#pragma unroll
-    for (int m = 0; m < MM; ++m) {
-      if (m >= M) break;
-      float e[KK], S = 0.f;
-#pragma unroll
-      for (int k = 0; k < KK; ++k) {
-        if (k >= K) break;
-        e[k] = coeff_e(logw, k, R.mu[m], R.sg[m]);
-        S += e[k];
-      }
-      const float inv = 1.f / (S + p.eps);
-#pragma unroll
-      for (int k = 0; k < KK; ++k) {
-        if (k >= K) break;
-        const float a = e[k] * inv;
-        float sn, cn;
-        sincosf(omegas[k] * R.ds[m], &sn, &cn);
-        cc[k] += R.pi[m] * a * cn;
-        cs[k] += R.pi[m] * a * sn;
-        om_row += omegas[k] * omegas[k] * a * a;
-      }
-    }
-    const int64_t rk = row * K, rm = row * M;
-    float b0 = 0.f;
+  const bool act = m < M;
+  CoeffPeak R;
+  coeff_peak(p, y, row, m, act, R);
+  // cc_k = Σ_m π_m a_mk cos(ω_k Δ*_m): this lane's term, summed over the group
+  float cc[KK], cs[KK];
+  float om = 0.f;  // Σ_k ω_k² a_mk² of this peak
+  {
+    float e[KK], S = 0.f;
 #pragma unroll
     for (int k = 0; k < KK; ++k) {
       if (k >= K) break;
-      cc_out[rk + k] = cc[k];
-      cs_out[rk + k] = cs[k];
-      b0 += cc[k];
+      e[k] = coeff_e(logw, k, R.mu, R.sg);
+      S += e[k];
     }
-    if (!p.subtract_b0) b0 = 0.f;
-    const float slope = p.use_slope ? p.c_scale * R.th : 0.f;
-    float mus = 0.f, dmain = 0.f;
+    const float inv = 1.f / (S + p.eps);
 #pragma unroll
-    for (int m = 0; m < MM; ++m) {
-      if (m >= M) break;
-      ds_out[rm + m] = R.ds[m];
-      pi_out[rm + m] = R.pi[m];
-      bl_out[rm + m] = load_y(y, p.y_bf16 != 0, row * p.y_stride + 4 * M + m);
-      mus += R.mu[m];
-      if (m == R.amax) dmain = R.ds[m];
+    for (int k = 0; k < KK; ++k) {
+      if (k >= K) break;
+      const float a = e[k] * inv;
+      float sn, cn;
+      sincosf(omegas[k] * R.ds, &sn, &cn);
+      const float w = act ? R.pi * a : 0.f;
+      cc[k] = grp_sum(w * cn);
+      cs[k] = grp_sum(w * sn);
+      if (act) om += omegas[k] * omegas[k] * a * a;
     }
-    slope_out[row] = slope;
-    b0_out[row] = b0;
-    dm_out[row] = dmain;
-    w_out[row] = p.width_min + (p.width_max - p.width_min) * sigm(mus / static_cast<float>(M));
-    if (p.training) {
-      r_omega = om_row;
-      float H = 0.f;
+  }
+  float b0 = 0.f;
 #pragma unroll
-      for (int m = 0; m < MM; ++m)
-        if (m < M) H -= R.pi[m] * logf(R.pi[m] + p.eps);
-      r_ent = fmaxf(p.entropy_floor - H, 0.f);
-      const float denom = fmaxf(p.delta_cap, 1.f);
-      float edge = 0.f;
+  for (int k = 0; k < KK; ++k)
+    if (k < K) b0 += cc[k];
+  if (!p.subtract_b0) b0 = 0.f;
+  const float slope = p.use_slope ? p.c_scale * R.th : 0.f;
+  const float mus = grp_sum(act ? R.mu : 0.f);
+  const float dmain = grp_sum(m == R.amax ? R.ds : 0.f);  // one nonzero term
+  if (valid) {
+    const int64_t rk = row * K, rm = row * M;
 #pragma unroll
-      for (int m = 0; m < MM; ++m) {
-        if (m >= M) break;
-        const float u = fminf(fmaxf(R.ds[m] / denom, 0.f), 1.f);
-        edge += fmaxf(p.delta_edge_eps - u, 0.f) + fmaxf(u - (1.f - p.delta_edge_eps), 0.f);
+    for (int k = 0; k < KK; ++k) {
+      if (k >= K) break;
+      if (k % kCoeffGroup == m) {
+        cc_out[rk + k] = cc[k];
+        cs_out[rk + k] = cs[k];
       }
-      r_edge = edge;
-      float bb = slope * (0.5f * static_cast<float>(p.L - 1)) - b0;
-#pragma unroll
-      for (int k = 0; k < KK; ++k)
-        if (k < K) bb += cc[k] * cmean[k] + cs[k] * smean[k];
-      r_b = bb;
+    }
+    if (act) {
+      ds_out[rm + m] = R.ds;
+      pi_out[rm + m] = R.pi;
+      bl_out[rm + m] = load_y(y, p.y_bf16 != 0, row * p.y_stride + 4 * M + m);
+    }
+    if (m == 0) {
+      slope_out[row] = slope;
+      b0_out[row] = b0;
+      dm_out[row] = dmain;
+      w_out[row] = p.width_min + (p.width_max - p.width_min) * sigm(mus / static_cast<float>(M));
     }
   }
   if (!p.training) return;
+  // per-lane terms: ω (per peak), entropy and zero-mean (per row, lane 0), edge (per peak)
+  double r_omega = 0.0, r_ent = 0.0, r_edge = 0.0, r_b = 0.0;
+  {
+    const float H = -grp_sum(act ? R.pi * logf(R.pi + p.eps) : 0.f);
+    const float denom = fmaxf(p.delta_cap, 1.f);
+    const float u = fminf(fmaxf(R.ds / denom, 0.f), 1.f);
+    const float edge = fmaxf(p.delta_edge_eps - u, 0.f) + fmaxf(u - (1.f - p.delta_edge_eps), 0.f);
+    float bb = slope * (0.5f * static_cast<float>(p.L - 1)) - b0;
+#pragma unroll
+    for (int k = 0; k < KK; ++k)
+      if (k < K) bb += cc[k] * cmean[k] + cs[k] * smean[k];
+    if (valid && act) {
+      r_omega = om;
+      r_edge = edge;
+    }
+    if (valid && m == 0) {
+      r_ent = fmaxf(p.entropy_floor - H, 0.f);
+      r_b = bb;
+    }
+  }
   // workgroup partial sums, fixed order: lanes by xor-butterfly, wavefronts in index order
   double v[4] = {r_omega, r_ent, r_edge, r_b};
   for (int i = 0; i < 4; ++i)
@@ -238,7 +251,7 @@ __global__ __launch_bounds__(256) void coeff_reg_kernel(scope_coeff_params p, in
   reg[5] = mb;
 }
 
-template <int MM, int KK>
+template <int KK>
 __global__ __launch_bounds__(kCoeffThreads) void coeff_bwd_kernel(
     scope_coeff_params p, const void* __restrict__ y, const float* __restrict__ omegas,
     const float* __restrict__ logw, const float* __restrict__ cmean, const float* __restrict__ smean,
@@ -246,12 +259,15 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_bwd_kernel(
     const float* __restrict__ g_b0, const float* __restrict__ g_ds, const float* __restrict__ g_pi,
     const float* __restrict__ g_bl, const float* __restrict__ g_dm, const float* __restrict__ g_w,
     const float* __restrict__ g_reg, const float* __restrict__ reg, void* __restrict__ dy) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kCoeffThreads + threadIdx.x;
-  if (row >= p.rows) return;
+  const int m = threadIdx.x % kCoeffGroup;
+  const int64_t row_id = static_cast<int64_t>(blockIdx.x) * kCoeffRows + threadIdx.x / kCoeffGroup;
+  const bool valid = row_id < p.rows;
+  const int64_t row = valid ? row_id : p.rows - 1;  // every lane takes part in the group reductions
   const int M = p.M, K = p.K;
+  const bool act = m < M;
   const int64_t rk = row * K, rm = row * M;
-  CoeffRow<MM> R;
-  coeff_row<MM>(p, y, row, R);
+  CoeffPeak R;
+  coeff_peak(p, y, row, m, act, R);
   float gcc[KK], gcs[KK];
 #pragma unroll
   for (int k = 0; k < KK; ++k) {
@@ -261,15 +277,10 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_bwd_kernel(
   }
   float gsl = g_slope ? g_slope[row] : 0.f;
   float gb0 = g_b0 ? g_b0[row] : 0.f;
-  float gds[MM], gpi[MM], gmu[MM], gsg[MM];
-#pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    if (m >= M) break;
-    gds[m] = g_ds ? g_ds[rm + m] : 0.f;
-    gpi[m] = g_pi ? g_pi[rm + m] : 0.f;
-    gmu[m] = gsg[m] = 0.f;
-  }
-  const float gr = (p.training && g_reg) ? g_reg[0] : 0.f;
+  float gds = g_ds && act ? g_ds[rm + m] : 0.f;
+  float gpi = g_pi && act ? g_pi[rm + m] : 0.f;
+  float gmu = 0.f, gsg = 0.f;
+  const float gr = (p.training && g_reg) ? g_reg[0] : 0.f;  // the same in every lane
   const float N = static_cast<float>(p.rows), NM = N * static_cast<float>(M);
   float c_om = 0.f;
   if (gr != 0.f) {
@@ -285,27 +296,18 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_bwd_kernel(
       gb0 -= gb;
     }
     if (p.lambda_entropy > 0.f && p.entropy_floor > 0.f) {
-      float H = 0.f;
-#pragma unroll
-      for (int m = 0; m < MM; ++m)
-        if (m < M) H -= R.pi[m] * logf(R.pi[m] + p.eps);
-      if (p.entropy_floor - H > 0.f) {
+      const float H = -grp_sum(act ? R.pi * logf(R.pi + p.eps) : 0.f);
+      if (p.entropy_floor - H > 0.f && act) {
         const float ge = gr * p.lambda_entropy / N;
-#pragma unroll
-        for (int m = 0; m < MM; ++m)
-          if (m < M) gpi[m] += ge * (logf(R.pi[m] + p.eps) + R.pi[m] / (R.pi[m] + p.eps));
+        gpi += ge * (logf(R.pi + p.eps) + R.pi / (R.pi + p.eps));
       }
     }
-    if (p.lambda_delta_edge > 0.f) {
+    if (p.lambda_delta_edge > 0.f && act) {
       const float denom = fmaxf(p.delta_cap, 1.f), ge = gr * p.lambda_delta_edge / NM;
-#pragma unroll
-      for (int m = 0; m < MM; ++m) {
-        if (m >= M) break;
-        const float x = R.ds[m] / denom;
-        const float u = fminf(fmaxf(x, 0.f), 1.f);
-        const float de = (p.delta_edge_eps - u > 0.f ? -1.f : 0.f) + (u - (1.f - p.delta_edge_eps) > 0.f ? 1.f : 0.f);
-        if (x >= 0.f && x <= 1.f) gds[m] += ge * de / denom;
-      }
+      const float x = R.ds / denom;
+      const float u = fminf(fmaxf(x, 0.f), 1.f);
+      const float de = (p.delta_edge_eps - u > 0.f ? -1.f : 0.f) + (u - (1.f - p.delta_edge_eps) > 0.f ? 1.f : 0.f);
+      if (x >= 0.f && x <= 1.f) gds += ge * de / denom;
     }
     if (p.lambda_omega > 0.f) c_om = gr * p.lambda_omega / NM * 2.f;
   }
@@ -314,20 +316,13 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_bwd_kernel(
     for (int k = 0; k < KK; ++k)
       if (k < K) gcc[k] += gb0;
   }
-  if (g_dm) {
-    const float gd = g_dm[row];
-#pragma unroll
-    for (int m = 0; m < MM; ++m)
-      if (m == R.amax) gds[m] += gd;
-  }
-#pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    if (m >= M) break;
+  if (g_dm && m == R.amax) gds += g_dm[row];
+  {
     float e[KK], a[KK], ga[KK], S = 0.f;
 #pragma unroll
     for (int k = 0; k < KK; ++k) {
       if (k >= K) break;
-      e[k] = coeff_e(logw, k, R.mu[m], R.sg[m]);
+      e[k] = coeff_e(logw, k, R.mu, R.sg);
       S += e[k];
     }
     const float inv = 1.f / (S + p.eps);
@@ -337,62 +332,55 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_bwd_kernel(
       if (k >= K) break;
       a[k] = e[k] * inv;
       float sn, cn;
-      sincosf(omegas[k] * R.ds[m], &sn, &cn);
+      sincosf(omegas[k] * R.ds, &sn, &cn);
       const float G = gcc[k] * cn + gcs[k] * sn;
       gpim += a[k] * G;
-      ga[k] = R.pi[m] * G + c_om * omegas[k] * omegas[k] * a[k];
-      gdsm += R.pi[m] * a[k] * omegas[k] * (gcs[k] * cn - gcc[k] * sn);
+      ga[k] = R.pi * G + c_om * omegas[k] * omegas[k] * a[k];
+      gdsm += R.pi * a[k] * omegas[k] * (gcs[k] * cn - gcc[k] * sn);
     }
-    gpi[m] += gpim;
-    gds[m] += gdsm;
+    gpi += gpim;
+    gds += gdsm;
     // a = e / (S + eps)
     float dot = 0.f;
 #pragma unroll
     for (int k = 0; k < KK; ++k)
       if (k < K) dot += ga[k] * a[k];
-    const float is2 = 1.f / (R.sg[m] * R.sg[m]);
+    const float is2 = 1.f / (R.sg * R.sg);
 #pragma unroll
     for (int k = 0; k < KK; ++k) {
       if (k >= K) break;
       const float ge = (ga[k] - dot) * inv * e[k];
-      const float d = logw[k] - R.mu[m];
-      gmu[m] += ge * d * is2;
-      gsg[m] += ge * d * d * is2 / R.sg[m];
+      const float d = logw[k] - R.mu;
+      gmu += ge * d * is2;
+      gsg += ge * d * d * is2 / R.sg;
     }
   }
   if (g_w) {
-    float mus = 0.f;
-#pragma unroll
-    for (int m = 0; m < MM; ++m)
-      if (m < M) mus += R.mu[m];
+    const float mus = grp_sum(act ? R.mu : 0.f);
     const float sw = sigm(mus / static_cast<float>(M));
-    const float gwm = g_w[row] * (p.width_max - p.width_min) * sw * (1.f - sw) / static_cast<float>(M);
-#pragma unroll
-    for (int m = 0; m < MM; ++m)
-      if (m < M) gmu[m] += gwm;
+    gmu += g_w[row] * (p.width_max - p.width_min) * sw * (1.f - sw) / static_cast<float>(M);
   }
-  float gsum = 0.f;
-#pragma unroll
-  for (int m = 0; m < MM; ++m)
-    if (m < M) gsum += R.pi[m] * gpi[m];
+  const float gsum = grp_sum(act ? R.pi * gpi : 0.f);
+  if (!valid) return;
   const bool bf = p.y_bf16 != 0;
   const int64_t base = row * p.y_stride;
   auto put = [&](int c, float v) {
     if (bf) static_cast<uint16_t*>(dy)[base + c] = f32_to_bf16(v);
     else static_cast<float*>(dy)[base + c] = v;
   };
-#pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    if (m >= M) break;
-    put(m, gds[m] * p.delta_cap * R.sd[m] * (1.f - R.sd[m]));
-    put(M + m, gmu[m] * (p.logw_max - p.logw_min) * R.sm[m] * (1.f - R.sm[m]));
-    put(2 * M + m, gsg[m] * 1.75f * R.ss[m] * (1.f - R.ss[m]));
-    put(3 * M + m, R.pi[m] * (gpi[m] - gsum));
+  if (act) {
+    put(m, gds * p.delta_cap * R.sd * (1.f - R.sd));
+    put(M + m, gmu * (p.logw_max - p.logw_min) * R.sm * (1.f - R.sm));
+    put(2 * M + m, gsg * 1.75f * R.ss * (1.f - R.ss));
+    put(3 * M + m, R.pi * (gpi - gsum));
     put(4 * M + m, g_bl ? g_bl[rm + m] : 0.f);
   }
-  int c = 5 * M;
-  if (p.use_slope) put(c++, gsl * p.c_scale * (1.f - R.th * R.th));
-  for (; c < p.y_cols; ++c) put(c, 0.f);
+  int c0 = 5 * M;
+  if (p.use_slope) {
+    if (m == 0) put(c0, gsl * p.c_scale * (1.f - R.th * R.th));
+    ++c0;
+  }
+  for (int c = c0 + m; c < p.y_cols; c += kCoeffGroup) put(c, 0.f);
 }
 
 }  // namespace scope
@@ -412,7 +400,7 @@ static int coeff_check(const scope_coeff_params* p, const char* who) {
 
 extern "C" int64_t scope_coeff_head_workspace_bytes(const scope_coeff_params* p) {
   if (!p || p->rows <= 0) return 0;
-  return static_cast<int64_t>(ceil_div(p->rows, kCoeffThreads)) * 4 * static_cast<int64_t>(sizeof(double));
+  return static_cast<int64_t>(ceil_div(p->rows, kCoeffRows)) * 4 * static_cast<int64_t>(sizeof(double));
 }
 
 extern "C" int scope_coeff_head_fwd(const scope_coeff_params* p, const void* y, const float* omegas,
@@ -427,16 +415,15 @@ extern "C" int scope_coeff_head_fwd(const scope_coeff_params* p, const void* y, 
                 "scope_coeff_head_fwd: null pointer");
   SCOPE_REQUIRE(!p->training || (reg && workspace && cos_mean && sin_mean),
                 "scope_coeff_head_fwd: training needs reg, workspace, cos_mean and sin_mean");
-  const int nblk = ceil_div(p->rows, kCoeffThreads);
+  const int nblk = ceil_div(p->rows, kCoeffRows);
   hipStream_t s = as_stream(stream);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(nblk), dim3(kCoeffThreads), 0, s, *p, y, omegas, log_omegas, cos_mean, sin_mean,
                        coeff_cos, coeff_sin, slope, b0, delta_star, pi, budget_logits, delta_main, width,
                        static_cast<double*>(workspace));
   };
-  if (p->M <= 2 && p->K <= 8) go(coeff_fwd_kernel<2, 8>);
-  else if (p->K <= 8) go(coeff_fwd_kernel<kMaxM, 8>);
-  else go(coeff_fwd_kernel<kMaxM, kMaxK>);
+  if (p->K <= 8) go(coeff_fwd_kernel<8>);
+  else go(coeff_fwd_kernel<kMaxK>);
   rc = check_launch("coeff_fwd_kernel");
   if (rc || !p->training) return rc;
   hipLaunchKernelGGL(coeff_reg_kernel, dim3(1), dim3(256), 0, s, *p, nblk, static_cast<const double*>(workspace), reg);
@@ -455,12 +442,11 @@ extern "C" int scope_coeff_head_bwd(const scope_coeff_params* p, const void* y, 
   SCOPE_REQUIRE(!(p->training && g_reg) || (reg && cos_mean && sin_mean),
                 "scope_coeff_head_bwd: a regulariser gradient needs reg, cos_mean and sin_mean");
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(ceil_div(p->rows, kCoeffThreads)), dim3(kCoeffThreads), 0, as_stream(stream), *p,
+    hipLaunchKernelGGL(kern, dim3(ceil_div(p->rows, kCoeffRows)), dim3(kCoeffThreads), 0, as_stream(stream), *p,
                        y, omegas, log_omegas, cos_mean, sin_mean, g_coeff_cos, g_coeff_sin, g_slope, g_b0,
                        g_delta_star, g_pi, g_budget_logits, g_delta_main, g_width, g_reg, reg, dy);
   };
-  if (p->M <= 2 && p->K <= 8) go(coeff_bwd_kernel<2, 8>);
-  else if (p->K <= 8) go(coeff_bwd_kernel<kMaxM, 8>);
-  else go(coeff_bwd_kernel<kMaxM, kMaxK>);
+  if (p->K <= 8) go(coeff_bwd_kernel<8>);
+  else go(coeff_bwd_kernel<kMaxK>);
   return check_launch("coeff_bwd_kernel");
 }
