@@ -613,6 +613,7 @@ def main_ref(args):
             scope_attention(q, k, v, block_mask=bm, scale=0.12, spectral=sp)
 
     def attn_fwd_bwd():
+        qd.grad = kd.grad = vd.grad = None  # no gradient accumulation adds in the timed region
         y = scope_attention(qd, kd, vd, block_mask=bm, scale=0.12, spectral=sp)
         y.backward(dout)
 
@@ -665,6 +666,9 @@ def graph_step_time(layer, q, k, v, dout, one, steps: int) -> dict:
     qs, ks, vs = (x.detach().clone().requires_grad_() for x in (q, k, v))
 
     def body():
+        # fresh gradients each step, as the eager step's fresh leaves get
+        # (accumulating into .grad would add three q-sized sums per step)
+        qs.grad = ks.grad = vs.grad = None
         y, reg, _ = layer(qs, ks, vs)
         torch.autograd.backward([y, reg], [dout, one])
         return y

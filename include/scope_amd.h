@@ -256,8 +256,15 @@ int scope_linear_wgrad(const scope_wgrad_params* p, const uint16_t* a, const uin
  * and every intermediate rounded to bf16 where the reference's tensors are;
  * D = 128, hidden = 256, 1 <= O <= 64.  Row r of q is row r % seg of
  * segment r / seg: q + (r / seg)·q_ss + (r % seg)·q_rs (elements); rows is
- * a multiple of 32; y, gy, dq, dz1, x1 and gyp are contiguous.  The weight
- * and bias gradients take x1 / gyp and dz1 / q to scope_linear_wgrad.
+ * a multiple of 32; y, gy, dq, dz1, x1 and gyp are contiguous.  x1 and dz1
+ * are optional (both null: not written).  The weight and bias gradients of
+ * the bf16 weight copies, rounded to bf16 (autograd of the two F.linear over
+ * all rows):
+ *   scope_coeff_mlp_wgrad  dW1 = Σ_r dz1^T q [256][128], db1 = Σ_r dz1 [256],
+ *                          dW2 = Σ_r gyp^T x1 [64][256], db2 = Σ_r gyp [64]
+ * from q and gyp alone (z1, x1 and dz1 recomputed per tile, never stored;
+ * seg a multiple of 128; the workspace is
+ * scope_coeff_mlp_wgrad_workspace_bytes); rows O.. of dW2 and db2 are zero.
  * ---------------------------------------------------------------------- */
 typedef struct {
   int64_t rows, seg, q_ss, q_rs;
@@ -269,6 +276,10 @@ int scope_coeff_mlp_fwd(const scope_mlp_params* p, const uint16_t* q, const floa
 int scope_coeff_mlp_bwd(const scope_mlp_params* p, const uint16_t* q, const uint16_t* gy, const float* w1,
                         const float* b1, const float* w2, const float* b2, uint16_t* dq, uint16_t* dz1,
                         uint16_t* x1, uint16_t* gyp, void* stream);
+int64_t scope_coeff_mlp_wgrad_workspace_bytes(const scope_mlp_params* p);
+int scope_coeff_mlp_wgrad(const scope_mlp_params* p, const uint16_t* q, const uint16_t* gyp, const float* w1,
+                          const float* b1, const float* w2, float* dw1, float* db1, float* dw2, float* db2,
+                          void* workspace, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sliding-window block masks of the layers without the pointer mask.

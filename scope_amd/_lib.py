@@ -100,6 +100,8 @@ _PROTOS = {
     "scope_linear_wgrad": (c_int, [C.POINTER(WgradParams)] + [P] * 6),
     "scope_coeff_mlp_fwd": (c_int, [C.POINTER(MlpParams)] + [P] * 7),
     "scope_coeff_mlp_bwd": (c_int, [C.POINTER(MlpParams)] + [P] * 11),
+    "scope_coeff_mlp_wgrad_workspace_bytes": (c_int64, [C.POINTER(MlpParams)]),
+    "scope_coeff_mlp_wgrad": (c_int, [C.POINTER(MlpParams)] + [P] * 11),
     "scope_swa_width": (c_int, [c_int64, c_int, c_int]),
     "scope_swa_blockmask": (c_int, [P, c_int64, c_int, c_int, P, P, P, P, P, P, P, P]),
     "scope_stats_counts_len": (c_int64, [C.POINTER(StatsParams)]),

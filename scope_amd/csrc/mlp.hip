@@ -456,13 +456,15 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_bwd_kernel(MlpArgs g) {
         xw[r / 2] = cvt_pk_bf16(xv[0], xv[1]);
         dw[r / 2] = cvt_pk_bf16(dv[0], dv[1]);
       }
-      // x1 and dz1 rows: hidden 32hb + 8q + 4gq .. +3 in register quad q
-      uint16_t* xr = g.x1 + row * kMlpH + 32 * hb + 4 * gq;
-      uint16_t* dr = g.dz1 + row * kMlpH + 32 * hb + 4 * gq;
+      if (g.x1) {
+        // x1 and dz1 rows: hidden 32hb + 8q + 4gq .. +3 in register quad q
+        uint16_t* xr = g.x1 + row * kMlpH + 32 * hb + 4 * gq;
+        uint16_t* dr = g.dz1 + row * kMlpH + 32 * hb + 4 * gq;
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        *reinterpret_cast<uint2*>(xr + 8 * qd) = make_uint2(xw[2 * qd], xw[2 * qd + 1]);
-        *reinterpret_cast<uint2*>(dr + 8 * qd) = make_uint2(dw[2 * qd], dw[2 * qd + 1]);
+        for (int qd = 0; qd < 4; ++qd) {
+          *reinterpret_cast<uint2*>(xr + 8 * qd) = make_uint2(xw[2 * qd], xw[2 * qd + 1]);
+          *reinterpret_cast<uint2*>(dr + 8 * qd) = make_uint2(dw[2 * qd], dw[2 * qd + 1]);
+        }
       }
       const uint4 dp[2] = {make_uint4(dw[0], dw[1], dw[2], dw[3]), make_uint4(dw[4], dw[5], dw[6], dw[7])};
 #pragma unroll
@@ -477,6 +479,229 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_bwd_kernel(MlpArgs g) {
         *reinterpret_cast<uint2*>(dqp + 32 * md + 8 * qd) =
             make_uint2(cvt_pk_bf16(dq[md][4 * qd], dq[md][4 * qd + 1]), cvt_pk_bf16(dq[md][4 * qd + 2], dq[md][4 * qd + 3]));
   }
+}
+
+// ---------------------------------------------------------------------------
+// The MLP's weight and bias gradients without its intermediates in memory:
+//   dW1 = Σ_r dz1[r]^T q[r], db1 = Σ_r dz1[r], dW2 = Σ_r gy[r]^T x1[r],
+//   db2 = Σ_r gy[r]
+// over all rows, with z1, x1 and dz1 recomputed per tile as in the row-wise
+// backward (the same bf16 rounding points).  A workgroup takes four hidden
+// blocks of 32 units (4·hq .. 4·hq + 3) over a contiguous run of 64-row tiles;
+// wavefront w computes hidden block 4·hq + w/2 for rows 32·(w%2) .. +31:
+//   Z = q·W1[hb]^T + b1[hb] and dX1 = gy·W2[:, hb] (v_mfma_f32_32x32x16_bf16:
+//   the tile's q and gy rows as A operands through LDS row reads, W1[hb] and
+//   W2[:, hb] as B operands in registers, b1 as one more k-step);
+//   their C layout (lane: hidden unit, register r: row 8(r/4) + 4g + r%4) is
+//   directly the A operand of dW1[hb] += dz1^T·q and dW2^T[hb] += x1^T·gy,
+//   whose k runs over rows in the slot order of the transpose reads
+//   (lds_kmajor_o) of the same q and gy tiles.
+// Four tile buffers: the copies run three tiles ahead of the MFMAs.  The two
+// wavefronts of a hidden block add their sums in LDS in a fixed order; each
+// workgroup writes one partial per row group, which wgrad_reduce_kernel adds
+// in group order (no atomics anywhere).
+// ---------------------------------------------------------------------------
+constexpr int kMwTileRows = 64;
+constexpr int kMwBufs = 4;
+constexpr int kMwMaxGroups = 128;
+constexpr int kMwPart1 = kMlpH * kMlpD + kMlpH;         // dW1 [256][128], db1 [256]
+constexpr int kMwPart2 = kMlpOMax * kMlpH + kMlpOMax;   // dW2 [64][256], db2 [64]
+constexpr int kMwCopies = 2 * kMwTileRows * 16 / kMlpThreads;  // global_load_lds per thread and tile (q, gy)
+
+struct MlpWgradLds {
+  uint16_t q[kMwBufs][kMwTileRows * 128];   // q rows, swizzled 256-byte rows (swz_off)
+  uint16_t gy[kMwBufs][kMwTileRows * 128];  // gy padded to 64 columns, in the same 256-byte-row layout
+};
+// the two wavefronts' sums of one hidden block, added in LDS at the end
+struct MlpWgradSum {
+  float dw1[32 * kMlpD];      // [hidden][d]
+  float dw2[32 * kMlpOMax];   // [hidden][o]
+  float db1[32];
+  float db2[kMlpOMax];
+};
+static_assert(4 * sizeof(MlpWgradSum) <= sizeof(MlpWgradLds), "mlp_wgrad_kernel: the sums reuse the tile buffers");
+static_assert(kMwCopies == 4, "mlp_wgrad_kernel: the waits below count four copies per tile");
+
+__global__ __launch_bounds__(kMlpThreads) void mlp_wgrad_kernel(MlpArgs g, float* __restrict__ part1,
+                                                                float* __restrict__ part2, int groups,
+                                                                int tiles_per_group) {
+  __shared__ __attribute__((aligned(16))) MlpWgradLds L;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, gq = lane / 32, lr = lane % 32;
+  // workgroup -> (hidden quad hq, row group gi); dispatch is round robin over
+  // the 8 XCDs, so with groups % 8 == 0 both quads of a row group share one
+  // XCD (and its L2 copy of the rows)
+  int hq, gi;
+  if (groups % 8 == 0) {
+    const int x = blockIdx.x % 8, j = blockIdx.x / 8;
+    hq = j % 2;
+    gi = (j / 2) * 8 + x;
+  } else {
+    hq = blockIdx.x % 2;
+    gi = blockIdx.x / 2;
+  }
+  const int hl = wave / 2, rsub = wave % 2;
+  const int hb = 4 * hq + hl;
+  const int h = 32 * hb + lr;  // this lane's hidden unit in the C layout
+
+  // B operands in registers: W1[h][16ks + 8gq .. +7] and W2[16ks + 8gq .. +7][h] (zero past O), bf16
+  uint4 wb[8], w2b[4];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const float4 u = *reinterpret_cast<const float4*>(g.w1 + h * kMlpD + 16 * ks + 8 * gq);
+    const float4 v = *reinterpret_cast<const float4*>(g.w1 + h * kMlpD + 16 * ks + 8 * gq + 4);
+    wb[ks] = make_uint4(cvt_pk_bf16(u.x, u.y), cvt_pk_bf16(u.z, u.w), cvt_pk_bf16(v.x, v.y), cvt_pk_bf16(v.z, v.w));
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    float w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int o = 16 * ks + 8 * gq + j;
+      w[j] = o < g.O ? g.w2[o * kMlpH + h] : 0.f;
+    }
+    w2b[ks] = make_uint4(cvt_pk_bf16(w[0], w[1]), cvt_pk_bf16(w[2], w[3]), cvt_pk_bf16(w[4], w[5]),
+                         cvt_pk_bf16(w[6], w[7]));
+  }
+  // the bias k-step: a column of ones (A, k = 0 in lane group 0) against b1[h] (B)
+  const uint4 ones_a = mlp_ones_b(gq);
+  const uint4 bias_b =
+      make_uint4(gq == 0 ? static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(g.b1[h]))) : 0u,
+                 0u, 0u, 0u);
+
+  const int64_t tiles = g.rows / kMwTileRows;  // rows is a multiple of 128 (checked on the host)
+  const int64_t t0 = static_cast<int64_t>(gi) * tiles_per_group;
+  const int64_t t1 = t0 + tiles_per_group < tiles ? t0 + tiles_per_group : tiles;
+  // tile copies: q rows (16 chunks of 16 bytes) and gy rows (8 chunks; the
+  // other half of each 256-byte row stays unused), two of each per thread
+  auto issue = [&](int64_t t, int buf) __attribute__((always_inline)) {
+    const int64_t r0 = t * kMwTileRows;
+    const uint16_t* qb = g.q + (r0 / g.seg) * g.q_ss + (r0 % g.seg) * g.q_rs;  // a tile never spans segments
+    const uint16_t* gb = g.gyp + r0 * kMlpOMax;
+#pragma unroll
+    for (int jj = 0; jj < kMwTileRows * 16 / kMlpThreads; ++jj) {
+      const int idx = jj * kMlpThreads + tid;
+      const int r = idx >> 4, c = (idx & 15) ^ swz(r);
+      g2lds16(qb, static_cast<uint32_t>((r * static_cast<int>(g.q_rs) + c * 8) * 2),
+              L.q[buf] + (jj * kMlpThreads + wave * 64) * 8);
+    }
+#pragma unroll
+    for (int jj = 0; jj < kMwTileRows * 16 / kMlpThreads; ++jj) {
+      const int idx = jj * kMlpThreads + tid;
+      const int r = idx >> 4, c = (idx & 15) ^ swz(r);
+      // every wavefront's copy has active lanes: 4 rows of 16 slots, 8 of them holding gy
+      if (c < kMlpOMax / 8)
+        g2lds16(gb, static_cast<uint32_t>((r * kMlpOMax + c * 8) * 2), L.gy[buf] + (jj * kMlpThreads + wave * 64) * 8);
+    }
+  };
+
+  const TileOffs to = tile_offs(lane);
+  f32x16_t acc1[4], acc2[2];  // dW1[hb] (d blocks), dW2^T[hb] (o blocks)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc1[i] = zero16();
+  acc2[0] = acc2[1] = zero16();
+  float db1 = 0.f, db2[2] = {0.f, 0.f};
+  const bool do_db2 = hb == 0;
+  for (int i = 0; i < kMwBufs - 1; ++i)
+    if (t0 + i < t1) issue(t0 + i, i);
+  for (int64_t t = t0; t < t1; ++t) {
+    const int buf = static_cast<int>((t - t0) % kMwBufs);
+    // tiles t+1 .. t+ahead were issued after tile t: wait for tile t alone
+    const int64_t ahead = (t1 - 1 - t) < kMwBufs - 2 ? (t1 - 1 - t) : kMwBufs - 2;
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | 8);  // vmcnt(2·kMwCopies)
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | 4);  // vmcnt(kMwCopies)
+    else
+      wait_vm0();
+    __syncthreads();  // tile t is in buf for everyone; every wavefront is done with tile t-1's buffer
+    if (t + kMwBufs - 1 < t1) issue(t + kMwBufs - 1, static_cast<int>((t + kMwBufs - 1 - t0) % kMwBufs));
+    const uint16_t* qt = L.q[buf];
+    const uint16_t* gt = L.gy[buf];
+    f32x16_t z = mfma32(ones_a, bias_b, zero16());
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) z = mfma32(lds_row8_o(qt, to, 32 * rsub, ks), wb[ks], z);
+    f32x16_t dx = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) dx = mfma32(lds_row8_o(gt, to, 32 * rsub, ks), w2b[ks], dx);
+    uint32_t xw[8], dw[8];
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      float xv[2], dv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float zz = bf16_round(z[r + i]);
+        const float sg = mlp_sigmoid(zz);
+        xv[i] = zz * sg;
+        dv[i] = bf16_round(dx[r + i]) * (sg * fmaf(zz, 1.f - sg, 1.f));  // SiLU'(z1)·dx1
+      }
+      xw[r / 2] = cvt_pk_bf16(xv[0], xv[1]);
+      dw[r / 2] = cvt_pk_bf16(dv[0], dv[1]);
+      db1 += bf16_lo(dw[r / 2]) + bf16_hi(dw[r / 2]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint4 xa = make_uint4(xw[4 * kk], xw[4 * kk + 1], xw[4 * kk + 2], xw[4 * kk + 3]);
+      const uint4 da = make_uint4(dw[4 * kk], dw[4 * kk + 1], dw[4 * kk + 2], dw[4 * kk + 3]);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) acc1[nb] = mfma32(da, lds_kmajor_o(qt, to, 32 * rsub + 16 * kk, nb), acc1[nb]);
+#pragma unroll
+      for (int ob = 0; ob < 2; ++ob) {
+        const uint4 gv = lds_kmajor_o(gt, to, 32 * rsub + 16 * kk, ob);
+        acc2[ob] = mfma32(xa, gv, acc2[ob]);
+        if (do_db2) {
+          const uint32_t w4[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) db2[ob] += bf16_lo(w4[j]) + bf16_hi(w4[j]);
+        }
+      }
+    }
+  }
+  wait_vm0();       // no copy may still target LDS
+  __syncthreads();  // every wavefront is done with the tiles: the sums take their place
+
+  // lanes l and l ^ 32 summed different rows of the same unit / column
+  db1 += __shfl_xor(db1, 32, 64);
+  db2[0] += __shfl_xor(db2[0], 32, 64);
+  db2[1] += __shfl_xor(db2[1], 32, 64);
+  MlpWgradSum& S = reinterpret_cast<MlpWgradSum*>(&L)[hl];
+  for (int step = 0; step < 2; ++step) {
+    if (rsub == step) {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float& d = S.dw1[(8 * (r / 4) + 4 * gq + r % 4) * kMlpD + 32 * nb + lr];
+          d = step == 0 ? acc1[nb][r] : d + acc1[nb][r];
+        }
+#pragma unroll
+      for (int ob = 0; ob < 2; ++ob)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float& d = S.dw2[(8 * (r / 4) + 4 * gq + r % 4) * kMlpOMax + 32 * ob + lr];
+          d = step == 0 ? acc2[ob][r] : d + acc2[ob][r];
+        }
+      if (gq == 0) {
+        S.db1[lr] = step == 0 ? db1 : S.db1[lr] + db1;
+        S.db2[lr] = step == 0 ? db2[0] : S.db2[lr] + db2[0];
+        S.db2[32 + lr] = step == 0 ? db2[1] : S.db2[32 + lr] + db2[1];
+      }
+    }
+    __syncthreads();
+  }
+  // this workgroup's hidden units 128·hq .. +127 of the row group's partials
+  float* p1 = part1 + static_cast<int64_t>(gi) * kMwPart1;
+  float* p2 = part2 + static_cast<int64_t>(gi) * kMwPart2;
+  const MlpWgradSum* SS = reinterpret_cast<const MlpWgradSum*>(&L);
+  for (int e = tid; e < 128 * kMlpD; e += kMlpThreads) {
+    const int hh = e / kMlpD;  // 0..127
+    p1[(128 * hq + hh) * kMlpD + e % kMlpD] = SS[hh / 32].dw1[(hh % 32) * kMlpD + e % kMlpD];
+  }
+  for (int e = tid; e < kMlpOMax * 128; e += kMlpThreads) {
+    const int o = e / 128, hh = e % 128;
+    p2[o * kMlpH + 128 * hq + hh] = SS[hh / 32].dw2[(hh % 32) * kMlpOMax + o];
+  }
+  if (tid < 128) p1[kMlpH * kMlpD + 128 * hq + tid] = SS[tid / 32].db1[tid % 32];
+  if (hq == 0 && tid < kMlpOMax) p2[kMlpOMax * kMlpH + tid] = SS[0].db2[tid];
 }
 
 }  // namespace
@@ -587,7 +812,8 @@ extern "C" int scope_coeff_mlp_bwd(const scope_mlp_params* p, const uint16_t* q,
                                    const float* b1, const float* w2, const float* b2, uint16_t* dq, uint16_t* dz1,
                                    uint16_t* x1, uint16_t* gyp, void* stream) {
   if (int rc = mlp_check(p, q, w1, b1, w2, b2, "scope_coeff_mlp_bwd")) return rc;
-  SCOPE_REQUIRE(gy && dq && dz1 && x1 && gyp, "scope_coeff_mlp_bwd: null pointer");
+  SCOPE_REQUIRE(gy && dq && gyp, "scope_coeff_mlp_bwd: null pointer");
+  SCOPE_REQUIRE((dz1 == nullptr) == (x1 == nullptr), "scope_coeff_mlp_bwd: dz1 and x1 are given together or not at all");
   SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(dq) | reinterpret_cast<uintptr_t>(dz1) | reinterpret_cast<uintptr_t>(x1) |
                   reinterpret_cast<uintptr_t>(gyp)) & 15) == 0,
                 "scope_coeff_mlp_bwd: dq, dz1, x1 and gyp must start on a 16-byte boundary");
@@ -599,4 +825,42 @@ extern "C" int scope_coeff_mlp_bwd(const scope_mlp_params* p, const uint16_t* q,
   g.gyp = gyp;
   hipLaunchKernelGGL(mlp_bwd_kernel, dim3(mlp_grid(p->rows)), dim3(kMlpThreads), 0, as_stream(stream), g);
   return check_launch("MLP backward kernel");
+}
+
+static int mlp_wgrad_groups(int64_t rows) {
+  const int64_t tiles = rows / kMwTileRows;
+  if (tiles < 8) return static_cast<int>(tiles);
+  const int64_t g = tiles < kMwMaxGroups ? tiles - tiles % 8 : kMwMaxGroups;
+  return static_cast<int>(g);
+}
+
+extern "C" int64_t scope_coeff_mlp_wgrad_workspace_bytes(const scope_mlp_params* p) {
+  if (!p || p->rows <= 0) return 0;
+  return static_cast<int64_t>(mlp_wgrad_groups(p->rows)) * (kMwPart1 + kMwPart2) * 4;
+}
+
+extern "C" int scope_coeff_mlp_wgrad(const scope_mlp_params* p, const uint16_t* q, const uint16_t* gyp,
+                                     const float* w1, const float* b1, const float* w2, float* dw1, float* db1,
+                                     float* dw2, float* db2, void* workspace, void* stream) {
+  // b2 takes no part in the gradients: b1 stands in for it in the shared checks
+  if (int rc = mlp_check(p, q, w1, b1, w2, b1, "scope_coeff_mlp_wgrad")) return rc;
+  SCOPE_REQUIRE(gyp && dw1 && db1 && dw2 && db2 && workspace, "scope_coeff_mlp_wgrad: null pointer");
+  SCOPE_REQUIRE(p->seg % 128 == 0, "scope_coeff_mlp_wgrad: seg=%lld must be a multiple of 128", (long long)p->seg);
+  SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(gyp) | reinterpret_cast<uintptr_t>(workspace)) & 15) == 0,
+                "scope_coeff_mlp_wgrad: gyp and workspace must start on a 16-byte boundary");
+  SCOPE_REQUIRE(p->q_rs < (1 << 24), "scope_coeff_mlp_wgrad: q's row stride must be below 2^24");
+  MlpArgs g = mlp_args(p, q, w1, b1, w2, b1);
+  g.gyp = const_cast<uint16_t*>(gyp);
+  const int groups = mlp_wgrad_groups(p->rows);
+  const int64_t tiles = p->rows / kMwTileRows;
+  const int tpg = static_cast<int>((tiles + groups - 1) / groups);
+  float* part1 = static_cast<float*>(workspace);
+  float* part2 = part1 + static_cast<int64_t>(groups) * kMwPart1;
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(mlp_wgrad_kernel, dim3(2 * groups), dim3(kMlpThreads), 0, s, g, part1, part2, groups, tpg);
+  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((kMwPart1 + 63) / 64), dim3(256), 0, s, part1, groups, kMlpH * kMlpD,
+                     kMlpH, 1, dw1, db1);
+  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((kMwPart2 + 63) / 64), dim3(256), 0, s, part2, groups,
+                     kMlpOMax * kMlpH, kMlpOMax, 1, dw2, db2);
+  return check_launch("MLP weight gradient kernels");
 }

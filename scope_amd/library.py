@@ -27,14 +27,16 @@ Operators (schemas are the decorated signatures below):
 * ``scope::coeff_head_fwd`` (+ autograd via ``scope::coeff_head_bwd``) — the
   coefficient head of SpectralBias.forward after its MLP (model/attn_bias.py:
   419-506);
-* ``scope::coeff_mlp`` (+ autograd: the row-wise backward on one fused kernel,
-  ``scope::coeff_mlp_bwd``, the weight and bias gradients on
+* ``scope::coeff_mlp`` (+ autograd: ``scope::coeff_mlp_bwd_wgrad``, the
+  row-wise backward and the weight and bias gradients on the fused kernels;
+  for row layouts those do not take, ``scope::coeff_mlp_bwd`` and
   ``scope::linear_wgrad``) — the head's shared MLP (model/attn_bias.py:271-276,
   380-386).
 
 Optional outputs that an operator cannot return as None (a gradient that is
 not asked for) are returned as empty tensors.
 """
+import functools
 from typing import Optional, Sequence
 
 import torch
@@ -500,6 +502,24 @@ def _(q, gy, w1, b1, w2, b2):
             q.new_empty(lead + (64,)))
 
 
+@torch.library.custom_op(f"{_NS}::coeff_mlp_bwd_wgrad", mutates_args=())
+def coeff_mlp_bwd_wgrad(q: Tensor, gy: Tensor, w1: Tensor, b1: Tensor, w2: Tensor,
+                        b2: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The whole MLP backward on the fused kernels: (dq bf16, dw1, db1, dw2,
+    db2 fp32), the weight and bias gradients from q and the padded output
+    gradient with z1, x1 and dz1 recomputed per tile (never stored)."""
+    dq, _, _, gyp = ops.coeff_mlp_bwd(q, gy, w1, b1, w2, b2, intermediates=False)
+    return (dq,) + ops.coeff_mlp_wgrad(q, gyp, w1, b1, w2)
+
+
+@coeff_mlp_bwd_wgrad.register_fake
+def _(q, gy, w1, b1, w2, b2):
+    O = w2.shape[0]
+    f = functools.partial(q.new_empty, dtype=_F32)
+    return (q.new_empty(tuple(q.shape[:-1]) + (q.shape[-1],)), f((w1.shape[0], w1.shape[1])), f((w1.shape[0],)),
+            f((O, w2.shape[1])), f((O,)))
+
+
 @torch.library.custom_op(f"{_NS}::coeff_mlp", mutates_args=())
 def coeff_mlp(q: Tensor, w1: Tensor, b1: Tensor, w2: Tensor, b2: Tensor) -> Tensor:
     """The head's shared MLP on q [..., D]: y = Linear(w2, b2)(SiLU(Linear(w1,
@@ -539,16 +559,23 @@ def _wgrad(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
 
 def _mlp_backward(ctx, gy):
     """Autograd of the two F.linear and the SiLU (the reference's backward):
-    dx1 = gy·W2, dz1 = SiLU'(z1)·dx1, dq = dz1·W1 with z1 and x1 recomputed
-    (one fused kernel for the forward's fused case, else the torch steps);
-    the weight and bias gradients, whose contraction runs over all rows, on
-    the split-row kernel.  The weights' gradients are those of their bf16
-    copies (rounded to bf16), in the weights' dtype."""
+    dx1 = gy·W2, dz1 = SiLU'(z1)·dx1, dq = dz1·W1 with z1 and x1 recomputed.
+    The forward's fused case with segments of a multiple of 128 rows runs
+    two fused kernels (dq; the weight and bias gradients, recomputing z1, x1
+    and dz1 per tile); other fused cases write x1 and dz1 for the split-row
+    weight-gradient kernel; the rest take the torch steps.  The weights'
+    gradients are those of their bf16 copies (rounded to bf16), in the
+    weights' dtype."""
     if gy is None:
         return None, None, None, None, None
     q, w1, b1, w2, b2 = ctx.saved_tensors
     dt = q.dtype
     O = w2.shape[0]
+    if ops.coeff_mlp_fused(q, w1, w2) and ops.coeff_mlp_wgrad_fused(q):
+        dq, dw1, db1, dw2, db2 = coeff_mlp_bwd_wgrad(q, gy, w1, b1, w2, b2)
+        if not ctx.needs_input_grad[0]:
+            dq = None
+        return dq, dw1.to(w1.dtype), db1.to(b1.dtype), dw2.to(w2.dtype), db2.to(b2.dtype)
     if ops.coeff_mlp_fused(q, w1, w2):
         dq, dz1, x1, gyp = coeff_mlp_bwd(q, gy, w1, b1, w2, b2)
         dw2, db2 = linear_wgrad(gyp, x1, True)

@@ -395,22 +395,56 @@ def coeff_mlp_fwd(q: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch
 
 
 def coeff_mlp_bwd(q: torch.Tensor, gy: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor,
-                  b2: torch.Tensor):
+                  b2: torch.Tensor, *, intermediates: bool = True):
     """The row-wise part of the MLP's backward: (dq [..., 128], dz1 [..., 256],
     x1 [..., 256], gy padded to [..., 64]), bf16, from the output gradient gy
-    [..., O]; z1 and x1 are recomputed from q."""
+    [..., O]; z1 and x1 are recomputed from q.  Without ``intermediates``,
+    dz1 and x1 are not written and come back as None."""
     dev = _gpu("coeff_mlp_bwd", q, gy, w1, b1, w2, b2)
     w1, b1, w2, b2 = (t.contiguous() for t in (w1, b1, w2, b2))
     qc, prm = _mlp_params(q, w2)
     gy = gy.to(q.dtype).contiguous()
     lead = q.shape[:-1]
     dq = torch.empty(lead + (128,), dtype=q.dtype, device=dev)
-    dz1 = torch.empty(lead + (256,), dtype=q.dtype, device=dev)
-    x1 = torch.empty(lead + (256,), dtype=q.dtype, device=dev)
+    dz1 = torch.empty(lead + (256,), dtype=q.dtype, device=dev) if intermediates else None
+    x1 = torch.empty(lead + (256,), dtype=q.dtype, device=dev) if intermediates else None
     gyp = torch.empty(lead + (64,), dtype=q.dtype, device=dev)
     call("scope_coeff_mlp_bwd", C.byref(prm), _p(qc), _p(gy), _p(w1), _p(b1), _p(w2), _p(b2), _p(dq), _p(dz1),
          _p(x1), _p(gyp), _stream(dev))
     return dq, dz1, x1, gyp
+
+
+def coeff_mlp_wgrad_fused(q: torch.Tensor) -> bool:
+    """Whether scope_coeff_mlp_wgrad takes q's row layout (segments of a
+    multiple of 128 rows)."""
+    lq = _row_layout(q)
+    return lq is not None and lq[1] % 128 == 0
+
+
+def coeff_mlp_wgrad(q: torch.Tensor, gyp: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor):
+    """The MLP's weight and bias gradients (dw1 [256][128], db1 [256], dw2
+    [O][256], db2 [O]), fp32 values of the bf16 weight copies' gradients
+    rounded to bf16, from q and the padded output gradient gyp [..., 64]
+    (coeff_mlp_bwd's fourth output); z1, x1 and dz1 are recomputed per tile
+    and never stored."""
+    dev = _gpu("coeff_mlp_wgrad", q, gyp, w1, b1, w2)
+    w1, b1, w2 = (t.contiguous() for t in (w1, b1, w2))
+    qc, prm = _mlp_params(q, w2)
+    if prm.seg % 128:
+        raise RuntimeError(f"coeff_mlp_wgrad: segments of {prm.seg} rows (a multiple of 128 is needed)")
+    gyp = gyp.contiguous()
+    if gyp.dtype != torch.bfloat16 or gyp.shape[-1] != 64 or gyp.numel() != prm.rows * 64:
+        raise RuntimeError("coeff_mlp_wgrad: gyp must be bf16 [..., 64] with q's rows")
+    O = w2.shape[0]
+    dw1 = torch.empty((256, 128), dtype=torch.float32, device=dev)
+    db1 = torch.empty(256, dtype=torch.float32, device=dev)
+    dw2 = torch.empty((64, 256), dtype=torch.float32, device=dev)
+    db2 = torch.empty(64, dtype=torch.float32, device=dev)
+    ws = torch.empty(max(16, int(query("scope_coeff_mlp_wgrad_workspace_bytes", C.byref(prm)))), dtype=torch.uint8,
+                     device=dev)
+    call("scope_coeff_mlp_wgrad", C.byref(prm), _p(qc), _p(gyp), _p(w1), _p(b1), _p(w2), _p(dw1), _p(db1), _p(dw2),
+         _p(db2), _p(ws), _stream(dev))
+    return dw1, db1, dw2[:O], db2[:O]
 
 
 def coeff_head_bwd(y: torch.Tensor, prm: dict, omegas: torch.Tensor, log_omegas: torch.Tensor,

@@ -163,6 +163,53 @@ def test_coeff_mlp_bwd_intermediates():
         assert float((diff > 0).float().mean()) < 0.02
 
 
+@pytest.mark.parametrize("rows", [4096, 131072])
+def test_coeff_mlp_wgrad_matches_split_row_kernel(rows):
+    """The fused weight and bias gradients (z1, x1, dz1 recomputed per tile)
+    against the split-row kernel on the stored x1 / dz1 of the same rows, and
+    both against fp64 sums of those bf16 intermediates: the two add in
+    different orders and both round to bf16 at the end, so they agree to one
+    bf16 step, on all but a few elements exactly."""
+    g = torch.Generator(device=DEV).manual_seed(rows)
+    O = 41
+    q = torch.randn((rows, 128), generator=g, device=DEV).to(torch.bfloat16)
+    w1 = torch.randn((256, 128), generator=g, device=DEV) * 0.05
+    b1 = torch.randn(256, generator=g, device=DEV) * 0.05
+    w2 = torch.randn((O, 256), generator=g, device=DEV) * 0.05
+    b2 = torch.randn(O, generator=g, device=DEV) * 0.05
+    gy = torch.randn((rows, O), generator=g, device=DEV).to(torch.bfloat16)
+    dq, dz1, x1, gyp = ops.coeff_mlp_bwd(q, gy, w1, b1, w2, b2)
+    dq2, none1, none2, gyp2 = ops.coeff_mlp_bwd(q, gy, w1, b1, w2, b2, intermediates=False)
+    assert none1 is None and none2 is None
+    assert torch.equal(dq, dq2) and torch.equal(gyp, gyp2)
+    fused = ops.coeff_mlp_wgrad(q, gyp, w1, b1, w2)
+    dw1, db1 = ops.linear_wgrad(dz1, q, round_bf16=True)
+    dw2, db2 = ops.linear_wgrad(gyp, x1, round_bf16=True)
+    split = (dw1, db1, dw2[:O], db2[:O])
+    torch.cuda.synchronize()
+    q64, d64, x64, g64 = (t.double() for t in (q, dz1, x1, gyp[:, :O]))
+    exact = (d64.t() @ q64, d64.sum(0), g64.t() @ x64, g64.sum(0))
+    for name, a, b, ex in zip(("dw1", "db1", "dw2", "db2"), fused, split, exact):
+        assert a.shape == b.shape == ex.shape, name
+        step = ex.abs() * 2.0 ** -7 + 1e-6 * float(ex.abs().max())
+        assert bool(((a.double() - b.double()).abs() <= step).all()), name
+        assert float((a != b).float().mean()) < 0.05, name
+        # each within bf16 rounding of the fp64 sum (a rounded fp32 sum)
+        assert bool(((a.double() - ex).abs() <= step).all()), name
+
+
+def test_coeff_mlp_wgrad_rejects_bad_layouts():
+    q = torch.zeros((4, 96, 128), device=DEV, dtype=torch.bfloat16)  # segments of 96 rows
+    w1, b1, w2 = torch.zeros((256, 128), device=DEV), torch.zeros(256, device=DEV), torch.zeros((41, 256), device=DEV)
+    gyp = torch.zeros((4, 96, 64), device=DEV, dtype=torch.bfloat16)
+    assert not ops.coeff_mlp_wgrad_fused(q[:, :, :])
+    with pytest.raises(RuntimeError):
+        ops.coeff_mlp_wgrad(q.transpose(0, 1), gyp, w1, b1, w2)
+    with pytest.raises(RuntimeError):
+        ops.coeff_mlp_wgrad(torch.zeros((128, 128), device=DEV, dtype=torch.bfloat16),
+                            torch.zeros((128, 41), device=DEV, dtype=torch.bfloat16), w1, b1, w2)
+
+
 def test_coeff_mlp_fp32_takes_the_torch_steps():
     """fp32 rows are not the fused kernels' case: the operator runs the
     reference's torch steps, equal to the oracle's forward."""
