@@ -29,16 +29,16 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
+// count and fill take a thread per list slot (h, qb, i): a thread per row
+// would wait for up to maxkv returning atomics one after another
 __global__ void tr_count_kernel(const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx, int H,
                                 int QB, int NB, int maxkv, int32_t* __restrict__ q_off) {
-  int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (row >= static_cast<int64_t>(H) * QB) return;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<int64_t>(H) * QB * maxkv) return;
+  const int64_t row = e / maxkv;
+  if (static_cast<int>(e % maxkv) >= kv_num[row]) return;
   const int h = static_cast<int>(row / QB);
-  const int n = kv_num[row];
-  for (int i = 0; i < n; ++i) {
-    const int kb = kv_idx[row * maxkv + i];
-    atomicAdd(&q_off[static_cast<int64_t>(h) * (NB + 1) + kb + 1], 1);
-  }
+  atomicAdd(&q_off[static_cast<int64_t>(h) * (NB + 1) + kv_idx[e] + 1], 1);
 }
 
 __global__ __launch_bounds__(1024) void tr_scan_kernel(int NB, int32_t* __restrict__ q_off) {
@@ -72,17 +72,15 @@ __global__ __launch_bounds__(1024) void tr_scan_kernel(int NB, int32_t* __restri
 __global__ void tr_fill_kernel(const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx, int H,
                                int QB, int NB, int maxkv, const int32_t* __restrict__ q_off,
                                int32_t* __restrict__ cursor, int32_t* __restrict__ q_list) {
-  int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (row >= static_cast<int64_t>(H) * QB) return;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<int64_t>(H) * QB * maxkv) return;
+  const int64_t row = e / maxkv;
+  if (static_cast<int>(e % maxkv) >= kv_num[row]) return;
   const int h = static_cast<int>(row / QB);
   const int qb = static_cast<int>(row % QB);
-  const int n = kv_num[row];
-  const int64_t list_stride = static_cast<int64_t>(QB) * maxkv;
-  for (int i = 0; i < n; ++i) {
-    const int kb = kv_idx[row * maxkv + i];
-    const int pos = atomicAdd(&cursor[static_cast<int64_t>(h) * NB + kb], 1);
-    q_list[h * list_stride + q_off[static_cast<int64_t>(h) * (NB + 1) + kb] + pos] = qb;
-  }
+  const int kb = kv_idx[e];
+  const int pos = atomicAdd(&cursor[static_cast<int64_t>(h) * NB + kb], 1);
+  q_list[static_cast<int64_t>(h) * QB * maxkv + q_off[static_cast<int64_t>(h) * (NB + 1) + kb] + pos] = qb;
 }
 
 // One workgroup of 256 threads per bucket: a list of up to 64 entries is sorted
@@ -192,11 +190,11 @@ static int transpose_launch(const int32_t* kv_num, const int32_t* kv_idx, int H,
   const int64_t n_cur = static_cast<int64_t>(H) * NB;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(n_off, 256)), dim3(256), 0, s, q_off, n_off, 0);
   hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(n_cur, 256)), dim3(256), 0, s, cursor, n_cur, 0);
-  const int64_t rows = static_cast<int64_t>(H) * QB;
-  hipLaunchKernelGGL(tr_count_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
+  const int64_t slots = static_cast<int64_t>(H) * QB * maxkv;
+  hipLaunchKernelGGL(tr_count_kernel, dim3(ceil_div(slots, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off);
   hipLaunchKernelGGL(tr_scan_kernel, dim3(H), dim3(1024), 0, s, NB, q_off);
-  hipLaunchKernelGGL(tr_fill_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
+  hipLaunchKernelGGL(tr_fill_kernel, dim3(ceil_div(slots, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off, cursor, q_list);
   hipLaunchKernelGGL(tr_sort_kernel, dim3(NB, H), dim3(256), cap * sizeof(int), s, NB, QB, maxkv, q_off, q_list, cap);
   return check_launch("transpose kernels");
