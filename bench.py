@@ -591,7 +591,11 @@ def main_ref(args):
                            slope=out[2], use_slope=True)
         return scope_attention(q_, k_, v_, block_mask=bm, scale=0.12, spectral=sp), out[11], bm
 
+    params = list(sb.parameters())
+
     def step():
+        for p_ in params:  # a training step's zero_grad(set_to_none=True): no accumulation adds
+            p_.grad = None
         qd, kd, vd = (x.detach().requires_grad_() for x in (q, k, v))
         y, reg, _ = layer(qd, kd, vd)
         torch.autograd.backward([y, reg], [dout, one])
@@ -619,7 +623,7 @@ def main_ref(args):
 
     t_fwd = time_region(attn_fwd_only, args.steps, args.warmup)
     t_attn = time_region(attn_fwd_bwd, args.steps, args.warmup)
-    graph = graph_step_time(layer, q, k, v, dout, one, args.steps)
+    graph = graph_step_time(layer, q, k, v, dout, one, args.steps, params)
     F_fwd, F_bwd = 4.0 * bs * bs * D * n_act, 10.0 * bs * bs * D * n_act
     res = {
         "metric": "SCOPE layer fwd+bwd on the reference's default path (qk_aug terms, reference-mode lists) "
@@ -658,7 +662,7 @@ def main_ref(args):
     print(json.dumps(res))
 
 
-def graph_step_time(layer, q, k, v, dout, one, steps: int) -> dict:
+def graph_step_time(layer, q, k, v, dout, one, steps: int, params=()) -> dict:
     """ms per fwd+bwd step of `layer` replayed from a captured HIP graph, and
     whether each checked replay's output equals an eager step's bit for bit."""
     import torch
@@ -669,6 +673,8 @@ def graph_step_time(layer, q, k, v, dout, one, steps: int) -> dict:
         # fresh gradients each step, as the eager step's fresh leaves get
         # (accumulating into .grad would add three q-sized sums per step)
         qs.grad = ks.grad = vs.grad = None
+        for p_ in params:
+            p_.grad = None
         y, reg, _ = layer(qs, ks, vs)
         torch.autograd.backward([y, reg], [dout, one])
         return y

@@ -1365,7 +1365,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int NT = 512;
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
 
+  // the gated mode runs its wavefronts in step (the staggered loop's second
+  // code path would cost it registers it does not have)
+  constexpr bool STAGGER = !GATE;
   __shared__ KvTile<MODE> buf0, buf1;
+  __shared__ typename std::conditional<STAGGER, KvTile<MODE>, int>::type buf2;
   __shared__ int kbs[kListLds];
   __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
 
@@ -1471,15 +1475,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
     return it;
   };
-  auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
-    const int kb = kb_at(it / NSUB);
-    const int rd = min(max(qb - kb, 0), a.QB - 1);
-    kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
-  };
   float bt = 0.f, rs_kb = 0.f, pm_kb = 0.f;
   float eb = 0.f;  // pair bias of the current list entry (log2 units)
   const float cs = a.scale_log2;
-  auto compute = [&](int kv0, const KvTile<MODE>& b) __attribute__((always_inline)) {
+  // part A of a tile: S, dP, the probabilities and dS (B operands dsb, pb) and the row sums
+  auto compute_a = [&](int kv0, const KvTile<MODE>& b, uint4 (&dsb)[2], uint4 (&pb)[2])
+                       __attribute__((always_inline)) {
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
     const float off = (MODE == 1 ? bt : rowc) + eb - lse2;
     // probabilities and dS^T: key j = 16·kb4 + 4g + r of the tile
@@ -1595,12 +1596,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       else probs(std::true_type{});
     }
     // B operands of k-step kk: blocks 2kk (slots 0-3) and 2kk+1 (slots 4-7)
-    uint4 dsb[2], pb[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       dsb[kk] = make_uint4(dw[4 * kk], dw[4 * kk + 1], dw[4 * kk + 2], dw[4 * kk + 3]);
       pb[kk] = make_uint4(pw[4 * kk], pw[4 * kk + 1], pw[4 * kk + 2], pw[4 * kk + 3]);
     }
+    rs_kb += rs;
+    pm_kb += pm;
+    rs_tot += rs;
+    pm_tot += pm;
+  };
+  // part B: dQ^T += K^T dS^T and, token modes, the feature gradients
+  auto compute_b = [&](const KvTile<MODE>& b, const uint4 (&dsb)[2], const uint4 (&pb)[2])
+                       __attribute__((always_inline)) {
     // dQ^T += K^T dS^T (step st = 8·kk + md), operands two steps ahead
     {
       constexpr int RB = 2;
@@ -1627,12 +1635,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           facc_p[fb] = mfma16(ft, pb[kk], facc_p[fb]);
         }
     }
-    rs_kb += rs;
-    pm_kb += pm;
-    rs_tot += rs;
-    pm_tot += pm;
   };
-  auto run = [&](int it, int nxt, const KvTile<MODE>& b) __attribute__((always_inline)) {
+  // part A of tile it with the block-mode bookkeeping; false when the
+  // wavefront has nothing to do for this tile
+  auto run_a = [&](int it, int nxt, const KvTile<MODE>& b, uint4 (&dsb)[2], uint4 (&pb)[2])
+                   __attribute__((always_inline)) -> bool {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (MODE == 1 && it % NSUB == 0) {
       // a key block's first tile is never skipped (it starts at or before every row)
@@ -1644,7 +1651,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
            (sa[4] * s1.x + sa[5] * s1.y + sa[6] * s1.z + sa[7] * s1.w);
     }
     if (it % NSUB == 0) eb = pbias ? kbias[it / NSUB] : 0.f;  // per key block (its first tile is never skipped)
-    if (kv0 <= wrow_lo + 15) compute(kv0, b);                 // else every key follows this wavefront's rows
+    const bool act = kv0 <= wrow_lo + 15;  // else every key follows this wavefront's rows
+    if (act) compute_a(kv0, b, dsb, pb);
     if (MODE == 1 && (nxt >= total || nxt / NSUB != it / NSUB)) {
       // last tile of this key block: fold its sums into the coefficient gradients
       const float4* t4 = reinterpret_cast<const float4*>(b.tab);
@@ -1659,25 +1667,85 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       rs_kb = pm_kb = 0.f;
     }
+    return act;
   };
 
   __syncthreads();  // kbs, kbias
+  // Wavefronts 0-3 (one per SIMD) process whole tiles and copy them (256
+  // threads) into three rotating buffers; wavefronts 4-7 run part of a tile
+  // behind: their k-th barrier falls between part A and part B of tile k-1,
+  // so the two wavefronts of a SIMD are not in the same phase.  At the
+  // leading group's k-th barrier the lagging group is done with tile k-2,
+  // whose buffer then takes tile k+1.  Both groups pass n+1 barriers for n
+  // tiles.
+  const int tid4 = tid & 255;
+  auto issue4 = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
+    const int kb = kb_at(it / NSUB);
+    const int rd = min(max(qb - kb, 0), a.QB - 1);
+    kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid4);
+  };
   int cur = next_valid(0);
-  if (cur < total) issue(cur, buf0);
-  while (cur < total) {
-    wait_vm0();
-    __syncthreads();  // tile cur is in buf0; every wavefront is done with buf1
-    int nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf1);
-    run(cur, nxt, buf0);
-    cur = nxt;
-    if (cur >= total) break;
-    wait_vm0();
-    __syncthreads();
-    nxt = next_valid(cur + 1);
-    if (nxt < total) issue(nxt, buf0);
-    run(cur, nxt, buf1);
-    cur = nxt;
+  if constexpr (!STAGGER) {
+    auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
+      const int kb = kb_at(it / NSUB);
+      const int rd = min(max(qb - kb, 0), a.QB - 1);
+      kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
+    };
+    auto step = [&](const KvTile<MODE>& bc, KvTile<MODE>& bn) __attribute__((always_inline)) {
+      wait_vm0();
+      __syncthreads();  // tile cur is in bc; every wavefront is done with bn
+      const int nxt = next_valid(cur + 1);
+      if (nxt < total) issue(nxt, bn);
+      uint4 dsb[2], pb[2];
+      if (run_a(cur, nxt, bc, dsb, pb)) compute_b(bc, dsb, pb);
+      cur = nxt;
+    };
+    if (cur < total) issue(cur, buf0);
+    while (cur < total) {
+      step(buf0, buf1);
+      if (cur >= total) break;
+      step(buf1, buf0);
+    }
+  } else if (wave < 4) {
+    if (cur < total) issue4(cur, buf0);
+    auto lead = [&](const KvTile<MODE>& bc, KvTile<MODE>& bn) __attribute__((always_inline)) {
+      wait_vm0();
+      __syncthreads();  // tile cur is in bc for everyone; the lagging group is done with bn
+      const int nxt = next_valid(cur + 1);
+      if (nxt < total) issue4(nxt, bn);
+      uint4 dsb[2], pb[2];
+      if (run_a(cur, nxt, bc, dsb, pb)) compute_b(bc, dsb, pb);
+      cur = nxt;
+    };
+    if constexpr (STAGGER) {
+      while (cur < total) {
+        lead(buf0, buf1);
+        if (cur >= total) break;
+        lead(buf1, buf2);
+        if (cur >= total) break;
+        lead(buf2, buf0);
+      }
+    }
+    __syncthreads();  // matches the lagging group's last barrier
+  } else {
+    __syncthreads();  // tile 0 is in buf0
+    auto lag = [&](const KvTile<MODE>& bc) __attribute__((always_inline)) {
+      const int nxt = next_valid(cur + 1);
+      uint4 dsb[2], pb[2];
+      const bool act = run_a(cur, nxt, bc, dsb, pb);
+      __syncthreads();  // the leading group starts the next tile
+      if (act) compute_b(bc, dsb, pb);
+      cur = nxt;
+    };
+    if constexpr (STAGGER) {
+      while (cur < total) {
+        lag(buf0);
+        if (cur >= total) break;
+        lag(buf1);
+        if (cur >= total) break;
+        lag(buf2);
+      }
+    }
   }
   wait_vm0();  // no copy may still target LDS when the workgroup exits
 
