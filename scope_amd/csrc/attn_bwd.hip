@@ -1341,7 +1341,7 @@ __device__ __forceinline__ uint4 lds_kmajor16_32(const uint16_t* tile, int kk, i
 // x summed over the four lane groups of 16 (lanes l, l ^ 16, l ^ 32, l ^ 48)
 __device__ __forceinline__ float sum_groups16(float x) {
   x += __shfl_xor(x, 16, 64);
-  return x + __shfl_xor(x, 32, 64);
+  return x + xor32(x);
 }
 
 // The q-major pass with 16 query rows per wavefront on v_mfma_f32_16x16x32_bf16:

@@ -240,6 +240,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 // features at about 16 mantissa bits.
 constexpr int kTokRow = 32;
 
+// x of lane l ^ 32: v_permlane32_swap exchanges the halves of two registers
+// without the LDS round trip of ds_bpermute (with both operands x, the
+// returned first register holds the swapped lanes 32-63, the second 0-31)
+__device__ __forceinline__ float xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

@@ -226,10 +226,22 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     f32x16_t s[2];
     s[0] = zero16();
     s[1] = zero16();
+    {
+      // operands of step st = 2·ks + mb read RA steps ahead into a ring
+      constexpr int RA = 2;
+      uint4 ka[RA + 1];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+      for (int i = 0; i < RA; ++i) ka[i] = lds_row8_o(b.k, to, (i % 2) * 32, i / 2);
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32(lds_row8_o(b.k, to, mb * 32, ks), qreg[ks], s[mb]);
+      for (int st = 0; st < 16; ++st) {
+        const int ks = st / 2, mb = st % 2;
+        if (st + RA < 16) ka[(st + RA) % (RA + 1)] = lds_row8_o(b.k, to, ((st + RA) % 2) * 32, (st + RA) / 2);
+        s[mb] = mfma32(ka[st % (RA + 1)], qreg[ks], s[mb]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     if (TOK) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
@@ -265,7 +277,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[mb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, xor32(mx));
     const float m_t = mx * csm + tconst;
     const bool raise = m_t > m_run + kLazy;
     if (__ballot(raise)) {
@@ -396,7 +408,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
     return;
   }
-  const float l_row = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_row = l_run + xor32(l_run);
   const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
   if (PV) {
     uint16_t* op = a.out + h * a.o_sh + R.row * a.o_st + 4 * g;
