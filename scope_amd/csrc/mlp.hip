@@ -188,10 +188,10 @@ __device__ __forceinline__ float round_bf16(float x) { return static_cast<float>
 // with eight interleaved accumulators (eight loads in flight per lane), and
 // the quarters are added in order: a fixed association, so the result does
 // not depend on scheduling.
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, int groups, int MN, int M,
-                                                           int rnd, float* __restrict__ dw, float* __restrict__ db) {
+__device__ __forceinline__ void wgrad_reduce_block(int blk, const float* __restrict__ part, int groups, int MN, int M,
+                                                   int rnd, float* __restrict__ dw, float* __restrict__ db) {
   __shared__ float qsum[4][64];
-  const int e = blockIdx.x * 64 + threadIdx.x % 64, quarter = threadIdx.x / 64;
+  const int e = blk * 64 + threadIdx.x % 64, quarter = threadIdx.x / 64;
   const int stride = MN + M;
   const int per_q = (groups + 3) / 4;
   const int w0 = quarter * per_q, w1 = min(groups, w0 + per_q);
@@ -216,6 +216,11 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
     dw[e] = t;
   else
     db[e - MN] = t;
+}
+
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, int groups, int MN, int M,
+                                                           int rnd, float* __restrict__ dw, float* __restrict__ db) {
+  wgrad_reduce_block(blockIdx.x, part, groups, MN, M, rnd, dw, db);
 }
 
 int wgrad_groups(const scope_wgrad_params* p) {
@@ -277,6 +282,14 @@ struct MlpLds {
 };
 
 __device__ __forceinline__ float bf16_round(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
+
+// q's row r0 (a wavefront's first row; its 32 rows lie in one segment, as
+// segments are a multiple of 32 rows): the segment split once per
+// wavefront, in scalar registers
+__device__ __forceinline__ const uint16_t* mlp_wave_rows(const MlpArgs& g, int64_t r0) {
+  const int64_t r = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(r0 >> 5))) * 32;
+  return g.q + (r / g.seg) * g.q_ss + (r % g.seg) * g.q_rs;
+}
 
 __device__ __forceinline__ float mlp_sigmoid(float z) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
@@ -344,7 +357,7 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_fwd_kernel(MlpArgs g) {
   for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
     const int64_t row = t * kMlpTileRows + wave * 32 + lr;  // rows is a multiple of 32: whole wavefronts
     if (t * kMlpTileRows + wave * 32 >= g.rows) break;
-    const uint16_t* qp = g.q + (row / g.seg) * g.q_ss + (row % g.seg) * g.q_rs + 8 * gq;
+    const uint16_t* qp = mlp_wave_rows(g, t * kMlpTileRows + wave * 32) + lr * g.q_rs + 8 * gq;
     uint4 xb[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) xb[ks] = *reinterpret_cast<const uint4*>(qp + 16 * ks);
@@ -399,7 +412,7 @@ __global__ __launch_bounds__(kMlpThreads) void mlp_bwd_kernel(MlpArgs g) {
   for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
     const int64_t row = t * kMlpTileRows + wave * 32 + lr;
     if (t * kMlpTileRows + wave * 32 >= g.rows) break;
-    const uint16_t* qp = g.q + (row / g.seg) * g.q_ss + (row % g.seg) * g.q_rs + 8 * gq;
+    const uint16_t* qp = mlp_wave_rows(g, t * kMlpTileRows + wave * 32) + lr * g.q_rs + 8 * gq;
     uint4 xb[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) xb[ks] = *reinterpret_cast<const uint4*>(qp + 16 * ks);
@@ -521,6 +534,18 @@ struct MlpWgradSum {
 };
 static_assert(4 * sizeof(MlpWgradSum) <= sizeof(MlpWgradLds), "mlp_wgrad_kernel: the sums reuse the tile buffers");
 static_assert(kMwCopies == 4, "mlp_wgrad_kernel: the waits below count four copies per tile");
+
+// both reductions of the MLP's partials in one launch: blocks [0, nb1) sum
+// part1 (dW1, db1), the rest part2 (dW2, db2)
+__global__ __launch_bounds__(256) void mlp_wgrad_reduce_kernel(const float* __restrict__ part1,
+                                                               const float* __restrict__ part2, int groups, int nb1,
+                                                               float* __restrict__ dw1, float* __restrict__ db1,
+                                                               float* __restrict__ dw2, float* __restrict__ db2) {
+  if (static_cast<int>(blockIdx.x) < nb1)
+    wgrad_reduce_block(blockIdx.x, part1, groups, kMlpH * kMlpD, kMlpH, 1, dw1, db1);
+  else
+    wgrad_reduce_block(blockIdx.x - nb1, part2, groups, kMlpOMax * kMlpH, kMlpOMax, 1, dw2, db2);
+}
 
 __global__ __launch_bounds__(kMlpThreads) void mlp_wgrad_kernel(MlpArgs g, float* __restrict__ part1,
                                                                 float* __restrict__ part2, int groups,
@@ -768,7 +793,8 @@ static int mlp_check(const scope_mlp_params* p, const uint16_t* q, const float* 
                 "%s: (D, hidden, outputs) = (%d, %d, %d); the kernel takes (128, 256, 1..64)", who, p->D, p->H, p->O);
   SCOPE_REQUIRE(p->rows > 0 && p->rows % 32 == 0, "%s: rows=%lld must be a positive multiple of 32", who,
                 (long long)p->rows);
-  SCOPE_REQUIRE(p->seg > 0 && p->rows % p->seg == 0, "%s: seg=%lld must divide rows", who, (long long)p->seg);
+  SCOPE_REQUIRE(p->seg > 0 && p->seg % 32 == 0 && p->rows % p->seg == 0,
+                "%s: seg=%lld must be a multiple of 32 dividing rows", who, (long long)p->seg);
   SCOPE_REQUIRE(p->q_rs >= kMlpD && p->q_rs % 8 == 0 && p->q_ss >= 0 && p->q_ss % 8 == 0,
                 "%s: q's row stride must cover a row and both strides be multiples of 8 elements", who);
   SCOPE_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(w1)) & 15) == 0,
@@ -858,9 +884,8 @@ extern "C" int scope_coeff_mlp_wgrad(const scope_mlp_params* p, const uint16_t* 
   float* part2 = part1 + static_cast<int64_t>(groups) * kMwPart1;
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(mlp_wgrad_kernel, dim3(2 * groups), dim3(kMlpThreads), 0, s, g, part1, part2, groups, tpg);
-  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((kMwPart1 + 63) / 64), dim3(256), 0, s, part1, groups, kMlpH * kMlpD,
-                     kMlpH, 1, dw1, db1);
-  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((kMwPart2 + 63) / 64), dim3(256), 0, s, part2, groups,
-                     kMlpOMax * kMlpH, kMlpOMax, 1, dw2, db2);
+  const int nb1 = (kMwPart1 + 63) / 64, nb2 = (kMwPart2 + 63) / 64;
+  hipLaunchKernelGGL(mlp_wgrad_reduce_kernel, dim3(nb1 + nb2), dim3(256), 0, s, part1, part2, groups, nb1, dw1, db1,
+                     dw2, db2);
   return check_launch("MLP weight gradient kernels");
 }

@@ -375,11 +375,15 @@ def _mlp_params(q: torch.Tensor, w2: torch.Tensor):
 
 def coeff_mlp_fused(q: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor) -> bool:
     """Whether the fused MLP kernels take these operands: bf16 rows of 128, fp32
-    contiguous weights [256][128] and [O][256] with O <= 64, rows a multiple of
-    32 (otherwise the operator runs the reference's torch steps)."""
-    return (q.dtype == torch.bfloat16 and q.shape[-1] == 128 and w1.dtype == torch.float32
+    contiguous weights [256][128] and [O][256] with O <= 64, rows (and the
+    segments of a [1, H, T, 128] view) a multiple of 32 (otherwise the
+    operator runs the reference's torch steps)."""
+    if not (q.dtype == torch.bfloat16 and q.shape[-1] == 128 and w1.dtype == torch.float32
             and w2.dtype == torch.float32 and tuple(w1.shape) == (256, 128) and w2.dim() == 2
-            and w2.shape[1] == 256 and 1 <= w2.shape[0] <= 64 and q.numel() // 128 % 32 == 0 and q.numel() > 0)
+            and w2.shape[1] == 256 and 1 <= w2.shape[0] <= 64 and q.numel() // 128 % 32 == 0 and q.numel() > 0):
+        return False
+    lq = _row_layout(q)
+    return lq is None or lq[1] % 32 == 0  # no row layout: the operands are copied to one segment
 
 
 def coeff_mlp_fwd(q: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor,
