@@ -46,7 +46,8 @@ __device__ __forceinline__ float load_y(const void* y, bool bf16, int64_t i) {
 // per row the kernels would run two wavefronts per SIMD, each working through
 // M·K exp and sincos calls one after another.
 constexpr int kCoeffGroup = 8;
-constexpr int kCoeffRows = kCoeffThreads / kCoeffGroup;  // rows per workgroup
+constexpr int kCoeffRows = kCoeffThreads / kCoeffGroup;  // rows per workgroup pass
+constexpr int kCoeffPasses = 4;                           // forward: passes per workgroup (one partial per 128 rows)
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
@@ -120,88 +121,91 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_fwd_kernel(
     float* __restrict__ ds_out, float* __restrict__ pi_out, float* __restrict__ bl_out, float* __restrict__ dm_out,
     float* __restrict__ w_out, double* __restrict__ partial) {
   const int m = threadIdx.x % kCoeffGroup;
-  const int64_t row_id = static_cast<int64_t>(blockIdx.x) * kCoeffRows + threadIdx.x / kCoeffGroup;
-  const bool valid = row_id < p.rows;
-  const int64_t row = valid ? row_id : p.rows - 1;  // every lane takes part in the group reductions
-  const int M = p.M, K = p.K;
-  const bool act = m < M;
-  CoeffPeak R;
-  coeff_peak(p, y, row, m, act, R);
-  // cc_k = Σ_m π_m a_mk cos(ω_k Δ*_m): this lane's term, summed over the group
-  float cc[KK], cs[KK];
-  float om = 0.f;  // Σ_k ω_k² a_mk² of this peak
-  {
-    float e[KK], S = 0.f;
-#pragma unroll
-    for (int k = 0; k < KK; ++k) {
-      if (k >= K) break;
-      e[k] = coeff_e(logw, k, R.mu, R.sg);
-      S += e[k];
-    }
-    const float inv = 1.f / (S + p.eps);
-#pragma unroll
-    for (int k = 0; k < KK; ++k) {
-      if (k >= K) break;
-      const float a = e[k] * inv;
-      float sn, cn;
-      sincosf(omegas[k] * R.ds, &sn, &cn);
-      const float w = act ? R.pi * a : 0.f;
-      cc[k] = grp_sum(w * cn);
-      cs[k] = grp_sum(w * sn);
-      if (act) om += omegas[k] * omegas[k] * a * a;
-    }
-  }
-  float b0 = 0.f;
-#pragma unroll
-  for (int k = 0; k < KK; ++k)
-    if (k < K) b0 += cc[k];
-  if (!p.subtract_b0) b0 = 0.f;
-  const float slope = p.use_slope ? p.c_scale * R.th : 0.f;
-  const float mus = grp_sum(act ? R.mu : 0.f);
-  const float dmain = grp_sum(m == R.amax ? R.ds : 0.f);  // one nonzero term
-  if (valid) {
-    const int64_t rk = row * K, rm = row * M;
-#pragma unroll
-    for (int k = 0; k < KK; ++k) {
-      if (k >= K) break;
-      if (k % kCoeffGroup == m) {
-        cc_out[rk + k] = cc[k];
-        cs_out[rk + k] = cs[k];
+  double r_omega = 0.0, r_ent = 0.0, r_edge = 0.0, r_b = 0.0;  // this lane's regulariser terms
+  for (int pass = 0; pass < kCoeffPasses; ++pass) {
+    const int64_t row_id = (static_cast<int64_t>(blockIdx.x) * kCoeffPasses + pass) * kCoeffRows +
+                           threadIdx.x / kCoeffGroup;
+    const bool valid = row_id < p.rows;
+    const int64_t row = valid ? row_id : p.rows - 1;  // every lane takes part in the group reductions
+    const int M = p.M, K = p.K;
+    const bool act = m < M;
+    CoeffPeak R;
+    coeff_peak(p, y, row, m, act, R);
+    // cc_k = Σ_m π_m a_mk cos(ω_k Δ*_m): this lane's term, summed over the group
+    float cc[KK], cs[KK];
+    float om = 0.f;  // Σ_k ω_k² a_mk² of this peak
+    {
+      float e[KK], S = 0.f;
+  #pragma unroll
+      for (int k = 0; k < KK; ++k) {
+        if (k >= K) break;
+        e[k] = coeff_e(logw, k, R.mu, R.sg);
+        S += e[k];
+      }
+      const float inv = 1.f / (S + p.eps);
+  #pragma unroll
+      for (int k = 0; k < KK; ++k) {
+        if (k >= K) break;
+        const float a = e[k] * inv;
+        float sn, cn;
+        sincosf(omegas[k] * R.ds, &sn, &cn);
+        const float w = act ? R.pi * a : 0.f;
+        cc[k] = grp_sum(w * cn);
+        cs[k] = grp_sum(w * sn);
+        if (act) om += omegas[k] * omegas[k] * a * a;
       }
     }
-    if (act) {
-      ds_out[rm + m] = R.ds;
-      pi_out[rm + m] = R.pi;
-      bl_out[rm + m] = load_y(y, p.y_bf16 != 0, row * p.y_stride + 4 * M + m);
+    float b0 = 0.f;
+  #pragma unroll
+    for (int k = 0; k < KK; ++k)
+      if (k < K) b0 += cc[k];
+    if (!p.subtract_b0) b0 = 0.f;
+    const float slope = p.use_slope ? p.c_scale * R.th : 0.f;
+    const float mus = grp_sum(act ? R.mu : 0.f);
+    const float dmain = grp_sum(m == R.amax ? R.ds : 0.f);  // one nonzero term
+    if (valid) {
+      const int64_t rk = row * K, rm = row * M;
+  #pragma unroll
+      for (int k = 0; k < KK; ++k) {
+        if (k >= K) break;
+        if (k % kCoeffGroup == m) {
+          cc_out[rk + k] = cc[k];
+          cs_out[rk + k] = cs[k];
+        }
+      }
+      if (act) {
+        ds_out[rm + m] = R.ds;
+        pi_out[rm + m] = R.pi;
+        bl_out[rm + m] = load_y(y, p.y_bf16 != 0, row * p.y_stride + 4 * M + m);
+      }
+      if (m == 0) {
+        slope_out[row] = slope;
+        b0_out[row] = b0;
+        dm_out[row] = dmain;
+        w_out[row] = p.width_min + (p.width_max - p.width_min) * sigm(mus / static_cast<float>(M));
+      }
     }
-    if (m == 0) {
-      slope_out[row] = slope;
-      b0_out[row] = b0;
-      dm_out[row] = dmain;
-      w_out[row] = p.width_min + (p.width_max - p.width_min) * sigm(mus / static_cast<float>(M));
+    if (p.training) {
+      // per-lane terms: ω (per peak), entropy and zero-mean (per row, lane 0), edge (per peak)
+      const float H = -grp_sum(act ? R.pi * logf(R.pi + p.eps) : 0.f);
+      const float denom = fmaxf(p.delta_cap, 1.f);
+      const float u = fminf(fmaxf(R.ds / denom, 0.f), 1.f);
+      const float edge = fmaxf(p.delta_edge_eps - u, 0.f) + fmaxf(u - (1.f - p.delta_edge_eps), 0.f);
+      float bb = slope * (0.5f * static_cast<float>(p.L - 1)) - b0;
+  #pragma unroll
+      for (int k = 0; k < KK; ++k)
+        if (k < K) bb += cc[k] * cmean[k] + cs[k] * smean[k];
+      if (valid && act) {
+        r_omega += om;
+        r_edge += edge;
+      }
+      if (valid && m == 0) {
+        r_ent += fmaxf(p.entropy_floor - H, 0.f);
+        r_b += bb;
+      }
     }
   }
   if (!p.training) return;
-  // per-lane terms: ω (per peak), entropy and zero-mean (per row, lane 0), edge (per peak)
-  double r_omega = 0.0, r_ent = 0.0, r_edge = 0.0, r_b = 0.0;
-  {
-    const float H = -grp_sum(act ? R.pi * logf(R.pi + p.eps) : 0.f);
-    const float denom = fmaxf(p.delta_cap, 1.f);
-    const float u = fminf(fmaxf(R.ds / denom, 0.f), 1.f);
-    const float edge = fmaxf(p.delta_edge_eps - u, 0.f) + fmaxf(u - (1.f - p.delta_edge_eps), 0.f);
-    float bb = slope * (0.5f * static_cast<float>(p.L - 1)) - b0;
-#pragma unroll
-    for (int k = 0; k < KK; ++k)
-      if (k < K) bb += cc[k] * cmean[k] + cs[k] * smean[k];
-    if (valid && act) {
-      r_omega = om;
-      r_edge = edge;
-    }
-    if (valid && m == 0) {
-      r_ent = fmaxf(p.entropy_floor - H, 0.f);
-      r_b = bb;
-    }
-  }
   // workgroup partial sums, fixed order: lanes by xor-butterfly, wavefronts in index order
   double v[4] = {r_omega, r_ent, r_edge, r_b};
   for (int i = 0; i < 4; ++i)
@@ -219,18 +223,29 @@ __global__ __launch_bounds__(kCoeffThreads) void coeff_fwd_kernel(
 }
 
 // reg = [total, omega, entropy, delta_edge, zero_mean, mean_b]; one workgroup:
-// thread t sums the workgroup partials t, t + 256, ... in order, then a fixed
-// tree over the threads
-__global__ __launch_bounds__(256) void coeff_reg_kernel(scope_coeff_params p, int nblk, const double* __restrict__ partial,
-                                                        float* __restrict__ reg) {
-  __shared__ double red[4][256];
+// thread t sums the workgroup partials t, t + 1024, ... into four interleaved
+// accumulators (loads in flight), added in a fixed order, then a fixed tree
+// over the threads
+constexpr int kRegThreads = 1024;
+__global__ __launch_bounds__(kRegThreads) void coeff_reg_kernel(scope_coeff_params p, int nblk,
+                                                                const double* __restrict__ partial,
+                                                                float* __restrict__ reg) {
+  __shared__ double red[4][kRegThreads];
   const int t = threadIdx.x;
-  double v[4] = {0.0, 0.0, 0.0, 0.0};
-  for (int b = t; b < nblk; b += 256)
-    for (int i = 0; i < 4; ++i) v[i] += partial[static_cast<int64_t>(b) * 4 + i];
-  for (int i = 0; i < 4; ++i) red[i][t] = v[i];
+  double v[4][4] = {};
+  int b = t;
+  for (; b + 3 * kRegThreads < nblk; b += 4 * kRegThreads)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[u][i] += partial[static_cast<int64_t>(b + u * kRegThreads) * 4 + i];
+  for (; b < nblk; b += kRegThreads)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[0][i] += partial[static_cast<int64_t>(b) * 4 + i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[i][t] = (v[0][i] + v[1][i]) + (v[2][i] + v[3][i]);
   __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
+  for (int o = kRegThreads / 2; o > 0; o >>= 1) {
     if (t < o)
       for (int i = 0; i < 4; ++i) red[i][t] += red[i][t + o];
     __syncthreads();
@@ -400,7 +415,7 @@ static int coeff_check(const scope_coeff_params* p, const char* who) {
 
 extern "C" int64_t scope_coeff_head_workspace_bytes(const scope_coeff_params* p) {
   if (!p || p->rows <= 0) return 0;
-  return static_cast<int64_t>(ceil_div(p->rows, kCoeffRows)) * 4 * static_cast<int64_t>(sizeof(double));
+  return static_cast<int64_t>(ceil_div(p->rows, kCoeffPasses * kCoeffRows)) * 4 * static_cast<int64_t>(sizeof(double));
 }
 
 extern "C" int scope_coeff_head_fwd(const scope_coeff_params* p, const void* y, const float* omegas,
@@ -415,7 +430,7 @@ extern "C" int scope_coeff_head_fwd(const scope_coeff_params* p, const void* y, 
                 "scope_coeff_head_fwd: null pointer");
   SCOPE_REQUIRE(!p->training || (reg && workspace && cos_mean && sin_mean),
                 "scope_coeff_head_fwd: training needs reg, workspace, cos_mean and sin_mean");
-  const int nblk = ceil_div(p->rows, kCoeffRows);
+  const int nblk = ceil_div(p->rows, kCoeffPasses * kCoeffRows);
   hipStream_t s = as_stream(stream);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(nblk), dim3(kCoeffThreads), 0, s, *p, y, omegas, log_omegas, cos_mean, sin_mean,
@@ -426,7 +441,8 @@ extern "C" int scope_coeff_head_fwd(const scope_coeff_params* p, const void* y, 
   else go(coeff_fwd_kernel<kMaxK>);
   rc = check_launch("coeff_fwd_kernel");
   if (rc || !p->training) return rc;
-  hipLaunchKernelGGL(coeff_reg_kernel, dim3(1), dim3(256), 0, s, *p, nblk, static_cast<const double*>(workspace), reg);
+  hipLaunchKernelGGL(coeff_reg_kernel, dim3(1), dim3(kRegThreads), 0, s, *p, nblk, static_cast<const double*>(workspace),
+                     reg);
   return check_launch("coeff_reg_kernel");
 }
 
