@@ -532,7 +532,7 @@ __device__ __forceinline__ void dkv_issue_part(const AttnArgs& a, int h, int64_t
     return;
   }
   if (MODE >= 2) {
-    const int r = tid >> 2, c = (tid & 3) ^ ((r >> 2) & 3);
+    const int r = tid >> 2, c = (tid & 3) ^ swz32(r);
     const char* base = reinterpret_cast<const char*>(a.qfeat + (hT + q0) * kTokRow);
     g2lds16(base, static_cast<uint32_t>((r * kTokRow + c * 8) * 2), reinterpret_cast<uint16_t*>(b.rb) + wave * 64 * 8);
   }

@@ -153,9 +153,13 @@ __device__ __forceinline__ uint4 lds_kmajor_o(const uint16_t* tile, const TileOf
 }
 
 // ---- swizzled 32-column tiles (64-byte rows: token features) ---------------
-// The 16-byte chunk c of row r is stored at chunk c ^ ((r/4) % 4): row reads
-// of 16 consecutive rows and transpose reads of 4 rows are conflict free.
-__device__ __forceinline__ int swz32_off(int r, int d) { return r * 32 + (((d >> 3) ^ ((r >> 2) & 3)) << 3) + (d & 7); }
+// The 16-byte chunk c of row r is stored at chunk c ^ swz32(r), swz32(r) the
+// two bits of (r/4) % 4 reversed.  Rows r and r + 4 lie 256 bytes apart, on the
+// same banks; with the reversed bits the transpose reads of lane groups 0 and
+// 1 (rows 0-3 and 4-7, chunks {0, 1} of each) land on chunks {0, 1} and
+// {2, 3}.  Row reads of 16 consecutive rows stay conflict free.
+__device__ __forceinline__ int swz32(int r) { return ((r >> 3) & 1) | (((r >> 2) & 1) << 1); }
+__device__ __forceinline__ int swz32_off(int r, int d) { return r * 32 + (((d >> 3) ^ swz32(r)) << 3) + (d & 7); }
 
 __device__ __forceinline__ uint4 lds_row8_32(const uint16_t* tile, int r, int d) {
   return *reinterpret_cast<const uint4*>(tile + swz32_off(r, d));
@@ -404,7 +408,7 @@ __device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, 
 #pragma unroll
     for (int idx0 = 0; idx0 < 256; idx0 += NT) {
       const int idx = idx0 + tid;
-      const int r = idx >> 2, c = (idx & 3) ^ ((r >> 2) & 3);
+      const int r = idx >> 2, c = (idx & 3) ^ swz32(r);
       if (idx < 256)
         g2lds16(fbase, static_cast<uint32_t>((r * kTokRow + c * 8) * 2), b.f + (idx0 + wave * 64) * 8);
     }
