@@ -151,7 +151,8 @@ int scope_pointer_bwd(const scope_ptr_bwd_params* p, const float* qbar, const fl
  * Transposed (q-major) lists.  Replaces BlockMask.from_kv_blocks ->
  * _transpose_ordered (torch:nn/attention/flex_attention.py:399-441, called at
  * model/attn_bias.py:867-873) with a compact CSR: for each kv block the
- * q-blocks that list it, ascending.
+ * q-blocks that list it, ascending; a head's entries past q_off[h][NB] are
+ * set to -1.
  * ---------------------------------------------------------------------- */
 int64_t scope_transpose_workspace_bytes(int H, int NB);
 int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB,

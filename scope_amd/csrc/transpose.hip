@@ -41,7 +41,10 @@ __global__ void tr_count_kernel(const int32_t* __restrict__ kv_num, const int32_
   atomicAdd(&q_off[static_cast<int64_t>(h) * (NB + 1) + kv_idx[e] + 1], 1);
 }
 
-__global__ __launch_bounds__(1024) void tr_scan_kernel(int NB, int32_t* __restrict__ q_off) {
+// also sets the head's list entries past its total to -1 (the fill kernel
+// writes only below it)
+__global__ __launch_bounds__(1024) void tr_scan_kernel(int NB, int32_t* __restrict__ q_off, int64_t list_len,
+                                                       int32_t* __restrict__ q_list) {
   const int h = blockIdx.x;
   int32_t* row = q_off + static_cast<int64_t>(h) * (NB + 1);
   __shared__ int tsum[1024];
@@ -67,6 +70,9 @@ __global__ __launch_bounds__(1024) void tr_scan_kernel(int NB, int32_t* __restri
     __syncthreads();
   }
   if (threadIdx.x == 0) row[0] = 0;
+  const int64_t total = carry_s;  // the head's entry count (carry after the last chunk)
+  int32_t* lst = q_list + static_cast<int64_t>(h) * list_len;
+  for (int64_t i = total + threadIdx.x; i < list_len; i += 1024) lst[i] = -1;
 }
 
 __global__ void tr_fill_kernel(const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx, int H,
@@ -193,7 +199,7 @@ static int transpose_launch(const int32_t* kv_num, const int32_t* kv_idx, int H,
   const int64_t slots = static_cast<int64_t>(H) * QB * maxkv;
   hipLaunchKernelGGL(tr_count_kernel, dim3(ceil_div(slots, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off);
-  hipLaunchKernelGGL(tr_scan_kernel, dim3(H), dim3(1024), 0, s, NB, q_off);
+  hipLaunchKernelGGL(tr_scan_kernel, dim3(H), dim3(1024), 0, s, NB, q_off, static_cast<int64_t>(QB) * maxkv, q_list);
   hipLaunchKernelGGL(tr_fill_kernel, dim3(ceil_div(slots, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off, cursor, q_list);
   hipLaunchKernelGGL(tr_sort_kernel, dim3(NB, H), dim3(256), cap * sizeof(int), s, NB, QB, maxkv, q_off, q_list, cap);

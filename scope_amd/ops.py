@@ -216,20 +216,19 @@ def pointer_bwd(qbar: torch.Tensor, kbar: torch.Tensor, kv_num: torch.Tensor, kv
 
 def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int, tail: int | None = None):
     """q lists (CSR): q_off [H, NB+1], q_list [H, QB*MAXKV].  Entries of a
-    head's q_list past q_off[h, NB] are left as allocated, or set to ``tail``."""
+    head's q_list past q_off[h, NB] are -1 (the kernels set them), or ``tail``."""
     dev = _gpu("transpose_blocks", kv_num, kv_idx)
     kv_num = _i32(kv_num.reshape(kv_num.shape[-2], kv_num.shape[-1]))
     H, QB = kv_num.shape
     kv_idx = _i32(kv_idx.reshape(H, QB, kv_idx.shape[-1]))
     maxkv = kv_idx.shape[-1]
     q_off = torch.empty((H, NB + 1), dtype=torch.int32, device=dev)
-    if tail is None:
-        q_list = torch.empty((H, QB * maxkv), dtype=torch.int32, device=dev)
-    else:
-        q_list = torch.full((H, QB * maxkv), int(tail), dtype=torch.int32, device=dev)
+    q_list = torch.empty((H, QB * maxkv), dtype=torch.int32, device=dev)
     ws = torch.empty(max(1, query("scope_transpose_workspace_bytes", H, NB)), dtype=torch.uint8, device=dev)
     call("scope_transpose_blocks", _p(kv_num), _p(kv_idx), H, QB, NB, maxkv, _p(q_off), _p(q_list), _p(ws),
          _stream(dev))
+    if tail is not None and int(tail) != -1:
+        q_list.masked_fill_(q_list == -1, int(tail))
     return q_off, q_list
 
 
@@ -291,7 +290,8 @@ def coeff_head_fwd(y: torch.Tensor, prm: dict, omegas: torch.Tensor, log_omegas:
                slope=torch.empty(lead, **f), b0=torch.empty(lead, **f), delta_star=torch.empty(lead + (M,), **f),
                pi=torch.empty(lead + (M,), **f), budget_logits=torch.empty(lead + (M,), **f),
                delta_main=torch.empty(lead, **f), width=torch.empty(lead, **f))
-    reg = torch.zeros(6, **f)
+    # the regulariser kernel writes all six values when training; otherwise they are zero
+    reg = torch.empty(6, **f) if prm["training"] else torch.zeros(6, **f)
     ws = torch.empty(max(1, int(query("scope_coeff_head_workspace_bytes", C.byref(c)))), dtype=torch.uint8,
                      device=dev)
     call("scope_coeff_head_fwd", C.byref(c), _p(y), _p(_f32(omegas)), _p(_f32(log_omegas)), _p(_f32(cos_mean)),

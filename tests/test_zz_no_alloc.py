@@ -46,7 +46,7 @@ def test_transpose_noalloc_equals_workspace_entry_point():
             n = int(want_off[h, NB])
             assert n == int(kv_num[h].sum())
             assert torch.equal(q_list[h, :n], want_list[h, :n]), f"head {h}"
-            assert bool((q_list[h, n:] == -7).all())  # nothing written past the filled entries
+            assert bool((q_list[h, n:] == -1).all())  # the entries past the filled ones are set to -1
 
 
 def test_transpose_noalloc_rejects_sizes_beyond_the_static_scratch():
