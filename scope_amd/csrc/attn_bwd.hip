@@ -325,13 +325,19 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     }
   }
 
-  // ---- epilogue: dQ = scale·o, coefficient gradients
+  // ---- epilogue: dQ = scale·o, coefficient gradients.  The lane's row and
+  // the addresses from it are formed again here from an opaque copy of the
+  // lane index, so that none of them is held (or spilled) through the tiles.
+  int lane_e = lane;
+  asm volatile("" : "+v"(lane_e));
+  const int ge = lane_e / 32, lrow_e = wave * 32 + lane_e % 32;
+  R.row = static_cast<int>(q0) + lrow_e;
   rs_tot += __shfl_xor(rs_tot, 32, 64);
   const float dd_err = rs_tot;  // Δ_true - Δ
   // the kv-major pass reads Δ_true = Δ + (Δ_true - Δ): its dS, dK and the
   // pair-bias sums then do not carry the bf16 rounding of the output
-  if (g == 0) a.delta[hT + R.row] = -(R.delta + dd_err);  // stored negated: the kv-major dP accumulators start from it
-  uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * g;
+  if (ge == 0) a.delta[hT + R.row] = -(R.delta + dd_err);  // stored negated: the kv-major dP accumulators start from it
+  uint16_t* dqp = a.dq + h * a.q_sh + R.row * a.q_st + 4 * ge;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
 #pragma unroll
@@ -343,18 +349,18 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
     }
   if (MODE == 1 && a.dcoeff_cos) {
     // g = 0 writes the cos coefficients of its row, g = 1 the sin ones
-    float* dst = (g == 0 ? a.dcoeff_cos : a.dcoeff_sin) + (hT + R.row) * a.K;
+    float* dst = (ge == 0 ? a.dcoeff_cos : a.dcoeff_sin) + (hT + R.row) * a.K;
     for (int k = 0; k < a.K; ++k) {
-      const float rs = gacc[row32_off(lrow_, 4 * g + k / 4) + k % 4];
-      const float pm = gacc[row32_off(lrow_, 4 * g + 2 + k / 4) + k % 4];
+      const float rs = gacc[row32_off(lrow_e, 4 * ge + k / 4) + k % 4];
+      const float pm = gacc[row32_off(lrow_e, 4 * ge + 2 + k / 4) + k % 4];
       dst[k] = a.beta * (rs - dd_err * pm);
     }
   }
   // ---- this row's softmax offset for every listed key block (the block term
   // as in the loop, plus the pair bias, minus lse), read per tile by the
   // kv-major pass; after the dQ store, when its accumulators are free
-  if (g == 0) {
-    float* rof = a.roff + lrow * a.maxkv * BS + lrow_;
+  if (ge == 0) {
+    float* rof = a.roff + lrow * a.maxkv * BS + lrow_e;
     for (int e = 0; e < n; ++e) {
       float t = pbias ? kbias[e] : 0.f;
       if (MODE == 1) {
@@ -363,7 +369,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
         float acc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float4 c4 = *reinterpret_cast<const float4*>(coef + row16_off(lrow_, i)), tt = t4[i];
+          const float4 c4 = *reinterpret_cast<const float4*>(coef + row16_off(lrow_e, i)), tt = t4[i];
           acc[i] = c4.x * tt.x + c4.y * tt.y + c4.z * tt.z + c4.w * tt.w;
         }
         t += (acc[0] + acc[1]) + (acc[2] + acc[3]);
