@@ -359,6 +359,8 @@ __global__ __launch_bounds__(256) void block_means_kernel(const uint16_t* __rest
   float sq[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float sk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   const int64_t t0 = static_cast<int64_t>(b) * bs;
+  // up to four rows' loads in flight per thread
+#pragma unroll 4
   for (int r = g; r < bs; r += kGroups) {
     const uint4 vq = *reinterpret_cast<const uint4*>(q + h * q_sh + (t0 + r) * q_st + c * 8);
     const uint4 vk = *reinterpret_cast<const uint4*>(k + h * k_sh + (t0 + r) * k_st + c * 8);
