@@ -1,7 +1,10 @@
-// Weight and bias gradients of a linear layer over many rows, for the MLP of
-// SpectralBias (model/attn_bias.py:271-276, 380-398: Linear(D, 2D) -> SiLU
-// -> Linear(2D, 5M+1), shared across heads and applied to every (b, h, t)
-// row).  Autograd's weight gradient of such a layer is a GEMM whose
+// The MLP of SpectralBias (model/attn_bias.py:271-276, 380-398: Linear(D,
+// 2D) -> SiLU -> Linear(2D, 5M+1), shared across heads and applied to every
+// (b, h, t) row): the fused forward, the row-wise backward (dq), the fused
+// weight and bias gradients that recompute the hidden layer per tile, and
+// the general split-row weight gradient of a linear layer below.
+//
+// Split-row weight gradient: autograd's weight gradient of a linear layer is a GEMM whose
 // contraction runs over all B·H·T rows (131072 at T = 16384, H = 8):
 //   dW[m][n] = Σ_r A[r][m] B[r][n],   db[m] = Σ_r A[r][m]
 // with A the output gradient and B the layer input.  The contraction is
@@ -248,8 +251,9 @@ void launch_wgrad(const WgradArgs& g, int groups, hipStream_t s) {
 //   x1 = SiLU(bf16(Z^T + b1)) in the C layout, which is directly the B
 //   operand of Y^T += W2·X1^T (A: W2^T through transpose reads).
 // The backward recomputes Z^T, takes dX1^T = W2^T·gY^T, dZ1 = SiLU'(z)·dx1
-// and dQ^T += W1^T·dZ1^T, and writes x1, dz1 and the output gradient padded
-// to 64 columns for the weight-gradient kernel above.  b1 enters Z^T as one
+// and dQ^T += W1^T·dZ1^T, and writes dq and the output gradient padded to 64
+// columns (for the fused weight-gradient kernel below), and x1 and dz1 when
+// asked (for the split-row kernel above).  b1 enters Z^T as one
 // more k-step (a row of ones against the bias).  Every intermediate is
 // rounded to bf16 where the reference's tensors are (z1, x1, dx1, dz1): the
 // head's outputs downstream (the peak positions among them) are not
