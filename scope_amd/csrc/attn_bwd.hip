@@ -13,16 +13,18 @@
 //   (C_k = Σ_j dS cos ω_k j, S_k = Σ_j dS sin ω_k j), slope / b0 / gate per element.
 // Pass A also stores, for the modes without token offsets, each row's
 // softmax offset for every listed key block (block term + pair bias - lse, log2
-// units): pass B copies the 64 offsets of a query tile into LDS with the tile
-// instead of recomputing them in every wavefront.
+// units), and in the token modes each row's offset without the pair bias
+// (-β·b0 - lse) and β·slope: pass B copies those of a query tile into LDS
+// with the tile instead of recomputing them in every wavefront.
 // Plan: per key block, its q-list is cut into chunks of kChunk q-blocks.
 // Pass B (kv-major, one workgroup per (head, 128 keys of a key block, chunk)):
 //   dK, dV over the q-list; a block with one chunk writes bf16 directly,
 //   longer lists write fp32 partials that a reduce kernel sums in chunk order
-//   (deterministic, no floating-point atomics).  Modes 0 and 1 run 16 keys
-//   per wavefront on v_mfma_f32_16x16x32_bf16, eight wavefronts in two
-//   staggered groups (attn_bwd_dkv16_kernel); the token modes run 32 keys per
-//   wavefront on the 32x32x16 form, four wavefronts (attn_bwd_dkv_kernel).
+//   (deterministic, no floating-point atomics).  Every mode but the gated
+//   token mode runs 16 keys per wavefront on v_mfma_f32_16x16x32_bf16, eight
+//   wavefronts in two staggered groups (attn_bwd_dkv16_kernel); the gated
+//   token mode runs 32 keys per wavefront on the 32x32x16 form, four
+//   wavefronts (attn_bwd_dkv_kernel).
 #include <math.h>
 
 #include <algorithm>

@@ -3,8 +3,9 @@
 // torch:nn/attention/flex_attention.py:399-441 (_transpose_ordered), which
 // builds a dense [H, NB, NB+1] matrix and argsorts it.
 //
-//   count  : q_off[h][kb+1] += 1 per listed (h, qb, kb)      (integer atomics)
-//   scan   : exclusive prefix sum per head (one workgroup per head)
+//   count  : q_off[h][kb+1] += 1 per listed (h, qb, kb)      (integer atomics, a thread per list slot)
+//   scan   : exclusive prefix sum per head (one workgroup per head); the
+//            head's list entries past its total set to -1
 //   fill   : q_list[h][q_off[h][kb] + cursor++] = qb          (integer atomics)
 //   sort   : each bucket sorted ascending (bitonic in LDS)
 // The atomics only fix the set of each bucket; the sort fixes its order, so
