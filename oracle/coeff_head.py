@@ -1,9 +1,9 @@
 """Oracle: the coefficient head of ``SpectralBias.forward`` in torch ops.
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).  The product runs the
-MLP's GEMMs in torch with its weight and bias gradients on a HIP kernel
-(``scope_linear_wgrad``), and the rest in the fused HIP kernels
-(``scope_coeff_head_fwd`` / ``scope_coeff_head_bwd``); this restates the
+MLP on fused HIP kernels (``scope_coeff_mlp_fwd`` / ``_bwd`` / ``_wgrad``)
+and the rest in the fused head kernels (``scope_coeff_head_fwd`` /
+``scope_coeff_head_bwd``); this restates the
 reference's steps one tensor op at a time, so autograd gives the reference's
 gradients.
 

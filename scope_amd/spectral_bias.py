@@ -231,9 +231,9 @@ class SpectralBias(nn.Module):
             q = q.detach()
         dt = q.dtype
         if self.share_across_heads:
-            # the two F.linear and the SiLU of the reference, as one operator (one
-            # fused kernel each way) whose weight and bias gradients (a
-            # contraction over all B·H·T rows) run on the split-row kernel
+            # the two F.linear and the SiLU of the reference, as one operator:
+            # a fused kernel forward, and backward one for dq and one for the
+            # weight and bias gradients (a contraction over all B·H·T rows)
             fc1: nn.Linear = self.mlp[0]
             fc2: nn.Linear = self.mlp[2]
             return library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias)
@@ -264,8 +264,8 @@ class SpectralBias(nn.Module):
 
     def forward(self, q: Tensor, *, docs: Tensor | None = None) -> tuple[Tensor, ...]:
         """q [B,H,L,D] on the GPU -> the reference's 12-tuple
-        (model/attn_bias.py:385-401): the MLP in torch, the rest in the fused
-        coefficient-head kernels.  Disabled, it returns zeros and uniform π
+        (model/attn_bias.py:385-401): the MLP and the rest of the head in fused
+        HIP kernels.  Disabled, it returns zeros and uniform π
         like the reference (:411-417).  There is no CPU path."""
         if not q.is_cuda:
             raise RuntimeError(f"SpectralBias.forward: q must live on the GPU (got {q.device}); there is no CPU path")
@@ -285,7 +285,7 @@ class SpectralBias(nn.Module):
         return z_k, z_k, z_l, z_l, z_m, z_pi, z_m, z_l, z_l, cos_wD, sin_wD, torch.zeros((), **f)
 
     def _forward_fused(self, q: Tensor, docs: Tensor | None) -> tuple[Tensor, ...]:
-        """GPU forward: the MLP in torch, then the fused coefficient head."""
+        """GPU forward: the fused MLP, then the fused coefficient head."""
         B, H, L, Dh = q.shape
         if H != self.num_heads:
             raise ValueError(f"expected H={self.num_heads}, got {H}")

@@ -159,6 +159,39 @@ def test_fused_head_matches_torch_steps_at_training_shape():
     assert err <= 2e-2 * gt.abs().max().item(), f"dq max err {err:.3e} vs max {gt.abs().max().item():.3e}"
 
 
+def test_fused_head_ragged_rows():
+    """600 rows (H=3, L=200: not a multiple of a forward workgroup's 128 rows,
+    so its last passes hold no rows) with M=5 peaks (three of a row's eight
+    lanes idle), training mode with the regularisers: the fused head against
+    the oracle's torch steps on the same y (outputs, reg_loss, and dy of
+    Σ⟨out, G⟩ + reg_loss)."""
+    from oracle.coeff_head import coeff_head_forward
+    from scope_amd import SpectralBias
+
+    torch.manual_seed(3)
+    H, L, M, K = 3, 200, 5, 6
+    sb = SpectralBias(head_dim=128, num_heads=H, L_train=L, M=M, K=K).to(DEV).train()
+    q = torch.randn((1, H, L, 128), device=DEV)
+    y0 = torch.randn((1, H, L, 5 * M + 1), device=DEV) * 2
+    y1, y2 = y0.clone().requires_grad_(), y0.clone().requires_grad_()
+    sb._mlp_forward = lambda _q: y1  # the head alone, on the given y
+    out_f = sb(q)
+    out_t = coeff_head_forward(sb, q, y=y2)
+    for i, n in enumerate(NAMES):
+        a, b = out_f[i].float(), out_t[i].float()
+        tol = 1e-4 * b.abs().max().item() + 1e-4 * b.abs()
+        assert ((a - b).abs() <= tol).all(), f"{n}: max err {(a - b).abs().max().item():.3e}"
+    assert torch.allclose(out_f[11], out_t[11], rtol=2e-4), (float(out_f[11]), float(out_t[11]))
+    g = torch.Generator(device=DEV).manual_seed(4)
+    G = [torch.randn(out_f[i].shape, generator=g, device=DEV) for i in range(9)]
+    lf = sum((out_f[i] * G[i]).sum() for i in range(9)) + out_f[11]
+    lt = sum((out_t[i] * G[i]).sum() for i in range(9)) + out_t[11]
+    gf, = torch.autograd.grad(lf, [y1])
+    gt, = torch.autograd.grad(lt, [y2])
+    tol = 2e-4 * gt.abs().max().item() + 2e-4 * gt.abs()
+    assert ((gf - gt).abs() <= tol).all(), f"dy max err {(gf - gt).abs().max().item():.3e}"
+
+
 def test_disabled_forward_on_gpu():
     """enabled=False returns zeros and uniform π like the reference
     (model/attn_bias.py:411-417), on the GPU."""

@@ -163,13 +163,15 @@ def test_coeff_mlp_bwd_intermediates():
         assert float((diff > 0).float().mean()) < 0.02
 
 
-@pytest.mark.parametrize("rows", [4096, 131072])
+@pytest.mark.parametrize("rows", [256, 640, 4096, 131072])
 def test_coeff_mlp_wgrad_matches_split_row_kernel(rows):
     """The fused weight and bias gradients (z1, x1, dz1 recomputed per tile)
     against the split-row kernel on the stored x1 / dz1 of the same rows, and
     both against fp64 sums of those bf16 intermediates: the two add in
     different orders and both round to bf16 at the end, so they agree to one
-    bf16 step, on all but a few elements exactly."""
+    bf16 step, on all but a few elements exactly.  256 rows make four row
+    groups (fewer than the 8 XCDs: the plain workgroup order), 640 rows eight
+    groups of which three hold no tile."""
     g = torch.Generator(device=DEV).manual_seed(rows)
     O = 41
     q = torch.randn((rows, 128), generator=g, device=DEV).to(torch.bfloat16)
