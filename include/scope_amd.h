@@ -482,6 +482,26 @@ int scope_decoder_qkv_glue(int T, int H, int D, int64_t rows, float eps, float v
                            uint16_t* k_out, uint16_t* v_out, int64_t k_sh, int64_t k_st, int64_t v_sh,
                            int64_t v_st, int cache_at_pos, void* stream);
 
+/* One row-vector product of the decoder's token step, fused with the ops
+ * around it (replaces, for one token, the torch chains of scoped_medium.py:
+ * the qkv projection of a normed row :339 with norm :266-267, the MLP
+ * :318-321, the residual adds :606-613 with the U-net skip :607, and the
+ * head :624-626).  x [K] bf16, W [N, K] bf16 with row stride ldw (elements):
+ *   x := bf16(x + addx) when addx [K] is given, that row written to xout;
+ *   x := F.rms_norm(x) (in fp32 with eps, rounded to bf16) when norm != 0;
+ *   z = bf16(W·x) per row, then by epi:
+ *     SCOPE_GEMV_PLAIN z -> out bf16 [N]
+ *     SCOPE_GEMV_RELU2 bf16(relu(z)²) -> out bf16 [N]
+ *     SCOPE_GEMV_RESID bf16(res + z), res [N] bf16 (out may be res) -> out bf16 [N]
+ *     SCOPE_GEMV_LOGIT 30·σ(z / 7.5) -> out fp32 [N]
+ * K in {256, 512, 1024, 2048, 4096}; x, w, addx and xout 16-byte aligned; out
+ * must not overlap x, addx or w.  No counterpart in the reference, whose
+ * forward runs these as separate ops on the whole sequence. */
+enum { SCOPE_GEMV_PLAIN = 0, SCOPE_GEMV_RELU2 = 1, SCOPE_GEMV_RESID = 2, SCOPE_GEMV_LOGIT = 3 };
+int scope_decoder_gemv(int N, int K, int64_t ldw, int norm, float eps, int epi, const uint16_t* x,
+                       const uint16_t* addx, uint16_t* xout, const uint16_t* w, const uint16_t* res,
+                       void* out, void* stream);
+
 int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
 int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
                    const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,

@@ -117,6 +117,7 @@ _PROTOS = {
     "scope_decode_attn_at": (c_int, [C.POINTER(DecodeParams)] + [P] * 11),
     "scope_decoder_qkv_glue": (c_int, [c_int, c_int, c_int, c_int64, c_float, c_float, c_float, P, P, P, P, P,
                                        c_int64, c_int64, P, P, P, c_int64, c_int64, c_int64, c_int64, c_int, P]),
+    "scope_decoder_gemv": (c_int, [c_int, c_int, c_int64, c_int, c_float, c_int, P, P, P, P, P, P, P]),
     "scope_attn_bwd": (c_int, [C.POINTER(AttnParams)] + [P] * 30),
     "scope_attn_bwd_phase": (c_int, [C.POINTER(AttnParams), c_int] + [P] * 30),
     "scope_probe_mfma_flops": (c_int64, [c_int, c_int]),

@@ -193,6 +193,122 @@ __global__ __launch_bounds__(kDecD) void qkv_glue_kernel(int H, int64_t rows, fl
   vc[h * v_sh + w * v_st + d] = f32_to_bf16(vv);
 }
 
+
+// ---------------------------------------------------------------------------
+// Row-vector products of the decoder's token step, fused with the ops around
+// them (one token: every weight row is read once, the step is bound by the
+// weights' bytes and by launches, so each kernel replaces a chain of torch
+// ops).  y = epi(W · pre(x)), x [K] bf16, W [N, K] bf16 (row stride ldw):
+//   pre: x := bf16(x + addx) when addx is given (the U-net skip, w = 1), that
+//        x written to xout by workgroup 0, then with norm bf16(x·r), r =
+//        1/sqrt(mean(x²) + eps) (F.rms_norm of a bf16 row);
+//   epi: the linear's bf16 output z = bf16(Σ W·x), then
+//        kGemvPlain z | kGemvRelu2 bf16(relu(z)²) | kGemvResid bf16(res + z) |
+//        kGemvLogit 30·σ(float(z) / 7.5) in fp32.
+// Each wavefront takes kGemvRows rows; lane l holds the input elements
+// 8·(l + 64c) .. +7 (c < K/512; at K = 256 lanes 32-63 hold none) and the
+// rows' chunks at the same columns.
+// ---------------------------------------------------------------------------
+constexpr int kGemvRows = 2;
+constexpr int kGemvWaves = 4;
+enum { kGemvPlain = 0, kGemvRelu2 = 1, kGemvResid = 2, kGemvLogit = 3 };
+
+__device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <int K, int EPI>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(int N, int64_t ldw, int norm, float eps,
+                                                               const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ addx,
+                                                               uint16_t* __restrict__ xout,
+                                                               const uint16_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ res,
+                                                               void* __restrict__ out) {
+  constexpr int NCH = K / 8, KC = (NCH + 63) / 64;  // 16-byte chunks per row and per lane
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool part = NCH % 64 != 0 && lane >= NCH % 64;  // K = 256: this lane holds no chunk
+  // chunk c of this lane in a row starting at p (zero for a lane without
+  // one, which reads chunk 0 so that every address stays inside the row)
+  auto chunk = [&](const uint16_t* p, int c) __attribute__((always_inline)) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p + 8 * (part ? 0 : lane + 64 * c));
+    return part ? make_uint4(0, 0, 0, 0) : u;
+  };
+  const int row0 = (blockIdx.x * kGemvWaves + wave) * kGemvRows;
+  // the weight chunks first, so that their loads are in flight during the prologue
+  uint4 wv[kGemvRows][KC];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r) {
+    const int row = min(row0 + r, N - 1);  // rows past N load row N-1 and write nothing
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      wv[r][c] = chunk(w + static_cast<int64_t>(row) * ldw, c);
+  }
+  float xv[KC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    unpack8(chunk(x, c), xv[c]);
+    if (addx) {
+      float av[8];
+      unpack8(chunk(addx, c), av);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[c][i] = bf16_to_f32(f32_to_bf16(__fadd_rn(xv[c][i], av[i])));
+    }
+    if (xout && blockIdx.x == 0 && wave == 0 && !part) {
+      uint4 o;
+      o.x = pack_bf16x2(xv[c][0], xv[c][1]);
+      o.y = pack_bf16x2(xv[c][2], xv[c][3]);
+      o.z = pack_bf16x2(xv[c][4], xv[c][5]);
+      o.w = pack_bf16x2(xv[c][6], xv[c][7]);
+      *reinterpret_cast<uint4*>(xout + 8 * (lane + 64 * c)) = o;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(xv[c][i], xv[c][i], ss);
+  }
+  if (norm) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+    const float r = 1.f / sqrtf(ss / K + eps);
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xv[c][i] = bf16_to_f32(f32_to_bf16(__fmul_rn(xv[c][i], r)));
+  }
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      float wf[8];
+      unpack8(wv[r][c], wf);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = fmaf(wf[i], xv[c][i], acc);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, kWave);
+    const int row = row0 + r;
+    if (lane != 0 || row >= N) continue;
+    const float z = bf16_to_f32(f32_to_bf16(acc));
+    if constexpr (EPI == kGemvPlain) {
+      static_cast<uint16_t*>(out)[row] = f32_to_bf16(z);
+    } else if constexpr (EPI == kGemvRelu2) {
+      const float hz = fmaxf(z, 0.f);
+      static_cast<uint16_t*>(out)[row] = f32_to_bf16(__fmul_rn(hz, hz));
+    } else if constexpr (EPI == kGemvResid) {
+      static_cast<uint16_t*>(out)[row] = f32_to_bf16(__fadd_rn(bf16_to_f32(res[row]), z));
+    } else {
+      const float v = __fdiv_rn(z, 7.5f);
+      static_cast<float*>(out)[row] = 30.f * (1.f / (1.f + expf(-v)));
+    }
+  }
+}
+
 }  // namespace scope
 
 using namespace scope;
@@ -255,4 +371,47 @@ extern "C" int scope_decoder_qkv_glue(int T, int H, int D, int64_t rows, float e
   hipLaunchKernelGGL(qkv_glue_kernel, dim3(T, H), dim3(kDecD), 0, as_stream(stream), H, rows, eps, va, vb, qkv, ve,
                      pos, cos_t, sin_t, rot_rows, rot_st, q_out, k_out, v_out, k_sh, k_st, v_sh, v_st, cache_at_pos);
   return check_launch("qkv_glue_kernel");
+}
+
+template <int K>
+static void gemv_launch(int epi, dim3 grid, hipStream_t st, int N, int64_t ldw, int norm, float eps,
+                        const uint16_t* x, const uint16_t* addx, uint16_t* xout, const uint16_t* w,
+                        const uint16_t* res, void* out) {
+  const dim3 blk(64 * kGemvWaves);
+  if (epi == kGemvPlain)
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvPlain>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (epi == kGemvRelu2)
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvRelu2>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (epi == kGemvResid)
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvResid>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvLogit>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+}
+
+extern "C" int scope_decoder_gemv(int N, int K, int64_t ldw, int norm, float eps, int epi, const uint16_t* x,
+                                  const uint16_t* addx, uint16_t* xout, const uint16_t* w, const uint16_t* res,
+                                  void* out, void* stream) {
+  SCOPE_REQUIRE(x && w && out, "scope_decoder_gemv: null pointer");
+  SCOPE_REQUIRE(N >= 1 && (K == 256 || K == 512 || K == 1024 || K == 2048 || K == 4096),
+                "scope_decoder_gemv: N=%d >= 1 and K in {256, 512, 1024, 2048, 4096} required (K=%d)", N, K);
+  SCOPE_REQUIRE(ldw >= K && ldw % 8 == 0, "scope_decoder_gemv: row stride %lld must be >= K and a multiple of 8",
+                (long long)ldw);
+  SCOPE_REQUIRE(epi >= SCOPE_GEMV_PLAIN && epi <= SCOPE_GEMV_LOGIT, "scope_decoder_gemv: unknown epilogue %d", epi);
+  SCOPE_REQUIRE((epi == SCOPE_GEMV_RESID) == (res != nullptr),
+                "scope_decoder_gemv: the residual is given exactly with SCOPE_GEMV_RESID");
+  SCOPE_REQUIRE(!xout || addx, "scope_decoder_gemv: xout needs addx");
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  SCOPE_REQUIRE(a16(x) && a16(w) && (!addx || a16(addx)) && (!xout || a16(xout)),
+                "scope_decoder_gemv: x, w, addx and xout must be 16-byte aligned");
+  static_assert(SCOPE_GEMV_PLAIN == kGemvPlain && SCOPE_GEMV_RELU2 == kGemvRelu2 &&
+                    SCOPE_GEMV_RESID == kGemvResid && SCOPE_GEMV_LOGIT == kGemvLogit,
+                "epilogue codes");
+  const dim3 grid(ceil_div(N, kGemvWaves * kGemvRows));
+  hipStream_t st = as_stream(stream);
+  if (K == 256) gemv_launch<256>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (K == 512) gemv_launch<512>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (K == 1024) gemv_launch<1024>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (K == 2048) gemv_launch<2048>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else gemv_launch<4096>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  return check_launch("gemv_kernel");
 }

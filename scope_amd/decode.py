@@ -237,17 +237,32 @@ class ScopeDecoder(nn.Module):
         if opens:  # positions of the new block not yet written carry the current document
             self.docs[t + 1:(qb + 1) * bs] = self.docs[t]
         ve = self._ve(tok)
-        x = x0 = _norm(F.embedding(tok, self.embed))
+        x = x0 = _norm(F.embedding(tok, self.embed))[0]
         skips = []
         n = len(self.skip_weights)
         H, D = cfg.num_heads, cfg.head_dim
+        gemv = ops.decoder_gemv
         for i, lay in enumerate(self.layers):
-            if i >= n:
-                x = _skip(x, self.skip_weights[i - n], skips.pop())
+            # the row-vector products run fused with their norms, activations
+            # and residual adds (ops.decoder_gemv); the U-net skip (weight 1)
+            # joins the next normed product
+            skip = None
             a, b = lay["lambdas"]
+            if i >= n:
+                if self.skip_weights[i - n] == 1.0 and "qkv" in lay and (a, b) == (1.0, 0.0):
+                    skip = skips.pop()
+                else:
+                    x = _skip(x, self.skip_weights[i - n], skips.pop())
             x = _mix(a, b, x, x0)
             if "qkv" in lay:
-                q, _, _ = self._qkv(lay, _norm(x), ve[i], td, i)  # k, v into cache row t
+                if skip is not None:
+                    qkv, x = gemv(x, lay["qkv"], norm=True, addx=skip)
+                else:
+                    qkv = gemv(x, lay["qkv"], norm=True)
+                va, vb = lay["vlam"]
+                q, _, _ = ops.decoder_qkv_glue(qkv[None], ve[i], td, self.rotary.cos, self.rotary.sin, heads=H, va=va,
+                                               vb=vb if ve[i] is not None else 0.0, k_out=self.k_cache[i],
+                                               v_out=self.v_cache[i])  # k, v into cache row t
                 if opens:
                     nb = qb + 1
                     qbar = torch.zeros((H, nb, D), dtype=torch.float32, device=self.device)
@@ -258,13 +273,14 @@ class ScopeDecoder(nn.Module):
                     self.list_idx[i][:, :kv_idx.shape[-1]].copy_(kv_idx[:, qb])
                 y, _ = ops.decode_attn(q[0], self.k_cache[i], self.v_cache[i], self.list_num[i], self.list_idx[i],
                                        self.docs, td, bs=bs, scale=cfg.attn_scale, workspace=self._ws)
-                x = x + F.linear(y.reshape(1, H * D), lay["proj"])
+                x = gemv(y.reshape(H * D), lay["proj"], epi="resid", res=x)
                 if closes:  # the block is complete: its key mean joins the candidates
                     self.kbar[i][:, qb] = self.k_cache[i][:, qb * bs:(qb + 1) * bs].float().mean(dim=1)
-            x = x + self._mlp(lay, x)
+            h2 = gemv(x, lay["mlp_fc"], norm=True, epi="relu2")
+            x = gemv(h2, lay["mlp_proj"], epi="resid", res=x)
             if i < n:
                 skips.append(x)
-        logits = self._logits(x)[0]
+        logits = gemv(x, self.lm_head, norm=True, epi="logit")
         td.add_(1)
         return logits
 

@@ -725,6 +725,40 @@ def decoder_qkv_glue(qkv: torch.Tensor, ve: torch.Tensor | None, pos: torch.Tens
     return q, kt, vt
 
 
+GEMV_EPI = {"plain": 0, "relu2": 1, "resid": 2, "logit": 3}
+
+
+def decoder_gemv(x: torch.Tensor, w: torch.Tensor, *, norm: bool = False, epi: str = "plain",
+                 res: torch.Tensor | None = None, addx: torch.Tensor | None = None, eps: float | None = None):
+    """One row-vector product of the decoder's token step with what surrounds
+    it: x [K] bf16 (plus addx [K], the U-net skip, when given), optionally
+    RMS-normed, times W [N, K] bf16, then the epilogue: "plain" -> bf16 [N],
+    "relu2" -> relu(z)² bf16, "resid" -> res + z bf16 (res [N]), "logit" ->
+    30·σ(z / 7.5) fp32.  With addx it returns (y, x + addx), else y."""
+    dev = _gpu("decoder_gemv", x, w, res, addx)
+    K = x.numel()
+    if x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise RuntimeError("decoder_gemv: x must be a contiguous bfloat16 row")
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or w.shape[1] != K or w.stride(1) != 1:
+        raise RuntimeError(f"decoder_gemv: w must be bfloat16 [N, {K}] with a unit column stride")
+    if epi not in GEMV_EPI:
+        raise ValueError(f"decoder_gemv: epi must be one of {sorted(GEMV_EPI)}")
+    N = w.shape[0]
+    if (epi == "resid") != (res is not None):
+        raise ValueError("decoder_gemv: res is given exactly with epi='resid'")
+    if res is not None and (res.dtype != torch.bfloat16 or res.numel() != N or not res.is_contiguous()):
+        raise RuntimeError(f"decoder_gemv: res must be a contiguous bfloat16 [{N}]")
+    if addx is not None and (addx.dtype != torch.bfloat16 or addx.numel() != K or not addx.is_contiguous()):
+        raise RuntimeError(f"decoder_gemv: addx must be a contiguous bfloat16 [{K}]")
+    out = torch.empty(N, dtype=torch.float32 if epi == "logit" else torch.bfloat16, device=dev)
+    xout = torch.empty(K, dtype=torch.bfloat16, device=dev) if addx is not None else None
+    # F.rms_norm's default eps for bf16 inputs is the epsilon of its fp32 compute type
+    e = torch.finfo(torch.float32).eps if eps is None else float(eps)
+    call("scope_decoder_gemv", N, K, w.stride(0), 1 if norm else 0, e, GEMV_EPI[epi], _p(x), _p(addx), _p(xout),
+         _p(w), _p(res), _p(out), _stream(dev))
+    return (out, xout) if addx is not None else out
+
+
 def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",

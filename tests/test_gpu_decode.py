@@ -107,6 +107,68 @@ def _small_model(window: int, max_len: int, use_graph: bool = True):
     return ScopeDecoder(cfg, max_len=max_len, device=DEV, seed=3, use_graph=use_graph)
 
 
+@pytest.mark.parametrize("N,K,norm,epi,skip", [(3072, 1024, True, "plain", True), (3072, 1024, True, "plain", False),
+                                                (4096, 1024, True, "relu2", False), (1024, 4096, False, "resid", False),
+                                                (1024, 1024, False, "resid", False), (50304, 1024, True, "logit", False),
+                                                (13, 256, True, "relu2", True), (9, 2048, False, "logit", False),
+                                                (768, 512, True, "resid", False)])
+def test_decoder_gemv_matches_torch_ops(N, K, norm, epi, skip):
+    """The fused row-vector products of the token step (decoder's sizes and
+    ragged ones) against the torch chains they replace on the same bf16
+    inputs: bf16(x + skip), F.rms_norm, F.linear, then relu(z)² / res + z /
+    30·σ(z / 7.5).  The linear's fp32 sums run in another order than the
+    library GEMM's, so z may round to a neighbouring bf16 value: the bar is
+    two bf16 steps of |z| (plus one of the epilogue's own rounding), and at
+    least 97% of the bf16 outputs equal."""
+    import torch.nn.functional as F
+
+    from scope_amd import ops
+
+    print(f"decoder gemv N={N} K={K} norm={norm} epi={epi} skip={skip}", flush=True)
+    g = torch.Generator().manual_seed(N * 7 + K)
+    x = torch.randn(K, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn((N, K), generator=g) * K ** -0.5).to(torch.bfloat16).to(DEV)
+    s_ = torch.randn(K, generator=g).to(torch.bfloat16).to(DEV) if skip else None
+    res = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV) if epi == "resid" else None
+    got = ops.decoder_gemv(x, w, norm=norm, epi=epi, res=res, addx=s_)
+    xi = x
+    if skip:
+        got, xpost = got
+        xi = x + s_
+        assert torch.equal(xpost, xi)
+    xn = F.rms_norm(xi, (K,)) if norm else xi
+    z = F.linear(xn[None], w)[0]
+    ref = {"plain": z, "relu2": F.relu(z).square(), "resid": (res + z) if res is not None else None,
+           "logit": 30 * torch.sigmoid(z.float() / 7.5)}[epi]
+    assert got.shape == ref.shape and got.dtype == ref.dtype
+    zf, gf, rf = z.float(), got.float(), ref.float()
+    step = 2.0 ** -8  # one bf16 step, relative
+    grow = {"plain": 1.0, "relu2": 2.0 * zf.abs(), "resid": 1.0, "logit": 1.0}[epi]  # d(epi)/dz bound
+    bar = 2 * step * zf.abs() * grow + step * rf.abs() + 1e-6
+    err = (gf - rf).abs()
+    assert bool((err <= bar).all()), f"max err {err.max().item():.3e} (worst ratio {(err / bar).max().item():.2f})"
+    if epi != "logit":
+        eq = (got == ref).float().mean().item()
+        print(f"  equal bf16 outputs {eq:.4f}, max err {err.max().item():.3e}", flush=True)
+        assert eq >= 0.97
+
+
+def test_decoder_gemv_rejects_bad_arguments():
+    from scope_amd import ops
+
+    x = torch.zeros(1024, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((64, 1024), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="K in"):
+        ops.decoder_gemv(torch.zeros(1000, dtype=torch.bfloat16, device=DEV), torch.zeros((64, 1000),
+                         dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError, match="res is given"):
+        ops.decoder_gemv(x, w, epi="resid")
+    with pytest.raises(RuntimeError, match="aligned"):
+        ops.decoder_gemv(torch.zeros(1028, dtype=torch.bfloat16, device=DEV)[4:], w)  # 8-byte offset
+    with pytest.raises(RuntimeError, match="bfloat16"):
+        ops.decoder_gemv(x.float(), w)
+
+
 def test_graph_steps_equal_eager_steps():
     """The steps inside a block run as one captured graph, replayed per
     token; every replay gives the logits of the eager step (same operations),
