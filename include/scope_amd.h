@@ -441,8 +441,9 @@ int scope_attn_block_mass(const scope_attn_params* p, const uint16_t* q, const u
  * position at a time).  q [H, D] (head stride q_sh); k_cache / v_cache
  * [H, T_cap, D] with (head, token) strides; kv_num [H], kv_idx [H, maxkv];
  * docs [T_cap] (entries up to t are read); out [H, D] bf16 (head stride
- * o_sh); lse [H] natural log (or NULL).  The workspace holds one partial
- * (max, sum, P·V row) per (head, list entry).
+ * o_sh); lse [H] natural log (or NULL).  The rows of q, k_cache and v_cache
+ * are 16-byte aligned (head and token strides multiples of 8).  The
+ * workspace holds one partial (max, sum, P·V row) per (head, list entry).
  * ---------------------------------------------------------------------- */
 typedef struct {
   int H, D, bs, maxkv;

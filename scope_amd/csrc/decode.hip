@@ -2,13 +2,13 @@
 // the KV cache, restricted to the current q-block's listed key blocks, with
 // the document-causal mask (keys j <= t of the same document).
 //
-// Split over the listed blocks: one wavefront per (head, list entry) scores
-// the entry's bs keys against the query (q staged in LDS, one key per lane
-// and step, fp32 dot products), keeps the entry's running max m, sum l and
-// unnormalised P·V row o[D] in a workspace; a second kernel merges the
-// entries of each head (max-rescaled sums) into the output row and its LSE.
-// Decode work is a few blocks of keys per head and layer: the kernels are
-// latency bound, so they favour many small workgroups over MFMA tiles.
+// Split over the listed blocks: one workgroup per (head, list entry) scores
+// the entry's bs keys against the query (fp32 dot products, sixteen lanes per
+// key row), keeps the entry's max m, sum l and unnormalised P·V row o[D] in a
+// workspace; a second kernel merges the entries of each head (max-rescaled
+// sums) into the output row and its LSE.  Decode work is a few blocks of
+// keys per head and layer: the kernels are bound by the latency of their
+// loads, so each workgroup issues all of its rows' loads at once.
 #include <math.h>
 
 #include "common.h"
@@ -22,83 +22,128 @@ constexpr float kDecLn2 = 0.6931471805599453f;
 }  // namespace
 
 // work: [H][maxkv][D + 2] fp32 = o[0..D), m (log2 units), l
-__global__ __launch_bounds__(64) void decode_part_kernel(scope_decode_params p, const uint16_t* __restrict__ q,
-                                                         const uint16_t* __restrict__ kc,
-                                                         const uint16_t* __restrict__ vc,
-                                                         const int32_t* __restrict__ kv_num,
-                                                         const int32_t* __restrict__ kv_idx,
-                                                         const int32_t* __restrict__ docs, float* __restrict__ work,
-                                                         const int64_t* __restrict__ t_dev) {
-  const int e = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+// One 256-thread workgroup per (list entry, head): wavefront w takes keys
+// w·BS/4 .. +BS/4 of the entry's block, sixteen lanes per key row (lane l
+// holds the 16-byte chunk l % 16, features 8·(l % 16) .. +7, of row l / 16
+// of each group of four), so that every load of the wavefront reads four
+// whole 256-byte rows.  The K and V chunks of all its rows are loaded first;
+// every row read lies in the entry's block, which the cache holds whole
+// (k0 <= t < T_cap, T_cap a multiple of BS).
+constexpr int kDecWaves = 4;
+
+template <int BS>
+__global__ __launch_bounds__(64 * kDecWaves) void decode_part_kernel(
+    scope_decode_params p, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx,
+    const int32_t* __restrict__ docs, float* __restrict__ work, const int64_t* __restrict__ t_dev) {
+  constexpr int PER = BS / kDecWaves, NIT = PER / 4;  // keys per wavefront, row groups per wavefront
+  const int e = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane >> 4, ch = lane & 15;
   float* w = work + (static_cast<int64_t>(h) * p.maxkv + e) * (kDecD + 2);
   const int n = kv_num[h];
   // the position: from the parameters, or from device memory (checked here:
   // a position outside the cache gives no mass and an all-zero output)
   const int64_t t = t_dev ? *t_dev : p.t;
-  const int64_t k0 = e < n ? static_cast<int64_t>(kv_idx[static_cast<int64_t>(h) * p.maxkv + e]) * p.bs : -1;
+  const int64_t k0 = e < n ? static_cast<int64_t>(kv_idx[static_cast<int64_t>(h) * p.maxkv + e]) * BS : -1;
   if (k0 < 0 || k0 > t || t < 0 || t >= p.T_cap) {  // unused slot, a block after the query, or no valid position
-    if (lane == 0) {
+    if (tid == 0) {
       w[kDecD] = -INFINITY;
       w[kDecD + 1] = 0.f;
     }
     return;
   }
-  __shared__ float qs[kDecD];
-  __shared__ float ps[256];  // P of the entry's keys (bs <= 256)
-  const uint16_t* qh = q + static_cast<int64_t>(h) * p.q_sh;
-  qs[2 * lane] = bf16_to_f32(qh[2 * lane]) * p.scale * kDecLog2e;
-  qs[2 * lane + 1] = bf16_to_f32(qh[2 * lane + 1]) * p.scale * kDecLog2e;
-  __syncthreads();
-  const int doc_t = docs[t];
-  // scores (log2 units), one key per lane per step
-  float m = -INFINITY;
-  for (int j0 = 0; j0 < p.bs; j0 += 64) {
-    const int64_t j = k0 + j0 + lane;
-    float s = -INFINITY;
-    if (j <= t && docs[j] == doc_t) {
-      const uint4* kr = reinterpret_cast<const uint4*>(kc + static_cast<int64_t>(h) * p.k_sh + j * p.k_st);
-      float acc = 0.f;
-#pragma unroll 4
-      for (int c = 0; c < kDecD / 8; ++c) {
-        const uint4 u = kr[c];
-        const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+  __shared__ float ps[BS];  // scores, then P, of the entry's keys
+  __shared__ float red[2][kDecWaves];
+  __shared__ float opart[kDecWaves][kDecD];
+  const int64_t jw = k0 + wave * PER;  // this wavefront's first key
+  const uint16_t* kr = kc + static_cast<int64_t>(h) * p.k_sh + 8 * ch;
+  const uint16_t* vr = vc + static_cast<int64_t>(h) * p.v_sh + 8 * ch;
+  uint4 ku[NIT], vu[NIT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc = fmaf(__uint_as_float(wv[i] << 16), qs[8 * c + 2 * i], acc);
-          acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), qs[8 * c + 2 * i + 1], acc);
-        }
-      }
-      s = acc;
+  for (int it = 0; it < NIT; ++it) {
+    const int64_t j = jw + 4 * it + sub;
+    ku[it] = *reinterpret_cast<const uint4*>(kr + j * p.k_st);
+    vu[it] = *reinterpret_cast<const uint4*>(vr + j * p.v_st);
+  }
+  float qv[8];
+  {
+    const uint4 u = *reinterpret_cast<const uint4*>(q + static_cast<int64_t>(h) * p.q_sh + 8 * ch);
+    const uint32_t wq[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qv[2 * i] = __uint_as_float(wq[i] << 16) * p.scale * kDecLog2e;
+      qv[2 * i + 1] = __uint_as_float(wq[i] & 0xffff0000u) * p.scale * kDecLog2e;
     }
-    ps[j0 + lane] = s;
-    m = fmaxf(m, s);
+  }
+  const int doc_t = docs[t];
+  // scores (log2 units) of the wavefront's keys: partial dot products over
+  // each lane's 8 features, summed over the row's sixteen lanes
+  float m = -INFINITY;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int64_t j = jw + 4 * it + sub;
+    const uint32_t wk[4] = {ku[it].x, ku[it].y, ku[it].z, ku[it].w};
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc = fmaf(__uint_as_float(wk[i] << 16), qv[2 * i], acc);
+      acc = fmaf(__uint_as_float(wk[i] & 0xffff0000u), qv[2 * i + 1], acc);
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, kWave);
+    const float sc = (j <= t && docs[min(j, t)] == doc_t) ? acc : -INFINITY;  // docs read up to t only
+    if (ch == 0) ps[j - k0] = sc;
+    m = fmaxf(m, sc);
   }
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-  float l = 0.f;
-  for (int j0 = 0; j0 < p.bs; j0 += 64) {
-    const float pv = m == -INFINITY ? 0.f : exp2f(ps[j0 + lane] - m);
-    ps[j0 + lane] = pv;
-    l += pv;
+  if (lane == 0) red[0][wave] = m;
+  __syncthreads();  // scores and the wavefronts' maxima
+  float M = red[0][0];
+#pragma unroll
+  for (int i = 1; i < kDecWaves; ++i) M = fmaxf(M, red[0][i]);
+  float pl = 0.f;
+  if (tid < BS) {
+    const float pv = M == -INFINITY ? 0.f : exp2f(ps[tid] - M);
+    ps[tid] = pv;
+    pl = pv;
   }
-  for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, kWave);
-  __syncthreads();
-  // o[d] for d = 2·lane, 2·lane + 1: Σ_j P_j v_j[d] (rows read whole by the wavefront)
-  float o0 = 0.f, o1 = 0.f;
-  const uint32_t* vr = reinterpret_cast<const uint32_t*>(vc + static_cast<int64_t>(h) * p.v_sh + k0 * p.v_st) + lane;
-  const int64_t vst = p.v_st / 2;  // in 32-bit words
-  for (int j = 0; j < p.bs; ++j) {
-    const float pj = ps[j];
-    if (pj != 0.f) {
-      const uint32_t u = vr[j * vst];
-      o0 = fmaf(pj, __uint_as_float(u << 16), o0);
-      o1 = fmaf(pj, __uint_as_float(u & 0xffff0000u), o1);
+  for (int o = 32; o > 0; o >>= 1) pl += __shfl_xor(pl, o, kWave);
+  if (lane == 0) red[1][wave] = pl;
+  __syncthreads();  // P and the wavefronts' sums
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < kDecWaves; ++i) L += red[1][i];
+  // o[8·ch .. +7] over the wavefront's keys (a masked key, P = 0, adds nothing
+  // whatever its cache row holds), summed over the four rows of each group
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const float pj = ps[wave * PER + 4 * it + sub];
+    const uint32_t wv[4] = {vu[it].x, vu[it].y, vu[it].z, vu[it].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = pj != 0.f ? fmaf(pj, __uint_as_float(wv[i] << 16), o[2 * i]) : o[2 * i];
+      o[2 * i + 1] = pj != 0.f ? fmaf(pj, __uint_as_float(wv[i] & 0xffff0000u), o[2 * i + 1]) : o[2 * i + 1];
     }
   }
-  w[2 * lane] = o0;
-  w[2 * lane + 1] = o1;
-  if (lane == 0) {
-    w[kDecD] = m;
-    w[kDecD + 1] = l;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    o[i] += __shfl_xor(o[i], 16, kWave);
+    o[i] += __shfl_xor(o[i], 32, kWave);
+  }
+  if (sub == 0)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) opart[wave][8 * ch + i] = o[i];
+  __syncthreads();  // every wavefront's P·V share
+  if (tid < kDecD) {
+    float acc = opart[0][tid];
+#pragma unroll
+    for (int i = 1; i < kDecWaves; ++i) acc += opart[i][tid];
+    w[tid] = acc;
+  }
+  if (tid == 0) {
+    w[kDecD] = M;
+    w[kDecD + 1] = L;
   }
 }
 
@@ -330,12 +375,21 @@ static int decode_launch(const scope_decode_params* p, const int64_t* t_dev, con
                 (long long)p->t, (long long)p->T_cap);
   SCOPE_REQUIRE(p->T_cap % p->bs == 0, "%s: cache length %lld not a multiple of bs=%d", fn, (long long)p->T_cap,
                 p->bs);
-  SCOPE_REQUIRE(p->k_st % 8 == 0 && p->k_sh % 8 == 0 && p->v_st % 2 == 0 && p->v_sh % 2 == 0 &&
-                    (reinterpret_cast<uintptr_t>(k_cache) & 15) == 0 && (reinterpret_cast<uintptr_t>(v_cache) & 3) == 0,
-                "%s: k rows must be 16-byte aligned and v rows 4-byte aligned", fn);
+  const auto a16 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
+  SCOPE_REQUIRE(p->k_st % 8 == 0 && p->k_sh % 8 == 0 && p->v_st % 8 == 0 && p->v_sh % 8 == 0 && p->q_sh % 8 == 0 &&
+                    a16(k_cache) && a16(v_cache) && a16(q),
+                "%s: the rows of q, k and v must be 16-byte aligned", fn);
   hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(decode_part_kernel, dim3(p->maxkv, p->H), dim3(64), 0, s, *p, q, k_cache, v_cache, kv_num,
-                     kv_idx, docs, static_cast<float*>(workspace), t_dev);
+  const dim3 grid(p->maxkv, p->H), blk(64 * kDecWaves);
+  float* ws = static_cast<float*>(workspace);
+  if (p->bs == 64)
+    hipLaunchKernelGGL(decode_part_kernel<64>, grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx, docs, ws, t_dev);
+  else if (p->bs == 128)
+    hipLaunchKernelGGL(decode_part_kernel<128>, grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx, docs, ws,
+                       t_dev);
+  else
+    hipLaunchKernelGGL(decode_part_kernel<256>, grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx, docs, ws,
+                       t_dev);
   int rc = check_launch("decode_part_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(p->H), dim3(kDecD), 0, s, *p, static_cast<const float*>(workspace),
