@@ -147,24 +147,50 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_part_kernel(
   }
 }
 
+// Feature d of one head's merged output from its maxkv partials w
+// ([maxkv][D + 2]): (o_d, M, L) with o_d = Σ_e 2^(m_e - M) o_e[d] / L.  The
+// entries go in groups of 16 whose loads are all issued before any is used
+// (one memory latency per group, not one per entry); a later group rescales
+// the running sums to its larger maximum.
+__device__ __forceinline__ float3 merge_entries(const float* __restrict__ w, int maxkv, int d) {
+  constexpr int U = 16;
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int e0 = 0; e0 < maxkv; e0 += U) {
+    float me[U], le[U], oe[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int e = min(e0 + i, maxkv - 1);  // in bounds; entries past maxkv are dropped below
+      me[i] = e0 + i < maxkv ? w[e * (kDecD + 2) + kDecD] : -INFINITY;
+      le[i] = w[e * (kDecD + 2) + kDecD + 1];
+      oe[i] = w[e * (kDecD + 2) + d];
+    }
+    float Mg = M;
+#pragma unroll
+    for (int i = 0; i < U; ++i) Mg = fmaxf(Mg, me[i]);
+    if (Mg == -INFINITY) continue;
+    if (M != -INFINITY && Mg != M) {
+      const float r = exp2f(M - Mg);
+      L *= r;
+      O *= r;
+    }
+    M = Mg;
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      if (me[i] == -INFINITY) continue;  // an unused slot (its o is not written)
+      const float sc = exp2f(me[i] - M);
+      L += sc * le[i];
+      O += sc * oe[i];
+    }
+  }
+  return make_float3(L > 0.f ? O / L : 0.f, M, L);
+}
+
 __global__ __launch_bounds__(kDecD) void decode_merge_kernel(scope_decode_params p, const float* __restrict__ work,
                                                              uint16_t* __restrict__ out, float* __restrict__ lse) {
   const int h = blockIdx.x, d = threadIdx.x;
-  const float* w = work + static_cast<int64_t>(h) * p.maxkv * (kDecD + 2);
-  float M = -INFINITY;
-  for (int e = 0; e < p.maxkv; ++e) M = fmaxf(M, w[e * (kDecD + 2) + kDecD]);
-  float L = 0.f, O = 0.f;
-  if (M != -INFINITY) {
-    for (int e = 0; e < p.maxkv; ++e) {
-      const float me = w[e * (kDecD + 2) + kDecD];
-      if (me == -INFINITY) continue;
-      const float sc = exp2f(me - M);
-      L += sc * w[e * (kDecD + 2) + kDecD + 1];
-      O += sc * w[e * (kDecD + 2) + d];
-    }
-  }
-  out[static_cast<int64_t>(h) * p.o_sh + d] = f32_to_bf16(L > 0.f ? O / L : 0.f);
-  if (d == 0 && lse) lse[h] = L > 0.f ? (M + log2f(L)) * kDecLn2 : -INFINITY;
+  const float3 r = merge_entries(work + static_cast<int64_t>(h) * p.maxkv * (kDecD + 2), p.maxkv, d);
+  out[static_cast<int64_t>(h) * p.o_sh + d] = f32_to_bf16(r.x);
+  if (d == 0 && lse) lse[h] = r.z > 0.f ? (r.y + log2f(r.z)) * kDecLn2 : -INFINITY;
 }
 
 // The attention layer's glue of the decoder for T tokens
