@@ -503,6 +503,21 @@ int scope_decoder_gemv(int N, int K, int64_t ldw, int norm, float eps, int epi, 
                        const uint16_t* addx, uint16_t* xout, const uint16_t* w, const uint16_t* res,
                        void* out, void* stream);
 
+/* The start of a decoder token step (replaces, for one token at the
+ * position *t_dev held on the device, the embedding and norm of
+ * scoped_medium.py:596-600 with the value embeddings :586-590, and the
+ * decoder's token and document bookkeeping): tokens[t] = *tok; docs[t] =
+ * docs[t-1] (0 at t = 0) + (*tok == eot); x0 [dm] = F.rms_norm(embed[*tok])
+ * (fp32 with eps, rounded to bf16); ve_out [3, dm] row i = table i's row
+ * *tok for each of ve0..ve2 given (NULL tables are skipped).  A token
+ * outside [0, vocab) or a position outside [0, T_cap) writes nothing.  dm a
+ * multiple of 8; tables and outputs 16-byte aligned.  No counterpart in the
+ * reference, which has no decode loop. */
+int scope_decoder_step_prologue(const int64_t* tok, const int64_t* t_dev, int64_t T_cap, int64_t vocab, int dm,
+                                float eps, int64_t eot, int64_t* tokens, int32_t* docs, const uint16_t* embed,
+                                const uint16_t* ve0, const uint16_t* ve1, const uint16_t* ve2, uint16_t* x0,
+                                uint16_t* ve_out, void* stream);
+
 int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
 int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
                    const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,

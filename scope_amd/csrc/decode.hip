@@ -380,6 +380,68 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(int N, int64_t ld
   }
 }
 
+
+// The start of a decoder token step at the position *t_dev = t (one
+// 256-thread workgroup): tokens[t] = tok, docs[t] = docs[t-1] (0 at t = 0)
+// + (tok == eot); x0 = F.rms_norm(embed[tok]) (fp32 with eps, rounded to
+// bf16); ve_out[i] = value_embed_i[tok] for the nve tables given.  A token
+// outside [0, vocab) or a position outside [0, T_cap) writes nothing (the
+// host checks the token of an eager step; a captured step relies on it).
+constexpr int kPrologueThreads = 256;
+
+__global__ __launch_bounds__(kPrologueThreads) void step_prologue_kernel(
+    const int64_t* __restrict__ tok_p, const int64_t* __restrict__ t_dev, int64_t T_cap, int64_t vocab, int dm,
+    float eps, int64_t eot, int64_t* __restrict__ tokens, int32_t* __restrict__ docs,
+    const uint16_t* __restrict__ embed, const uint16_t* __restrict__ ve0, const uint16_t* __restrict__ ve1,
+    const uint16_t* __restrict__ ve2, uint16_t* __restrict__ x0, uint16_t* __restrict__ ve_out) {
+  const int tid = threadIdx.x;
+  const int64_t tok = *tok_p, t = *t_dev;
+  if (tok < 0 || tok >= vocab || t < 0 || t >= T_cap) return;  // uniform over the workgroup
+  if (tid == 0) {
+    tokens[t] = tok;
+    docs[t] = (t > 0 ? docs[t - 1] : 0) + (tok == eot ? 1 : 0);
+  }
+  // dm / 8 chunks of 8 features; thread i takes chunks i, i + 256, ...
+  __shared__ float part[kPrologueThreads / kWave];
+  const uint16_t* er = embed + tok * dm;
+  float ss = 0.f;
+  for (int c = tid; c < dm / 8; c += kPrologueThreads) {
+    const uint4 u = *reinterpret_cast<const uint4*>(er + 8 * c);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = __uint_as_float(w[i] << 16), b = __uint_as_float(w[i] & 0xffff0000u);
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPrologueThreads / kWave; ++i) tot += part[i];
+  const float r = 1.f / sqrtf(tot / dm + eps);
+  for (int c = tid; c < dm / 8; c += kPrologueThreads) {
+    const uint4 u = *reinterpret_cast<const uint4*>(er + 8 * c);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    uint4 o;
+    uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ow[i] = pack_bf16x2(__fmul_rn(__uint_as_float(w[i] << 16), r), __fmul_rn(__uint_as_float(w[i] & 0xffff0000u), r));
+    *reinterpret_cast<uint4*>(x0 + 8 * c) = o;
+  }
+  const uint16_t* ves[3] = {ve0, ve1, ve2};
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    if (!ves[i]) continue;
+    for (int c = tid; c < dm / 8; c += kPrologueThreads)
+      *reinterpret_cast<uint4*>(ve_out + static_cast<int64_t>(i) * dm + 8 * c) =
+          *reinterpret_cast<const uint4*>(ves[i] + tok * dm + 8 * c);
+  }
+}
+
 }  // namespace scope
 
 using namespace scope;
@@ -494,4 +556,22 @@ extern "C" int scope_decoder_gemv(int N, int K, int64_t ldw, int norm, float eps
   else if (K == 2048) gemv_launch<2048>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
   else gemv_launch<4096>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
   return check_launch("gemv_kernel");
+}
+
+extern "C" int scope_decoder_step_prologue(const int64_t* tok, const int64_t* t_dev, int64_t T_cap, int64_t vocab,
+                                           int dm, float eps, int64_t eot, int64_t* tokens, int32_t* docs,
+                                           const uint16_t* embed, const uint16_t* ve0, const uint16_t* ve1,
+                                           const uint16_t* ve2, uint16_t* x0, uint16_t* ve_out, void* stream) {
+  SCOPE_REQUIRE(tok && t_dev && tokens && docs && embed && x0, "scope_decoder_step_prologue: null pointer");
+  SCOPE_REQUIRE(!(ve0 || ve1 || ve2) || ve_out, "scope_decoder_step_prologue: value embeddings need ve_out");
+  SCOPE_REQUIRE(T_cap >= 1 && vocab >= 1 && dm >= 8 && dm % 8 == 0 && dm <= 65536,
+                "scope_decoder_step_prologue: T_cap=%lld, vocab=%lld >= 1 and dm=%d a multiple of 8 required",
+                (long long)T_cap, (long long)vocab, dm);
+  const auto a16 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
+  SCOPE_REQUIRE(a16(embed) && a16(x0) && (!ve0 || a16(ve0)) && (!ve1 || a16(ve1)) && (!ve2 || a16(ve2)) &&
+                    (!ve_out || a16(ve_out)),
+                "scope_decoder_step_prologue: the embedding tables and outputs must be 16-byte aligned");
+  hipLaunchKernelGGL(step_prologue_kernel, dim3(1), dim3(kPrologueThreads), 0, as_stream(stream), tok, t_dev, T_cap,
+                     vocab, dm, eps, eot, tokens, docs, embed, ve0, ve1, ve2, x0, ve_out);
+  return check_launch("step_prologue_kernel");
 }

@@ -230,14 +230,15 @@ class ScopeDecoder(nn.Module):
         cfg = self.cfg
         bs = cfg.block_size
         td = self._t_dev
-        self.tokens.index_copy_(0, td, tok)
-        prev = torch.where(td > 0, self.docs.index_select(0, (td - 1).clamp(min=0)), 0)
-        self.docs.index_copy_(0, td, (prev + (tok == EOT)).to(torch.int32))
+        # token and document bookkeeping, the embedding, its norm and the
+        # value embeddings in one kernel
+        x0, ve3 = ops.decoder_step_prologue(tok, td, self.tokens, self.docs, self.embed, self.value_embeds, eot=EOT)
         qb = t // bs
         if opens:  # positions of the new block not yet written carry the current document
             self.docs[t + 1:(qb + 1) * bs] = self.docs[t]
-        ve = self._ve(tok)
-        x = x0 = _norm(F.embedding(tok, self.embed))[0]
+        v0, v1, v2 = ve3[0:1], ve3[1:2], ve3[2:3]
+        ve = [v0, v1, v2] + [None] * (cfg.num_layers - 6) + [v0, v1, v2]
+        x = x0
         skips = []
         n = len(self.skip_weights)
         H, D = cfg.num_heads, cfg.head_dim

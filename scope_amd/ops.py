@@ -759,6 +759,33 @@ def decoder_gemv(x: torch.Tensor, w: torch.Tensor, *, norm: bool = False, epi: s
     return (out, xout) if addx is not None else out
 
 
+def decoder_step_prologue(tok: torch.Tensor, t_dev: torch.Tensor, tokens: torch.Tensor, docs: torch.Tensor,
+                          embed: torch.Tensor, value_embeds, *, eot: int, eps: float | None = None):
+    """The start of a decoder token step at the position t_dev (int64 [1] on
+    the device): tokens[t] = tok, docs[t] = docs[t-1] + (tok == eot), and
+    returns (x0 [dm] = F.rms_norm(embed[tok]) bf16, ve [len(value_embeds), dm]
+    bf16 rows of the value-embedding tables, or None without tables)."""
+    dev = _gpu("decoder_step_prologue", tok, t_dev, tokens, docs, embed, *value_embeds)
+    if tok.dtype != torch.int64 or tok.numel() != 1 or t_dev.dtype != torch.int64 or t_dev.numel() != 1:
+        raise RuntimeError("decoder_step_prologue: tok and t_dev must be one int64 element each")
+    if tokens.dtype != torch.int64 or docs.dtype != torch.int32 or tokens.numel() != docs.numel() \
+            or not tokens.is_contiguous() or not docs.is_contiguous():
+        raise RuntimeError("decoder_step_prologue: tokens int64 [T_cap] and docs int32 [T_cap], contiguous")
+    if len(value_embeds) > 3:
+        raise ValueError("decoder_step_prologue: at most 3 value-embedding tables")
+    V, dm = embed.shape
+    for tb in (embed, *value_embeds):
+        if tb.dtype != torch.bfloat16 or not tb.is_contiguous() or tb.shape != (V, dm):
+            raise RuntimeError(f"decoder_step_prologue: embedding tables must be contiguous bfloat16 [{V}, {dm}]")
+    x0 = torch.empty(dm, dtype=torch.bfloat16, device=dev)
+    ve = torch.empty((len(value_embeds), dm), dtype=torch.bfloat16, device=dev) if value_embeds else None
+    tabs = list(value_embeds) + [None] * (3 - len(value_embeds))
+    e = torch.finfo(torch.float32).eps if eps is None else float(eps)
+    call("scope_decoder_step_prologue", _p(tok), _p(t_dev), tokens.numel(), V, dm, e, int(eot), _p(tokens),
+         _p(docs), _p(embed), *(_p(x) for x in tabs), _p(x0), _p(ve), _stream(dev))
+    return x0, ve
+
+
 def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_tok_end, *, bs: int, scale: float,
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",

@@ -169,6 +169,48 @@ def test_decoder_gemv_rejects_bad_arguments():
         ops.decoder_gemv(x.float(), w)
 
 
+def test_decoder_step_prologue_matches_torch_ops():
+    """The fused start of a token step against the torch ops it replaces:
+    tokens[t] and docs[t] (t = 0, an end-of-text token opening a document,
+    a plain token) exactly, the value-embedding rows exactly, x0 =
+    F.rms_norm(embedding) within one bf16 step (the sum of squares runs in
+    another order) and equal on at least 99% of its features; a token
+    outside the vocabulary writes nothing."""
+    import torch.nn.functional as F
+
+    from scope_amd import ops
+
+    V, dm, T_cap, eot = 50257, 1024, 256, 50256
+    g = torch.Generator().manual_seed(17)
+    embed = torch.randn((V, dm), generator=g).to(torch.bfloat16).to(DEV)
+    ves = [torch.randn((V, dm), generator=g).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    tokens = torch.zeros(T_cap, dtype=torch.int64, device=DEV)
+    docs = torch.zeros(T_cap, dtype=torch.int32, device=DEV)
+    docs[:10] = 3
+    for t, tk in ((0, 123), (10, eot), (11, 4567), (12, V + 5)):
+        print(f"step prologue t={t} tok={tk}", flush=True)
+        tok = torch.tensor([tk], dtype=torch.int64, device=DEV)
+        td = torch.tensor([t], dtype=torch.int64, device=DEV)
+        tok_before, doc_before = tokens.clone(), docs.clone()
+        if tk >= V:
+            ops.decoder_step_prologue(tok, td, tokens, docs, embed, ves, eot=eot)
+            torch.cuda.synchronize()
+            assert torch.equal(tokens, tok_before) and torch.equal(docs, doc_before)
+            continue
+        x0, ve = ops.decoder_step_prologue(tok, td, tokens, docs, embed, ves, eot=eot)
+        exp_doc = (int(doc_before[t - 1]) if t > 0 else 0) + (1 if tk == eot else 0)
+        assert int(tokens[t]) == tk and int(docs[t]) == exp_doc
+        others = torch.ones(T_cap, dtype=torch.bool, device=DEV)
+        others[t] = False
+        assert torch.equal(tokens[others], tok_before[others]) and torch.equal(docs[others], doc_before[others])
+        for i in range(3):
+            assert torch.equal(ve[i], ves[i][tk])
+        ref = F.rms_norm(embed[tk][None], (dm,))[0]
+        err = (x0.float() - ref.float()).abs()
+        assert bool((err <= 2.0 ** -8 * ref.float().abs() + 1e-6).all()), f"max err {err.max().item():.3e}"
+        assert (x0 == ref).float().mean().item() >= 0.99
+
+
 def test_graph_steps_equal_eager_steps():
     """The steps inside a block run as one captured graph, replayed per
     token; every replay gives the logits of the eager step (same operations),
