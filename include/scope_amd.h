@@ -467,6 +467,20 @@ int scope_decode_attn_at(const scope_decode_params* p, const int64_t* t_dev, con
                          const int32_t* kv_idx, const int32_t* docs, void* workspace, uint16_t* out,
                          float* lse, void* stream);
 
+/* scope_decode_attn_at with the attention layer's glue fused in, for one
+ * token (the decode step inside a block, where the lists are fixed): from
+ * qkv [3H, D] bf16 (the qkv projection) it forms q, k and v exactly as
+ * scope_decoder_qkv_glue does (eps, va, vb, ve [H·D] or NULL, rotary tables
+ * cos_t / sin_t [rot_rows, D/2] with row stride rot_st, at the position
+ * *t_dev), writes k and v to row *t_dev of k_cache / v_cache, and attends
+ * with the new row; q_out [H, D] (or NULL) receives q.  One launch instead
+ * of the glue's and the attention's.  No counterpart in the reference. */
+int scope_decode_attn_glue_at(const scope_decode_params* p, const int64_t* t_dev, const uint16_t* qkv,
+                              const uint16_t* ve, float va, float vb, float eps, const float* cos_t,
+                              const float* sin_t, int64_t rot_rows, int64_t rot_st, uint16_t* k_cache,
+                              uint16_t* v_cache, const int32_t* kv_num, const int32_t* kv_idx, const int32_t* docs,
+                              void* workspace, uint16_t* out, float* lse, uint16_t* q_out, void* stream);
+
 /* The decoder attention layer's glue for T tokens (replaces, in the token
  * loop and the prefill, scoped_medium.py:339-345 with norm :266-267 and
  * Rotary :291-310): from qkv [T, 3H, D] bf16 (the qkv projection), q and k

@@ -31,11 +31,27 @@ constexpr float kDecLn2 = 0.6931471805599453f;
 // (k0 <= t < T_cap, T_cap a multiple of BS).
 constexpr int kDecWaves = 4;
 
-template <int BS>
+// The attention layer's glue fused into the decode attention (one token):
+// q, k, v of the token from its qkv row [3H, D] (the qkv projection), q and
+// k RMS-normed and rotated at position t, v mixed with ve, exactly as
+// qkv_glue_kernel forms them; k and v go to cache row t.
+struct DecGlue {
+  const uint16_t* qkv;
+  const uint16_t* ve;  // [H·D] or null
+  float va, vb, eps;
+  const float* cos_t;
+  const float* sin_t;
+  int64_t rot_rows, rot_st;
+  uint16_t* q_out;  // [H, D] or null
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+};
+
+template <int BS, bool GLUE>
 __global__ __launch_bounds__(64 * kDecWaves) void decode_part_kernel(
     scope_decode_params p, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx,
-    const int32_t* __restrict__ docs, float* __restrict__ work, const int64_t* __restrict__ t_dev) {
+    const int32_t* __restrict__ docs, float* __restrict__ work, const int64_t* __restrict__ t_dev, DecGlue gl) {
   constexpr int PER = BS / kDecWaves, NIT = PER / 4;  // keys per wavefront, row groups per wavefront
   const int e = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane >> 4, ch = lane & 15;
@@ -45,7 +61,53 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_part_kernel(
   // a position outside the cache gives no mass and an all-zero output)
   const int64_t t = t_dev ? *t_dev : p.t;
   const int64_t k0 = e < n ? static_cast<int64_t>(kv_idx[static_cast<int64_t>(h) * p.maxkv + e]) * BS : -1;
-  if (k0 < 0 || k0 > t || t < 0 || t >= p.T_cap) {  // unused slot, a block after the query, or no valid position
+  // GLUE: the token's rotated q (as fp32 of its bf16 values) and its k, v rows
+  __shared__ float gq[GLUE ? kDecD : 1], gx[GLUE ? 2 * kDecD : 1], gpart[kDecWaves];
+  __shared__ __attribute__((aligned(16))) uint16_t gk[GLUE ? kDecD : 8], gv[GLUE ? kDecD : 8];
+  if constexpr (GLUE) {
+    const bool pos_ok = t >= 0 && t < p.T_cap && t < gl.rot_rows;  // uniform over the workgroup
+    if (pos_ok) {
+      const int d = tid & (kDecD - 1), isk = tid >= kDecD;  // threads 0-127: q, 128-255: k
+      const float x = bf16_to_f32(gl.qkv[(isk ? p.H + h : h) * kDecD + d]);
+      float sq = x * x;
+      for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+      if (lane == 0) gpart[wave] = sq;
+      __syncthreads();
+      const float r = 1.f / sqrtf((gpart[2 * isk] + gpart[2 * isk + 1]) / kDecD + gl.eps);
+      const float xn = bf16_to_f32(f32_to_bf16(__fmul_rn(x, r)));
+      gx[isk * kDecD + d] = xn;
+      __syncthreads();
+      constexpr int HD = kDecD / 2;
+      const float c = gl.cos_t[t * gl.rot_st + (d % HD)], sn = gl.sin_t[t * gl.rot_st + (d % HD)];
+      const float y = d < HD ? __fadd_rn(__fmul_rn(xn, c), __fmul_rn(gx[isk * kDecD + d + HD], sn))
+                             : __fadd_rn(__fmul_rn(gx[isk * kDecD + d - HD], -sn), __fmul_rn(xn, c));
+      const uint16_t yb = f32_to_bf16(y);
+      if (isk) {
+        gk[d] = yb;
+      } else {
+        gq[d] = bf16_to_f32(yb);
+        if (gl.q_out && e == 0) gl.q_out[static_cast<int64_t>(h) * kDecD + d] = yb;
+        const float v = bf16_to_f32(gl.qkv[(2 * p.H + h) * kDecD + d]);
+        float vv = bf16_to_f32(f32_to_bf16(__fmul_rn(gl.va, v)));
+        if (gl.ve) {
+          const float ev = bf16_to_f32(gl.ve[static_cast<int64_t>(h) * kDecD + d]);
+          vv = bf16_to_f32(f32_to_bf16(__fadd_rn(vv, bf16_to_f32(f32_to_bf16(__fmul_rn(gl.vb, ev))))));
+        }
+        gv[d] = f32_to_bf16(vv);
+      }
+      __syncthreads();
+      // cache row t, written once per head (the workgroup whose block holds
+      // t takes the new row from LDS, not from the cache)
+      if (e == 0 && tid < kDecD) {
+        gl.k_cache[h * p.k_sh + t * p.k_st + tid] = gk[tid];
+        gl.v_cache[h * p.v_sh + t * p.v_st + tid] = gv[tid];
+      }
+    } else if (gl.q_out && e == 0 && tid < kDecD) {
+      gl.q_out[static_cast<int64_t>(h) * kDecD + tid] = 0;
+    }
+  }
+  if (k0 < 0 || k0 > t || t < 0 || t >= p.T_cap || (GLUE && t >= gl.rot_rows)) {
+    // an unused slot, a block after the query, or no valid position
     if (tid == 0) {
       w[kDecD] = -INFINITY;
       w[kDecD + 1] = 0.f;
@@ -64,9 +126,16 @@ __global__ __launch_bounds__(64 * kDecWaves) void decode_part_kernel(
     const int64_t j = jw + 4 * it + sub;
     ku[it] = *reinterpret_cast<const uint4*>(kr + j * p.k_st);
     vu[it] = *reinterpret_cast<const uint4*>(vr + j * p.v_st);
+    if (GLUE && j == t) {  // the token's own row: the new k, v
+      ku[it] = *reinterpret_cast<const uint4*>(&gk[8 * ch]);
+      vu[it] = *reinterpret_cast<const uint4*>(&gv[8 * ch]);
+    }
   }
   float qv[8];
-  {
+  if constexpr (GLUE) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[i] = gq[8 * ch + i] * p.scale * kDecLog2e;
+  } else {
     const uint4 u = *reinterpret_cast<const uint4*>(q + static_cast<int64_t>(h) * p.q_sh + 8 * ch);
     const uint32_t wq[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -280,7 +349,7 @@ __global__ __launch_bounds__(kDecD) void qkv_glue_kernel(int H, int64_t rows, fl
 // 8·(l + 64c) .. +7 (c < K/512; at K = 256 lanes 32-63 hold none) and the
 // rows' chunks at the same columns.
 // ---------------------------------------------------------------------------
-constexpr int kGemvRows = 2;
+constexpr int kGemvRows = 1;
 constexpr int kGemvWaves = 4;
 enum { kGemvPlain = 0, kGemvRelu2 = 1, kGemvResid = 2, kGemvLogit = 3 };
 
@@ -454,8 +523,8 @@ extern "C" int64_t scope_decode_workspace_bytes(const scope_decode_params* p) {
 static int decode_launch(const scope_decode_params* p, const int64_t* t_dev, const uint16_t* q,
                          const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* kv_num,
                          const int32_t* kv_idx, const int32_t* docs, void* workspace, uint16_t* out, float* lse,
-                         void* stream, const char* fn) {
-  SCOPE_REQUIRE(p && q && k_cache && v_cache && kv_num && kv_idx && docs && workspace && out, "%s: null pointer", fn);
+                         void* stream, const char* fn, const DecGlue* glue = nullptr) {
+  SCOPE_REQUIRE(p && (q || glue) && k_cache && v_cache && kv_num && kv_idx && docs && workspace && out, "%s: null pointer", fn);
   SCOPE_REQUIRE(p->D == kDecD, "%s: head dim D=%d (supported: 128)", fn, p->D);
   SCOPE_REQUIRE(p->bs == 64 || p->bs == 128 || p->bs == 256, "%s: block size %d (64, 128, 256)", fn, p->bs);
   SCOPE_REQUIRE(p->H >= 1 && p->maxkv >= 1 && p->maxkv <= 65535, "%s: bad H=%d / maxkv=%d", fn, p->H, p->maxkv);
@@ -465,19 +534,33 @@ static int decode_launch(const scope_decode_params* p, const int64_t* t_dev, con
                 p->bs);
   const auto a16 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0; };
   SCOPE_REQUIRE(p->k_st % 8 == 0 && p->k_sh % 8 == 0 && p->v_st % 8 == 0 && p->v_sh % 8 == 0 && p->q_sh % 8 == 0 &&
-                    a16(k_cache) && a16(v_cache) && a16(q),
+                    a16(k_cache) && a16(v_cache) && (glue || a16(q)),
                 "%s: the rows of q, k and v must be 16-byte aligned", fn);
   hipStream_t s = as_stream(stream);
   const dim3 grid(p->maxkv, p->H), blk(64 * kDecWaves);
   float* ws = static_cast<float*>(workspace);
-  if (p->bs == 64)
-    hipLaunchKernelGGL(decode_part_kernel<64>, grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx, docs, ws, t_dev);
-  else if (p->bs == 128)
-    hipLaunchKernelGGL(decode_part_kernel<128>, grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx, docs, ws,
-                       t_dev);
-  else
-    hipLaunchKernelGGL(decode_part_kernel<256>, grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx, docs, ws,
-                       t_dev);
+  if (glue) {
+    if (p->bs == 64)
+      hipLaunchKernelGGL((decode_part_kernel<64, true>), grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx, docs,
+                         ws, t_dev, *glue);
+    else if (p->bs == 128)
+      hipLaunchKernelGGL((decode_part_kernel<128, true>), grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx,
+                         docs, ws, t_dev, *glue);
+    else
+      hipLaunchKernelGGL((decode_part_kernel<256, true>), grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx,
+                         docs, ws, t_dev, *glue);
+  } else {
+    const DecGlue none{};
+    if (p->bs == 64)
+      hipLaunchKernelGGL((decode_part_kernel<64, false>), grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx,
+                         docs, ws, t_dev, none);
+    else if (p->bs == 128)
+      hipLaunchKernelGGL((decode_part_kernel<128, false>), grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx,
+                         docs, ws, t_dev, none);
+    else
+      hipLaunchKernelGGL((decode_part_kernel<256, false>), grid, blk, 0, s, *p, q, k_cache, v_cache, kv_num, kv_idx,
+                         docs, ws, t_dev, none);
+  }
   int rc = check_launch("decode_part_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(p->H), dim3(kDecD), 0, s, *p, static_cast<const float*>(workspace),
@@ -574,4 +657,18 @@ extern "C" int scope_decoder_step_prologue(const int64_t* tok, const int64_t* t_
   hipLaunchKernelGGL(step_prologue_kernel, dim3(1), dim3(kPrologueThreads), 0, as_stream(stream), tok, t_dev, T_cap,
                      vocab, dm, eps, eot, tokens, docs, embed, ve0, ve1, ve2, x0, ve_out);
   return check_launch("step_prologue_kernel");
+}
+
+extern "C" int scope_decode_attn_glue_at(const scope_decode_params* p, const int64_t* t_dev, const uint16_t* qkv,
+                                         const uint16_t* ve, float va, float vb, float eps, const float* cos_t,
+                                         const float* sin_t, int64_t rot_rows, int64_t rot_st, uint16_t* k_cache,
+                                         uint16_t* v_cache, const int32_t* kv_num, const int32_t* kv_idx,
+                                         const int32_t* docs, void* workspace, uint16_t* out, float* lse,
+                                         uint16_t* q_out, void* stream) {
+  SCOPE_REQUIRE(t_dev && qkv && cos_t && sin_t, "scope_decode_attn_glue_at: null pointer");
+  SCOPE_REQUIRE(p && p->H >= 1 && p->H <= 65535 && rot_rows >= 1 && rot_st >= kDecD / 2,
+                "scope_decode_attn_glue_at: bad H or rotary tables");
+  DecGlue g{qkv, ve, va, vb, eps, cos_t, sin_t, rot_rows, rot_st, q_out, k_cache, v_cache};
+  return decode_launch(p, t_dev, nullptr, k_cache, v_cache, kv_num, kv_idx, docs, workspace, out, lse, stream,
+                       "scope_decode_attn_glue_at", &g);
 }

@@ -261,10 +261,12 @@ class ScopeDecoder(nn.Module):
                 else:
                     qkv = gemv(x, lay["qkv"], norm=True)
                 va, vb = lay["vlam"]
-                q, _, _ = ops.decoder_qkv_glue(qkv[None], ve[i], td, self.rotary.cos, self.rotary.sin, heads=H, va=va,
-                                               vb=vb if ve[i] is not None else 0.0, k_out=self.k_cache[i],
-                                               v_out=self.v_cache[i])  # k, v into cache row t
+                vb = vb if ve[i] is not None else 0.0
                 if opens:
+                    # the block's lists are chosen from this token's q: the glue
+                    # (k, v into cache row t), the reselection, then the attention
+                    q, _, _ = ops.decoder_qkv_glue(qkv[None], ve[i], td, self.rotary.cos, self.rotary.sin, heads=H,
+                                                   va=va, vb=vb, k_out=self.k_cache[i], v_out=self.v_cache[i])
                     nb = qb + 1
                     qbar = torch.zeros((H, nb, D), dtype=torch.float32, device=self.device)
                     qbar[:, qb] = q[0].float()
@@ -272,8 +274,15 @@ class ScopeDecoder(nn.Module):
                     self.list_num[i].copy_(kv_num[:, qb])
                     self.list_idx[i].zero_()
                     self.list_idx[i][:, :kv_idx.shape[-1]].copy_(kv_idx[:, qb])
-                y, _ = ops.decode_attn(q[0], self.k_cache[i], self.v_cache[i], self.list_num[i], self.list_idx[i],
-                                       self.docs, td, bs=bs, scale=cfg.attn_scale, workspace=self._ws)
+                    y, _ = ops.decode_attn(q[0], self.k_cache[i], self.v_cache[i], self.list_num[i], self.list_idx[i],
+                                           self.docs, td, bs=bs, scale=cfg.attn_scale, workspace=self._ws)
+                else:
+                    # lists fixed within the block: the glue runs inside the attention
+                    # (k, v into cache row t there)
+                    y, _, _ = ops.decode_attn_glue(qkv, ve[i], td, self.rotary.cos, self.rotary.sin, self.k_cache[i],
+                                                   self.v_cache[i], self.list_num[i], self.list_idx[i], self.docs,
+                                                   heads=H, va=va, vb=vb, bs=bs, scale=cfg.attn_scale,
+                                                   workspace=self._ws)
                 x = gemv(y.reshape(H * D), lay["proj"], epi="resid", res=x)
                 if closes:  # the block is complete: its key mean joins the candidates
                     self.kbar[i][:, qb] = self.k_cache[i][:, qb * bs:(qb + 1) * bs].float().mean(dim=1)

@@ -684,6 +684,48 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
     return out, lse
 
 
+def decode_attn_glue(qkv: torch.Tensor, ve: torch.Tensor | None, t_dev: torch.Tensor, cos: torch.Tensor,
+                     sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_num: torch.Tensor,
+                     kv_idx: torch.Tensor, docs: torch.Tensor, *, heads: int, va: float, vb: float, bs: int,
+                     scale: float, workspace: torch.Tensor | None = None, eps: float | None = None,
+                     want_q: bool = False):
+    """``decoder_qkv_glue`` of one token (qkv [3·heads·D] bf16) fused into
+    ``decode_attn`` at the device position t_dev: k and v go to cache row t
+    and the attention uses them.  Returns (out [heads, D] bf16, lse [heads],
+    q [heads, D] bf16 or None)."""
+    from ._lib import DecodeParams
+
+    dev = _gpu("decode_attn_glue", qkv, ve, t_dev, cos, sin, k_cache, v_cache, kv_num, kv_idx, docs)
+    D = k_cache.shape[-1]
+    if qkv.dtype != torch.bfloat16 or not qkv.is_contiguous() or qkv.numel() != 3 * heads * D:
+        raise RuntimeError("decode_attn_glue: qkv must be a contiguous bfloat16 [3*heads*D]")
+    if ve is not None and (ve.dtype != torch.bfloat16 or not ve.is_contiguous() or ve.numel() != heads * D):
+        raise RuntimeError("decode_attn_glue: ve must be a contiguous bfloat16 [heads*D]")
+    if t_dev.dtype != torch.int64 or t_dev.numel() != 1:
+        raise RuntimeError("decode_attn_glue: t_dev must be one int64 element")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape or cos.stride(-1) != 1 \
+            or sin.stride() != cos.stride() or cos.shape[-1] != D // 2:
+        raise RuntimeError("decode_attn_glue: cos/sin must be float32 [rows, D/2] with the same strides")
+    for n_, x in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if x.dtype != torch.bfloat16 or x.dim() != 3 or x.shape[0] != heads or x.stride(-1) != 1:
+            raise RuntimeError(f"decode_attn_glue: {n_} must be bfloat16 [heads, T_cap, D] with a unit last stride")
+    kv_idx = _i32(kv_idx)
+    prm = DecodeParams(H=heads, D=D, bs=int(bs), maxkv=kv_idx.shape[-1], T_cap=k_cache.shape[1], t=0,
+                       scale=float(scale), q_sh=D, k_sh=k_cache.stride(0), k_st=k_cache.stride(1),
+                       v_sh=v_cache.stride(0), v_st=v_cache.stride(1), o_sh=D)
+    need = int(query("scope_decode_workspace_bytes", C.byref(prm)))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    out = torch.empty((heads, D), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(heads, dtype=torch.float32, device=dev)
+    q = torch.empty((heads, D), dtype=torch.bfloat16, device=dev) if want_q else None
+    e = torch.finfo(torch.float32).eps if eps is None else float(eps)
+    call("scope_decode_attn_glue_at", C.byref(prm), _p(t_dev), _p(qkv), _p(ve), float(va), float(vb), e, _p(cos),
+         _p(sin), cos.shape[0], cos.stride(0), _p(k_cache), _p(v_cache), _p(_i32(kv_num)), _p(kv_idx),
+         _p(_i32(docs.reshape(-1))), _p(workspace), _p(out), _p(lse), _p(q), _stream(dev))
+    return out, lse, q
+
+
 def decoder_qkv_glue(qkv: torch.Tensor, ve: torch.Tensor | None, pos: torch.Tensor, cos: torch.Tensor,
                      sin: torch.Tensor, *, heads: int, va: float, vb: float, k_out: torch.Tensor | None = None,
                      v_out: torch.Tensor | None = None, eps: float | None = None):

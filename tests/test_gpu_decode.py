@@ -211,6 +211,43 @@ def test_decoder_step_prologue_matches_torch_ops():
         assert (x0 == ref).float().mean().item() >= 0.99
 
 
+@pytest.mark.parametrize("bs,t,with_ve", [(128, 1000, True), (128, 1023, False), (64, 0, True), (256, 777, False)])
+def test_decode_attn_glue_equals_glue_then_attention(bs, t, with_ve):
+    """The glue fused into the decode attention against the glue kernel
+    followed by the plain attention on copies of the same caches: the same
+    output, LSE, q and cache rows, bit for bit (the same arithmetic; the
+    fused kernel takes the token's own k, v row from LDS)."""
+    from scope_amd import ops
+
+    H, T_cap, D, maxkv = 4, 2048, 128, 6
+    print(f"decode attn glue bs={bs} t={t} ve={with_ve}", flush=True)
+    g = torch.Generator().manual_seed(bs + t)
+    kc = torch.randn((H, T_cap, D), generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn((H, T_cap, D), generator=g).to(torch.bfloat16).to(DEV)
+    qkv = torch.randn(3 * H * D, generator=g).to(torch.bfloat16).to(DEV)
+    ve = torch.randn(H * D, generator=g).to(torch.bfloat16).to(DEV) if with_ve else None
+    docs = docs_with_boundaries(T_cap, 4, seed=t).to(DEV)
+    qb = t // bs
+    kv_idx = torch.zeros((H, maxkv), dtype=torch.int32)
+    kv_num = torch.zeros(H, dtype=torch.int32)
+    for h in range(H):
+        cand = sorted(set([qb, max(qb - 1, 0), 0] + torch.randint(0, qb + 1, (2,), generator=g).tolist()))
+        kv_num[h] = len(cand)
+        kv_idx[h, :len(cand)] = torch.tensor(cand)
+    kv_num, kv_idx = kv_num.to(DEV), kv_idx.to(DEV)
+    theta = torch.arange(T_cap, dtype=torch.float32)[:, None] * torch.rand(D // 2, generator=g)[None]
+    cos, sin = theta.cos().to(DEV), theta.sin().to(DEV)
+    td = torch.tensor([t], dtype=torch.int64, device=DEV)
+    k2, v2 = kc.clone(), vc.clone()
+    q_ref, _, _ = ops.decoder_qkv_glue(qkv[None], ve, td, cos, sin, heads=H, va=0.5, vb=0.5, k_out=k2, v_out=v2)
+    o_ref, l_ref = ops.decode_attn(q_ref[0], k2, v2, kv_num, kv_idx, docs, td, bs=bs, scale=0.12)
+    out, lse, q = ops.decode_attn_glue(qkv, ve, td, cos, sin, kc, vc, kv_num, kv_idx, docs, heads=H, va=0.5, vb=0.5,
+                                       bs=bs, scale=0.12, want_q=True)
+    assert torch.equal(q, q_ref[0])
+    assert torch.equal(kc, k2) and torch.equal(vc, v2)
+    assert torch.equal(out, o_ref) and torch.equal(lse, l_ref)
+
+
 def test_graph_steps_equal_eager_steps():
     """The steps inside a block run as one captured graph, replayed per
     token; every replay gives the logits of the eager step (same operations),
