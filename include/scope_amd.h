@@ -532,6 +532,12 @@ int scope_decoder_step_prologue(const int64_t* tok, const int64_t* t_dev, int64_
                                 const uint16_t* ve0, const uint16_t* ve1, const uint16_t* ve2, uint16_t* x0,
                                 uint16_t* ve_out, void* stream);
 
+/* The greedy choice of the decoder's token loop: *out = the index of the
+ * largest of x[0..n) fp32 (the first on ties, as torch.argmax; NaN values
+ * are never chosen; all NaN gives 0).  One workgroup.  No counterpart in the
+ * reference, which has no decode loop. */
+int scope_argmax_f32(const float* x, int64_t n, int64_t* out, void* stream);
+
 int64_t scope_attn_bwd_workspace_bytes(const scope_attn_params* p);
 int scope_attn_bwd(const scope_attn_params* p, const uint16_t* q, const uint16_t* k,
                    const uint16_t* v, const uint16_t* out, const uint16_t* dout, const float* lse,

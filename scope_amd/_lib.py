@@ -118,6 +118,7 @@ _PROTOS = {
     "scope_decoder_qkv_glue": (c_int, [c_int, c_int, c_int, c_int64, c_float, c_float, c_float, P, P, P, P, P,
                                        c_int64, c_int64, P, P, P, c_int64, c_int64, c_int64, c_int64, c_int, P]),
     "scope_decoder_gemv": (c_int, [c_int, c_int, c_int64, c_int, c_float, c_int, P, P, P, P, P, P, P]),
+    "scope_argmax_f32": (c_int, [P, c_int64, P, P]),
     "scope_decode_attn_glue_at": (c_int, [C.POINTER(DecodeParams), P, P, P, c_float, c_float, c_float, P, P, c_int64,
                                           c_int64, P, P, P, P, P, P, P, P, P, P]),
     "scope_decoder_step_prologue": (c_int, [P, P, c_int64, c_int64, c_int, c_float, c_int64, P, P, P, P, P, P, P, P,

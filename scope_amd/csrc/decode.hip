@@ -345,11 +345,10 @@ __global__ __launch_bounds__(kDecD) void qkv_glue_kernel(int H, int64_t rows, fl
 //   epi: the linear's bf16 output z = bf16(Σ W·x), then
 //        kGemvPlain z | kGemvRelu2 bf16(relu(z)²) | kGemvResid bf16(res + z) |
 //        kGemvLogit 30·σ(float(z) / 7.5) in fp32.
-// Each wavefront takes kGemvRows rows; lane l holds the input elements
+// Each wavefront takes R rows (1; 2 for N >= 16384, the logit head); lane l holds the input elements
 // 8·(l + 64c) .. +7 (c < K/512; at K = 256 lanes 32-63 hold none) and the
 // rows' chunks at the same columns.
 // ---------------------------------------------------------------------------
-constexpr int kGemvRows = 1;
 constexpr int kGemvWaves = 4;
 enum { kGemvPlain = 0, kGemvRelu2 = 1, kGemvResid = 2, kGemvLogit = 3 };
 
@@ -362,7 +361,7 @@ __device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
   }
 }
 
-template <int K, int EPI>
+template <int K, int EPI, int R>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(int N, int64_t ldw, int norm, float eps,
                                                                const uint16_t* __restrict__ x,
                                                                const uint16_t* __restrict__ addx,
@@ -379,11 +378,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(int N, int64_t ld
     const uint4 u = *reinterpret_cast<const uint4*>(p + 8 * (part ? 0 : lane + 64 * c));
     return part ? make_uint4(0, 0, 0, 0) : u;
   };
-  const int row0 = (blockIdx.x * kGemvWaves + wave) * kGemvRows;
+  const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
   // the weight chunks first, so that their loads are in flight during the prologue
-  uint4 wv[kGemvRows][KC];
+  uint4 wv[R][KC];
 #pragma unroll
-  for (int r = 0; r < kGemvRows; ++r) {
+  for (int r = 0; r < R; ++r) {
     const int row = min(row0 + r, N - 1);  // rows past N load row N-1 and write nothing
 #pragma unroll
     for (int c = 0; c < KC; ++c)
@@ -421,7 +420,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(int N, int64_t ld
       for (int i = 0; i < 8; ++i) xv[c][i] = bf16_to_f32(f32_to_bf16(__fmul_rn(xv[c][i], r)));
   }
 #pragma unroll
-  for (int r = 0; r < kGemvRows; ++r) {
+  for (int r = 0; r < R; ++r) {
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
@@ -508,6 +507,41 @@ __global__ __launch_bounds__(kPrologueThreads) void step_prologue_kernel(
     for (int c = tid; c < dm / 8; c += kPrologueThreads)
       *reinterpret_cast<uint4*>(ve_out + static_cast<int64_t>(i) * dm + 8 * c) =
           *reinterpret_cast<const uint4*>(ves[i] + tok * dm + 8 * c);
+  }
+}
+
+
+// Greedy choice of the decode loop: the index of the largest of n fp32
+// values (the first one on ties, as torch.argmax; NaN values are never
+// chosen), one 1024-thread workgroup.
+constexpr int kArgmaxThreads = 1024;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ x, int64_t n,
+                                                                int64_t* __restrict__ out) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float best = -INFINITY;
+  int64_t bi = n;  // n: none yet
+  for (int64_t i = tid; i < n; i += kArgmaxThreads) {
+    const float v = x[i];
+    if (v > best || (bi == n && v == best)) {  // strictly larger; the first index of a -inf run
+      best = v;
+      bi = i;
+    }
+  }
+  auto better = [](float v, int64_t i, float bv, int64_t b) { return v > bv || (v == bv && i < b); };
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, kWave);
+    const int64_t oi = __shfl_xor(bi, o, kWave);
+    if (better(ov, oi, best, bi)) best = ov, bi = oi;
+  }
+  __shared__ float sv[kArgmaxThreads / kWave];
+  __shared__ int64_t si[kArgmaxThreads / kWave];
+  if (lane == 0) sv[wave] = best, si[wave] = bi;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w)
+      if (better(sv[w], si[w], best, bi)) best = sv[w], bi = si[w];
+    *out = bi < n ? bi : 0;  // all NaN: index 0
   }
 }
 
@@ -598,19 +632,34 @@ extern "C" int scope_decoder_qkv_glue(int T, int H, int D, int64_t rows, float e
   return check_launch("qkv_glue_kernel");
 }
 
-template <int K>
-static void gemv_launch(int epi, dim3 grid, hipStream_t st, int N, int64_t ldw, int norm, float eps,
-                        const uint16_t* x, const uint16_t* addx, uint16_t* xout, const uint16_t* w,
-                        const uint16_t* res, void* out) {
+template <int K, int R>
+static void gemv_launch_r(int epi, dim3 grid, hipStream_t st, int N, int64_t ldw, int norm, float eps,
+                          const uint16_t* x, const uint16_t* addx, uint16_t* xout, const uint16_t* w,
+                          const uint16_t* res, void* out) {
   const dim3 blk(64 * kGemvWaves);
   if (epi == kGemvPlain)
-    hipLaunchKernelGGL((gemv_kernel<K, kGemvPlain>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvPlain, R>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res,
+                       out);
   else if (epi == kGemvRelu2)
-    hipLaunchKernelGGL((gemv_kernel<K, kGemvRelu2>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvRelu2, R>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res,
+                       out);
   else if (epi == kGemvResid)
-    hipLaunchKernelGGL((gemv_kernel<K, kGemvResid>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvResid, R>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res,
+                       out);
   else
-    hipLaunchKernelGGL((gemv_kernel<K, kGemvLogit>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvLogit, R>), grid, blk, 0, st, N, ldw, norm, eps, x, addx, xout, w, res,
+                       out);
+}
+
+// one row per wavefront (more workgroups in flight), two for the logit head's
+// N >= 16384 rows, where the extra workgroups cost more than they hide
+template <int K>
+static void gemv_launch(int epi, hipStream_t st, int N, int64_t ldw, int norm, float eps, const uint16_t* x,
+                        const uint16_t* addx, uint16_t* xout, const uint16_t* w, const uint16_t* res, void* out) {
+  if (N >= 16384)
+    gemv_launch_r<K, 2>(epi, dim3(ceil_div(N, kGemvWaves * 2)), st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else
+    gemv_launch_r<K, 1>(epi, dim3(ceil_div(N, kGemvWaves)), st, N, ldw, norm, eps, x, addx, xout, w, res, out);
 }
 
 extern "C" int scope_decoder_gemv(int N, int K, int64_t ldw, int norm, float eps, int epi, const uint16_t* x,
@@ -631,13 +680,12 @@ extern "C" int scope_decoder_gemv(int N, int K, int64_t ldw, int norm, float eps
   static_assert(SCOPE_GEMV_PLAIN == kGemvPlain && SCOPE_GEMV_RELU2 == kGemvRelu2 &&
                     SCOPE_GEMV_RESID == kGemvResid && SCOPE_GEMV_LOGIT == kGemvLogit,
                 "epilogue codes");
-  const dim3 grid(ceil_div(N, kGemvWaves * kGemvRows));
   hipStream_t st = as_stream(stream);
-  if (K == 256) gemv_launch<256>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
-  else if (K == 512) gemv_launch<512>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
-  else if (K == 1024) gemv_launch<1024>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
-  else if (K == 2048) gemv_launch<2048>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
-  else gemv_launch<4096>(epi, grid, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  if (K == 256) gemv_launch<256>(epi, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (K == 512) gemv_launch<512>(epi, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (K == 1024) gemv_launch<1024>(epi, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else if (K == 2048) gemv_launch<2048>(epi, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
+  else gemv_launch<4096>(epi, st, N, ldw, norm, eps, x, addx, xout, w, res, out);
   return check_launch("gemv_kernel");
 }
 
@@ -671,4 +719,11 @@ extern "C" int scope_decode_attn_glue_at(const scope_decode_params* p, const int
   DecGlue g{qkv, ve, va, vb, eps, cos_t, sin_t, rot_rows, rot_st, q_out, k_cache, v_cache};
   return decode_launch(p, t_dev, nullptr, k_cache, v_cache, kv_num, kv_idx, docs, workspace, out, lse, stream,
                        "scope_decode_attn_glue_at", &g);
+}
+
+extern "C" int scope_argmax_f32(const float* x, int64_t n, int64_t* out, void* stream) {
+  SCOPE_REQUIRE(x && out, "scope_argmax_f32: null pointer");
+  SCOPE_REQUIRE(n >= 1, "scope_argmax_f32: n=%lld >= 1 required", (long long)n);
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, as_stream(stream), x, n, out);
+  return check_launch("argmax_kernel");
 }

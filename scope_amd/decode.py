@@ -341,6 +341,5 @@ class ScopeDecoder(nn.Module):
         tok = torch.as_tensor(first, device=self.device)
         for s in range(n_steps):
             logits = self.step(tok)
-            tok = logits[:self.cfg.vocab_size].argmax()
-            out[s] = tok
+            tok = ops.argmax(logits[:self.cfg.vocab_size], out=out[s:s + 1])  # written in place
         return out

@@ -801,6 +801,21 @@ def decoder_gemv(x: torch.Tensor, w: torch.Tensor, *, norm: bool = False, epi: s
     return (out, xout) if addx is not None else out
 
 
+def argmax(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Index of the largest element of a contiguous fp32 vector (the first on
+    ties, as torch.argmax; NaN never chosen), as an int64 [1] tensor on the
+    device (``out`` when given)."""
+    dev = _gpu("argmax", x, out)
+    if x.dtype != torch.float32 or not x.is_contiguous() or x.numel() < 1:
+        raise RuntimeError("argmax: x must be a non-empty contiguous float32 tensor")
+    if out is None:
+        out = torch.empty(1, dtype=torch.int64, device=dev)
+    elif out.dtype != torch.int64 or out.numel() != 1:
+        raise RuntimeError("argmax: out must be one int64 element")
+    call("scope_argmax_f32", _p(x), x.numel(), _p(out), _stream(dev))
+    return out
+
+
 def decoder_step_prologue(tok: torch.Tensor, t_dev: torch.Tensor, tokens: torch.Tensor, docs: torch.Tensor,
                           embed: torch.Tensor, value_embeds, *, eot: int, eps: float | None = None):
     """The start of a decoder token step at the position t_dev (int64 [1] on

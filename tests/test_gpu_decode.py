@@ -248,6 +248,21 @@ def test_decode_attn_glue_equals_glue_then_attention(bs, t, with_ve):
     assert torch.equal(out, o_ref) and torch.equal(lse, l_ref)
 
 
+def test_argmax_matches_torch():
+    """The greedy choice against torch.argmax: random logits, ties (the first
+    index wins), the maximum in the last element, one element, -inf runs."""
+    from scope_amd import ops
+
+    g = torch.Generator().manual_seed(23)
+    cases = [torch.rand(50257, generator=g) * 30, torch.zeros(5000), torch.arange(4096, dtype=torch.float32),
+             torch.tensor([3.0]), torch.full((777,), -float("inf"))]
+    cases[0][[100, 40000]] = 31.0  # a tie at the maximum
+    cases[1][[17, 4000]] = 2.0
+    for x in cases:
+        xd = x.to(DEV)
+        assert int(ops.argmax(xd)) == int(xd.argmax()), (x.numel(), int(ops.argmax(xd)), int(xd.argmax()))
+
+
 def test_graph_steps_equal_eager_steps():
     """The steps inside a block run as one captured graph, replayed per
     token; every replay gives the logits of the eager step (same operations),
