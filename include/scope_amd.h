@@ -524,7 +524,8 @@ int scope_decoder_gemv(int N, int K, int64_t ldw, int norm, float eps, int epi, 
  * docs[t-1] (0 at t = 0) + (*tok == eot); x0 [dm] = F.rms_norm(embed[*tok])
  * (fp32 with eps, rounded to bf16); ve_out [3, dm] row i = table i's row
  * *tok for each of ve0..ve2 given (NULL tables are skipped).  A token
- * outside [0, vocab) or a position outside [0, T_cap) writes nothing.  dm a
+ * outside [0, vocab) or a position outside [0, T_cap) leaves tokens and docs
+ * as they are and writes zeros to x0 and the given tables' rows.  dm a
  * multiple of 8; tables and outputs 16-byte aligned.  No counterpart in the
  * reference, which has no decode loop. */
 int scope_decoder_step_prologue(const int64_t* tok, const int64_t* t_dev, int64_t T_cap, int64_t vocab, int dm,

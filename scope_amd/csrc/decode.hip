@@ -453,8 +453,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(int N, int64_t ld
 // 256-thread workgroup): tokens[t] = tok, docs[t] = docs[t-1] (0 at t = 0)
 // + (tok == eot); x0 = F.rms_norm(embed[tok]) (fp32 with eps, rounded to
 // bf16); ve_out[i] = value_embed_i[tok] for the nve tables given.  A token
-// outside [0, vocab) or a position outside [0, T_cap) writes nothing (the
-// host checks the token of an eager step; a captured step relies on it).
+// outside [0, vocab) or a position outside [0, T_cap) leaves tokens and docs
+// as they are and writes zero rows.
 constexpr int kPrologueThreads = 256;
 
 __global__ __launch_bounds__(kPrologueThreads) void step_prologue_kernel(
@@ -464,7 +464,15 @@ __global__ __launch_bounds__(kPrologueThreads) void step_prologue_kernel(
     const uint16_t* __restrict__ ve2, uint16_t* __restrict__ x0, uint16_t* __restrict__ ve_out) {
   const int tid = threadIdx.x;
   const int64_t tok = *tok_p, t = *t_dev;
-  if (tok < 0 || tok >= vocab || t < 0 || t >= T_cap) return;  // uniform over the workgroup
+  if (tok < 0 || tok >= vocab || t < 0 || t >= T_cap) {  // uniform over the workgroup
+    const bool given[3] = {ve0 != nullptr, ve1 != nullptr, ve2 != nullptr};  // rows exist for given tables only
+    for (int c = tid; c < dm / 8; c += kPrologueThreads) {
+      *reinterpret_cast<uint4*>(x0 + 8 * c) = make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < 3; ++i)
+        if (given[i]) *reinterpret_cast<uint4*>(ve_out + static_cast<int64_t>(i) * dm + 8 * c) = make_uint4(0, 0, 0, 0);
+    }
+    return;
+  }
   if (tid == 0) {
     tokens[t] = tok;
     docs[t] = (t > 0 ? docs[t - 1] : 0) + (tok == eot ? 1 : 0);
@@ -521,11 +529,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float best = -INFINITY;
   int64_t bi = n;  // n: none yet
-  for (int64_t i = tid; i < n; i += kArgmaxThreads) {
-    const float v = x[i];
-    if (v > best || (bi == n && v == best)) {  // strictly larger; the first index of a -inf run
-      best = v;
-      bi = i;
+  // sixteen loads in flight per thread, then compared in index order
+  constexpr int U = 16;
+  for (int64_t i0 = tid; i0 < n; i0 += static_cast<int64_t>(U) * kArgmaxThreads) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + static_cast<int64_t>(u) * kArgmaxThreads;
+      v[u] = i < n ? x[i] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + static_cast<int64_t>(u) * kArgmaxThreads;
+      if (i < n && (v[u] > best || (bi == n && v[u] == best))) {  // strictly larger; the first of a -inf run
+        best = v[u];
+        bi = i;
+      }
     }
   }
   auto better = [](float v, int64_t i, float bv, int64_t b) { return v > bv || (v == bv && i < b); };

@@ -301,6 +301,9 @@ class ScopeDecoder(nn.Module):
         t = self.t
         if t >= self.max_len:
             raise ValueError("step: the cache is full")
+        if not isinstance(token, torch.Tensor) or not token.is_cuda:  # a host token is checked here
+            if not 0 <= int(token) < self.cfg.vocab_size:
+                raise ValueError(f"step: token {int(token)} outside the vocabulary [0, {self.cfg.vocab_size})")
         tok = torch.as_tensor(token, device=self.device).reshape(1).long()
         opens = t % bs == 0 or not self.have_lists
         closes = t % bs == bs - 1

@@ -175,7 +175,7 @@ def test_decoder_step_prologue_matches_torch_ops():
     a plain token) exactly, the value-embedding rows exactly, x0 =
     F.rms_norm(embedding) within one bf16 step (the sum of squares runs in
     another order) and equal on at least 99% of its features; a token
-    outside the vocabulary writes nothing."""
+    outside the vocabulary changes neither and gives zero rows."""
     import torch.nn.functional as F
 
     from scope_amd import ops
@@ -193,9 +193,10 @@ def test_decoder_step_prologue_matches_torch_ops():
         td = torch.tensor([t], dtype=torch.int64, device=DEV)
         tok_before, doc_before = tokens.clone(), docs.clone()
         if tk >= V:
-            ops.decoder_step_prologue(tok, td, tokens, docs, embed, ves, eot=eot)
+            x0, ve = ops.decoder_step_prologue(tok, td, tokens, docs, embed, ves[:2], eot=eot)
             torch.cuda.synchronize()
             assert torch.equal(tokens, tok_before) and torch.equal(docs, doc_before)
+            assert torch.all(x0 == 0) and ve.shape == (2, dm) and torch.all(ve == 0)
             continue
         x0, ve = ops.decoder_step_prologue(tok, td, tokens, docs, embed, ves, eot=eot)
         exp_doc = (int(doc_before[t - 1]) if t > 0 else 0) + (1 if tk == eot else 0)
