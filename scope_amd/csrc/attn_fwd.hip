@@ -181,6 +181,17 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
+  // mass: this lane's probability sum over the tiles of list entry pent,
+  // folded into the entry's slot (one wavefront reduction) when the entry changes
+  float pacc = 0.f;
+  int pent = -1;
+  auto mass_flush = [&]() __attribute__((always_inline)) {
+    if (pent < 0) return;
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1) pacc += __shfl_xor(pacc, o2, 64);
+    if (lane == 0) mslot[pent * NW + wave] += pacc;
+    pacc = 0.f;
+  };
   float lse2 = 0.f;  // mass: the row's LSE in log2 units
   if (MASS) lse2 = a.lse[hT + R.row] * kLog2e;
   float bt = 0.f;  // block mode: β·bias of the current key block (log2 units)
@@ -265,9 +276,11 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) ps += __builtin_amdgcn_exp2f(fmaf(s[mb][r], csm, off));
-#pragma unroll
-      for (int o2 = 32; o2 > 0; o2 >>= 1) ps += __shfl_xor(ps, o2, 64);
-      if (lane == 0) mslot[(it / NSUB) * NW + wave] += ps;
+      if (it / NSUB != pent) {  // the tiles of a list entry come in a row (it / NSUB is uniform)
+        mass_flush();
+        pent = it / NSUB;
+      }
+      pacc += ps;
       return false;
     }
 
@@ -398,6 +411,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
 
   // ---- epilogue
   if (MASS) {
+    mass_flush();
     __syncthreads();  // every wavefront's shares are in mslot
     float* mrow = a.mass + lrow * a.QB;
     for (int e = tid; e < n; e += NT) {
