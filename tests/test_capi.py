@@ -92,6 +92,16 @@ def test_ops_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         ops.attn_fwd(q, q, q, torch.ones((2, 2), dtype=torch.int32), torch.zeros((2, 2, 1), dtype=torch.int32),
                      docs, torch.zeros(2, dtype=torch.int32), bs=128, scale=0.12)
+    # the decoder's token-step ops
+    x = torch.zeros(1024, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.decoder_gemv(x, torch.zeros((8, 1024), dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.argmax(torch.zeros(10))
+    i1 = torch.zeros(1, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.decoder_step_prologue(i1, i1, torch.zeros(8, dtype=torch.int64), torch.zeros(8, dtype=torch.int32),
+                                  torch.zeros((4, 1024), dtype=torch.bfloat16), [], eot=3)
 
 
 def test_missing_library_raises(tmp_path):
