@@ -366,11 +366,12 @@ __device__ __forceinline__ void token_qfeat(const AttnArgs& a, int64_t hT, int64
 
 // ---- one 64-key tile staged in LDS (q-major passes: forward, dQ) -----------
 // Filled by global_load_lds; two buffers alternate so the copies of tile j+1
-// run under the MFMAs of tile j.
-template <int MODE>
+// run under the MFMAs of tile j.  WV = false: no V rows (the forward's LSE
+// and block-mass kinds, which form no P·V).
+template <int MODE, bool WV = true>
 struct alignas(16) KvTile {
   uint16_t k[64 * 128];                      // K rows, swizzled (swz_off)
-  uint16_t v[64 * 128];                      // V rows, swizzled
+  uint16_t v[WV ? 64 * 128 : 8];             // V rows, swizzled
   int docs[64];                              // document id per key
   float tab[16];                             // block mode: table row of distance qb - kb
   uint16_t f[MODE >= 2 ? 64 * kTokRow : 8];  // token modes: key features [64][32] (swz32_off)
@@ -380,8 +381,9 @@ constexpr int kListLds = 1024;  // kv-list entries staged in LDS: the widest lis
 
 // Issue the copies of keys kv0 .. kv0+63 (and the block-table row rdist) into
 // b; NT threads (128, 256 or 512) take part.
-template <int MODE, int NT>
-__device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, int rdist, KvTile<MODE>& b, int tid) {
+template <int MODE, int NT, bool WV = true>
+__device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, int rdist, KvTile<MODE, WV>& b,
+                                         int tid) {
   static_assert(NT == 128 || NT == 256 || NT == 512, "kv_issue: 128, 256 or 512 threads");
   // kv0, rdist and the wavefront index are the same in every lane: the row
   // bases live in scalar registers and each lane adds a 32-bit byte offset
@@ -396,7 +398,8 @@ __device__ __forceinline__ void kv_issue(const AttnArgs& a, int h, int64_t kv0, 
     const int idx = jj * NT + tid;
     const int r = idx >> 4, c = (idx & 15) ^ swz(r);
     g2lds16(kbase, static_cast<uint32_t>((r * static_cast<int>(a.k_st) + c * 8) * 2), b.k + (jj * NT + wave * 64) * 8);
-    g2lds16(vbase, static_cast<uint32_t>((r * static_cast<int>(a.v_st) + c * 8) * 2), b.v + (jj * NT + wave * 64) * 8);
+    if constexpr (WV)
+      g2lds16(vbase, static_cast<uint32_t>((r * static_cast<int>(a.v_st) + c * 8) * 2), b.v + (jj * NT + wave * 64) * 8);
   }
   if (wave == 0 && lane < 16) g2lds16(a.docs + k0, lane * 16, b.docs);
   if (MODE == 1 && wave == 1 && lane < 4) {

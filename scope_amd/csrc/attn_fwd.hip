@@ -49,8 +49,8 @@ struct FwdRow {
 // s holds the log2-domain score without the row offset (x·scale·log2e + the
 // per-element terms).  Modes 0 and 1 leave the raw q·k (the scale is applied
 // inside the exponent's FMA) and only mask.  Masked entries are -inf.
-template <int MODE, bool MASK>
-__device__ __forceinline__ void fwd_scores(const AttnArgs& a, const KvTile<MODE>& b, const FwdRow& R, int kv0,
+template <int MODE, bool MASK, typename Tile>
+__device__ __forceinline__ void fwd_scores(const AttnArgs& a, const Tile& b, const FwdRow& R, int kv0,
                                            int lane, f32x16_t (&s)[2]) {
   constexpr bool TOK = MODE >= 2, GATE = MODE == 3;
   const int g = lane >> 5;
@@ -116,8 +116,9 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
   // (see the loop below), which needs a third tile buffer
   constexpr bool STAGGER = PV && BS == 256;
 
-  __shared__ KvTile<MODE> buf0, buf1;
-  __shared__ typename std::conditional<STAGGER, KvTile<MODE>, int>::type buf2;
+  using Tile = KvTile<MODE, PV>;  // the LSE and mass kinds stage no V rows
+  __shared__ Tile buf0, buf1;
+  __shared__ typename std::conditional<STAGGER, Tile, int>::type buf2;
   // key-block indices of the list (< 65536, checked on the host): 16 bits keep the
   // bs=128 workgroup under half of the CU's LDS, two workgroups per CU
   __shared__ uint16_t kbs[kListLds];
@@ -209,14 +210,14 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     while (it < total && kb_at(it / NSUB) * BS + (it % NSUB) * BN > qmax) ++it;
     return it;
   };
-  auto issue = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
+  auto issue = [&](int it, Tile& b) __attribute__((always_inline)) {
     const int kb = kb_at(it / NSUB);
     const int rd = min(max(qb - kb, 0), a.QB - 1);
-    kv_issue<MODE, NT>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
+    kv_issue<MODE, NT, PV>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
   };
   // one tile in two parts: scores and probabilities (P^T as bf16 B operands
   // in pb; false when the wavefront has nothing to do), then O^T += V^T P^T
-  auto run_a = [&](int it, const KvTile<MODE>& b, uint4 (&pb)[4]) __attribute__((always_inline)) -> bool {
+  auto run_a = [&](int it, const Tile& b, uint4 (&pb)[4]) __attribute__((always_inline)) -> bool {
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (kv0 > wrow_lo + 31) return false;  // every key follows this wavefront's rows
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
@@ -325,13 +326,13 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     l_run += psum;
     return PV;
   };
-  auto run_b = [&](const KvTile<MODE>& b, const uint4 (&pb)[4]) __attribute__((always_inline)) {
+  auto run_b = [&](const Tile& b, const uint4 (&pb)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
       for (int md = 0; md < 4; ++md) o[md] = mfma32(lds_kmajor_o(b.v, to, 16 * s2, md), pb[s2], o[md]);
   };
-  auto run = [&](int it, const KvTile<MODE>& b) __attribute__((always_inline)) {
+  auto run = [&](int it, const Tile& b) __attribute__((always_inline)) {
     uint4 pb[4];
     if (run_a(it, b, pb)) run_b(b, pb);
   };
@@ -347,15 +348,15 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     // group is done with tile k-2, whose buffer then takes tile k+1.  Both
     // groups pass n+1 barriers for n tiles.
     const int tid4 = tid & 255;
-    auto issue4 = [&](int it, KvTile<MODE>& b) __attribute__((always_inline)) {
+    auto issue4 = [&](int it, Tile& b) __attribute__((always_inline)) {
       const int kb = kb_at(it / NSUB);
       const int rd = min(max(qb - kb, 0), a.QB - 1);
-      kv_issue<MODE, 256>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid4);
+      kv_issue<MODE, 256, PV>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid4);
     };
     if (wave < 4) {
       int cur = next_valid(0);
       if (cur < total) issue4(cur, buf0);
-      auto lead = [&](KvTile<MODE>& bc, KvTile<MODE>& bn) __attribute__((always_inline)) {
+      auto lead = [&](Tile& bc, Tile& bn) __attribute__((always_inline)) {
         wait_vm0();
         __syncthreads();  // tile cur is in bc for everyone; the lagging group is done with bn
         const int nxt = next_valid(cur + 1);
@@ -374,7 +375,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     } else {
       __syncthreads();  // tile 0 is in buf0
       int cur = next_valid(0);
-      auto lag = [&](const KvTile<MODE>& bc) __attribute__((always_inline)) {
+      auto lag = [&](const Tile& bc) __attribute__((always_inline)) {
         uint4 pb[4];
         const bool act = run_a(cur, bc, pb);
         __syncthreads();  // the leading group starts the next tile
