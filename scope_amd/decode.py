@@ -134,6 +134,9 @@ class ScopeDecoder(nn.Module):
         self.list_idx = [torch.zeros((H, width), dtype=torch.int32, device=device) if "qkv" in lay else None
                          for lay in self.layers]
         self.have_lists = False
+        # a dict here makes every reselection record, per attention layer, the
+        # query row it chose from, its logits and its lists (eager steps only)
+        self.record: dict | None = None
         self.docs = torch.zeros(max_len, dtype=torch.int32, device=device)
         self.tokens = torch.zeros(max_len, dtype=torch.int64, device=device)
         self.t = 0
@@ -171,14 +174,15 @@ class ScopeDecoder(nn.Module):
     def _logits(self, x: torch.Tensor) -> torch.Tensor:
         return 30 * torch.sigmoid(F.linear(_norm(x), self.lm_head).float() / 7.5)
 
-    def _select(self, qbar: torch.Tensor, kbar: torch.Tensor, nb: int):
+    def _select(self, qbar: torch.Tensor, kbar: torch.Tensor, nb: int, return_logits: bool = False):
         """Block-scoring lists of blocks 0..nb-1 from q̄, k̄ [H, nb, D]."""
         cfg = self.cfg
         T = nb * cfg.block_size
         ds_ptr, ds_local, _ = ops.doc_starts(self.docs[:T], cfg.block_size)
         return ops.pointer_select(ds_ptr, ds_local, bs=cfg.block_size, NB=nb, H=cfg.num_heads, window=cfg.window,
                                   n_global=cfg.n_global, budget=cfg.budget, qbar=qbar, kbar=kbar, temp=1.0,
-                                  logit_scale=cfg.block_size / math.sqrt(cfg.head_dim), noise="none")
+                                  logit_scale=cfg.block_size / math.sqrt(cfg.head_dim), noise="none",
+                                  return_logits=return_logits)
 
     # ---- prefill ---------------------------------------------------------------
     @torch.no_grad()
@@ -212,7 +216,7 @@ class ScopeDecoder(nn.Module):
                 self.kbar[i][:, :T // bs] = kbar
                 kv_num, kv_idx, _ = self._select(qbar, kbar, T // bs)
                 y, _ = ops.attn_fwd(qh[None], kh[None], vh[None], kv_num, kv_idx, docs, ds_tok_end, bs=bs,
-                                    scale=cfg.attn_scale)
+                                    scale=cfg.attn_scale, check=False)
                 x = x + F.linear(y[0].transpose(0, 1).reshape(T, -1), lay["proj"])
             x = x + self._mlp(lay, x)
             if i < n:
@@ -270,19 +274,25 @@ class ScopeDecoder(nn.Module):
                     nb = qb + 1
                     qbar = torch.zeros((H, nb, D), dtype=torch.float32, device=self.device)
                     qbar[:, qb] = q[0].float()
-                    kv_num, kv_idx, _ = self._select(qbar, self.kbar[i][:, :nb].contiguous(), nb)
+                    if self.record is None:
+                        kv_num, kv_idx, _ = self._select(qbar, self.kbar[i][:, :nb].contiguous(), nb)
+                    else:
+                        kv_num, kv_idx, _, lg = self._select(qbar, self.kbar[i][:, :nb].contiguous(), nb,
+                                                             return_logits=True)
+                        self.record[i] = dict(q=qbar[:, qb].clone(), logits=lg.clone(), kv_num=kv_num.clone(),
+                                              kv_idx=kv_idx.clone())
                     self.list_num[i].copy_(kv_num[:, qb])
                     self.list_idx[i].zero_()
                     self.list_idx[i][:, :kv_idx.shape[-1]].copy_(kv_idx[:, qb])
                     y, _ = ops.decode_attn(q[0], self.k_cache[i], self.v_cache[i], self.list_num[i], self.list_idx[i],
-                                           self.docs, td, bs=bs, scale=cfg.attn_scale, workspace=self._ws)
+                                           self.docs, td, bs=bs, scale=cfg.attn_scale, workspace=self._ws, check=False)
                 else:
                     # lists fixed within the block: the glue runs inside the attention
                     # (k, v into cache row t there)
                     y, _, _ = ops.decode_attn_glue(qkv, ve[i], td, self.rotary.cos, self.rotary.sin, self.k_cache[i],
                                                    self.v_cache[i], self.list_num[i], self.list_idx[i], self.docs,
                                                    heads=H, va=va, vb=vb, bs=bs, scale=cfg.attn_scale,
-                                                   workspace=self._ws)
+                                                   workspace=self._ws, check=False)
                 x = gemv(y.reshape(H * D), lay["proj"], epi="resid", res=x)
                 if closes:  # the block is complete: its key mean joins the candidates
                     self.kbar[i][:, qb] = self.k_cache[i][:, qb * bs:(qb + 1) * bs].float().mean(dim=1)

@@ -355,3 +355,54 @@ def test_block_start_reselection_matches_oracle_choice():
     for h in range(cfg.num_heads):
         want = ref["packed"][h, qb, :ref["kv_num"][h, qb]]
         assert list(kv_idx[h, :int(kv_num[h])].numpy()) == list(want), h
+
+
+def test_block_start_reselection_every_layer_full_config():
+    """The full decoder configuration (16 layers, d_model 1024, window 4,
+    budget 4, one global block) after a 20-block prompt with three documents:
+    at the next block start, every attention layer's reselection (the new
+    token's query against the cached key-block means of blocks 0..20) gives
+    logits within 1e-4·(1 + |ref|) of fp64 from the recorded query and means
+    (on the candidates: the kernel marks the window, the global block and
+    later blocks -inf), and lists equal to the oracle's block-scoring
+    selection on those logits."""
+    from scope_amd.decode import DecoderConfig, ScopeDecoder
+
+    cfg = DecoderConfig()
+    bs, D = cfg.block_size, cfg.head_dim
+    T0 = 20 * bs
+    g = torch.Generator().manual_seed(8)
+    toks = torch.randint(0, 50257, (T0 + 1,), generator=g)
+    toks[[100, 200]] = 50256  # the current document starts in block 1: 15 candidates beyond window and global
+    print("full-config block-start reselection, every layer", flush=True)
+    m = ScopeDecoder(cfg, max_len=T0 + bs, device=DEV, seed=0, use_graph=False)
+    m.prefill(toks[:T0])
+    m.record = {}
+    m.step(toks[T0])
+    torch.cuda.synchronize()
+    qb = T0 // bs
+    nb = qb + 1
+    docs = m.docs[:nb * bs].cpu().numpy()
+    layers = sorted(m.record)
+    assert layers == [i for i, lay in enumerate(m.layers) if "qkv" in lay] and len(layers) == cfg.num_layers - 1
+    n_far = 0
+    for i in layers:
+        rec = m.record[i]
+        lg = rec["logits"].cpu()
+        want = (bs / math.sqrt(D)) * torch.einsum("hd,hkd->hk", rec["q"].double().cpu(), m.kbar[i][:, :nb].double().cpu())
+        fin = torch.isfinite(lg[:, qb])  # the window, the global block and later blocks are no candidates
+        assert bool((fin.sum(-1) > cfg.budget).all()), f"layer {i}: the selection has no choice to make"
+        err = ((lg[:, qb].double() - want).abs() / (1 + want.abs()))[fin].max().item()
+        assert err <= 1e-4, f"layer {i}: logits off by {err:.3g}"
+        ref = OP.pointer_select_blockscore(lg.numpy(), docs, bs=bs, window=cfg.window, n_global=cfg.n_global,
+                                           budget=cfg.budget)
+        kv_num, kv_idx = rec["kv_num"].cpu(), rec["kv_idx"].cpu()
+        got_num, got_idx = m.list_num[i].cpu(), m.list_idx[i].cpu()
+        for h in range(cfg.num_heads):
+            want_list = list(ref["packed"][h, qb, :ref["kv_num"][h, qb]])
+            assert list(kv_idx[h, qb, :int(kv_num[h, qb])].numpy()) == want_list, (i, h)
+            assert list(got_idx[h, :int(got_num[h])].numpy()) == want_list, (i, h)
+            n_far += sum(1 for kb in want_list if kb < qb - cfg.window + 1 and kb != 0)
+    print(f"  {len(layers)} layers x {cfg.num_heads} heads equal the oracle; {n_far} picks outside the window "
+          f"and the global block", flush=True)
+    assert n_far > 0

@@ -18,12 +18,16 @@ What is compared:
   spectral coefficient gradients against the fp32 oracle;
 * dK/dV of one ordinary key block against the fp32 oracle over every q-block
   that lists it;
+* out and lse of every row of heads 0 and H-1 against a row reference: fp32
+  torch on the device over each q-block's listed key blocks (the block term,
+  the document-causal mask and the list applied as in the oracle), computed
+  from q, k, v and the coefficients alone;
 * dK/dV of every hot key block (more than 32 users: the global blocks whose
   sums run through the multi-chunk partials and the reduce; up to 4096 users,
   128 chunks, at a million tokens) against a column reference: the key
-  block's column of P and dS in fp32 torch on the device from the kernel's
-  own lse and out (both checked above on sampled rows), and the same column
-  reference is checked against the oracle on the ordinary key block.
+  block's column of P and dS in fp32 torch on the device from the row
+  reference's lse and out (not the kernel's), and the same column reference
+  is checked against the oracle on the ordinary key block.
 
 Bar written in every comparison: |got - ref| <= 2e-2 + 1e-2·|ref|."""
 from __future__ import annotations
@@ -44,10 +48,55 @@ SCALE, BETA = 0.12, 0.5
 CHUNK = 32
 
 
+def _rows_ref(h, bs, q, k, v, kv_num, kv_idx, docs, cc, cs, om, batch=32):
+    """out [T, D] and lse [T] (fp32, natural log) of every row of head h: each
+    q-block attends over its first kv_num listed key blocks with
+    s = scale·q·k + β·Σ_k (A_k cos ω_k r + B_k sin ω_k r), r = qb - kb, and the
+    document-causal mask; fp32 torch on the device, q-blocks in batches."""
+    T, D = q.shape[2], q.shape[3]
+    NB, L = T // bs, kv_idx.shape[-1]
+    Qh, Kh, Vh = q[0, h], k[0, h], v[0, h]
+    ar = torch.arange(bs, device=DEV)
+    out = torch.empty((T, D), dtype=torch.float32, device=DEV)
+    lse = torch.empty(T, dtype=torch.float32, device=DEV)
+    for i0 in range(0, NB, batch):
+        qb = torch.arange(i0, min(NB, i0 + batch), device=DEV)
+        G = qb.numel()
+        idx = kv_idx[h, qb].long()  # [G, L]
+        valid = torch.arange(L, device=DEV)[None] < kv_num[h, qb][:, None]
+        keys = (idx[..., None] * bs + ar).reshape(G, L * bs)
+        rows = (qb[:, None] * bs + ar).reshape(G, bs)
+        s = SCALE * torch.matmul(Qh[rows].float(), Kh[keys].float().transpose(1, 2).contiguous())  # [G, bs, L·bs]
+        ph = (qb[:, None] - idx).float()[..., None] * om  # [G, L, K]
+        bt = torch.matmul(cc[0, h][rows], torch.cos(ph).transpose(1, 2).contiguous())
+        bt = BETA * (bt + torch.matmul(cs[0, h][rows], torch.sin(ph).transpose(1, 2).contiguous()))  # [G, bs, L]
+        s = s.view(G, bs, L, bs) + bt[..., None]
+        ok = (valid[:, None, :, None] & (keys.view(G, 1, L, bs) <= rows.view(G, bs, 1, 1))
+              & (docs[keys].view(G, 1, L, bs) == docs[rows].view(G, bs, 1, 1)))
+        s = torch.where(ok, s, torch.full_like(s, -math.inf)).view(G, bs, L * bs)
+        lg = torch.logsumexp(s, dim=-1)  # [G, bs]; -inf for a row without visible keys
+        p = torch.where(torch.isinf(lg)[..., None], torch.zeros_like(s), torch.exp(s - lg[..., None]))
+        out[rows.reshape(-1)] = torch.matmul(p, Vh[keys].float()).reshape(G * bs, D)
+        lse[rows.reshape(-1)] = lg.reshape(-1)
+    return out, lse
+
+
+def _check_dev(name, got, want):
+    """The bar on the device (float64), for whole heads."""
+    got, want = got.double(), want.double()
+    both_inf = torch.isinf(got) & torch.isinf(want) & (torch.sign(got) == torch.sign(want))
+    err = torch.where(both_inf, torch.zeros_like(got), (got - want).abs())
+    ratio = (err / (2e-2 + 1e-2 * want.abs().nan_to_num(posinf=0.0, neginf=0.0))).nan_to_num(nan=math.inf)
+    worst = float(ratio.max())
+    print(f"    {name}: worst ratio {worst:.3f}", flush=True)
+    assert worst <= 1.0, f"{name}: worst tolerance ratio {worst:.3f}"
+
+
 def _column_ref(h, kb, bs, q, k, v, dout, out, lse, kv_num, kv_idx, docs, cc, cs, om):
     """dK, dV [bs, D] of key block kb in head h: fp32 torch on the device,
     P_ij = exp(s_ij - lse_i) over the rows whose q-block lists kb,
-    dS = P∘(dO·V^T - rowsum(dO∘O)), dV = P^T·dO, dK = scale·dS^T·Q."""
+    dS = P∘(dO·V^T - rowsum(dO∘O)), dV = P^T·dO, dK = scale·dS^T·Q.
+    out [T, D] and lse [T] are head h's rows (the row reference's)."""
     T = q.shape[2]
     cols = slice(kb * bs, (kb + 1) * bs)
     Qh, dO = q[0, h].float(), dout[0, h].float()
@@ -61,10 +110,10 @@ def _column_ref(h, kb, bs, q, k, v, dout, out, lse, kv_num, kv_idx, docs, cc, cs
     i = torch.arange(T, device=DEV)[:, None]
     j = torch.arange(kb * bs, (kb + 1) * bs, device=DEV)[None, :]
     ok = (i >= j) & (docs[:, None] == docs[cols][None, :]) & listed[rowq][:, None]
-    P = torch.where(ok, torch.exp(s - lse[0, h][:, None]), torch.zeros_like(s))
+    P = torch.where(ok, torch.exp(s - lse[:, None]), torch.zeros_like(s))
     del s
     dV = P.T @ dO
-    dS = P * (dO @ Vb.T - (dO * out[0, h].float()).sum(-1)[:, None])
+    dS = P * (dO @ Vb.T - (dO * out).sum(-1)[:, None])
     dK = SCALE * (dS.T @ Qh)
     return dK.cpu(), dV.cpu()
 
@@ -125,7 +174,19 @@ def _layer_checks(step, inp, heads, sample_qbs, bs, n_hot_max=None):
         print(f"   key block {kb_o} ({len(users_o)} users)", flush=True)
         _check("dk", gr["dk"][0, h, sl].float().cpu(), gk[sl])
         _check("dv", gr["dv"][0, h, sl].float().cpu(), gv[sl])
-        ck, cv = _column_ref(h, kb_o, bs, t["q"], t["k"], t["v"], t["dout"], out, lse, kv_num, kv_idx, docs,
+        # every row of the head: the row reference against the oracle's
+        # sampled blocks, then the kernel against the row reference
+        ro_all, rl_all = _rows_ref(h, bs, t["q"], t["k"], t["v"], kv_num, kv_idx, docs, t["coeff_cos"],
+                                   t["coeff_sin"], om)
+        for qb in sample_qbs:
+            sl_q = slice(qb * bs, (qb + 1) * bs)
+            ro, rl = res[(0, qb)]
+            _check(f"row reference out of q-block {qb} vs oracle", ro_all[sl_q].cpu(), ro.detach())
+            _check(f"row reference lse of q-block {qb} vs oracle", rl_all[sl_q].cpu(), rl.detach())
+        print(f"   every row of head {h}", flush=True)
+        _check_dev("out", out[0, h].float(), ro_all)
+        _check_dev("lse", lse[0, h], rl_all)
+        ck, cv = _column_ref(h, kb_o, bs, t["q"], t["k"], t["v"], t["dout"], ro_all, rl_all, kv_num, kv_idx, docs,
                              t["coeff_cos"], t["coeff_sin"], om)
         _check("column reference dk vs oracle", ck, gk[sl])
         _check("column reference dv vs oracle", cv, gv[sl])
@@ -135,13 +196,14 @@ def _layer_checks(step, inp, heads, sample_qbs, bs, n_hot_max=None):
         if n_hot_max is not None:
             hot = hot[np.argsort(-n_users[hot], kind="stable")][:n_hot_max]
         for kb in hot.tolist():
-            ck, cv = _column_ref(h, kb, bs, t["q"], t["k"], t["v"], t["dout"], out, lse, kv_num, kv_idx, docs,
-                                 t["coeff_cos"], t["coeff_sin"], om)
+            ck, cv = _column_ref(h, kb, bs, t["q"], t["k"], t["v"], t["dout"], ro_all, rl_all, kv_num, kv_idx,
+                                 docs, t["coeff_cos"], t["coeff_sin"], om)
             sl = slice(kb * bs, (kb + 1) * bs)
             print(f"   hot key block {kb} ({int(n_users[kb])} users, {-(-int(n_users[kb]) // CHUNK)} chunks)",
                   flush=True)
             _check("dk", gr["dk"][0, h, sl].float().cpu(), ck)
             _check("dv", gr["dv"][0, h, sl].float().cpu(), cv)
+        del ro_all, rl_all
 
 
 def _lists_vs_oracle(step, window, n_global, budget):

@@ -2,7 +2,8 @@
 layer): pointer selection over 4096 candidates with in-kernel counter Gumbel
 noise (bit-exact), the block means feeding it, the mask statistics, and the
 block-sparse attention forward and backward on sampled blocks (also at the
-64k-token training shape, bs=128).
+64k-token training shape, bs=128, with all eight heads: heads 0 and 7 are
+compared).
 
 The attention oracle is evaluated only where it is cheap and still complete:
 out / lse / dq of a few q-blocks (each depends only on its own list), and dk /
@@ -82,15 +83,15 @@ def test_c5_block_means():
     assert np.abs(kbar.cpu().numpy() - rk).max() < 1e-6
 
 
-@pytest.mark.parametrize("T,BS,W,G,B", [(1 << 20, 256, 2, 1, 8), (65536, 128, 4, 1, 4)])
-def test_attention_sampled_blocks(T, BS, W, G, B):
-    """The million-token layer (bs 256) and the 64k training shape (bs 128)."""
+@pytest.mark.parametrize("T,BS,W,G,B,H", [(1 << 20, 256, 2, 1, 8, 1), (65536, 128, 4, 1, 4, 8)])
+def test_attention_sampled_blocks(T, BS, W, G, B, H):
+    """The million-token layer (bs 256, one head) and the 64k training shape
+    (bs 128, all eight heads run, heads 0 and 7 compared)."""
     import scope_amd
     from scope_amd import ops
     from scope_amd.blockmask import ScopeBlockMask
 
     NB = T // BS
-    H = 1
     scale, beta = 0.12, 0.5
     print(f"attention fwd+bwd T={T} H={H} bs={BS} W{W} G{G} B{B}", flush=True)
     rng = np.random.default_rng(9)
@@ -112,48 +113,44 @@ def test_attention_sampled_blocks(T, BS, W, G, B):
     out.backward(dout.to(DEV))
     torch.cuda.synchronize()
     print("  gpu done", flush=True)
+    q_off, q_list = ops.transpose_blocks(kv_num.to(DEV).int(), kv_idx.to(DEV).int(), NB)
+
+    def check(name, got, want):
+        ok, worst = tol_check(got, want)
+        print(f"    {name}: worst ratio {worst:.3f}", flush=True)
+        assert ok, f"{name}: worst tolerance ratio {worst:.3f}"
 
     # sampled q-blocks: first, a middle one, last
     qbs = [0, NB // 2 + 3, NB - 1]
-    # one key block (not the global block 0) and every q-block that lists it
-    kb = NB // 3
-    q_off, q_list = ops.transpose_blocks(kv_num.to(DEV).int(), kv_idx.to(DEV).int(), NB)
-    o0, o1 = int(q_off[0, kb]), int(q_off[0, kb + 1])
-    users = sorted(set(q_list[0, o0:o1].cpu().tolist()))
-    assert users and all(int(u_) >= kb for u_ in users)
-    rows = sorted(set(qbs) | set(users))
-    print(f"  oracle over {len(rows)} q-blocks (key block {kb} has {len(users)})", flush=True)
+    for h in sorted({0, H - 1}):
+        # one key block (not the global block 0) and every q-block that lists it
+        kb = NB // 3
+        o0, o1 = int(q_off[h, kb]), int(q_off[h, kb + 1])
+        users = sorted(set(q_list[h, o0:o1].cpu().tolist()))
+        assert users and all(int(u_) >= kb for u_ in users)
+        rows = sorted(set(qbs) | set(users))
+        print(f"  head {h}: oracle over {len(rows)} q-blocks (key block {kb} has {len(users)})", flush=True)
 
-    qq, kk, vv = (x[0].float().requires_grad_() for x in (q, k, v))
-    cc, cs = A[0].float().requires_grad_(), Bc[0].float().requires_grad_()
-    res = OA.attention_blocksparse(qq, kk, vv, kv_num, kv_idx, docs, bs=BS, scale=scale, beta=beta,
-                                   bias_mode="block", coeff_cos=cc, coeff_sin=cs, omegas=om,
-                                   heads=[0], qblocks=rows)
-    loss = 0.0
-    for qb in rows:
-        o, _ = res[(0, qb)]
-        loss = loss + (o * dout[0, 0, qb * BS:(qb + 1) * BS].float()).sum()
-    loss.backward()
+        qq, kk, vv = (x[0, h:h + 1].float().requires_grad_() for x in (q, k, v))
+        cc, cs = A[0, h:h + 1].float().requires_grad_(), Bc[0, h:h + 1].float().requires_grad_()
+        res = OA.attention_blocksparse(qq, kk, vv, kv_num[h:h + 1], kv_idx[h:h + 1], docs, bs=BS, scale=scale,
+                                       beta=beta, bias_mode="block", coeff_cos=cc, coeff_sin=cs, omegas=om,
+                                       heads=[0], qblocks=rows)
+        loss = 0.0
+        for qb in rows:
+            o, _ = res[(0, qb)]
+            loss = loss + (o * dout[0, h, qb * BS:(qb + 1) * BS].float()).sum()
+        loss.backward()
 
-    for qb in qbs:
-        sl = slice(qb * BS, (qb + 1) * BS)
-        ro, rl = res[(0, qb)]
-        for name, got, want in (("out", out[0, 0, sl].float().cpu(), ro.detach()),
-                                ("lse", lse[0, 0, sl].float().cpu(), rl.detach()),
-                                ("dq", qd.grad[0, 0, sl].float().cpu(), qq.grad[0, sl])):
-            ok, worst = tol_check(got, want)
-            print(f"  q-block {qb} {name}: worst ratio {worst:.3f}", flush=True)
-            assert ok, f"{name} of q-block {qb}: worst tolerance ratio {worst:.3f}"
-    sl = slice(kb * BS, (kb + 1) * BS)
-    for name, got, want in (("dk", kd.grad[0, 0, sl].float().cpu(), kk.grad[0, sl]),
-                            ("dv", vd.grad[0, 0, sl].float().cpu(), vv.grad[0, sl])):
-        ok, worst = tol_check(got, want)
-        print(f"  key block {kb} {name}: worst ratio {worst:.3f}", flush=True)
-        assert ok, f"{name} of key block {kb}: worst tolerance ratio {worst:.3f}"
-    # coefficient gradients of the sampled rows
-    for qb in qbs:
-        sl = slice(qb * BS, (qb + 1) * BS)
-        for name, got, want in (("dcoeff_cos", cd.grad[0, 0, sl].cpu(), cc.grad[0, sl]),
-                                ("dcoeff_sin", sd.grad[0, 0, sl].cpu(), cs.grad[0, sl])):
-            ok, worst = tol_check(got, want)
-            assert ok, f"{name} of q-block {qb}: worst tolerance ratio {worst:.3f}"
+        for qb in qbs:
+            sl = slice(qb * BS, (qb + 1) * BS)
+            ro, rl = res[(0, qb)]
+            check(f"q-block {qb} out", out[0, h, sl].float().cpu(), ro.detach())
+            check(f"q-block {qb} lse", lse[0, h, sl].float().cpu(), rl.detach())
+            check(f"q-block {qb} dq", qd.grad[0, h, sl].float().cpu(), qq.grad[0, sl])
+            # coefficient gradients of the sampled rows
+            check(f"q-block {qb} dcoeff_cos", cd.grad[0, h, sl].cpu(), cc.grad[0, sl])
+            check(f"q-block {qb} dcoeff_sin", sd.grad[0, h, sl].cpu(), cs.grad[0, sl])
+        sl = slice(kb * BS, (kb + 1) * BS)
+        check(f"key block {kb} dk", kd.grad[0, h, sl].float().cpu(), kk.grad[0, sl])
+        check(f"key block {kb} dv", vd.grad[0, h, sl].float().cpu(), vv.grad[0, sl])
