@@ -173,6 +173,18 @@ int scope_transpose_blocks(const int32_t* kv_num, const int32_t* kv_idx, int H, 
 int scope_transpose_blocks_noalloc(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB,
                                    int maxkv, int32_t* q_off, int32_t* q_list, void* stream);
 
+/* List validation.  The reference's pack (model/attn_bias.py:825-837)
+ * guarantees what every kernel here relies on: for each row (h, qb),
+ * 0 <= kv_num <= MAXKV and the first kv_num entries are distinct key blocks
+ * in [0, NB), each <= qb for the causal masks.  This checks a list that did
+ * not come from the library's own builders.  res (device int32 [5]) receives
+ * the number of rows with kv_num outside [0, MAXKV], of entries outside
+ * [0, NB), of entries after their q-block (only with causal != 0), of
+ * repeated entries, and the first offending row h·QB + qb (INT32_MAX when
+ * there is none).  Asynchronous on the stream; NB <= 65536. */
+int scope_check_lists(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv, int causal,
+                      int32_t* res, void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused coefficient head.  Replaces the [B,H,L,M,K] mixture of
  * SpectralBias.forward between the MLP output and the returned terms

@@ -93,6 +93,7 @@ _PROTOS = {
     "scope_transpose_workspace_bytes": (c_int64, [c_int, c_int]),
     "scope_transpose_blocks": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P, P, P]),
     "scope_transpose_blocks_noalloc": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P, P]),
+    "scope_check_lists": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, P, P]),
     "scope_coeff_head_workspace_bytes": (c_int64, [C.POINTER(CoeffParams)]),
     "scope_coeff_head_fwd": (c_int, [C.POINTER(CoeffParams)] + [P] * 17),
     "scope_coeff_head_bwd": (c_int, [C.POINTER(CoeffParams)] + [P] * 18),

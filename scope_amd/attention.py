@@ -144,5 +144,5 @@ def teacher_block_mass(q: torch.Tensor, k: torch.Tensor, docs: torch.Tensor, *, 
         kw = dict(bias_mode="token", beta=spectral.beta, table=spectral_table(spectral.omegas, T, bs, "token"),
                   coeff_cos=spectral.coeff_cos, coeff_sin=spectral.coeff_sin,
                   slope=spectral.slope if spectral.use_slope else None, use_slope=spectral.use_slope)
-    mass, _ = ops.attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, bs=bs, scale=scale, **kw)
+    mass, _ = ops.attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, bs=bs, scale=scale, **kw, check=False)
     return mass

@@ -37,6 +37,18 @@ class ScopeBlockMask:
     ds_local: torch.Tensor | None = None
     extras: dict = field(default_factory=dict)  # radius / centre (reference mode), picks / logits (block scoring)
     _q_lists: tuple | None = field(default=None, repr=False)
+    # validate the lists on construction (ops.check_lists: 0 <= kv_num <= MAXKV
+    # distinct key blocks in [0, NB), each <= its q-block; RuntimeError
+    # otherwise); the library's own builders, whose kernels guarantee that,
+    # pass False
+    check: bool = field(default=True, repr=False)
+
+    def __post_init__(self):
+        if self.kv_num_blocks.shape[-1] * self.BLOCK_SIZE != self.docs.numel():
+            raise RuntimeError(f"ScopeBlockMask: {self.kv_num_blocks.shape[-1]} q-blocks of {self.BLOCK_SIZE} do not "
+                               f"cover the {self.docs.numel()} document ids")
+        if self.check:
+            ops.check_lists(self.kv_num_blocks, self.kv_indices, self.num_blocks, who="ScopeBlockMask")
 
     @property
     def seq_len(self) -> int:
@@ -137,5 +149,5 @@ def create_blockmasks(input_seq: torch.Tensor | None, sliding_window_num_blocks,
         out.append(ScopeBlockMask(
             kv_num_blocks=kv_num.expand(num_heads, -1).reshape(1, num_heads, -1).contiguous(),
             kv_indices=kv_idx.expand(num_heads, -1, -1).reshape(1, num_heads, *kv_idx.shape).contiguous(),
-            BLOCK_SIZE=block_size, docs=docs, ds_tok_end=ds_tok_end, extras=dict(swa=swa)))
+            BLOCK_SIZE=block_size, docs=docs, ds_tok_end=ds_tok_end, extras=dict(swa=swa), check=False))
     return out[0], out[1]

@@ -39,7 +39,9 @@ __global__ void tr_count_kernel(const int32_t* __restrict__ kv_num, const int32_
   const int64_t row = e / maxkv;
   if (static_cast<int>(e % maxkv) >= kv_num[row]) return;
   const int h = static_cast<int>(row / QB);
-  atomicAdd(&q_off[static_cast<int64_t>(h) * (NB + 1) + kv_idx[e] + 1], 1);
+  const int kb = kv_idx[e];
+  if (kb < 0 || kb >= NB) return;  // an entry outside the key blocks is no block (scope_check_lists reports it)
+  atomicAdd(&q_off[static_cast<int64_t>(h) * (NB + 1) + kb + 1], 1);
 }
 
 // also sets the head's list entries past its total to -1 (the fill kernel
@@ -86,6 +88,7 @@ __global__ void tr_fill_kernel(const int32_t* __restrict__ kv_num, const int32_t
   const int h = static_cast<int>(row / QB);
   const int qb = static_cast<int>(row % QB);
   const int kb = kv_idx[e];
+  if (kb < 0 || kb >= NB) return;  // skipped by the count kernel too
   const int pos = atomicAdd(&cursor[static_cast<int64_t>(h) * NB + kb], 1);
   q_list[static_cast<int64_t>(h) * QB * maxkv + q_off[static_cast<int64_t>(h) * (NB + 1) + kb] + pos] = qb;
 }
@@ -143,6 +146,58 @@ __global__ __launch_bounds__(256) void tr_sort_kernel(int NB, int QB, int maxkv,
     }
   }
   for (int i = lane; i < n; i += nt) b[i] = s[i];
+}
+
+// List validation: one wavefront per row (h, qb) of the compact lists, a
+// bitmap of the row's key blocks in LDS (NB bits per wavefront) to find
+// repeated entries.  res: [0] rows whose kv_num is outside [0, maxkv],
+// [1] entries outside [0, NB), [2] entries after their q-block (causal
+// lists), [3] repeated entries, [4] the first offending row h·QB + qb
+// (INT_MAX when there is none).  res is set to {0, 0, 0, 0, INT_MAX} by
+// chk_init_kernel first.
+__global__ void chk_init_kernel(int32_t* __restrict__ res) {
+  if (threadIdx.x < 4) res[threadIdx.x] = 0;
+  if (threadIdx.x == 4) res[4] = INT_MAX;
+}
+
+__global__ __launch_bounds__(256) void chk_lists_kernel(const int32_t* __restrict__ kv_num,
+                                                       const int32_t* __restrict__ kv_idx, int H, int QB, int NB,
+                                                       int maxkv, int causal, int32_t* __restrict__ res) {
+  extern __shared__ uint32_t bm_all[];
+  const int words = (NB + 31) >> 5;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (row >= static_cast<int64_t>(H) * QB) return;  // uniform per wavefront; no barrier follows
+  uint32_t* bm = bm_all + static_cast<int64_t>(wave) * words;
+  for (int w = lane; w < words; w += kWave) bm[w] = 0u;
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's clears have landed
+  __builtin_amdgcn_wave_barrier();
+  const int qb = static_cast<int>(row % QB);
+  const int n = kv_num[row];
+  int bad[4] = {0, 0, 0, 0};
+  if (n < 0 || n > maxkv) {
+    bad[0] = lane == 0;
+  } else {
+    for (int e = lane; e < n; e += kWave) {
+      const int kb = kv_idx[row * maxkv + e];
+      if (kb < 0 || kb >= NB) {
+        ++bad[1];
+      } else if (causal && kb > qb) {
+        ++bad[2];
+      } else {
+        const uint32_t bit = 1u << (kb & 31);
+        if (atomicOr(&bm[kb >> 5], bit) & bit) ++bad[3];
+      }
+    }
+  }
+  int any = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = wave_sum_i32(bad[i]);
+    if (t && lane == 0) atomicAdd(&res[i], t);
+    any |= t;
+  }
+  if (any && lane == 0) atomicMin(&res[4], static_cast<int32_t>(row));
 }
 
 // Address of `scratch` on each device, looked up once per device with that
@@ -236,6 +291,20 @@ int scope_transpose_blocks_noalloc(const int32_t* kv_num, const int32_t* kv_idx,
   rc = noalloc_scratch(stream, &cursor);
   if (rc) return rc;
   return transpose_launch(kv_num, kv_idx, H, QB, NB, maxkv, q_off, q_list, cursor, as_stream(stream));
+}
+
+int scope_check_lists(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv, int causal,
+                      int32_t* res, void* stream) {
+  SCOPE_REQUIRE(kv_num && kv_idx && res, "scope_check_lists: null pointer");
+  SCOPE_REQUIRE(H >= 1 && QB >= 1 && NB >= 1 && maxkv >= 1, "scope_check_lists: bad sizes");
+  SCOPE_REQUIRE(NB <= 65536, "scope_check_lists: NB=%d above 65536", NB);
+  const hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(chk_init_kernel, dim3(1), dim3(64), 0, s, res);
+  const int64_t rows = static_cast<int64_t>(H) * QB;
+  const size_t lds = static_cast<size_t>(4) * ((NB + 31) / 32) * sizeof(uint32_t);
+  hipLaunchKernelGGL(chk_lists_kernel, dim3(ceil_div(rows, 4)), dim3(256), lds, s, kv_num, kv_idx, H, QB, NB, maxkv,
+                     causal ? 1 : 0, res);
+  return check_launch("scope_check_lists");
 }
 
 }  // extern "C"

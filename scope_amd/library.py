@@ -163,7 +163,7 @@ def soft_pointer_bias(q: Tensor, k: Tensor, kv_num: Tensor, kv_idx: Tensor, pick
     block means of q, k; q̄, k̄ are returned for the backward."""
     qbar, kbar = ops.block_means(q, k, bs)
     pb = ops.pointer_pair_bias(kv_num, kv_idx, picks, bs=bs, window=window, n_global=n_global, soft_temp=soft_temp,
-                               qbar=qbar, kbar=kbar, prior=prior, logit_scale=logit_scale)
+                               qbar=qbar, kbar=kbar, prior=prior, logit_scale=logit_scale, check=False)
     return pb, qbar, kbar
 
 
@@ -180,7 +180,7 @@ def pair_bias_from_logits(kv_num: Tensor, kv_idx: Tensor, picks: Tensor, logits:
     """The soft weights of the picks from given logits [H,QB,NB] (constants:
     no gradient)."""
     return ops.pointer_pair_bias(kv_num, kv_idx, picks, bs=bs, window=window, n_global=n_global,
-                                 soft_temp=soft_temp, logits_in=logits)
+                                 soft_temp=soft_temp, logits_in=logits, check=False)
 
 
 @pair_bias_from_logits.register_fake
@@ -197,7 +197,7 @@ def soft_pointer_bwd(qbar: Tensor, kbar: Tensor, kv_num: Tensor, kv_idx: Tensor,
     dq = torch.empty_like(q_like, dtype=torch.bfloat16).zero_()
     dk = torch.empty_like(k_like, dtype=torch.bfloat16).zero_()
     ops.pointer_bwd(qbar, kbar, kv_num, kv_idx, q_off, q_list, pair_bias, dpair_bias.contiguous(), dq, dk, bs=bs,
-                    logit_scale=logit_scale, soft_temp=soft_temp)
+                    logit_scale=logit_scale, soft_temp=soft_temp, check=False)
     return dq, dk
 
 
@@ -234,7 +234,7 @@ soft_pointer_bias.register_autograd(_soft_backward, setup_context=_soft_setup)
 def transpose_blocks(kv_num: Tensor, kv_idx: Tensor, NB: int) -> tuple[Tensor, Tensor]:
     """(q_off [H, NB+1], q_list [H, QB*MAXKV]); a head's entries past
     q_off[h, NB] are -1."""
-    return ops.transpose_blocks(kv_num, kv_idx, NB, tail=-1)
+    return ops.transpose_blocks(kv_num, kv_idx, NB, tail=-1, check=False)
 
 
 @transpose_blocks.register_fake
@@ -305,7 +305,7 @@ def attn_fwd(q: Tensor, k: Tensor, v: Tensor, kv_num: Tensor, kv_idx: Tensor, do
                         bias_mode=_MODES[bias_mode], table=table, coeff_cos=coeff_cos, coeff_sin=coeff_sin, b0=b0,
                         slope=slope, delta_main=delta_main, width=width, use_slope=use_slope,
                         subtract_b0=subtract_b0, gate_kind=_GATES[gate_kind], ramp_lambda=ramp_lambda, tau=tau,
-                        pair_bias=pair_bias)
+                        pair_bias=pair_bias, check=False)
 
 
 @attn_fwd.register_fake
@@ -347,7 +347,7 @@ def attn_bwd(q: Tensor, k: Tensor, v: Tensor, out: Tensor, dout: Tensor, lse: Te
                      beta=beta, bias_mode=_MODES[bias_mode], table=table, coeff_cos=coeff_cos, coeff_sin=coeff_sin,
                      b0=b0, slope=slope, delta_main=delta_main, width=width, use_slope=use_slope,
                      subtract_b0=subtract_b0, gate_kind=_GATES[gate_kind], ramp_lambda=ramp_lambda, tau=tau,
-                     need_coeff_grads=need_coeff_grads, pair_bias=pair_bias, need_pair_grad=need_pair_grad)
+                     need_coeff_grads=need_coeff_grads, pair_bias=pair_bias, need_pair_grad=need_pair_grad, check=False)
     rest = tuple(_none(q.device) if g[n] is None else g[n] for n in _BWD_NAMES)
     return (g["dq"], g["dk"], g["dv"]) + rest
 
@@ -545,15 +545,18 @@ def _mlp_setup(ctx, inputs, output):
 
 def _wgrad(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
     """Weight and bias gradient of a linear layer (output gradient a, input b):
-    the split-row kernel for bf16, a plain product for other dtypes."""
-    if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16:
-        M = a.shape[-1]
-        Mp = 64 if M <= 64 else (128 if M <= 128 else 256)
-        if Mp != M:  # pad the output columns to a multiple the kernel takes
-            a = F.pad(a.reshape(-1, M), (0, Mp - M))
-        dw, db = linear_wgrad(a, b, True)
-        return dw[:M], db[:M]
-    a2, b2 = a.reshape(-1, a.shape[-1]), b.reshape(-1, b.shape[-1])
+    the split-row kernel where it takes the operands (bf16, the output columns
+    padded to 64, 128 or 256, a supported (M, N), rows a multiple of 64),
+    else the product autograd of F.linear computes (in the operands' dtype,
+    bf16 results rounded, as autograd rounds them)."""
+    M = a.shape[-1]
+    Mp = 64 if M <= 64 else (128 if M <= 128 else 256)
+    if a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and M <= 256:
+        ap = F.pad(a.reshape(-1, M), (0, Mp - M)) if Mp != M else a  # pad the output columns
+        if ops.linear_wgrad_takes(ap, b):
+            dw, db = linear_wgrad(ap, b, True)
+            return dw[:M], db[:M]
+    a2, b2 = a.reshape(-1, M), b.reshape(-1, b.shape[-1])
     return a2.t().matmul(b2).float(), a2.sum(0).float()
 
 
@@ -563,9 +566,10 @@ def _mlp_backward(ctx, gy):
     The forward's fused case with segments of a multiple of 128 rows runs
     two fused kernels (dq; the weight and bias gradients, recomputing z1, x1
     and dz1 per tile); other fused cases write x1 and dz1 for the split-row
-    weight-gradient kernel; the rest take the torch steps.  The weights'
-    gradients are those of their bf16 copies (rounded to bf16), in the
-    weights' dtype."""
+    weight-gradient kernel where it takes them (rows and segments a multiple
+    of 64), else for the product autograd computes; the rest take the torch
+    steps.  The weights' gradients are those of their bf16 copies (rounded to
+    bf16), in the weights' dtype."""
     if gy is None:
         return None, None, None, None, None
     q, w1, b1, w2, b2 = ctx.saved_tensors
@@ -578,7 +582,7 @@ def _mlp_backward(ctx, gy):
         return dq, dw1.to(w1.dtype), db1.to(b1.dtype), dw2.to(w2.dtype), db2.to(b2.dtype)
     if ops.coeff_mlp_fused(q, w1, w2):
         dq, dz1, x1, gyp = coeff_mlp_bwd(q, gy, w1, b1, w2, b2)
-        dw2, db2 = linear_wgrad(gyp, x1, True)
+        dw2, db2 = _wgrad(gyp, x1)  # gyp: gy padded to 64 columns with zeros
         dw2, db2 = dw2[:O], db2[:O]
         if not ctx.needs_input_grad[0]:
             dq = None

@@ -170,10 +170,14 @@ def pointer_select(ds_ptr: torch.Tensor, ds_local: torch.Tensor, *, bs: int, NB:
 def pointer_pair_bias(kv_num: torch.Tensor, kv_idx: torch.Tensor, picks: torch.Tensor, *, bs: int, window: int,
                       n_global: int, soft_temp: float, qbar: torch.Tensor | None = None,
                       kbar: torch.Tensor | None = None, logits_in: torch.Tensor | None = None,
-                      prior: torch.Tensor | None = None, logit_scale: float = 1.0) -> torch.Tensor:
+                      prior: torch.Tensor | None = None, logit_scale: float = 1.0,
+                      check: bool = True) -> torch.Tensor:
     """Soft pointer weights as a per-list-entry score bias [H,QB,L] (log σ(z/τ_w)
-    on the pick entries, 0 elsewhere), aligned with kv_idx."""
+    on the pick entries, 0 elsewhere), aligned with kv_idx.  ``check``:
+    validate the lists first (``check_lists``)."""
     dev = _gpu("pointer_pair_bias", kv_num, kv_idx, picks, qbar, kbar, logits_in, prior)
+    if check:
+        check_lists(kv_num, kv_idx, kv_num.shape[-1], who="pointer_pair_bias")
     H, NB = kv_num.shape[-2], kv_num.shape[-1]
     L = kv_idx.shape[-1]
     budget = picks.shape[-1]
@@ -195,12 +199,16 @@ def pointer_pair_bias(kv_num: torch.Tensor, kv_idx: torch.Tensor, picks: torch.T
 
 def pointer_bwd(qbar: torch.Tensor, kbar: torch.Tensor, kv_num: torch.Tensor, kv_idx: torch.Tensor,
                 q_off: torch.Tensor, q_list: torch.Tensor, pair_bias: torch.Tensor, dpair_bias: torch.Tensor,
-                dq: torch.Tensor, dk: torch.Tensor, *, bs: int, logit_scale: float, soft_temp: float) -> None:
+                dq: torch.Tensor, dk: torch.Tensor, *, bs: int, logit_scale: float, soft_temp: float,
+                check: bool = True) -> None:
     """Add the soft pointer weights' gradient path (through the block means)
-    to dq and dk [1,H,T,D] bf16 in place."""
+    to dq and dk [1,H,T,D] bf16 in place.  ``check``: validate kv_num /
+    kv_idx first (``check_lists``); q_off / q_list must be their transpose."""
     from ._lib import PtrBwdParams
 
     dev = _gpu("pointer_bwd", qbar, kbar, kv_num, kv_idx, q_off, q_list, pair_bias, dpair_bias, dq, dk)
+    if check:
+        check_lists(kv_num, kv_idx, qbar.shape[1], who="pointer_bwd")
     H, NB, D = qbar.shape
     L = kv_idx.shape[-1]
     _, _, _, qsh, qst = _bhtd("pointer_bwd dq", dq)
@@ -214,10 +222,62 @@ def pointer_bwd(qbar: torch.Tensor, kbar: torch.Tensor, kv_num: torch.Tensor, kv
          _p(_f32(dpair_bias)), _p(dq), _p(dk), _p(ws), _stream(dev))
 
 
-def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int, tail: int | None = None):
+def _check_lists_host(kn: torch.Tensor, ki: torch.Tensor, NB: int, causal: bool) -> list[int]:
+    """The counters of scope_check_lists, in torch on the host."""
+    H, QB, maxkv = ki.shape
+    kn, ki = kn.long(), ki.long()
+    bad_num = (kn < 0) | (kn > maxkv)
+    e = torch.arange(maxkv)
+    used = (e[None, None] < kn[..., None]) & ~bad_num[..., None]
+    oor = used & ((ki < 0) | (ki >= NB))
+    late = used & ~oor & (ki > torch.arange(QB)[None, :, None]) if causal else torch.zeros_like(used)
+    ok = used & ~oor & ~late
+    srt = torch.where(ok, ki, NB + e).sort(dim=-1).values  # unused slots get distinct values >= NB
+    dup = ((srt[..., 1:] == srt[..., :-1]) & (srt[..., 1:] < NB)).sum(-1)
+    row_bad = (bad_num | oor.any(-1) | late.any(-1) | (dup > 0)).flatten()
+    first = int(torch.nonzero(row_bad)[0, 0]) if bool(row_bad.any()) else 2 ** 31 - 1
+    return [int(bad_num.sum()), int(oor.sum()), int(late.sum()), int(dup.sum()), first]
+
+
+def check_lists(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int, *, causal: bool = True,
+                who: str = "check_lists") -> None:
+    """Raise ``RuntimeError`` unless every row (h, qb) of the compact lists
+    kv_num [.., H, QB] / kv_idx [.., H, QB, MAXKV] holds 0 <= kv_num <= MAXKV
+    distinct key blocks in [0, NB), each <= qb when ``causal`` — what the
+    reference's pack guarantees (model/attn_bias.py:825-837) and every kernel
+    here relies on.  GPU tensors: ``scope_check_lists`` and a host read of its
+    counters (skipped under graph capture, where nothing may synchronise);
+    CPU tensors: the same rules in torch."""
+    H, QB = int(kv_num.shape[-2]), int(kv_num.shape[-1])
+    maxkv = int(kv_idx.shape[-1])
+    if kv_num.numel() != H * QB or kv_idx.numel() != H * QB * maxkv:
+        raise RuntimeError(f"{who}: kv_num {tuple(kv_num.shape)} and kv_indices {tuple(kv_idx.shape)} do not match")
+    if kv_num.is_cuda or kv_idx.is_cuda:
+        dev = _gpu(who, kv_num, kv_idx)
+        if torch.cuda.is_current_stream_capturing():
+            return
+        res = torch.empty(5, dtype=torch.int32, device=dev)
+        call("scope_check_lists", _p(_i32(kv_num.reshape(H, QB))), _p(_i32(kv_idx.reshape(H, QB, maxkv))), H, QB,
+             int(NB), maxkv, int(bool(causal)), _p(res), _stream(dev))
+        r = res.tolist()
+    else:
+        r = _check_lists_host(kv_num.reshape(H, QB), kv_idx.reshape(H, QB, maxkv), int(NB), bool(causal))
+    if any(r[:4]):
+        h, qb = divmod(int(r[4]), QB)
+        raise RuntimeError(f"{who}: malformed block lists: {r[0]} rows with kv_num outside [0, {maxkv}], {r[1]} "
+                           f"entries outside [0, {NB}), {r[2]} entries after their q-block, {r[3]} repeated "
+                           f"entries (first bad row: head {h}, q-block {qb})")
+
+
+def transpose_blocks(kv_num: torch.Tensor, kv_idx: torch.Tensor, NB: int, tail: int | None = None, *,
+                     check: bool = True):
     """q lists (CSR): q_off [H, NB+1], q_list [H, QB*MAXKV].  Entries of a
-    head's q_list past q_off[h, NB] are -1 (the kernels set them), or ``tail``."""
+    head's q_list past q_off[h, NB] are -1 (the kernels set them), or ``tail``.
+    ``check``: validate the lists first (``check_lists``, one host read);
+    the library's own callers pass lists its builders made and skip it."""
     dev = _gpu("transpose_blocks", kv_num, kv_idx)
+    if check:
+        check_lists(kv_num, kv_idx, NB, who="transpose_blocks")
     kv_num = _i32(kv_num.reshape(kv_num.shape[-2], kv_num.shape[-1]))
     H, QB = kv_num.shape
     kv_idx = _i32(kv_idx.reshape(H, QB, kv_idx.shape[-1]))
@@ -320,6 +380,25 @@ def _row_layout(x: torch.Tensor):
     return None
 
 
+WGRAD_SHAPES = {(64, 128), (64, 256), (128, 128), (128, 256), (256, 64), (256, 128)}
+
+
+def linear_wgrad_takes(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Whether ``linear_wgrad`` takes a [..., M] and b [..., N] as they are:
+    bf16, (M, N) one of WGRAD_SHAPES, and rows (and every segment of rows of
+    a strided operand) a multiple of 64 (scope_linear_wgrad's limits)."""
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or (a.shape[-1], b.shape[-1]) not in WGRAD_SHAPES:
+        return False
+    rows = a.numel() // max(1, a.shape[-1])
+    if rows == 0 or rows % 64 or b.numel() // max(1, b.shape[-1]) != rows:
+        return False
+    for x in (a, b):
+        lx = _row_layout(x)
+        if lx is not None and (lx[1] % 64 or lx[3] % 8 or (lx[1] != lx[0] and lx[2] % 8) or x.data_ptr() % 16):
+            return False
+    return True
+
+
 def linear_wgrad(a: torch.Tensor, b: torch.Tensor, *, round_bf16: bool = True, want_db: bool = True):
     """dw [M, N] = Σ_r a[r]^T b[r] and db [M] = Σ_r a[r] over the rows of a
     [..., M] and b [..., N] (bf16, the same rows): the weight and bias
@@ -332,11 +411,11 @@ def linear_wgrad(a: torch.Tensor, b: torch.Tensor, *, round_bf16: bool = True, w
         raise RuntimeError("linear_wgrad: a and b must be bf16")
     M, N = a.shape[-1], b.shape[-1]
     la, lb = _row_layout(a), _row_layout(b)
-    if la is None:
-        a = a.contiguous()
+    if la is None:  # copied to one segment of rows
+        a = a.contiguous().reshape(-1, M)
         la = _row_layout(a)
     if lb is None:
-        b = b.contiguous()
+        b = b.contiguous().reshape(-1, N)
         lb = _row_layout(b)
     if la[0] != lb[0]:
         raise RuntimeError(f"linear_wgrad: {la[0]} rows of a against {lb[0]} rows of b")
@@ -364,8 +443,8 @@ def linear_wgrad(a: torch.Tensor, b: torch.Tensor, *, round_bf16: bool = True, w
 
 def _mlp_params(q: torch.Tensor, w2: torch.Tensor):
     lq = _row_layout(q)
-    if lq is None:
-        q = q.contiguous()
+    if lq is None:  # e.g. [B, H, L, D] with B > 1: copied to one segment of rows
+        q = q.contiguous().reshape(-1, q.shape[-1])
         lq = _row_layout(q)
     rows, seg, ss, rs = lq
     if seg == rows:
@@ -599,11 +678,13 @@ def empty_like_layout(x: torch.Tensor) -> torch.Tensor:
 def attn_fwd(q, k, v, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float, beta: float = 0.5,
              bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None, slope=None,
              delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
-             ramp_lambda=0.0, tau=64.0, out=None, pair_bias=None):
+             ramp_lambda=0.0, tau=64.0, out=None, pair_bias=None, check: bool = True):
     """Block-sparse attention forward -> (out like q, lse [1,H,T] fp32, natural log).
     ``pair_bias`` [H,QB,MAXKV] (aligned with kv_idx) is added to every score of
-    each listed tile."""
+    each listed tile.  ``check``: validate the lists first (``check_lists``)."""
     dev = _gpu("attn_fwd", q, k, v, kv_num, kv_idx, docs, ds_tok_end, pair_bias)
+    if check:
+        check_lists(kv_num, kv_idx, q.shape[-2] // bs, who="attn_fwd")
     out = empty_like_layout(q) if out is None else out
     kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
     m = BIAS_MODES[bias_mode]
@@ -624,10 +705,13 @@ def attn_fwd(q, k, v, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float
 def attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: float, beta: float = 0.5,
                     bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None, slope=None,
                     delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
-                    ramp_lambda=0.0, tau=64.0):
+                    ramp_lambda=0.0, tau=64.0, check: bool = True):
     """Attention probability mass per (head, q-block, listed key block),
-    summed over the q-block's rows -> (mass [H, QB, NB] fp32, lse [1,H,T])."""
+    summed over the q-block's rows -> (mass [H, QB, NB] fp32, lse [1,H,T]).
+    ``check``: validate the lists first (``check_lists``)."""
     dev = _gpu("attn_block_mass", q, k, kv_num, kv_idx, docs, ds_tok_end)
+    if check:
+        check_lists(kv_num, kv_idx, q.shape[-2] // bs, who="attn_block_mass")
     kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
     m = BIAS_MODES[bias_mode]
     K = coeff_cos.shape[-1] if (m and coeff_cos is not None) else 0
@@ -646,15 +730,19 @@ def attn_block_mass(q, k, kv_num, kv_idx, docs, ds_tok_end, *, bs: int, scale: f
 
 def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_num: torch.Tensor,
                 kv_idx: torch.Tensor, docs: torch.Tensor, t: int | torch.Tensor, *, bs: int, scale: float,
-                workspace: torch.Tensor | None = None):
+                workspace: torch.Tensor | None = None, check: bool = True):
     """Attention of the token at position t: q [H, D] bf16 against the cache
     k_cache / v_cache [H, T_cap, D] over the listed blocks kv_idx [H, maxkv]
     (kv_num [H]) -> (out [H, D] bf16, lse [H] natural log).  ``t`` is an int,
     or a one-element int64 tensor on the device that the kernel reads (no host
-    sync; what a captured decode step needs)."""
+    sync; what a captured decode step needs).  ``check``: validate the list
+    first (distinct blocks of the cache; ``check_lists``, skipped under capture)."""
     from ._lib import DecodeParams
 
     dev = _gpu("decode_attn", q, k_cache, v_cache, kv_num, kv_idx, docs)
+    if check:
+        check_lists(kv_num.reshape(-1, 1), kv_idx.reshape(kv_idx.shape[0], 1, -1), k_cache.shape[1] // bs,
+                    causal=False, who="decode_attn")
     if q.dim() != 2 or k_cache.dim() != 3 or v_cache.dim() != 3:
         raise RuntimeError("decode_attn: q [H, D], caches [H, T_cap, D]")
     for n_, x in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
@@ -688,14 +776,17 @@ def decode_attn_glue(qkv: torch.Tensor, ve: torch.Tensor | None, t_dev: torch.Te
                      sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_num: torch.Tensor,
                      kv_idx: torch.Tensor, docs: torch.Tensor, *, heads: int, va: float, vb: float, bs: int,
                      scale: float, workspace: torch.Tensor | None = None, eps: float | None = None,
-                     want_q: bool = False):
+                     want_q: bool = False, check: bool = True):
     """``decoder_qkv_glue`` of one token (qkv [3·heads·D] bf16) fused into
     ``decode_attn`` at the device position t_dev: k and v go to cache row t
     and the attention uses them.  Returns (out [heads, D] bf16, lse [heads],
-    q [heads, D] bf16 or None)."""
+    q [heads, D] bf16 or None).  ``check`` as in ``decode_attn``."""
     from ._lib import DecodeParams
 
     dev = _gpu("decode_attn_glue", qkv, ve, t_dev, cos, sin, k_cache, v_cache, kv_num, kv_idx, docs)
+    if check:
+        check_lists(kv_num.reshape(-1, 1), kv_idx.reshape(kv_idx.shape[0], 1, -1), k_cache.shape[1] // bs,
+                    causal=False, who="decode_attn_glue")
     D = k_cache.shape[-1]
     if qkv.dtype != torch.bfloat16 or not qkv.is_contiguous() or qkv.numel() != 3 * heads * D:
         raise RuntimeError("decode_attn_glue: qkv must be a contiguous bfloat16 [3*heads*D]")
@@ -847,13 +938,16 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
              beta: float = 0.5, bias_mode: str = "none", table=None, coeff_cos=None, coeff_sin=None, b0=None,
              slope=None, delta_main=None, width=None, use_slope=False, subtract_b0=False, gate_kind="none",
              ramp_lambda=0.0, tau=64.0, need_coeff_grads: bool = True, phase_hook=None, pair_bias=None,
-             need_pair_grad: bool = False):
+             need_pair_grad: bool = False, check: bool = True):
     """Block-sparse attention backward -> dict of gradients.  With
     ``phase_hook`` the phases (q-major dQ pass; kv-major plan, dK/dV kernel
     and reduce) are launched separately and the hook is called before, between
     and after them with the phase name ("dq", "plan", "dkv", "reduce", "end")
-    (used for per-kernel timing)."""
+    (used for per-kernel timing).  ``check``: validate kv_num / kv_idx first
+    (``check_lists``); q_off / q_list must be their transpose."""
     dev = _gpu("attn_bwd", q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list)
+    if check:
+        check_lists(kv_num, kv_idx, q.shape[-2] // bs, who="attn_bwd")
     kv_idx3 = _i32(kv_idx.reshape(-1, kv_idx.shape[-2], kv_idx.shape[-1]))
     m = BIAS_MODES[bias_mode]
     K = coeff_cos.shape[-1] if (m and coeff_cos is not None) else 0

@@ -34,6 +34,53 @@ TOKEN_EDGES = [0, 127, 255, 511, 1023, 2047, 4095, 8191, 16383, 32767, 65535, 13
 BLOCK_EDGES = [0, 1, 3, 7, 15, 31, 63, 127, 255, 511, 1023, 2047, 4095, 8191]
 
 
+class _PerHeadMLP(torch.autograd.Function):
+    """The per-head MLP of ``share_across_heads=False`` (model/attn_bias.py:387-398):
+    y[b,h,l] = W2[h]·SiLU(W1[h]·q[b,h,l] + b1[h]) + b2[h] in q's dtype, the
+    weights cast to it, as the reference's two einsums.  Every batched
+    product here takes contiguous operands (weights transposed once and
+    copied, rows of every head gathered), forward and backward, so no batched
+    bf16 product sees a transposed view.  The weights' gradients are those
+    of their cast copies, in the weights' dtype, as autograd through the
+    reference's ``.to(dt)`` gives them."""
+
+    @staticmethod
+    def _hidden(q, w1, b1):
+        dt = q.dtype
+        w1t = w1.to(dt).transpose(1, 2).contiguous()  # [H, D, K]
+        z = torch.matmul(q.contiguous(), w1t[None]) + b1.to(dt)[None, :, None, :]
+        return z, F.silu(z)
+
+    @staticmethod
+    def forward(ctx, q, w1, b1, w2, b2):
+        dt = q.dtype
+        _, x = _PerHeadMLP._hidden(q, w1, b1)
+        w2t = w2.to(dt).transpose(1, 2).contiguous()  # [H, K, O]
+        ctx.save_for_backward(q, w1, b1, w2, b2)
+        return torch.matmul(x, w2t[None]) + b2.to(dt)[None, :, None, :]
+
+    @staticmethod
+    def backward(ctx, gy):
+        q, w1, b1, w2, b2 = ctx.saved_tensors
+        dt = q.dtype
+        B, H, L, D = q.shape
+        gy = gy.to(dt).contiguous()
+        z, x = _PerHeadMLP._hidden(q, w1, b1)
+        dz = torch.ops.aten.silu_backward(torch.matmul(gy, w2.to(dt).contiguous()[None]), z)
+        dq = torch.matmul(dz, w1.to(dt).contiguous()[None]) if ctx.needs_input_grad[0] else None
+
+        def rows_t(t):  # [B, H, L, C] -> [H, C, B·L]
+            return t.permute(1, 3, 0, 2).reshape(H, t.shape[-1], B * L).contiguous()
+
+        def rows(t):  # [B, H, L, C] -> [H, B·L, C]
+            return t.permute(1, 0, 2, 3).reshape(H, B * L, t.shape[-1]).contiguous()
+
+        dw1 = torch.bmm(rows_t(dz), rows(q))
+        dw2 = torch.bmm(rows_t(gy), rows(x))
+        db1, db2 = dz.sum(dim=(0, 2)), gy.sum(dim=(0, 2))
+        return dq, dw1.to(w1.dtype), db1.to(b1.dtype), dw2.to(w2.dtype), db2.to(b2.dtype)
+
+
 class SpectralBias(nn.Module):
     """Query-conditioned Fourier bias over Δ = q_idx - kv_idx plus the
     pointer-driven block mask (model/attn_bias.py:68-73)."""
@@ -237,9 +284,7 @@ class SpectralBias(nn.Module):
             fc1: nn.Linear = self.mlp[0]
             fc2: nn.Linear = self.mlp[2]
             return library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias)
-        x = torch.einsum("bhld,hkd->bhlk", q, self.w1.to(dt)) + self.b1.to(dt)[None, :, None, :]
-        x = F.silu(x)
-        return torch.einsum("bhlk,hok->bhlo", x, self.w2.to(dt)) + self.b2.to(dt)[None, :, None, :]
+        return _PerHeadMLP.apply(q, self.w1, self.b1, self.w2, self.b2)
 
     def _get_trig_tables(self, L: int, device: torch.device):
         key = (L, device)
@@ -396,7 +441,7 @@ class SpectralBias(nn.Module):
             self._dbg_ptr_radius0_frac.copy_(values[5])
         return ScopeBlockMask(kv_num_blocks=kv_num[None], kv_indices=kv_idx[None], BLOCK_SIZE=block_size,
                               docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local,
-                              extras=dict(radius=radius, centre=centre))
+                              extras=dict(radius=radius, centre=centre), check=False)
 
     # ---- pointer mask, block-scoring mode
     @torch.no_grad()
@@ -436,7 +481,8 @@ class SpectralBias(nn.Module):
         if return_logits:
             extras["logits"] = lg
         bm = ScopeBlockMask(kv_num_blocks=kv_num[None], kv_indices=kv_idx[None], BLOCK_SIZE=block_size,
-                            docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local, extras=extras)
+                            docs=docs32, ds_tok_end=ds_tok_end, ds_ptr=ds_ptr, ds_local=ds_local, extras=extras,
+                            check=False)
         if soft_temp is not None and soft_temp > 0 and budget_blocks > 0:
             if logits is None:
                 from .attention import soft_pointer_bias
