@@ -222,3 +222,67 @@ def test_coeff_mlp_fp32_takes_the_torch_steps():
     assert not ops.coeff_mlp_fused(q, fc1.weight, fc2.weight)
     y = library.coeff_mlp(q, fc1.weight, fc1.bias, fc2.weight, fc2.bias)
     assert torch.equal(y, mlp_forward(sb, q))
+
+
+def _mlp_run(fn, q0, params, gy):
+    q = q0.detach().clone().requires_grad_()
+    for p_ in params:
+        p_.grad = None
+    y = fn(q)
+    y.backward(gy)
+    if q.is_cuda:
+        torch.cuda.synchronize()
+    return [y.detach(), q.grad] + [p_.grad.clone() for p_ in params]
+
+
+@pytest.mark.parametrize("case", ["bf16_L96", "bf16_D64", "bf16_B2", "fp32", "per_head_bf16", "per_head_fp32"])
+def test_coeff_mlp_other_shapes_vs_fp64(case):
+    """The shapes the fused weight-gradient kernel does not take: segments of
+    96 rows (fused forward and row-wise backward, the weight gradients on the
+    torch product), head_dim 64 (torch steps; the split-row kernel for the
+    second layer's weights), batch 2 (copied to one segment of rows), fp32
+    rows, and per-head weights (share_across_heads=False, in bf16 and fp32).
+    Output, dq and the four weight and bias gradients against fp64 on the
+    CPU from the same operands (weights rounded to q's dtype): at least as
+    close as the reference's torch steps run on the CPU in q's dtype (1.5x
+    their error, max and mean, plus 1e-6 of the largest value)."""
+    import copy
+
+    B, H, L, D, dt, shared = {"bf16_L96": (1, 8, 96, 128, torch.bfloat16, True),
+                              "bf16_D64": (1, 8, 256, 64, torch.bfloat16, True),
+                              "bf16_B2": (2, 4, 256, 128, torch.bfloat16, True),
+                              "fp32": (1, 4, 256, 128, torch.float32, True),
+                              "per_head_bf16": (1, 4, 256, 128, torch.bfloat16, False),
+                              "per_head_fp32": (1, 4, 256, 128, torch.float32, False)}[case]
+    sb = SpectralBias(head_dim=D, num_heads=H, L_train=L, K=6, M=8, share_across_heads=shared).to(DEV).train()
+    g = torch.Generator().manual_seed(11)
+    with torch.no_grad():
+        for p_ in sb.parameters():
+            if p_.requires_grad and p_.dim() >= 1 and p_.numel() > 8:
+                p_.copy_((torch.randn(p_.shape, generator=g) * 0.05).to(DEV))
+    params = list(sb.mlp.parameters()) if shared else [sb.w1, sb.b1, sb.w2, sb.b2]
+    q0 = torch.randn((B, H, L, D), generator=g).to(dt)
+    O = 5 * 8 + (1 if sb.use_slope else 0)
+    gy = torch.randn((B, H, L, O), generator=g).to(dt)
+    if shared and dt == torch.bfloat16:
+        fc1, fc2 = sb.mlp[0], sb.mlp[2]
+        fused = ops.coeff_mlp_fused(q0.to(DEV), fc1.weight, fc2.weight)
+        assert fused == (D == 128), case
+        assert not (fused and ops.coeff_mlp_wgrad_fused(q0.to(DEV))), case  # the fused weight gradients do not run
+    got = _mlp_run(lambda q: sb._mlp_forward(q), q0.to(DEV), params, gy.to(DEV))
+    sb_cpu = copy.deepcopy(sb).cpu()
+    params_cpu = list(sb_cpu.mlp.parameters()) if shared else [sb_cpu.w1, sb_cpu.b1, sb_cpu.w2, sb_cpu.b2]
+    ref = _mlp_run(lambda q: mlp_forward(sb_cpu, q), q0, params_cpu, gy)
+    sb64 = copy.deepcopy(sb_cpu).double()
+    with torch.no_grad():
+        for p_, p32 in zip(sb64.mlp.parameters() if shared else [sb64.w1, sb64.b1, sb64.w2, sb64.b2], params_cpu):
+            p_.copy_(p32.to(dt).double())
+    params64 = list(sb64.mlp.parameters()) if shared else [sb64.w1, sb64.b1, sb64.w2, sb64.b2]
+    exact = _mlp_run(lambda q: mlp_forward(sb64, q), q0.double(), params64, gy.double())
+    for name, a, r, ex in zip(("y", "dq", "dw1", "db1", "dw2", "db2"), got, ref, exact):
+        assert a.shape == ex.shape and a.dtype == r.dtype, name
+        e_got, e_ref = (a.double().cpu() - ex).abs(), (r.double() - ex).abs()
+        floor = 1e-6 * float(ex.abs().max())
+        print(f"  {case} {name}: max err {float(e_got.max()):.3g} (torch steps {float(e_ref.max()):.3g})", flush=True)
+        assert float(e_got.max()) <= 1.5 * float(e_ref.max()) + floor, name
+        assert float(e_got.mean()) <= 1.5 * float(e_ref.mean()) + floor, name

@@ -62,3 +62,36 @@ def test_transpose_noalloc_rejects_sizes_beyond_the_static_scratch():
         ops.transpose_blocks_noalloc(kv_num, kv_idx, q_off, q_list)
     torch.cuda.synchronize()
     assert bool((q_off == 0).all())
+
+
+def test_transpose_noalloc_replayed_from_a_captured_graph():
+    """Captured once in a HIP graph (torch.cuda.CUDAGraph) after one eager
+    call, then replayed three times with new lists copied into the captured
+    inputs and the outputs overwritten by eager work between the replays:
+    every replay equals scope_transpose_blocks on those lists, bit for bit."""
+    from scope_amd import ops
+
+    H, T, bs, W, G, B = 4, 65536, 128, 2, 1, 4
+    NB = T // bs
+    kv_num, kv_idx = _lists(H, T, bs, W, G, B, 3, seed=100)
+    q_off = torch.zeros((H, NB + 1), dtype=torch.int32, device=DEV)
+    q_list = torch.zeros((H, NB * kv_idx.shape[-1]), dtype=torch.int32, device=DEV)
+    ops.transpose_blocks_noalloc(kv_num, kv_idx, q_off, q_list)  # eager: the scratch address is looked up here
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.transpose_blocks_noalloc(kv_num, kv_idx, q_off, q_list)
+    torch.cuda.synchronize()
+    for seed in (101, 102, 103):
+        print(f"graph replay with lists of seed {seed}", flush=True)
+        kn, ki = _lists(H, T, bs, W, G, B, 1 + seed % 5, seed=seed)
+        kv_num.copy_(kn)
+        kv_idx.copy_(ki)
+        q_off.fill_(-7)
+        q_list.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want_off, want_list = ops.transpose_blocks(kn, ki, NB)
+        assert torch.equal(q_off, want_off)
+        assert torch.equal(q_list, want_list)
