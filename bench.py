@@ -52,6 +52,14 @@ lists with local 8, half 4, M 8, budget 64 in total, temperature 0.5): the
 coefficient head, the reference-mode mask, the attention and the whole
 backward; ``--T 65536`` for the training shape.
 
+The default line also carries, timed after the headline with their own
+events: ``reference_default_layer`` (the ``--workload ref`` figures below at
+T=16384), and in ``cpu_baseline`` the oracle's attention on a bounded sample,
+the reference's own CPU path at config 1, and ``pointer_and_stats``: the
+oracle's block-scoring selection and mask statistics (kernels 1 and 3) on the
+host at config 1 and at this workload, beside the GPU time of the same two
+phases.
+
 ``--workload decode`` runs the 16-layer decoder (d_model 1024, 8 heads of
 128, MLP 4096 ReLU², vocabulary 50304, bf16, random weights): a prefill of
 131072 seeded uniform-random tokens, then 256 greedy decode steps with the
@@ -558,19 +566,24 @@ def main_decode(args):
 
 
 def main_ref(args):
+    """The reference's default layer path as its own bench line (see ref_layer)."""
+    print(json.dumps(ref_layer(args.H, args.T if args.T != 131072 else 16384, args.steps, args.warmup)))
+
+
+def ref_layer(H: int, T: int, steps: int, warmup: int) -> dict:
     """The reference's default layer path (scoped_medium.py:334-466 with the
     defaults of :692-727): SpectralBias.forward (MLP + coefficient head, K=6
     bands, M=8 peaks), build_pointer_blockmask in reference mode (local 8,
     half 4, budget 64 in total, temperature 0.5, "pi" radii, no global
     blocks), the attention with the qk_aug terms (token offsets, slope, no
     gate) and the whole backward, through scope_attention / SpectralBias as
-    the reference would call them."""
+    the reference would call them.  Timed with events around `steps`
+    back-to-back steps after `warmup`."""
     import torch
 
     from scope_amd import SpectralBias, SpectralTerms, scope_attention
 
-    H, D, bs = args.H, 128, 128
-    T = args.T if args.T != 131072 else 16384
+    D, bs = 128, 128
     inp = make_inputs(H, T, D, bs, needle=False)
     q, k, v, dout, docs = (inp[n].cuda() for n in ("q", "k", "v", "dout", "docs"))
     sb = SpectralBias(head_dim=D, num_heads=H, L_train=4096, K=6, M=8, use_pointer_mask=True,
@@ -604,7 +617,7 @@ def main_ref(args):
         _, _, bm = layer(q, k, v)
     n_act = int(bm.kv_num_blocks.sum())
     maxkv = bm.maxkv
-    t_step = time_region(step, args.steps, args.warmup)
+    t_step = time_region(step, steps, warmup)
     # the attention alone on the same lists and terms
     qd, kd, vd = (x.detach().requires_grad_() for x in (q, k, v))
     with torch.no_grad():
@@ -621,9 +634,9 @@ def main_ref(args):
         y = scope_attention(qd, kd, vd, block_mask=bm, scale=0.12, spectral=sp)
         y.backward(dout)
 
-    t_fwd = time_region(attn_fwd_only, args.steps, args.warmup)
-    t_attn = time_region(attn_fwd_bwd, args.steps, args.warmup)
-    graph = graph_step_time(layer, q, k, v, dout, one, args.steps, params)
+    t_fwd = time_region(attn_fwd_only, steps, warmup)
+    t_attn = time_region(attn_fwd_bwd, steps, warmup)
+    graph = graph_step_time(layer, q, k, v, dout, one, steps, params)
     F_fwd, F_bwd = 4.0 * bs * bs * D * n_act, 10.0 * bs * bs * D * n_act
     res = {
         "metric": "SCOPE layer fwd+bwd on the reference's default path (qk_aug terms, reference-mode lists) "
@@ -631,8 +644,8 @@ def main_ref(args):
         "value": round((F_fwd + F_bwd) / t_step / 1e12, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(t_step * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
@@ -659,7 +672,7 @@ def main_ref(args):
                          achieved=round((F_fwd + F_bwd) / t_attn / 1e12, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                          frac=round((F_fwd + F_bwd) / t_attn / 1e12 / PEAK_BF16_TFLOPS, 4), traffic=None),
     }
-    print(json.dumps(res))
+    return res
 
 
 def graph_step_time(layer, q, k, v, dout, one, steps: int, params=()) -> dict:
@@ -794,6 +807,82 @@ def cpu_baseline(inp, step, seconds: float, bs: int):
                 sample=f"oracle block-sparse attention fwd+bwd (torch fp32 on CPU) for {n_rows} (head, q-block) "
                        f"rows of the same mask ({done_tiles} active {bs}x{bs} tiles, {t_used:.1f} s)",
                 seconds=round(t_used, 2), cpu_count=os.cpu_count(), cpu_model=cpu_model())
+
+
+def cpu_pointer_stats(configs, seconds: float) -> dict:
+    """Kernels 1 and 3 on the host: the oracle's block-scoring selection
+    (block means, logits bs/√D·q̄·k̄ + radius prior, counter Gumbel noise,
+    top-budget picks, union and pack; oracle/pointer.py) and its mask
+    statistics (oracle/stats.py:blockscore_stats), numpy on the host cores,
+    repeated until `seconds` per config are used; beside them the GPU time of
+    the same two phases on the same inputs (doc starts + block means +
+    selection; the statistics kernel), events around `reps` launches.
+    configs: (name, inputs, bs, window, n_global, budget)."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_info
+
+    from oracle import pointer as OP
+    from oracle import stats as OS
+    from scope_amd import ops
+
+    out = {}
+    for name, inp, bs, W, G, B in configs:
+        q, k, docs = inp["q"][0].float().numpy(), inp["k"][0].float().numpy(), inp["docs"].numpy()
+        H, T, D = q.shape
+        NB = T // bs
+        prior = radius_prior(NB, PRIOR_SCALE)
+        hh, qq, kk = np.meshgrid(np.arange(H), np.arange(NB), np.arange(NB), indexing="ij")
+
+        def kernel1():
+            lg = OP.pointer_logits(OP.block_means(q, bs), OP.block_means(k, bs), logit_scale=bs / math.sqrt(D),
+                                   prior=prior.double().numpy()).astype(np.float32)
+            g = OP.gumbel_from_u(OP.counter_uniform(1234, hh, qq, kk))
+            return OP.pointer_select_blockscore(lg, docs, bs=bs, window=W, n_global=G, budget=B, gumbel=g)
+
+        n1 = n3 = 0
+        t1 = t3 = 0.0
+        while t1 + t3 < seconds:
+            t0 = time.perf_counter()
+            sel = kernel1()
+            t1 += time.perf_counter() - t0
+            n1 += 1
+            t0 = time.perf_counter()
+            OS.blockscore_stats(sel["kv_num"], sel["picks"], sel["ds_ptr"], sel["ds_local"], maxkv=sel["maxkv"],
+                                local_blocks=W)
+            t3 += time.perf_counter() - t0
+            n3 += 1
+        gq, gk, gd = (inp[n].cuda() for n in ("q", "k", "docs"))
+        gprior = prior.cuda()
+        res = {}
+
+        def gpu_k1():
+            ds_ptr, ds_local, _ = ops.doc_starts(gd, bs)
+            qbar, kbar = ops.block_means(gq, gk, bs)
+            res["sel"] = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=NB, H=H, window=W, n_global=G, budget=B,
+                                            qbar=qbar, kbar=kbar, prior=gprior, temp=1.0,
+                                            logit_scale=bs / math.sqrt(D), noise="counter", seed=1234)
+            res["ds"] = (ds_ptr, ds_local)
+
+        gpu_k1()
+        kv_num, kv_idx, picks = res["sel"]
+        ds_ptr, ds_local = res["ds"]
+
+        def gpu_k3():
+            ops.mask_stats(H=H, QB=NB, bs=bs, kv_num=kv_num, picks=picks, ds_ptr=ds_ptr, ds_local=ds_local,
+                           maxkv_bins=kv_idx.shape[-1] + 1, bs_local_blocks=W)
+
+        g1 = time_region(gpu_k1, 20, 3)
+        g3 = time_region(gpu_k3, 20, 3)
+        out[name] = dict(H=H, T=T, block=bs, window=W, n_global=G, budget=B,
+                         cpu_select_ms=round(t1 / n1 * 1e3, 3), cpu_stats_ms=round(t3 / n3 * 1e3, 3),
+                         cpu_calls=n1, cpu_seconds=round(t1 + t3, 2),
+                         gpu_select_ms=round(g1 * 1e3, 4), gpu_stats_ms=round(g3 * 1e3, 4),
+                         select_speedup=round(t1 / n1 / g1, 1), stats_speedup=round(t3 / n3 / g3, 1))
+    blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+    return dict(kind="port", unit="ms per call", configs=out, cores=blas[0] if blas else 1,
+                cores_note="numpy: the logit products on the BLAS threads, the rest on one thread",
+                cpu_count=os.cpu_count(), cpu_model=cpu_model())
 
 
 def c1_lists(inp, bs: int, window: int, n_global: int, budget: int, seed: int):
@@ -1055,10 +1144,20 @@ def main():
     roofline["frac_of_measured"] = round(achieved / mp["mfma_bf16_tflops"], 4)
     pointer["peak_measured"] = mp["hbm_copy_gbs"]
     pointer["block_means_frac_of_measured"] = round(pointer["block_means_achieved"] / mp["hbm_copy_gbs"], 4)
+    if not train and (H, T, bs) == (8, 131072, 256):
+        # the reference's default layer (T=16384, bs 128, token offsets, reference-mode
+        # lists), timed after the headline with its own events and steps
+        res["reference_default_layer"] = ref_layer(8, 16384, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(inp, step, args.cpu_seconds, bs)
         if not train:
             res["cpu_baseline"]["reference_path_c1"] = cpu_reference_path_c1(args.cpu_seconds)
+            c1 = make_inputs(6, 4096, D, 128, n_docs=1, needle=False)
+            res["cpu_baseline"]["pointer_and_stats"] = cpu_pointer_stats(
+                [("config 1: H=6, T=4096, bs 128, window 3, global 1, budget 2", c1, 128, 3, 1, 2),
+                 (f"this workload: H={H}, T={T}, bs {bs}, window {args.window}, global {args.n_global}, "
+                  f"budget {args.budget}", inp, bs, args.window, args.n_global, args.budget)],
+                min(args.cpu_seconds, 10.0))
     if args.copy_probe_mib > 0:
         src = torch.ones(args.copy_probe_mib << 18, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
