@@ -215,9 +215,30 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     const int rd = min(max(qb - kb, 0), a.QB - 1);
     kv_issue<MODE, NT, PV>(a, h, static_cast<int64_t>(kb) * BS + (it % NSUB) * BN, rd, b, tid);
   };
+  // probabilities of one 32-key half mb of a tile's scores into pb[2mb], pb[2mb + 1]
+  auto probs_half = [&](const f32x16_t& sm, int mb, float csm, float off, uint4 (&pb)[4], float& psum)
+                        __attribute__((always_inline)) {
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        p[j] = __builtin_amdgcn_exp2f(fmaf(sm[hf * 8 + j], csm, off));
+        psum += p[j];
+      }
+      pb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
+                                   cvt_pk_bf16(p[6], p[7]));
+    }
+  };
+  // a tile cut between its two halves of probabilities (run_a with SPLIT):
+  // the second half's scores, its exponent offset and the partial row sum
+  f32x16_t sp_s1 = zero16();
+  float sp_off = 0.f, sp_csm = 0.f, sp_psum = 0.f;
   // one tile in two parts: scores and probabilities (P^T as bf16 B operands
-  // in pb; false when the wavefront has nothing to do), then O^T += V^T P^T
-  auto run_a = [&](int it, const Tile& b, uint4 (&pb)[4]) __attribute__((always_inline)) -> bool {
+  // in pb; false when the wavefront has nothing to do), then O^T += V^T P^T.
+  // With SPLIT the probabilities of the second 32-key half are left to run_a_rest.
+  auto run_a = [&](int it, const Tile& b, uint4 (&pb)[4], auto split) __attribute__((always_inline)) -> bool {
+    constexpr bool SPLIT = decltype(split)::value;
     const int kv0 = kb_at(it / NSUB) * BS + (it % NSUB) * BN;
     if (kv0 > wrow_lo + 31) return false;  // every key follows this wavefront's rows
     const bool full = (kv0 + BN - 1 <= wrow_lo) && (ds_end <= kv0);
@@ -310,22 +331,26 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
     const float off = m_run == -INFINITY ? -INFINITY : tconst - m_run;
 
     float psum = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        float p[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(fmaf(s[mb][hf * 8 + j], csm, off));
-          psum += p[j];
-        }
-        pb[mb * 2 + hf] = make_uint4(cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
-                                     cvt_pk_bf16(p[6], p[7]));
-      }
+    probs_half(s[0], 0, csm, off, pb, psum);
+    if constexpr (SPLIT) {
+      sp_s1 = s[1];
+      sp_off = off;
+      sp_csm = csm;
+      sp_psum = psum;
+      return PV;
+    }
+    probs_half(s[1], 1, csm, off, pb, psum);
     l_run += psum;
     return PV;
   };
+  // the second half of a tile that run_a left with SPLIT
+  auto run_a_rest = [&](uint4 (&pb)[4]) __attribute__((always_inline)) {
+    float psum = sp_psum;
+    probs_half(sp_s1, 1, sp_csm, sp_off, pb, psum);
+    l_run += psum;
+  };
+  using NoSplit = std::integral_constant<bool, false>;
+  using Split = std::integral_constant<bool, true>;
   auto run_b = [&](const Tile& b, const uint4 (&pb)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2)
@@ -334,7 +359,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
   };
   auto run = [&](int it, const Tile& b) __attribute__((always_inline)) {
     uint4 pb[4];
-    if (run_a(it, b, pb)) run_b(b, pb);
+    if (run_a(it, b, pb, NoSplit{})) run_b(b, pb);
   };
 
   __syncthreads();  // kbs
@@ -373,21 +398,31 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
       __syncthreads();  // matches the lagging group's last barrier
     } else {
+      // The lagging group's barrier falls between the two halves of a tile's
+      // probabilities: after the leading group's k-th barrier it finishes the
+      // probabilities of tile k-1 (VALU) while the leading group runs the
+      // scores of tile k (MFMA), runs P·V of tile k-1 and the scores of tile
+      // k (MFMA) under the leading group's probabilities, and starts the
+      // probabilities of tile k (VALU) under the leading group's P·V.
       __syncthreads();  // tile 0 is in buf0
       int cur = next_valid(0);
-      auto lag = [&](const Tile& bc) __attribute__((always_inline)) {
-        uint4 pb[4];
-        const bool act = run_a(cur, bc, pb);
-        __syncthreads();  // the leading group starts the next tile
-        if (act) run_b(bc, pb);
+      uint4 pb[4];
+      bool act = cur < total && run_a(cur, buf0, pb, Split{});
+      auto lag = [&](const Tile& bc, const Tile& bn) __attribute__((always_inline)) {
+        __syncthreads();  // the leading group starts the tile after cur
+        if (act) {
+          run_a_rest(pb);
+          run_b(bc, pb);
+        }
         cur = next_valid(cur + 1);
+        act = cur < total && run_a(cur, bn, pb, Split{});
       };
       while (cur < total) {
-        lag(buf0);
+        lag(buf0, buf1);
         if (cur >= total) break;
-        lag(buf1);
+        lag(buf1, buf2);
         if (cur >= total) break;
-        lag(buf2);
+        lag(buf2, buf0);
       }
     }
   } else {
