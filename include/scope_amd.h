@@ -115,6 +115,12 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
                          const int32_t* ds_ptr, const int32_t* ds_local, int32_t* kv_num,
                          int32_t* kv_idx /* [H,QB,W+budget+G] */, int32_t* picks /* [H,QB,budget] */,
                          float* logits_out /* [H,QB,NB] or NULL */, void* stream);
+/* With qbar/kbar (D = 128), NB >= 1024 and a logits_out buffer, the logits
+ * of the lower triangle are first computed on fp32 MFMA into logits_out (a
+ * product of the block-mean matrices: the sum order differs from the
+ * per-candidate fmaf chain used otherwise, within fp32 rounding) and the
+ * selection reads them back; give logits_out to get that path at long
+ * sequences.  scope_pointer_pair_bias keeps the fmaf chain. */
 
 /* Soft pointer weights (no reference counterpart: build_pointer_blockmask
  * selects under torch.no_grad, model/attn_bias.py:623; this is the

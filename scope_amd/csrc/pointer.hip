@@ -122,26 +122,29 @@ __global__ __launch_bounds__(1024) void doc_scan_kernel(int NB, int bs, int doc_
                                                          int32_t* __restrict__ ds_local,
                                                          int32_t* __restrict__ ds_tok_end) {
   __shared__ int carry_s;
-  __shared__ int tmax[1024];
+  __shared__ int wmax[16];
   if (threadIdx.x == 0) carry_s = -1;
-  __syncthreads();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   for (int base = 0; base < NB; base += 1024) {
     int b = base + threadIdx.x;
     int lc = b < NB ? ds_tok_end[b] : -1;
     int fc = b < NB ? ds_local[b] : 0;
-    // inclusive prefix max of lc within the chunk (Hillis-Steele)
-    tmax[threadIdx.x] = lc;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-      int v = threadIdx.x >= o ? tmax[threadIdx.x - o] : -1;
-      __syncthreads();
-      tmax[threadIdx.x] = max(tmax[threadIdx.x], v);
-      __syncthreads();
+    // inclusive prefix max of lc within the chunk: within each wavefront by
+    // shuffles, then over the wavefronts' maxima
+    int v = lc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(v, o, 64);
+      if (lane >= o) v = max(v, u);
     }
-    int carry = carry_s;
-    int incl = max(tmax[threadIdx.x], carry);
-    int excl = max(threadIdx.x > 0 ? tmax[threadIdx.x - 1] : -1, carry);
-    __syncthreads();
+    if (lane == 63) wmax[wv] = v;
+    __syncthreads();  // wmax complete; carry_s of the previous chunk visible
+    int before = carry_s;  // maximum of everything before this wavefront
+    for (int w = 0; w < wv; ++w) before = max(before, wmax[w]);
+    const int incl = max(v, before);
+    const int prev = __shfl_up(incl, 1, 64);
+    const int excl = lane > 0 ? prev : before;
+    __syncthreads();  // everyone has read wmax and carry_s
     if (threadIdx.x == 1023) carry_s = incl;
     if (b < NB) {
       int64_t first_tok = static_cast<int64_t>(b) * bs;
@@ -411,8 +414,10 @@ __device__ __forceinline__ bool better(float za, int ka, float zb, int kb) {
 // candidates).
 constexpr int kScoreQ = 8;
 
-// KB: slots of the per-lane top list (the budget rounded up to 2, 4, 8 or 16)
-template <int D, int KB>
+// KB: slots of the per-lane top list (the budget rounded up to 2, 4, 8 or 16).
+// LG: the logits are given (logits_in): each wavefront walks its own
+// candidates, the logits of four chunks loaded ahead, no k̄ staging.
+template <int D, int KB, bool LG = false>
 __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, const float* __restrict__ qbar,
                                                                  const float* __restrict__ kbar,
                                                                  const float* __restrict__ logits_in,
@@ -427,7 +432,7 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
   constexpr int kStride = D + 4;  // padded k̄ row in LDS (16-byte aligned, conflict-free float4 reads)
   constexpr int NT = kScoreQ * kWave;
   constexpr int PF = (kWave * D / 4 + NT - 1) / NT;  // float4 of a chunk per thread
-  __shared__ float ks[2][kWave * kStride];
+  __shared__ float ks[LG ? 1 : 2][LG ? 4 : kWave * kStride];  // k̄ chunks (not with given logits)
   __shared__ int lists[kScoreQ * 64];
   const scope_ptr_score_params& P = A.p;
   const int NB = P.NB;
@@ -447,12 +452,6 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
   const int ghi = min(ds_p + G - 1, qbc);         // global = [ds_p, ghi] (G > 0)
   const int64_t rowq = static_cast<int64_t>(h) * NB + qbc;
 
-  float qv[D];
-  if (!logits_in) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) qv[d] = qbar[rowq * D + d];
-  }
-
   // per-lane top-B list, sorted best first
   float tz[KB];
   int tk[KB];
@@ -461,7 +460,61 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
     tz[i] = -INFINITY;
     tk[i] = INT_MAX;
   }
+  // candidate kb with its logit: the noise and the insertion into the list
+  auto consider = [&](int kb, float logit) __attribute__((always_inline)) {
+    float z = logit / P.temp;
+    if (P.noise_mode != 0) {
+      float u = P.noise_mode == 1 ? gumbel_u[rowq * NB + kb]
+                                  : counter_uniform(P.seed, static_cast<uint32_t>(h), static_cast<uint32_t>(qbc),
+                                                    static_cast<uint32_t>(kb));
+      z = z + gumbel_of(u, P.eps);
+    }
+    // insertion into the sorted list (compile-time indexed, predicated)
+    float cz = z;
+    int ck = kb;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      if (i < B && better(cz, ck, tz[i], tk[i])) {
+        float z2 = tz[i];
+        int k2 = tk[i];
+        tz[i] = cz;
+        tk[i] = ck;
+        cz = z2;
+        ck = k2;
+      }
+    }
+  };
+  if constexpr (LG) {
+    // this wavefront's candidates lie in [ds_p, qb]; chunks of 64, one per lane
+    constexpr int PFN = 4;
+    float lq[PFN];
+    const int lo = ds_p;
+    const bool copy_out = logits_out && logits_out != logits_in;
+    auto load = [&](int kb0) __attribute__((always_inline)) {
+      const int kb = kb0 + lane;
+      return active && kb <= qbc ? logits_in[rowq * NB + kb] : 0.f;
+    };
+#pragma unroll
+    for (int i = 0; i < PFN; ++i) lq[i] = load(lo + i * kWave);
+    for (int kb0 = lo; kb0 <= qbc; kb0 += PFN * kWave) {
+#pragma unroll
+      for (int i = 0; i < PFN; ++i) {
+        const int kb = kb0 + i * kWave + lane;
+        const float logit = lq[i];
+        lq[i] = load(kb0 + (i + PFN) * kWave);  // the chunk PFN ahead (0 past the row)
+        if (copy_out && active && kb <= qbc) logits_out[rowq * NB + kb] = logit;
+        const bool cand = active && kb <= qbc && !(kb >= wlo) && !(G > 0 && kb <= ghi);
+        if (cand) consider(kb, logit);
+      }
+    }
+  }
 
+  if constexpr (!LG) {
+  float qv[D];
+  if (!logits_in) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) qv[d] = qbar[rowq * D + d];
+  }
   // kb range of the workgroup: [ds_ptr of its first q-block, its last q-block]
   const int lo_wg = ds_ptr_a[qb0];
   const int hi_wg = min(qb0 + kScoreQ - 1, NB - 1);
@@ -518,34 +571,13 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
       }
       if (logits_out) logits_out[rowq * NB + kb] = logit;
     }
-    if (cand) {
-      float z = logit / P.temp;
-      if (P.noise_mode != 0) {
-        float u = P.noise_mode == 1 ? gumbel_u[rowq * NB + kb]
-                                    : counter_uniform(P.seed, static_cast<uint32_t>(h), static_cast<uint32_t>(qbc),
-                                                      static_cast<uint32_t>(kb));
-        z = z + gumbel_of(u, P.eps);
-      }
-      // insertion into the sorted list (compile-time indexed, predicated)
-      float cz = z;
-      int ck = kb;
-#pragma unroll
-      for (int i = 0; i < KB; ++i) {
-        if (i < B && better(cz, ck, tz[i], tk[i])) {
-          float z2 = tz[i];
-          int k2 = tk[i];
-          tz[i] = cz;
-          tk[i] = ck;
-          cz = z2;
-          ck = k2;
-        }
-      }
-    }
+    if (cand) consider(kb, logit);
     if (!logits_in && more) {
       stash(buf ^ 1);
       buf ^= 1;
     }
   }
+  }  // !LG
   if (logits_out && active) {
     // entries outside [ds_ptr, qb] are not candidates: -inf
     for (int kb = lane; kb < NB; kb += kWave)
@@ -589,6 +621,81 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
   if (active && lane == 0) kv_num[rowq] = n;
 }
 
+
+// ---------------------------------------------------------------------------
+// block-scoring logits on fp32 MFMA (long sequences)
+// ---------------------------------------------------------------------------
+// logit[h, qb, kb] = logit_scale·q̄[qb]·k̄[kb] + prior[qb - kb] for kb <= qb, as
+// a product of the block-mean matrices on v_mfma_f32_32x32x2_f32 (fp32
+// operands, fp32 accumulation).  One workgroup of four wavefronts per 64x64
+// tile of the lower triangle; each wavefront computes a 32x32 quarter over D
+// in steps of 2 from operands it loads itself.  The
+// selection then reads the logits (ptr_score_kernel with logits_in).  With
+// thousands of candidates per q-block the wavefront-per-row dot products of
+// ptr_score_kernel (a fmaf chain per candidate) would take several times
+// longer; the sum order differs, within fp32 rounding.
+constexpr int kLgTile = 64;
+
+typedef float f32x16v_t __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float logit_scale,
+                                                         const float* __restrict__ qbar,
+                                                         const float* __restrict__ kbar,
+                                                         const float* __restrict__ prior, int64_t prior_stride,
+                                                         float* __restrict__ logits) {
+  constexpr int D = 128;
+  // linear index -> (h, row tile rt, column tile ct <= rt)
+  const int nt = (NB + kLgTile - 1) / kLgTile;
+  const int per_h = nt * (nt + 1) / 2;
+  const int h = blockIdx.x / per_h;
+  int rem = blockIdx.x % per_h;
+  // rt: the largest r with r(r+1)/2 <= rem
+  int rt = static_cast<int>((sqrtf(8.f * static_cast<float>(rem) + 1.f) - 1.f) * 0.5f);
+  while (rt * (rt + 1) / 2 > rem) --rt;
+  while ((rt + 1) * (rt + 2) / 2 <= rem) ++rt;
+  const int ct = rem - rt * (rt + 1) / 2;
+  const int r0 = rt * kLgTile, c0 = ct * kLgTile;
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64, m = lane % 32, g = lane / 32;
+  const int wr = wave / 2, wc = wave % 2;
+  // each lane reads its operands straight from memory (q̄, k̄ stay in the
+  // caches): MFMA j of each group of four takes d = 8·group + 4g + j for lane
+  // half g, one float4 per operand and group; two accumulators (even and odd
+  // groups) halve the dependent chain
+  const int qr = min(r0 + wr * 32 + m, NB - 1), kr = min(c0 + wc * 32 + m, NB - 1);
+  const float* qa = qbar + (static_cast<int64_t>(h) * NB + qr) * D + 4 * g;
+  const float* kb_ = kbar + (static_cast<int64_t>(h) * NB + kr) * D + 4 * g;
+  float4 a4[D / 8], b4[D / 8];
+#pragma unroll
+  for (int grp = 0; grp < D / 8; ++grp) {
+    a4[grp] = *reinterpret_cast<const float4*>(qa + 8 * grp);
+    b4[grp] = *reinterpret_cast<const float4*>(kb_ + 8 * grp);
+  }
+  f32x16v_t acc[2];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[0][i] = acc[1][i] = 0.f;
+#pragma unroll
+  for (int grp = 0; grp < D / 8; ++grp) {
+    f32x16v_t& c = acc[grp & 1];
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].x, b4[grp].x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].y, b4[grp].y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].z, b4[grp].z, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].w, b4[grp].w, c, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[0][i] += acc[1][i];
+  // C layout: column m (key block c0 + 32wc + m), register r -> row 8(r/4) + 4g + r%4
+  const int kb = c0 + wc * 32 + m;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int qb = r0 + wr * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+    if (qb < NB && kb <= qb) {
+      float lg = logit_scale * acc[0][r];
+      if (prior) lg = lg + prior[h * prior_stride + (qb - kb)];
+      logits[(static_cast<int64_t>(h) * NB + qb) * NB + kb] = lg;
+    }
+  }
+}
 
 // two floats -> packed bf16 pair (round to nearest even; lo in the low half)
 __device__ __forceinline__ uint32_t bf16_pack(float lo, float hi) {
@@ -847,6 +954,10 @@ int scope_block_means(const uint16_t* q, const uint16_t* k, int H, int64_t T, in
   return check_launch("block_means_kernel");
 }
 
+// number of blocks from which scope_pointer_select computes the logits on MFMA
+// (when it has a logits_out buffer to hold them)
+constexpr int kLogitsGemmNB = 1024;
+
 int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, const float* kbar,
                          const float* logits_in, const float* prior, const float* gumbel_u, const int32_t* ds_ptr,
                          const int32_t* ds_local, int32_t* kv_num, int32_t* kv_idx, int32_t* picks,
@@ -868,12 +979,26 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
   SCOPE_REQUIRE(A.N <= 64, "scope_pointer_select: list length %d exceeds 64", A.L);
   dim3 grid(ceil_div(p->NB, kScoreQ), p->H);
   hipStream_t st = as_stream(stream);
+  if (!logits_in && logits_out && p->D == 128 && p->NB >= kLogitsGemmNB) {
+    // long sequences: the logits on fp32 MFMA into logits_out, then the selection reads them
+    const int nt = ceil_div(p->NB, kLgTile);
+    hipLaunchKernelGGL(ptr_logits_kernel, dim3(p->H * (nt * (nt + 1) / 2)), dim3(256), 0, st, p->H, p->NB,
+                       p->logit_scale, qbar, kbar, prior, prior ? p->prior_head_stride : 0, logits_out);
+    logits_in = logits_out;
+    qbar = kbar = nullptr;
+    prior = nullptr;  // already in the logits
+  }
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(kScoreQ * 64), 0, st, A, qbar, kbar, logits_in, prior, gumbel_u, ds_ptr,
                        ds_local, kv_num, kv_idx, picks, logits_out);
   };
   const int kb = p->budget <= 2 ? 2 : p->budget <= 4 ? 4 : p->budget <= 8 ? 8 : 16;
-  if (p->D == 128) {
+  if (logits_in) {
+    if (kb == 2) go(ptr_score_kernel<128, 2, true>);
+    else if (kb == 4) go(ptr_score_kernel<128, 4, true>);
+    else if (kb == 8) go(ptr_score_kernel<128, 8, true>);
+    else go(ptr_score_kernel<128, 16, true>);
+  } else if (p->D == 128) {
     if (kb == 2) go(ptr_score_kernel<128, 2>);
     else if (kb == 4) go(ptr_score_kernel<128, 4>);
     else if (kb == 8) go(ptr_score_kernel<128, 8>);

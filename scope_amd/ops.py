@@ -159,12 +159,18 @@ def pointer_select(ds_ptr: torch.Tensor, ds_local: torch.Tensor, *, bs: int, NB:
     kv_num = torch.empty((H, NB), dtype=torch.int32, device=dev)
     kv_idx = torch.empty((H, NB, L), dtype=torch.int32, device=dev)
     picks = torch.empty((H, NB, max(budget, 1)), dtype=torch.int32, device=dev)
-    logits = torch.empty((H, NB, NB), dtype=torch.float32, device=dev) if return_logits else None
+    # from LOGITS_GEMM_NB blocks on (D = 128) the library computes the logits on
+    # MFMA into the logits buffer before the selection reads them: give it one
+    gemm = logits_in is None and qbar is not None and D == 128 and NB >= LOGITS_GEMM_NB
+    logits = torch.empty((H, NB, NB), dtype=torch.float32, device=dev) if (return_logits or gemm) else None
     call("scope_pointer_select", C.byref(prm), _p(_f32(qbar)), _p(_f32(kbar)), _p(_f32(logits_in)), _p(prior),
          _p(_f32(gumbel_u) if noise_mode == 1 else None), _p(_i32(ds_ptr)), _p(_i32(ds_local)), _p(kv_num),
          _p(kv_idx), _p(picks), _p(logits), _stream(dev))
     picks = picks[..., :budget]
     return (kv_num, kv_idx, picks, logits) if return_logits else (kv_num, kv_idx, picks)
+
+
+LOGITS_GEMM_NB = 1024  # pointer.hip kLogitsGemmNB
 
 
 def pointer_pair_bias(kv_num: torch.Tensor, kv_idx: torch.Tensor, picks: torch.Tensor, *, bs: int, window: int,

@@ -288,5 +288,35 @@ def test_c5_h8_layer():
     step()
     torch.cuda.synchronize()
     print(f"  layer done (N_act {int(step.last['kv_num'].sum())})", flush=True)
+    # the selection over 4096 candidates (logits on fp32 MFMA at this length):
+    # the step's lists again with the logits returned, each sampled row's
+    # logits within 1e-4·(1 + |ref|) of fp64 from the block means, and heads
+    # 0 and H-1 equal to the oracle's selection on those logits
+    ds_ptr, ds_local, _ = ops.doc_starts(inp["docs"], bs)
+    ls = bs / math.sqrt(D)
+    kv_num, kv_idx, picks, lg = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=NB, H=H, window=2, n_global=1,
+                                                   budget=8, qbar=qbar, kbar=kbar, prior=step.prior, temp=1.0,
+                                                   logit_scale=ls, noise="counter", seed=step.seed,
+                                                   return_logits=True)
+    assert torch.equal(kv_num, step.last["kv_num"]) and torch.equal(kv_idx, step.last["kv_idx"])
+    prior64 = step.prior.double().cpu()
+    for h in (0, H - 1):
+        rows = [0, 1, 777, NB // 2, NB - 2, NB - 1]
+        q64, k64 = qbar[h, rows].double().cpu(), kbar[h].double().cpu()
+        want = ls * (q64 @ k64.T)
+        for i, qb in enumerate(rows):
+            want[i, :qb + 1] += prior64[qb - torch.arange(qb + 1)]
+            got = lg[h, qb, :qb + 1].double().cpu()
+            err = float(((got - want[i, :qb + 1]).abs() / (1 + want[i, :qb + 1].abs())).max())
+            assert err <= 1e-4, f"head {h}, q-block {qb}: logits off by {err:.3g}"
+        lgh = lg[h:h + 1].cpu().numpy()
+        qq, kk = np.meshgrid(np.arange(NB), np.arange(NB), indexing="ij")
+        gh = OP.gumbel_from_u(OP.counter_uniform(step.seed, np.full_like(qq, h), qq, kk))[None]
+        ref = OP.pointer_select_blockscore(lgh, inp["docs"].cpu().numpy(), bs=bs, window=2, n_global=1, budget=8,
+                                           gumbel=gh)
+        assert np.array_equal(picks[h:h + 1].cpu().numpy(), ref["picks"]), f"picks of head {h}"
+        assert np.array_equal(kv_idx[h:h + 1].cpu().numpy(), ref["packed"]), f"lists of head {h}"
+        print(f"  head {h}: logits within 1e-4 of fp64, lists equal to the oracle's selection", flush=True)
+    del lg
     sample = [0, NB // 2 + 3, NB - 1]
     _layer_checks(step, inp, [0, H - 1], sample, bs, n_hot_max=2)
