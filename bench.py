@@ -97,6 +97,9 @@ def parse():
     ap.add_argument("--n-global", type=int, default=2)
     ap.add_argument("--sweep", action="store_true", help="also time budgets 2 and 4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ref-layer", action="store_true",
+                    help="leave the reference's default layer out of the default line (profiles of the headline "
+                         "kernels alone)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--workload", choices=["pointer", "train", "swa", "coeff", "teacher", "decode", "ref"],
                     default="pointer")
@@ -760,7 +763,8 @@ def measured_traffic(kernel: str, H: int, T: int, bs: int, budget: int):
         return None, None
     with open(path) as fh:
         data = json.load(fh)
-    k = data.get("kernels", {}).get(kernel)
+    kernels = data.get("kernels", {})
+    k = kernels.get(kernel) or kernels.get(kernel.split("<")[0])
     if not k:
         return None, None
     return int(k["bytes"]), os.path.relpath(path, ROOT)
@@ -1071,7 +1075,8 @@ def main():
     dom = max(per_kernel, key=lambda p: ph[p])
     flops, kname = per_kernel[dom]
     achieved = flops / (ph[dom] / 1e3) / 1e12
-    traffic, tsrc = measured_traffic(kname, H, T, bs, args.budget)
+    # the instance of this block size in the block-offset bias mode (1)
+    traffic, tsrc = measured_traffic(f"{kname}<{bs},1>", H, T, bs, args.budget)
     roofline = dict(bound="mfma", kernel=kname, achieved=round(achieved, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                     frac=round(achieved / PEAK_BF16_TFLOPS, 4), traffic=traffic, traffic_source=tsrc,
                     flops_per_launch=flops, launch_ms=round(ph[dom], 4))
@@ -1144,7 +1149,7 @@ def main():
     roofline["frac_of_measured"] = round(achieved / mp["mfma_bf16_tflops"], 4)
     pointer["peak_measured"] = mp["hbm_copy_gbs"]
     pointer["block_means_frac_of_measured"] = round(pointer["block_means_achieved"] / mp["hbm_copy_gbs"], 4)
-    if not train and (H, T, bs) == (8, 131072, 256):
+    if not train and (H, T, bs) == (8, 131072, 256) and not args.no_ref_layer:
         # the reference's default layer (T=16384, bs 128, token offsets, reference-mode
         # lists), timed after the headline with its own events and steps
         res["reference_default_layer"] = ref_layer(8, 16384, args.steps, args.warmup)

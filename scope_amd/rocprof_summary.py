@@ -29,7 +29,7 @@ import os
 import sys
 
 KERNELS = ("attn_fwd_kernel", "attn_fwd_kernel(lse)", "attn_fwd_kernel(mass)", "attn_bwd_dq2_kernel",
-           "attn_bwd_dq16_kernel", "attn_bwd_dq_kernel", "attn_bwd_dkv16_kernel", "attn_bwd_dkv_kernel", "bwd_reduce_kernel", "block_means_kernel", "ptr_score_kernel",
+           "attn_bwd_dq16_kernel", "attn_bwd_dq_kernel", "attn_bwd_dkv16_kernel", "attn_bwd_dkv_kernel", "bwd_reduce_kernel", "block_means_kernel", "ptr_logits_kernel", "ptr_score_kernel",
            "stats_kernel", "tr_fill_kernel", "tr_sort_kernel", "tr_count_kernel", "swa_count_kernel",
            "swa_rows_kernel", "swa_pad_kernel", "coeff_fwd_kernel", "coeff_bwd_kernel", "coeff_reg_kernel",
            "probe_mfma_kernel", "probe_copy_kernel")
@@ -37,7 +37,9 @@ COPY = "copyBuffer"
 FWD_KINDS = {"0": "", "1": "(lse)", "2": "(mass)"}
 
 
-def _short(name: str) -> str:
+def _base(name: str) -> str:
+    """The kernel's name without namespace and template arguments (the
+    forward's kind as a suffix), or the tail of an unknown name."""
     if "attn_fwd_kernel<" in name:
         args = name.split("attn_fwd_kernel<", 1)[1].split(">", 1)[0].split(",")
         kind = args[2].strip() if len(args) > 2 else "0"
@@ -47,6 +49,25 @@ def _short(name: str) -> str:
             return k
     name = name.replace("(anonymous namespace)::", "")
     return name.split("(")[0][-60:]
+
+
+def _short(name: str) -> str:
+    """_base, with the block size and bias mode of an attention kernel
+    (``attn_bwd_dkv16_kernel<256,1>``): one run can hold several instances
+    (the headline layer and the reference's default layer)."""
+    b = _base(name)
+    if not b.startswith("attn_"):
+        return b
+    stem = b.split("(")[0]
+    if stem + "<" not in name:
+        return b
+    args = [a.strip() for a in name.split(stem + "<", 1)[1].split(">", 1)[0].split(",")]
+    return f"{stem}<{','.join(args[:2])}>" + b[len(stem):]
+
+
+def _order(k: str) -> tuple[int, str]:
+    b = k.split("<")[0] + (k.split(">", 1)[1] if ">" in k else "")
+    return (KERNELS.index(b) if b in KERNELS else len(KERNELS), k)
 
 
 def _csv(dir_: str, suffix: str) -> list[dict]:
@@ -91,8 +112,8 @@ def pmc_table(dir_: str) -> list[str]:
     lines = [f"SIMDs {simds}, XCDs {xcds}; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs)", "",
              "| kernel | MFMA busy | VALU / MFMA instr | LDS instr / MFMA | LDS bank conflict / LDS active | wait / wave cycles |",
              "|---|---|---|---|---|---|"]
-    for k in KERNELS:
-        if k not in acc:
+    for k in sorted(acc, key=_order):
+        if _order(k)[0] == len(KERNELS):
             continue
         m = {c: sum(v) / len(v) for c, v in acc[k].items()}
         if "SQ_VALU_MFMA_BUSY_CYCLES" not in m or not m.get("GRBM_GUI_ACTIVE"):
