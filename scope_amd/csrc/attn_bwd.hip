@@ -330,9 +330,9 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
   // ---- epilogue: dQ = scale·o, coefficient gradients.  The lane's row and
   // the addresses from it are formed again here from an opaque copy of the
   // lane index, so that none of them is held (or spilled) through the tiles.
-  int lane_e = lane;
-  asm volatile("" : "+v"(lane_e));
-  const int ge = lane_e / 32, lrow_e = wave * 32 + lane_e % 32;
+  int tid_e = tid;
+  asm volatile("" : "+v"(tid_e));
+  const int lane_e = tid_e % 64, ge = lane_e / 32, lrow_e = (tid_e / 64) * 32 + lane_e % 32;
   R.row = static_cast<int>(q0) + lrow_e;
   rs_tot += __shfl_xor(rs_tot, 32, 64);
   const float dd_err = rs_tot;  // Δ_true - Δ
@@ -776,7 +776,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   const int32_t* ql = a.q_list + static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb];
 
   const int tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid % 64, g = lane / 32, lr = lane % 32;
   const int64_t kv0 = static_cast<int64_t>(kb) * BS + zpart * 128;  // first key row of this workgroup
   const int64_t wkv_lo = kv0 + wave * 32;
   const int64_t wkv = wkv_lo + lr;
@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   const int32_t* ql = a.q_list + static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb];
 
   const int tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64, g = lane / 16, c = lane % 16;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid % 64, g = lane / 16, c = lane % 16;
   const int64_t kv0 = static_cast<int64_t>(kb) * BS + zpart * 128;  // first key row of this workgroup
   const int wkv_lo = static_cast<int>(kv0) + wave * 16;
   const int wkv = wkv_lo + c;
@@ -1382,7 +1382,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float kbias[kListLds];  // pair bias per list entry (log2 units), when given
 
   const int tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64, g = lane / 16, c = lane % 16;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid % 64, g = lane / 16, c = lane % 16;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
   const int h = tile / (a.QB * SPLIT), qb = (tile / SPLIT) % a.QB, part = tile % SPLIT;
   const int64_t q0 = static_cast<int64_t>(qb) * BS + part * 128;

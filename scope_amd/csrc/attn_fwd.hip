@@ -129,7 +129,7 @@ __global__ __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) voi
   __shared__ __attribute__((aligned(16))) float coef[MODE == 1 ? BS * 16 : 4];
 
   const int tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64, g = lane / 32, lr = lane % 32;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid % 64, g = lane / 32, lr = lane % 32;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
   const int h = tile / a.QB, qb = tile % a.QB;
   const int64_t q0 = static_cast<int64_t>(qb) * BS;
