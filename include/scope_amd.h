@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SCOPE_ABI_VERSION 2
+#define SCOPE_ABI_VERSION 3
 
 enum {
   SCOPE_OK = 0,
@@ -107,7 +107,12 @@ typedef struct {
   uint64_t seed;                /* noise_mode 2                                          */
   float eps;                    /* Gumbel eps (1e-9)                                     */
   int64_t prior_head_stride;    /* 0: prior is [NB] shared; NB: prior is [H, NB]         */
+  int flags;                    /* SCOPE_PTR_* bits below (ABI 3)                        */
 } scope_ptr_score_params;
+
+/* flags: logits_out is only the work buffer of the MFMA logits below; its
+ * entries outside [ds_ptr, qb] are left unset instead of set to -inf. */
+#define SCOPE_PTR_LOGITS_SCRATCH 1
 
 int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, const float* kbar,
                          const float* logits_in /* [H,QB,NB] or NULL */,
@@ -116,11 +121,14 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
                          int32_t* kv_idx /* [H,QB,W+budget+G] */, int32_t* picks /* [H,QB,budget] */,
                          float* logits_out /* [H,QB,NB] or NULL */, void* stream);
 /* With qbar/kbar (D = 128), NB >= 1024 and a logits_out buffer, the logits
- * of the lower triangle are first computed on fp32 MFMA into logits_out (a
- * product of the block-mean matrices: the sum order differs from the
- * per-candidate fmaf chain used otherwise, within fp32 rounding) and the
- * selection reads them back; give logits_out to get that path at long
- * sequences.  scope_pointer_pair_bias keeps the fmaf chain. */
+ * of the lower triangle are first computed into logits_out as a product of
+ * the block-mean matrices on bf16 MFMA, each fp32 mean split into two bf16
+ * parts (hi·hi + hi·lo + lo·hi: within about 1e-5 of the fp32 dot product,
+ * relative to Σ|q̄_d·k̄_d|, where the per-candidate fmaf chain used otherwise
+ * rounds at fp32), and the selection reads them back; give logits_out to get
+ * that path at long sequences (with SCOPE_PTR_LOGITS_SCRATCH when the caller
+ * does not read the logits).  scope_pointer_pair_bias keeps the fmaf
+ * chain. */
 
 /* Soft pointer weights (no reference counterpart: build_pointer_blockmask
  * selects under torch.no_grad, model/attn_bias.py:623; this is the

@@ -12,7 +12,7 @@ import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCOPE_AMD_LIB", os.path.join(HERE, "libscope_amd.so"))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 c_int, c_int64, c_float, c_void_p, c_char_p, c_uint64 = C.c_int, C.c_int64, C.c_float, C.c_void_p, C.c_char_p, C.c_uint64
 
@@ -28,7 +28,9 @@ class PtrRefParams(C.Structure):
 class PtrScoreParams(C.Structure):
     _fields_ = [("H", c_int), ("NB", c_int), ("D", c_int), ("bs", c_int), ("window", c_int), ("n_global", c_int),
                 ("budget", c_int), ("temp", c_float), ("logit_scale", c_float), ("noise_mode", c_int),
-                ("seed", c_uint64), ("eps", c_float), ("prior_head_stride", c_int64)]
+                ("seed", c_uint64), ("eps", c_float), ("prior_head_stride", c_int64), ("flags", c_int)]
+
+PTR_LOGITS_SCRATCH = 1  # SCOPE_PTR_LOGITS_SCRATCH
 
 
 class StatsParams(C.Structure):

@@ -13,7 +13,7 @@
 #include <limits.h>
 #include <math.h>
 
-#include "common.h"
+#include "attn_common.h"
 
 namespace scope {
 
@@ -452,37 +452,41 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
   const int ghi = min(ds_p + G - 1, qbc);         // global = [ds_p, ghi] (G > 0)
   const int64_t rowq = static_cast<int64_t>(h) * NB + qbc;
 
-  // per-lane top-B list, sorted best first
+  // per-lane top-KB list (KB >= B), sorted best first; an empty slot holds
+  // z = NaN (and kb = INT_MAX) until the merge, which sees -inf there
   float tz[KB];
   int tk[KB];
 #pragma unroll
   for (int i = 0; i < KB; ++i) {
-    tz[i] = -INFINITY;
+    tz[i] = __builtin_nanf("");
     tk[i] = INT_MAX;
   }
-  // candidate kb with its logit: the noise and the insertion into the list
+  const bool unit_temp = P.temp == 1.f;  // z = logit / 1 is the logit itself
+  // candidate kb with its logit: the noise and the insertion into the list.
+  // A lane meets its candidates in increasing kb (both loops below), so a new
+  // candidate loses every tie on z to the entries already listed: it goes
+  // into the first slot whose z it exceeds (!(z <= tz) is also true on an
+  // empty slot, so a -inf z still takes the first empty one, as the lower
+  // index wins its tie with an empty slot's -inf), and the slots below shift
+  // down.  The compares all read the list before the insertion.
   auto consider = [&](int kb, float logit) __attribute__((always_inline)) {
-    float z = logit / P.temp;
+    float z = unit_temp ? logit : logit / P.temp;
     if (P.noise_mode != 0) {
       float u = P.noise_mode == 1 ? gumbel_u[rowq * NB + kb]
                                   : counter_uniform(P.seed, static_cast<uint32_t>(h), static_cast<uint32_t>(qbc),
                                                     static_cast<uint32_t>(kb));
       z = z + gumbel_of(u, P.eps);
     }
-    // insertion into the sorted list (compile-time indexed, predicated)
-    float cz = z;
-    int ck = kb;
+    bool c[KB];
 #pragma unroll
-    for (int i = 0; i < KB; ++i) {
-      if (i < B && better(cz, ck, tz[i], tk[i])) {
-        float z2 = tz[i];
-        int k2 = tk[i];
-        tz[i] = cz;
-        tk[i] = ck;
-        cz = z2;
-        ck = k2;
-      }
+    for (int i = 0; i < KB; ++i) c[i] = !(z <= tz[i]);
+#pragma unroll
+    for (int i = KB - 1; i > 0; --i) {
+      tz[i] = c[i - 1] ? tz[i - 1] : (c[i] ? z : tz[i]);
+      tk[i] = c[i - 1] ? tk[i - 1] : (c[i] ? kb : tk[i]);
     }
+    tz[0] = c[0] ? z : tz[0];
+    tk[0] = c[0] ? kb : tk[0];
   };
   if constexpr (LG) {
     // this wavefront's candidates lie in [ds_p, qb]; chunks of 64, one per lane
@@ -578,13 +582,15 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
     }
   }
   }  // !LG
-  if (logits_out && active) {
+  if (logits_out && active && !(P.flags & SCOPE_PTR_LOGITS_SCRATCH)) {
     // entries outside [ds_ptr, qb] are not candidates: -inf
     for (int kb = lane; kb < NB; kb += kWave)
       if (kb < ds_p || kb > qbc) logits_out[rowq * NB + kb] = -INFINITY;
   }
 
   // wave merge: B rounds of arg-best over the lanes' list heads
+#pragma unroll
+  for (int i = 0; i < KB; ++i) tz[i] = tk[i] == INT_MAX ? -INFINITY : tz[i];
   int* list = lists + wave * 64;
   for (int i = 0; i < B; ++i) {
     float bz = tz[0];
@@ -623,20 +629,29 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
 
 
 // ---------------------------------------------------------------------------
-// block-scoring logits on fp32 MFMA (long sequences)
+// block-scoring logits on bf16 MFMA with split operands (long sequences)
 // ---------------------------------------------------------------------------
-// logit[h, qb, kb] = logit_scale·q̄[qb]·k̄[kb] + prior[qb - kb] for kb <= qb, as
-// a product of the block-mean matrices on v_mfma_f32_32x32x2_f32 (fp32
-// operands, fp32 accumulation).  One workgroup of four wavefronts per 64x64
-// tile of the lower triangle; each wavefront computes a 32x32 quarter over D
-// in steps of 2 from operands it loads itself.  The
-// selection then reads the logits (ptr_score_kernel with logits_in).  With
-// thousands of candidates per q-block the wavefront-per-row dot products of
-// ptr_score_kernel (a fmaf chain per candidate) would take several times
-// longer; the sum order differs, within fp32 rounding.
-constexpr int kLgTile = 64;
-
-typedef float f32x16v_t __attribute__((ext_vector_type(16)));
+// logit[h, qb, kb] = logit_scale·q̄[qb]·k̄[kb] + prior[qb - kb] for kb <= qb.
+// Each fp32 mean x is split into bf16 parts x = hi + lo + e with
+// hi = bf16(x), lo = bf16(x - hi) and |e| <= 2^-18·|x|, and the product takes
+// hi·hi + hi·lo + lo·hi on v_mfma_f32_32x32x16_bf16 (exact bf16 products,
+// fp32 accumulation); the dropped lo·lo and the e terms are at most
+// 3·2^-18 of |q̄_d·k̄_d| per term, far below the 1e-4 the selection's logits
+// are held to.  The selection then reads the logits (ptr_score_kernel with
+// logits_in).  With thousands of candidates per q-block the
+// wavefront-per-row dot products of ptr_score_kernel (a fmaf chain per
+// candidate) would take several times longer; the sum order differs, within
+// fp32 rounding.
+//
+// One workgroup of four wavefronts per CU loops over the 128x128 tiles of
+// the lower triangle (all heads).  A tile's 128 q̄ rows and 128 k̄ rows are
+// loaded into registers while the previous tile's MFMAs run, then split
+// once into hi and lo bf16 tiles in LDS (rows padded by 16 bytes, so the
+// 16-byte operand reads of 32 rows spread over the banks); each wavefront
+// computes a 64x64 quarter (2x2 blocks of 32x32, 12 MFMAs per step of 16
+// over D).
+constexpr int kLgTile = 128;
+constexpr int kLgRow = 128 + 8;  // padded bf16 row of a split tile
 
 __global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float logit_scale,
                                                          const float* __restrict__ qbar,
@@ -644,55 +659,115 @@ __global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float lo
                                                          const float* __restrict__ prior, int64_t prior_stride,
                                                          float* __restrict__ logits) {
   constexpr int D = 128;
-  // linear index -> (h, row tile rt, column tile ct <= rt)
+  constexpr int NF = kLgTile * D / 4 / 256;  // float4 per thread and operand
+  // [operand: q̄ hi, q̄ lo, k̄ hi, k̄ lo][row][d]
+  __shared__ __attribute__((aligned(16))) uint16_t sp[4][kLgTile * kLgRow];
+  // the tile's prior values: prior[d] for d = qb - kb in dbase .. dbase + 255,
+  // one per thread
+  static_assert(2 * kLgTile == 256, "one prior value per thread");
+  __shared__ float spr[2 * kLgTile];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, m = lane % 32, g = lane / 32;
+  const int wr = wave / 2, wc = wave % 2;  // this wavefront's 64x64 quarter
   const int nt = (NB + kLgTile - 1) / kLgTile;
   const int per_h = nt * (nt + 1) / 2;
-  const int h = blockIdx.x / per_h;
-  int rem = blockIdx.x % per_h;
-  // rt: the largest r with r(r+1)/2 <= rem
-  int rt = static_cast<int>((sqrtf(8.f * static_cast<float>(rem) + 1.f) - 1.f) * 0.5f);
-  while (rt * (rt + 1) / 2 > rem) --rt;
-  while ((rt + 1) * (rt + 2) / 2 <= rem) ++rt;
-  const int ct = rem - rt * (rt + 1) / 2;
-  const int r0 = rt * kLgTile, c0 = ct * kLgTile;
-  const int tid = threadIdx.x;
-  const int wave = tid / 64, lane = tid % 64, m = lane % 32, g = lane / 32;
-  const int wr = wave / 2, wc = wave % 2;
-  // each lane reads its operands straight from memory (q̄, k̄ stay in the
-  // caches): MFMA j of each group of four takes d = 8·group + 4g + j for lane
-  // half g, one float4 per operand and group; two accumulators (even and odd
-  // groups) halve the dependent chain
-  const int qr = min(r0 + wr * 32 + m, NB - 1), kr = min(c0 + wc * 32 + m, NB - 1);
-  const float* qa = qbar + (static_cast<int64_t>(h) * NB + qr) * D + 4 * g;
-  const float* kb_ = kbar + (static_cast<int64_t>(h) * NB + kr) * D + 4 * g;
-  float4 a4[D / 8], b4[D / 8];
+  const int total = H * per_h;
+  // tile index -> (h, row tile rt, column tile ct <= rt)
+  auto coords = [&](int t, int& h, int& rt, int& ct) __attribute__((always_inline)) {
+    h = t / per_h;
+    const int rem = t % per_h;
+    rt = static_cast<int>((sqrtf(8.f * static_cast<float>(rem) + 1.f) - 1.f) * 0.5f);
+    while (rt * (rt + 1) / 2 > rem) --rt;
+    while ((rt + 1) * (rt + 2) / 2 <= rem) ++rt;
+    ct = rem - rt * (rt + 1) / 2;
+  };
+  // raw operands of a tile: float4 f = tid + 256·i of the 128x128 q̄ (a) and
+  // k̄ (b) row blocks, row f / 32, d = 4·(f % 32)
+  float4 ra[NF], rb[NF];
+  float rp = 0.f;  // this thread's prior value of the tile (index tid of its window)
+  auto load = [&](int t) __attribute__((always_inline)) {
+    int h, rt, ct;
+    coords(t, h, rt, ct);
+    if (prior) {
+      const int d = (rt - ct) * kLgTile - (kLgTile - 1) + tid;
+      rp = d >= 0 && d < NB ? prior[h * prior_stride + d] : 0.f;
+    }
 #pragma unroll
-  for (int grp = 0; grp < D / 8; ++grp) {
-    a4[grp] = *reinterpret_cast<const float4*>(qa + 8 * grp);
-    b4[grp] = *reinterpret_cast<const float4*>(kb_ + 8 * grp);
-  }
-  f32x16v_t acc[2];
+    for (int i = 0; i < NF; ++i) {
+      const int f = tid + 256 * i, r = f / (D / 4), d4 = f % (D / 4);
+      const int qr = min(rt * kLgTile + r, NB - 1), kr = min(ct * kLgTile + r, NB - 1);
+      ra[i] = *reinterpret_cast<const float4*>(qbar + (static_cast<int64_t>(h) * NB + qr) * D + 4 * d4);
+      rb[i] = *reinterpret_cast<const float4*>(kbar + (static_cast<int64_t>(h) * NB + kr) * D + 4 * d4);
+    }
+  };
+  auto stash = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[0][i] = acc[1][i] = 0.f;
+    for (int i = 0; i < NF; ++i) {
+      const int f = tid + 256 * i, r = f / (D / 4), d4 = f % (D / 4);
+      const float4 v[2] = {ra[i], rb[i]};
 #pragma unroll
-  for (int grp = 0; grp < D / 8; ++grp) {
-    f32x16v_t& c = acc[grp & 1];
-    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].x, b4[grp].x, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].y, b4[grp].y, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].z, b4[grp].z, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[grp].w, b4[grp].w, c, 0, 0, 0);
-  }
+      for (int o = 0; o < 2; ++o) {
+        const uint32_t h01 = cvt_pk_bf16(v[o].x, v[o].y), h23 = cvt_pk_bf16(v[o].z, v[o].w);
+        const uint32_t l01 = cvt_pk_bf16(v[o].x - bf16_lo(h01), v[o].y - bf16_hi(h01));
+        const uint32_t l23 = cvt_pk_bf16(v[o].z - bf16_lo(h23), v[o].w - bf16_hi(h23));
+        *reinterpret_cast<uint2*>(&sp[2 * o][r * kLgRow + 4 * d4]) = make_uint2(h01, h23);
+        *reinterpret_cast<uint2*>(&sp[2 * o + 1][r * kLgRow + 4 * d4]) = make_uint2(l01, l23);
+      }
+    }
+  };
+  int t = blockIdx.x;
+  if (t < total) load(t);
+  for (; t < total; t += gridDim.x) {
+    int h, rt, ct;
+    coords(t, h, rt, ct);
+    __syncthreads();  // every wavefront is done reading the previous tile
+    stash();
+    spr[tid] = rp;
+    const int dbase = (rt - ct) * kLgTile - (kLgTile - 1);
+    __syncthreads();  // the split tile is complete
+    if (t + static_cast<int>(gridDim.x) < total) load(t + gridDim.x);  // under this tile's MFMAs
+    f32x16_t acc[2][2];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[0][i] += acc[1][i];
-  // C layout: column m (key block c0 + 32wc + m), register r -> row 8(r/4) + 4g + r%4
-  const int kb = c0 + wc * 32 + m;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int qb = r0 + wr * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-    if (qb < NB && kb <= qb) {
-      float lg = logit_scale * acc[0][r];
-      if (prior) lg = lg + prior[h * prior_stride + (qb - kb)];
-      logits[(static_cast<int64_t>(h) * NB + qb) * NB + kb] = lg;
+      for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      // A: row m of block i, d = 16ks + 8g .. +7; B: the same for the key rows
+      uint4 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int ar = (64 * wr + 32 * i + m) * kLgRow + 16 * ks + 8 * g;
+        const int br = (64 * wc + 32 * i + m) * kLgRow + 16 * ks + 8 * g;
+        ah[i] = *reinterpret_cast<const uint4*>(&sp[0][ar]);
+        al[i] = *reinterpret_cast<const uint4*>(&sp[1][ar]);
+        bh[i] = *reinterpret_cast<const uint4*>(&sp[2][br]);
+        bl[i] = *reinterpret_cast<const uint4*>(&sp[3][br]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = mfma32(ah[i], bh[j], acc[i][j]);
+          acc[i][j] = mfma32(ah[i], bl[j], acc[i][j]);
+          acc[i][j] = mfma32(al[i], bh[j], acc[i][j]);
+        }
+    }
+    // C layout: column m (key block), register r -> row 8(r/4) + 4g + r%4
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int kb = ct * kLgTile + 64 * wc + 32 * j + m;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qb = rt * kLgTile + 64 * wr + 32 * i + 8 * (r / 4) + 4 * g + (r % 4);
+          if (qb < NB && kb <= qb) {
+            float lg = logit_scale * acc[i][j][r];
+            if (prior) lg = lg + spr[qb - kb - dbase];
+            logits[(static_cast<int64_t>(h) * NB + qb) * NB + kb] = lg;
+          }
+        }
     }
   }
 }
@@ -954,6 +1029,19 @@ int scope_block_means(const uint16_t* q, const uint16_t* k, int H, int64_t T, in
   return check_launch("block_means_kernel");
 }
 
+// compute units of the current device (one persistent workgroup each), per device
+static int num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // number of blocks from which scope_pointer_select computes the logits on MFMA
 // (when it has a logits_out buffer to hold them)
 constexpr int kLogitsGemmNB = 1024;
@@ -980,9 +1068,10 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
   dim3 grid(ceil_div(p->NB, kScoreQ), p->H);
   hipStream_t st = as_stream(stream);
   if (!logits_in && logits_out && p->D == 128 && p->NB >= kLogitsGemmNB) {
-    // long sequences: the logits on fp32 MFMA into logits_out, then the selection reads them
+    // long sequences: the logits on bf16 MFMA (split operands) into logits_out, then the selection reads them
+    // one workgroup per CU looping over the tiles
     const int nt = ceil_div(p->NB, kLgTile);
-    hipLaunchKernelGGL(ptr_logits_kernel, dim3(p->H * (nt * (nt + 1) / 2)), dim3(256), 0, st, p->H, p->NB,
+    hipLaunchKernelGGL(ptr_logits_kernel, dim3(min(p->H * (nt * (nt + 1) / 2), num_cus())), dim3(256), 0, st, p->H, p->NB,
                        p->logit_scale, qbar, kbar, prior, prior ? p->prior_head_stride : 0, logits_out);
     logits_in = logits_out;
     qbar = kbar = nullptr;

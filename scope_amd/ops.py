@@ -11,7 +11,7 @@ import math
 import torch
 
 from . import _lib
-from ._lib import AttnParams, PtrRefParams, PtrScoreParams, StatsParams, call, query
+from ._lib import PTR_LOGITS_SCRATCH, AttnParams, PtrRefParams, PtrScoreParams, StatsParams, call, query
 
 BIAS_MODES = {"none": 0, "block": 1, "token": 2}
 GATE_KINDS = {"none": 0, "softplus": 1, "relu": 2}
@@ -163,6 +163,8 @@ def pointer_select(ds_ptr: torch.Tensor, ds_local: torch.Tensor, *, bs: int, NB:
     # MFMA into the logits buffer before the selection reads them: give it one
     gemm = logits_in is None and qbar is not None and D == 128 and NB >= LOGITS_GEMM_NB
     logits = torch.empty((H, NB, NB), dtype=torch.float32, device=dev) if (return_logits or gemm) else None
+    # a buffer only the library reads: its non-candidate entries are not set to -inf
+    prm.flags = PTR_LOGITS_SCRATCH if (gemm and not return_logits) else 0
     call("scope_pointer_select", C.byref(prm), _p(_f32(qbar)), _p(_f32(kbar)), _p(_f32(logits_in)), _p(prior),
          _p(_f32(gumbel_u) if noise_mode == 1 else None), _p(_i32(ds_ptr)), _p(_i32(ds_local)), _p(kv_num),
          _p(kv_idx), _p(picks), _p(logits), _stream(dev))

@@ -288,7 +288,7 @@ def test_c5_h8_layer():
     step()
     torch.cuda.synchronize()
     print(f"  layer done (N_act {int(step.last['kv_num'].sum())})", flush=True)
-    # the selection over 4096 candidates (logits on fp32 MFMA at this length):
+    # the selection over 4096 candidates (logits on bf16 MFMA from the split means at this length):
     # the step's lists again with the logits returned, each sampled row's
     # logits within 1e-4·(1 + |ref|) of fp64 from the block means, and heads
     # 0 and H-1 equal to the oracle's selection on those logits

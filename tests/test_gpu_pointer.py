@@ -179,9 +179,11 @@ def test_pointer_select_gumbel_exact(noise):
     assert np.array_equal(kv_idx.cpu().numpy(), ref["packed"])
 
 
-@pytest.mark.parametrize("H,T,bs", [(6, 4096, 128), (8, 131072, 256)])
+@pytest.mark.parametrize("H,T,bs", [(6, 4096, 128), (8, 131072, 256), (4, 131072, 128), (2, 140800, 128)])
 def test_block_means_and_logits(H, T, bs):
-    """Fused block means + q̄·k̄ logits vs fp64; selection exact given the kernel's logits."""
+    """Fused block means + q̄·k̄ logits vs fp64; selection exact given the kernel's logits.
+    From 1024 blocks on (the last two cases; 1100 blocks is no multiple of the
+    64-block tiles) the logits come from the bf16 MFMA product of the split means."""
     from scope_amd import ops
 
     q, k, _ = qkv(H, T, seed=5)
@@ -203,7 +205,9 @@ def test_block_means_and_logits(H, T, bs):
     ds = ds_ptr.cpu().numpy()
     causal = (np.arange(NB)[None, :] <= np.arange(NB)[:, None]) & (np.arange(NB)[None, :] >= ds[:, None])
     diff = np.abs(lg - ref_lg)[:, causal]
-    assert diff.max() < 1e-4 * (1 + np.abs(ref_lg[:, causal]).max())
+    rel = (diff / (1 + np.abs(ref_lg[:, causal]))).max()
+    print(f"  NB={NB}: logits within {rel:.3g}·(1 + |ref|) of fp64", flush=True)
+    assert rel < 1e-4
     assert np.all(np.isneginf(lg[:, ~causal]))
     ref = OP.pointer_select_blockscore(lg, docs.numpy(), bs=bs, window=2, n_global=1, budget=4)
     assert np.array_equal(picks.cpu().numpy(), ref["picks"])
