@@ -214,6 +214,47 @@ def test_block_means_and_logits(H, T, bs):
     assert np.array_equal(kv_idx.cpu().numpy(), ref["packed"])
 
 
+@pytest.mark.parametrize("H,T,bs,budget,noise,n_docs", [(4, 131072, 128, 4, "counter", 3), (2, 140800, 128, 8, "counter", 1),
+                                                         (2, 140800, 128, 2, "none", 5), (2, 262144, 256, 8, "uniform", 2),
+                                                         (2, 140800, 128, 12, "counter", 2)])
+def test_scratch_logits_selection_equals_logits_path(H, T, bs, budget, noise, n_docs):
+    """From 1024 blocks on, a selection whose logits the caller does not read
+    (SCOPE_PTR_LOGITS_SCRATCH: the buffer's non-candidate entries are left
+    unset) must give the picks and lists of the call that returns the
+    logits, and those must equal the oracle's selection on the returned
+    logits, for every noise mode and budgets up to 12."""
+    from scope_amd import ops
+
+    q, k, _ = qkv(H, T, seed=11)
+    NB = T // bs
+    docs = docs_with_boundaries(T, n_docs, 3).to(DEV)
+    qbar, kbar = ops.block_means(q.to(DEV), k.to(DEV), bs)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs, bs)
+    prior = torch.from_numpy((-0.05 * np.log1p(np.arange(NB))).astype(np.float32)).to(DEV)
+    gu = (torch.rand((H, NB, NB), generator=torch.Generator(device=DEV).manual_seed(4), device=DEV)
+          if noise == "uniform" else None)
+    kw = dict(bs=bs, NB=NB, H=H, window=2, n_global=1, budget=budget, qbar=qbar, kbar=kbar, prior=prior,
+              logit_scale=bs / np.sqrt(128.0), noise=noise, gumbel_u=gu, seed=99)
+    kn1, ki1, pk1 = ops.pointer_select(ds_ptr, ds_local, **kw)
+    kn2, ki2, pk2, lg = ops.pointer_select(ds_ptr, ds_local, return_logits=True, **kw)
+    torch.cuda.synchronize()
+    print(f"  NB={NB} budget={budget} noise={noise}: {int(kn1.sum())} listed blocks", flush=True)
+    assert torch.equal(pk1, pk2)
+    assert torch.equal(kn1, kn2)
+    assert torch.equal(ki1, ki2)
+    # and the logits path against the oracle's selection on those logits (head 0)
+    lg0 = lg[:1].cpu().numpy()
+    g0 = None
+    if noise == "counter":
+        qq, kk = np.meshgrid(np.arange(NB), np.arange(NB), indexing="ij")
+        g0 = OP.gumbel_from_u(OP.counter_uniform(99, np.zeros_like(qq), qq, kk))[None]
+    elif noise == "uniform":
+        g0 = OP.gumbel_from_u(gu[:1].cpu().numpy())
+    ref = OP.pointer_select_blockscore(lg0, docs.cpu().numpy(), bs=bs, window=2, n_global=1, budget=budget, gumbel=g0)
+    assert np.array_equal(pk2[:1].cpu().numpy(), ref["picks"])
+    assert np.array_equal(ki2[:1].cpu().numpy(), ref["packed"])
+
+
 def test_planted_needle_is_selected():
     """C3-style needle: a key block = 3 × a query block's mean query, ≥64
     blocks back; the noise-free selection must pick it for that q-block."""
