@@ -477,6 +477,7 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
                                                     static_cast<uint32_t>(kb));
       z = z + gumbel_of(u, P.eps);
     }
+    if (z != z) return;  // a NaN z (from NaN logits) never enters, as in the general comparison
     bool c[KB];
 #pragma unroll
     for (int i = 0; i < KB; ++i) c[i] = !(z <= tz[i]);
