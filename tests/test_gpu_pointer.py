@@ -133,16 +133,24 @@ def test_doc_starts_vs_oracle():
 # ---------------------------------------------------------------------------
 # block-scoring mode
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("H,T,bs,W,G,B,n_docs", [(6, 4096, 128, 3, 1, 2, 1), (8, 65536, 128, 4, 1, 4, 1),
-                                                 (8, 131072, 256, 2, 2, 8, 16), (2, 8192, 256, 2, 2, 16, 5)])
-def test_pointer_select_given_logits_exact(H, T, bs, W, G, B, n_docs):
+@pytest.mark.parametrize("H,T,bs,W,G,B,n_docs,ninf", [
+    (6, 4096, 128, 3, 1, 2, 1, 0), (8, 65536, 128, 4, 1, 4, 1, 0), (8, 131072, 256, 2, 2, 8, 16, 0),
+    (2, 8192, 256, 2, 2, 16, 5, 0),
+    # edges: a window as wide as the sequence, no pointer budget, one block, a
+    # document per block, and half of the logits -inf (rows with fewer finite
+    # candidates than the budget pick -inf ones in block order)
+    (2, 1024, 128, 8, 2, 3, 2, 0), (2, 2048, 128, 2, 1, 0, 3, 0), (1, 128, 128, 2, 1, 2, 1, 0),
+    (2, 4096, 128, 2, 2, 4, 32, 0), (4, 8192, 128, 2, 1, 6, 3, 1)])
+def test_pointer_select_given_logits_exact(H, T, bs, W, G, B, n_docs, ninf):
     """Selection given the same fp32 logits (with ties) is bit-exact."""
     from scope_amd import ops
 
-    print(f"select H={H} T={T} bs={bs} W={W} G={G} B={B}", flush=True)
+    print(f"select H={H} T={T} bs={bs} W={W} G={G} B={B} docs={n_docs} -inf={ninf}", flush=True)
     NB = T // bs
     rng = np.random.default_rng(T + B)
     logits = (np.round(rng.standard_normal((H, NB, NB)) * 4) / 4).astype(np.float32)  # many ties
+    if ninf:
+        logits[rng.random((H, NB, NB)) < 0.5] = -np.inf
     docs = docs_with_boundaries(T, n_docs, 3)
     ref = OP.pointer_select_blockscore(logits, docs.numpy(), bs=bs, window=W, n_global=G, budget=B, temp=0.5)
     ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
