@@ -170,6 +170,32 @@ def radius_prior(NB: int, scale: float):
     return -scale * torch.log1p(torch.arange(NB, dtype=torch.float32))
 
 
+class EventSets:
+    """One set of start/end events per recorded step, so that the recorded
+    steps run back to back, as in the timed region (no synchronisation
+    between them: a phase at the start of a step does not absorb the host's
+    launch latency), and are read after one synchronisation."""
+
+    def __init__(self, names):
+        self.names = list(names)
+        self.sets: list = []
+        self.n = 0
+
+    def next(self):
+        import torch
+
+        if self.n == len(self.sets):
+            self.sets.append({p: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                              for p in self.names})
+        ev = self.sets[self.n]
+        self.n += 1
+        return ev
+
+    def drain(self):
+        used, self.n = self.sets[:self.n], 0
+        return used
+
+
 class Step:
     """The hot path on GPU-resident inputs; phase events on the current stream."""
 
@@ -190,16 +216,14 @@ class Step:
         self.phases = ["pointer", "stats", "transpose", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv", "attn_bwd_aux"]
         if self.soft_temp > 0:
             self.phases.append("pointer_bwd")
-        self.ev = {p: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for p in self.phases}
+        # "_aux": the span of the kv-major kernels; "_means": the block means alone
+        self.evs = EventSets(self.phases + ["_aux", "_means"])
         self.acc = {p: 0.0 for p in self.phases}
-        self.aux_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        self.means_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         self.means_ms = 0.0
 
     def __call__(self, record=False):
         ops, t, bs = self.ops, self.t, self.bs
-        ev = self.ev
+        ev = self.evs.next() if record else None
 
         def mark(p, i):
             if record:
@@ -207,11 +231,9 @@ class Step:
 
         mark("pointer", 0)
         ds_ptr, ds_local, ds_tok_end = ops.doc_starts(t["docs"], bs)
-        if record:
-            self.means_ev[0].record()
+        mark("_means", 0)
         qbar, kbar = ops.block_means(t["q"], t["k"], bs)
-        if record:
-            self.means_ev[1].record()
+        mark("_means", 1)
         ls = bs / math.sqrt(t["q"].shape[-1])
         kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=self.NB, H=self.H,
                                                    window=self.window, n_global=self.n_global, budget=self.budget,
@@ -238,7 +260,6 @@ class Step:
                                 coeff_sin=t["coeff_sin"], pair_bias=pb, check=False)
         mark("attn_fwd", 1)
         # attn_bwd_dkv is the dK/dV kernel alone; attn_bwd_aux its plan and reduce kernels
-        aux = self.aux_ev
 
         def hook(phase):
             if phase == "dq":
@@ -247,13 +268,11 @@ class Step:
                 mark("attn_bwd_dq", 1)
                 mark("attn_bwd_aux", 0)
             elif phase == "dkv":
-                if record:
-                    aux[0].record()
+                mark("_aux", 0)
                 mark("attn_bwd_dkv", 0)
             elif phase == "reduce":
                 mark("attn_bwd_dkv", 1)
-                if record:
-                    aux[1].record()
+                mark("_aux", 1)
             else:
                 mark("attn_bwd_aux", 1)
 
@@ -270,11 +289,12 @@ class Step:
                          grads=grads, q_off=q_off, q_list=q_list, ds_tok_end=ds_tok_end, pair_bias=pb)
 
     def collect(self):
-        for p in self.phases:
-            self.acc[p] += self.ev[p][0].elapsed_time(self.ev[p][1])
-        # the aux span brackets the dK/dV kernel: remove it
-        self.acc["attn_bwd_aux"] -= self.aux_ev[0].elapsed_time(self.aux_ev[1])
-        self.means_ms += self.means_ev[0].elapsed_time(self.means_ev[1])
+        for ev in self.evs.drain():
+            for p in self.phases:
+                self.acc[p] += ev[p][0].elapsed_time(ev[p][1])
+            # the aux span brackets the dK/dV kernel: remove it
+            self.acc["attn_bwd_aux"] -= ev["_aux"][0].elapsed_time(ev["_aux"][1])
+            self.means_ms += ev["_means"][0].elapsed_time(ev["_means"][1])
 
 
 class SwaStep:
@@ -291,16 +311,16 @@ class SwaStep:
         self.H, self.T = self.t["q"].shape[1], self.t["q"].shape[2]
         self.NB = self.T // bs
         self.phases = ["swa_mask", "transpose", "attn_fwd", "attn_bwd"]
-        self.ev = {p: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for p in self.phases}
+        self.evs = EventSets(self.phases)
         self.acc = {p: 0.0 for p in self.phases}
 
     def __call__(self, record=False):
         ops, t, bs = self.ops, self.t, self.bs
+        ev = self.evs.next() if record else None
 
         def mark(p, i):
             if record:
-                self.ev[p][i].record()
+                ev[p][i].record()
 
         mark("swa_mask", 0)
         r = ops.swa_blockmask(t["docs"], bs, self.window)
@@ -322,8 +342,9 @@ class SwaStep:
         self.last = dict(kv_num=kv_num, kv_idx=kv_idx, out=out, lse=lse, grads=grads)
 
     def collect(self):
-        for p in self.phases:
-            self.acc[p] += self.ev[p][0].elapsed_time(self.ev[p][1])
+        for ev in self.evs.drain():
+            for p in self.phases:
+                self.acc[p] += ev[p][0].elapsed_time(ev[p][1])
 
 
 def main_swa(args):
@@ -731,10 +752,9 @@ def time_steps(step, steps, warmup):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step(record=True)
-        torch.cuda.synchronize()
-        step.collect()
+        step(record=True)  # back to back, as in the timed region
     torch.cuda.synchronize()
+    step.collect()
     return (time.perf_counter() - t0) / steps
 
 
