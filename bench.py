@@ -1100,6 +1100,10 @@ def main():
     roofline = dict(bound="mfma", kernel=kname, achieved=round(achieved, 2), peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                     frac=round(achieved / PEAK_BF16_TFLOPS, 4), traffic=traffic, traffic_source=tsrc,
                     flops_per_launch=flops, launch_ms=round(ph[dom], 4))
+    # what the kernel executes: the kv-major pass also recomputes S and dP
+    executed = 8.0 * bs * bs * D * n_act if dom == "attn_bwd_dkv" else flops
+    roofline["executed_flops_per_launch"] = executed
+    roofline["executed_achieved"] = round(executed / (ph[dom] / 1e3) / 1e12, 2)
     # the pointer path is HBM-bound: q and k read once (bf16), the document ids,
     # and the compact lists written (the byte count of the workload definition)
     maxkv = int(step.last["kv_idx"].shape[-1])
@@ -1167,6 +1171,10 @@ def main():
     res["measured_peaks"] = mp
     roofline["peak_measured"] = mp["mfma_bf16_tflops"]
     roofline["frac_of_measured"] = round(achieved / mp["mfma_bf16_tflops"], 4)
+    # the MFMA rate on random operands, at the clock the power limit leaves
+    roofline["peak_measured_random"] = mp["mfma_bf16_tflops_random"]
+    roofline["executed_frac_of_measured_random"] = round(roofline["executed_achieved"] / mp["mfma_bf16_tflops_random"],
+                                                         4)
     pointer["peak_measured"] = mp["hbm_copy_gbs"]
     pointer["block_means_frac_of_measured"] = round(pointer["block_means_achieved"] / mp["hbm_copy_gbs"], 4)
     if not train and (H, T, bs) == (8, 131072, 256) and not args.no_ref_layer:

@@ -607,10 +607,15 @@ int scope_attn_bwd_phase(const scope_attn_params* p, int phases, const uint16_t*
  * scope_probe_mfma: blocks x 4 wavefronts each run four independent bf16
  * v_mfma_f32_32x32x16 chains of iters steps, writing one float per thread to
  * out [blocks*256]; scope_probe_mfma_flops gives the FLOP count of one call.
+ * scope_probe_mfma_data: the same chains (same FLOP count) on operands from
+ * data: operands [blocks*256][16] 16-byte bf16x8 values (8 A and 8 B
+ * operands per thread, cycled); iters a multiple of 8.  With random data
+ * this is the MFMA rate under the power limit that attention operands see.
  * scope_probe_copy: streaming copy of bytes (multiple of 16, 16-byte aligned
  * buffers); 2·bytes move through HBM. */
 int64_t scope_probe_mfma_flops(int blocks, int iters);
 int scope_probe_mfma(float* out, int blocks, int iters, void* stream);
+int scope_probe_mfma_data(const void* operands, float* out, int blocks, int iters, void* stream);
 int scope_probe_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 #ifdef __cplusplus

@@ -130,6 +130,7 @@ _PROTOS = {
     "scope_attn_bwd_phase": (c_int, [C.POINTER(AttnParams), c_int] + [P] * 30),
     "scope_probe_mfma_flops": (c_int64, [c_int, c_int]),
     "scope_probe_mfma": (c_int, [P, c_int, c_int, P]),
+    "scope_probe_mfma_data": (c_int, [P, P, c_int, c_int, P]),
     "scope_probe_copy": (c_int, [P, P, c_int64, P]),
 }
 

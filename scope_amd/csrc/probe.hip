@@ -24,6 +24,37 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(float* __restrict__ out
   out[static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x] = s;
 }
 
+// The same four chains on data: each lane's A and B operands cycle through 8
+// register sets each, loaded from `ops` (16 uint4 per thread), so the MFMA
+// inputs toggle as attention operands do.  With random bf16 data the chip
+// draws more power per MFMA than with the constant operands above, and its
+// power limit lowers the clock.  iters is a multiple of 8.
+__global__ __launch_bounds__(256) void probe_mfma_data_kernel(const uint4* __restrict__ ops, float* __restrict__ out,
+                                                              int iters) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  uint4 a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = ops[t * 16 + i];
+    b[i] = ops[t * 16 + 8 + i];
+  }
+  f32x16_t c0 = zero16(), c1 = zero16(), c2 = zero16(), c3 = zero16();
+  for (int i = 0; i < iters; i += 8) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const uint4 bb = b[(s + 3) & 7];
+      c0 = mfma32(a[s], bb, c0);
+      c1 = mfma32(a[(s + 1) & 7], bb, c1);
+      c2 = mfma32(a[(s + 2) & 7], bb, c2);
+      c3 = mfma32(a[(s + 5) & 7], bb, c3);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s += c0[r] + c1[r] + c2[r] + c3[r];
+  out[t] = s;
+}
+
 // Streaming copy, 16 bytes per lane per step, grid-stride.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void probe_copy_kernel(const u32x4_t* __restrict__ src, u32x4_t* __restrict__ dst,
@@ -46,6 +77,15 @@ extern "C" int scope_probe_mfma(float* out, int blocks, int iters, void* stream)
   SCOPE_REQUIRE(out && blocks > 0 && iters > 0, "scope_probe_mfma: bad arguments");
   hipLaunchKernelGGL(probe_mfma_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), out, iters);
   return check_launch("probe_mfma_kernel");
+}
+
+extern "C" int scope_probe_mfma_data(const void* operands, float* out, int blocks, int iters, void* stream) {
+  SCOPE_REQUIRE(operands && out && blocks > 0 && iters > 0 && iters % 8 == 0,
+                "scope_probe_mfma_data: bad arguments (iters must be a positive multiple of 8)");
+  SCOPE_REQUIRE((reinterpret_cast<uintptr_t>(operands) & 15) == 0, "scope_probe_mfma_data: 16-byte aligned operands");
+  hipLaunchKernelGGL(probe_mfma_data_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint4*>(operands), out, iters);
+  return check_launch("probe_mfma_data_kernel");
 }
 
 extern "C" int scope_probe_copy(const void* src, void* dst, int64_t bytes, void* stream) {

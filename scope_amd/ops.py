@@ -1010,8 +1010,10 @@ def log2e() -> float:
 def measure_peaks(device: torch.device | str = "cuda", *, mfma_iters: int = 16384, copy_mib: int = 1024,
                   repeats: int = 5) -> dict:
     """Measured ceilings on this GPU: bf16 dense MFMA TFLOP/s (independent
-    32x32x16 chains on every SIMD) and HBM copy GB/s (2 x bytes per copy).
-    The best of `repeats` timed launches is reported."""
+    32x32x16 chains on every SIMD) on constant operands and on random bf16
+    operands in [-1, 1) (which draw the power attention's operands draw, so
+    the power limit lowers the clock), and HBM copy GB/s (2 x bytes per
+    copy).  The best of `repeats` timed launches is reported."""
     dev = torch.device(device)
     _gpu("measure_peaks", torch.empty(1, device=dev))
     lib = _lib.load()
@@ -1020,6 +1022,8 @@ def measure_peaks(device: torch.device | str = "cuda", *, mfma_iters: int = 1638
     blocks = props.multi_processor_count * 2  # 8 wavefronts per CU: 2 per SIMD
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
     flops = lib.scope_probe_mfma_flops(blocks, mfma_iters)
+    g = torch.Generator(device=dev).manual_seed(7)
+    ops_rnd = (torch.rand((blocks * 256, 16, 8), generator=g, device=dev) * 2 - 1).to(torch.bfloat16)
     src = torch.ones(copy_mib << 18, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     nbytes = src.numel() * 4
@@ -1037,7 +1041,11 @@ def measure_peaks(device: torch.device | str = "cuda", *, mfma_iters: int = 1638
         return min(ts)
 
     t_mfma = best(lambda: call("scope_probe_mfma", _p(out), blocks, mfma_iters, st))
+    it8 = mfma_iters // 8 * 8
+    t_data = best(lambda: call("scope_probe_mfma_data", _p(ops_rnd), _p(out), blocks, it8, st))
     t_copy = best(lambda: call("scope_probe_copy", _p(src), _p(dst), nbytes, st))
-    return dict(mfma_bf16_tflops=round(flops / t_mfma / 1e12, 1), hbm_copy_gbs=round(2 * nbytes / t_copy / 1e9, 1),
+    return dict(mfma_bf16_tflops=round(flops / t_mfma / 1e12, 1),
+                mfma_bf16_tflops_random=round(lib.scope_probe_mfma_flops(blocks, it8) / t_data / 1e12, 1),
+                hbm_copy_gbs=round(2 * nbytes / t_copy / 1e9, 1),
                 mfma_probe=f"{blocks} workgroups x 4 wavefronts x 4 chains x {mfma_iters} steps",
                 copy_probe=f"{copy_mib} MiB copy (read + write)")
