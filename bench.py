@@ -744,6 +744,52 @@ def graph_step_time(layer, q, k, v, dout, one, steps: int, params=()) -> dict:
         return dict(ms=None, check=f"not captured: {type(ex).__name__}: {ex}"[:200])
 
 
+def graph_time_layer(step, steps: int) -> dict:
+    """ms per step of the headline step replayed from one captured HIP graph
+    (no host launches between the ~40 kernels), and whether every checked
+    replay's lists, output, LSE and gradients equal an eager step's bit for
+    bit."""
+    import torch
+
+    keys = ("kv_num", "kv_idx", "out", "lse")
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        cap = dict(step.last)
+        step()  # eager, fresh tensors
+        torch.cuda.synchronize()
+        ref = dict(step.last)
+
+        def same():
+            a = [cap[k_] for k_ in keys] + [cap["grads"][n_] for n_ in ("dq", "dk", "dv")]
+            b = [ref[k_] for k_ in keys] + [ref["grads"][n_] for n_ in ("dq", "dk", "dv")]
+            return all(bool(torch.equal(x, y)) for x, y in zip(a, b))
+
+        ok = True
+        for _ in range(3):  # replays with eager work and synchronisations between them
+            g.replay()
+            torch.cuda.synchronize()
+            ok = ok and same()
+            step()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return dict(ms=round(e0.elapsed_time(e1) / steps, 4), check="equal to eager" if ok else "DIFFERS from eager")
+    except Exception as ex:  # capture not possible here: report why, keep the eager numbers
+        return dict(ms=None, check=f"not captured: {type(ex).__name__}: {ex}"[:200])
+
+
 def time_steps(step, steps, warmup):
     import torch
 
@@ -1155,6 +1201,12 @@ def main():
         "roofline": roofline,
         "pointer_roofline": pointer,
     }
+    # the same step replayed from one captured HIP graph (an extra: `value`
+    # stays the eager step's)
+    graph = graph_time_layer(step, args.steps)
+    res["graph_ms_per_step"] = graph["ms"]
+    res["graph_tflops"] = round((F_fwd + F_bwd) / graph["ms"] / 1e9, 2) if graph["ms"] else None
+    res["graph_check"] = graph["check"]
     if args.sweep:
         sweep = {}
         for b in (2, 4):
