@@ -1041,7 +1041,7 @@ def measure_peaks(device: torch.device | str = "cuda", *, mfma_iters: int = 1638
         return min(ts)
 
     t_mfma = best(lambda: call("scope_probe_mfma", _p(out), blocks, mfma_iters, st))
-    it8 = mfma_iters // 8 * 8
+    it8 = max(8, mfma_iters // 8 * 8)  # the data probe's steps come in groups of 8
     t_data = best(lambda: call("scope_probe_mfma_data", _p(ops_rnd), _p(out), blocks, it8, st))
     t_copy = best(lambda: call("scope_probe_copy", _p(src), _p(dst), nbytes, st))
     return dict(mfma_bf16_tflops=round(flops / t_mfma / 1e12, 1),
