@@ -230,9 +230,10 @@ class Step:
                 ev[p][i].record()
 
         mark("pointer", 0)
-        ds_ptr, ds_local, ds_tok_end = ops.doc_starts(t["docs"], bs)
+        # block means with the document starts folded in (the per-block phase
+        # rides on the block-means pass, then the scan)
         mark("_means", 0)
-        qbar, kbar = ops.block_means(t["q"], t["k"], bs)
+        qbar, kbar, ds_ptr, ds_local, ds_tok_end = ops.block_means_docs(t["q"], t["k"], t["docs"], bs)
         mark("_means", 1)
         ls = bs / math.sqrt(t["q"].shape[-1])
         kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=self.NB, H=self.H,

@@ -97,6 +97,14 @@ int scope_pointer_mask_ref(const scope_ptr_ref_params* p, const float* delta_sta
 int scope_block_means(const uint16_t* q, const uint16_t* k, int H, int64_t T, int D, int bs,
                       int64_t q_sh, int64_t q_st, int64_t k_sh, int64_t k_st, float* qbar,
                       float* kbar, void* stream);
+/* scope_block_means and scope_doc_starts in two launches instead of three:
+ * the per-block document phase runs inside the block-means pass (on head
+ * 0's workgroups), then the scan.  The same outputs, bit for bit, as the two
+ * calls; T < 2^31. */
+int scope_block_means_docs(const uint16_t* q, const uint16_t* k, const int32_t* docs, int H, int64_t T,
+                           int D, int bs, int64_t q_sh, int64_t q_st, int64_t k_sh, int64_t k_st,
+                           int doc_clamp, int reset_len, float* qbar, float* kbar, int32_t* ds_ptr,
+                           int32_t* ds_local, int32_t* ds_tok_end, void* stream);
 
 typedef struct {
   int H, NB, D, bs;

@@ -88,6 +88,8 @@ _PROTOS = {
     "scope_ptr_ref_maxkv": (c_int, [C.POINTER(PtrRefParams)]),
     "scope_pointer_mask_ref": (c_int, [C.POINTER(PtrRefParams), P, P, P, P, P, P, P, P, P, P]),
     "scope_block_means": (c_int, [P, P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int64, c_int64, P, P, P]),
+    "scope_block_means_docs": (c_int, [P, P, P, c_int, c_int64, c_int, c_int, c_int64, c_int64, c_int64, c_int64,
+                                       c_int, c_int, P, P, P, P, P, P]),
     "scope_pointer_select": (c_int, [C.POINTER(PtrScoreParams), P, P, P, P, P, P, P, P, P, P, P, P]),
     "scope_pointer_pair_bias": (c_int, [C.POINTER(PtrScoreParams), c_float, P, P, P, P, P, P, P, P, P]),
     "scope_pointer_bwd_workspace_bytes": (c_int64, [C.POINTER(PtrBwdParams)]),

@@ -346,12 +346,19 @@ __global__ __launch_bounds__(256) void ptr_ref_kernel(RefLaunch A, const float* 
 // ---------------------------------------------------------------------------
 // block means
 // ---------------------------------------------------------------------------
+// With docs (scope_block_means_docs), the workgroups of head 0 also do the
+// first phase of the document starts for their block (doc_blocks_kernel's
+// work): the last change point inside it into last_change[b], whether its
+// first token is one into first_change[b].
 template <int D>
 __global__ __launch_bounds__(256) void block_means_kernel(const uint16_t* __restrict__ q,
                                                            const uint16_t* __restrict__ k, int bs,
                                                            int64_t q_sh, int64_t q_st, int64_t k_sh,
                                                            int64_t k_st, int NB, float* __restrict__ qbar,
-                                                           float* __restrict__ kbar) {
+                                                           float* __restrict__ kbar,
+                                                           const int32_t* __restrict__ docs = nullptr,
+                                                           int32_t* __restrict__ last_change = nullptr,
+                                                           int32_t* __restrict__ first_change = nullptr) {
   constexpr int kChunks = D / 8;        // 16-byte chunks per row
   constexpr int kGroups = 256 / kChunks;  // row groups
   __shared__ float red[2][kGroups][D + 4];
@@ -390,6 +397,24 @@ __global__ __launch_bounds__(256) void block_means_kernel(const uint16_t* __rest
     for (int gg = 0; gg < kGroups; ++gg) s += red[which][gg][d];
     float* out = which ? kbar : qbar;
     out[(static_cast<int64_t>(h) * NB + b) * D + d] = s / static_cast<float>(bs);
+  }
+  if (docs && h == 0) {
+    // the block's last change point: the maximum over the tokens, per
+    // wavefront by shuffles, then over the four wavefronts
+    __shared__ int wbest[4];
+    int best = -1;
+    for (int i = threadIdx.x; i < bs; i += 256) {
+      const int64_t t = t0 + i;
+      if (t == 0 || docs[t] != docs[t - 1]) best = max(best, static_cast<int>(t));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) best = max(best, __shfl_xor(best, o, 64));
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      last_change[b] = max(max(wbest[0], wbest[1]), max(wbest[2], wbest[3]));
+      first_change[b] = (t0 == 0 || docs[t0] != docs[t0 - 1]) ? 1 : 0;
+    }
   }
 }
 
@@ -1012,22 +1037,46 @@ int scope_pointer_mask_ref(const scope_ptr_ref_params* p, const float* delta_sta
   return check_launch("ptr_ref_kernel");
 }
 
-int scope_block_means(const uint16_t* q, const uint16_t* k, int H, int64_t T, int D, int bs, int64_t q_sh,
-                      int64_t q_st, int64_t k_sh, int64_t k_st, float* qbar, float* kbar, void* stream) {
-  SCOPE_REQUIRE(q && k && qbar && kbar, "scope_block_means: null pointer");
-  SCOPE_REQUIRE(D == 64 || D == 128, "scope_block_means: D=%d (supported: 64, 128)", D);
-  SCOPE_REQUIRE(bs > 0 && T % bs == 0, "scope_block_means: T=%lld not a multiple of bs=%d", (long long)T, bs);
+static int block_means_launch(const char* who, const uint16_t* q, const uint16_t* k, int H, int64_t T, int D, int bs,
+                              int64_t q_sh, int64_t q_st, int64_t k_sh, int64_t k_st, float* qbar, float* kbar,
+                              const int32_t* docs, int32_t* last_change, int32_t* first_change, hipStream_t st) {
+  SCOPE_REQUIRE(q && k && qbar && kbar, "%s: null pointer", who);
+  SCOPE_REQUIRE(D == 64 || D == 128, "%s: D=%d (supported: 64, 128)", who, D);
+  SCOPE_REQUIRE(bs > 0 && T > 0 && T % bs == 0, "%s: T=%lld not a positive multiple of bs=%d", who, (long long)T, bs);
   SCOPE_REQUIRE(q_st % 8 == 0 && k_st % 8 == 0 && q_sh % 8 == 0 && k_sh % 8 == 0,
-                "scope_block_means: strides must keep 16-byte row alignment");
+                "%s: strides must keep 16-byte row alignment", who);
   const int NB = static_cast<int>(T / bs);
   dim3 grid(NB, H);
   if (D == 128)
-    hipLaunchKernelGGL(block_means_kernel<128>, grid, dim3(256), 0, as_stream(stream), q, k, bs, q_sh, q_st, k_sh,
-                       k_st, NB, qbar, kbar);
+    hipLaunchKernelGGL(block_means_kernel<128>, grid, dim3(256), 0, st, q, k, bs, q_sh, q_st, k_sh, k_st, NB, qbar,
+                       kbar, docs, last_change, first_change);
   else
-    hipLaunchKernelGGL(block_means_kernel<64>, grid, dim3(256), 0, as_stream(stream), q, k, bs, q_sh, q_st, k_sh,
-                       k_st, NB, qbar, kbar);
+    hipLaunchKernelGGL(block_means_kernel<64>, grid, dim3(256), 0, st, q, k, bs, q_sh, q_st, k_sh, k_st, NB, qbar,
+                       kbar, docs, last_change, first_change);
   return check_launch("block_means_kernel");
+}
+
+int scope_block_means(const uint16_t* q, const uint16_t* k, int H, int64_t T, int D, int bs, int64_t q_sh,
+                      int64_t q_st, int64_t k_sh, int64_t k_st, float* qbar, float* kbar, void* stream) {
+  return block_means_launch("scope_block_means", q, k, H, T, D, bs, q_sh, q_st, k_sh, k_st, qbar, kbar, nullptr,
+                            nullptr, nullptr, as_stream(stream));
+}
+
+int scope_block_means_docs(const uint16_t* q, const uint16_t* k, const int32_t* docs, int H, int64_t T, int D, int bs,
+                           int64_t q_sh, int64_t q_st, int64_t k_sh, int64_t k_st, int doc_clamp, int reset_len,
+                           float* qbar, float* kbar, int32_t* ds_ptr, int32_t* ds_local, int32_t* ds_tok_end,
+                           void* stream) {
+  SCOPE_REQUIRE(docs && ds_ptr && ds_local && ds_tok_end, "scope_block_means_docs: null pointer");
+  SCOPE_REQUIRE(T < (1ll << 31), "scope_block_means_docs: T=%lld exceeds int32 token indices", (long long)T);
+  hipStream_t st = as_stream(stream);
+  // the document-block phase rides on head 0's workgroups; its outputs go
+  // where doc_scan_kernel reads them (ds_tok_end, ds_local)
+  int rc = block_means_launch("scope_block_means_docs", q, k, H, T, D, bs, q_sh, q_st, k_sh, k_st, qbar, kbar, docs,
+                              ds_tok_end, ds_local, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(doc_scan_kernel, dim3(1), dim3(1024), 0, st, static_cast<int>(T / bs), bs, doc_clamp, reset_len,
+                     ds_ptr, ds_local, ds_tok_end);
+  return check_launch("doc_scan_kernel");
 }
 
 // compute units of the current device (one persistent workgroup each), per device

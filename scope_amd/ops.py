@@ -139,6 +139,29 @@ def block_means(q: torch.Tensor, k: torch.Tensor, bs: int):
     return qbar, kbar
 
 
+def block_means_docs(q: torch.Tensor, k: torch.Tensor, docs: torch.Tensor, bs: int, *, doc_clamp: bool = True,
+                     reset_len: int = 0):
+    """``block_means`` and ``doc_starts`` in one call with one launch fewer
+    (``scope_block_means_docs``) -> (q̄, k̄, ds_ptr, ds_local, ds_tok_end)."""
+    dev = _gpu("block_means_docs", q, k, docs)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise RuntimeError("block_means_docs: q and k must be bfloat16")
+    H, T, D, qsh, qst = _bhtd("block_means_docs q", q)
+    _, Tk, _, ksh, kst = _bhtd("block_means_docs k", k)
+    docs = _i32(docs.reshape(-1))
+    if Tk != T or docs.numel() != T:
+        raise RuntimeError(f"block_means_docs: q has {T} tokens, k {Tk}, docs {docs.numel()}")
+    if T % bs:
+        raise RuntimeError(f"block_means_docs: T={T} not a multiple of bs={bs}")
+    NB = T // bs
+    qbar = torch.empty((H, NB, D), dtype=torch.float32, device=dev)
+    kbar = torch.empty((H, NB, D), dtype=torch.float32, device=dev)
+    ds = [torch.empty(NB, dtype=torch.int32, device=dev) for _ in range(3)]
+    call("scope_block_means_docs", _p(q), _p(k), _p(docs), H, T, D, bs, qsh, qst, ksh, kst, int(bool(doc_clamp)),
+         int(max(0, reset_len)), _p(qbar), _p(kbar), _p(ds[0]), _p(ds[1]), _p(ds[2]), _stream(dev))
+    return qbar, kbar, ds[0], ds[1], ds[2]
+
+
 def pointer_select(ds_ptr: torch.Tensor, ds_local: torch.Tensor, *, bs: int, NB: int, H: int, window: int,
                    n_global: int, budget: int, qbar: torch.Tensor | None = None, kbar: torch.Tensor | None = None,
                    logits_in: torch.Tensor | None = None, prior: torch.Tensor | None = None, temp: float = 1.0,
