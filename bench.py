@@ -1087,7 +1087,7 @@ def cpu_reference_path_c1(seconds: float):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the SCOPE hot path is sharded by head across GPUs "
+        print(json.dumps({"error": "bench.py measures one GPU: the SCOPE hot path is sharded by head across GPUs "
                                    "(no exchange inside the layer), multi-GPU runs are out of scope",
                           "n_gpus": args.gpus}))
         sys.exit(1)

@@ -89,7 +89,7 @@ int scope_pointer_mask_ref(const scope_ptr_ref_params* p, const float* delta_sta
 
 /* ------------------------------------------------------------------------
  * Block-scoring pointer selection (block-mean q·k + radius prior + Gumbel
- * top-k under a budget; the BASELINE specification of kernel 1).  Produces
+ * top-k under a budget: the block-scoring form of the pointer kernel).  Produces
  * the same (kv_num, kv_idx) layout as build_pointer_blockmask
  * (model/attn_bias.py:825-837) for the union window ∪ pointers ∪ global.
  * ---------------------------------------------------------------------- */

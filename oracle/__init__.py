@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in ``scope_amd`` imports this package:
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` use it, and there only as the checker (or as the timed CPU
+``bench.py`` use it, and there only to check results (or as the timed CPU
 baseline), never as a fallback for the GPU path.
 
 Modules:

@@ -19,7 +19,7 @@ Bias modes:
       + slope(i)·Δ·[use_slope] - λ·gate((|Δ - Δmain(i)| - width(i))/τ)
   with gate = softplus | relu | none.  The reference evaluates cos/sin from
   bf16 tables (model/attn_bias.py:336-337); the oracle uses exact fp64.
-* block (BASELINE configuration semantics), r = qb(i) - kb(j):
+* block (the block-offset bias of the benchmark workloads), r = qb(i) - kb(j):
       Σ_k A_k(i) cos(ω_k r) + B_k(i) sin(ω_k r)
 
 Parity pins (tests/test_oracle_attention.py): torch's own eager

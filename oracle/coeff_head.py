@@ -25,8 +25,8 @@ Parity pins (tests/test_host.py): vectors recorded from the reference's own
 module (``tests/golden/make_reference_vectors.py``), in eval mode and in
 training mode with every regulariser together and alone, including the
 gradients of the outputs and of reg_loss with respect to q and the MLP
-weights.  Runs on any torch device (the GPU tests use it as the checker of the
-fused kernels at sizes the CPU would take minutes over).
+weights.  Runs on any torch device (the GPU tests compare the fused kernels
+with it at sizes the CPU would take minutes over).
 """
 from __future__ import annotations
 

@@ -10,8 +10,9 @@ from oracle import pointer as OP
 
 
 def tol_check(got: torch.Tensor, ref: torch.Tensor, atol: float = 2e-2, rtol: float = 1e-2) -> tuple[bool, float]:
-    """|got - ref| <= atol + rtol·|ref| elementwise (
-    2e-2 max-abs / 1e-2 relative); returns (ok, max violation ratio)."""
+    """|got - ref| <= atol + rtol·|ref| elementwise (the parity bar of the
+    attention outputs and gradients: 2e-2 max-abs / 1e-2 relative); returns
+    (ok, max violation ratio)."""
     got = got.double().cpu()
     ref = ref.double().cpu()
     both_inf = torch.isinf(got) & torch.isinf(ref) & (torch.sign(got) == torch.sign(ref))

@@ -1,6 +1,6 @@
 """bench.py's command line on the host: the arguments the driver passes
 parse, and a request for more than one GPU exits with a JSON line that says
-this build measures one GPU (nothing is launched)."""
+the bench measures one GPU (nothing is launched)."""
 from __future__ import annotations
 
 import json

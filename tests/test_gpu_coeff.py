@@ -141,7 +141,7 @@ def test_fused_head_matches_torch_steps_at_training_shape():
         a, b = out_f[i].float(), out_h[i].float()
         tol = 1e-4 * b.abs().max().item() + 1e-4 * b.abs()
         assert ((a - b).abs() <= tol).all(), f"{n}: max err {(a - b).abs().max().item():.3e}"
-    out_t = coeff_head_forward(sb, q2)  # the oracle, as the checker, on the same GPU
+    out_t = coeff_head_forward(sb, q2)  # the oracle, on the same GPU
     for i, n in enumerate(NAMES):
         a, b = out_f[i].float(), out_t[i].float()
         tol = 2.0 ** -6 * b.abs().max().item() + 2.0 ** -6 * b.abs()
