@@ -1,5 +1,4 @@
-"""bench.py's command line on the host: the arguments the driver passes
-parse, and a request for more than one GPU exits with a JSON line that says
+"""bench.py's command line on the host: the usual arguments parse, and a request for more than one GPU exits with a JSON line that says
 the bench measures one GPU (nothing is launched)."""
 from __future__ import annotations
 
