@@ -1026,10 +1026,6 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
                 dwidth=dwd, dpair_bias=dpb)
 
 
-def log2e() -> float:
-    return 1.0 / math.log(2.0)
-
-
 def measure_peaks(device: torch.device | str = "cuda", *, mfma_iters: int = 16384, copy_mib: int = 1024,
                   repeats: int = 5) -> dict:
     """Measured ceilings on this GPU: bf16 dense MFMA TFLOP/s (independent
