@@ -6,7 +6,6 @@ GPU tensors; there is no CPU path.
 from __future__ import annotations
 
 import ctypes as C
-import math
 
 import torch
 
