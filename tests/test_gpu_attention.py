@@ -3,8 +3,6 @@ against the fp64 dense-masked oracle.  Bar (written in every comparison):
 |got - ref| <= 2e-2 + 1e-2·|ref| elementwise, for outputs, LSE and gradients."""
 from __future__ import annotations
 
-import math
-
 import pytest
 import torch
 

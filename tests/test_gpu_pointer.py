@@ -9,7 +9,7 @@ import torch
 
 from oracle import pointer as OP
 from oracle import stats as OS
-from tests.golden import load_cases, pointer_case_args, pointer_case_reps
+from tests.golden import load_cases
 from tests.helpers import docs_with_boundaries, qkv
 
 pytestmark = pytest.mark.gpu

@@ -7,8 +7,6 @@ v_mfma_f32_32x32x16_bf16 (lane l holds row/column l % 32, k = 8·(l // 32)
 .. +7)."""
 from __future__ import annotations
 
-import ctypes as C
-
 import numpy as np
 import pytest
 import torch

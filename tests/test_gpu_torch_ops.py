@@ -19,7 +19,6 @@ import math
 import pytest
 import torch
 
-import scope_amd
 from scope_amd import SpectralBias, SpectralTerms, library, scope_attention
 
 pytestmark = pytest.mark.gpu

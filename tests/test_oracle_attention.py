@@ -7,7 +7,6 @@ import math
 import warnings
 
 import numpy as np
-import pytest
 import torch
 import torch.nn.functional as F
 
