@@ -14,7 +14,8 @@ Operators (schemas are the decorated signatures below):
 
 * ``scope::doc_starts``, ``scope::pointer_mask_ref`` — build_pointer_blockmask
   (model/attn_bias.py:623-873), reference mode;
-* ``scope::block_means``, ``scope::pointer_select`` — block-scoring selection;
+* ``scope::block_means`` (or ``scope::block_means_docs``, with the document
+  starts folded in), ``scope::pointer_select`` — block-scoring selection;
 * ``scope::soft_pointer_bias`` (+ autograd via ``scope::soft_pointer_bwd``),
   ``scope::pair_bias_from_logits``;
 * ``scope::transpose_blocks`` — BlockMask.from_kv_blocks' q lists
@@ -126,6 +127,20 @@ def block_means(q: Tensor, k: Tensor, bs: int) -> tuple[Tensor, Tensor]:
 def _(q, k, bs):
     H, T, D = _bht(q)
     return q.new_empty((H, T // bs, D), dtype=_F32), q.new_empty((H, T // bs, D), dtype=_F32)
+
+
+@torch.library.custom_op(f"{_NS}::block_means_docs", mutates_args=())
+def block_means_docs(q: Tensor, k: Tensor, docs: Tensor, bs: int, doc_clamp: bool,
+                     reset_len: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    return ops.block_means_docs(q, k, docs, bs, doc_clamp=doc_clamp, reset_len=reset_len)
+
+
+@block_means_docs.register_fake
+def _(q, k, docs, bs, doc_clamp, reset_len):
+    H, T, D = _bht(q)
+    NB = T // bs
+    means = tuple(q.new_empty((H, NB, D), dtype=_F32) for _ in range(2))
+    return means + tuple(docs.new_empty(NB, dtype=_I32) for _ in range(3))
 
 
 @torch.library.custom_op(f"{_NS}::pointer_select", mutates_args=())

@@ -464,10 +464,13 @@ class SpectralBias(nn.Module):
         H = q.shape[1]
         NB = T // block_size
         docs32 = docs.to(torch.int32)
-        ds_ptr, ds_local, ds_tok_end = library.doc_starts(docs32, block_size, bool(self.pointer_doc_clamp), 0)
         qbar = kbar = None
         if logits is None:
-            qbar, kbar = library.block_means(q, k, block_size)
+            # the block means with the document starts folded in (one launch fewer)
+            qbar, kbar, ds_ptr, ds_local, ds_tok_end = library.block_means_docs(
+                q, k, docs32, block_size, bool(self.pointer_doc_clamp), 0)
+        else:
+            ds_ptr, ds_local, ds_tok_end = library.doc_starts(docs32, block_size, bool(self.pointer_doc_clamp), 0)
         if noise == "counter" and not self.training:
             noise = "none"
         scale = float(block_size) / math.sqrt(q.shape[-1]) if logit_scale is None else float(logit_scale)

@@ -54,6 +54,7 @@ def test_opcheck_selection_and_list_operators():
     NB = q.shape[2] // bs
     torch.library.opcheck(S.doc_starts.default, (docs, bs, True, 0))
     torch.library.opcheck(S.block_means.default, (q, k, bs))
+    torch.library.opcheck(S.block_means_docs.default, (q, k, docs, bs, True, 0))
     ds_ptr, ds_local, dse, qbar, kbar, kn, ki, pk = _lists(q, k, docs, bs)
     for noise, seed in ((0, 0), (2, library.seed_to_signed(2 ** 64 - 3))):
         torch.library.opcheck(S.pointer_select.default, (ds_ptr, ds_local, qbar, kbar, None, None, None, bs, NB, 2, 2,

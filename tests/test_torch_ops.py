@@ -177,7 +177,7 @@ def test_layer_exports_as_one_graph():
     assert "scope.attn_fwd.default" in targets and "scope.spectral_table.default" in targets
     # the mask build runs under no_grad: its operators sit in the wrapped submodule
     sub = "".join(str(m.code) for _, m in ep.graph_module.named_modules())
-    for n in ("doc_starts", "block_means", "pointer_select"):
+    for n in ("block_means_docs", "pointer_select"):
         assert f"torch.ops.scope.{n}.default" in sub, n
 
 
@@ -226,7 +226,7 @@ def test_forward_backward_traces_through_the_autograd_formulas():
         gm = make_fx(f)(q, k, v, cc, cs)
     targets = [str(n.target) for n in gm.graph.nodes if n.op == "call_function"]
     order = [t.split(".")[1] for t in targets if t.startswith("scope.")]
-    assert order == ["doc_starts", "block_means", "pointer_select", "spectral_table", "transpose_blocks", "attn_fwd",
+    assert order == ["block_means_docs", "pointer_select", "spectral_table", "transpose_blocks", "attn_fwd",
                      "attn_bwd"], order
 
 
