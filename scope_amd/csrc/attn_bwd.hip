@@ -16,7 +16,7 @@
 // units), and in the token modes each row's offset without the pair bias
 // (-β·b0 - lse) and β·slope: pass B copies those of a query tile into LDS
 // with the tile instead of recomputing them in every wavefront.
-// Plan: per key block, its q-list is cut into chunks of kChunk q-blocks.
+// Plan: per key block, its q-list is cut into chunks of 32 or 64 q-blocks.
 // Pass B (kv-major, one workgroup per (head, 128 keys of a key block, chunk)):
 //   dK, dV over the q-list; a block with one chunk writes bf16 directly,
 //   longer lists write fp32 partials that a reduce kernel sums in chunk order
@@ -33,11 +33,14 @@
 
 namespace scope {
 
-// q-blocks per dK/dV work item: q-lists of up to kChunk entries (the window,
-// the pointer picks and the global blocks of documents up to kChunk blocks
+// q-blocks per dK/dV work item: q-lists of up to one chunk (the window, the
+// pointer picks and the global blocks of documents up to a chunk of blocks
 // long) are one item and write bf16 directly; only longer lists pay for fp32
-// partials and their reduce
-constexpr int kChunk = 32;
+// partials and their reduce.  32 q-blocks keep the items short where a head
+// has few blocks; from 2048 blocks per head, 64 halve the partials and their
+// reduce for the global blocks that every q-block of a long document lists.
+constexpr int kChunkMax = 64;
+__host__ __device__ __forceinline__ int bwd_chunk(int QB) { return QB >= 2048 ? 64 : 32; }
 
 // ---------------------------------------------------------------------------
 // pass A
@@ -384,7 +387,7 @@ __global__ __launch_bounds__(2 * BS) void attn_bwd_dq2_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // plan: chunked work items for the kv-major pass
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, const int32_t* __restrict__ q_off,
+__global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, int chunk, const int32_t* __restrict__ q_off,
                                                          int32_t* __restrict__ items_start,
                                                          int32_t* __restrict__ slots_start,
                                                          int32_t* __restrict__ multi) {
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(1024) void bwd_plan_kernel(int NB, const int32_t* _
     int nit = 0, nsl = 0, nml = 0;
     if (kb < NB) {
       const int n = off[kb + 1] - off[kb];
-      const int nch = max(1, (n + kChunk - 1) / kChunk);
+      const int nch = max(1, (n + chunk - 1) / chunk);
       nit = nch;
       nsl = nch > 1 ? nch : 0;
       nml = nch > 1 ? 1 : 0;
@@ -454,6 +457,7 @@ struct KvPlan {
   float* part_dv;
   int64_t max_slots;  // per head
   int max_items;      // work items per head (upper bound)
+  int chunk;          // q-blocks per work item (bwd_chunk)
 };
 
 // q_pos[h][i] = the position of key block kb in the kv list of q-block
@@ -739,10 +743,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
 
   __shared__ DkvBuf<MODE> buf0, buf1;
   __shared__ __attribute__((aligned(16))) float offw[4][BM];
-  __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunk * 16 : 4];
-  __shared__ int qbs[kChunk], dse[kChunk], epos[kChunk];
-  __shared__ float ebias[kChunk];
-  __shared__ float pslot[kChunk][4];  // pair-bias gradient: per entry and wavefront
+  __shared__ __attribute__((aligned(16))) float tabs[MODE == 1 ? kChunkMax * 16 : 4];
+  __shared__ int qbs[kChunkMax], dse[kChunkMax], epos[kChunkMax];
+  __shared__ float ebias[kChunkMax];
+  __shared__ float pslot[kChunkMax][4];  // pair-bias gradient: per entry and wavefront
 
   constexpr int P = BS / 128;  // workgroups (128 keys each) per key block
   const int NB = a.QB;
@@ -770,8 +774,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
   const int chunk = x - its[kb];
   const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
   const int nq = qo[kb + 1] - qo[kb];
-  const int nch = max(1, (nq + kChunk - 1) / kChunk);
-  const int i0 = chunk * kChunk, i1 = min(nq, i0 + kChunk);
+  const int CH = pl.chunk;
+  const int nch = max(1, (nq + CH - 1) / CH);
+  const int i0 = chunk * CH, i1 = min(nq, i0 + CH);
   const int ne = max(0, i1 - i0);
   const int32_t* ql = a.q_list + static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb];
 
@@ -802,7 +807,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(AttnArgs a, KvPlan pl
     ebias[tid] = eb;
     epos[tid] = pos;
   }
-  for (int t = tid; DP && t < kChunk * 4; t += blockDim.x) pslot[t / 4][t % 4] = 0.f;
+  for (int t = tid; DP && t < CH * 4; t += blockDim.x) pslot[t / 4][t % 4] = 0.f;
   // block-mode table row of distance qb - kb (clamped: a later key block is fully masked anyway)
   for (int t = tid; MODE == 1 && t < ne * 16; t += blockDim.x) {
     const int r = min(max(ql[i0 + t / 16] - kb, 0), NB - 1);
@@ -1119,8 +1124,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   constexpr int NS = BS / BM;
 
   __shared__ DkvBuf<MODE> buf0, buf1, buf2;
-  __shared__ int qbs[kChunk], dse[kChunk], epos[kChunk];
-  __shared__ float pslot[kChunk][8];  // pair-bias gradient: per entry and wavefront
+  __shared__ int qbs[kChunkMax], dse[kChunkMax], epos[kChunkMax];
+  __shared__ float pslot[kChunkMax][8];  // pair-bias gradient: per entry and wavefront
 
   constexpr int P = BS / 128;  // workgroups (128 keys each) per key block
   const int NB = a.QB;
@@ -1144,8 +1149,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
   const int chunk = x - its[kb];
   const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
   const int nq = qo[kb + 1] - qo[kb];
-  const int nch = max(1, (nq + kChunk - 1) / kChunk);
-  const int i0 = chunk * kChunk, i1 = min(nq, i0 + kChunk);
+  const int CH = pl.chunk;
+  const int nch = max(1, (nq + CH - 1) / CH);
+  const int i0 = chunk * CH, i1 = min(nq, i0 + CH);
   const int ne = max(0, i1 - i0);
   const int32_t* ql = a.q_list + static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb];
 
@@ -1168,7 +1174,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv16_kernel(AttnArgs a, KvPlan 
     // position of kb in this q-block's list: its offsets rows in roff
     epos[tid] = pl.q_pos[static_cast<int64_t>(h) * a.QB * a.maxkv + qo[kb] + i0 + tid];
   }
-  for (int t = tid; DP && t < kChunk * 8; t += blockDim.x) pslot[t / 8][t % 8] = 0.f;
+  for (int t = tid; DP && t < CH * 8; t += blockDim.x) pslot[t / 8][t % 8] = 0.f;
   __syncthreads();  // qbs, epos
   // the offsets of tile j (q-block qbs[e], rows (f % NS)·64 .. +63 of the list entry)
   auto tile_rof = [&](int j) __attribute__((always_inline)) -> const float* {
@@ -1878,7 +1884,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) 
     }
     const int kb = pl.multi[static_cast<int64_t>(h) * (NB + 1) + 1 + m];
     const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
-    const int nch = (qo[kb + 1] - qo[kb] + kChunk - 1) / kChunk;
+    const int nch = (qo[kb + 1] - qo[kb] + pl.chunk - 1) / pl.chunk;
     const int64_t slot0 = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb];
     const float4* pk = reinterpret_cast<const float4*>(pl.part_dk) + slot0 * per_slot + e0;
     const float4* pv = reinterpret_cast<const float4*>(pl.part_dv) + slot0 * per_slot + e0;
@@ -1937,9 +1943,10 @@ struct BwdLayout {
 static BwdLayout bwd_layout(const scope_attn_params* p) {
   BwdLayout L = {};
   const int64_t QB = p->T / p->bs, NB = QB;
-  const int64_t per_head_items = NB + (QB * p->maxkv + kChunk - 1) / kChunk;
+  const int chunk = bwd_chunk(static_cast<int>(QB));
+  const int64_t per_head_items = NB + (QB * p->maxkv + chunk - 1) / chunk;
   L.max_items = static_cast<int>(per_head_items);
-  L.max_slots = (2 * QB * p->maxkv + kChunk - 1) / kChunk + 1;
+  L.max_slots = (2 * QB * p->maxkv + chunk - 1) / chunk + 1;
   auto al = [](int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); };
   int64_t o = 0;
   L.delta = o;
@@ -2020,7 +2027,8 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
   }
   if (phases & SCOPE_BWD_DKV) phases |= SCOPE_BWD_DKV_PLAN | SCOPE_BWD_DKV_MAIN | SCOPE_BWD_DKV_REDUCE;
   if (phases & SCOPE_BWD_DKV_PLAN) {
-    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, a.q_off, const_cast<int32_t*>(pl.items_start),
+    hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, pl.chunk, a.q_off,
+                       const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start), const_cast<int32_t*>(pl.multi));
     if (pl.q_pos)
       hipLaunchKernelGGL(qpos_kernel, dim3(a.QB, a.H), dim3(64), 0, s, a, const_cast<int32_t*>(pl.q_pos));
@@ -2125,6 +2133,7 @@ extern "C" int scope_attn_bwd_phase(const scope_attn_params* p, int phases, cons
   a.rowslope = a.rowoff ? a.rowoff + static_cast<int64_t>(p->H) * p->T : nullptr;
   pl.max_slots = L.max_slots;
   pl.max_items = L.max_items;
+  pl.chunk = bwd_chunk(a.QB);
   hipStream_t s = as_stream(stream);
   const int grid_q = p->H * a.QB;
   a.dpair = p->dpair_bias ? reinterpret_cast<float*>(ws + L.dpair) : nullptr;

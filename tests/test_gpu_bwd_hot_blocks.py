@@ -29,7 +29,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 ATOL, RTOL = 2e-2, 1e-2
 SCALE, BETA = 0.12, 0.5
-CHUNK = 32  # q-blocks per kv-major work item (attn_bwd.hip kChunk)
+CHUNK = 32  # q-blocks per kv-major work item below 2048 key blocks per head (attn_bwd.hip bwd_chunk)
 
 
 def _docs(T: int, cuts: list[int]) -> torch.Tensor:

@@ -22,9 +22,10 @@ What is compared:
   torch on the device over each q-block's listed key blocks (the block term,
   the document-causal mask and the list applied as in the oracle), computed
   from q, k, v and the coefficients alone;
-* dK/dV of every hot key block (more than 32 users: the global blocks whose
-  sums run through the multi-chunk partials and the reduce; up to 4096 users,
-  128 chunks, at a million tokens) against a column reference: the key
+* dK/dV of every hot key block (more users than one kv-major work item
+  takes: 32 q-blocks, 64 from 2048 key blocks per head; the global blocks
+  whose sums run through the multi-chunk partials and the reduce; up to 4096
+  users, 64 chunks, at a million tokens) against a column reference: the key
   block's column of P and dS in fp32 torch on the device from the row
   reference's lse and out (not the kernel's), and the same column reference
   is checked against the oracle on the ordinary key block.
@@ -45,7 +46,11 @@ from tests.helpers import tol_check
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 SCALE, BETA = 0.12, 0.5
-CHUNK = 32
+
+
+def _chunk(NB: int) -> int:
+    """q-blocks per kv-major work item: 32, or 64 from 2048 key blocks per head."""
+    return 64 if NB >= 2048 else 32
 
 
 def _rows_ref(h, bs, q, k, v, kv_num, kv_idx, docs, cc, cs, om, batch=32):
@@ -157,7 +162,7 @@ def _layer_checks(step, inp, heads, sample_qbs, bs, n_hot_max=None):
     for h in heads:
         print(f"  head {h}", flush=True)
         # an ordinary key block (fp32 oracle over all of its users) and every hot one (column reference)
-        kb_o = next(kb for kb in range(NB // 3, NB) if 1 <= len(_users(q_off, q_list, h, kb)) <= CHUNK)
+        kb_o = next(kb for kb in range(NB // 3, NB) if 1 <= len(_users(q_off, q_list, h, kb)) <= _chunk(NB))
         users_o = _users(q_off, q_list, h, kb_o)
         res, gq, gk, gv, gc, gs = _oracle_rows(h, sample_qbs, users_o, bs, t["q"], t["k"], t["v"], t["dout"], docs,
                                                kv_num, kv_idx, t["coeff_cos"], t["coeff_sin"], om)
@@ -191,15 +196,15 @@ def _layer_checks(step, inp, heads, sample_qbs, bs, n_hot_max=None):
         _check("column reference dk vs oracle", ck, gk[sl])
         _check("column reference dv vs oracle", cv, gv[sl])
         n_users = np.diff(q_off[h].numpy())
-        hot = np.flatnonzero(n_users > CHUNK)
-        assert hot.size, "no key block with more than 32 users"
+        hot = np.flatnonzero(n_users > _chunk(NB))
+        assert hot.size, f"no key block with more than {_chunk(NB)} users"
         if n_hot_max is not None:
             hot = hot[np.argsort(-n_users[hot], kind="stable")][:n_hot_max]
         for kb in hot.tolist():
             ck, cv = _column_ref(h, kb, bs, t["q"], t["k"], t["v"], t["dout"], ro_all, rl_all, kv_num, kv_idx,
                                  docs, t["coeff_cos"], t["coeff_sin"], om)
             sl = slice(kb * bs, (kb + 1) * bs)
-            print(f"   hot key block {kb} ({int(n_users[kb])} users, {-(-int(n_users[kb]) // CHUNK)} chunks)",
+            print(f"   hot key block {kb} ({int(n_users[kb])} users, {-(-int(n_users[kb]) // _chunk(NB))} chunks)",
                   flush=True)
             _check("dk", gr["dk"][0, h, sl].float().cpu(), ck)
             _check("dv", gr["dv"][0, h, sl].float().cpu(), cv)
