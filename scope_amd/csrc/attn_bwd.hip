@@ -462,19 +462,35 @@ struct KvPlan {
 
 // q_pos[h][i] = the position of key block kb in the kv list of q-block
 // q_list[h][i], for every entry i of kb's q-list (its first kv_num entries
-// are unique; a scan of independent loads).  One workgroup per (kb, h).
-__global__ __launch_bounds__(64) void qpos_kernel(AttnArgs a, int32_t* __restrict__ q_pos) {
-  const int kb = blockIdx.x, h = blockIdx.y;
+// are unique; a scan of independent loads).  A thread per q-list entry: the
+// entry's key block is the bucket of q_off that holds i (a binary search),
+// so a key block listed by every q-block (a long document's global block)
+// is spread over as many threads as it has entries.
+__global__ __launch_bounds__(256) void qpos_kernel(AttnArgs a, int32_t* __restrict__ q_pos) {
   const int NB = a.QB;
-  const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
-  const int64_t base = static_cast<int64_t>(h) * a.QB * a.maxkv;
-  for (int i = qo[kb] + threadIdx.x; i < qo[kb + 1]; i += blockDim.x) {
+  const int64_t per_head = static_cast<int64_t>(a.QB) * a.maxkv;
+  const int64_t n = per_head * a.H;
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; s < n;
+       s += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int h = static_cast<int>(s / per_head);
+    const int i = static_cast<int>(s % per_head);
+    const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
+    if (i >= qo[NB]) continue;  // past the head's entries
+    // the largest kb with qo[kb] <= i: qo[kb] <= i < qo[kb + 1]
+    int lo = 0, hi = NB - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (qo[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    const int kb = lo;
+    const int64_t base = static_cast<int64_t>(h) * per_head;
     const int qb = a.q_list[base + i];
     const int64_t row = static_cast<int64_t>(h) * a.QB + qb;
-    const int n = min(a.kv_num[row], a.maxkv);
+    const int nl = min(a.kv_num[row], a.maxkv);
     const int32_t* lst = a.kv_idx + row * a.maxkv;
     int pos = -1;
-    for (int e = 0; e < n; ++e)
+    for (int e = 0; e < nl; ++e)
       if (lst[e] == kb) pos = e;
     q_pos[base + i] = pos;
   }
@@ -2030,8 +2046,11 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
     hipLaunchKernelGGL(bwd_plan_kernel, dim3(a.H), dim3(1024), 0, s, a.QB, pl.chunk, a.q_off,
                        const_cast<int32_t*>(pl.items_start),
                        const_cast<int32_t*>(pl.slots_start), const_cast<int32_t*>(pl.multi));
-    if (pl.q_pos)
-      hipLaunchKernelGGL(qpos_kernel, dim3(a.QB, a.H), dim3(64), 0, s, a, const_cast<int32_t*>(pl.q_pos));
+    if (pl.q_pos) {
+      const int64_t n = static_cast<int64_t>(a.H) * a.QB * a.maxkv;
+      const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 65536));
+      hipLaunchKernelGGL(qpos_kernel, dim3(blocks), dim3(256), 0, s, a, const_cast<int32_t*>(pl.q_pos));
+    }
   }
   const bool dp = a.dpair != nullptr;  // the pair-bias gradient runs in its own instantiation
   if (phases & SCOPE_BWD_DKV_MAIN) {
