@@ -6,11 +6,12 @@ GPU tensors; there is no CPU path.
 from __future__ import annotations
 
 import ctypes as C
+import threading
 
 import torch
 
 from . import _lib
-from ._lib import PTR_LOGITS_SCRATCH, AttnParams, PtrRefParams, PtrScoreParams, StatsParams, call, query
+from ._lib import PTR_LOGITS_SCRATCH, AttnParams, PtrRefParams, PtrScoreParams, StatsParams, query
 
 BIAS_MODES = {"none": 0, "block": 1, "token": 2}
 GATE_KINDS = {"none": 0, "softplus": 1, "relu": 2}
@@ -26,8 +27,36 @@ SV_NAMES = ["pi_entropy_mean", "ptr_docstart_frac", "ptr_outside_local_frac", "p
             "bs_ptr_block0_frac_excl", "bs_ptr_docstart_frac"]
 
 
+# Tensors whose pointers _p handed out, held until the next call() returns.
+_held = threading.local()
+
+
 def _p(t: torch.Tensor | None):
-    return None if t is None else C.c_void_p(t.data_ptr())
+    """Device pointer of t for a library call.  t stays referenced until the
+    next ``call`` returns: a dtype or layout copy made inside an argument list
+    (``_p(_i32(x))``) would otherwise go back to torch's caching allocator
+    before the launch, and a later copy in the same argument list could be
+    given its memory, so the kernel would read one operand in place of
+    another.  (Argument lists must not themselves run a ``call``.)"""
+    if t is None:
+        return None
+    held = getattr(_held, "ts", None)
+    if held is None:
+        held = _held.ts = []
+    held.append(t)
+    return C.c_void_p(t.data_ptr())
+
+
+def call(name: str, *args) -> None:
+    """``_lib.call`` (raise on a non-zero status), then release the tensors
+    held for the arguments: the launch is on the stream by then, so torch's
+    allocator hands their memory to later work on that stream only after it."""
+    try:
+        _lib.call(name, *args)
+    finally:
+        held = getattr(_held, "ts", None)
+        if held:
+            held.clear()
 
 
 def _stream(dev: torch.device):
@@ -1005,10 +1034,11 @@ def attn_bwd(q, k, v, out, dout, lse, kv_num, kv_idx, q_off, q_list, docs, ds_to
     ddm = torch.empty((1, H, T), **z) if gate else None
     dwd = torch.empty((1, H, T), **z) if gate else None
     ws = torch.empty(max(16, query("scope_attn_bwd_workspace_bytes", C.byref(prm))), dtype=torch.uint8, device=dev)
-    args = (_p(q), _p(k), _p(v), _p(out), _p(dout), _p(_f32(lse)), _p(_i32(kv_num)), _p(kv_idx3), _p(_i32(q_off)),
-            _p(_i32(q_list)), _p(_i32(docs.reshape(-1))), _p(_i32(ds_tok_end)), _p(table), _p(_f32(coeff_cos)),
-            _p(_f32(coeff_sin)), _p(_f32(b0)), _p(_f32(slope)), _p(_f32(delta_main)), _p(_f32(width)), _p(dq),
-            _p(dk), _p(dv), _p(dcc), _p(dcs), _p(db0), _p(dsl), _p(ddm), _p(dwd), _p(ws), _stream(dev))
+    # the converted inputs as locals: with phase_hook the same pointers serve four calls
+    ins = (_f32(lse), _i32(kv_num), kv_idx3, _i32(q_off), _i32(q_list), _i32(docs.reshape(-1)), _i32(ds_tok_end),
+           table, _f32(coeff_cos), _f32(coeff_sin), _f32(b0), _f32(slope), _f32(delta_main), _f32(width))
+    args = (_p(q), _p(k), _p(v), _p(out), _p(dout), *(_p(t) for t in ins), _p(dq), _p(dk), _p(dv), _p(dcc), _p(dcs),
+            _p(db0), _p(dsl), _p(ddm), _p(dwd), _p(ws), _stream(dev))
     if phase_hook is None:
         call("scope_attn_bwd", C.byref(prm), *args)
     else:

@@ -23,6 +23,8 @@ def test_device_counters_equal_host(H, QB, maxkv, seed):
     for causal in (True, False):
         want = ops._check_lists_host(tn, ti, QB, causal)
         res = torch.empty(5, dtype=torch.int32, device=DEV)
+        # two device copies made in the argument list: each stays referenced
+        # until the call returns, so the second cannot take the first's memory
         ops.call("scope_check_lists", ops._p(tn.to(DEV)), ops._p(ti.to(DEV)), H, QB, QB, maxkv, int(causal),
                  ops._p(res), ops._stream(torch.device(DEV)))
         got = res.tolist()
@@ -79,3 +81,28 @@ def test_entry_points_reject_malformed_lists():
                         bs=bs, scale=0.1)
     torch.cuda.synchronize()
     assert np.isfinite(out.float().cpu().numpy()).all()
+
+
+def test_int64_lists_and_documents_equal_int32():
+    """Lists and document ids in int64 (the reference's dtypes) are copied to
+    int32 inside the call's argument list: outputs equal the int32 call's bit
+    for bit, forward and backward."""
+    H, T, D, bs, W = 2, 2048, 128, 128, 3
+    QB = T // bs
+    g = torch.Generator(device=DEV).manual_seed(5)
+    q, k, v, do = (torch.randn((1, H, T, D), generator=g, device=DEV).to(torch.bfloat16) for _ in range(4))
+    docs = torch.zeros(T, dtype=torch.int32, device=DEV)
+    docs[700:] = 1
+    docs[1500:] = 2
+    _, _, ds_tok_end = ops.doc_starts(docs, bs)
+    kn, ki = _valid_lists(H, QB, W)
+    q_off, q_list = ops.transpose_blocks(kn, ki, QB)
+    out, lse = ops.attn_fwd(q, k, v, kn, ki, docs, ds_tok_end, bs=bs, scale=0.1)
+    out64, lse64 = ops.attn_fwd(q, k, v, kn.long(), ki.long(), docs.long(), ds_tok_end.long(), bs=bs, scale=0.1)
+    assert torch.equal(out, out64) and torch.equal(lse, lse64)
+    g32 = ops.attn_bwd(q, k, v, out, do, lse, kn, ki, q_off, q_list, docs, ds_tok_end, bs=bs, scale=0.1)
+    g64 = ops.attn_bwd(q, k, v, out, do, lse, kn.long(), ki.long(), q_off.long(), q_list.long(), docs.long(),
+                       ds_tok_end.long(), bs=bs, scale=0.1)
+    assert g32.keys() == g64.keys()
+    for key, a in g32.items():
+        assert (a is None and g64[key] is None) or torch.equal(a, g64[key]), key

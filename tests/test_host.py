@@ -170,3 +170,29 @@ def test_coefficient_head_training_regularisers_and_grads_match_reference():
         for n, x in zip(PARAM_NAMES, gr1):
             ref = torch.from_numpy(g[f"greg_{tag}_{n}"])
             assert torch.allclose(x.reshape(ref.shape), ref, rtol=1e-4, atol=1e-5 * max(ref.abs().max().item(), 1e-30)), (tag, n)
+
+
+def test_pointer_arguments_outlive_their_temporaries_until_the_call_returns():
+    """A copy made inside a call's argument list (``_p(_i32(x))``) stays
+    referenced until ``call`` returns, also when the call fails; otherwise the
+    caching allocator could give its memory to the next copy in the same
+    list.  The call here fails its argument check in the library before any
+    GPU work (a null pointer)."""
+    import weakref
+
+    from scope_amd import ScopeLibraryError, ops
+
+    refs = []
+
+    def copy(x):
+        y = ops._i32(x)  # int64 -> a new int32 tensor
+        refs.append(weakref.ref(y))
+        return y
+
+    x = torch.arange(8, dtype=torch.int64)
+    with pytest.raises(ScopeLibraryError, match="null pointer"):
+        ops.call("scope_transpose_blocks", ops._p(copy(x)), ops._p(copy(x)), 1, 2, 2, 4, None, None, None, None)
+    assert all(r() is None for r in refs)  # released once the call returned
+    p1, p2 = ops._p(copy(x)), ops._p(copy(x))
+    assert all(r() is not None for r in refs[2:]) and p1.value != p2.value  # held, so not reused
+    ops._held.ts.clear()
