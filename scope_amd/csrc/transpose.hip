@@ -7,7 +7,8 @@
 //   scan   : exclusive prefix sum per head (one workgroup per head); the
 //            head's list entries past its total set to -1
 //   fill   : q_list[h][q_off[h][kb] + cursor++] = qb          (integer atomics)
-//   sort   : each bucket sorted ascending (bitonic in LDS)
+//   sort   : each bucket sorted ascending (bitonic over a wavefront's lanes,
+//            or a counting sort in LDS for a bucket longer than 64)
 // The atomics only fix the set of each bucket; the sort fixes its order, so
 // the result is deterministic.
 #include <limits.h>
@@ -30,18 +31,59 @@ __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
-// count and fill take a thread per list slot (h, qb, i): a thread per row
-// would wait for up to maxkv returning atomics one after another
+// count and fill take a thread per list slot, in the order (h, i, qb): the
+// lanes of a wavefront hold position i of 64 consecutive rows.  A key block
+// listed at the same position by many rows (a document's global block, first
+// in every row's ascending list) then falls on whole wavefronts, which add
+// to its counter with one atomic: the lanes whose bucket equals the first
+// active lane's are counted by a ballot.
+struct SlotEntry {
+  int64_t bucket;  // h·NB + kb, or -1 for an empty or out-of-range slot
+  int qb;
+};
+
+__device__ __forceinline__ SlotEntry slot_entry(const int32_t* __restrict__ kv_num,
+                                                const int32_t* __restrict__ kv_idx, int QB, int NB, int maxkv,
+                                                int64_t e) {
+  const int64_t per_head = static_cast<int64_t>(maxkv) * QB;
+  const int h = static_cast<int>(e / per_head);
+  const int64_t r = e % per_head;
+  const int i = static_cast<int>(r / QB);
+  const int qb = static_cast<int>(r % QB);
+  const int64_t row = static_cast<int64_t>(h) * QB + qb;
+  SlotEntry s{-1, qb};
+  if (i >= kv_num[row]) return s;
+  const int kb = kv_idx[row * maxkv + i];
+  if (kb < 0 || kb >= NB) return s;  // an entry outside the key blocks is no block (scope_check_lists reports it)
+  s.bucket = static_cast<int64_t>(h) * NB + kb;
+  return s;
+}
+
+// The lanes of the calling (active) lanes whose bucket equals the first
+// active lane's, and whether this lane is one of them.
+__device__ __forceinline__ uint64_t same_bucket_lanes(int64_t bucket, bool* mine) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bucket));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(bucket) >> 32));
+  const int64_t first = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+  *mine = bucket == first;
+  return __ballot(*mine);
+}
+
 __global__ void tr_count_kernel(const int32_t* __restrict__ kv_num, const int32_t* __restrict__ kv_idx, int H,
                                 int QB, int NB, int maxkv, int32_t* __restrict__ q_off) {
   const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (e >= static_cast<int64_t>(H) * QB * maxkv) return;
-  const int64_t row = e / maxkv;
-  if (static_cast<int>(e % maxkv) >= kv_num[row]) return;
-  const int h = static_cast<int>(row / QB);
-  const int kb = kv_idx[e];
-  if (kb < 0 || kb >= NB) return;  // an entry outside the key blocks is no block (scope_check_lists reports it)
-  atomicAdd(&q_off[static_cast<int64_t>(h) * (NB + 1) + kb + 1], 1);
+  const SlotEntry s = slot_entry(kv_num, kv_idx, QB, NB, maxkv, e);
+  if (s.bucket < 0) return;
+  // q_off[h][kb + 1] sits at bucket + h + 1
+  const int64_t at = s.bucket + s.bucket / NB + 1;
+  bool mine = false;
+  const uint64_t grp = same_bucket_lanes(s.bucket, &mine);
+  if (mine) {
+    if (lane_id() == __ffsll(static_cast<unsigned long long>(grp)) - 1) atomicAdd(&q_off[at], __popcll(grp));
+  } else {
+    atomicAdd(&q_off[at], 1);
+  }
 }
 
 // also sets the head's list entries past its total to -1 (the fill kernel
@@ -83,69 +125,103 @@ __global__ void tr_fill_kernel(const int32_t* __restrict__ kv_num, const int32_t
                                int32_t* __restrict__ cursor, int32_t* __restrict__ q_list) {
   const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (e >= static_cast<int64_t>(H) * QB * maxkv) return;
-  const int64_t row = e / maxkv;
-  if (static_cast<int>(e % maxkv) >= kv_num[row]) return;
-  const int h = static_cast<int>(row / QB);
-  const int qb = static_cast<int>(row % QB);
-  const int kb = kv_idx[e];
-  if (kb < 0 || kb >= NB) return;  // skipped by the count kernel too
-  const int pos = atomicAdd(&cursor[static_cast<int64_t>(h) * NB + kb], 1);
-  q_list[static_cast<int64_t>(h) * QB * maxkv + q_off[static_cast<int64_t>(h) * (NB + 1) + kb] + pos] = qb;
+  const SlotEntry s = slot_entry(kv_num, kv_idx, QB, NB, maxkv, e);
+  if (s.bucket < 0) return;  // skipped by the count kernel too
+  const int h = static_cast<int>(s.bucket / NB);
+  const int kb = static_cast<int>(s.bucket % NB);
+  bool mine = false;
+  const uint64_t grp = same_bucket_lanes(s.bucket, &mine);
+  int pos;
+  if (mine) {
+    const int leader = __ffsll(static_cast<unsigned long long>(grp)) - 1;
+    int base = 0;
+    if (lane_id() == leader) base = atomicAdd(&cursor[s.bucket], __popcll(grp));
+    base = __shfl(base, leader, kWave);
+    pos = base + __popcll(grp & ((1ull << lane_id()) - 1));
+  } else {
+    pos = atomicAdd(&cursor[s.bucket], 1);
+  }
+  q_list[static_cast<int64_t>(h) * QB * maxkv + q_off[static_cast<int64_t>(h) * (NB + 1) + kb] + pos] = s.qb;
 }
 
-// One workgroup of 256 threads per bucket: a list of up to 64 entries is sorted
-// in registers by the first wavefront (bitonic over the lanes); a longer one
-// (a global block listed by every q-block of a long document) by the whole
-// workgroup, bitonic in LDS.
+// Four buckets per workgroup of 256 threads.  A bucket of up to 64 entries
+// is sorted in registers by its own wavefront (bitonic over the lanes).  A
+// longer one (a global block listed by every q-block of a long document) is
+// sorted by the whole workgroup by counting: its entries are q-blocks in
+// [0, QB), so per-value counts in LDS, their exclusive prefix sum and a
+// write of each value count times give the ascending list, repeats kept.
+constexpr int kSortBuckets = 4;
+
 __global__ __launch_bounds__(256) void tr_sort_kernel(int NB, int QB, int maxkv, const int32_t* __restrict__ q_off,
-                                                     int32_t* __restrict__ q_list, int cap) {
-  extern __shared__ int s[];
+                                                     int32_t* __restrict__ q_list) {
+  extern __shared__ int cnt[];  // [QB]
+  __shared__ int wtot[kSortBuckets];
   const int h = blockIdx.y;
-  const int kb = blockIdx.x;
-  const int64_t o0 = q_off[static_cast<int64_t>(h) * (NB + 1) + kb];
-  const int n = q_off[static_cast<int64_t>(h) * (NB + 1) + kb + 1] - static_cast<int>(o0);
-  if (n <= 1) return;
-  int32_t* b = q_list + static_cast<int64_t>(h) * QB * maxkv + o0;
-  const int lane = threadIdx.x;
-  const int nt = blockDim.x;
-  if (n <= kWave) {
-    if (lane >= kWave) return;
-    // register bitonic over 64 lanes
-    int v = lane < n ? b[lane] : INT_MAX;
+  const int kb0 = blockIdx.x * kSortBuckets;
+  const int32_t* off = q_off + static_cast<int64_t>(h) * (NB + 1);
+  int32_t* lst = q_list + static_cast<int64_t>(h) * QB * maxkv;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  {
+    const int kb = kb0 + wave;
+    const int o0 = kb < NB ? off[kb] : 0;
+    const int n = kb < NB ? off[kb + 1] - o0 : 0;
+    if (n > 1 && n <= kWave) {
+      int32_t* b = lst + o0;
+      int v = lane < n ? b[lane] : INT_MAX;
 #pragma unroll
-    for (int k = 2; k <= kWave; k <<= 1) {
+      for (int k = 2; k <= kWave; k <<= 1) {
 #pragma unroll
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        int o = __shfl_xor(v, j, kWave);
-        bool lower = (lane & j) == 0;
-        bool up = (lane & k) == 0;
-        int mn = min(v, o), mx = max(v, o);
-        v = (lower == up) ? mn : mx;
-      }
-    }
-    if (lane < n) b[lane] = v;
-    return;
-  }
-  const int N = next_pow2(n);
-  if (N > cap) return;  // guarded on the host: cap >= next_pow2(QB)
-  for (int i = lane; i < N; i += nt) s[i] = i < n ? b[i] : INT_MAX;
-  __syncthreads();
-  for (int k = 2; k <= N; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = lane; i < (N >> 1); i += nt) {
-        int lo = 2 * j * (i / j) + (i % j);
-        int hi = lo + j;
-        bool up = (lo & k) == 0;
-        int a = s[lo], c = s[hi];
-        if ((a > c) == up) {
-          s[lo] = c;
-          s[hi] = a;
+        for (int j = k >> 1; j > 0; j >>= 1) {
+          const int o = __shfl_xor(v, j, kWave);
+          const bool lower = (lane & j) == 0;
+          const bool up = (lane & k) == 0;
+          const int mn = min(v, o), mx = max(v, o);
+          v = (lower == up) ? mn : mx;
         }
       }
-      __syncthreads();
+      if (lane < n) b[lane] = v;
     }
   }
-  for (int i = lane; i < n; i += nt) b[i] = s[i];
+  // the long buckets, one after another (the bounds are the same for every
+  // thread, so every barrier below is reached by the whole workgroup)
+  const int per = (QB + 255) / 256;  // values per thread in the prefix sum
+  for (int w = 0; w < kSortBuckets; ++w) {
+    const int kb = kb0 + w;
+    if (kb >= NB) break;
+    const int o0 = off[kb];
+    const int n = off[kb + 1] - o0;
+    if (n <= kWave) continue;
+    int32_t* b = lst + o0;
+    for (int v = tid; v < QB; v += 256) cnt[v] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += 256) {
+      const int v = b[i];
+      if (v >= 0 && v < QB) atomicAdd(&cnt[v], 1);  // the fill writes q-blocks only
+    }
+    __syncthreads();
+    // exclusive prefix sum over the values: thread t takes [t·per, t·per + per)
+    const int v0 = min(tid * per, QB), v1 = min(v0 + per, QB);
+    int mine = 0;
+    for (int v = v0; v < v1; ++v) mine += cnt[v];
+    int incl = mine;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int t = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += t;
+    }
+    if (lane == kWave - 1) wtot[wave] = incl;
+    __syncthreads();
+    int base = incl - mine;
+    for (int ww = 0; ww < wave; ++ww) base += wtot[ww];
+    for (int v = v0; v < v1; ++v) {
+      const int c = cnt[v];
+      for (int r = 0; r < c; ++r) b[base + r] = v;
+      base += c;
+    }
+    __syncthreads();  // cnt and wtot are reused by the next long bucket
+  }
 }
 
 // List validation: one wavefront per row (h, qb) of the compact lists, a
@@ -239,7 +315,7 @@ static int transpose_checks(const int32_t* kv_num, const int32_t* kv_idx, int H,
                             const int32_t* q_off, const int32_t* q_list, const char* fn) {
   SCOPE_REQUIRE(kv_num && kv_idx && q_off && q_list, "%s: null pointer", fn);
   SCOPE_REQUIRE(H >= 1 && QB >= 1 && NB >= 1 && maxkv >= 1, "%s: bad sizes", fn);
-  SCOPE_REQUIRE(next_pow2(QB) * 4 <= 64 * 1024, "%s: QB=%d exceeds the LDS sort capacity", fn, QB);
+  SCOPE_REQUIRE(static_cast<int64_t>(QB) * 4 <= 64 * 1024, "%s: QB=%d exceeds the LDS sort capacity", fn, QB);
   return SCOPE_OK;
 }
 
@@ -247,7 +323,6 @@ static int transpose_checks(const int32_t* kv_num, const int32_t* kv_idx, int H,
 // (zeroed here by a kernel, so the launches can be captured in a graph).
 static int transpose_launch(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv,
                             int32_t* q_off, int32_t* q_list, int32_t* cursor, hipStream_t s) {
-  const int cap = next_pow2(QB);
   const int64_t n_off = static_cast<int64_t>(H) * (NB + 1);
   const int64_t n_cur = static_cast<int64_t>(H) * NB;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(n_off, 256)), dim3(256), 0, s, q_off, n_off, 0);
@@ -258,7 +333,8 @@ static int transpose_launch(const int32_t* kv_num, const int32_t* kv_idx, int H,
   hipLaunchKernelGGL(tr_scan_kernel, dim3(H), dim3(1024), 0, s, NB, q_off, static_cast<int64_t>(QB) * maxkv, q_list);
   hipLaunchKernelGGL(tr_fill_kernel, dim3(ceil_div(slots, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off, cursor, q_list);
-  hipLaunchKernelGGL(tr_sort_kernel, dim3(NB, H), dim3(256), cap * sizeof(int), s, NB, QB, maxkv, q_off, q_list, cap);
+  hipLaunchKernelGGL(tr_sort_kernel, dim3(ceil_div(NB, kSortBuckets), H), dim3(256), QB * sizeof(int), s, NB, QB,
+                     maxkv, q_off, q_list);
   return check_launch("transpose kernels");
 }
 
