@@ -9,6 +9,7 @@ like FlexAttention's captured-buffer gradients.
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -54,13 +55,17 @@ def spectral_table(omegas: torch.Tensor, T: int, bs: int, mode: str) -> torch.Te
     per (ω, T, bs, mode) in eager mode and rebuilt in compiled graphs."""
     if torch.compiler.is_compiling() or isinstance(omegas, FakeTensor):  # traced: no cache keyed on pointers
         return library.spectral_table(omegas, T, bs, _MODE[mode])
+    # the entry also holds a weak reference to the ω tensor it was built
+    # from: a new tensor that the allocator placed at a freed one's address
+    # (a per-call .to(device) copy, another module's ω) is not that tensor
     key = (omegas.data_ptr(), omegas._version, omegas.device, T, bs, mode)
-    tab = _TABLES.get(key)
-    if tab is None:
-        if len(_TABLES) > 16:
-            _TABLES.clear()
-        tab = library.spectral_table(omegas, T, bs, _MODE[mode])
-        _TABLES[key] = tab
+    hit = _TABLES.get(key)
+    if hit is not None and hit[0]() is omegas:
+        return hit[1]
+    if len(_TABLES) > 16:
+        _TABLES.clear()
+    tab = library.spectral_table(omegas, T, bs, _MODE[mode])
+    _TABLES[key] = (weakref.ref(omegas), tab)
     return tab
 
 

@@ -134,3 +134,23 @@ def test_attn_fwd_c1_full_size_blocksparse_oracle():
         worst = max(worst, w1, w2)
         assert ok and ok2, f"(h={h}, qb={qb}) worst ratio {max(w1, w2):.3f}"
     print(f"C1 worst tolerance ratio {worst:.3f}")
+
+
+@pytest.mark.parametrize("mode", ["block", "token"])
+def test_spectral_table_cache_follows_the_tensor(mode):
+    """The cached cos/sin table belongs to the ω tensor it was built from: a
+    new ω of other values (here allocated where a freed one lay, as per-call
+    .to(device) copies are) gets its own table, and an in-place change of ω
+    rebuilds it."""
+    from scope_amd import library
+    from scope_amd.attention import spectral_table
+
+    T, bs = 4096, 128
+    m = {"block": 1, "token": 2}[mode]
+    om1 = omegas_block(8).to(DEV)
+    spectral_table(om1, T, bs, mode)
+    del om1
+    om2 = (omegas_block(8) * 1.5).to(DEV)
+    assert torch.equal(spectral_table(om2, T, bs, mode), library.spectral_table(om2, T, bs, m))
+    om2.mul_(0.5)
+    assert torch.equal(spectral_table(om2, T, bs, mode), library.spectral_table(om2, T, bs, m))
