@@ -1877,22 +1877,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // dK and dV of the key blocks whose q-list spans several chunks: the sum of
 // the chunks' fp32 partials in chunk order, dK scaled, rounded to bf16.  A
 // fixed grid walks the work units (multi-chunk key block of any head, one of
-// kSlices column slices), so no workgroup is launched for a single-chunk
-// block and a long q-list (a global block listed by every q-block of a long
-// document) is summed by many workgroups.  Each thread sums PT float4
-// columns, two chunks at a time (2·2·PT loads in flight), which spreads the
-// unit's dependent index loads over many data loads.
+// kSlices column slices of 256 float4), so no workgroup is launched for a
+// single-chunk block and a long q-list (a global block listed by every
+// q-block of a long document) is summed by many workgroups: at bs=256 one
+// key block is 32 units.  Each thread sums one float4 column of dK and of dV,
+// four chunks at a time (eight loads in flight); the partials are read once,
+// by nontemporal loads.
 template <int BS>
 __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) {
-  constexpr int D = 128, kSlices = 8, PT = BS * D / 4 / kSlices / 256;
+  constexpr int D = 128;
   constexpr int64_t per_slot = static_cast<int64_t>(BS) * D / 4;  // float4 per partial
+  constexpr int kSlices = static_cast<int>(per_slot / 256);
+  constexpr int kAhead = 4;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int NB = a.QB;
   int total = 0;
   for (int h = 0; h < a.H; ++h) total += pl.multi[static_cast<int64_t>(h) * (NB + 1)];
   const int64_t units = static_cast<int64_t>(total) * kSlices;
   for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
     int m = static_cast<int>(u / kSlices);
-    const int e0 = static_cast<int>(u % kSlices) * PT * 256 + threadIdx.x;
+    const int e0 = static_cast<int>(u % kSlices) * 256 + threadIdx.x;
     int h = 0;
     for (int c = pl.multi[0]; m >= c && h + 1 < a.H; c = pl.multi[static_cast<int64_t>(h) * (NB + 1)]) {
       m -= c;
@@ -1902,52 +1906,35 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) 
     const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
     const int nch = (qo[kb + 1] - qo[kb] + pl.chunk - 1) / pl.chunk;
     const int64_t slot0 = h * pl.max_slots + pl.slots_start[static_cast<int64_t>(h) * (NB + 1) + kb];
-    const float4* pk = reinterpret_cast<const float4*>(pl.part_dk) + slot0 * per_slot + e0;
-    const float4* pv = reinterpret_cast<const float4*>(pl.part_dv) + slot0 * per_slot + e0;
-    float4 sk[PT], sv[PT];
+    const f32x4* pk = reinterpret_cast<const f32x4*>(pl.part_dk) + slot0 * per_slot + e0;
+    const f32x4* pv = reinterpret_cast<const f32x4*>(pl.part_dv) + slot0 * per_slot + e0;
+    f32x4 sk = {0.f, 0.f, 0.f, 0.f}, sv = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nch; c += kAhead) {
+      f32x4 xk[kAhead], xv[kAhead];
 #pragma unroll
-    for (int t = 0; t < PT; ++t) sk[t] = sv[t] = make_float4(0.f, 0.f, 0.f, 0.f);
-    auto add = [](float4& acc, const float4 x) __attribute__((always_inline)) {
-      acc.x += x.x;
-      acc.y += x.y;
-      acc.z += x.z;
-      acc.w += x.w;
-    };
-    for (int c = 0; c < nch; c += 2) {
-      const bool two = c + 1 < nch;
-      float4 xk[2][PT], xv[2][PT];
-#pragma unroll
-      for (int t = 0; t < PT; ++t) {
-        xk[0][t] = pk[c * per_slot + t * 256];
-        xv[0][t] = pv[c * per_slot + t * 256];
-        if (two) {
-          xk[1][t] = pk[(c + 1) * per_slot + t * 256];
-          xv[1][t] = pv[(c + 1) * per_slot + t * 256];
+      for (int i = 0; i < kAhead; ++i) {
+        if (c + i < nch) {
+          xk[i] = __builtin_nontemporal_load(pk + (c + i) * per_slot);
+          xv[i] = __builtin_nontemporal_load(pv + (c + i) * per_slot);
         }
       }
 #pragma unroll
-      for (int t = 0; t < PT; ++t) {
-        add(sk[t], xk[0][t]);
-        add(sv[t], xv[0][t]);
-        if (two) {
-          add(sk[t], xk[1][t]);
-          add(sv[t], xv[1][t]);
+      for (int i = 0; i < kAhead; ++i) {
+        if (c + i < nch) {
+          sk += xk[i];
+          sv += xv[i];
         }
       }
     }
     const int64_t kv0 = static_cast<int64_t>(kb) * BS;
-#pragma unroll
-    for (int t = 0; t < PT; ++t) {
-      const int e4 = e0 + t * 256;
-      const int r = (e4 * 4) / D, d = (e4 * 4) % D;
-      uint2 vk, vv;
-      vk.x = cvt_pk_bf16(sk[t].x * a.scale, sk[t].y * a.scale);
-      vk.y = cvt_pk_bf16(sk[t].z * a.scale, sk[t].w * a.scale);
-      vv.x = cvt_pk_bf16(sv[t].x, sv[t].y);
-      vv.y = cvt_pk_bf16(sv[t].z, sv[t].w);
-      *reinterpret_cast<uint2*>(a.dk + h * a.k_sh + (kv0 + r) * a.k_st + d) = vk;
-      *reinterpret_cast<uint2*>(a.dv + h * a.v_sh + (kv0 + r) * a.v_st + d) = vv;
-    }
+    const int r = (e0 * 4) / D, d = (e0 * 4) % D;
+    uint2 vk, vv;
+    vk.x = cvt_pk_bf16(sk.x * a.scale, sk.y * a.scale);
+    vk.y = cvt_pk_bf16(sk.z * a.scale, sk.w * a.scale);
+    vv.x = cvt_pk_bf16(sv.x, sv.y);
+    vv.y = cvt_pk_bf16(sv.z, sv.w);
+    *reinterpret_cast<uint2*>(a.dk + h * a.k_sh + (kv0 + r) * a.k_st + d) = vk;
+    *reinterpret_cast<uint2*>(a.dv + h * a.v_sh + (kv0 + r) * a.v_st + d) = vv;
   }
 }
 
