@@ -744,9 +744,15 @@ __global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float lo
       }
     }
   };
-  int t = blockIdx.x;
-  if (t < total) load(t);
-  for (; t < total; t += gridDim.x) {
+  // XCD-contiguous tile ranges: workgroup b runs on XCD b % 8 and takes every
+  // (grid/8)-th tile of that XCD's eighth of the (head, row tile, column
+  // tile) sequence, so an XCD's L2 serves the q̄ and k̄ rows of its own
+  // heads (one head per XCD at H = 8).  The grid is a multiple of 8.
+  const int xcd = blockIdx.x % 8, per_x = gridDim.x / 8;
+  const int t_hi = static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8);
+  int t = static_cast<int>(static_cast<int64_t>(total) * xcd / 8) + static_cast<int>(blockIdx.x / 8);
+  if (t < t_hi) load(t);
+  for (; t < t_hi; t += per_x) {
     int h, rt, ct;
     coords(t, h, rt, ct);
     __syncthreads();  // every wavefront is done reading the previous tile
@@ -754,7 +760,7 @@ __global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float lo
     spr[tid] = rp;
     const int dbase = (rt - ct) * kLgTile - (kLgTile - 1);
     __syncthreads();  // the split tile is complete
-    if (t + static_cast<int>(gridDim.x) < total) load(t + gridDim.x);  // under this tile's MFMAs
+    if (t + per_x < t_hi) load(t + per_x);  // under this tile's MFMAs
     f32x16_t acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -1124,7 +1130,8 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
     // long sequences: the logits on bf16 MFMA (split operands) into logits_out, then the selection reads them
     // one workgroup per CU looping over the tiles
     const int nt = ceil_div(p->NB, kLgTile);
-    hipLaunchKernelGGL(ptr_logits_kernel, dim3(min(p->H * (nt * (nt + 1) / 2), num_cus())), dim3(256), 0, st, p->H, p->NB,
+    const int lg_grid = std::max(8, std::min(p->H * (nt * (nt + 1) / 2), num_cus()) / 8 * 8);
+    hipLaunchKernelGGL(ptr_logits_kernel, dim3(lg_grid), dim3(256), 0, st, p->H, p->NB,
                        p->logit_scale, qbar, kbar, prior, prior ? p->prior_head_stride : 0, logits_out);
     logits_in = logits_out;
     qbar = kbar = nullptr;
