@@ -672,32 +672,36 @@ __global__ __launch_bounds__(kScoreQ * 64) void ptr_score_kernel(ScoreLaunch A, 
 // candidate) would take several times longer; the sum order differs, within
 // fp32 rounding.
 //
-// One workgroup of four wavefronts per CU loops over the 128x128 tiles of
-// the lower triangle (all heads).  A tile's 128 q̄ rows and 128 k̄ rows are
-// loaded into registers while the previous tile's MFMAs run, then split
-// once into hi and lo bf16 tiles in LDS (rows padded by 16 bytes, so the
-// 16-byte operand reads of 32 rows spread over the banks); each wavefront
-// computes a 64x64 quarter (2x2 blocks of 32x32, 12 MFMAs per step of 16
-// over D).
+// One workgroup of sixteen wavefronts per CU (the split tiles' 139 KB of
+// LDS leave room for one) loops over the 128x128 tiles of the lower
+// triangle (all heads).  A tile's 128 q̄ rows and 128 k̄ rows are loaded into
+// registers while the previous tile's MFMAs run, then split once into hi and
+// lo bf16 tiles in LDS (rows padded by 16 bytes, so the 16-byte operand reads
+// of 32 rows spread over the banks); each wavefront computes a 32x32
+// sixteenth (3 MFMAs per step of 16 over D).  The tile loop is latency
+// bound: at T=1M with four wavefronts of 64x64 it took 195 us, with eight
+// of 32x64 147 us, with sixteen 131 us (the stores of the logits alone are
+// about 50 us of HBM time).
 constexpr int kLgTile = 128;
 constexpr int kLgRow = 128 + 8;  // padded bf16 row of a split tile
 
-__global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float logit_scale,
+__global__ __launch_bounds__(1024) void ptr_logits_kernel(int H, int NB, float logit_scale,
                                                          const float* __restrict__ qbar,
                                                          const float* __restrict__ kbar,
                                                          const float* __restrict__ prior, int64_t prior_stride,
                                                          float* __restrict__ logits) {
   constexpr int D = 128;
-  constexpr int NF = kLgTile * D / 4 / 256;  // float4 per thread and operand
+  constexpr int NT = 1024;
+  constexpr int NF = kLgTile * D / 4 / NT;  // float4 per thread and operand
   // [operand: q̄ hi, q̄ lo, k̄ hi, k̄ lo][row][d]
   __shared__ __attribute__((aligned(16))) uint16_t sp[4][kLgTile * kLgRow];
   // the tile's prior values: prior[d] for d = qb - kb in dbase .. dbase + 255,
   // one per thread
-  static_assert(2 * kLgTile == 256, "one prior value per thread");
+  static_assert(2 * kLgTile == 256, "one prior value per thread of the first 256");
   __shared__ float spr[2 * kLgTile];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, m = lane % 32, g = lane / 32;
-  const int wr = wave / 2, wc = wave % 2;  // this wavefront's 64x64 quarter
+  const int wr = wave / 4, wc = wave % 4;  // this wavefront's 32x32 sixteenth of the tile
   const int nt = (NB + kLgTile - 1) / kLgTile;
   const int per_h = nt * (nt + 1) / 2;
   const int total = H * per_h;
@@ -717,13 +721,13 @@ __global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float lo
   auto load = [&](int t) __attribute__((always_inline)) {
     int h, rt, ct;
     coords(t, h, rt, ct);
-    if (prior) {
+    if (prior && tid < 2 * kLgTile) {
       const int d = (rt - ct) * kLgTile - (kLgTile - 1) + tid;
       rp = d >= 0 && d < NB ? prior[h * prior_stride + d] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < NF; ++i) {
-      const int f = tid + 256 * i, r = f / (D / 4), d4 = f % (D / 4);
+      const int f = tid + NT * i, r = f / (D / 4), d4 = f % (D / 4);
       const int qr = min(rt * kLgTile + r, NB - 1), kr = min(ct * kLgTile + r, NB - 1);
       ra[i] = *reinterpret_cast<const float4*>(qbar + (static_cast<int64_t>(h) * NB + qr) * D + 4 * d4);
       rb[i] = *reinterpret_cast<const float4*>(kbar + (static_cast<int64_t>(h) * NB + kr) * D + 4 * d4);
@@ -732,7 +736,7 @@ __global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float lo
   auto stash = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NF; ++i) {
-      const int f = tid + 256 * i, r = f / (D / 4), d4 = f % (D / 4);
+      const int f = tid + NT * i, r = f / (D / 4), d4 = f % (D / 4);
       const float4 v[2] = {ra[i], rb[i]};
 #pragma unroll
       for (int o = 0; o < 2; ++o) {
@@ -757,52 +761,34 @@ __global__ __launch_bounds__(256) void ptr_logits_kernel(int H, int NB, float lo
     coords(t, h, rt, ct);
     __syncthreads();  // every wavefront is done reading the previous tile
     stash();
-    spr[tid] = rp;
+    if (tid < 2 * kLgTile) spr[tid] = rp;
     const int dbase = (rt - ct) * kLgTile - (kLgTile - 1);
     __syncthreads();  // the split tile is complete
     if (t + per_x < t_hi) load(t + per_x);  // under this tile's MFMAs
-    f32x16_t acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+    f32x16_t acc = zero16();
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      // A: row m of block i, d = 16ks + 8g .. +7; B: the same for the key rows
-      uint4 ah[2], al[2], bh[2], bl[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int ar = (64 * wr + 32 * i + m) * kLgRow + 16 * ks + 8 * g;
-        const int br = (64 * wc + 32 * i + m) * kLgRow + 16 * ks + 8 * g;
-        ah[i] = *reinterpret_cast<const uint4*>(&sp[0][ar]);
-        al[i] = *reinterpret_cast<const uint4*>(&sp[1][ar]);
-        bh[i] = *reinterpret_cast<const uint4*>(&sp[2][br]);
-        bl[i] = *reinterpret_cast<const uint4*>(&sp[3][br]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[i][j] = mfma32(ah[i], bh[j], acc[i][j]);
-          acc[i][j] = mfma32(ah[i], bl[j], acc[i][j]);
-          acc[i][j] = mfma32(al[i], bh[j], acc[i][j]);
-        }
+      // A: q̄ row 32·wr + m, d = 16ks + 8g .. +7; B: the same for k̄ row 32·wc + m
+      const int ar = (32 * wr + m) * kLgRow + 16 * ks + 8 * g;
+      const int br = (32 * wc + m) * kLgRow + 16 * ks + 8 * g;
+      const uint4 ah = *reinterpret_cast<const uint4*>(&sp[0][ar]);
+      const uint4 al = *reinterpret_cast<const uint4*>(&sp[1][ar]);
+      const uint4 bh = *reinterpret_cast<const uint4*>(&sp[2][br]);
+      const uint4 bl = *reinterpret_cast<const uint4*>(&sp[3][br]);
+      acc = mfma32(ah, bh, acc);
+      acc = mfma32(ah, bl, acc);
+      acc = mfma32(al, bh, acc);
     }
     // C layout: column m (key block), register r -> row 8(r/4) + 4g + r%4
+    const int kb = ct * kLgTile + 32 * wc + m;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int kb = ct * kLgTile + 64 * wc + 32 * j + m;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qb = rt * kLgTile + 64 * wr + 32 * i + 8 * (r / 4) + 4 * g + (r % 4);
-          if (qb < NB && kb <= qb) {
-            float lg = logit_scale * acc[i][j][r];
-            if (prior) lg = lg + spr[qb - kb - dbase];
-            logits[(static_cast<int64_t>(h) * NB + qb) * NB + kb] = lg;
-          }
-        }
+    for (int r = 0; r < 16; ++r) {
+      const int qb = rt * kLgTile + 32 * wr + 8 * (r / 4) + 4 * g + (r % 4);
+      if (qb < NB && kb <= qb) {
+        float lg = logit_scale * acc[r];
+        if (prior) lg = lg + spr[qb - kb - dbase];
+        logits[(static_cast<int64_t>(h) * NB + qb) * NB + kb] = lg;
+      }
     }
   }
 }
@@ -1131,7 +1117,7 @@ int scope_pointer_select(const scope_ptr_score_params* p, const float* qbar, con
     // one workgroup per CU looping over the tiles
     const int nt = ceil_div(p->NB, kLgTile);
     const int lg_grid = std::max(8, std::min(p->H * (nt * (nt + 1) / 2), num_cus()) / 8 * 8);
-    hipLaunchKernelGGL(ptr_logits_kernel, dim3(lg_grid), dim3(256), 0, st, p->H, p->NB,
+    hipLaunchKernelGGL(ptr_logits_kernel, dim3(lg_grid), dim3(1024), 0, st, p->H, p->NB,
                        p->logit_scale, qbar, kbar, prior, prior ? p->prior_head_stride : 0, logits_out);
     logits_in = logits_out;
     qbar = kbar = nullptr;
