@@ -365,7 +365,8 @@ def window_and_global(qb: int, ds_ptr: int, ds_local: int, W: int, G: int, NB: i
 
 def pointer_select_blockscore(logits: np.ndarray, docs: np.ndarray, *, bs: int, window: int,
                               n_global: int, budget: int, temp: float = 1.0,
-                              gumbel: np.ndarray | None = None, doc_clamp: bool = True) -> dict:
+                              gumbel: np.ndarray | None = None, doc_clamp: bool = True,
+                              rows=None) -> dict:
     """Block-scoring selection from fp32 logits [H,QB,NB].
 
     Per (h, qb):
@@ -376,7 +377,9 @@ def pointer_select_blockscore(logits: np.ndarray, docs: np.ndarray, *, bs: int, 
       picks   = top-``budget`` of cand by z, ties → lower kb; short lists are
                 padded with qb (removed again by the dedupe)
       list    = sort-dedupe-pack(window ++ picks ++ global)
-    ``gumbel`` is the transformed noise g [H,QB,NB] (fp32), or None."""
+    ``gumbel`` is the transformed noise g [H,QB,NB] (fp32), or None.
+    ``rows``: compute only these q-blocks (the other rows of the result are
+    left as for an empty selection), for long sequences in tests."""
     H, QB, NB = logits.shape
     ds_ptr, ds_local, _ = doc_start_blocks(docs, bs, doc_clamp=doc_clamp)
     t = F32(max(float(temp), 1e-6))
@@ -386,7 +389,7 @@ def pointer_select_blockscore(logits: np.ndarray, docs: np.ndarray, *, bs: int, 
     raw = np.zeros((H, QB, maxkv), dtype=np.int32)
     picks = np.full((H, QB, budget), -1, dtype=np.int32)
     for h in range(H):
-        for qb in range(QB):
+        for qb in (range(QB) if rows is None else rows):
             win, glb = window_and_global(qb, int(ds_ptr[qb]), int(ds_local[qb]), W, G, NB)
             excl = set(win) | set(glb)
             cand = [kb for kb in range(int(ds_ptr[qb]), qb + 1) if kb not in excl]

@@ -357,3 +357,43 @@ def test_blockscore_stats_vs_oracle():
     assert v[7] == ref["ptr_block0_frac"]
     assert v[8] == ref["ptr_block0_frac_excl"]
     assert v[9] == ref["ptr_docstart_frac"]
+
+
+@pytest.mark.parametrize("budget,noise", [(8, "counter"), (12, "none"), (3, "uniform")])
+def test_pointer_select_given_logits_past_4096_candidates(budget, noise):
+    """Rows with up to 4200 candidates (more than one 4096-candidate pass of
+    a wavefront's 64 lanes over 64 chunks) equal the oracle's selection on the
+    same logits, ties and -inf logits included, in a second document that
+    starts at block 300 (the oracle computes only the checked rows)."""
+    from scope_amd import ops
+
+    H, NB, bs = 1, 4500, 128
+    T = NB * bs
+    print(f"select past 4096 candidates NB={NB} budget={budget} noise={noise}", flush=True)
+    rng = np.random.default_rng(budget)
+    logits = (np.round(rng.standard_normal((H, NB, NB)) * 4) / 4).astype(np.float32)  # many ties
+    logits[rng.random((H, NB, NB)) < 0.2] = -np.inf
+    docs = torch.zeros(T, dtype=torch.int32)
+    docs[300 * bs:] = 1  # the second document starts at block 300
+    rows = [0, 5, 299, 300, 301, 363, 364, 2000, 4095, 4395, 4396, 4397, 4459, 4460, 4499]
+    seed = 0xBEEF_1234
+    g = u = None
+    if noise == "uniform":
+        u = rng.random((H, NB, NB)).astype(np.float32)
+        g = OP.gumbel_from_u(u)
+    elif noise == "counter":
+        g = np.zeros((H, NB, NB), dtype=np.float32)
+        for qb in rows:
+            g[0, qb] = OP.gumbel_from_u(OP.counter_uniform(seed, np.zeros(NB, np.int64), np.full(NB, qb), np.arange(NB)))
+    ref = OP.pointer_select_blockscore(logits, docs.numpy(), bs=bs, window=2, n_global=1, budget=budget, gumbel=g,
+                                       temp=0.5, rows=rows)
+    ds_ptr, ds_local, _ = ops.doc_starts(docs.to(DEV), bs)
+    kv_num, kv_idx, picks = ops.pointer_select(ds_ptr, ds_local, bs=bs, NB=NB, H=H, window=2, n_global=1,
+                                               budget=budget, logits_in=torch.from_numpy(logits).to(DEV), temp=0.5,
+                                               noise=noise, seed=seed,
+                                               gumbel_u=torch.from_numpy(u).to(DEV) if u is not None else None)
+    picks, kv_num, kv_idx = picks.cpu().numpy(), kv_num.cpu().numpy(), kv_idx.cpu().numpy()
+    for qb in rows:
+        assert np.array_equal(picks[0, qb], ref["picks"][0, qb]), qb
+        assert kv_num[0, qb] == ref["kv_num"][0, qb], qb
+        assert np.array_equal(kv_idx[0, qb], ref["packed"][0, qb]), qb
