@@ -304,6 +304,50 @@ def test_transpose_blocks_vs_oracle(H, T, bs, W, G, B):
         assert np.array_equal(got_list[h, :n], q_list[h, :n])
 
 
+@pytest.mark.parametrize("H,QB,maxkv,hot", [(2, 300, 7, 0), (3, 2000, 12, 2), (1, 4096, 5, 1)])
+def test_transpose_blocks_long_buckets_and_repeats(H, QB, maxkv, hot):
+    """The transpose straight through the C ABI (no list check) against a
+    sort of each key block's q-blocks: buckets from 1 to QB entries (``hot``
+    key blocks listed by every row, as a long document's global blocks are;
+    the long ones are sorted by counting), entries outside the key blocks
+    skipped, and rows that list a key block more than once keeping every
+    repeat (the count, fill and sort treat list slots independently)."""
+    from scope_amd import ops
+
+    print(f"transpose H={H} QB={QB} maxkv={maxkv} hot={hot}", flush=True)
+    NB = QB
+    rng = np.random.default_rng(QB)
+    kn = rng.integers(0, maxkv + 1, size=(H, QB)).astype(np.int32)
+    ki = rng.integers(-3, NB + 3, size=(H, QB, maxkv)).astype(np.int32)  # a few outside [0, NB)
+    ki[:, :, :hot] = np.arange(hot, dtype=np.int32)  # key blocks 0 .. hot-1 in every row
+    kn[:, :] = np.maximum(kn, hot)
+    dup = rng.random((H, QB)) < 0.1
+    ki[:, :, -1][dup] = ki[:, :, 0][dup]  # a repeat of the row's first entry
+    want = {}
+    for h in range(H):
+        for qb in range(QB):
+            for e in range(kn[h, qb]):
+                kb = int(ki[h, qb, e])
+                if 0 <= kb < NB:
+                    want.setdefault((h, kb), []).append(qb)
+    tn, ti = torch.from_numpy(kn).to(DEV), torch.from_numpy(ki).to(DEV)
+    q_off = torch.empty((H, NB + 1), dtype=torch.int32, device=DEV)
+    q_list = torch.empty((H, QB * maxkv), dtype=torch.int32, device=DEV)
+    ws = torch.empty(max(1, ops.query("scope_transpose_workspace_bytes", H, NB)), dtype=torch.uint8, device=DEV)
+    ops.call("scope_transpose_blocks", ops._p(tn), ops._p(ti), H, QB, NB, maxkv, ops._p(q_off), ops._p(q_list),
+             ops._p(ws), ops._stream(torch.device(DEV)))
+    off, lst = q_off.cpu().numpy(), q_list.cpu().numpy()
+    longest = 0
+    for h in range(H):
+        for kb in range(NB):
+            got = lst[h, off[h, kb]:off[h, kb + 1]].tolist()
+            exp = sorted(want.get((h, kb), []))
+            longest = max(longest, len(exp))
+            assert got == exp, (h, kb)
+        assert np.all(lst[h, off[h, NB]:] == -1)
+    assert hot == 0 or longest >= QB  # the hot buckets hold every row (and its repeats)
+
+
 @pytest.mark.parametrize("name", sorted(FORWARD_CASES))
 def test_forward_stats_match_reference_vectors(name):
     from scope_amd import ops
