@@ -1882,7 +1882,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // q-block of a long document) is summed by many workgroups: at bs=256 one
 // key block is 32 units.  Each thread sums one float4 column of dK and of dV,
 // four chunks at a time (eight loads in flight); the partials are read once,
-// by nontemporal loads.
+// by nontemporal loads.  Each workgroup first forms the exclusive prefix of
+// the heads' multi-chunk counts in LDS (one load per head, all in parallel),
+// so a unit finds its head by a search in LDS and its key block, q-list
+// length and first slot by one level of loads.
 template <int BS>
 __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) {
   constexpr int D = 128;
@@ -1890,18 +1893,41 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(AttnArgs a, KvPlan pl) 
   constexpr int kSlices = static_cast<int>(per_slot / 256);
   constexpr int kAhead = 4;
   typedef float f32x4 __attribute__((ext_vector_type(4)));
+  extern __shared__ int hoff[];  // [H]: multi-chunk key blocks of the heads before h
+  __shared__ int wsum[4];
   const int NB = a.QB;
-  int total = 0;
-  for (int h = 0; h < a.H; ++h) total += pl.multi[static_cast<int64_t>(h) * (NB + 1)];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int total = 0;  // the same in every thread
+  for (int h0 = 0; h0 < a.H; h0 += 256) {
+    const int h = h0 + static_cast<int>(threadIdx.x);
+    const int c = h < a.H ? pl.multi[static_cast<int64_t>(h) * (NB + 1)] : 0;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int t = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += t;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int base = total;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    if (h < a.H) hoff[h] = base + incl - c;
+    total += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();  // hoff complete; wsum free for the next 256 heads
+  }
   const int64_t units = static_cast<int64_t>(total) * kSlices;
   for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
     int m = static_cast<int>(u / kSlices);
     const int e0 = static_cast<int>(u % kSlices) * 256 + threadIdx.x;
-    int h = 0;
-    for (int c = pl.multi[0]; m >= c && h + 1 < a.H; c = pl.multi[static_cast<int64_t>(h) * (NB + 1)]) {
-      m -= c;
-      ++h;
+    // the head: the largest h with hoff[h] <= m (heads without multi-chunk
+    // blocks share their successor's offset and are passed over)
+    int h = 0, hi = a.H - 1;
+    while (h < hi) {
+      const int mid = (h + hi + 1) / 2;
+      if (hoff[mid] <= m) h = mid;
+      else hi = mid - 1;
     }
+    m -= hoff[h];
     const int kb = pl.multi[static_cast<int64_t>(h) * (NB + 1) + 1 + m];
     const int32_t* qo = a.q_off + static_cast<int64_t>(h) * (NB + 1);
     const int nch = (qo[kb + 1] - qo[kb] + pl.chunk - 1) / pl.chunk;
@@ -2055,7 +2081,7 @@ static void launch_bwd(const AttnArgs& a, const KvPlan& pl, int mode, int phases
     else hipLaunchKernelGGL((attn_bwd_dkv16_kernel<BS, 0, false>), gk, dim3(512), 0, s, a, pl);
   }
   if (phases & SCOPE_BWD_DKV_REDUCE) {
-    hipLaunchKernelGGL(bwd_reduce_kernel<BS>, gr, dim3(256), 0, s, a, pl);
+    hipLaunchKernelGGL(bwd_reduce_kernel<BS>, gr, dim3(256), static_cast<size_t>(a.H) * sizeof(int), s, a, pl);
     if (a.dpair && dpair_out) {
       const int64_t n = static_cast<int64_t>(a.H) * a.QB * a.maxkv;
       const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
