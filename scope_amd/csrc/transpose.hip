@@ -87,10 +87,12 @@ __global__ void tr_count_kernel(const int32_t* __restrict__ kv_num, const int32_
 }
 
 // also sets the head's list entries past its total to -1 (the fill kernel
-// writes only below it)
+// writes only below it) and clears the head's fill cursors (the count kernel
+// before it does not read them, the fill kernel after it does)
 __global__ __launch_bounds__(1024) void tr_scan_kernel(int NB, int32_t* __restrict__ q_off, int64_t list_len,
-                                                       int32_t* __restrict__ q_list) {
+                                                       int32_t* __restrict__ q_list, int32_t* __restrict__ cursor) {
   const int h = blockIdx.x;
+  for (int i = threadIdx.x; i < NB; i += 1024) cursor[static_cast<int64_t>(h) * NB + i] = 0;
   int32_t* row = q_off + static_cast<int64_t>(h) * (NB + 1);
   __shared__ int tsum[1024];
   __shared__ int carry_s;
@@ -320,17 +322,17 @@ static int transpose_checks(const int32_t* kv_num, const int32_t* kv_idx, int H,
 }
 
 // count -> scan -> fill -> sort with `cursor` [H·NB] as the fill cursors
-// (zeroed here by a kernel, so the launches can be captured in a graph).
+// (cleared by the scan kernel, not by a memset, so the launches can be
+// captured in a graph).
 static int transpose_launch(const int32_t* kv_num, const int32_t* kv_idx, int H, int QB, int NB, int maxkv,
                             int32_t* q_off, int32_t* q_list, int32_t* cursor, hipStream_t s) {
   const int64_t n_off = static_cast<int64_t>(H) * (NB + 1);
-  const int64_t n_cur = static_cast<int64_t>(H) * NB;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(n_off, 256)), dim3(256), 0, s, q_off, n_off, 0);
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(ceil_div(n_cur, 256)), dim3(256), 0, s, cursor, n_cur, 0);
   const int64_t slots = static_cast<int64_t>(H) * QB * maxkv;
   hipLaunchKernelGGL(tr_count_kernel, dim3(ceil_div(slots, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off);
-  hipLaunchKernelGGL(tr_scan_kernel, dim3(H), dim3(1024), 0, s, NB, q_off, static_cast<int64_t>(QB) * maxkv, q_list);
+  hipLaunchKernelGGL(tr_scan_kernel, dim3(H), dim3(1024), 0, s, NB, q_off, static_cast<int64_t>(QB) * maxkv, q_list,
+                     cursor);
   hipLaunchKernelGGL(tr_fill_kernel, dim3(ceil_div(slots, 256)), dim3(256), 0, s, kv_num, kv_idx, H, QB, NB, maxkv,
                      q_off, cursor, q_list);
   hipLaunchKernelGGL(tr_sort_kernel, dim3(ceil_div(NB, kSortBuckets), H), dim3(256), QB * sizeof(int), s, NB, QB,
